@@ -1,0 +1,138 @@
+// cm_pool.hip -- the Pooling unit: MAX / AVG / LP1 / LP2 over NCHW planes.
+//
+// Windowed pools: one thread per output element, neighbouring threads on neighbouring
+// output columns so that a tap's loads across a wavefront are one contiguous run of the
+// input row (stride stride_w).  Global pools (a window as large as the plane, the
+// MobileNet GlobalAveragePool 7x7 case) use one wavefront per output: the plane is read
+// 64 lanes at a time and reduced across the wavefront.
+#include "cm_common.h"
+
+namespace cm {
+namespace {
+
+__device__ __forceinline__ int sat16l(long long v) {
+    return v > 32767 ? 32767 : (v < -32768 ? -32768 : (int)v);
+}
+
+// _pool_poly_sqrt (_simulate.py:230-272) on the exact sum S of squares (value S * 2^-16):
+// S = m 4^k 2^16, m in [1, 4) cut to 16 fraction bits; Horner with the 2^-15 coefficients
+// 252, -3091, 21076, 14529, every partial floored at 2^-20; the result 2^k * t floored at
+// 2^-16.  Returns the result at 2^-16.
+__device__ __forceinline__ long long poly_sqrt(long long S) {
+    if (S <= 0) return 0;
+    const int e = 63 - __clzll((unsigned long long)S);
+    const int d = e - 16;
+    const int k = d >= 0 ? d / 2 : -((-d + 1) / 2);
+    const long long M = 2 * k >= 0 ? (S >> (2 * k)) : (S << (-2 * k));
+    const long long T1 = (252LL * M - 3091LL * 65536) >> 11;
+    const long long T2 = (T1 * M + 21076LL * 2097152) >> 16;
+    const long long T3 = (T2 * M + 14529LL * 2097152) >> 16;
+    return k >= 4 ? (T3 << (k - 4)) : (T3 >> (4 - k));
+}
+
+struct PoolGeom {
+    uint32_t in_h, in_w, out_h, out_w, ph, pw, sh, sw, pt, pl, dh, dw, type, lp, cip;
+};
+
+// The pooled value of one window from its running max / sum and the count of valid taps
+// (_simulate.py:275-358 then truncate).
+__device__ __forceinline__ int finish(const PoolGeom& g, long long mx, long long sum, uint32_t valid) {
+    if (g.type == 0) return valid ? (int)mx : -32768;
+    if (g.type == 1) {
+        long long d = g.cip ? (long long)g.ph * g.pw : (long long)valid;
+        if (d < 1) d = 1;
+        const long long inv = ((1LL << 23) + d / 2) / d;
+        return sat16l((sum * inv) >> 23);
+    }
+    if (g.lp == 1) return sat16l(sum);
+    return sat16l(poly_sqrt(sum) >> 8);
+}
+
+__device__ __forceinline__ void tap(const PoolGeom& g, long long v, long long& mx, long long& sum) {
+    mx = v > mx ? v : mx;
+    if (g.type == 1) sum += v;
+    else if (g.type == 2) sum += g.lp == 1 ? (v < 0 ? -v : v) : v * v;
+}
+
+__global__ __launch_bounds__(256) void pool_kernel(const int16_t* __restrict__ x,
+                                                   int16_t* __restrict__ y, uint64_t total,
+                                                   PoolGeom g) {
+    for (uint64_t o = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total;
+         o += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t ow = (uint32_t)(o % g.out_w);
+        const uint64_t t = o / g.out_w;
+        const uint32_t oh = (uint32_t)(t % g.out_h);
+        const uint64_t nc = t / g.out_h;
+        const int16_t* xp = x + nc * g.in_h * g.in_w;
+        long long mx = INT64_MIN, sum = 0;
+        uint32_t valid = 0;
+        for (uint32_t a = 0; a < g.ph; a++) {
+            const long long ih = (long long)oh * g.sh + (long long)a * g.dh - g.pt;
+            if (ih < 0 || ih >= g.in_h) continue;
+            for (uint32_t b = 0; b < g.pw; b++) {
+                const long long iw = (long long)ow * g.sw + (long long)b * g.dw - g.pl;
+                if (iw < 0 || iw >= g.in_w) continue;
+                valid++;
+                tap(g, xp[ih * g.in_w + iw], mx, sum);
+            }
+        }
+        y[o] = (int16_t)finish(g, mx, sum, valid);
+    }
+}
+
+// Global pool (window == plane, stride 1, no padding, out 1x1): one wavefront per plane.
+__global__ __launch_bounds__(256) void pool_global_kernel(const int16_t* __restrict__ x,
+                                                          int16_t* __restrict__ y, uint64_t planes,
+                                                          PoolGeom g) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint64_t nc = (uint64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (nc >= planes) return;
+    const uint32_t hw = g.in_h * g.in_w;
+    const int16_t* xp = x + nc * hw;
+    long long mx = INT64_MIN, sum = 0;
+    for (uint32_t i = lane; i < hw; i += 64) tap(g, xp[i], mx, sum);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        long long om = __shfl_xor(mx, off, 64);
+        mx = om > mx ? om : mx;
+        sum += __shfl_xor(sum, off, 64);
+    }
+    if (lane == 0) y[nc] = (int16_t)finish(g, mx, sum, hw);
+}
+
+}  // namespace
+}  // namespace cm
+
+extern "C" int cm_pool(const int16_t* x, int16_t* y, uint32_t batch, uint32_t channels,
+                       uint32_t in_h, uint32_t in_w, uint32_t out_h, uint32_t out_w,
+                       uint32_t pool_h, uint32_t pool_w, uint32_t stride_h, uint32_t stride_w,
+                       uint32_t pad_top, uint32_t pad_left, uint32_t dil_h, uint32_t dil_w,
+                       uint32_t pool_type, uint32_t lp_order, uint32_t count_include_pad,
+                       void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    if (pool_type > 2) return fail(CM_EINVAL, "pool: pool_type %u", pool_type);
+    if (pool_h == 0 || pool_w == 0 || stride_h == 0 || stride_w == 0 || dil_h == 0 || dil_w == 0)
+        return fail(CM_EINVAL, "pool: zero window, stride or dilation");
+    const uint64_t planes = (uint64_t)batch * channels;
+    const uint64_t total = planes * out_h * out_w;
+    if (total == 0) return CM_OK;
+    PoolGeom g{in_h, in_w, out_h, out_w, pool_h, pool_w, stride_h, stride_w, pad_top, pad_left,
+               dil_h, dil_w, pool_type, lp_order, count_include_pad};
+    hipStream_t s = as_stream(stream);
+    const bool global = out_h == 1 && out_w == 1 && pool_h == in_h && pool_w == in_w &&
+                        pad_top == 0 && pad_left == 0 && dil_h == 1 && dil_w == 1;
+    if (global) {
+        hipLaunchKernelGGL(pool_global_kernel, dim3((unsigned)((planes + 3) / 4)), dim3(256), 0, s,
+                           x, y, planes, g);
+        CM_LAUNCH_CHECK("pool_global_kernel");
+    } else {
+        uint64_t blocks = (total + 255) / 256;
+        if (blocks > 65536ull * 8) blocks = 65536ull * 8;
+        hipLaunchKernelGGL(pool_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, total, g);
+        CM_LAUNCH_CHECK("pool_kernel");
+    }
+    return CM_OK;
+}

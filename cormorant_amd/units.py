@@ -1,0 +1,299 @@
+"""The five units as calls on device tensors: the register contracts of the reference's
+kernels (VectorOP.h:319-333, MatmulKernel.h:228-242, ConvKernel.h:229-259,
+PoolingKernel.h:120-140, ROWOPS_RTL_KERNEL.md section 1.2), dispatched to libcormo_hip.so.
+
+Every function takes torch tensors on the GPU holding raw lanes (int16; uint8 byte images
+for row-ops), checks on the host that each access the kernels will make stays inside the
+tensors (so a bad register value raises instead of faulting the GPU), and enqueues the work
+on the current torch stream.  Outputs are written into the tensors the caller passes.
+"""
+from __future__ import annotations
+
+from typing import Iterable, Optional, Sequence
+
+import torch
+
+from . import _lib
+
+OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_RELU, OP_RELU6 = 0, 1, 2, 3, 4, 5
+OP_LEAKY_RELU, OP_SILU, OP_GELU, OP_GELU_TANH, OP_SOFTMAX, OP_SOFTMAX_T = 6, 7, 8, 9, 10, 11
+ACT_NONE, ACT_RELU, ACT_RELU6, ACT_LEAKY_RELU, ACT_SILU, ACT_GELU, ACT_GELU_TANH = range(7)
+POOL_MAX, POOL_AVG, POOL_LP = 0, 1, 2
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _require(t: torch.Tensor, name: str, dtype, elems: int) -> None:
+    if t is None:
+        raise ValueError(f"{name} is required")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.numel() < elems:
+        raise ValueError(f"{name} holds {t.numel()} elements; the call touches {elems}")
+
+
+def init() -> None:
+    """Build and upload the unit tables for the current device."""
+    _lib.check(_lib.lib().cm_init(), "cm_init")
+
+
+# ---------------------------------------------------------------- VectorOP
+def vectorop_extent(size: int, op: int, outer: int, a_inc: int, b_inc: int):
+    """(a, b, c) elements a call touches (whole 8-lane words per run)."""
+    padded = (size + 7) & ~7
+    if outer == 0 or size == 0:
+        return 0, 0, 0
+    if op == OP_SOFTMAX:
+        return (outer - 1) * a_inc + padded, 0, (outer - 1) * b_inc + padded
+    if op == OP_SOFTMAX_T:
+        nq = outer & ~15
+        if nq == 0:
+            return 0, 0, 0
+        return (size - 1) * a_inc + nq, 0, (nq - 1) * b_inc + padded
+    a = (outer - 1) * a_inc + padded
+    b = (outer - 1) * b_inc + padded if op < OP_RELU else 0
+    return a, b, (outer - 1) * (a_inc + b_inc) + padded
+
+
+def vectorop(a: torch.Tensor, b: Optional[torch.Tensor], c: torch.Tensor, size: int, op: int,
+             outer: int = 1, a_inc: int = 0, b_inc: int = 0, act: int = 0, alpha: int = 0,
+             smx_cm: int = 0, smx_cfg: int = 0, smx_mask: int = 0) -> torch.Tensor:
+    """VectorOPKernel (VectorOP.h:319-333): ops 0..9 element-wise with the fused
+    activation; 10 / 11 the softmax unit."""
+    na, nb, nc = vectorop_extent(size, op, outer, a_inc, b_inc)
+    _require(a, "a", torch.int16, na)
+    _require(c, "c", torch.int16, nc)
+    if nb:
+        _require(b, "b", torch.int16, nb)
+    rc = _lib.lib().cm_vectorop(_ptr(a), _ptr(b) if nb else None, _ptr(c), size, op, outer, a_inc,
+                                b_inc, act, alpha & 0xFFFFFFFF, smx_cm, smx_cfg, smx_mask, _stream())
+    _lib.check(rc, "cm_vectorop")
+    return c
+
+
+# ---------------------------------------------------------------- Matmul
+def matmul_b_extent(k: int, m: int, b_packed: int, gemv_kw: int) -> int:
+    if gemv_kw:
+        return k * m
+    if b_packed:
+        return ((m + 31) // 32) * k * 32
+    return k * m
+
+
+def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, n: int, k: int, m: int,
+           batch: int = 1, a_bs: int = 0, b_bs: int = 0, c_bs: Optional[int] = None,
+           b_packed: int = 0, gemv_kw: int = 0, wrap32: bool = False) -> torch.Tensor:
+    """MatmulKernel (MatmulKernel.h:228-242); C row-major [n][m] per batch slice."""
+    if c_bs is None:
+        c_bs = n * m
+    if batch and n and m:
+        _require(a, "a", torch.int16, (batch - 1) * a_bs + n * k)
+        _require(b, "b", torch.int16, (batch - 1) * b_bs + matmul_b_extent(k, m, b_packed, gemv_kw))
+        _require(c, "c", torch.int16, (batch - 1) * c_bs + n * m)
+    rc = _lib.lib().cm_matmul(_ptr(a), _ptr(b), _ptr(c), n, k, m, batch, a_bs, b_bs, c_bs,
+                              int(b_packed), int(gemv_kw), int(bool(wrap32)), _stream())
+    _lib.check(rc, "cm_matmul")
+    return c
+
+
+# ---------------------------------------------------------------- Conv
+def conv_weight_numel(out_ch: int, in_ch: int, kh: int, kw: int, depthwise: bool) -> int:
+    """Elements of the packed weight image (ConvKernel.h:142-150)."""
+    if depthwise:
+        return out_ch * ((kh * kw + 7) & ~7)
+    tiles = (in_ch + 15) // 16
+    rem = in_ch - (tiles - 1) * 16
+    return out_ch * kh * kw * ((tiles - 1) * 16 + (8 if rem <= 8 else 16))
+
+
+def conv_y_extent(batch, out_ch, out_h, out_w, y_cs=0, y_cn=0, y_gs=0) -> int:
+    plane = out_h * out_w
+    cs = y_cs or plane
+    if y_cn:
+        last = max((c % y_cn) * cs + (c // y_cn) * y_gs for c in range(out_ch))
+        return last + plane
+    return (batch - 1) * out_ch * plane + (out_ch - 1) * cs + plane
+
+
+def conv(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], y: torch.Tensor,
+         batch: int, in_ch: int, in_h: int, in_w: int, out_ch: int, out_h: int, out_w: int,
+         kh: int, kw: int, stride_h: int = 1, stride_w: int = 1, dilation_h: int = 1,
+         dilation_w: int = 1, pad_top: int = 0, pad_left: int = 0, has_bias: int = 0,
+         is_depthwise: int = 0, y_cs: int = 0, y_cn: int = 0, y_gs: int = 0,
+         wrap32: bool = False) -> torch.Tensor:
+    """ConvKernel (ConvKernel.h:229-259) on packed weights."""
+    if batch and out_ch and out_h and out_w:
+        _require(x, "x", torch.int16, batch * in_ch * in_h * in_w)
+        _require(w, "w", torch.int16, conv_weight_numel(out_ch, in_ch, kh, kw, bool(is_depthwise)))
+        if has_bias:
+            _require(bias, "bias", torch.int16, out_ch)
+        _require(y, "y", torch.int16, conv_y_extent(batch, out_ch, out_h, out_w, y_cs, y_cn, y_gs))
+        for oh_max, in_dim, k, s, d, p, nm in ((out_h, in_h, kh, stride_h, dilation_h, pad_top, "h"),
+                                               (out_w, in_w, kw, stride_w, dilation_w, pad_left, "w")):
+            if s == 0 or d == 0:
+                raise ValueError(f"conv: zero stride / dilation along {nm}")
+    rc = _lib.lib().cm_conv(_ptr(x), _ptr(w), _ptr(bias) if has_bias else None, _ptr(y), batch,
+                            in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w,
+                            dilation_h, dilation_w, pad_top, pad_left, int(has_bias),
+                            int(is_depthwise), y_cs, y_cn, y_gs, int(bool(wrap32)), _stream())
+    _lib.check(rc, "cm_conv")
+    return y
+
+
+# ---------------------------------------------------------------- Pool
+def pool(x: torch.Tensor, y: torch.Tensor, batch: int, channels: int, in_h: int, in_w: int,
+         out_h: int, out_w: int, pool_h: int, pool_w: int, stride_h: int = 1, stride_w: int = 1,
+         pad_top: int = 0, pad_left: int = 0, dil_h: int = 1, dil_w: int = 1,
+         pool_type: int = POOL_MAX, lp_order: int = 2, count_include_pad: int = 0) -> torch.Tensor:
+    """PoolingKernel (PoolingKernel.h:120-140)."""
+    _require(x, "x", torch.int16, batch * channels * in_h * in_w)
+    _require(y, "y", torch.int16, batch * channels * out_h * out_w)
+    rc = _lib.lib().cm_pool(_ptr(x), _ptr(y), batch, channels, in_h, in_w, out_h, out_w, pool_h,
+                            pool_w, stride_h, stride_w, pad_top, pad_left, dil_h, dil_w, pool_type,
+                            lp_order, count_include_pad, _stream())
+    _lib.check(rc, "cm_pool")
+    return y
+
+
+# ---------------------------------------------------------------- RowOps
+RO_COPY, RO_ADDX, RO_DEQUANT, RO_MULACT, RO_NORM, RO_ROPE, RO_XPOSE, RO_TLOAD = 1, 2, 3, 4, 5, 6, 7, 8
+RO_FOLD, RO_GATE = 9, 10
+K_I16, K_I32, K_F32 = 0, 1, 2
+F_B_EN, F_P_BCAST, F_P_KEEP, F_RELU, F_NORM_LN, F_SCALE = (1 << 12, 1 << 13, 1 << 14, 1 << 15,
+                                                         1 << 16, 1 << 17)
+
+
+def _kb(kind: int) -> int:
+    return 2 if kind == K_I16 else 4
+
+
+def rowops_extents(op, n, c1, c2, a_s1, a_s2, b_s1, b_s2, c_s1, c_s2, aux=0, win_lo=0,
+                   win_hi=0xFFFFFFFF):
+    """Byte extents (a, b, c, p) one job touches; None where the job has no work."""
+    code = op & 15
+    if code == RO_FOLD:
+        s, m = aux & 15, (aux >> 4) & 127
+        if not (n and c1 and c2 and m):
+            return None
+        out = c2 * c1 * n * 2
+        s0 = b_s2 - (1 << 32) if b_s2 >= 1 << 31 else b_s2
+        a_s2s = a_s2 - (1 << 32) if a_s2 >= 1 << 31 else a_s2
+        lo = max(s0, win_lo)
+        hi = min(s0 + (c1 - 1) * b_s1 + n, win_hi)     # exclusive source column bound
+        if hi <= lo:
+            a_lo, a_hi = 0, 0
+        else:
+            ks = [0, (c2 - 1) * a_s2s]
+            a_lo = min(ks) + 2 * lo
+            a_hi = max(ks) + 2 * hi
+        return (a_lo, a_hi), 0, (out + 15) & ~15, 0
+    if not (n and c1 and c2) or n > 4096:
+        return None
+    last = (c2 - 1), (c1 - 1)
+    if code == RO_TLOAD:
+        return (0, last[0] * a_s2 + last[1] * a_s1 + 4 * n), 0, 0, 0
+    if code == RO_XPOSE:
+        R = aux & 15
+        if not 1 <= R <= 8:
+            return None
+        a_end = last[0] * a_s2 + last[1] * a_s1 + (R - 1) * b_s1 + 2 * n
+        c_end = last[0] * c_s2 + last[1] * c_s1 + (n - 1) * b_s2 + 2 * R
+        if b_s2 == 2 * R:
+            c_end = last[0] * c_s2 + last[1] * c_s1 + ((2 * R * n + 15) & ~15)
+        return (0, a_end), 0, c_end, 0
+    ak, bk, ck = (op >> 4) & 3, (op >> 6) & 3, (op >> 8) & 3
+    if code == RO_DEQUANT:
+        ck = K_F32
+    a_row = ((_kb(ak) * n + 15) & ~15)
+    a_end = last[0] * a_s2 + last[1] * a_s1 + (2 * n if code == RO_ROPE else _kb(ak) * n)
+    b_end = 0
+    if code == RO_ROPE:
+        HD = aux & 0xFFF
+        if HD == 0 or HD & 15 or HD > 128 or n % HD:
+            return None
+        b_end = last[0] * b_s2 + last[1] * b_s1 + 8 * HD
+    elif (op & F_B_EN) and code != RO_DEQUANT:
+        b_end = last[0] * b_s2 + last[1] * b_s1 + _kb(bk) * n
+    c_end = last[0] * c_s2 + last[1] * c_s1 + ((_kb(ck) * n + 15) & ~15)
+    p_end = 16 * (1 if op & F_P_BCAST else n)
+    del a_row
+    return (0, a_end), b_end, c_end, p_end
+
+
+def _byte_ptr(t: torch.Tensor, off: int = 0) -> int:
+    return t.data_ptr() + off
+
+
+def rowops(a, b, c, p, op: int, n: int, c1: int, c2: int, a_s1: int, a_s2: int, b_s1: int,
+           b_s2: int, c_s1: int, c_s2: int, eps: int = 0, aux: int = 0, bq_sh: int = 0,
+           win_lo: int = 0, win_hi: int = 0xFFFFFFFF, a_off: int = 0, b_off: int = 0,
+           c_off: int = 0, p_off: int = 0) -> None:
+    """One RowOpsKernel job (ROWOPS_RTL_KERNEL.md 1.2) on GPU uint8 byte images; the
+    `*_off` arguments are byte offsets into each image (run_rowops' a_off / b_off / c_off,
+    rowops_nodes.py:143-151)."""
+    ext = rowops_extents(op, n, c1, c2, a_s1, a_s2, b_s1, b_s2, c_s1, c_s2, aux, win_lo, win_hi)
+    if ext is not None:
+        (a_lo, a_hi), b_end, c_end, p_end = ext
+        for t, nm, off, lo, hi in ((a, "a", a_off, a_lo, a_hi), (b, "b", b_off, 0, b_end),
+                                   (c, "c", c_off, 0, c_end), (p, "p", p_off, 0, p_end)):
+            if hi <= lo:
+                continue
+            if t is None or not t.is_cuda or t.dtype != torch.uint8 or not t.is_contiguous():
+                raise ValueError(f"rowops: {nm} must be a contiguous GPU uint8 tensor")
+            if off + lo < 0 or off + hi > t.numel():
+                raise ValueError(f"rowops: {nm} accesses bytes [{off + lo}, {off + hi}) of {t.numel()}")
+    rc = _lib.lib().cm_rowops(
+        _byte_ptr(a, a_off) if a is not None else None, _byte_ptr(b, b_off) if b is not None else None,
+        _byte_ptr(c, c_off) if c is not None else None, _byte_ptr(p, p_off) if p is not None else None,
+        op, n, c1, c2, a_s1, a_s2, b_s1, b_s2, c_s1, c_s2, int(eps), aux, bq_sh, win_lo, win_hi,
+        _stream())
+    _lib.check(rc, "cm_rowops")
+
+
+def rowops_chain(seg: torch.Tensor, jobs: Sequence[dict]) -> None:
+    """A descriptor chain over one GPU byte segment: each job's a / b / c / p are byte
+    offsets into ``seg`` (the layout of the reference's chain fixtures)."""
+    descs = (_lib.CmRowopsDesc * len(jobs))()
+    base = seg.data_ptr()
+    for d, j in zip(descs, jobs):
+        ext = rowops_extents(j["op"], j["n"], j["c1"], j["c2"], j["a_s1"], j["a_s2"], j["b_s1"],
+                             j["b_s2"], j["c_s1"], j["c_s2"], j.get("aux", 0), j.get("win_lo", 0),
+                             j.get("win_hi", 0xFFFFFFFF))
+        if ext is not None:
+            (a_lo, a_hi), b_end, c_end, p_end = ext
+            for key, lo, hi in (("a", a_lo, a_hi), ("b", 0, b_end), ("c", 0, c_end), ("p", 0, p_end)):
+                if hi > lo and (j[key] + lo < 0 or j[key] + hi > seg.numel()):
+                    raise ValueError(f"rowops chain: job {j.get('label')} {key} leaves the segment")
+        for f in ("op", "n", "c1", "c2", "a_s1", "a_s2", "b_s1", "b_s2", "c_s1", "c_s2", "aux",
+                  "bq_sh", "win_lo", "win_hi"):
+            setattr(d, f, int(j.get(f, 0xFFFFFFFF if f == "win_hi" else 0)))
+        d.eps = int(j.get("eps", 0))
+        for key in ("a", "b", "c", "p"):
+            setattr(d, key, base + int(j[key]))
+    rc = _lib.lib().cm_rowops_chain(descs, len(jobs), _stream())
+    _lib.check(rc, "cm_rowops_chain")
+
+
+def host_act_table(act: int):
+    """The library's full activation table (act 4..6) as a numpy int16 array."""
+    import numpy as np
+    out = np.zeros(65536, np.int16)
+    _lib.check(_lib.lib().cm_host_act_table(act, out.ctypes.data), "cm_host_act_table")
+    return out
+
+
+def host_rowops_table_image():
+    import numpy as np
+    out = np.zeros(65536, np.uint8)
+    _lib.check(_lib.lib().cm_host_rowops_table_image(out.ctypes.data), "cm_host_rowops_table_image")
+    return out

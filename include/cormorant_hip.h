@@ -1,0 +1,153 @@
+/*
+ * cormorant_hip.h -- C ABI of libcormo_hip.so: the five units of the fixed-point simulator
+ * (VectorOP with its activation and softmax units, Matmul, Conv, Pooling, RowOps) as
+ * gfx950 HIP kernels.
+ *
+ * Conventions (all entry points):
+ *   - Tensors are DEVICE pointers to raw two's-complement lanes (value = raw * 2^-f):
+ *     int16 unless stated, int32 / float32 where a row-ops kind says so.  The caller owns
+ *     every buffer; outputs are written into preallocated memory.
+ *   - Counts and strides are the reference unit's register values (elements unless a
+ *     register is documented in bytes).
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream).  Calls are
+ *     asynchronous on that stream; they are thread-safe per stream.
+ *   - Return value: CM_OK (0) or a negative CM_E* status; cm_last_error() describes the
+ *     last failure of the calling thread.  Nothing throws across the ABI.
+ *
+ * Each entry point cites the reference interface it replaces (paths relative to the
+ * reference checkout).
+ */
+#ifndef CORMORANT_HIP_H
+#define CORMORANT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CM_OK 0
+#define CM_EINVAL (-1)   /* a register value outside the unit's contract */
+#define CM_EALIGN (-2)   /* a pointer or stride breaks the 16-byte word contract */
+#define CM_EHIP (-3)     /* a HIP runtime call failed */
+#define CM_ENOMEM (-4)   /* workspace allocation failed */
+
+/* Version of this ABI (major * 100 + minor). */
+int cm_abi_version(void);
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* cm_last_error(void);
+
+/* Prepare the current device: builds the activation tables (glibc double formulas,
+ * vectorop_act.py:60-114), the softmax exponential table (vectorop_smx.py:29-34) and the
+ * row-ops table image (rowops_spec.py:605-616) and uploads them.  Every entry point calls
+ * it on first use of a device; calling it first keeps that work out of timed regions. */
+int cm_init(void);
+
+/* Host-side copies of the tables cm_init builds (no device work): the full 65 536-entry
+ * activation table of act 4 (SiLU), 5 (GELU erf) or 6 (GELU tanh), ascending raw input
+ * (vectorop_act.kernel_table, vectorop_act.py:107-114); and the 64 KiB row-ops table image
+ * (rowops_spec.table_image, rowops_spec.py:605-616). */
+int cm_host_act_table(int act, int16_t* out65536);
+int cm_host_rowops_table_image(uint8_t* out65536);
+
+/* ---------------------------------------------------------------- VectorOP
+ * Replaces VectorOPKernel (kernels/vectorop_rtl/model/include/VectorOP.h:319-333) and the
+ * simulator's VectorOP branch (inference-scheduler/src/codegen/_simulate.py:721-765), the
+ * activation unit (vectorop_act.py:60-114) and the softmax unit
+ * (vectorop_smx.py:37-79, smx_nodes.py:121-338):
+ *   op 0..9: c[o*(a_inc+b_inc) + i] = act(op(a[o*a_inc + i], b[o*b_inc + i])),
+ *            o < outer, i < size; b is not read for the unary ops (op >= 4);
+ *   op 10:   softmax rows: row o at a + o*a_inc -> c + o*b_inc, o < outer;
+ *   op 11:   softmax columns: s[size keys][outer queries] (row stride a_inc) ->
+ *            P[q][size] at c + q*b_inc for q < (outer & ~15).
+ * Every run is written as whole 8-lane (16-byte) words, the lanes past `size` 0, so `c`
+ * must cover them; a, b, c 16-byte aligned; a_inc and b_inc multiples of 8 (or 0) for
+ * ops 0..9 (the unit's alignment contract, VectorOP.h:222-236).  Softmax rows take
+ * size <= 65535.  DIV follows the simulator: trunc(a*256/b) saturated, b == 0 gives
+ * +32767 (a > 0), -32768 (a < 0), 0 (a == 0). */
+int cm_vectorop(const int16_t* a, const int16_t* b, int16_t* c, uint32_t size, uint32_t op,
+                uint32_t outer, uint32_t a_inc, uint32_t b_inc, uint32_t act, uint32_t alpha,
+                uint32_t smx_cm, uint32_t smx_cfg, uint32_t smx_mask, void* stream);
+
+/* ---------------------------------------------------------------- Matmul
+ * Replaces MatmulKernel (kernels/matmul_rtl/model/include/MatmulKernel.h:228-242) and the
+ * simulator's MatMul branches (_simulate.py:620-633 Q8.8, :814-835 power-of-two):
+ *   C[bt][i][j] = sat16(floor(acc / 2^8)), acc = sum_kk A[bt][i][kk] * B[bt][kk][j]
+ * with n rows of A, k inner, m columns of B, `batch` slices a_bs / b_bs / c_bs elements
+ * apart (0 = broadcast).  acc is exact (wrap32 = 0, the simulator's Q8.8 path) or wrapped
+ * to int32 first (wrap32 = 1, the power-of-two path).  B image: b_packed = 0 row-major
+ * [k][m]; 1 the tile-major packed layout ((j/32)*k + kk)*32 + j%32 (MatmulKernel.h:91-113);
+ * gemv_kw in {1,2,4,8} the kernel-width image (MatmulKernel.h:115-156).  C is row-major
+ * [n][m].  Limits: 1 <= k <= 65536 (the unit's 4096 is not needed here). */
+int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
+              uint32_t m, uint32_t batch, int64_t a_bs, int64_t b_bs, int64_t c_bs,
+              uint32_t b_packed, uint32_t gemv_kw, uint32_t wrap32, void* stream);
+
+/* ---------------------------------------------------------------- Conv
+ * Replaces ConvKernel (kernels/conv_rtl/model/include/ConvKernel.h:229-259) and the
+ * simulator's Conv branches (_simulate.py:121-220, 643-660, 784-812): NCHW x, packed
+ * weights (ConvKernel.h:136-159: [out_ch][ceil(in_ch/16)][kh][kw][16 or 8 lanes];
+ * depthwise [out_ch][roundup(kh*kw, 8)]), bias [roundup(out_ch, 8)] when has_bias,
+ *   y = sat16(floor((bias << 8 + sum x*w) / 2^8))  (wrap32: the sum wraps to int32 first),
+ * implicit zero padding, and the y channel pattern: channel c's plane at
+ * (c mod y_cn)*y_cs + (c div y_cn)*y_gs (y_cs = 0: out_h*out_w, y_cn = 0: one group;
+ * batch must be 1 when either is set).  kh, kw <= 7 (the unit's bound). */
+int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
+            uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
+            uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
+            uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
+            uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise, uint32_t y_cs,
+            uint32_t y_cn, uint32_t y_gs, uint32_t wrap32, void* stream);
+
+/* ---------------------------------------------------------------- Pooling
+ * Replaces PoolingKernel (kernels/pool_rtl/model/include/PoolingKernel.h:120-140) and the
+ * simulator's pool reference (_simulate.py:230-358, 701-719): pool_type 0 MAX, 1 AVG
+ * (sum * round(2^23/d) >> 23), 2 LP (lp_order 1: sum |x|; 2: the polynomial square root);
+ * NCHW in and out. */
+int cm_pool(const int16_t* x, int16_t* y, uint32_t batch, uint32_t channels, uint32_t in_h,
+            uint32_t in_w, uint32_t out_h, uint32_t out_w, uint32_t pool_h, uint32_t pool_w,
+            uint32_t stride_h, uint32_t stride_w, uint32_t pad_top, uint32_t pad_left,
+            uint32_t dil_h, uint32_t dil_w, uint32_t pool_type, uint32_t lp_order,
+            uint32_t count_include_pad, void* stream);
+
+/* ---------------------------------------------------------------- RowOps
+ * Replaces one RowOpsKernel job: the register block of
+ * doc/kernels/ROWOPS_RTL_KERNEL.md section 1.2 (driven by run_rowops,
+ * inference-scheduler/src/rowops_nodes.py:143-151) with the integer specifications of
+ * inference-scheduler/src/rowops_spec.py.  a, b, c, p are device byte addresses (the
+ * registers 0x20 / 0x30 / 0x40 / 0x50), every stride in BYTES; op carries the code [3:0],
+ * the kinds and the flags (B_EN, P_BCAST, P_KEEP, RELU, NORM_LN, SCALE).  Row outputs
+ * are whole 16-byte words, the lanes past n written 0 (TRANSPOSE with scattered granules
+ * writes exactly its granules).  The parameter RAM is emulated per device: a job that
+ * loads parameters copies its block into it, a P_KEEP job reads what the last load left.
+ * TLOAD (op 8) loads the table image from `a` (4096 int32 words in order). */
+int cm_rowops(const void* a, const void* b, void* c, const void* p, uint32_t op, uint32_t n,
+              uint32_t c1, uint32_t c2, uint32_t a_s1, uint32_t a_s2, uint32_t b_s1,
+              uint32_t b_s2, uint32_t c_s1, uint32_t c_s2, int64_t eps, uint32_t aux,
+              uint32_t bq_sh, uint32_t win_lo, uint32_t win_hi, void* stream);
+
+/* One row-ops descriptor (ROWOPS_RTL_KERNEL.md section 1.6: the argument registers
+ * 0x10 .. 0x6C in register order), pointers as device addresses. */
+typedef struct cm_rowops_desc {
+    uint32_t op, n, c1, c2;
+    uint64_t a;
+    uint32_t a_s1, a_s2;
+    uint64_t b;
+    uint32_t b_s1, b_s2;
+    uint64_t c;
+    uint32_t c_s1, c_s2;
+    uint64_t p;
+    int64_t eps;
+    uint32_t aux, bq_sh, win_lo, win_hi;
+} cm_rowops_desc;
+
+/* A descriptor chain: the jobs of a HOST array in order on `stream`, each reading what
+ * the previous ones wrote (ROWOPS_RTL_KERNEL.md section 1.6; no 16-job cap). */
+int cm_rowops_chain(const cm_rowops_desc* jobs, uint32_t n_jobs, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CORMORANT_HIP_H */
