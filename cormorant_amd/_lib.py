@@ -39,7 +39,27 @@ SIGNATURES = {
     "cm_pool": (_I32, [_P, _P] + [_U32] * 17 + [_P]),
     "cm_rowops": (_I32, [_P, _P, _P, _P] + [_U32] * 10 + [_I64] + [_U32] * 4 + [_P]),
     "cm_rowops_chain": (_I32, [ctypes.POINTER(CmRowopsDesc), _U32, _P]),
+    "cm_timing_enable": (_I32, [_I32]),
+    "cm_timing_read": (_I32, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
+                              ctypes.POINTER(ctypes.c_uint64)]),
+    "cm_timing_reset": (_I32, []),
 }
+
+
+def timing_enable(on: bool) -> None:
+    check(lib().cm_timing_enable(1 if on else 0), "cm_timing_enable")
+
+
+def timing_reset() -> None:
+    check(lib().cm_timing_reset(), "cm_timing_reset")
+
+
+def timing_read(kernel: str):
+    """(total milliseconds, launches) of the recorded launches of ``kernel``."""
+    ms = ctypes.c_double(0.0)
+    n = ctypes.c_uint64(0)
+    check(lib().cm_timing_read(kernel.encode(), ctypes.byref(ms), ctypes.byref(n)), "cm_timing_read")
+    return ms.value, n.value
 
 _lib = None
 

@@ -51,6 +51,29 @@ int state(DeviceState** out);
 // for the device).
 int workspace(DeviceState* st, size_t bytes, void** out);
 
+// Records a HIP event pair around the launches in its scope while timing is enabled
+// (cm_timing_enable); `name` must be a string literal.
+class TimedLaunch {
+  public:
+    TimedLaunch(const char* name, hipStream_t s);
+    ~TimedLaunch();
+    TimedLaunch(const TimedLaunch&) = delete;
+    TimedLaunch& operator=(const TimedLaunch&) = delete;
+
+  private:
+    int slot_ = -1;
+    hipStream_t s_;
+};
+
+// Launch `kernel` on `stream` under the timing name `name` (a string literal) and check
+// the launch; the launch is timed while timing is enabled.
+#define CM_LAUNCH(name, kernel, grid, block, shmem, stream, ...)                     \
+    do {                                                                             \
+        ::cm::TimedLaunch tl_(name, stream);                                        \
+        hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);        \
+    } while (0);                                                                     \
+    CM_LAUNCH_CHECK(name)
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }

@@ -358,13 +358,11 @@ struct Planes {
 
 template <class Src, bool KFast>
 int run_split(const Src& src, uint64_t src_slice, Planes& pl, hipStream_t s) {
-    hipLaunchKernelGGL((split_kernel<Src, KFast>), dim3(pl.lines_p / 64, pl.nslab, pl.slices), dim3(256),
+    CM_LAUNCH("split_kernel", (split_kernel<Src, KFast>), dim3(pl.lines_p / 64, pl.nslab, pl.slices), dim3(256),
                        0, s, src, src_slice, pl.hi, pl.lo, pl.part, pl.lines_p, pl.kp, pl.nslab);
-    CM_LAUNCH_CHECK("split_kernel");
     const uint64_t n = (uint64_t)pl.lines_p * pl.slices;
-    hipLaunchKernelGGL(sum_slabs_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, s, pl.part, pl.sum,
+    CM_LAUNCH("sum_slabs_kernel", sum_slabs_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, s, pl.part, pl.sum,
                        pl.lines_p, pl.nslab, pl.slices);
-    CM_LAUNCH_CHECK("sum_slabs_kernel");
     return CM_OK;
 }
 
@@ -375,10 +373,9 @@ int run_gemm(const Planes& A, const Planes& B, uint32_t batch, long long kconst,
     const uint64_t a_slice = A.slices > 1 ? (uint64_t)A.lines_p * A.kp : 0;
     const uint64_t b_slice = B.slices > 1 ? (uint64_t)B.lines_p * B.kp : 0;
     const uint64_t rs_slice = A.slices > 1 ? A.lines_p : 0, cs_slice = B.slices > 1 ? B.lines_p : 0;
-    hipLaunchKernelGGL(gemm_planes_kernel<Epi>, dim3(tiles_r * tiles_c, batch), dim3(256), 0, s, A.hi,
+    CM_LAUNCH("gemm_planes_kernel", gemm_planes_kernel<Epi>, dim3(tiles_r * tiles_c, batch), dim3(256), 0, s, A.hi,
                        A.lo, A.sum, a_slice, rs_slice, B.hi, B.lo, B.sum, b_slice, cs_slice, tiles_r,
                        tiles_c, A.kp, kconst, epi);
-    CM_LAUNCH_CHECK("gemm_planes_kernel");
     return CM_OK;
 }
 
@@ -452,11 +449,10 @@ extern "C" int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, 
         const uint64_t total = (uint64_t)batch * out_ch * plane;
         uint64_t blocks = (total + 255) / 256;
         if (blocks > 65536ull * 8) blocks = 65536ull * 8;
-        hipLaunchKernelGGL(conv_dw_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, w, bptr, y, total,
+        CM_LAUNCH("conv_dw_kernel", conv_dw_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, w, bptr, y, total,
                            out_ch, in_h, in_w, out_h, out_w, kh, kw, stride_h, stride_w, dilation_h,
                            dilation_w, pad_top, pad_left, (kh * kw + 7) & ~7u, cs, y_cn, y_gs,
                            wrap32 ? 1u : 0u);
-        CM_LAUNCH_CHECK("conv_dw_kernel");
         return CM_OK;
     }
     const uint32_t tiles = (in_ch + 15) / 16;

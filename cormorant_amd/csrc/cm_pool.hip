@@ -125,14 +125,12 @@ extern "C" int cm_pool(const int16_t* x, int16_t* y, uint32_t batch, uint32_t ch
     const bool global = out_h == 1 && out_w == 1 && pool_h == in_h && pool_w == in_w &&
                         pad_top == 0 && pad_left == 0 && dil_h == 1 && dil_w == 1;
     if (global) {
-        hipLaunchKernelGGL(pool_global_kernel, dim3((unsigned)((planes + 3) / 4)), dim3(256), 0, s,
+        CM_LAUNCH("pool_global_kernel", pool_global_kernel, dim3((unsigned)((planes + 3) / 4)), dim3(256), 0, s,
                            x, y, planes, g);
-        CM_LAUNCH_CHECK("pool_global_kernel");
     } else {
         uint64_t blocks = (total + 255) / 256;
         if (blocks > 65536ull * 8) blocks = 65536ull * 8;
-        hipLaunchKernelGGL(pool_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, total, g);
-        CM_LAUNCH_CHECK("pool_kernel");
+        CM_LAUNCH("pool_kernel", pool_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, total, g);
     }
     return CM_OK;
 }

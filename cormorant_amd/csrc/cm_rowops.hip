@@ -312,9 +312,8 @@ int run_job(DeviceState* st, const Job& j, const uint8_t* p, hipStream_t s) {
     const uint32_t code = j.op & 15;
     if (code == RO_TLOAD) {
         if (j.n == 0 || j.c1 == 0 || j.c2 == 0) return CM_OK;
-        hipLaunchKernelGGL(ro_tload_kernel, dim3(grid_for((u64)j.n * j.c1 * j.c2)), dim3(256), 0, s, j,
+        CM_LAUNCH("ro_tload_kernel", ro_tload_kernel, dim3(grid_for((u64)j.n * j.c1 * j.c2)), dim3(256), 0, s, j,
                            st->ro_tables);
-        CM_LAUNCH_CHECK("ro_tload_kernel");
         return CM_OK;
     }
     if (code == RO_FOLD) {
@@ -322,8 +321,7 @@ int run_job(DeviceState* st, const Job& j, const uint8_t* p, hipStream_t s) {
         if (j.n == 0 || j.c1 == 0 || j.c2 == 0 || m == 0) return CM_OK;
         if (reinterpret_cast<uintptr_t>(j.c) & 15) return fail(CM_EALIGN, "rowops FOLD: c not 16-byte aligned");
         const u64 total = ((u64)j.c2 * j.c1 * j.n + 7) & ~7ull;
-        hipLaunchKernelGGL(ro_fold_kernel, dim3(grid_for(total)), dim3(256), 0, s, j);
-        CM_LAUNCH_CHECK("ro_fold_kernel");
+        CM_LAUNCH("ro_fold_kernel", ro_fold_kernel, dim3(grid_for(total)), dim3(256), 0, s, j);
         return CM_OK;
     }
     if (j.n == 0 || j.c1 == 0 || j.c2 == 0) return CM_OK;
@@ -331,8 +329,7 @@ int run_job(DeviceState* st, const Job& j, const uint8_t* p, hipStream_t s) {
     if (code == RO_XPOSE) {
         const uint32_t R = j.aux & 15;
         if (R == 0 || R > 8) return CM_OK;        // outside the contract: the unit writes nothing
-        hipLaunchKernelGGL(ro_xpose_kernel, dim3(grid_for((u64)j.n * R * j.c1 * j.c2)), dim3(256), 0, s, j);
-        CM_LAUNCH_CHECK("ro_xpose_kernel");
+        CM_LAUNCH("ro_xpose_kernel", ro_xpose_kernel, dim3(grid_for((u64)j.n * R * j.c1 * j.c2)), dim3(256), 0, s, j);
         return CM_OK;
     }
     if (code < RO_COPY || code > RO_GATE) return fail(CM_EINVAL, "rowops: op code %u", code);
@@ -362,16 +359,14 @@ int run_job(DeviceState* st, const Job& j, const uint8_t* p, hipStream_t s) {
         st->pram_bcast = bcast_job;
     }
     if (code == RO_NORM) {
-        hipLaunchKernelGGL(ro_norm_kernel, dim3(grid_for((u64)j.c1 * j.c2, 4)), dim3(256), 0, s, j, params,
+        CM_LAUNCH("ro_norm_kernel", ro_norm_kernel, dim3(grid_for((u64)j.c1 * j.c2, 4)), dim3(256), 0, s, j, params,
                            dst, entries, bcast, st->ro_tables);
-        CM_LAUNCH_CHECK("ro_norm_kernel");
         return CM_OK;
     }
     const uint32_t cb = code == RO_DEQUANT ? 4 : (((j.op >> 8) & 3) == 0 ? 2 : 4);
     const u64 words = (u64)((j.n * cb + 15) / 16) * j.c1 * j.c2;
-    hipLaunchKernelGGL(ro_stream_kernel, dim3(grid_for(words)), dim3(256), 0, s, j, params, dst, entries,
+    CM_LAUNCH("ro_stream_kernel", ro_stream_kernel, dim3(grid_for(words)), dim3(256), 0, s, j, params, dst, entries,
                        bcast, st->ro_tables);
-    CM_LAUNCH_CHECK("ro_stream_kernel");
     return CM_OK;
 }
 

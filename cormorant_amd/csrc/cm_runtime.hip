@@ -154,9 +154,81 @@ int workspace(DeviceState* st, size_t bytes, void** out) {
     return CM_OK;
 }
 
+// ---------------------------------------------------------------- kernel timing
+struct TimingRecord {
+    const char* name;
+    hipEvent_t start, stop;
+};
+static std::mutex g_tmu;
+static bool g_timing = false;
+static std::vector<TimingRecord> g_records;
+static std::vector<hipEvent_t> g_free_events;
+
+static hipEvent_t take_event() {
+    if (!g_free_events.empty()) {
+        hipEvent_t e = g_free_events.back();
+        g_free_events.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+TimedLaunch::TimedLaunch(const char* name, hipStream_t s) : s_(s) {
+    std::lock_guard<std::mutex> lk(g_tmu);
+    if (!g_timing) return;
+    TimingRecord r{name, take_event(), take_event()};
+    if (!r.start || !r.stop) return;
+    if (hipEventRecord(r.start, s) != hipSuccess) return;
+    g_records.push_back(r);
+    slot_ = (int)g_records.size() - 1;
+}
+
+TimedLaunch::~TimedLaunch() {
+    if (slot_ < 0) return;
+    std::lock_guard<std::mutex> lk(g_tmu);
+    if (slot_ < (int)g_records.size()) hipEventRecord(g_records[slot_].stop, s_);
+}
+
 }  // namespace cm
 
 extern "C" {
+
+int cm_timing_enable(int on) {
+    std::lock_guard<std::mutex> lk(cm::g_tmu);
+    cm::g_timing = on != 0;
+    return CM_OK;
+}
+
+int cm_timing_reset(void) {
+    std::lock_guard<std::mutex> lk(cm::g_tmu);
+    for (auto& r : cm::g_records) {
+        hipEventSynchronize(r.stop);
+        cm::g_free_events.push_back(r.start);
+        cm::g_free_events.push_back(r.stop);
+    }
+    cm::g_records.clear();
+    return CM_OK;
+}
+
+int cm_timing_read(const char* kernel, double* total_ms, uint64_t* launches) {
+    std::lock_guard<std::mutex> lk(cm::g_tmu);
+    double sum = 0.0;
+    uint64_t n = 0;
+    for (auto& r : cm::g_records) {
+        if (std::strcmp(r.name, kernel) != 0) continue;
+        CM_HIP_CHECK(hipEventSynchronize(r.stop));
+        float ms = 0.f;
+        CM_HIP_CHECK(hipEventElapsedTime(&ms, r.start, r.stop));
+        sum += ms;
+        n++;
+    }
+    if (total_ms) *total_ms = sum;
+    if (launches) *launches = n;
+    return CM_OK;
+}
+
 
 int cm_abi_version(void) { return 100; }
 

@@ -250,9 +250,8 @@ int launch_ew(const int16_t* a, const int16_t* b, int16_t* c, uint32_t size, uin
         tab = st->act_tab + (act - ACT_SILU) * kActTabBytes;
         len = st->act_len[act - ACT_SILU];
     }
-    hipLaunchKernelGGL(vectorop_kernel<OP>, dim3((unsigned)blocks), dim3(threads), 0, s, a, b, c,
+    CM_LAUNCH("vectorop_kernel", vectorop_kernel<OP>, dim3((unsigned)blocks), dim3(threads), 0, s, a, b, c,
                        size, outer, (uint64_t)a_inc, (uint64_t)b_inc, act, alpha, tab, len);
-    CM_LAUNCH_CHECK("vectorop_kernel");
     return CM_OK;
 }
 
@@ -280,15 +279,13 @@ extern "C" int cm_vectorop(const int16_t* a, const int16_t* b, int16_t* c, uint3
         if (b_inc & 7) return fail(CM_EALIGN, "softmax: output stride %u not a multiple of 8", b_inc);
         if (op == OP_SOFTMAX) {
             if (a_inc & 7) return fail(CM_EALIGN, "softmax rows: input stride %u not a multiple of 8", a_inc);
-            hipLaunchKernelGGL(softmax_rows_kernel, dim3(ceil_div(outer, 4)), dim3(256), 0, s, a, c,
+            CM_LAUNCH("softmax_rows_kernel", softmax_rows_kernel, dim3(ceil_div(outer, 4)), dim3(256), 0, s, a, c,
                                size, outer, (uint64_t)a_inc, (uint64_t)b_inc, r, st->smx_tab);
-            CM_LAUNCH_CHECK("softmax_rows_kernel");
         } else {
             uint32_t nq = outer & ~15u;
             if (nq == 0) return CM_OK;
-            hipLaunchKernelGGL(softmax_cols_kernel, dim3(ceil_div(nq, 64)), dim3(256), 0, s, a, c,
+            CM_LAUNCH("softmax_cols_kernel", softmax_cols_kernel, dim3(ceil_div(nq, 64)), dim3(256), 0, s, a, c,
                                size, nq, (uint64_t)a_inc, (uint64_t)b_inc, r, st->smx_tab);
-            CM_LAUNCH_CHECK("softmax_cols_kernel");
         }
         return CM_OK;
     }

@@ -51,6 +51,15 @@ int cm_init(void);
 int cm_host_act_table(int act, int16_t* out65536);
 int cm_host_rowops_table_image(uint8_t* out65536);
 
+/* Kernel timing (the role of the board runtime's per-call profiler,
+ * inference-scheduler/runtime/inference_prof.c): while enabled, every kernel launch of the
+ * library records a HIP event pair on its stream.  cm_timing_read waits for the recorded
+ * launches of `kernel` (a name such as "gemm_planes_kernel") and returns their summed
+ * duration and count; cm_timing_reset drops every record. */
+int cm_timing_enable(int on);
+int cm_timing_read(const char* kernel, double* total_ms, uint64_t* launches);
+int cm_timing_reset(void);
+
 /* ---------------------------------------------------------------- VectorOP
  * Replaces VectorOPKernel (kernels/vectorop_rtl/model/include/VectorOP.h:319-333) and the
  * simulator's VectorOP branch (inference-scheduler/src/codegen/_simulate.py:721-765), the
