@@ -25,7 +25,6 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128, BN = 128, BK = 64;     // output tile; k step in elements (= plane bytes)
-constexpr int LDSR = BK + 16;                  // LDS row pitch in bytes: conflict-free b128 reads
 constexpr int SLAB = 1024;                     // k per partial-sum slab
 
 __device__ __forceinline__ uint32_t pack_hi(const int16_t* v) {   // 4 high bytes
@@ -147,6 +146,119 @@ __global__ __launch_bounds__(256) void split_kernel(Src src, uint64_t src_slice,
     if ((t & 3) == 0) part[((uint64_t)bt * nslab + slab) * lines_p + l0 + my_line] = sum;
 }
 
+// ---------------------------------------------------------------- bandwidth split kernels
+// Padding is written as the value 128 (A' = 0: the byte pair (0, 0)) and left out of the sums.
+constexpr int16_t kPad = 128;
+
+// Rows with k contiguous (the matmul A, row stride lda, 16-byte aligned rows): one wavefront
+// per row, 8 k per lane per 16-byte load; grid (ceil(lines_p / 4), nslab, slices).
+__global__ __launch_bounds__(256) void split_rows_kernel(const int16_t* __restrict__ src, uint64_t slice,
+                                                         uint64_t lda, uint32_t rows, uint32_t k,
+                                                         int8_t* __restrict__ hi, int8_t* __restrict__ lo,
+                                                         int32_t* __restrict__ part, uint32_t lines_p,
+                                                         uint32_t kp, uint32_t nslab) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6), slab = blockIdx.y, bt = blockIdx.z;
+    if (row >= lines_p) return;
+    const int16_t* r = src + bt * slice + (uint64_t)row * lda;
+    const uint64_t po = ((uint64_t)bt * lines_p + row) * kp;
+    int32_t sum = 0;
+    const uint32_t k_end = min(kp, (slab + 1) * SLAB);
+    for (uint32_t k0 = slab * SLAB + 8 * lane; k0 < k_end; k0 += 512) {
+        int4 v;
+        if (row < rows && k0 + 8 <= k) {
+            v = *reinterpret_cast<const int4*>(r + k0);
+        } else {
+            int16_t e[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) e[q] = (row < rows && k0 + q < k) ? r[k0 + q] : kPad;
+            v = *reinterpret_cast<const int4*>(e);
+        }
+        const int16_t* e = reinterpret_cast<const int16_t*>(&v);
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            if (row < rows && k0 + q < k) sum += e[q];
+        const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+        // high bytes (1, 3 of each dword) and low bytes (0, 2) of 8 lanes
+        const uint32_t h0 = __builtin_amdgcn_perm(w[1], w[0], 0x07050301u);
+        const uint32_t h1 = __builtin_amdgcn_perm(w[3], w[2], 0x07050301u);
+        const uint32_t l0 = __builtin_amdgcn_perm(w[1], w[0], 0x06040200u) ^ 0x80808080u;
+        const uint32_t l1 = __builtin_amdgcn_perm(w[3], w[2], 0x06040200u) ^ 0x80808080u;
+        *reinterpret_cast<uint2*>(hi + po + k0) = make_uint2(h0, h1);
+        *reinterpret_cast<uint2*>(lo + po + k0) = make_uint2(l0, l1);
+    }
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    if (lane == 0) part[((uint64_t)bt * nslab + slab) * lines_p + row] = sum;
+}
+
+// Columns of a k-major image (row-major B [k][m] with m % 8 == 0, or the packed 32-column
+// tiles): lane = 4 consecutive k, wave = 8 columns, workgroup = 32 columns; each lane loads
+// 4 rows x 8 columns and transposes them in registers (byte permutes) into one dword of 4 k
+// per column and plane, so a wavefront writes 256 contiguous bytes of each output line.
+// Grid (ceil(lines_p / 32), nslab, slices).
+__global__ __launch_bounds__(256) void split_cols_kernel(const int16_t* __restrict__ src, uint64_t slice,
+                                                         uint32_t packed, uint32_t m, uint32_t k,
+                                                         int8_t* __restrict__ hi, int8_t* __restrict__ lo,
+                                                         int32_t* __restrict__ part, uint32_t lines_p,
+                                                         uint32_t kp, uint32_t nslab) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t j0 = blockIdx.x * 32 + (threadIdx.x >> 6) * 8, slab = blockIdx.y, bt = blockIdx.z;
+    if (j0 >= lines_p) return;
+    const int16_t* b = src + bt * slice;
+    int32_t sum[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const uint32_t k_end = min(kp, (slab + 1) * SLAB);
+    const bool cols_real = j0 + 8 <= m;
+    for (uint32_t k0 = slab * SLAB + 4 * lane; k0 < k_end; k0 += 256) {
+        uint32_t d[4][4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const uint32_t kk = k0 + r;
+            int4 v;
+            if (kk < k && cols_real) {
+                const uint64_t off = packed ? ((uint64_t)(j0 >> 5) * k + kk) * 32 + (j0 & 31)
+                                            : (uint64_t)kk * m + j0;
+                v = *reinterpret_cast<const int4*>(b + off);
+            } else {
+                int16_t e[8];
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const uint32_t j = j0 + q;
+                    const uint64_t off = packed ? ((uint64_t)(j >> 5) * k + kk) * 32 + (j & 31)
+                                                : (uint64_t)kk * m + j;
+                    e[q] = (kk < k && j < m) ? b[off] : kPad;
+                }
+                v = *reinterpret_cast<const int4*>(e);
+            }
+            d[r][0] = (uint32_t)v.x; d[r][1] = (uint32_t)v.y; d[r][2] = (uint32_t)v.z; d[r][3] = (uint32_t)v.w;
+            const int16_t* e = reinterpret_cast<const int16_t*>(&v);
+            if (kk < k) {
+#pragma unroll
+                for (int q = 0; q < 8; q++)
+                    if (j0 + q < m) sum[q] += e[q];
+            }
+        }
+#pragma unroll
+        for (int c2 = 0; c2 < 4; c2++) {               // columns 2 c2 and 2 c2 + 1
+            const uint32_t xh = __builtin_amdgcn_perm(d[1][c2], d[0][c2], 0x07030501u);
+            const uint32_t yh = __builtin_amdgcn_perm(d[3][c2], d[2][c2], 0x07030501u);
+            const uint32_t xl = __builtin_amdgcn_perm(d[1][c2], d[0][c2], 0x06020400u);
+            const uint32_t yl = __builtin_amdgcn_perm(d[3][c2], d[2][c2], 0x06020400u);
+            const uint64_t o0 = ((uint64_t)bt * lines_p + j0 + 2 * c2) * kp + k0;
+            const uint64_t o1 = o0 + kp;
+            *reinterpret_cast<uint32_t*>(hi + o0) = __builtin_amdgcn_perm(yh, xh, 0x05040100u);
+            *reinterpret_cast<uint32_t*>(hi + o1) = __builtin_amdgcn_perm(yh, xh, 0x07060302u);
+            *reinterpret_cast<uint32_t*>(lo + o0) = __builtin_amdgcn_perm(yl, xl, 0x05040100u) ^ 0x80808080u;
+            *reinterpret_cast<uint32_t*>(lo + o1) = __builtin_amdgcn_perm(yl, xl, 0x07060302u) ^ 0x80808080u;
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        int32_t v = sum[q];
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        if (lane == 0) part[((uint64_t)bt * nslab + slab) * lines_p + j0 + q] = v;
+    }
+}
+
 // line sums = the sum of the slab partials
 __global__ void sum_slabs_kernel(const int32_t* __restrict__ part, int32_t* __restrict__ out,
                                  uint32_t lines_p, uint32_t nslab, uint32_t slices) {
@@ -159,17 +271,16 @@ __global__ void sum_slabs_kernel(const int32_t* __restrict__ part, int32_t* __re
 }
 
 // ---------------------------------------------------------------- epilogues
+// An epilogue names where output row `i` of slice `bt` starts (nullptr past the last row)
+// and adds a per-row bias to the sum; columns are contiguous within a row.
 struct EpiMatmul {              // C[bt][i][j] = c + bt * c_bs + i * m + j
     int16_t* c;
     uint64_t c_bs;
     uint32_t rows, cols, wrap;
-    __device__ void store(uint32_t bt, uint32_t i, uint32_t j, long long acc) const {
-        if (i >= rows || j >= cols) return;
-        if (wrap) acc = (long long)(int32_t)(uint32_t)(unsigned long long)acc;
-        long long q = acc >> 8;
-        c[bt * c_bs + (uint64_t)i * cols + j] = (int16_t)(q > 32767 ? 32767 : (q < -32768 ? -32768 : q));
-    }
     __device__ long long row_bias(uint32_t) const { return 0; }
+    __device__ int16_t* row_ptr(uint32_t bt, uint32_t i) const {
+        return i < rows ? c + bt * c_bs + (uint64_t)i * cols : nullptr;
+    }
 };
 struct EpiConv {                // y pattern (ConvKernel.h:250-258); acc seeded with bias << 8
     int16_t* y;
@@ -177,26 +288,57 @@ struct EpiConv {                // y pattern (ConvKernel.h:250-258); acc seeded 
     uint64_t img;               // elements per image (out_ch * plane)
     uint32_t rows, cols, cs, cn, gs, wrap;
     __device__ long long row_bias(uint32_t i) const { return bias && i < rows ? (long long)bias[i] * 256 : 0; }
-    __device__ void store(uint32_t bt, uint32_t i, uint32_t j, long long acc) const {
-        if (i >= rows || j >= cols) return;
-        if (wrap) acc = (long long)(int32_t)(uint32_t)(unsigned long long)acc;
-        long long q = acc >> 8;
-        uint64_t base = cn ? (uint64_t)(i % cn) * cs + (uint64_t)(i / cn) * gs : (uint64_t)i * cs;
-        y[bt * img + base + j] = (int16_t)(q > 32767 ? 32767 : (q < -32768 ? -32768 : q));
+    __device__ int16_t* row_ptr(uint32_t bt, uint32_t i) const {
+        if (i >= rows) return nullptr;
+        const uint64_t base = cn ? (uint64_t)(i % cn) * cs + (uint64_t)(i / cn) * gs : (uint64_t)i * cs;
+        return y + bt * img + base;
     }
 };
 
+// The unit's output rule on the recombined sum: floor(acc / 2^8) saturated to int16, the
+// sum wrapped to int32 first on the power-of-two path.
+__device__ __forceinline__ int16_t out_rule(long long acc, uint32_t wrap) {
+    if (wrap) acc = (long long)(int32_t)(uint32_t)(unsigned long long)acc;
+    const long long q = acc >> 8;
+    return (int16_t)(q > 32767 ? 32767 : (q < -32768 ? -32768 : q));
+}
+
 // ---------------------------------------------------------------- the plane GEMM
 // Grid: x = output tiles of one slice (XCD-aware order), y = batch slice.  a_slice /
-// b_slice (plane elements per slice, 0 = broadcast), sum slices likewise.
+// b_slice (plane elements per slice, 0 = broadcast), sum slices likewise.  4 waves in a
+// 2 x 2 arrangement, 64 x 64 outputs each: 2 x 2 blocks of v_mfma_i32_32x32x32_i8 (the
+// i8 MFMA that sustains the full rate on gfx950), three int32 accumulators per block.
+//
+// Pipeline (one workgroup per CU, so the overlap is scheduled within each wave):
+//   * global -> LDS copies (global_load_lds_dwordx4, no registers) run two k steps ahead
+//     into a ring of three LDS stages;
+//   * a k step is two 32-k substeps; substep 1's fragments are read while substep 0's MFMAs
+//     run, and step k+1's stage is published (own copies waited for, barrier) between the
+//     substeps, so its substep-0 fragments are read while substep 1's MFMAs run.
+// LDS layout: per stage and plane a [128 rows][64 B] tile; row r holds its 16-byte chunk c
+// at chunk c ^ ((r >> 2) & 3), so any 16 consecutive rows of one chunk hit 16 distinct
+// bank groups.  A direct copy writes 1 KiB (16 rows) per wave instruction, lane l at 16 l.
+constexpr int STAGES = 3;
+constexpr int PLANE_TILE = BM * BK;            // 8 KiB
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ void lds_copy16(const int8_t* g, int8_t* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
+}
+
 template <class Epi>
 __global__ __launch_bounds__(256, 1) void gemm_planes_kernel(
     const int8_t* __restrict__ Ahi, const int8_t* __restrict__ Alo, const int32_t* __restrict__ rsum,
     uint64_t a_slice, uint64_t rs_slice, const int8_t* __restrict__ Bhi, const int8_t* __restrict__ Blo,
     const int32_t* __restrict__ csum, uint64_t b_slice, uint64_t cs_slice, uint32_t tiles_r,
     uint32_t tiles_c, uint32_t kp, long long kconst, Epi epi) {
-    __shared__ __attribute__((aligned(16))) int8_t sA[2][BM * LDSR];
-    __shared__ __attribute__((aligned(16))) int8_t sB[2][BN * LDSR];
+    // three LDS stages as separate arrays: with the loop unrolled by three every access
+    // names its stage statically, so the compiler can tell the in-flight copies into the
+    // other stages from the fragment reads and does not wait for them
+    __shared__ __attribute__((aligned(1024))) int8_t sm0[4][PLANE_TILE];   // Ah, Al, Bh, Bl
+    __shared__ __attribute__((aligned(1024))) int8_t sm1[4][PLANE_TILE];
+    __shared__ __attribute__((aligned(1024))) int8_t sm2[4][PLANE_TILE];
 
     // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so
     // give each XCD a contiguous range of tiles (column-major: tiles sharing a B column
@@ -206,96 +348,161 @@ __global__ __launch_bounds__(256, 1) void gemm_planes_kernel(
     if ((ntiles & 7) == 0) g = (g & 7) * (ntiles >> 3) + (g >> 3);
     const uint32_t tr = g % tiles_r, tc = g / tiles_r;
     const uint32_t bt = blockIdx.y;
-    const int8_t* ah = Ahi + bt * a_slice + (uint64_t)tr * BM * kp;
-    const int8_t* al = Alo + bt * a_slice + (uint64_t)tr * BM * kp;
-    const int8_t* bh = Bhi + bt * b_slice + (uint64_t)tc * BN * kp;
-    const int8_t* bl = Blo + bt * b_slice + (uint64_t)tc * BN * kp;
 
     const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
-    const uint32_t wr = wave >> 1, wc = wave & 1, li = lane & 15, lk = lane >> 4;
-    // global -> LDS: thread t copies rows (t >> 2) and (t >> 2) + 64, 16-byte chunk t & 3
-    const uint32_t ld_row = t >> 2, ld_chunk = (t & 3) * 16;
+    const uint32_t wr = wave >> 1, wc = wave & 1, l32 = lane & 31, lh = lane >> 5;
 
-    v4i hh[4][4], mid[4][4], ll[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) hh[i][j] = mid[i][j] = ll[i][j] = v4i{0, 0, 0, 0};
+    // copy assignment: wave w fills 16-row blocks 2w and 2w + 1 of each plane; lane l
+    // takes row 16 b + l / 4, physical chunk l % 4 = logical chunk (l % 4) ^ swizzle
+    const uint32_t crow0 = 32 * wave + (lane >> 2), crow1 = crow0 + 16;
+    const uint32_t cchunk0 = ((lane & 3) ^ ((crow0 >> 2) & 3)) * 16;
+    const uint32_t cchunk1 = ((lane & 3) ^ ((crow1 >> 2) & 3)) * 16;
+    const int8_t* src[4] = {Ahi + bt * a_slice + (uint64_t)tr * BM * kp, Alo + bt * a_slice + (uint64_t)tr * BM * kp,
+                            Bhi + bt * b_slice + (uint64_t)tc * BN * kp, Blo + bt * b_slice + (uint64_t)tc * BN * kp};
+    const uint64_t g0 = (uint64_t)crow0 * kp + cchunk0, g1 = (uint64_t)crow1 * kp + cchunk1;
+    const uint32_t dst0 = __builtin_amdgcn_readfirstlane(2048 * wave), dst1 = dst0 + 1024;
 
-    uint4 ra[4], rb[4];
-    auto gload = [&](uint32_t k0) {
+    // fragment read offsets: lane reads row base32 + l32, logical chunk 2 s + lh (substep s)
+    const uint32_t sw = (l32 >> 2) & 3;
+    const uint32_t fa_row = (wr * 64 + l32) * BK, fb_row = (wc * 64 + l32) * BK;
+    const uint32_t ch0 = ((0 + lh) ^ sw) * 16, ch1 = ((2 + lh) ^ sw) * 16;
+
+    v16i hh[2][2], mid[2][2], ll[2][2];
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const uint64_t ro = (uint64_t)(ld_row + 64 * h) * kp + k0 + ld_chunk;
-            ra[2 * h] = *reinterpret_cast<const uint4*>(ah + ro);
-            ra[2 * h + 1] = *reinterpret_cast<const uint4*>(al + ro);
-            rb[2 * h] = *reinterpret_cast<const uint4*>(bh + ro);
-            rb[2 * h + 1] = *reinterpret_cast<const uint4*>(bl + ro);
-        }
-    };
-    // the low planes of each stage (the high planes are sA / sB)
-    __shared__ __attribute__((aligned(16))) int8_t sAl[2][BM * LDSR];
-    __shared__ __attribute__((aligned(16))) int8_t sBl[2][BN * LDSR];
-    auto store_stage = [&](int st) {
+    for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const uint32_t off = (ld_row + 64 * h) * LDSR + ld_chunk;
-            *reinterpret_cast<uint4*>(&sA[st][off]) = ra[2 * h];
-            *reinterpret_cast<uint4*>(&sAl[st][off]) = ra[2 * h + 1];
-            *reinterpret_cast<uint4*>(&sB[st][off]) = rb[2 * h];
-            *reinterpret_cast<uint4*>(&sBl[st][off]) = rb[2 * h + 1];
-        }
-    };
+        for (int j = 0; j < 2; j++) hh[i][j] = mid[i][j] = ll[i][j] = v16i{};
+    // fragments: [substep][block]
+    v4i ah0[2], al0[2], bh0[2], bl0[2], ah1[2], al1[2], bh1[2], bl1[2];
 
     const uint32_t nk = kp / BK;
-    gload(0);
-    store_stage(0);
-    __syncthreads();
-    for (uint32_t kt = 0; kt < nk; kt++) {
-        const int st = kt & 1;
-        if (kt + 1 < nk) gload((kt + 1) * BK);
-        v4i fa_h[4], fa_l[4], fb_h[4], fb_l[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t ra_off = (wr * 64 + i * 16 + li) * LDSR + lk * 16;
-            const uint32_t rb_off = (wc * 64 + i * 16 + li) * LDSR + lk * 16;
-            fa_h[i] = *reinterpret_cast<const v4i*>(&sA[st][ra_off]);
-            fa_l[i] = *reinterpret_cast<const v4i*>(&sAl[st][ra_off]);
-            fb_h[i] = *reinterpret_cast<const v4i*>(&sB[st][rb_off]);
-            fb_l[i] = *reinterpret_cast<const v4i*>(&sBl[st][rb_off]);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                hh[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa_h[i], fb_h[j], hh[i][j], 0, 0, 0);
-                mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa_h[i], fb_l[j], mid[i][j], 0, 0, 0);
-                mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa_l[i], fb_h[j], mid[i][j], 0, 0, 0);
-                ll[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa_l[i], fb_l[j], ll[i][j], 0, 0, 0);
-            }
-        if (kt + 1 < nk) {
-            store_stage(st ^ 1);
-            __syncthreads();
-        }
+#define CM_ISSUE(SM, step)                                                        \
+    {                                                                             \
+        const uint64_t k_ = (uint64_t)(step) * BK;                                \
+        _Pragma("unroll") for (int p = 0; p < 4; p++) {                           \
+            lds_copy16(src[p] + g0 + k_, &SM[p][dst0]);                           \
+            lds_copy16(src[p] + g1 + k_, &SM[p][dst1]);                           \
+        }                                                                         \
+    }
+#define CM_FRAGS(SM, CH, AH, AL, BH, BL)                                                   \
+    _Pragma("unroll") for (int b = 0; b < 2; b++) {                                        \
+        AH[b] = *reinterpret_cast<const v4i*>(&SM[0][fa_row + b * 32 * BK + CH]);          \
+        AL[b] = *reinterpret_cast<const v4i*>(&SM[1][fa_row + b * 32 * BK + CH]);          \
+        BH[b] = *reinterpret_cast<const v4i*>(&SM[2][fb_row + b * 32 * BK + CH]);          \
+        BL[b] = *reinterpret_cast<const v4i*>(&SM[3][fb_row + b * 32 * BK + CH]);          \
+    }
+    // four MFMAs of one product (ACC += X[i] * Y[j] over the 2 x 2 blocks)
+#define CM_MFMA4(ACC, X, Y)                                                                       \
+    _Pragma("unroll") for (int i = 0; i < 2; i++) _Pragma("unroll") for (int j = 0; j < 2; j++)   \
+        ACC[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(X[i], Y[j], ACC[i][j], 0, 0, 0);
+    // the 16 MFMAs of one substep, ordered so that no MFMA waits on the one before
+#define CM_MFMA(AH, AL, BH, BL)                                                                   \
+    _Pragma("unroll") for (int i = 0; i < 2; i++) _Pragma("unroll") for (int j = 0; j < 2; j++)   \
+        hh[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(AH[i], BH[j], hh[i][j], 0, 0, 0);       \
+    _Pragma("unroll") for (int i = 0; i < 2; i++) _Pragma("unroll") for (int j = 0; j < 2; j++)   \
+        mid[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(AH[i], BL[j], mid[i][j], 0, 0, 0);     \
+    _Pragma("unroll") for (int i = 0; i < 2; i++) _Pragma("unroll") for (int j = 0; j < 2; j++)   \
+        ll[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(AL[i], BL[j], ll[i][j], 0, 0, 0);       \
+    _Pragma("unroll") for (int i = 0; i < 2; i++) _Pragma("unroll") for (int j = 0; j < 2; j++)   \
+        mid[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(AL[i], BH[j], mid[i][j], 0, 0, 0);
+    // Publish step kt+1: this wave's copies of it are done once at most the 8 of the step
+    // issued after it remain in flight (vmcnt 8), its own fragment reads are done
+    // (lgkmcnt 0), then every wave's arrive at the barrier.
+#define CM_PUBLISH()                                                              \
+    __builtin_amdgcn_s_waitcnt(0x0078);                                           \
+    __builtin_amdgcn_s_barrier();
+    // One k step: SMC holds step kt, SMN step kt+1, SMI receives step kt+2.  Every step has
+    // the same shape: past the last step the copy repeats step nk-1 into the free stage
+    // SMI and the next-step fragments read a stage that is not used, so exactly 8 copies
+    // are in flight at every publish.
+#define CM_STEP(kt, SMC, SMN, SMI)                                                \
+    {                                                                             \
+        CM_ISSUE(SMI, min((kt) + 2, nk - 1))                                      \
+        CM_MFMA4(hh, ah0, bh0)                                                    \
+        __builtin_amdgcn_sched_barrier(0);                                        \
+        CM_FRAGS(SMC, ch1, ah1, al1, bh1, bl1)                                    \
+        __builtin_amdgcn_sched_barrier(0);                                        \
+        CM_MFMA4(mid, ah0, bl0)                                                   \
+        CM_MFMA4(ll, al0, bl0)                                                    \
+        CM_MFMA4(mid, al0, bh0)                                                   \
+        __builtin_amdgcn_sched_barrier(0);                                        \
+        CM_PUBLISH()                                                              \
+        CM_FRAGS(SMN, ch0, ah0, al0, bh0, bl0)                                    \
+        __builtin_amdgcn_sched_barrier(0);                                        \
+        CM_MFMA(ah1, al1, bh1, bl1)                                               \
+        __builtin_amdgcn_sched_barrier(0);                                        \
     }
 
-    // epilogue: lane holds D[4 * lk + r][li] of each 16x16 block
-    const int32_t* rs = rsum + bt * rs_slice;
-    const int32_t* cs = csum + bt * cs_slice;
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const uint32_t row = tr * BM + wr * 64 + i * 16 + lk * 4 + r;
-            const long long rterm = 128LL * rs[row] - kconst + epi.row_bias(row);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t col = tc * BN + wc * 64 + j * 16 + li;
-                long long acc = ((long long)hh[i][j][r] << 16) + ((long long)mid[i][j][r] << 8) +
-                                (long long)ll[i][j][r] + rterm + 128LL * cs[col];
-                epi.store(bt, row, col, acc);
-            }
+    CM_ISSUE(sm0, 0)
+    CM_ISSUE(sm1, min(1u, nk - 1))
+    CM_PUBLISH()
+    CM_FRAGS(sm0, ch0, ah0, al0, bh0, bl0)
+    uint32_t kt = 0;
+    for (; kt + 3 <= nk; kt += 3) {
+        CM_STEP(kt, sm0, sm1, sm2)
+        CM_STEP(kt + 1, sm1, sm2, sm0)
+        CM_STEP(kt + 2, sm2, sm0, sm1)
+    }
+    if (kt < nk) CM_STEP(kt, sm0, sm1, sm2)
+    if (kt + 1 < nk) CM_STEP(kt + 1, sm1, sm2, sm0)
+    __builtin_amdgcn_s_waitcnt(0x0070);      // no copy may land after the workgroup ends
+#undef CM_STEP
+#undef CM_PUBLISH
+#undef CM_MFMA
+#undef CM_MFMA4
+#undef CM_FRAGS
+#undef CM_ISSUE
+
+    // ---- epilogue.  Per-row terms 128 rowsum - 16384 K + bias << 8 and per-column terms
+    // 128 colsum go to LDS once; every lane recombines its accumulators (it holds
+    // D[8 (r / 4) + 4 lh + r % 4][l32] of each 32 x 32 block) into int16 results in an LDS
+    // tile, which the workgroup then writes out row by row in 16-byte pieces.
+    constexpr int OP = BN;                                        // output tile row pitch (32 KiB in sm0)
+    long long* rterm = reinterpret_cast<long long*>(&sm1[0][0]);  // [128]
+    long long* cterm = rterm + BM;                                // [128]
+    int16_t* otile = reinterpret_cast<int16_t*>(&sm0[0][0]);       // [128][OP]
+    __syncthreads();                                              // every wave is done with LDS
+    {
+        const int32_t* rs = rsum + bt * rs_slice;
+        const int32_t* cs = csum + bt * cs_slice;
+        if (t < BM) {
+            const uint32_t row = tr * BM + t;
+            rterm[t] = 128LL * rs[row] - kconst + epi.row_bias(row);
+        } else {
+            cterm[t - BM] = 128LL * cs[tc * BN + (t - BM)];
         }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const uint32_t cl = wc * 64 + j * 32 + l32;
+        const long long ct = cterm[cl];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t rl = wr * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                const long long acc = ((long long)hh[i][j][r] << 16) + ((long long)mid[i][j][r] << 8) +
+                                      (long long)ll[i][j][r] + rterm[rl] + ct;
+                otile[rl * OP + cl] = out_rule(acc, epi.wrap);
+            }
+    }
+    __syncthreads();
+    // write out: 128 rows x 16 pieces of 8 columns, 8 pieces per thread
+    const uint32_t col0 = tc * BN;
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        const uint32_t idx = q * 256 + t, rl = idx >> 4, pc = (idx & 15) * 8;
+        int16_t* dst = epi.row_ptr(bt, tr * BM + rl);
+        if (dst == nullptr || col0 + pc >= epi.cols) continue;
+        dst += col0 + pc;
+        const int16_t* src_row = otile + rl * OP + pc;
+        if (col0 + pc + 8 <= epi.cols && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+            *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src_row);
+        } else {
+            for (int e = 0; e < 8 && col0 + pc + e < epi.cols; e++) dst[e] = src_row[e];
+        }
+    }
 }
 
 // ---------------------------------------------------------------- depthwise conv
@@ -356,6 +563,13 @@ struct Planes {
     }
 };
 
+int run_sums(Planes& pl, hipStream_t s) {
+    const uint64_t n = (uint64_t)pl.lines_p * pl.slices;
+    CM_LAUNCH("sum_slabs_kernel", sum_slabs_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, s, pl.part, pl.sum,
+              pl.lines_p, pl.nslab, pl.slices);
+    return CM_OK;
+}
+
 template <class Src, bool KFast>
 int run_split(const Src& src, uint64_t src_slice, Planes& pl, hipStream_t s) {
     CM_LAUNCH("split_kernel", (split_kernel<Src, KFast>), dim3(pl.lines_p / 64, pl.nslab, pl.slices), dim3(256),
@@ -399,7 +613,8 @@ extern "C" int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_
     int rc = state(&st);
     if (rc) return rc;
     if (n == 0 || m == 0 || batch == 0) return CM_OK;
-    if (k == 0 || k > 65536) return fail(CM_EINVAL, "matmul: k = %u outside 1 .. 65536", k);
+    // the limb sums HL + LH stay exact in int32 for k <= 32768
+    if (k == 0 || k > 32768) return fail(CM_EINVAL, "matmul: k = %u outside 1 .. 32768", k);
     if (gemv_kw && gemv_kw != 1 && gemv_kw != 2 && gemv_kw != 4 && gemv_kw != 8)
         return fail(CM_EINVAL, "matmul: gemv_kw %u", gemv_kw);
     if (gemv_kw > 1 && (k % (16 * gemv_kw)))
@@ -415,10 +630,25 @@ extern "C" int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_
     char* p = static_cast<char*>(ws);
     A.carve(p);
     B.carve(p);
-    rc = run_split<SrcRowMajor, true>(SrcRowMajor{a, n, k, k}, sa > 1 ? (uint64_t)a_bs : 0, A, s);
+    const uint64_t a_slice = sa > 1 ? (uint64_t)a_bs : 0, b_slice = sb > 1 ? (uint64_t)b_bs : 0;
+    if (aligned16(a) && (k & 7) == 0 && (a_slice & 7) == 0) {
+        CM_LAUNCH("split_kernel", split_rows_kernel, dim3(A.lines_p / 4, A.nslab, A.slices), dim3(256), 0, s,
+                  a, a_slice, (uint64_t)k, n, k, A.hi, A.lo, A.part, A.lines_p, A.kp, A.nslab);
+        rc = run_sums(A, s);
+    } else {
+        rc = run_split<SrcRowMajor, true>(SrcRowMajor{a, n, k, k}, a_slice, A, s);
+    }
     if (rc) return rc;
     const uint32_t layout = gemv_kw ? 2 : (b_packed ? 1 : 0);
-    rc = run_split<SrcMatB, false>(SrcMatB{b, m, k, m, layout, gemv_kw}, sb > 1 ? (uint64_t)b_bs : 0, B, s);
+    const bool fast_b = aligned16(b) && (b_slice & 7) == 0 &&
+                        (layout == 1 || (layout == 0 && (m & 7) == 0) || (layout == 2 && gemv_kw == 1 && (m & 7) == 0));
+    if (fast_b) {
+        CM_LAUNCH("split_kernel", split_cols_kernel, dim3(B.lines_p / 32, B.nslab, B.slices), dim3(256), 0, s,
+                  b, b_slice, layout == 1 ? 1u : 0u, m, k, B.hi, B.lo, B.part, B.lines_p, B.kp, B.nslab);
+        rc = run_sums(B, s);
+    } else {
+        rc = run_split<SrcMatB, false>(SrcMatB{b, m, k, m, layout, gemv_kw}, b_slice, B, s);
+    }
     if (rc) return rc;
     EpiMatmul epi{c, (uint64_t)c_bs, n, m, wrap32 ? 1u : 0u};
     return run_gemm(A, B, batch, 16384LL * k, epi, s);
@@ -458,6 +688,8 @@ extern "C" int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, 
     const uint32_t tiles = (in_ch + 15) / 16;
     const uint32_t rem = in_ch - (tiles - 1) * 16, last = rem <= 8 ? 8 : 16;
     const uint32_t per_m = kh * kw * ((tiles - 1) * 16 + last);
+    if ((uint64_t)in_ch * kh * kw > 32768)
+        return fail(CM_EINVAL, "conv: in_ch * kh * kw = %u above 32768", in_ch * kh * kw);
     const uint32_t kpad = tiles * kh * kw * 16;
     const uint32_t kp = (uint32_t)round_up(kpad, BK);
     Planes A = make_planes(out_ch, kp, 1), B = make_planes(plane, kp, batch);
