@@ -1,0 +1,63 @@
+"""Value <-> raw conversions of the reference's fixed-point element type (Q8.8 ap_fixed<16,8>
+and power-of-two exponents), used at the edges of a simulated graph.
+
+Mirrors inference-scheduler/src/dtype.py: ``quantize`` (clip, round half to even,
+dtype.py:367-369), ``truncate`` (clip, floor, :371-377), ``quantize_exp`` / ``truncate_exp``
+(:278-291) and the raw storage encodings (``float_to_storage`` :391-395, ``exp_to_storage``).
+Inside the simulator every tensor is a raw int16 lane array on the device with an exponent
+f (value = raw * 2^-f); the float64 values of the reference's API appear only here.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+I16_LO, I16_HI = -32768, 32767
+
+
+class ApFixed16:
+    """ap_fixed<16, I>: 16-bit two's complement with F = 16 - I fraction bits."""
+
+    def __init__(self, integer_bits: int = 8):
+        self.W, self.I = 16, integer_bits
+        self.F = 16 - integer_bits
+        self.scale = float(1 << self.F)
+        self.min_val = -float(1 << (integer_bits - 1))
+        self.max_val = float(1 << (integer_bits - 1)) - 1.0 / self.scale
+
+    name = property(lambda self: f"ap_fixed<16,{self.I}>")
+    frac_bits = property(lambda self: self.F)
+    raw_range = property(lambda self: (float(I16_LO), float(I16_HI)))
+
+    # -- the reference's value-domain rules ---------------------------------------------
+    def quantize(self, x) -> np.ndarray:
+        """clip, then round half to even at 2^-F (dtype.py:367-369)."""
+        c = np.clip(np.asarray(x, np.float64), self.min_val, self.max_val)
+        return np.round(c * self.scale) / self.scale
+
+    def truncate(self, x) -> np.ndarray:
+        """clip, then floor at 2^-F: a kernel output (dtype.py:371-377)."""
+        c = np.clip(np.asarray(x, np.float64), self.min_val, self.max_val)
+        return np.floor(c * self.scale) / self.scale
+
+    def quantize_exp(self, x, f) -> np.ndarray:
+        """round half to even at 2^-f, saturate, NaN -> 0 (dtype.py:278-285)."""
+        s = np.power(2.0, np.asarray(f, np.float64))
+        x = np.asarray(x, np.float64)
+        r = np.round(np.where(np.isnan(x), 0.0, x) * s)
+        return np.clip(r, I16_LO, I16_HI) / s
+
+    # -- raw lanes ------------------------------------------------------------------------
+    def to_raw(self, values, f=None) -> np.ndarray:
+        """Raw int16 of values on the 2^-f grid (f = F by default): rint(v * 2^f), saturated.
+        Values off the grid are rounded half to even (float_to_storage / exp_to_storage)."""
+        s = np.power(2.0, np.asarray(self.F if f is None else f, np.float64))
+        r = np.round(np.asarray(values, np.float64) * s)
+        return np.clip(r, I16_LO, I16_HI).astype(np.int16)
+
+    def from_raw(self, raw, f=None) -> np.ndarray:
+        """float64 values raw * 2^-f."""
+        s = np.power(2.0, np.asarray(self.F if f is None else f, np.float64))
+        return np.asarray(raw, np.float64) / s
+
+
+AP_FIXED_16_8 = ApFixed16(8)

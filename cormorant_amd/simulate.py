@@ -1,0 +1,301 @@
+"""The fixed-point simulator on the GPU: ``Simulator(graph).simulate(inputs)`` is the
+reference's ``CodeGenerator.simulate`` (inference-scheduler/src/codegen/_simulate.py:382-403)
+and ``_forward_pass`` its per-node dispatch (:541-769), with every node run by the HIP units.
+
+Values cross the API as float64 arrays (value = raw * 2^-f, exact), as in the reference.
+Inside, each tensor is a raw int16 (int32 / float32 for row-ops kinds) torch tensor on the
+device with its exponent, so a graph runs from node to node without leaving HBM; the
+conversion happens once at the graph's inputs, weights and returned tensors.
+"""
+from __future__ import annotations
+
+from typing import Dict, Iterable, Optional
+
+import numpy as np
+import torch
+
+from . import units
+from .dtype import AP_FIXED_16_8, ApFixed16
+from .graph import (ConvNode, Graph, MatmulNode, PoolNode, ReshapeNode, RowOpsNode, ScheduledNode,
+                    SchedulerError, SoftmaxVopNode, TensorInfo)
+from .packing import conv_bias_image, conv_weight_image, pack_matmul_b
+
+_TORCH = {"i16": torch.int16, "i32": torch.int32, "f32": torch.float32}
+
+
+def _pad8(n: int) -> int:
+    return (n + 7) & ~7
+
+
+class Simulator:
+    """Forward-simulates ``graph`` with the HIP units on ``device``."""
+
+    def __init__(self, graph: Graph, dtype: ApFixed16 = AP_FIXED_16_8, device: str = "cuda"):
+        self._graph = graph
+        self._dtype = dtype
+        self.device = torch.device(device)
+        self._weights: Dict[str, torch.Tensor] = {}      # raw device copies of the weights
+        self._images: Dict[str, torch.Tensor] = {}       # packed weight images
+        self._infos: Dict[str, TensorInfo] = {}
+        for t in graph.input_tensors + graph.output_tensors:
+            self._infos[t.onnx_name] = t
+        for sn in graph.nodes:
+            for t in list(sn.inputs) + [sn.output]:
+                if t is not None:
+                    self._infos.setdefault(t.onnx_name, t)
+        units.init()
+
+    # ------------------------------------------------------------------ public API
+    def simulate(self, inputs: Dict[str, np.ndarray]) -> Dict[str, np.ndarray]:
+        """float64 inputs (on their grids) -> float64 graph outputs (_simulate.py:382-403)."""
+        arrays = self._forward_pass(inputs, keep=[t.onnx_name for t in self._graph.output_tensors])
+        return {t.onnx_name: arrays[t.onnx_name] for t in self._graph.output_tensors}
+
+    def _forward_pass(self, input_arrays: Dict[str, np.ndarray], errors_out=None, states=None,
+                      keep: Optional[Iterable[str]] = None) -> Dict[str, np.ndarray]:
+        """Run every node; returns float64 values of every tensor visited, or only ``keep``
+        (the reference's lean mode, _simulate.py:541-592).  ``errors_out`` / ``states`` are
+        accepted for the reference's signature; residual statistics are not computed."""
+        raw = self.forward_raw({name: self._to_device(self._tensor(name), v)
+                                for name, v in input_arrays.items()})
+        wanted = set(raw) if keep is None else set(keep)
+        return {name: self._to_values(self._tensor(name), t) for name, t in raw.items() if name in wanted}
+
+    def forward_raw(self, raw_inputs: Dict[str, torch.Tensor]) -> Dict[str, torch.Tensor]:
+        """The device-resident path: raw input tensors in, raw tensors of every node out."""
+        raw: Dict[str, torch.Tensor] = dict(raw_inputs)
+        for sn in self._graph.nodes:
+            if isinstance(sn, MatmulNode):
+                raw[sn.output.onnx_name] = self._matmul(sn, raw)
+            elif isinstance(sn, ConvNode):
+                raw[sn.output.onnx_name] = self._conv(sn, raw)
+            elif isinstance(sn, ReshapeNode):
+                raw[sn.output.onnx_name] = self._get(sn.inputs[0], raw)
+            elif isinstance(sn, PoolNode):
+                raw[sn.output.onnx_name] = self._pool(sn, raw)
+            elif isinstance(sn, SoftmaxVopNode):
+                raw[sn.output.onnx_name] = self._softmax(sn, raw)
+            elif isinstance(sn, RowOpsNode):
+                raw[sn.output.onnx_name] = self._rowops(sn, raw)
+            elif isinstance(sn, ScheduledNode):
+                raw[sn.output.onnx_name] = self._vectorop(sn, raw)
+            else:
+                raise SchedulerError(f"_forward_pass: unsupported node {type(sn).__name__}")
+        return raw
+
+    # ------------------------------------------------------------------ conversions
+    def _tensor(self, name: str) -> TensorInfo:
+        return self._infos[name]
+
+    def _exp(self, t: TensorInfo):
+        return self._dtype.frac_bits if t.exp is None else t.exp
+
+    def _to_device(self, t: TensorInfo, values: np.ndarray) -> torch.Tensor:
+        v = np.asarray(values, np.float64).reshape(t.shape)
+        if t.kind == "f32":
+            return torch.from_numpy(v.astype(np.float32)).to(self.device)
+        if t.kind == "i32":
+            s = np.power(2.0, np.asarray(self._exp(t), np.float64))
+            return torch.from_numpy(np.round(v * s).astype(np.int32)).to(self.device)
+        return torch.from_numpy(self._dtype.to_raw(v, self._exp(t))).to(self.device)
+
+    def _to_values(self, t: TensorInfo, raw: torch.Tensor) -> np.ndarray:
+        r = raw.detach().cpu().numpy().reshape(t.shape)
+        if t.kind == "f32":
+            return r.astype(np.float64)
+        return self._dtype.from_raw(r, self._exp(t))
+
+    def _get(self, t: TensorInfo, raw: Dict[str, torch.Tensor]) -> torch.Tensor:
+        if t.onnx_name in raw:
+            return raw[t.onnx_name]
+        if t.data is None:
+            raise KeyError(f"tensor '{t.onnx_name}' has no value (not an input, weight or node output)")
+        w = self._weights.get(t.onnx_name)
+        if w is None:
+            # a weight as the kernels read it (_simulate.py:531-539): quantized to the element
+            # type's grid; with a rank-1 exponent the stored data is raw / 2^F, so its raw lanes
+            # are the Q8.8 raw; otherwise the raw at the tensor's own exponent
+            q = self._dtype.quantize(np.asarray(t.data, np.float64).reshape(t.shape))
+            r = self._dtype.to_raw(q) if t.wexp is not None else self._dtype.to_raw(q, self._exp(t))
+            w = torch.from_numpy(r).to(self.device)
+            self._weights[t.onnx_name] = w
+        return w
+
+    def _new(self, t: TensorInfo, numel: Optional[int] = None) -> torch.Tensor:
+        return torch.empty(t.numel if numel is None else numel, dtype=_TORCH[t.kind], device=self.device)
+
+    @staticmethod
+    def _padded(x: torch.Tensor, rows: int, n: int, n_pad: int) -> torch.Tensor:
+        if n == n_pad:
+            return x.reshape(-1).contiguous()
+        out = torch.zeros((rows, n_pad), dtype=x.dtype, device=x.device)
+        out[:, :n] = x.reshape(rows, n)
+        return out.reshape(-1)
+
+    # ------------------------------------------------------------------ units
+    def _pow2(self, *ts: TensorInfo) -> bool:
+        return any(t is not None and (t.exp is not None or t.wexp is not None) for t in ts)
+
+    def _matmul(self, sn: MatmulNode, raw) -> torch.Tensor:
+        at, bt, ot = sn.inputs[0], sn.inputs[1], sn.output
+        a, b = self._get(at, raw), self._get(bt, raw)
+        n, k = at.shape[-2], at.shape[-1]
+        m = bt.shape[-1]
+        if bt.shape[-2] != k:
+            raise SchedulerError(f"MatMul: A [.., {n}, {k}] x B {list(bt.shape)}")
+        a_batch = int(np.prod(at.shape[:-2])) if len(at.shape) > 2 else 1
+        b_batch = int(np.prod(bt.shape[:-2])) if len(bt.shape) > 2 else 1
+        batch = max(a_batch, b_batch)
+        if a_batch not in (1, batch) or b_batch not in (1, batch):
+            raise SchedulerError("MatMul: batch dimensions do not broadcast")
+        wrap = self._pow2(at, bt, ot)
+        if wrap:
+            self._check_exponents(at, bt, ot)
+        c = self._new(ot, batch * n * m)
+        if bt.data is not None and b_batch == 1:
+            # a shared weight: the packed image once (the scheduler's packing)
+            img = self._images.get(bt.onnx_name)
+            if img is None:
+                img = torch.from_numpy(pack_matmul_b(b.cpu().numpy().reshape(k, m))).to(self.device)
+                self._images[bt.onnx_name] = img
+            units.matmul(a.reshape(-1), img, c, n, k, m, batch=batch, a_bs=n * k if a_batch > 1 else 0,
+                         b_bs=0, c_bs=n * m, b_packed=1, wrap32=wrap)
+        else:
+            units.matmul(a.reshape(-1).contiguous(), b.reshape(-1).contiguous(), c, n, k, m, batch=batch,
+                         a_bs=n * k if a_batch > 1 else 0, b_bs=k * m if b_batch > 1 else 0,
+                         c_bs=n * m, wrap32=wrap)
+        return c
+
+    def _check_exponents(self, at: TensorInfo, bt: TensorInfo, ot: TensorInfo) -> None:
+        """Every product of column j must sit at 2^-(f_out[j] + F) (_simulate.py:821-827)."""
+        F = self._dtype.frac_bits
+        k, m = bt.shape[-2], bt.shape[-1]
+        fa = np.broadcast_to(at.exp_full(F).reshape(-1) if np.ndim(at.exp_full(F)) else at.exp_full(F), (k,))
+        fw = np.broadcast_to(bt.wexp if bt.wexp is not None else bt.exp_full(F), (k, m))
+        fo = np.broadcast_to(ot.exp_full(F), (m,))
+        if not np.array_equal(fa[:, None] + fw, np.broadcast_to(fo[None, :] + F, (k, m))):
+            raise ValueError("MatMul: exponents are inconsistent (accumulator not on the 2^-(f_out+F) grid)")
+
+    def _conv(self, sn: ConvNode, raw) -> torch.Tensor:
+        xt, wt, ot = sn.inputs[0], sn.inputs[1], sn.output
+        bias_t = sn.inputs[2] if sn.has_bias else None
+        x = self._get(xt, raw)
+        img = self._images.get(wt.onnx_name)
+        if img is None:
+            w = self._get(wt, raw).cpu().numpy().reshape(wt.shape)
+            img = torch.from_numpy(conv_weight_image(w, sn.is_depthwise)).to(self.device)
+            self._images[wt.onnx_name] = img
+        bias = None
+        if bias_t is not None:
+            key = bias_t.onnx_name + "#bias"
+            bias = self._images.get(key)
+            if bias is None:
+                bias = torch.from_numpy(conv_bias_image(self._get(bias_t, raw).cpu().numpy())).to(self.device)
+                self._images[key] = bias
+        y = self._new(ot)
+        units.conv(x.reshape(-1).contiguous(), img, bias, y, sn.batch, sn.in_ch, sn.in_h, sn.in_w, sn.out_ch,
+                   sn.out_h, sn.out_w, sn.kh, sn.kw, sn.stride_h, sn.stride_w, sn.dilation_h, sn.dilation_w,
+                   sn.pad_top, sn.pad_left, int(bias is not None), int(sn.is_depthwise),
+                   wrap32=self._pow2(xt, wt, ot))
+        return y
+
+    def _pool(self, sn: PoolNode, raw) -> torch.Tensor:
+        xt, ot = sn.inputs[0], sn.output
+        y = self._new(ot)
+        units.pool(self._get(xt, raw).reshape(-1).contiguous(), y, xt.shape[0], xt.shape[1], xt.shape[2],
+                   xt.shape[3], ot.shape[2], ot.shape[3], sn.pool_h, sn.pool_w, sn.stride_h, sn.stride_w,
+                   sn.pad_top, sn.pad_left, sn.dil_h, sn.dil_w, sn.pool_type, sn.lp_order,
+                   sn.count_include_pad)
+        return y
+
+    def _vectorop(self, sn: ScheduledNode, raw) -> torch.Tensor:
+        """_simulate.py:721-765: both operands at the element type's grid; a smaller operand
+        repeats over leading blocks (nodes.py:226-303)."""
+        ot = sn.output
+        a = self._get(sn.inputs[0], raw).reshape(-1)
+        total = ot.numel
+        c = self._new(ot, _pad8(total))
+        if sn.arity == 1:
+            if a.numel() != total:
+                raise SchedulerError("unary VectorOP: input and output sizes differ")
+            units.vectorop(self._padded(a, 1, total, _pad8(total)), None, c, total, sn.op_code,
+                           act=sn.act, alpha=sn.alpha)
+            return c[:total]
+        b = self._get(sn.inputs[1], raw).reshape(-1)
+        na, nb = a.numel(), b.numel()
+        if total % na or total % nb or max(na, nb) != total:
+            raise SchedulerError(f"VectorOP: operands of {na} and {nb} elements onto {total}")
+        small = min(na, nb)
+        if small == total:
+            units.vectorop(self._padded(a, 1, total, _pad8(total)), self._padded(b, 1, total, _pad8(total)),
+                           c, total, sn.op_code, act=sn.act, alpha=sn.alpha)
+            return c[:total]
+        outer = total // small
+        if small % 8 == 0:
+            # broadcast through the registers: the repeated operand has increment 0
+            a_inc, b_inc = (small, 0) if na == total else (0, small)
+            units.vectorop(a.contiguous(), b.contiguous(), c, small, sn.op_code, outer=outer, a_inc=a_inc,
+                           b_inc=b_inc, act=sn.act, alpha=sn.alpha)
+            return c[:total]
+        # a chunk that is not a whole number of 8-lane words: repeat it in memory
+        if na < total:
+            a = a.repeat(outer)
+        else:
+            b = b.repeat(outer)
+        units.vectorop(self._padded(a, 1, total, _pad8(total)), self._padded(b, 1, total, _pad8(total)), c,
+                       total, sn.op_code, act=sn.act, alpha=sn.alpha)
+        return c[:total]
+
+    def _softmax(self, sn: SoftmaxVopNode, raw) -> torch.Tensor:
+        xt, ot = sn.inputs[0], sn.output
+        x = self._get(xt, raw)
+        if not sn.keys_major:
+            n = xt.shape[-1]
+            rows = xt.numel // n
+            np8 = _pad8(n)
+            c = torch.empty(rows * np8, dtype=torch.int16, device=self.device)
+            units.vectorop(self._padded(x, rows, n, np8), None, c, n, units.OP_SOFTMAX, outer=rows, a_inc=np8,
+                           b_inc=np8, smx_cm=sn.cm, smx_cfg=sn.cfg, smx_mask=sn.mask)
+            return c.reshape(rows, np8)[:, :n].reshape(-1).contiguous()
+        keys, queries = xt.shape[-2], xt.shape[-1]
+        heads = xt.numel // (keys * queries)
+        if queries % 16:
+            raise SchedulerError("keys-major softmax: the query count must be a multiple of 16")
+        kp = _pad8(keys)
+        out = torch.empty(heads * queries * kp, dtype=torch.int16, device=self.device)
+        xs = x.reshape(heads, keys * queries)
+        for h in range(heads):
+            units.vectorop(xs[h].contiguous(), None, out[h * queries * kp:(h + 1) * queries * kp], keys,
+                           units.OP_SOFTMAX_T, outer=queries, a_inc=queries, b_inc=kp, smx_cm=sn.cm,
+                           smx_cfg=sn.cfg, smx_mask=sn.mask)
+        return out.reshape(heads * queries, kp)[:, :keys].reshape(-1).contiguous()
+
+    def _rowops(self, sn: RowOpsNode, raw) -> torch.Tensor:
+        """One job over [rows, n] tensors; rows are re-laid at 16-byte strides."""
+        at, ot = sn.inputs[0], sn.output
+        bt = sn.inputs[1] if len(sn.inputs) > 1 else None
+        n = at.shape[-1]
+        rows = at.numel // n
+        kb = {"i16": 2, "i32": 4, "f32": 4}
+
+        def rowbuf(t: Optional[TensorInfo], x: Optional[torch.Tensor], width: int):
+            stride = (kb[t.kind] * width + 15) & ~15
+            per = stride // kb[t.kind]
+            buf = torch.zeros(rows * per, dtype=_TORCH[t.kind], device=self.device)
+            if x is not None:
+                buf.view(rows, per)[:, :width] = x.reshape(rows, width)
+            return buf, stride, per
+
+        a_buf, a_s1, _ = rowbuf(at, self._get(at, raw), n)
+        b_buf, b_s1 = None, 0
+        if bt is not None:
+            b_buf, b_s1, _ = rowbuf(bt, self._get(bt, raw), bt.shape[-1])
+        c_buf, c_s1, c_per = rowbuf(ot, None, ot.shape[-1])
+        p = torch.from_numpy(np.ascontiguousarray(sn.params, np.uint8)).to(self.device)
+        as_u8 = lambda t: t.view(torch.uint8) if t is not None else None
+        units.rowops(as_u8(a_buf), as_u8(b_buf), as_u8(c_buf), p, sn.op, n, rows, 1, a_s1, 0, b_s1, 0,
+                     c_s1, 0, sn.eps, sn.aux, sn.bq_sh, sn.win_lo, sn.win_hi)
+        return c_buf.view(rows, c_per)[:, :ot.shape[-1]].reshape(-1).contiguous()
+
+
+__all__ = ["Simulator"]

@@ -1,0 +1,324 @@
+"""Seeded random parity of every unit against the oracle, beyond the fixtures: full-range
+int16 operands (saturation, the int32 wrap of the power-of-two path), all B images, odd
+geometries, DIV by zero, masked softmax, every row-ops op; outputs poisoned first so that
+a stray or missing write shows."""
+import numpy as np
+import pytest
+
+from gpu_util import POISON16, dev16, dev8, host, poisoned16
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def U():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from cormorant_amd import units
+    units.init()
+    return units
+
+
+def rint16(rng, n, lo=-32768, hi=32768):
+    return rng.integers(lo, hi, n).astype(np.int16)
+
+
+def pack_b(b, k, m):
+    mp = (m + 31) // 32 * 32
+    p = np.zeros((k, mp), np.int16)
+    p[:, :m] = b.reshape(k, m)
+    return np.ascontiguousarray(p.reshape(k, mp // 32, 32).transpose(1, 0, 2)).reshape(-1)
+
+
+def gemv_image(b, k, m, kw):
+    """matmul_gemv_index (MatmulKernel.h:148-154)."""
+    b = b.reshape(k, m)
+    if kw == 1:
+        return b.reshape(-1).copy()
+    img = np.zeros(k * m, np.int16)
+    for kk in range(k):
+        c = (kk // (16 * kw)) * 16 + kk % 16
+        j = (kk // 16) % kw
+        img[(c * m + np.arange(m)) * kw + j] = b[kk]
+    return img
+
+
+MM_CASES = [  # n, k, m, batch, a_bs_mode, b_bs_mode, layout, kw, full_range, wrap
+    (1, 1, 1, 1, 1, 1, "row", 0, True, False),
+    (37, 300, 70, 1, 1, 1, "row", 0, True, False),
+    (37, 300, 70, 1, 1, 1, "row", 0, True, True),
+    (130, 520, 200, 3, 1, 0, "packed", 0, False, False),
+    (130, 520, 200, 3, 0, 1, "packed", 0, True, True),
+    (5, 256, 96, 2, 1, 1, "gemv", 2, False, False),
+    (3, 512, 64, 1, 1, 1, "gemv", 4, True, True),
+    (2, 256, 40, 2, 1, 0, "gemv", 8, False, False),
+    (16, 960, 136, 1, 1, 1, "gemv", 1, False, False),
+    (256, 4096, 128, 1, 1, 1, "packed", 0, True, False),
+    (200, 13, 333, 2, 1, 1, "row", 0, True, True),
+]
+
+
+@pytest.mark.parametrize("case", MM_CASES, ids=lambda c: "n%d_k%d_m%d_b%d_%s%d_%s" % (
+    c[0], c[1], c[2], c[3], c[6], c[7], "wrap" if c[9] else "sat"))
+def test_matmul_random(U, oracle_lib, case):
+    n, k, m, batch, am, bm, layout, kw, full, wrap = case
+    rng = np.random.default_rng(n * 7 + k + m)
+    lim = 32768 if full else 2048
+    a_bs, b_bs = (n * k if am else 0), (k * m if bm else 0)
+    a = rint16(rng, max(batch - 1, 0) * a_bs + n * k, -lim, lim)
+    bl = [rint16(rng, k * m, -lim, lim) for _ in range(batch if bm else 1)]
+    if layout == "packed":
+        imgs = [pack_b(x, k, m) for x in bl]
+    elif layout == "gemv":
+        imgs = [gemv_image(x, k, m, kw) for x in bl]
+    else:
+        imgs = bl
+    img_len = len(imgs[0])
+    b = np.concatenate(imgs)
+    b_bs_img = img_len if bm else 0
+    want = oracle_lib.matmul(a, b, n, k, m, batch, a_bs, b_bs_img, n * m, int(layout == "packed"),
+                             kw if layout == "gemv" else 0, wrap)
+    c = poisoned16(batch * n * m + 8)
+    U.matmul(dev16(a), dev16(b), c, n, k, m, batch, a_bs, b_bs_img, n * m, int(layout == "packed"),
+             kw if layout == "gemv" else 0, wrap)
+    got = host(c)
+    np.testing.assert_array_equal(got[:batch * n * m], want)
+    assert (got[batch * n * m:] == POISON16).all()
+
+
+def test_matmul_q88_saturates_where_int32_would_wrap(U, oracle_lib):
+    """acc = 16 * 32767^2 exceeds int32: the Q8.8 path saturates the true sum, the
+    power-of-two path wraps it (_simulate.py:620-633 vs 814-835; test_numeric.py:148-184)."""
+    k = 16
+    a = np.full(k, 32767, np.int16)
+    b = np.full(k, 32767, np.int16)
+    for wrap, expect in ((False, 32767), (True, None)):
+        c = poisoned16(8)
+        U.matmul(dev16(a), dev16(b), c, 1, k, 1, wrap32=wrap)
+        got = int(host(c)[0])
+        acc = 16 * 32767 * 32767
+        if expect is None:
+            w = (acc + 2 ** 31) % 2 ** 32 - 2 ** 31
+            expect = max(-32768, min(32767, w >> 8))
+        assert got == expect
+
+
+def test_matmul_c2_shape_against_numpy_float64(U):
+    """The C2 workload shape (4 x 512 x 4096 x 4096, shared packed B) against the reference's
+    own CPU algorithm (float64 np.matmul + clip/floor), every output."""
+    import bench
+    from oracle import sim_numpy
+    a, b, bp = bench.make_inputs(7)
+    c = poisoned16(4 * 512 * 4096)
+    U.matmul(dev16(a.reshape(-1)), dev16(bp), c, 512, 4096, 4096, 4, 512 * 4096, 0, 512 * 4096, 1, 0, False)
+    np.testing.assert_array_equal(host(c).reshape(4, 512, 4096), sim_numpy.matmul_q88(a, b))
+
+
+CONV_CASES = [  # batch, C, H, W, M, kh, kw, sh, sw, dh, dw, pt, pl, pb, pr, bias, dwise, full, wrap
+    (2, 3, 31, 29, 17, 7, 7, 2, 2, 1, 1, 3, 3, 3, 3, 1, 0, False, False),
+    (1, 21, 12, 13, 40, 3, 3, 1, 1, 2, 2, 2, 2, 2, 2, 1, 0, True, False),
+    (3, 40, 9, 9, 33, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 0, 0, True, True),
+    (1, 64, 14, 14, 64, 3, 3, 2, 1, 1, 1, 1, 0, 1, 2, 1, 0, False, False),
+    (2, 24, 15, 17, 24, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, True, False),
+    (1, 16, 20, 20, 16, 5, 5, 2, 2, 1, 1, 2, 2, 2, 2, 0, 1, True, True),
+    (32, 3, 16, 16, 32, 3, 3, 2, 2, 1, 1, 1, 1, 1, 1, 1, 0, False, False),
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES, ids=lambda c: "b%d_c%d_%dx%d_m%d_k%dx%d_s%d%d%s%s" % (
+    c[0], c[1], c[2], c[3], c[4], c[5], c[6], c[7], c[8], "_dw" if c[16] else "", "_wrap" if c[18] else ""))
+def test_conv_random(U, oracle_lib, case):
+    from cormorant_amd.packing import conv_bias_image, conv_weight_image
+    (bt, C, H, W, M, kh, kw, sh, sw, dh, dw, pt, pl, pb, pr, has_b, dwise, full, wrap) = case
+    rng = np.random.default_rng(C * 31 + M)
+    lim = 32768 if full else 1024
+    oh = (H + pt + pb - dh * (kh - 1) - 1) // sh + 1
+    ow = (W + pl + pr - dw * (kw - 1) - 1) // sw + 1
+    x = rint16(rng, bt * C * H * W, -lim, lim)
+    w = conv_weight_image(rint16(rng, M * (1 if dwise else C) * kh * kw, -lim, lim).reshape(
+        M, 1 if dwise else C, kh, kw), bool(dwise))
+    bias = conv_bias_image(rint16(rng, M, -lim, lim))
+    want = oracle_lib.conv(x, w, bias if has_b else None, bt * M * oh * ow, bt, C, H, W, M, oh, ow, kh, kw,
+                           sh, sw, dh, dw, pt, pl, has_b, dwise, wrap32=wrap)
+    y = poisoned16(bt * M * oh * ow + 8)
+    U.conv(dev16(x), dev16(w), dev16(bias), y, bt, C, H, W, M, oh, ow, kh, kw, sh, sw, dh, dw, pt, pl, has_b,
+           dwise, wrap32=wrap)
+    got = host(y)
+    np.testing.assert_array_equal(got[:bt * M * oh * ow], want)
+    assert (got[bt * M * oh * ow:] == POISON16).all()
+
+
+@pytest.mark.parametrize("op", range(10))
+@pytest.mark.parametrize("act", range(7))
+def test_vectorop_all_ops_and_acts(U, oracle_lib, op, act):
+    rng = np.random.default_rng(op * 10 + act)
+    size, outer = 1000, 3
+    a = rint16(rng, size * outer + 8)
+    b = rint16(rng, size * outer + 8)
+    if op == 3:
+        b[::7] = 0                       # DIV by zero: the simulator's +-inf / NaN rules
+        a[::14] = 0
+    alpha = int(rng.integers(0, 1 << 32))
+    a_inc = b_inc = 1000
+    c_len = (outer - 1) * 2000 + 1000
+    want = np.full(c_len + 8, 0x5A5A, np.int16)
+    oracle_lib.vectorop(a, b, c_len + 8, size, op, outer, a_inc, b_inc, act, alpha, c=want)
+    c = poisoned16(c_len + 8)
+    U.vectorop(dev16(a), dev16(b), c, size, op, outer, a_inc, b_inc, act, alpha)
+    np.testing.assert_array_equal(host(c), want)
+
+
+def test_vectorop_large_and_broadcast(U, oracle_lib):
+    rng = np.random.default_rng(11)
+    n = 3_000_001
+    a, b = rint16(rng, n + 7), rint16(rng, n + 7)
+    want = oracle_lib.vectorop(a, b, n + 7, n, 2, act=5)
+    c = poisoned16(n + 7)
+    U.vectorop(dev16(a), dev16(b), c, n, 2, act=5)
+    np.testing.assert_array_equal(host(c), want)
+    # b repeats (b_inc 0) over 400 runs of 4096
+    a = rint16(rng, 400 * 4096)
+    b = rint16(rng, 4096)
+    want = oracle_lib.vectorop(a, b, 400 * 4096, 4096, 0, 400, 4096, 0, 1)
+    c = poisoned16(400 * 4096)
+    U.vectorop(dev16(a), dev16(b), c, 4096, 0, 400, 4096, 0, 1)
+    np.testing.assert_array_equal(host(c), want)
+
+
+@pytest.mark.parametrize("n,rows,mask,cfg", [(384, 40, 384, 0x0813), (2048, 3, 2048, 0x0F0C),
+                                             (1, 9, 1, 0x0813), (1000, 17, 37 | (16 << 16), 0x0A11),
+                                             (5000, 2, 4000, 0x0813)])
+def test_softmax_rows_random(U, oracle_lib, n, rows, mask, cfg):
+    rng = np.random.default_rng(n + rows)
+    n8 = (n + 7) & ~7
+    a = rint16(rng, rows * n8, -3000, 3000)
+    want = np.full(rows * n8 + 8, 0x5A5A, np.int16)
+    oracle_lib.vectorop(a, None, rows * n8 + 8, n, 10, rows, n8, n8, 0, 0, 12102203, cfg, mask, c=want)
+    c = poisoned16(rows * n8 + 8)
+    U.vectorop(dev16(a), None, c, n, 10, rows, n8, n8, smx_cm=12102203, smx_cfg=cfg, smx_mask=mask)
+    np.testing.assert_array_equal(host(c), want)
+
+
+@pytest.mark.parametrize("keys,queries,mask", [(384, 384, 384), (1024, 64, 1024), (37, 16, 37),
+                                               (96, 50, 1 | (96 << 16)), (200, 48, 100 | (3 << 16))])
+def test_softmax_cols_random(U, oracle_lib, keys, queries, mask):
+    rng = np.random.default_rng(keys + queries)
+    k8 = (keys + 7) & ~7
+    a = rint16(rng, keys * queries, -4000, 4000)
+    c_len = queries * k8 + 8
+    want = np.full(c_len, 0x5A5A, np.int16)
+    oracle_lib.vectorop(a, None, c_len, keys, 11, queries, queries, k8, 0, 0, 12102203, 0x0C1A, mask, c=want)
+    c = poisoned16(c_len)
+    U.vectorop(dev16(a), None, c, keys, 11, queries, queries, k8, smx_cm=12102203, smx_cfg=0x0C1A,
+               smx_mask=mask)
+    np.testing.assert_array_equal(host(c), want)
+
+
+POOL_CASES = [  # N, C, H, W, ph, pw, sh, sw, pt, pl, pb, pr, dh, dw, type, lp, cip
+    (2, 5, 17, 19, 3, 3, 2, 2, 1, 1, 1, 1, 1, 1, 0, 2, 0),
+    (1, 7, 13, 11, 3, 2, 1, 2, 1, 0, 1, 1, 2, 1, 1, 2, 0),
+    (1, 7, 13, 11, 3, 3, 2, 2, 1, 1, 1, 1, 1, 1, 1, 2, 1),
+    (2, 3, 9, 9, 2, 2, 2, 2, 0, 0, 0, 0, 1, 1, 2, 1, 0),
+    (2, 3, 9, 9, 3, 3, 2, 2, 1, 1, 1, 1, 1, 1, 2, 2, 0),
+    (32, 64, 7, 7, 7, 7, 1, 1, 0, 0, 0, 0, 1, 1, 1, 2, 0),
+    (4, 32, 6, 6, 6, 6, 1, 1, 0, 0, 0, 0, 1, 1, 0, 2, 0),
+    (3, 16, 5, 5, 5, 5, 1, 1, 0, 0, 0, 0, 1, 1, 2, 2, 0),
+]
+
+
+@pytest.mark.parametrize("case", POOL_CASES)
+def test_pool_random(U, oracle_lib, case):
+    N, C, H, W, ph, pw, sh, sw, pt, pl, pb, pr, dh, dw, typ, lp, cip = case
+    rng = np.random.default_rng(H * W + typ)
+    oh = (H + pt + pb - dh * (ph - 1) - 1) // sh + 1
+    ow = (W + pl + pr - dw * (pw - 1) - 1) // sw + 1
+    x = rint16(rng, N * C * H * W)
+    want = oracle_lib.pool(x, N, C, H, W, oh, ow, ph, pw, sh, sw, pt, pl, dh, dw, typ, lp, cip)
+    y = poisoned16(N * C * oh * ow + 8)
+    U.pool(dev16(x), y, N, C, H, W, oh, ow, ph, pw, sh, sw, pt, pl, dh, dw, typ, lp, cip)
+    got = host(y)
+    np.testing.assert_array_equal(got[:N * C * oh * ow], want)
+    assert (got[N * C * oh * ow:] == POISON16).all()
+
+
+def _params(rng, n, g_lo=0, g_hi=1 << 31, bq=1 << 21, sh=(0, 63), sb=(0, 63), sc=(0, 63)):
+    p = np.zeros((n, 16), np.uint8)
+    p[:, 0:4] = rng.integers(g_lo, g_hi, n).astype(np.int64).astype(np.uint32).view(np.uint8).reshape(n, 4)
+    p[:, 4:8] = rng.integers(-bq, bq, n).astype(np.int32).view(np.uint8).reshape(n, 4)
+    p[:, 8] = rng.integers(sh[0], sh[1] + 1, n)
+    p[:, 9] = rng.integers(sb[0], sb[1] + 1, n)
+    p[:, 10] = rng.integers(sc[0], sc[1] + 1, n)
+    return p.reshape(-1)
+
+
+RO_CASES = [  # label, op word, n, rows, blocks, kinds (a, b, c bytes), param ranges, aux, eps, bq_sh
+    ("copy_i16", 1 | (1 << 12), 300, 5, 2),
+    ("addx_i32_i16_i32", 2 | (1 << 4) | (1 << 8) | (1 << 12), 768, 6, 1),
+    ("addx_relu_bcast", 2 | (1 << 12) | (1 << 13) | (1 << 15), 100, 4, 3),
+    ("copy_scale", 1 | (1 << 17), 257, 3, 1),
+    ("dequant_i32", 3 | (1 << 4) | (2 << 8), 333, 4, 1),
+    ("mulact", 4 | (1 << 12), 2560, 3, 1),
+    ("gate", 10 | (1 << 12), 500, 3, 1),
+    ("norm_rms_i32", 5 | (1 << 4), 960, 5, 1),
+    ("norm_ln_i16", 5 | (1 << 16), 768, 7, 1),
+    ("norm_ln_i32_4096", 5 | (1 << 4) | (1 << 16), 4096, 2, 1),
+    ("rope_hd64", 6 | (2 << 6), 320, 4, 1),
+]
+
+
+@pytest.mark.parametrize("case", RO_CASES, ids=lambda c: c[0])
+def test_rowops_random(U, oracle_lib, case):
+    label, op, n, c1, c2 = case
+    rng = np.random.default_rng(len(label) * 1000 + n)
+    code = op & 15
+    ak, bk, ck = (op >> 4) & 3, (op >> 6) & 3, (op >> 8) & 3
+    kb = lambda kd: 2 if kd == 0 else 4
+    if code == 3:
+        ck = 2
+    a_s1 = (kb(ak) * n + 15) & ~15
+    b_n = 2 * (0xFFF & 64) if code == 6 else n
+    b_s1 = (8 * 64 + 15) & ~15 if code == 6 else (kb(bk) * n + 15) & ~15
+    c_s1 = ((kb(ck) * n + 15) & ~15) + 16
+    a_s2, b_s2, c_s2 = a_s1 * c1 + 32, b_s1 * c1 + 16, c_s1 * c1 + 48
+    lim_a = 1 << 20 if ak == 1 else 1 << 15
+    a = np.zeros(a_s2 * c2, np.uint8)
+    b = np.zeros(b_s2 * c2, np.uint8)
+    for i2 in range(c2):
+        for i1 in range(c1):
+            off = i2 * a_s2 + i1 * a_s1
+            vals = rng.integers(-lim_a, lim_a, n).astype(np.int16 if ak == 0 else np.int32)
+            a[off:off + kb(ak) * n] = vals.view(np.uint8)
+            boff = i2 * b_s2 + i1 * b_s1
+            if code == 6:
+                cs = rng.integers(-(1 << 23), 1 << 23, 128).astype(np.int32)
+                b[boff:boff + 512] = cs.view(np.uint8)
+            else:
+                bv = rng.integers(-32768, 32768, n).astype(np.int16 if bk == 0 else np.int32)
+                b[boff:boff + kb(bk) * n] = bv.view(np.uint8)
+    eps, aux, bq_sh = 0, 0, 0
+    if code == 5:
+        p = _params(rng, n, 1 << 29, 1 << 31, 1 << 20, sc=(30, 45))
+        eps, bq_sh = int(rng.integers(0, 1 << 20)), 20
+    elif code == 6:
+        aux = 64
+        p = _params(rng, n, sh=(0, 2), sb=(0, 2), sc=(20, 26))
+    elif code == 4:
+        p = _params(rng, n, sh=(0, 6), sc=(14, 30))
+    elif code == 10:
+        p = _params(rng, n, sh=(0, 5), sb=(0, 5), sc=(30, 40))
+    elif code == 3:
+        p = _params(rng, n, sc=(0, 30))
+    elif op & (1 << 17):
+        p = _params(rng, n, 0, 1 << 25, 1 << 10, sh=(0, 4), sb=(0, 4), sc=(10, 30))
+    else:
+        p = _params(rng, n, sh=(0, 12), sb=(0, 12), sc=(0, 16))
+        bq_sh = 3
+    c_len = c_s2 * c2
+    want = np.full(c_len, 0xDE, np.uint8)
+    oracle_lib.rowops_reset_params()
+    oracle_lib.rowops(a, b, want, p, op, n, c1, c2, a_s1, a_s2, b_s1, b_s2, c_s1, c_s2, eps, aux, bq_sh)
+    cd = dev8(np.full(c_len, 0xDE, np.uint8))
+    U.rowops(dev8(a), dev8(b), cd, dev8(p), op, n, c1, c2, a_s1, a_s2, b_s1, b_s2, c_s1, c_s2, eps, aux,
+             bq_sh)
+    np.testing.assert_array_equal(host(cd), want)
