@@ -66,7 +66,7 @@ def forward(graph, inputs):
             n8 = (n + 7) & ~7
             xr = np.zeros((rows, n8), np.int16)
             xr[:, :n] = x.reshape(rows, n)
-            c = cm.vectorop(xr.reshape(-1), None, rows * n8, n, 10, rows, n8, n8, 0, 0, sn.cm, sn.cfg, sn.mask)
+            c = cm.vectorop(xr.reshape(-1), None, rows * n8, n, 10, rows, n8, n8, 0, 0, sn.cm, sn.cfg, sn.mask_reg(n))
             fp = (sn.cfg >> 8) & 31
             vals[out.onnx_name] = (c.reshape(rows, n8)[:, :n].astype(np.float64) / 2.0 ** fp).reshape(out.shape)
         elif isinstance(sn, G.ScheduledNode):
