@@ -6,6 +6,7 @@ import numpy as np
 import pytest
 
 from gpu_util import POISON16, dev16, dev8, host, poisoned16
+from rowops_cases import RO_CASES, make_job
 
 pytestmark = pytest.mark.gpu
 
@@ -242,83 +243,14 @@ def test_pool_random(U, oracle_lib, case):
     assert (got[N * C * oh * ow:] == POISON16).all()
 
 
-def _params(rng, n, g_lo=0, g_hi=1 << 31, bq=1 << 21, sh=(0, 63), sb=(0, 63), sc=(0, 63)):
-    p = np.zeros((n, 16), np.uint8)
-    p[:, 0:4] = rng.integers(g_lo, g_hi, n).astype(np.int64).astype(np.uint32).view(np.uint8).reshape(n, 4)
-    p[:, 4:8] = rng.integers(-bq, bq, n).astype(np.int32).view(np.uint8).reshape(n, 4)
-    p[:, 8] = rng.integers(sh[0], sh[1] + 1, n)
-    p[:, 9] = rng.integers(sb[0], sb[1] + 1, n)
-    p[:, 10] = rng.integers(sc[0], sc[1] + 1, n)
-    return p.reshape(-1)
-
-
-RO_CASES = [  # label, op word, n, rows, blocks, kinds (a, b, c bytes), param ranges, aux, eps, bq_sh
-    ("copy_i16", 1 | (1 << 12), 300, 5, 2),
-    ("addx_i32_i16_i32", 2 | (1 << 4) | (1 << 8) | (1 << 12), 768, 6, 1),
-    ("addx_relu_bcast", 2 | (1 << 12) | (1 << 13) | (1 << 15), 100, 4, 3),
-    ("copy_scale", 1 | (1 << 17), 257, 3, 1),
-    ("dequant_i32", 3 | (1 << 4) | (2 << 8), 333, 4, 1),
-    ("mulact", 4 | (1 << 12), 2560, 3, 1),
-    ("gate", 10 | (1 << 12), 500, 3, 1),
-    ("norm_rms_i32", 5 | (1 << 4), 960, 5, 1),
-    ("norm_ln_i16", 5 | (1 << 16), 768, 7, 1),
-    ("norm_ln_i32_4096", 5 | (1 << 4) | (1 << 16), 4096, 2, 1),
-    ("rope_hd64", 6 | (2 << 6), 320, 4, 1),
-]
-
-
 @pytest.mark.parametrize("case", RO_CASES, ids=lambda c: c[0])
 def test_rowops_random(U, oracle_lib, case):
-    label, op, n, c1, c2 = case
-    rng = np.random.default_rng(len(label) * 1000 + n)
-    code = op & 15
-    ak, bk, ck = (op >> 4) & 3, (op >> 6) & 3, (op >> 8) & 3
-    kb = lambda kd: 2 if kd == 0 else 4
-    if code == 3:
-        ck = 2
-    a_s1 = (kb(ak) * n + 15) & ~15
-    b_n = 2 * (0xFFF & 64) if code == 6 else n
-    b_s1 = (8 * 64 + 15) & ~15 if code == 6 else (kb(bk) * n + 15) & ~15
-    c_s1 = ((kb(ck) * n + 15) & ~15) + 16
-    a_s2, b_s2, c_s2 = a_s1 * c1 + 32, b_s1 * c1 + 16, c_s1 * c1 + 48
-    lim_a = 1 << 20 if ak == 1 else 1 << 15
-    a = np.zeros(a_s2 * c2, np.uint8)
-    b = np.zeros(b_s2 * c2, np.uint8)
-    for i2 in range(c2):
-        for i1 in range(c1):
-            off = i2 * a_s2 + i1 * a_s1
-            vals = rng.integers(-lim_a, lim_a, n).astype(np.int16 if ak == 0 else np.int32)
-            a[off:off + kb(ak) * n] = vals.view(np.uint8)
-            boff = i2 * b_s2 + i1 * b_s1
-            if code == 6:
-                cs = rng.integers(-(1 << 23), 1 << 23, 128).astype(np.int32)
-                b[boff:boff + 512] = cs.view(np.uint8)
-            else:
-                bv = rng.integers(-32768, 32768, n).astype(np.int16 if bk == 0 else np.int32)
-                b[boff:boff + kb(bk) * n] = bv.view(np.uint8)
-    eps, aux, bq_sh = 0, 0, 0
-    if code == 5:
-        p = _params(rng, n, 1 << 29, 1 << 31, 1 << 20, sc=(30, 45))
-        eps, bq_sh = int(rng.integers(0, 1 << 20)), 20
-    elif code == 6:
-        aux = 64
-        p = _params(rng, n, sh=(0, 2), sb=(0, 2), sc=(20, 26))
-    elif code == 4:
-        p = _params(rng, n, sh=(0, 6), sc=(14, 30))
-    elif code == 10:
-        p = _params(rng, n, sh=(0, 5), sb=(0, 5), sc=(30, 40))
-    elif code == 3:
-        p = _params(rng, n, sc=(0, 30))
-    elif op & (1 << 17):
-        p = _params(rng, n, 0, 1 << 25, 1 << 10, sh=(0, 4), sb=(0, 4), sc=(10, 30))
-    else:
-        p = _params(rng, n, sh=(0, 12), sb=(0, 12), sc=(0, 16))
-        bq_sh = 3
-    c_len = c_s2 * c2
+    a, b, p, c_len, r = make_job(case)
     want = np.full(c_len, 0xDE, np.uint8)
     oracle_lib.rowops_reset_params()
-    oracle_lib.rowops(a, b, want, p, op, n, c1, c2, a_s1, a_s2, b_s1, b_s2, c_s1, c_s2, eps, aux, bq_sh)
+    oracle_lib.rowops(a, b, want, p, r["op"], r["n"], r["c1"], r["c2"], r["a_s1"], r["a_s2"], r["b_s1"],
+                      r["b_s2"], r["c_s1"], r["c_s2"], r["eps"], r["aux"], r["bq_sh"])
     cd = dev8(np.full(c_len, 0xDE, np.uint8))
-    U.rowops(dev8(a), dev8(b), cd, dev8(p), op, n, c1, c2, a_s1, a_s2, b_s1, b_s2, c_s1, c_s2, eps, aux,
-             bq_sh)
+    U.rowops(dev8(a), dev8(b), cd, dev8(p), r["op"], r["n"], r["c1"], r["c2"], r["a_s1"], r["a_s2"], r["b_s1"],
+             r["b_s2"], r["c_s1"], r["c_s2"], r["eps"], r["aux"], r["bq_sh"])
     np.testing.assert_array_equal(host(cd), want)
