@@ -6,17 +6,18 @@
 //   sum_k a b = sum_k A'B' + 128 sum_k a + 128 sum_k b - 16384 K,   A' = a - 128, B' = b - 128
 //   sum_k A'B' = 2^16 HH + 2^8 (HL + LH) + LL
 // where HH, HL, LH, LL are sums of byte products, each exact in int32 (|h l| <= 2^14, so
-// K <= 2^16 keeps every partial below 2^31).  Four v_mfma_i32_16x16x64_i8 per 16x16 block
-// and 64-k step accumulate HH, MID = HL + LH and LL; the epilogue recombines them in int64
-// with the row / column sums, then applies the unit's output rule: floor(acc / 2^8)
-// saturated to int16, after an int32 wrap for the power-of-two path.  Padding of k (beyond K
-// or past the channels of a conv tile) is the byte pair (0, 0) -- A' = 0 -- on both sides and
-// is left out of the sums, so it contributes nothing.
+// K <= 32768 keeps HL + LH below 2^31).  Per 32 x 32 block and 32-k substep, four
+// v_mfma_i32_32x32x32_i8 accumulate HH, MID = HL + LH and LL; the epilogue recombines them
+// with the row / column sums in int32 (int64 only for K > 8192 on the saturating path) and
+// applies the unit's output rule: floor(acc / 2^8) saturated to int16, after an int32 wrap
+// for the power-of-two path.  Padding of k (beyond K or past the channels of a conv tile)
+// is the byte pair (0, 0) -- A' = 0 -- on both sides and is left out of the sums, so it
+// contributes nothing.
 //
-// Data flow (first version): split kernels write the two byte planes of A as [rows][kp]
-// and of B as [cols][kp] (k contiguous, the MFMA operand order; B is transposed through LDS),
-// plus per-1024-k partial row / column sums; the plane GEMM stages 128x64 byte tiles of each
-// plane in LDS and runs 4 waves of 64x64 outputs.
+// Data flow: split kernels write the two byte planes of A as [rows][kp] and of B as
+// [cols][kp] (k contiguous, the MFMA operand order; B transposed in registers or LDS), plus
+// per-1024-k partial row / column sums; the plane GEMM streams 64-k tiles of the four planes
+// into LDS with direct global -> LDS copies and sums the partials in its prologue.
 #include "cm_common.h"
 
 namespace cm {
@@ -24,7 +25,7 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 128, BN = 128, BK = 64;     // output tile; k step in elements (= plane bytes)
+constexpr int BN = 128, BK = 64;               // output tile columns; k step in elements (= plane bytes)
 constexpr int SLAB = 1024;                     // k per partial-sum slab
 
 __device__ __forceinline__ uint32_t pack_hi(const int16_t* v) {   // 4 high bytes
@@ -259,25 +260,15 @@ __global__ __launch_bounds__(256) void split_cols_kernel(const int16_t* __restri
     }
 }
 
-// line sums = the sum of the slab partials
-__global__ void sum_slabs_kernel(const int32_t* __restrict__ part, int32_t* __restrict__ out,
-                                 uint32_t lines_p, uint32_t nslab, uint32_t slices) {
-    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (uint64_t)lines_p * slices) return;
-    uint64_t bt = i / lines_p, l = i - bt * lines_p;
-    int32_t s = 0;
-    for (uint32_t q = 0; q < nslab; q++) s += part[(bt * nslab + q) * lines_p + l];
-    out[i] = s;
-}
-
 // ---------------------------------------------------------------- epilogues
-// An epilogue names where output row `i` of slice `bt` starts (nullptr past the last row)
-// and adds a per-row bias to the sum; columns are contiguous within a row.
+// An epilogue names where output row `i` of slice `bt` starts (nullptr past the last row),
+// the raw per-row bias (added to the sum as bias << 8), and whether every row start and the
+// column count are even (then two adjacent results go out as one 4-byte store).
 struct EpiMatmul {              // C[bt][i][j] = c + bt * c_bs + i * m + j
     int16_t* c;
     uint64_t c_bs;
-    uint32_t rows, cols, wrap;
-    __device__ long long row_bias(uint32_t) const { return 0; }
+    uint32_t rows, cols, wrap, pairs;
+    __device__ int32_t row_bias(uint32_t) const { return 0; }
     __device__ int16_t* row_ptr(uint32_t bt, uint32_t i) const {
         return i < rows ? c + bt * c_bs + (uint64_t)i * cols : nullptr;
     }
@@ -286,8 +277,8 @@ struct EpiConv {                // y pattern (ConvKernel.h:250-258); acc seeded 
     int16_t* y;
     const int16_t* bias;
     uint64_t img;               // elements per image (out_ch * plane)
-    uint32_t rows, cols, cs, cn, gs, wrap;
-    __device__ long long row_bias(uint32_t i) const { return bias && i < rows ? (long long)bias[i] * 256 : 0; }
+    uint32_t rows, cols, cs, cn, gs, wrap, pairs;
+    __device__ int32_t row_bias(uint32_t i) const { return bias && i < rows ? (int32_t)bias[i] : 0; }
     __device__ int16_t* row_ptr(uint32_t bt, uint32_t i) const {
         if (i >= rows) return nullptr;
         const uint64_t base = cn ? (uint64_t)(i % cn) * cs + (uint64_t)(i / cn) * gs : (uint64_t)i * cs;
@@ -295,54 +286,136 @@ struct EpiConv {                // y pattern (ConvKernel.h:250-258); acc seeded 
     }
 };
 
-// The unit's output rule on the recombined sum: floor(acc / 2^8) saturated to int16, the
-// sum wrapped to int32 first on the power-of-two path.
-__device__ __forceinline__ int16_t out_rule(long long acc, uint32_t wrap) {
-    if (wrap) acc = (long long)(int32_t)(uint32_t)(unsigned long long)acc;
-    const long long q = acc >> 8;
-    return (int16_t)(q > 32767 ? 32767 : (q < -32768 ? -32768 : q));
+// Recombination modes of the output rule floor(acc / 2^8) -> int16:
+//   acc = 2^16 HH + 2^8 MID + LL + 128 rowsum + 128 colsum - 16384 K + 2^8 bias.
+// With rowsum = 2 rh' + rl', colsum likewise (arithmetic shift, low bit),
+//   floor(acc / 2^8) = 2^8 HH + MID + rh + ch + ((LL + rl + cl) >> 8),
+//   rh = bias - 64 K + (rowsum >> 1), rl = 128 (rowsum & 1), ch = colsum >> 1, cl = 128 (colsum & 1),
+// every term but 2^8 HH exact in int32 for K <= 32768.
+//   kSatNarrow (K <= 8192): |the rest| < 2^29.1, so clamping HH to +-2^22 keeps the sum in
+//     int32 and cannot change a saturated result (|2^8 HH| > 2^30 then decides the sign);
+//   kWrap: the sum wrapped to int32 first, i.e. floor(acc / 2^8) mod 2^24, sign-extended;
+//   kSatWide (K > 8192, saturating): the sum in int64.
+enum : uint32_t { kSatNarrow = 0, kWrap = 1, kSatWide = 2 };
+
+__device__ __forceinline__ int32_t clamp_i32(int32_t v, int32_t lo, int32_t hi) {   // v_med3_i32
+    return min(max(v, lo), hi);
+}
+
+template <uint32_t MODE>
+__device__ __forceinline__ int32_t recombine(int32_t hh, int32_t mid, int32_t ll, int32_t rhch, int32_t rlcl) {
+    const int32_t y = mid + rhch + ((ll + rlcl) >> 8);
+    int32_t q;
+    if (MODE == kSatNarrow) {
+        q = (int32_t)((uint32_t)clamp_i32(hh, -(1 << 22), 1 << 22) << 8) + y;
+    } else if (MODE == kWrap) {
+        q = (int32_t)(((uint32_t)hh << 8) + (uint32_t)y);
+        q = (q << 8) >> 8;
+    } else {
+        const long long w = ((long long)hh << 8) + (long long)mid + (long long)rhch + ((ll + rlcl) >> 8);
+        q = (int32_t)(w > 32767 ? 32767 : (w < -32768 ? -32768 : w));
+    }
+    return clamp_i32(q, -32768, 32767);
+}
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// Store one wave's 64 x 64 results.  A lane holds D[8 (r / 4) + 4 lh + r % 4][l32] of each
+// 32 x 32 block.  With PAIRS, lanes 2c and 2c + 1 swap one result per row pair (DPP
+// quad_perm [1,0,3,2]) so that the even lane stores columns (2c, 2c + 1) of row r and the
+// odd lane the same columns of row r + 1, as one 4-byte store each.
+template <uint32_t MODE, bool PAIRS, class Epi>
+__device__ __forceinline__ void store_wave_tile(const v16i (&hh)[2][2], const v16i (&mid)[2][2],
+                                                const v16i (&ll)[2][2], const int2* rterm, const int2* cterm,
+                                                uint32_t bt, uint32_t row0, uint32_t col0, uint32_t wr,
+                                                uint32_t wc, uint32_t l32, uint32_t lh, const Epi& epi) {
+    const uint32_t odd = l32 & 1;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const uint32_t cl = wc * 64 + j * 32 + l32, col = col0 + cl;
+        const int2 ct = cterm[cl];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const uint32_t rl = wr * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                const int2 r0 = rterm[rl], r1 = rterm[rl + 1];
+                const int32_t q0 = recombine<MODE>(hh[i][j][r], mid[i][j][r], ll[i][j][r], r0.x + ct.x, r0.y + ct.y);
+                const int32_t q1 = recombine<MODE>(hh[i][j][r + 1], mid[i][j][r + 1], ll[i][j][r + 1], r1.x + ct.x,
+                                                   r1.y + ct.y);
+                if (PAIRS) {
+                    const int32_t give = odd ? q0 : q1;
+                    const int32_t got = __builtin_amdgcn_mov_dpp(give, 0xB1, 0xF, 0xF, false);
+                    const uint32_t lo = (uint32_t)(odd ? got : q0) & 0xFFFFu;
+                    const uint32_t hi = (uint32_t)(odd ? q1 : got) << 16;
+                    int16_t* dst = epi.row_ptr(bt, row0 + rl + odd);
+                    if (dst != nullptr && col - odd < epi.cols)
+                        *reinterpret_cast<uint32_t*>(dst + col - odd) = lo | hi;
+                } else if (col < epi.cols) {
+                    int16_t* d0 = epi.row_ptr(bt, row0 + rl);
+                    int16_t* d1 = epi.row_ptr(bt, row0 + rl + 1);
+                    if (d0 != nullptr) d0[col] = (int16_t)q0;
+                    if (d1 != nullptr) d1[col] = (int16_t)q1;
+                }
+                // one row pair at a time: hoisting the term loads of later pairs would
+                // need more registers than the accumulators leave
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
 }
 
 // ---------------------------------------------------------------- the plane GEMM
 // Grid: x = output tiles of one slice (XCD-aware order), y = batch slice.  a_slice /
-// b_slice (plane elements per slice, 0 = broadcast), sum slices likewise.  4 waves in a
-// 2 x 2 arrangement, 64 x 64 outputs each: 2 x 2 blocks of v_mfma_i32_32x32x32_i8 (the
-// i8 MFMA that sustains the full rate on gfx950), three int32 accumulators per block.
+// b_slice: plane bytes per slice (0 = broadcast); the row / column partial sums per SLAB of
+// k sit at part[(slice * nslab + s) * lines + line] (slice stride 0 = broadcast).
 //
-// Pipeline (one workgroup per CU, so the overlap is scheduled within each wave):
-//   * global -> LDS copies (global_load_lds_dwordx4, no registers) run two k steps ahead
-//     into a ring of three LDS stages;
-//   * a k step is two 32-k substeps; substep 1's fragments are read while substep 0's MFMAs
-//     run, and step k+1's stage is published (own copies waited for, barrier) between the
-//     substeps, so its substep-0 fragments are read while substep 1's MFMAs run.
-// LDS layout: per stage and plane a [128 rows][64 B] tile; row r holds its 16-byte chunk c
-// at chunk c ^ ((r >> 2) & 3), so any 16 consecutive rows of one chunk hit 16 distinct
-// bank groups.  A direct copy writes 1 KiB (16 rows) per wave instruction, lane l at 16 l.
-constexpr int STAGES = 3;
-constexpr int PLANE_TILE = BM * BK;            // 8 KiB
-
-typedef int v16i __attribute__((ext_vector_type(16)));
-
+// A workgroup computes a (64 WR) x 128 tile with 2 WR waves in a WR x 2 arrangement, 64 x 64
+// outputs each: 2 x 2 blocks of v_mfma_i32_32x32x32_i8 (the i8 MFMA that sustains the full
+// rate on gfx950), three int32 accumulators per block (192 registers), so two waves share
+// each SIMD:
+//   WR = 4, NST = 3: 8 waves, one workgroup per CU, a three-stage LDS ring (144 KiB) with
+//     the copies two steps ahead.  Both waves of a SIMD meet at the same barriers, so
+//     neither is starved (with two workgroups per CU the older one takes issue priority and
+//     the younger finishes alone, at one wave per SIMD);
+//   WR = 2, NST = 2: 4 waves, two workgroups per CU, a two-stage ring (64 KiB), for row
+//     counts that do not fill 256-row tiles.
+// Step k issues the global -> LDS copies (global_load_lds_dwordx4, no registers) of step
+// k + NST - 1 at its top, and ends by waiting for this wave's copies of step k + 1 and its
+// fragment reads, then for every wave (barrier).  LDS layout: per stage and plane a
+// [rows][64 B] tile; row r holds its 16-byte chunk c at chunk c ^ ((r >> 2) & 3), so any
+// 16 consecutive rows of one chunk hit 16 distinct bank groups.  A direct copy writes 1 KiB
+// (16 rows) per wave instruction, lane l at 16 l.
 __device__ __forceinline__ void lds_copy16(const int8_t* g, int8_t* lds_wave_base) {
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
 }
 
-template <class Epi>
-__global__ __launch_bounds__(256, 1) void gemm_planes_kernel(
-    const int8_t* __restrict__ Ahi, const int8_t* __restrict__ Alo, const int32_t* __restrict__ rsum,
-    uint64_t a_slice, uint64_t rs_slice, const int8_t* __restrict__ Bhi, const int8_t* __restrict__ Blo,
-    const int32_t* __restrict__ csum, uint64_t b_slice, uint64_t cs_slice, uint32_t tiles_r,
-    uint32_t tiles_c, uint32_t kp, long long kconst, Epi epi) {
-    // three LDS stages as separate arrays: with the loop unrolled by three every access
-    // names its stage statically, so the compiler can tell the in-flight copies into the
-    // other stages from the fragment reads and does not wait for them
-    __shared__ __attribute__((aligned(1024))) int8_t sm0[4][PLANE_TILE];   // Ah, Al, Bh, Bl
-    __shared__ __attribute__((aligned(1024))) int8_t sm1[4][PLANE_TILE];
-    __shared__ __attribute__((aligned(1024))) int8_t sm2[4][PLANE_TILE];
+template <int WR, int NST, class Epi>
+__global__ __launch_bounds__(128 * WR, 8 / (2 * WR)) void gemm_planes_kernel(
+    const int8_t* __restrict__ Ahi, const int8_t* __restrict__ Alo, const int32_t* __restrict__ rpart,
+    uint64_t a_slice, uint64_t rp_slice, uint32_t a_lines, const int8_t* __restrict__ Bhi,
+    const int8_t* __restrict__ Blo, const int32_t* __restrict__ cpart, uint64_t b_slice, uint64_t cp_slice,
+    uint32_t b_lines, uint32_t nslab, uint32_t tiles_r, uint32_t tiles_c, uint32_t kp, int32_t k64,
+    uint32_t mode, Epi epi) {
+    constexpr int TM = 64 * WR;                  // tile rows
+    constexpr int NT = 128 * WR;                 // threads
+    constexpr int NW = 2 * WR;                   // waves
+    constexpr int A_T = TM * BK, B_T = BN * BK;  // plane tile bytes
+    constexpr int STAGE = 2 * A_T + 2 * B_T;     // Ah, Al, Bh, Bl
+    constexpr int BCP = 8 / NW;                  // 16-row blocks of a B plane per wave
+    constexpr int NC = 2 * 2 + 2 * BCP;          // copies per thread and step
+    static_assert(NST == 2 || NST == 3, "two or three stages");
+    // the stages as separate arrays: with the loop unrolled by NST every access names its
+    // stage statically, so the compiler tells the copies in flight into the other stages
+    // from the fragment reads
+    __shared__ __attribute__((aligned(1024))) int8_t sm0[STAGE];
+    __shared__ __attribute__((aligned(1024))) int8_t sm1[STAGE];
+    __shared__ __attribute__((aligned(1024))) int8_t sm2[NST == 3 ? STAGE : 16];
+    __shared__ int2 rterm[TM], cterm[BN];        // (h, l) halves
 
     // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so
     // give each XCD a contiguous range of tiles (column-major: tiles sharing a B column
-    // strip, the larger operand, run on one XCD and share its L2).
+    // strip run on one XCD and share its L2).
     const uint32_t ntiles = tiles_r * tiles_c;
     uint32_t g = blockIdx.x;
     if ((ntiles & 7) == 0) g = (g & 7) * (ntiles >> 3) + (g >> 3);
@@ -352,15 +425,31 @@ __global__ __launch_bounds__(256, 1) void gemm_planes_kernel(
     const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const uint32_t wr = wave >> 1, wc = wave & 1, l32 = lane & 31, lh = lane >> 5;
 
-    // copy assignment: wave w fills 16-row blocks 2w and 2w + 1 of each plane; lane l
-    // takes row 16 b + l / 4, physical chunk l % 4 = logical chunk (l % 4) ^ swizzle
-    const uint32_t crow0 = 32 * wave + (lane >> 2), crow1 = crow0 + 16;
-    const uint32_t cchunk0 = ((lane & 3) ^ ((crow0 >> 2) & 3)) * 16;
-    const uint32_t cchunk1 = ((lane & 3) ^ ((crow1 >> 2) & 3)) * 16;
-    const int8_t* src[4] = {Ahi + bt * a_slice + (uint64_t)tr * BM * kp, Alo + bt * a_slice + (uint64_t)tr * BM * kp,
-                            Bhi + bt * b_slice + (uint64_t)tc * BN * kp, Blo + bt * b_slice + (uint64_t)tc * BN * kp};
-    const uint64_t g0 = (uint64_t)crow0 * kp + cchunk0, g1 = (uint64_t)crow1 * kp + cchunk1;
-    const uint32_t dst0 = __builtin_amdgcn_readfirstlane(2048 * wave), dst1 = dst0 + 1024;
+    // row / column terms of the epilogue, summed from the slab partials now so that their
+    // loads overlap the first copies
+    for (uint32_t e = t; e < TM + BN; e += NT) {
+        const bool is_row = e < TM;
+        const uint32_t line = is_row ? tr * TM + e : tc * BN + (e - TM);
+        const int32_t* pp = is_row ? rpart + bt * rp_slice + line : cpart + bt * cp_slice + line;
+        const uint32_t stride = is_row ? a_lines : b_lines;
+        int32_t sum = 0;
+        for (uint32_t q = 0; q < nslab; q++) sum += pp[(uint64_t)q * stride];
+        if (is_row) rterm[e] = make_int2(epi.row_bias(line) - k64 + (sum >> 1), (sum & 1) << 7);
+        else cterm[e - TM] = make_int2(sum >> 1, (sum & 1) << 7);
+    }
+
+    // copy assignment: wave w fills 16-row blocks 2w, 2w + 1 of each A plane and BCP blocks
+    // from BCP w of each B plane; lane l takes row 16 b + l / 4, physical chunk l % 4 =
+    // logical chunk (l % 4) ^ swizzle (the swizzle depends on l / 4 only)
+    const uint32_t lrow = lane >> 2, cchunk = ((lane & 3) ^ ((lrow >> 2) & 3)) * 16;
+    const uint64_t a_base = bt * a_slice + (uint64_t)tr * TM * kp, b_base = bt * b_slice + (uint64_t)tc * BN * kp;
+    const int8_t* ah_src = Ahi + a_base + (uint64_t)(32 * wave + lrow) * kp + cchunk;
+    const int8_t* al_src = Alo + a_base + (uint64_t)(32 * wave + lrow) * kp + cchunk;
+    const int8_t* bh_src = Bhi + b_base + (uint64_t)(16 * BCP * wave + lrow) * kp + cchunk;
+    const int8_t* bl_src = Blo + b_base + (uint64_t)(16 * BCP * wave + lrow) * kp + cchunk;
+    const uint64_t kp16 = (uint64_t)16 * kp;
+    const uint32_t a_dst = __builtin_amdgcn_readfirstlane(2048 * wave);
+    const uint32_t b_dst = __builtin_amdgcn_readfirstlane(1024 * BCP * wave);
 
     // fragment read offsets: lane reads row base32 + l32, logical chunk 2 s + lh (substep s)
     const uint32_t sw = (l32 >> 2) & 3;
@@ -372,137 +461,115 @@ __global__ __launch_bounds__(256, 1) void gemm_planes_kernel(
     for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++) hh[i][j] = mid[i][j] = ll[i][j] = v16i{};
-    // fragments: [substep][block]
-    v4i ah0[2], al0[2], bh0[2], bl0[2], ah1[2], al1[2], bh1[2], bl1[2];
+    v4i ah[2], al[2], bh[2], bl[2];
 
     const uint32_t nk = kp / BK;
-#define CM_ISSUE(SM, step)                                                        \
-    {                                                                             \
-        const uint64_t k_ = (uint64_t)(step) * BK;                                \
-        _Pragma("unroll") for (int p = 0; p < 4; p++) {                           \
-            lds_copy16(src[p] + g0 + k_, &SM[p][dst0]);                           \
-            lds_copy16(src[p] + g1 + k_, &SM[p][dst1]);                           \
-        }                                                                         \
+    // Copy group: the two waves sharing a SIMD (w and w + 4 of 8, as dispatched) issue
+    // their copies in different substeps.  With 4 waves per workgroup all are group 0.
+    const uint32_t cgrp = NW == 8 ? __builtin_amdgcn_readfirstlane((wave >> 2) & 1) : 0;
+    // Copy q of a step (0, 1: A hi; 2, 3: A lo; then B hi, B lo); A rows 16 apart, B blocks.
+#define CM_COPY(SM, step, q)                                                                        \
+    {                                                                                               \
+        const uint64_t k_ = (uint64_t)(step) * BK;                                                  \
+        if ((q) < 2) lds_copy16(ah_src + (q) * kp16 + k_, &SM[a_dst + 1024 * (q)]);                 \
+        else if ((q) < 4) lds_copy16(al_src + ((q) - 2) * kp16 + k_, &SM[A_T + a_dst + 1024 * ((q) - 2)]); \
+        else if ((q) < 4 + BCP)                                                                     \
+            lds_copy16(bh_src + ((q) - 4) * kp16 + k_, &SM[2 * A_T + b_dst + 1024 * ((q) - 4)]);    \
+        else                                                                                        \
+            lds_copy16(bl_src + ((q) - 4 - BCP) * kp16 + k_, &SM[2 * A_T + B_T + b_dst + 1024 * ((q) - 4 - BCP)]); \
     }
-#define CM_FRAGS(SM, CH, AH, AL, BH, BL)                                                   \
+    // The copies of slot s (after the s-th group of four MFMAs, 0..7): waves of copy group
+    // g issue theirs in slots 4g .. 4g + 3, two, two, then the rest.
+#define CM_COPIES(SM, step, slot)                                                 \
+    if (((slot) >> 2) == cgrp) {                                                  \
+        constexpr int s_ = (slot) & 3;                                            \
+        if (s_ < 2) { CM_COPY(SM, step, 2 * s_) CM_COPY(SM, step, 2 * s_ + 1) }   \
+        else if (NC == 6) { CM_COPY(SM, step, 2 + s_) }                           \
+        else { CM_COPY(SM, step, 2 * s_) CM_COPY(SM, step, 2 * s_ + 1) }          \
+    }                                                                             \
+    __builtin_amdgcn_sched_barrier(0);
+#define CM_FRAGS(SM, CH)                                                                   \
     _Pragma("unroll") for (int b = 0; b < 2; b++) {                                        \
-        AH[b] = *reinterpret_cast<const v4i*>(&SM[0][fa_row + b * 32 * BK + CH]);          \
-        AL[b] = *reinterpret_cast<const v4i*>(&SM[1][fa_row + b * 32 * BK + CH]);          \
-        BH[b] = *reinterpret_cast<const v4i*>(&SM[2][fb_row + b * 32 * BK + CH]);          \
-        BL[b] = *reinterpret_cast<const v4i*>(&SM[3][fb_row + b * 32 * BK + CH]);          \
-    }
-    // four MFMAs of one product (ACC += X[i] * Y[j] over the 2 x 2 blocks)
+        ah[b] = *reinterpret_cast<const v4i*>(&SM[fa_row + b * 32 * BK + CH]);             \
+        al[b] = *reinterpret_cast<const v4i*>(&SM[A_T + fa_row + b * 32 * BK + CH]);       \
+        bh[b] = *reinterpret_cast<const v4i*>(&SM[2 * A_T + fb_row + b * 32 * BK + CH]);   \
+        bl[b] = *reinterpret_cast<const v4i*>(&SM[2 * A_T + B_T + fb_row + b * 32 * BK + CH]); \
+    }                                                                                      \
+    __builtin_amdgcn_sched_barrier(0);
+    // four MFMAs of one limb product over the 2 x 2 blocks
 #define CM_MFMA4(ACC, X, Y)                                                                       \
     _Pragma("unroll") for (int i = 0; i < 2; i++) _Pragma("unroll") for (int j = 0; j < 2; j++)   \
-        ACC[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(X[i], Y[j], ACC[i][j], 0, 0, 0);
-    // the 16 MFMAs of one substep, ordered so that no MFMA waits on the one before
-#define CM_MFMA(AH, AL, BH, BL)                                                                   \
-    _Pragma("unroll") for (int i = 0; i < 2; i++) _Pragma("unroll") for (int j = 0; j < 2; j++)   \
-        hh[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(AH[i], BH[j], hh[i][j], 0, 0, 0);       \
-    _Pragma("unroll") for (int i = 0; i < 2; i++) _Pragma("unroll") for (int j = 0; j < 2; j++)   \
-        mid[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(AH[i], BL[j], mid[i][j], 0, 0, 0);     \
-    _Pragma("unroll") for (int i = 0; i < 2; i++) _Pragma("unroll") for (int j = 0; j < 2; j++)   \
-        ll[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(AL[i], BL[j], ll[i][j], 0, 0, 0);       \
-    _Pragma("unroll") for (int i = 0; i < 2; i++) _Pragma("unroll") for (int j = 0; j < 2; j++)   \
-        mid[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(AL[i], BH[j], mid[i][j], 0, 0, 0);
-    // Publish step kt+1: this wave's copies of it are done once at most the 8 of the step
-    // issued after it remain in flight (vmcnt 8), its own fragment reads are done
-    // (lgkmcnt 0), then every wave's arrive at the barrier.
-#define CM_PUBLISH()                                                              \
-    __builtin_amdgcn_s_waitcnt(0x0078);                                           \
-    __builtin_amdgcn_s_barrier();
-    // One k step: SMC holds step kt, SMN step kt+1, SMI receives step kt+2.  Every step has
-    // the same shape: past the last step the copy repeats step nk-1 into the free stage
-    // SMI and the next-step fragments read a stage that is not used, so exactly 8 copies
-    // are in flight at every publish.
-#define CM_STEP(kt, SMC, SMN, SMI)                                                \
+        ACC[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(X[i], Y[j], ACC[i][j], 0, 0, 0);       \
+    __builtin_amdgcn_sched_barrier(0);
+    // One k step on stage SMC while later steps land in the others; SMI receives step
+    // kt + NST - 1 (past the last step the copy repeats step nk - 1, so every step has the
+    // same shape).  Two 32-k substeps of 16 MFMAs (hh, mid = h l, ll, mid = l h: no MFMA
+    // waits on the one before); the step's copies sit between MFMA groups of the substep
+    // of the wave's copy group, so that while one wave of a SIMD spends issue cycles on
+    // copies the other has MFMAs to issue, and the sched_barriers keep the compiler from
+    // gathering them.  The end of the step waits for this wave's copies of step kt + 1
+    // (this step's NC may stay in flight with three stages) and fragment reads, then for
+    // every wave.
+#define CM_SUBSTEP(SMC, SMI, st, CH, S0)                                          \
+    CM_FRAGS(SMC, CH)                                                             \
+    CM_MFMA4(hh, ah, bh) CM_COPIES(SMI, st, S0)                                   \
+    CM_MFMA4(mid, ah, bl) CM_COPIES(SMI, st, S0 + 1)                              \
+    CM_MFMA4(ll, al, bl) CM_COPIES(SMI, st, S0 + 2)                               \
+    CM_MFMA4(mid, al, bh) CM_COPIES(SMI, st, S0 + 3)
+#define CM_STEP(kt, SMC, SMI)                                                     \
     {                                                                             \
-        CM_ISSUE(SMI, min((kt) + 2, nk - 1))                                      \
-        CM_MFMA4(hh, ah0, bh0)                                                    \
-        __builtin_amdgcn_sched_barrier(0);                                        \
-        CM_FRAGS(SMC, ch1, ah1, al1, bh1, bl1)                                    \
-        __builtin_amdgcn_sched_barrier(0);                                        \
-        CM_MFMA4(mid, ah0, bl0)                                                   \
-        CM_MFMA4(ll, al0, bl0)                                                    \
-        CM_MFMA4(mid, al0, bh0)                                                   \
-        __builtin_amdgcn_sched_barrier(0);                                        \
-        CM_PUBLISH()                                                              \
-        CM_FRAGS(SMN, ch0, ah0, al0, bh0, bl0)                                    \
-        __builtin_amdgcn_sched_barrier(0);                                        \
-        CM_MFMA(ah1, al1, bh1, bl1)                                               \
-        __builtin_amdgcn_sched_barrier(0);                                        \
+        const uint32_t st_ = min((kt) + NST - 1, nk - 1);                         \
+        CM_SUBSTEP(SMC, SMI, st_, ch0, 0)                                         \
+        CM_SUBSTEP(SMC, SMI, st_, ch1, 4)                                         \
+        __builtin_amdgcn_s_waitcnt(NST == 3 ? (0x0070 | NC) : 0x0070);            \
+        __builtin_amdgcn_s_barrier();                                             \
     }
+#define CM_ISSUE(SM, step)                                                        \
+    _Pragma("unroll") for (int q_ = 0; q_ < NC; q_++) CM_COPY(SM, step, q_)
 
-    CM_ISSUE(sm0, 0)
-    CM_ISSUE(sm1, min(1u, nk - 1))
-    CM_PUBLISH()
-    CM_FRAGS(sm0, ch0, ah0, al0, bh0, bl0)
     uint32_t kt = 0;
-    for (; kt + 3 <= nk; kt += 3) {
-        CM_STEP(kt, sm0, sm1, sm2)
-        CM_STEP(kt + 1, sm1, sm2, sm0)
-        CM_STEP(kt + 2, sm2, sm0, sm1)
+    if constexpr (NST == 3) {
+        CM_ISSUE(sm0, 0)
+        CM_ISSUE(sm1, min(1u, nk - 1))
+        __builtin_amdgcn_s_waitcnt(0x0070 | NC);
+        __builtin_amdgcn_s_barrier();
+        for (; kt + 3 <= nk; kt += 3) {
+            CM_STEP(kt, sm0, sm2)
+            CM_STEP(kt + 1, sm1, sm0)
+            CM_STEP(kt + 2, sm2, sm1)
+        }
+        if (kt < nk) CM_STEP(kt, sm0, sm2)
+        if (kt + 1 < nk) CM_STEP(kt + 1, sm1, sm0)
+    } else {
+        CM_ISSUE(sm0, 0)
+        __builtin_amdgcn_s_waitcnt(0x0070);
+        __builtin_amdgcn_s_barrier();
+        for (; kt + 2 <= nk; kt += 2) {
+            CM_STEP(kt, sm0, sm1)
+            CM_STEP(kt + 1, sm1, sm0)
+        }
+        if (kt < nk) CM_STEP(kt, sm0, sm1)
     }
-    if (kt < nk) CM_STEP(kt, sm0, sm1, sm2)
-    if (kt + 1 < nk) CM_STEP(kt + 1, sm1, sm2, sm0)
     __builtin_amdgcn_s_waitcnt(0x0070);      // no copy may land after the workgroup ends
+#undef CM_ISSUE
 #undef CM_STEP
-#undef CM_PUBLISH
-#undef CM_MFMA
+#undef CM_SUBSTEP
 #undef CM_MFMA4
 #undef CM_FRAGS
-#undef CM_ISSUE
+#undef CM_COPIES
+#undef CM_COPY
 
-    // ---- epilogue.  Per-row terms 128 rowsum - 16384 K + bias << 8 and per-column terms
-    // 128 colsum go to LDS once; every lane recombines its accumulators (it holds
-    // D[8 (r / 4) + 4 lh + r % 4][l32] of each 32 x 32 block) into int16 results in an LDS
-    // tile, which the workgroup then writes out row by row in 16-byte pieces.
-    constexpr int OP = BN;                                        // output tile row pitch (32 KiB in sm0)
-    long long* rterm = reinterpret_cast<long long*>(&sm1[0][0]);  // [128]
-    long long* cterm = rterm + BM;                                // [128]
-    int16_t* otile = reinterpret_cast<int16_t*>(&sm0[0][0]);       // [128][OP]
-    __syncthreads();                                              // every wave is done with LDS
-    {
-        const int32_t* rs = rsum + bt * rs_slice;
-        const int32_t* cs = csum + bt * cs_slice;
-        if (t < BM) {
-            const uint32_t row = tr * BM + t;
-            rterm[t] = 128LL * rs[row] - kconst + epi.row_bias(row);
-        } else {
-            cterm[t - BM] = 128LL * cs[tc * BN + (t - BM)];
-        }
+    // ---- epilogue: one uniform dispatch to the store routine of this mode
+    const uint32_t row0 = tr * TM, col0 = tc * BN;
+#define CM_STORE(M, P) store_wave_tile<M, P>(hh, mid, ll, rterm, cterm, bt, row0, col0, wr, wc, l32, lh, epi)
+    if (mode == kSatNarrow) {
+        if (epi.pairs) CM_STORE(kSatNarrow, true); else CM_STORE(kSatNarrow, false);
+    } else if (mode == kWrap) {
+        if (epi.pairs) CM_STORE(kWrap, true); else CM_STORE(kWrap, false);
+    } else {
+        if (epi.pairs) CM_STORE(kSatWide, true); else CM_STORE(kSatWide, false);
     }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const uint32_t cl = wc * 64 + j * 32 + l32;
-        const long long ct = cterm[cl];
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const uint32_t rl = wr * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                const long long acc = ((long long)hh[i][j][r] << 16) + ((long long)mid[i][j][r] << 8) +
-                                      (long long)ll[i][j][r] + rterm[rl] + ct;
-                otile[rl * OP + cl] = out_rule(acc, epi.wrap);
-            }
-    }
-    __syncthreads();
-    // write out: 128 rows x 16 pieces of 8 columns, 8 pieces per thread
-    const uint32_t col0 = tc * BN;
-#pragma unroll
-    for (int q = 0; q < 8; q++) {
-        const uint32_t idx = q * 256 + t, rl = idx >> 4, pc = (idx & 15) * 8;
-        int16_t* dst = epi.row_ptr(bt, tr * BM + rl);
-        if (dst == nullptr || col0 + pc >= epi.cols) continue;
-        dst += col0 + pc;
-        const int16_t* src_row = otile + rl * OP + pc;
-        if (col0 + pc + 8 <= epi.cols && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
-            *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src_row);
-        } else {
-            for (int e = 0; e < 8 && col0 + pc + e < epi.cols; e++) dst[e] = src_row[e];
-        }
-    }
+#undef CM_STORE
 }
 
 // ---------------------------------------------------------------- depthwise conv
@@ -546,56 +613,59 @@ __global__ __launch_bounds__(256) void conv_dw_kernel(const int16_t* __restrict_
 }
 
 // ---------------------------------------------------------------- drivers
+// Byte planes [slices][lines_p][kp] of one operand and its partial line sums
+// [slices][nslab][lines_p].
 struct Planes {
     int8_t *hi, *lo;
-    int32_t *part, *sum;
+    int32_t* part;
     uint32_t lines_p, kp, nslab, slices;
     size_t bytes() const {
-        return (size_t)slices * lines_p * kp * 2 + (size_t)slices * nslab * lines_p * 4 +
-               (size_t)slices * lines_p * 4 + 1024;
+        return (size_t)slices * lines_p * kp * 2 + (size_t)slices * nslab * lines_p * 4 + 1024;
     }
     void carve(char*& p) {
         hi = reinterpret_cast<int8_t*>(p); p += (size_t)slices * lines_p * kp;
         lo = reinterpret_cast<int8_t*>(p); p += (size_t)slices * lines_p * kp;
         part = reinterpret_cast<int32_t*>(p); p += (size_t)slices * nslab * lines_p * 4;
-        sum = reinterpret_cast<int32_t*>(p); p += (size_t)slices * lines_p * 4;
         p = reinterpret_cast<char*>(round_up(reinterpret_cast<uintptr_t>(p), 256));
     }
 };
-
-int run_sums(Planes& pl, hipStream_t s) {
-    const uint64_t n = (uint64_t)pl.lines_p * pl.slices;
-    CM_LAUNCH("sum_slabs_kernel", sum_slabs_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, s, pl.part, pl.sum,
-              pl.lines_p, pl.nslab, pl.slices);
-    return CM_OK;
-}
 
 template <class Src, bool KFast>
 int run_split(const Src& src, uint64_t src_slice, Planes& pl, hipStream_t s) {
     CM_LAUNCH("split_kernel", (split_kernel<Src, KFast>), dim3(pl.lines_p / 64, pl.nslab, pl.slices), dim3(256),
                        0, s, src, src_slice, pl.hi, pl.lo, pl.part, pl.lines_p, pl.kp, pl.nslab);
-    const uint64_t n = (uint64_t)pl.lines_p * pl.slices;
-    CM_LAUNCH("sum_slabs_kernel", sum_slabs_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, s, pl.part, pl.sum,
-                       pl.lines_p, pl.nslab, pl.slices);
     return CM_OK;
 }
+
+// Tile rows of the GEMM for an A operand of `lines` rows: 256 once there are that many.
+uint32_t gemm_tile_rows(uint32_t lines) { return lines >= 256 ? 256 : 128; }
 
 template <class Epi>
-int run_gemm(const Planes& A, const Planes& B, uint32_t batch, long long kconst, const Epi& epi,
-             hipStream_t s) {
-    const uint32_t tiles_r = A.lines_p / BM, tiles_c = B.lines_p / BN;
+int run_gemm(const Planes& A, const Planes& B, uint32_t batch, uint32_t k, Epi epi, hipStream_t s) {
+    const uint32_t tm = gemm_tile_rows(A.lines_p);
+    if (A.lines_p % tm) return fail(CM_EINVAL, "gemm: %u planes rows not a multiple of %u", A.lines_p, tm);
+    const uint32_t tiles_r = A.lines_p / tm, tiles_c = B.lines_p / BN;
     const uint64_t a_slice = A.slices > 1 ? (uint64_t)A.lines_p * A.kp : 0;
     const uint64_t b_slice = B.slices > 1 ? (uint64_t)B.lines_p * B.kp : 0;
-    const uint64_t rs_slice = A.slices > 1 ? A.lines_p : 0, cs_slice = B.slices > 1 ? B.lines_p : 0;
-    CM_LAUNCH("gemm_planes_kernel", gemm_planes_kernel<Epi>, dim3(tiles_r * tiles_c, batch), dim3(256), 0, s, A.hi,
-                       A.lo, A.sum, a_slice, rs_slice, B.hi, B.lo, B.sum, b_slice, cs_slice, tiles_r,
-                       tiles_c, A.kp, kconst, epi);
+    const uint64_t rp_slice = A.slices > 1 ? (uint64_t)A.nslab * A.lines_p : 0;
+    const uint64_t cp_slice = B.slices > 1 ? (uint64_t)B.nslab * B.lines_p : 0;
+    const uint32_t mode = epi.wrap ? kWrap : (k <= 8192 ? kSatNarrow : kSatWide);
+    const dim3 grid(tiles_r * tiles_c, batch);
+    if (tm == 256) {
+        CM_LAUNCH("gemm_planes_kernel", (gemm_planes_kernel<4, 3, Epi>), grid, dim3(512), 0, s, A.hi, A.lo, A.part,
+                  a_slice, rp_slice, A.lines_p, B.hi, B.lo, B.part, b_slice, cp_slice, B.lines_p, A.nslab, tiles_r,
+                  tiles_c, A.kp, (int32_t)(64 * k), mode, epi);
+    } else {
+        CM_LAUNCH("gemm_planes_kernel", (gemm_planes_kernel<2, 2, Epi>), grid, dim3(256), 0, s, A.hi, A.lo, A.part,
+                  a_slice, rp_slice, A.lines_p, B.hi, B.lo, B.part, b_slice, cp_slice, B.lines_p, A.nslab, tiles_r,
+                  tiles_c, A.kp, (int32_t)(64 * k), mode, epi);
+    }
     return CM_OK;
 }
 
-Planes make_planes(uint32_t lines, uint32_t kp, uint32_t slices) {
+Planes make_planes(uint32_t lines, uint32_t kp, uint32_t slices, uint32_t align = 128) {
     Planes p{};
-    p.lines_p = (uint32_t)round_up(lines, 128);
+    p.lines_p = (uint32_t)round_up(lines, align);
     p.kp = kp;
     p.nslab = ceil_div(kp, SLAB);
     p.slices = slices;
@@ -623,7 +693,7 @@ extern "C" int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_
     hipStream_t s = as_stream(stream);
     const uint32_t kp = (uint32_t)round_up(k, BK);
     const uint32_t sa = (batch > 1 && a_bs != 0) ? batch : 1, sb = (batch > 1 && b_bs != 0) ? batch : 1;
-    Planes A = make_planes(n, kp, sa), B = make_planes(m, kp, sb);
+    Planes A = make_planes(n, kp, sa, gemm_tile_rows(n)), B = make_planes(m, kp, sb);
     void* ws;
     rc = workspace(st, A.bytes() + B.bytes(), &ws);
     if (rc) return rc;
@@ -634,7 +704,6 @@ extern "C" int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_
     if (aligned16(a) && (k & 7) == 0 && (a_slice & 7) == 0) {
         CM_LAUNCH("split_kernel", split_rows_kernel, dim3(A.lines_p / 4, A.nslab, A.slices), dim3(256), 0, s,
                   a, a_slice, (uint64_t)k, n, k, A.hi, A.lo, A.part, A.lines_p, A.kp, A.nslab);
-        rc = run_sums(A, s);
     } else {
         rc = run_split<SrcRowMajor, true>(SrcRowMajor{a, n, k, k}, a_slice, A, s);
     }
@@ -645,13 +714,13 @@ extern "C" int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_
     if (fast_b) {
         CM_LAUNCH("split_kernel", split_cols_kernel, dim3(B.lines_p / 32, B.nslab, B.slices), dim3(256), 0, s,
                   b, b_slice, layout == 1 ? 1u : 0u, m, k, B.hi, B.lo, B.part, B.lines_p, B.kp, B.nslab);
-        rc = run_sums(B, s);
     } else {
         rc = run_split<SrcMatB, false>(SrcMatB{b, m, k, m, layout, gemv_kw}, b_slice, B, s);
     }
     if (rc) return rc;
-    EpiMatmul epi{c, (uint64_t)c_bs, n, m, wrap32 ? 1u : 0u};
-    return run_gemm(A, B, batch, 16384LL * k, epi, s);
+    const bool pairs = (reinterpret_cast<uintptr_t>(c) & 3) == 0 && (m & 1) == 0 && (c_bs & 1) == 0;
+    EpiMatmul epi{c, (uint64_t)c_bs, n, m, wrap32 ? 1u : 0u, pairs ? 1u : 0u};
+    return run_gemm(A, B, batch, k, epi, s);
 }
 
 extern "C" int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
@@ -692,7 +761,7 @@ extern "C" int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, 
         return fail(CM_EINVAL, "conv: in_ch * kh * kw = %u above 32768", in_ch * kh * kw);
     const uint32_t kpad = tiles * kh * kw * 16;
     const uint32_t kp = (uint32_t)round_up(kpad, BK);
-    Planes A = make_planes(out_ch, kp, 1), B = make_planes(plane, kp, batch);
+    Planes A = make_planes(out_ch, kp, 1, gemm_tile_rows(out_ch)), B = make_planes(plane, kp, batch);
     void* ws;
     rc = workspace(st, A.bytes() + B.bytes(), &ws);
     if (rc) return rc;
@@ -705,6 +774,9 @@ extern "C" int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, 
                  pad_top, pad_left, plane};
     rc = run_split<SrcIm2col, false>(im, (uint64_t)in_ch * in_h * in_w, B, s);
     if (rc) return rc;
-    EpiConv epi{y, bptr, (uint64_t)out_ch * plane, out_ch, plane, cs, y_cn, y_gs, wrap32 ? 1u : 0u};
-    return run_gemm(A, B, batch, 16384LL * in_ch * kh * kw, epi, s);
+    const uint64_t img = (uint64_t)out_ch * plane;
+    const bool pairs = (reinterpret_cast<uintptr_t>(y) & 3) == 0 && (plane & 1) == 0 && (cs & 1) == 0 &&
+                       (y_gs & 1) == 0 && (img & 1) == 0;
+    EpiConv epi{y, bptr, img, out_ch, plane, cs, y_cn, y_gs, wrap32 ? 1u : 0u, pairs ? 1u : 0u};
+    return run_gemm(A, B, batch, in_ch * kh * kw, epi, s);
 }

@@ -57,7 +57,32 @@ MM_CASES = [  # n, k, m, batch, a_bs_mode, b_bs_mode, layout, kw, full_range, wr
     (16, 960, 136, 1, 1, 1, "gemv", 1, False, False),
     (256, 4096, 128, 1, 1, 1, "packed", 0, True, False),
     (200, 13, 333, 2, 1, 1, "row", 0, True, True),
+    (9, 8192, 17, 1, 1, 1, "packed", 0, True, False),      # last k of the int32 recombination
+    (9, 9000, 17, 1, 1, 1, "packed", 0, True, False),      # int64 recombination
+    (3, 32768, 5, 1, 1, 1, "row", 0, True, False),
+    (3, 32768, 5, 1, 1, 1, "row", 0, True, True),
 ]
+
+
+@pytest.mark.parametrize("k", [1, 8192, 8193, 32768])
+@pytest.mark.parametrize("wrap", [False, True])
+def test_matmul_extreme_operands(U, oracle_lib, k, wrap):
+    """Rows and columns of the int16 extremes: the largest |sum| each recombination path meets."""
+    n, m = 4, 6
+    a = np.empty((n, k), np.int16)
+    a[0], a[1], a[2], a[3] = -32768, 32767, -32768, 32767
+    a[3, ::2] = -32768
+    b = np.empty((k, m), np.int16)
+    b[:, 0], b[:, 1], b[:, 2], b[:, 3], b[:, 4], b[:, 5] = -32768, 32767, -32768, 32767, 1, -1
+    b[1::2, 2] = 32767
+    b[::3, 5] = 0
+    a, b = a.reshape(-1), b.reshape(-1)
+    want = oracle_lib.matmul(a, b, n, k, m, 1, 0, 0, n * m, 0, 0, wrap)
+    c = poisoned16(n * m + 8)
+    U.matmul(dev16(a), dev16(b), c, n, k, m, 1, 0, 0, n * m, 0, 0, wrap)
+    got = host(c)
+    np.testing.assert_array_equal(got[:n * m], want)
+    assert (got[n * m:] == POISON16).all()
 
 
 @pytest.mark.parametrize("case", MM_CASES, ids=lambda c: "n%d_k%d_m%d_b%d_%s%d_%s" % (
