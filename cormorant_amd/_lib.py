@@ -43,11 +43,17 @@ SIGNATURES = {
     "cm_timing_read": (_I32, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                               ctypes.POINTER(ctypes.c_uint64)]),
     "cm_timing_reset": (_I32, []),
+    "cm_timing_select": (_I32, [ctypes.c_char_p]),
 }
 
 
 def timing_enable(on: bool) -> None:
     check(lib().cm_timing_enable(1 if on else 0), "cm_timing_enable")
+
+
+def timing_select(kernel: str = "") -> None:
+    """Record only launches of ``kernel`` ("" = every kernel)."""
+    check(lib().cm_timing_select(kernel.encode()), "cm_timing_select")
 
 
 def timing_reset() -> None:

@@ -151,88 +151,131 @@ __global__ __launch_bounds__(256) void split_kernel(Src src, uint64_t src_slice,
 // Padding is written as the value 128 (A' = 0: the byte pair (0, 0)) and left out of the sums.
 constexpr int16_t kPad = 128;
 
+// The byte planes of 8 int16 values (one 16-byte load): high bytes (1, 3 of each dword) and
+// low bytes (0, 2, top bit flipped) as two 8-byte words.
+__device__ __forceinline__ void split8(const int4 v, uint2& h, uint2& l) {
+    const uint32_t w0 = (uint32_t)v.x, w1 = (uint32_t)v.y, w2 = (uint32_t)v.z, w3 = (uint32_t)v.w;
+    h = make_uint2(__builtin_amdgcn_perm(w1, w0, 0x07050301u), __builtin_amdgcn_perm(w3, w2, 0x07050301u));
+    l = make_uint2(__builtin_amdgcn_perm(w1, w0, 0x06040200u) ^ 0x80808080u,
+                   __builtin_amdgcn_perm(w3, w2, 0x06040200u) ^ 0x80808080u);
+}
+
+__device__ __forceinline__ int32_t sum8(const int4 v) {   // sum of the 8 int16 lanes
+    const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+    int32_t s = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) s += (int32_t)(int16_t)(w[q] & 0xFFFF) + ((int32_t)w[q] >> 16);
+    return s;
+}
+
 // Rows with k contiguous (the matmul A, row stride lda, 16-byte aligned rows): one wavefront
-// per row, 8 k per lane per 16-byte load; grid (ceil(lines_p / 4), nslab, slices).
+// per row and SLAB of k, 8 k per lane per 16-byte load, the slab's loads all in flight
+// before the first is used; grid (ceil(lines_p / 4), nslab, slices).
 __global__ __launch_bounds__(256) void split_rows_kernel(const int16_t* __restrict__ src, uint64_t slice,
                                                          uint64_t lda, uint32_t rows, uint32_t k,
                                                          int8_t* __restrict__ hi, int8_t* __restrict__ lo,
                                                          int32_t* __restrict__ part, uint32_t lines_p,
                                                          uint32_t kp, uint32_t nslab) {
+    constexpr int U = SLAB / 512;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6), slab = blockIdx.y, bt = blockIdx.z;
     if (row >= lines_p) return;
     const int16_t* r = src + bt * slice + (uint64_t)row * lda;
     const uint64_t po = ((uint64_t)bt * lines_p + row) * kp;
-    int32_t sum = 0;
-    const uint32_t k_end = min(kp, (slab + 1) * SLAB);
-    for (uint32_t k0 = slab * SLAB + 8 * lane; k0 < k_end; k0 += 512) {
-        int4 v;
-        if (row < rows && k0 + 8 <= k) {
-            v = *reinterpret_cast<const int4*>(r + k0);
-        } else {
+    const bool real_row = row < rows;
+    int4 v[U];
+    if (real_row && (slab + 1) * SLAB <= k) {          // the whole slab is real: no branches
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = *reinterpret_cast<const int4*>(r + slab * SLAB + 512 * u + 8 * lane);
+    } else {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t k0 = slab * SLAB + 512 * u + 8 * lane;
             int16_t e[8];
 #pragma unroll
-            for (int q = 0; q < 8; q++) e[q] = (row < rows && k0 + q < k) ? r[k0 + q] : kPad;
-            v = *reinterpret_cast<const int4*>(e);
+            for (int q = 0; q < 8; q++) e[q] = (real_row && k0 + q < k) ? r[k0 + q] : kPad;
+            v[u] = *reinterpret_cast<const int4*>(e);
         }
-        const int16_t* e = reinterpret_cast<const int16_t*>(&v);
+    }
+    int32_t sum = 0;
 #pragma unroll
-        for (int q = 0; q < 8; q++)
-            if (row < rows && k0 + q < k) sum += e[q];
-        const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
-        // high bytes (1, 3 of each dword) and low bytes (0, 2) of 8 lanes
-        const uint32_t h0 = __builtin_amdgcn_perm(w[1], w[0], 0x07050301u);
-        const uint32_t h1 = __builtin_amdgcn_perm(w[3], w[2], 0x07050301u);
-        const uint32_t l0 = __builtin_amdgcn_perm(w[1], w[0], 0x06040200u) ^ 0x80808080u;
-        const uint32_t l1 = __builtin_amdgcn_perm(w[3], w[2], 0x06040200u) ^ 0x80808080u;
-        *reinterpret_cast<uint2*>(hi + po + k0) = make_uint2(h0, h1);
-        *reinterpret_cast<uint2*>(lo + po + k0) = make_uint2(l0, l1);
+    for (int u = 0; u < U; u++) {
+        const uint32_t k0 = slab * SLAB + 512 * u + 8 * lane;
+        if (k0 >= kp) continue;
+        if (real_row && k0 + 8 <= k) {
+            sum += sum8(v[u]);
+        } else {
+            const int16_t* e = reinterpret_cast<const int16_t*>(&v[u]);
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                if (real_row && k0 + q < k) sum += e[q];
+        }
+        uint2 h, l;
+        split8(v[u], h, l);
+        *reinterpret_cast<uint2*>(hi + po + k0) = h;
+        *reinterpret_cast<uint2*>(lo + po + k0) = l;
     }
     for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
     if (lane == 0) part[((uint64_t)bt * nslab + slab) * lines_p + row] = sum;
 }
 
 // Columns of a k-major image (row-major B [k][m] with m % 8 == 0, or the packed 32-column
-// tiles): lane = 4 consecutive k, wave = 8 columns, workgroup = 32 columns; each lane loads
-// 4 rows x 8 columns and transposes them in registers (byte permutes) into one dword of 4 k
-// per column and plane, so a wavefront writes 256 contiguous bytes of each output line.
-// Grid (ceil(lines_p / 32), nslab, slices).
+// tiles).  A wavefront takes 32 columns and 256 k of one SLAB: lane = (r4, c8) with
+// r4 = lane / 4 picking 4 consecutive k of each 64-k group and c8 = lane % 4 picking 8
+// columns, so one load instruction reads 16 rows x 64 contiguous bytes.  Each lane loads
+// its 4 groups x 4 rows x 8 columns at once, then transposes every 4 x 8 block in registers
+// (byte permutes) into one dword of 4 k per column and plane.  A workgroup is the four
+// 256-k quarters of one slab; their column sums meet in LDS.  Grid (ceil(lines_p / 32),
+// nslab, slices).
 __global__ __launch_bounds__(256) void split_cols_kernel(const int16_t* __restrict__ src, uint64_t slice,
                                                          uint32_t packed, uint32_t m, uint32_t k,
                                                          int8_t* __restrict__ hi, int8_t* __restrict__ lo,
                                                          int32_t* __restrict__ part, uint32_t lines_p,
                                                          uint32_t kp, uint32_t nslab) {
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t j0 = blockIdx.x * 32 + (threadIdx.x >> 6) * 8, slab = blockIdx.y, bt = blockIdx.z;
-    if (j0 >= lines_p) return;
+    __shared__ int32_t csum[4][32];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t r4 = lane >> 2, c8 = lane & 3;
+    const uint32_t jg = blockIdx.x * 32, slab = blockIdx.y, bt = blockIdx.z;
+    const uint32_t j0 = jg + 8 * c8;                       // this lane's first column
     const int16_t* b = src + bt * slice;
-    int32_t sum[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    const uint32_t k_end = min(kp, (slab + 1) * SLAB);
+    const uint32_t kq = slab * SLAB + 256 * wave;          // this wave's first k
     const bool cols_real = j0 + 8 <= m;
-    for (uint32_t k0 = slab * SLAB + 4 * lane; k0 < k_end; k0 += 256) {
+    // element (kk, j) of the image
+    auto at = [&](uint32_t kk, uint32_t j) -> uint64_t {
+        return packed ? ((uint64_t)(j >> 5) * k + kk) * 32 + (j & 31) : (uint64_t)kk * m + j;
+    };
+    int4 v[4][4];
+    if (cols_real && kq + 256 <= k) {                  // every load is real: no branches
+        const int16_t* p0 = b + at(kq + 4 * r4, j0);
+        const uint64_t rs = packed ? 32 : m;           // elements per k row
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) v[g][r] = *reinterpret_cast<const int4*>(p0 + (64 * g + r) * rs);
+    } else {
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t kk = kq + 64 * g + 4 * r4 + r;
+                int16_t e[8];
+#pragma unroll
+                for (int q = 0; q < 8; q++) e[q] = (kk < k && j0 + q < m) ? b[at(kk, j0 + q)] : kPad;
+                v[g][r] = *reinterpret_cast<const int4*>(e);
+            }
+    }
+    int32_t sum[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const uint32_t k0 = kq + 64 * g + 4 * r4;
+        if (k0 >= kp) continue;
         uint32_t d[4][4];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const uint32_t kk = k0 + r;
-            int4 v;
-            if (kk < k && cols_real) {
-                const uint64_t off = packed ? ((uint64_t)(j0 >> 5) * k + kk) * 32 + (j0 & 31)
-                                            : (uint64_t)kk * m + j0;
-                v = *reinterpret_cast<const int4*>(b + off);
-            } else {
-                int16_t e[8];
-#pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    const uint32_t j = j0 + q;
-                    const uint64_t off = packed ? ((uint64_t)(j >> 5) * k + kk) * 32 + (j & 31)
-                                                : (uint64_t)kk * m + j;
-                    e[q] = (kk < k && j < m) ? b[off] : kPad;
-                }
-                v = *reinterpret_cast<const int4*>(e);
-            }
-            d[r][0] = (uint32_t)v.x; d[r][1] = (uint32_t)v.y; d[r][2] = (uint32_t)v.z; d[r][3] = (uint32_t)v.w;
-            const int16_t* e = reinterpret_cast<const int16_t*>(&v);
-            if (kk < k) {
+            d[r][0] = (uint32_t)v[g][r].x; d[r][1] = (uint32_t)v[g][r].y;
+            d[r][2] = (uint32_t)v[g][r].z; d[r][3] = (uint32_t)v[g][r].w;
+            if (k0 + r < k) {
+                const int16_t* e = reinterpret_cast<const int16_t*>(&v[g][r]);
 #pragma unroll
                 for (int q = 0; q < 8; q++)
                     if (j0 + q < m) sum[q] += e[q];
@@ -252,12 +295,21 @@ __global__ __launch_bounds__(256) void split_cols_kernel(const int16_t* __restri
             *reinterpret_cast<uint32_t*>(lo + o1) = __builtin_amdgcn_perm(yl, xl, 0x07060302u) ^ 0x80808080u;
         }
     }
+    // column sums: over the 16 lanes of one c8 (lane bits 2..5), then the four waves
 #pragma unroll
     for (int q = 0; q < 8; q++) {
-        int32_t v = sum[q];
-        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-        if (lane == 0) part[((uint64_t)bt * nslab + slab) * lines_p + j0 + q] = v;
+        int32_t x = sum[q];
+        for (int off = 4; off < 64; off <<= 1) x += __shfl_xor(x, off, 64);
+        sum[q] = x;
     }
+    if (r4 == 0) {
+#pragma unroll
+        for (int q = 0; q < 8; q++) csum[wave][8 * c8 + q] = sum[q];
+    }
+    __syncthreads();
+    if (threadIdx.x < 32 && jg + threadIdx.x < lines_p)
+        part[((uint64_t)bt * nslab + slab) * lines_p + jg + threadIdx.x] =
+            csum[0][threadIdx.x] + csum[1][threadIdx.x] + csum[2][threadIdx.x] + csum[3][threadIdx.x];
 }
 
 // ---------------------------------------------------------------- epilogues
@@ -702,7 +754,7 @@ extern "C" int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_
     B.carve(p);
     const uint64_t a_slice = sa > 1 ? (uint64_t)a_bs : 0, b_slice = sb > 1 ? (uint64_t)b_bs : 0;
     if (aligned16(a) && (k & 7) == 0 && (a_slice & 7) == 0) {
-        CM_LAUNCH("split_kernel", split_rows_kernel, dim3(A.lines_p / 4, A.nslab, A.slices), dim3(256), 0, s,
+        CM_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(A.lines_p / 4, A.nslab, A.slices), dim3(256), 0, s,
                   a, a_slice, (uint64_t)k, n, k, A.hi, A.lo, A.part, A.lines_p, A.kp, A.nslab);
     } else {
         rc = run_split<SrcRowMajor, true>(SrcRowMajor{a, n, k, k}, a_slice, A, s);
@@ -712,7 +764,7 @@ extern "C" int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_
     const bool fast_b = aligned16(b) && (b_slice & 7) == 0 &&
                         (layout == 1 || (layout == 0 && (m & 7) == 0) || (layout == 2 && gemv_kw == 1 && (m & 7) == 0));
     if (fast_b) {
-        CM_LAUNCH("split_kernel", split_cols_kernel, dim3(B.lines_p / 32, B.nslab, B.slices), dim3(256), 0, s,
+        CM_LAUNCH("split_cols_kernel", split_cols_kernel, dim3(B.lines_p / 32, B.nslab, B.slices), dim3(256), 0, s,
                   b, b_slice, layout == 1 ? 1u : 0u, m, k, B.hi, B.lo, B.part, B.lines_p, B.kp, B.nslab);
     } else {
         rc = run_split<SrcMatB, false>(SrcMatB{b, m, k, m, layout, gemv_kw}, b_slice, B, s);

@@ -4,6 +4,7 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <string>
 #include <vector>
 
 #include "cm_common.h"
@@ -161,6 +162,7 @@ struct TimingRecord {
 };
 static std::mutex g_tmu;
 static bool g_timing = false;
+static std::string g_select;          // record only this kernel name (empty: all)
 static std::vector<TimingRecord> g_records;
 static std::vector<hipEvent_t> g_free_events;
 
@@ -170,14 +172,16 @@ static hipEvent_t take_event() {
         g_free_events.pop_back();
         return e;
     }
+    // timing only: no system-scope fence (its cache writeback and invalidation would slow
+    // the launches being timed and the ones after them)
     hipEvent_t e = nullptr;
-    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) return nullptr;
     return e;
 }
 
 TimedLaunch::TimedLaunch(const char* name, hipStream_t s) : s_(s) {
     std::lock_guard<std::mutex> lk(g_tmu);
-    if (!g_timing) return;
+    if (!g_timing || (!g_select.empty() && g_select != name)) return;
     TimingRecord r{name, take_event(), take_event()};
     if (!r.start || !r.stop) return;
     if (hipEventRecord(r.start, s) != hipSuccess) return;
@@ -188,7 +192,7 @@ TimedLaunch::TimedLaunch(const char* name, hipStream_t s) : s_(s) {
 TimedLaunch::~TimedLaunch() {
     if (slot_ < 0) return;
     std::lock_guard<std::mutex> lk(g_tmu);
-    if (slot_ < (int)g_records.size()) hipEventRecord(g_records[slot_].stop, s_);
+    if (slot_ < (int)g_records.size()) (void)hipEventRecord(g_records[slot_].stop, s_);
 }
 
 }  // namespace cm
@@ -201,10 +205,16 @@ int cm_timing_enable(int on) {
     return CM_OK;
 }
 
+int cm_timing_select(const char* kernel) {
+    std::lock_guard<std::mutex> lk(cm::g_tmu);
+    cm::g_select = kernel ? kernel : "";
+    return CM_OK;
+}
+
 int cm_timing_reset(void) {
     std::lock_guard<std::mutex> lk(cm::g_tmu);
     for (auto& r : cm::g_records) {
-        hipEventSynchronize(r.stop);
+        (void)hipEventSynchronize(r.stop);
         cm::g_free_events.push_back(r.start);
         cm::g_free_events.push_back(r.stop);
     }

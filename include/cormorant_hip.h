@@ -59,6 +59,10 @@ int cm_host_rowops_table_image(uint8_t* out65536);
 int cm_timing_enable(int on);
 int cm_timing_read(const char* kernel, double* total_ms, uint64_t* launches);
 int cm_timing_reset(void);
+/* Record only the launches of `kernel` (NULL or "": every kernel), so that timing one
+ * kernel inside a loop adds two events per launch of it and none elsewhere.  The events
+ * skip the system-scope fence, so they neither flush caches nor slow the launches after. */
+int cm_timing_select(const char* kernel);
 
 /* ---------------------------------------------------------------- VectorOP
  * Replaces VectorOPKernel (kernels/vectorop_rtl/model/include/VectorOP.h:319-333) and the
