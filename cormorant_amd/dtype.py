@@ -2,8 +2,10 @@
 and power-of-two exponents), used at the edges of a simulated graph.
 
 Mirrors inference-scheduler/src/dtype.py: ``quantize`` (clip, round half to even,
-dtype.py:367-369), ``truncate`` (clip, floor, :371-377), ``quantize_exp`` / ``truncate_exp``
-(:278-291) and the raw storage encodings (``float_to_storage`` :391-395, ``exp_to_storage``).
+dtype.py:367-369), ``truncate`` (clip, floor, :371-377), ``truncate_div`` (clip, toward zero,
+:379-383), ``host_quantize`` (NaN -> 0, then quantize, :214-219), ``quantize_exp`` /
+``truncate_exp`` (:278-291) and the raw storage encodings (``float_to_storage`` :391-395,
+``exp_to_storage``).
 Inside the simulator every tensor is a raw int16 lane array on the device with an exponent
 f (value = raw * 2^-f); the float64 values of the reference's API appear only here.
 """
@@ -38,6 +40,27 @@ class ApFixed16:
         """clip, then floor at 2^-F: a kernel output (dtype.py:371-377)."""
         c = np.clip(np.asarray(x, np.float64), self.min_val, self.max_val)
         return np.floor(c * self.scale) / self.scale
+
+    def truncate_div(self, x) -> np.ndarray:
+        """clip, then toward zero at 2^-F: the DIV output (C integer division, dtype.py:379-383)."""
+        c = np.clip(np.asarray(x, np.float64), self.min_val, self.max_val)
+        return np.trunc(c * self.scale) / self.scale
+
+    def host_quantize(self, x) -> np.ndarray:
+        """What a host op writes back for a double result: NaN -> 0, then quantize
+        (dtype.py:214-219, the generated C host_st())."""
+        x = np.asarray(x, np.float64)
+        return self.quantize(np.where(np.isnan(x), 0.0, x))
+
+    def truncate_exp(self, x, f) -> np.ndarray:
+        """floor at 2^-f, saturate: a kernel output at a power-of-two exponent (dtype.py:287-291)."""
+        s = np.power(2.0, np.asarray(f, np.float64))
+        return np.clip(np.floor(np.asarray(x, np.float64) * s), I16_LO, I16_HI) / s
+
+    def float_to_storage(self, x) -> np.ndarray:
+        """The uint16 storage lanes of values (clip, round half to even; dtype.py:391-395)."""
+        c = np.clip(np.asarray(x, np.float64), self.min_val, self.max_val)
+        return np.round(c * self.scale).astype(np.int16).view(np.uint16)
 
     def quantize_exp(self, x, f) -> np.ndarray:
         """round half to even at 2^-f, saturate, NaN -> 0 (dtype.py:278-285)."""

@@ -33,6 +33,7 @@ class TensorInfo:
     data: Optional[np.ndarray] = None
     wexp: Optional[np.ndarray] = None
     kind: str = "i16"                 # "i16", "i32" (row-ops residual), "f32" (dequant output)
+    raw: bool = False                 # ``data`` holds raw lanes of ``kind`` (a table), not values
 
     @property
     def numel(self) -> int:

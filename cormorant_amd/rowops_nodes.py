@@ -1,0 +1,534 @@
+"""Row-ops node adapters: the reference's RowOps nodes (inference-scheduler/src/rowops_nodes.py)
+as jobs of the GPU row-ops unit.
+
+Each adapter takes what the reference's factory takes -- the tensors with their exponents
+and the float parameters (gamma, beta, eps, bias, the RoPE tables) -- derives the job
+constants and the 16-byte-per-column parameter block exactly as the reference's scheduler
+does (rowops_spec.py norm_params / gamma_scale / beta_bits / bias_bits / bias_params /
+param_block), checks the same eligibility rules (SchedulerError), and lowers to one or
+more ``RoJob``s that ``Simulator`` runs with ``units.rowops`` over raw device tensors.
+The arithmetic itself is the unit's (cm_rowops), so an adapter's output is the
+reference's ``reference()`` of the node bit for bit.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import List, Optional, Sequence
+
+import numpy as np
+
+from .graph import SchedulerError, TensorInfo
+from .units import (F_B_EN, F_NORM_LN, F_P_BCAST, F_RELU, RO_ADDX, RO_COPY, RO_DEQUANT, RO_MULACT,
+                    RO_NORM, RO_ROPE)
+
+# the unit's fixed-point constants (rowops_spec.py:44-49, 316-320)
+P1_BITS = 24          # the normalised value at 2^-24
+BQ_BITS = 20          # beta as an int22 at 2^-20
+ROPE_BITS = 23        # cos / sin as int24 at 2^-23
+SILU_BITS = 20        # silu(g) at 2^-20
+G_BITS = 14           # the gate at 2^-14 inside the unit
+N_MAX = 4096          # elements per row
+K_I16, K_I32, K_F32 = 0, 1, 2
+BIAS_EXTRA = 8        # a COPY with a bias sums 8 bits below the finer grid (rowops_spec.py:160)
+I32_HI = 2 ** 31 - 1
+
+
+# ---------------------------------------------------------------- job constants
+def opword(op: int, ak: int = K_I16, bk: int = K_I16, ck: int = K_I16, b_en=False, p_bcast=False,
+           relu=False, ln=False) -> int:
+    """The op register: [3:0] op, [5:4] / [7:6] / [9:8] the A / B / C kinds, then the flags
+    (rowops_spec.py:569-576)."""
+    return (op | (ak << 4) | (bk << 6) | (ck << 8) | (F_B_EN if b_en else 0) | (F_P_BCAST if p_bcast else 0)
+            | (F_RELU if relu else 0) | (F_NORM_LN if ln else 0))
+
+
+def gamma_scale(gamma) -> int:
+    """g such that the largest |gamma| * 2^g lies in [2^30, 2^31) (rowops_spec.py:124-130)."""
+    m = float(np.max(np.abs(np.asarray(gamma, np.float64)))) if np.size(gamma) else 0.0
+    return 0 if m == 0.0 else 30 - math.floor(math.log2(m))
+
+
+def beta_bits(beta) -> int:
+    """The finest scale 2^-bb (bb <= 20) at which round(beta * 2^bb) fits an int22
+    (rowops_spec.py:133-144)."""
+    if beta is None:
+        return BQ_BITS
+    m = float(np.max(np.abs(np.asarray(beta, np.float64)))) if np.size(beta) else 0.0
+    bb = BQ_BITS
+    while bb > 0 and abs(round(m * 2.0 ** bb)) >= 1 << 21:
+        bb -= 1
+    return bb
+
+
+def bias_bits(bias, f: int) -> int:
+    """A residual bias' scale: the sum's exponent, coarser only where beta_bits needs it
+    (rowops_spec.py:147-151)."""
+    return min(int(f), beta_bits(bias))
+
+
+def quant_bias(bias, f: int) -> np.ndarray:
+    """The bias values as the unit adds them at 2^-f: rounded once at 2^-bias_bits
+    (rowops_spec.py:154-157)."""
+    bb = bias_bits(bias, f)
+    return np.rint(np.asarray(bias, np.float64) * 2.0 ** bb) / 2.0 ** bb
+
+
+def bias_exp(bias, f_x, f_out, extra: int = BIAS_EXTRA) -> np.ndarray:
+    """Per column, the exponent a COPY with a bias sums at: max(f_x, f_out) + extra, at most
+    24, lowered where round(bias * 2^fp) would leave the int22, never below max(f_x, f_out)
+    (rowops_spec.py:163-183)."""
+    bias = np.asarray(bias, np.float64).reshape(-1)
+    n = bias.size
+    lo = np.maximum(np.broadcast_to(np.asarray(f_x, np.int64), (n,)),
+                    np.broadcast_to(np.asarray(f_out, np.int64), (n,)))
+    fp = np.minimum(lo + extra, 24)
+    for _ in range(64):
+        over = np.abs(np.rint(bias * np.power(2.0, fp.astype(np.float64)))) > (1 << 21) - 1
+        if not over.any():
+            break
+        fp = np.where(over, fp - 1, fp)
+    if (fp < lo).any():
+        raise SchedulerError("bias_exp: a bias too large for the int22 parameter at the output's grid")
+    return fp
+
+
+def bias_params(bias, f_x, f_out):
+    """(Bq' [n], sh_a [n], sh_c [n]) of a COPY with a bias at fp = bias_exp
+    (rowops_spec.py:186-196)."""
+    fp = bias_exp(bias, f_x, f_out)
+    n = fp.size
+    bq = np.rint(np.asarray(bias, np.float64).reshape(-1) * np.power(2.0, fp.astype(np.float64))).astype(np.int64)
+    return (bq, fp - np.broadcast_to(np.asarray(f_x, np.int64), (n,)),
+            fp - np.broadcast_to(np.asarray(f_out, np.int64), (n,)))
+
+
+def norm_params(gamma, n: int, eps: float, f_in: int, beta=None, rms: bool = False):
+    """(G int32 [n], g, Bq [n] or None, E): gamma (times sqrt(n) for RMSNorm) at 2^-g, eps as
+    the eps register (eps n^2 2^(2 f_in) for LayerNorm, eps n 2^(2 f_in) for RMSNorm), and
+    beta at the 2^-(24 + g) scale of the product, i.e. round(beta 2^bb) << (24 + g - bb)
+    (rowops_spec.py:199-219)."""
+    gamma = np.asarray(gamma, np.float64)
+    gs = gamma * math.sqrt(n) if rms else gamma
+    g = gamma_scale(gs)
+    G = np.rint(gs * 2.0 ** g).astype(np.int64)
+    if rms:
+        return G, g, None, int(round(eps * n * 2.0 ** (2 * f_in)))
+    E = int(round(eps * n * n * 2.0 ** (2 * f_in)))
+    if beta is None:
+        return G, g, None, E
+    bb = beta_bits(beta)
+    Bq = np.rint(np.asarray(beta, np.float64) * 2.0 ** bb).astype(np.int64) << (P1_BITS + g - bb)
+    return G, g, Bq, E
+
+
+def param_block(G, Bq, sh_a, sh_b, sh_c) -> np.ndarray:
+    """The parameter block of the columns as bytes: per column a 16-byte entry of int32 G,
+    int32 Bq' (an int22, sign-extended), u8 sh_a, sh_b, sh_c and zeros
+    (ROWOPS_RTL_KERNEL.md 1.3; rowops_spec.py:579-601).  Scalars broadcast."""
+    G = np.asarray(G, np.int64).reshape(-1)
+    n = G.size
+    cols = [np.broadcast_to(np.asarray(0 if v is None else v, np.int64), (n,)) for v in (Bq, sh_a, sh_b, sh_c)]
+    Bq, sa, sb, sc = cols
+    if (np.abs(G) > I32_HI).any() or (Bq < -(1 << 21)).any() or (Bq >= 1 << 21).any():
+        raise SchedulerError("param_block: G beyond int32 or Bq' beyond int22")
+    sh = np.stack([sa, sb, sc])
+    if (sh < 0).any() or (sh > 63).any():
+        raise SchedulerError("param_block: a shift outside 0..63")
+    img = np.zeros((n, 16), np.uint8)
+    img[:, 0:4] = (G & 0xFFFFFFFF).astype("<u4").view(np.uint8).reshape(n, 4)
+    img[:, 4:8] = (Bq & 0xFFFFFFFF).astype("<u4").view(np.uint8).reshape(n, 4)
+    img[:, 8], img[:, 9], img[:, 10] = sa, sb, sc
+    return img.reshape(-1)
+
+
+def pblock(G, Bq, sh_a, sh_b, sh_c, n: int):
+    """(block, bcast): one entry with P_BCAST when every column's fields agree, else n
+    entries (rowops_nodes.py:377-384)."""
+    cols = [np.broadcast_to(np.asarray(0 if v is None else v, np.int64), (n,)) for v in (G, Bq, sh_a, sh_b, sh_c)]
+    bcast = all(bool((c == c[0]).all()) for c in cols)
+    if bcast:
+        cols = [c[:1] for c in cols]
+    return param_block(*cols), bcast
+
+
+def rope_tables_raw(cos, sin):
+    """int24 at 2^-23 of the cos / sin tables (rowops_spec.py:267-271)."""
+    return (np.rint(np.asarray(cos, np.float64) * 2.0 ** ROPE_BITS).astype(np.int64),
+            np.rint(np.asarray(sin, np.float64) * 2.0 ** ROPE_BITS).astype(np.int64))
+
+
+def rope_table(cos, sin) -> np.ndarray:
+    """The table a ROPE job streams as B: per position 2 HD int32, cos[0..HD) then
+    sin[0..HD), the float32 [C][HD/2] tables repeated over both halves
+    (rowops_nodes.py rope_raw_tensor)."""
+    cos = np.asarray(cos, np.float32)
+    sin = np.asarray(sin, np.float32)
+    cr, sr = rope_tables_raw(np.concatenate([cos, cos], 1).astype(np.float64),
+                             np.concatenate([sin, sin], 1).astype(np.float64))
+    return np.ascontiguousarray(np.concatenate([cr, sr], axis=1).astype(np.int32))
+
+
+# ---------------------------------------------------------------- jobs
+@dataclass
+class RoJob:
+    """One RowOpsKernel job over the rows of the node's tensors: columns [col0, col0 + n)
+    of A, C (and B, unless ``b_row0`` selects table rows), the op word, the parameter
+    block and the eps / aux / bq_sh registers."""
+    op: int
+    params: np.ndarray
+    n: int
+    col0: int = 0
+    eps: int = 0
+    aux: int = 0
+    bq_sh: int = 0
+    b_row0: Optional[int] = None     # B is a table: job row t reads table row b_row0 + t
+
+
+def _exps(t: TensorInfo, F: int, n: int) -> np.ndarray:
+    """Per-column exponents of the last axis (a scalar exponent broadcast)."""
+    e = np.asarray(F if t.exp is None else t.exp, np.int64).reshape(-1)
+    if e.size == 1:
+        return np.full(n, int(e[0]), np.int64)
+    if e.size != n:
+        raise SchedulerError(f"tensor '{t.onnx_name}': {e.size} exponents for rows of {n}")
+    return e
+
+
+def _require(cond, what: str, msg: str):
+    if not cond:
+        raise SchedulerError(f"{what}: {msg}")
+
+
+class RowOpsAdapter:
+    """Base of the adapters: ``inputs`` / ``output`` tensors and ``jobs()``."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+
+    def jobs(self) -> List[RoJob]:
+        raise NotImplementedError
+
+    @property
+    def n(self) -> int:
+        return int(self.inputs[0].shape[-1])
+
+    @property
+    def rows(self) -> int:
+        return self.inputs[0].numel // self.n
+
+
+# ---------------------------------------------------------------- adapters
+@dataclass
+class LayerNormRoNode(RowOpsAdapter):
+    """ONNX LayerNormalization of Q8.8 rows on the unit (rowops_nodes.py:161-262): NORM with
+    NORM_LN, gamma at 2^-g, beta as Bq' at 2^-bb, eps as E = eps n^2 2^16."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    gamma: Optional[np.ndarray] = None
+    beta: Optional[np.ndarray] = None
+    eps: float = 1e-5
+    F: int = 8
+
+    def __post_init__(self):
+        n, what = self.n, f"LayerNormalization '{self.output.onnx_name}'"
+        for t in (self.inputs[0], self.output):
+            _require(t.exp is None and t.kind == "i16", what, f"'{t.onnx_name}' is not a plain Q8.8 tensor")
+        _require(n <= N_MAX, what, f"rows of {n} elements (the unit takes {N_MAX})")
+        self.gamma = np.ones(n) if self.gamma is None else np.asarray(self.gamma, np.float64).reshape(-1)
+        self.beta = np.zeros(n) if self.beta is None else np.asarray(self.beta, np.float64).reshape(-1)
+        _require(np.isfinite(self.gamma).all() and np.isfinite(self.beta).all(), what, "gamma / beta are not finite")
+        G, g, _bq, E = norm_params(self.gamma, n, self.eps, self.F, beta=self.beta)
+        _require(g + 4 <= 63 and P1_BITS + g - 8 <= 63, what, f"gamma's exponent 2^-{g} beyond the shifts")
+        bb = beta_bits(self.beta)
+        bqp = np.rint(self.beta * 2.0 ** bb).astype(np.int64)
+        _require((np.abs(bqp) < 2 ** 21).all() and P1_BITS + g - bb <= 63, what, "beta beyond the int22")
+        _require(0 <= E < 2 ** 63, what, f"eps {self.eps} beyond the eps register")
+        self.g, self.bb, self.E = int(g), int(bb), int(E)
+        self._params = param_block(G, bqp, 0, 0, P1_BITS + g - self.F)
+
+    def jobs(self):
+        return [RoJob(opword(RO_NORM, ln=True), self._params, self.n, eps=self.E, bq_sh=P1_BITS + self.g - self.bb)]
+
+
+@dataclass
+class LayerNorm32RoNode(RowOpsAdapter):
+    """A LayerNorm of the int32 residual at 2^-fr into int16 at per-channel exponents
+    (rowops_nodes.py:1282-1412, _layernorm32)."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    gamma: np.ndarray = None
+    beta: np.ndarray = None
+    eps: float = 1e-6
+    F: int = 8
+
+    def __post_init__(self):
+        h, y = self.inputs[0], self.output
+        n, what = self.n, f"LayerNorm32 '{y.onnx_name}'"
+        fr = _exps(h, self.F, n)
+        _require(h.kind == "i32" and (fr == fr[0]).all(), what, "h: the int32 residual at one exponent")
+        _require(y.kind == "i16" and y.numel == h.numel and y.shape[-1] == n, what, "output: int16 of h's shape")
+        gamma = np.asarray(self.gamma, np.float64).reshape(-1)
+        beta = np.asarray(self.beta, np.float64).reshape(-1)
+        _require(gamma.size == n and beta.size == n and np.isfinite(gamma).all() and np.isfinite(beta).all(),
+                 what, "gamma / beta [n]")
+        G, g, _bq, E = norm_params(gamma, n, self.eps, int(fr[0]), beta=beta)
+        bb = beta_bits(beta)
+        bq = np.rint(beta * 2.0 ** bb).astype(np.int64)
+        sh_c = P1_BITS + g - _exps(y, self.F, n)
+        _require((sh_c >= 0).all() and (sh_c <= 63).all() and 0 <= P1_BITS + g - bb <= 63, what,
+                 f"gamma's exponent 2^-{g} beyond the shifts")
+        _require(0 <= E < 2 ** 63, what, f"eps {self.eps} beyond the eps register")
+        _require(n <= N_MAX, what, f"rows of {n} beyond {N_MAX}")
+        self.fr, self.g, self.bb, self.E = int(fr[0]), int(g), int(bb), int(E)
+        self._params, self.bcast = pblock(G, bq, 0, 0, sh_c, n)
+
+    def jobs(self):
+        return [RoJob(opword(RO_NORM, K_I32, K_I16, K_I16, p_bcast=self.bcast, ln=True), self._params, self.n,
+                      eps=self.E, bq_sh=P1_BITS + self.g - self.bb)]
+
+
+@dataclass
+class RMSNormRoNode(RowOpsAdapter):
+    """LlmRMSNorm of an int32 tensor at 2^-fr into int16 at per-channel exponents, rows of
+    gamma's length (rowops_nodes.py:449-496, from_llm_rmsnorm :617-649)."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    gamma: np.ndarray = None
+    eps: float = 1e-5
+    F: int = 8
+
+    @property
+    def n(self) -> int:
+        return int(np.asarray(self.gamma).size)
+
+    def __post_init__(self):
+        h, y = self.inputs[0], self.output
+        self.gamma = np.asarray(self.gamma, np.float64).reshape(-1)
+        n, W, what = self.n, int(h.shape[-1]), f"RMSNorm '{y.onnx_name}'"
+        fr = _exps(h, self.F, W)
+        _require(h.kind == "i32" and (fr == fr[0]).all(), what, "h: an int32 tensor at one exponent")
+        _require(y.kind == "i16" and y.numel == h.numel and y.shape[-1] == W, what, "output: int16 of h's shape")
+        _require(W % n == 0 and n <= N_MAX, what, "gamma size")
+        G, g, _b, E = norm_params(self.gamma, n, self.eps, int(fr[0]), rms=True)
+        fo = _exps(y, self.F, W)
+        _require((fo.reshape(-1, n) == fo[:n]).all(), what, "output exponents: one per channel of a head")
+        sh_c = P1_BITS + g - fo[:n]
+        _require((sh_c >= 0).all() and (sh_c <= 63).all(), what, f"gamma's exponent 2^-{g} beyond the shifts")
+        _require(0 <= E < 2 ** 63, what, f"eps {self.eps} beyond the eps register")
+        self.fr, self.g, self.E = int(fr[0]), int(g), int(E)
+        self._params, self.bcast = pblock(G, 0, 0, 0, sh_c, n)
+
+    def jobs(self):
+        return [RoJob(opword(RO_NORM, K_I32, K_I16, K_I16, p_bcast=self.bcast), self._params, self.n, eps=self.E)]
+
+
+@dataclass
+class ResAddRoNode(RowOpsAdapter):
+    """LlmResAdd: h1 = sat32(h + (d << (fr - f_d))), the int32 residual plus the int16 delta at
+    its per-channel exponents, one ADDX job (rowops_nodes.py:401-447, from_llm_resadd)."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    F: int = 8
+
+    def __post_init__(self):
+        h, d, y = self.inputs[0], self.inputs[1], self.output
+        n, what = self.n, f"ResAdd '{y.onnx_name}'"
+        fr = _exps(h, self.F, n)
+        _require(h.kind == "i32" and (fr == fr[0]).all() and y.kind == "i32"
+                 and (_exps(y, self.F, n) == fr[0]).all(), what, "h and the output: the int32 residual at one exponent")
+        _require(d.kind == "i16" and d.shape[-1] == n and d.numel == h.numel == y.numel, what,
+                 "delta: int16 of the residual's shape")
+        fd = _exps(d, self.F, n)
+        _require((fd <= fr[0]).all() and (fr[0] - fd <= 63).all(), what, "delta exponents beyond the residual's")
+        _require(n <= N_MAX, what, f"rows of {n} beyond {N_MAX}")
+        self.fr = int(fr[0])
+        self._params, self.bcast = pblock(0, 0, 0, self.fr - fd, 0, n)
+
+    def jobs(self):
+        return [RoJob(opword(RO_ADDX, K_I32, K_I16, K_I32, b_en=True, p_bcast=self.bcast), self._params, self.n)]
+
+
+@dataclass
+class ResAddBiasRoNode(RowOpsAdapter):
+    """A residual add with a per-channel bias (VitResAdd): h1 = sat32(h + (d << (fr - f_d)) +
+    (Bq' << (fr - bb))), Bq' = round(bias 2^bb), bb = bias_bits(bias, fr); h int16 or int32
+    at one exponent (rowops_nodes.py:1237-1280, _resadd_bias)."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    bias: np.ndarray = None
+    F: int = 8
+
+    def __post_init__(self):
+        h, d, y = self.inputs[0], self.inputs[1], self.output
+        n, what = self.n, f"ResAddBias '{y.onnx_name}'"
+        fr = _exps(y, self.F, n)
+        fa = _exps(h, self.F, n)
+        _require(y.kind == "i32" and (fr == fr[0]).all(), what, "the output: the int32 residual at one exponent")
+        _require(h.kind == "i16" or (fa == fa[0]).all(), what, "an int32 h at one exponent")
+        _require(d.kind == "i16" and d.shape[-1] == n and d.numel == h.numel == y.numel, what, "shapes")
+        fd = _exps(d, self.F, n)
+        fr = int(fr[0])
+        _require((fa <= fr).all() and (fd <= fr).all() and (fr - fa <= 63).all() and (fr - fd <= 63).all(), what,
+                 f"exponents beyond the residual's 2^-{fr}")
+        bias = np.asarray(self.bias, np.float64).reshape(-1)
+        _require(bias.size == n and np.isfinite(bias).all(), what, "bias [n]")
+        self.fr, self.bb, self.a32 = fr, bias_bits(bias, fr), h.kind == "i32"
+        bq = np.rint(bias * 2.0 ** self.bb).astype(np.int64)
+        self._params, self.bcast = pblock(0, bq, fr - fa, fr - fd, 0, n)
+
+    def jobs(self):
+        op = opword(RO_ADDX, K_I32 if self.a32 else K_I16, K_I16, K_I32, b_en=True, p_bcast=self.bcast)
+        return [RoJob(op, self._params, self.n, bq_sh=self.fr - self.bb)]
+
+
+@dataclass
+class WidenRoNode(RowOpsAdapter):
+    """LlmWiden: int16 at per-channel exponents -> int32 at one exponent fy >= each, exact
+    (one COPY, A << (fy - f[c]); rowops_nodes.py:498-539, from_llm_widen)."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    F: int = 8
+
+    def __post_init__(self):
+        x, y = self.inputs[0], self.output
+        n, what = self.n, f"Widen '{y.onnx_name}'"
+        _require(x.kind == "i16" and y.kind == "i32" and y.numel == x.numel and y.shape[-1] == n, what, "shapes")
+        fx, fy = _exps(x, self.F, n), _exps(y, self.F, n)
+        _require((fy == fy[0]).all() and (fx <= fy[0]).all() and (fy[0] - fx <= 16).all(), what,
+                 "one output exponent, at most 16 finer than each input's")
+        self._params, self.bcast = pblock(0, 0, fy[0] - fx, 0, 0, n)
+
+    def jobs(self):
+        return [RoJob(opword(RO_COPY, K_I16, K_I16, K_I32, p_bcast=self.bcast), self._params, self.n)]
+
+
+@dataclass
+class SiluMulRoNode(RowOpsAdapter):
+    """LlmSiluMul: a = silu(g) * u, g int16 at per-channel exponents <= 14, u and a at theirs,
+    one MULACT job (rowops_nodes.py:540-563, from_llm_silu_mul)."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    F: int = 8
+
+    def __post_init__(self):
+        g, u, y = self.inputs[0], self.inputs[1], self.output
+        n, what = self.n, f"SiluMul '{y.onnx_name}'"
+        for t in (g, u, y):
+            _require(t.kind == "i16" and t.shape[-1] == n and t.numel == g.numel, what, "int16 tensors of one shape")
+        fg, fu, fa = (_exps(t, self.F, n) for t in (g, u, y))
+        _require((fg <= G_BITS).all(), what, f"gate exponents above {G_BITS}")
+        sh_c = SILU_BITS + fu - fa
+        _require((sh_c >= 0).all() and (sh_c <= 63).all(), what, "up / output exponents beyond the shifts")
+        _require(n <= N_MAX, what, f"rows of {n} beyond {N_MAX}")
+        self._params, self.bcast = pblock(0, 0, G_BITS - fg, 0, sh_c, n)
+
+    def jobs(self):
+        return [RoJob(opword(RO_MULACT, b_en=True, p_bcast=self.bcast), self._params, self.n)]
+
+
+@dataclass
+class DequantRoNode(RowOpsAdapter):
+    """LlmDequant: int16 at per-channel exponents (or the int32 residual) -> float32
+    raw * 2^-f[c], round to nearest even (exact below 2^24).  A single row longer than the
+    unit's 4096 (the logits) runs as one job per contiguous chunk, each with the parameter
+    block of its columns (rowops_nodes.py:2501-2612, from_llm_dequant)."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    F: int = 8
+    align_elems: int = 8
+
+    def __post_init__(self):
+        x, y = self.inputs[0], self.output
+        n, what = self.n, f"Dequant '{y.onnx_name}'"
+        _require(x.kind in ("i16", "i32") and y.kind == "f32" and y.numel == x.numel and y.shape[-1] == n, what,
+                 "shapes / kinds")
+        f = _exps(x, self.F, n)
+        _require((f >= 0).all() and (f <= 63).all(), what, "exponents beyond the shifts")
+        self.a32 = x.kind == "i32"
+        if n <= N_MAX:
+            pb, bc = pblock(0, 0, 0, 0, f, n)
+            self._chunks = [(0, n, pb, bc)]
+            return
+        _require(x.numel == n, what, f"a row of {n} (> {N_MAX}): one row")
+        nc = next((d for d in range(N_MAX, 0, -1) if n % d == 0 and d % self.align_elems == 0), 0)
+        _require(nc > 0, what, f"a row of {n} has no divisor <= {N_MAX} that is a multiple of {self.align_elems}")
+        self._chunks = [(k * nc, nc) + pblock(0, 0, 0, 0, f[k * nc:(k + 1) * nc], nc) for k in range(n // nc)]
+
+    def jobs(self):
+        ak = K_I32 if self.a32 else K_I16
+        return [RoJob(opword(RO_DEQUANT, ak, K_I16, K_F32, p_bcast=bc), pb, nc, col0=c0)
+                for c0, nc, pb, bc in self._chunks]
+
+
+@dataclass
+class BiasCopyRoNode(RowOpsAdapter):
+    """A COPY with a per-column bias (the vision / TTS bias adds): y = sat16(rne((x << (fp -
+    f_x)) + round(bias 2^fp), fp - f_out)), then ReLU with ``relu`` -- rowops_spec.bias_round
+    (rowops_spec.py:199-208) with fp = bias_exp."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    bias: np.ndarray = None
+    relu: bool = False
+    F: int = 8
+
+    def __post_init__(self):
+        x, y = self.inputs[0], self.output
+        n, what = self.n, f"BiasCopy '{y.onnx_name}'"
+        _require(x.kind == "i16" and y.kind == "i16" and y.numel == x.numel and y.shape[-1] == n, what, "shapes")
+        bias = np.asarray(self.bias, np.float64).reshape(-1)
+        _require(bias.size == n and n <= N_MAX, what, "bias [n], rows of at most 4096")
+        bq, sa, sc = bias_params(bias, _exps(x, self.F, n), _exps(y, self.F, n))
+        self._params, self.bcast = pblock(0, bq, sa, 0, sc, n)
+
+    def jobs(self):
+        return [RoJob(opword(RO_COPY, relu=self.relu, p_bcast=self.bcast), self._params, self.n)]
+
+
+@dataclass
+class RopeRoNode(RowOpsAdapter):
+    """Rotate-half RoPE of [T][nh * HD] rows (q or k) at per-head exponents into int16 at the
+    output's per-head exponents, position pos + t for row t -- one ROPE job with the cos / sin
+    table as B (rowops_spec.rope; the RoPE jobs of AttnPrepRoNode, rowops_nodes.py:1008-1014
+    and from_llm_attn_prep's rope_params :1181-1191).  ``table`` is the float32 [C][HD/2]
+    cos / sin pair."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    heads: int = 1
+    head_dim: int = 16
+    cos: np.ndarray = None
+    sin: np.ndarray = None
+    pos: int = 0
+    F: int = 8
+    table: Optional[TensorInfo] = field(default=None, init=False)
+
+    def __post_init__(self):
+        x, y = self.inputs[0], self.output
+        nh, HD = self.heads, self.head_dim
+        n, what = self.n, f"RoPE '{y.onnx_name}'"
+        _require(n == nh * HD and HD % 2 == 0 and n <= N_MAX, what, f"rows of {nh} x {HD}")
+        _require(x.kind == "i16" and y.kind == "i16" and y.numel == x.numel and y.shape[-1] == n, what, "shapes")
+        fx = _exps(x, self.F, n).reshape(nh, HD)
+        fo = _exps(y, self.F, n).reshape(nh, HD)
+        half = HD // 2
+        frot = np.concatenate([fx[:, half:], fx[:, :half]], axis=1)
+        fp = np.maximum(fx, frot)
+        sa, sb, sc = fp - fx, fp - frot, fp + ROPE_BITS - fo
+        _require((sa <= 63).all() and (sb <= 63).all() and (sc >= 0).all() and (sc <= 63).all(), what,
+                 "RoPE exponents beyond the shifts")
+        tab = rope_table(self.cos, self.sin)
+        _require(tab.shape[1] == 2 * HD and 0 <= self.pos and self.pos + self.rows <= tab.shape[0], what,
+                 "cos / sin tables [C][HD/2] covering pos .. pos + rows")
+        self.table = TensorInfo(f"{y.onnx_name}__rope_table", list(tab.shape), data=tab, kind="i32", raw=True)
+        self._params, self.bcast = pblock(0, 0, sa.reshape(-1), sb.reshape(-1), sc.reshape(-1), n)
+
+    def jobs(self):
+        return [RoJob(opword(RO_ROPE, K_I16, K_I32, K_I16, b_en=True, p_bcast=self.bcast), self._params, self.n,
+                      aux=self.head_dim, b_row0=self.pos)]
+
+
+ADAPTERS = (LayerNormRoNode, LayerNorm32RoNode, RMSNormRoNode, ResAddRoNode, ResAddBiasRoNode, WidenRoNode,
+            SiluMulRoNode, DequantRoNode, BiasCopyRoNode, RopeRoNode)
+
+__all__ = ["RoJob", "RowOpsAdapter", "opword", "gamma_scale", "beta_bits", "bias_bits", "quant_bias", "bias_exp",
+           "bias_params", "norm_params", "param_block", "pblock", "rope_tables_raw", "rope_table"] + \
+          [c.__name__ for c in ADAPTERS]

@@ -19,8 +19,11 @@ from .dtype import AP_FIXED_16_8, ApFixed16
 from .graph import (ConvNode, Graph, MatmulNode, PoolNode, ReshapeNode, RowOpsNode, ScheduledNode,
                     SchedulerError, SoftmaxVopNode, TensorInfo)
 from .packing import conv_bias_image, conv_weight_image, pack_matmul_b
+from .rowops_nodes import RoJob, RowOpsAdapter
 
 _TORCH = {"i16": torch.int16, "i32": torch.int32, "f32": torch.float32}
+_NP = {"i16": np.int16, "i32": np.int32, "f32": np.float32}
+_KB = {"i16": 2, "i32": 4, "f32": 4}
 
 
 def _pad8(n: int) -> int:
@@ -77,6 +80,8 @@ class Simulator:
                 raw[sn.output.onnx_name] = self._softmax(sn, raw)
             elif isinstance(sn, RowOpsNode):
                 raw[sn.output.onnx_name] = self._rowops(sn, raw)
+            elif isinstance(sn, RowOpsAdapter):
+                raw[sn.output.onnx_name] = self._adapter(sn, raw)
             elif isinstance(sn, ScheduledNode):
                 raw[sn.output.onnx_name] = self._vectorop(sn, raw)
             else:
@@ -111,6 +116,9 @@ class Simulator:
         if t.data is None:
             raise KeyError(f"tensor '{t.onnx_name}' has no value (not an input, weight or node output)")
         w = self._weights.get(t.onnx_name)
+        if w is None and t.raw:
+            w = torch.from_numpy(np.ascontiguousarray(np.asarray(t.data).astype(_NP[t.kind]))).to(self.device)
+            self._weights[t.onnx_name] = w
         if w is None:
             # a weight as the kernels read it (_simulate.py:531-539): quantized to the element
             # type's grid; with a rank-1 exponent the stored data is raw / 2^F, so its raw lanes
@@ -296,6 +304,46 @@ class Simulator:
         units.rowops(as_u8(a_buf), as_u8(b_buf), as_u8(c_buf), p, sn.op, n, rows, 1, a_s1, 0, b_s1, 0,
                      c_s1, 0, sn.eps, sn.aux, sn.bq_sh, sn.win_lo, sn.win_hi)
         return c_buf.view(rows, c_per)[:, :ot.shape[-1]].reshape(-1).contiguous()
+
+    def _rows16(self, x2d: torch.Tensor, kind: str):
+        """[rows][w] lanes re-laid at a 16-byte row stride: (buffer, stride bytes, lanes per row)."""
+        rows, w = x2d.shape
+        per = ((_KB[kind] * w + 15) & ~15) // _KB[kind]
+        buf = torch.zeros((rows, per), dtype=_TORCH[kind], device=self.device)
+        buf[:, :w] = x2d
+        return buf, per * _KB[kind], per
+
+    def _adapter(self, sn: RowOpsAdapter, raw) -> torch.Tensor:
+        """A row-ops adapter: its jobs over row views of the tensors (rows of ``n`` = the job
+        width; a job covers the columns [col0, col0 + n) of every row)."""
+        at, ot = sn.inputs[0], sn.output
+        bt = getattr(sn, "table", None) or (sn.inputs[1] if len(sn.inputs) > 1 else None)
+        jobs = sn.jobs()
+        width = max(j.col0 + j.n for j in jobs)
+        rows = at.numel // width
+        a2d = self._get(at, raw).reshape(rows, width)
+        out = torch.empty((rows, width), dtype=_TORCH[ot.kind], device=self.device)
+        b_all = self._get(bt, raw) if bt is not None else None
+        u8 = lambda t: t.reshape(-1).view(torch.uint8) if t is not None else None   # noqa: E731
+        for j in jobs:
+            a_buf, a_s1, _ = self._rows16(a2d[:, j.col0:j.col0 + j.n], at.kind)
+            b_buf, b_s1 = None, 0
+            if b_all is not None:
+                if j.b_row0 is None:
+                    b2d = b_all.reshape(rows, width)[:, j.col0:j.col0 + j.n]
+                else:
+                    tab = b_all.reshape(-1, int(bt.shape[-1]))
+                    if j.b_row0 + rows > tab.shape[0]:
+                        raise SchedulerError("row-ops job: table rows past the table")
+                    b2d = tab[j.b_row0:j.b_row0 + rows]
+                b_buf, b_s1, _ = self._rows16(b2d, bt.kind)
+            c_buf, c_s1, c_per = self._rows16(torch.zeros((rows, j.n), dtype=_TORCH[ot.kind], device=self.device),
+                                              ot.kind)
+            p = torch.from_numpy(np.ascontiguousarray(j.params, np.uint8)).to(self.device)
+            units.rowops(u8(a_buf), u8(b_buf), u8(c_buf), p, j.op, j.n, rows, 1, a_s1, 0, b_s1, 0, c_s1, 0,
+                         j.eps, j.aux, j.bq_sh, 0, 0xFFFFFFFF)
+            out[:, j.col0:j.col0 + j.n] = c_buf[:, :j.n]
+        return out.reshape(-1)
 
 
 __all__ = ["Simulator"]
