@@ -34,6 +34,8 @@ class TensorInfo:
     wexp: Optional[np.ndarray] = None
     kind: str = "i16"                 # "i16", "i32" (row-ops residual), "f32" (dequant output)
     raw: bool = False                 # ``data`` holds raw lanes of ``kind`` (a table), not values
+    chexp: Optional[np.ndarray] = None        # per-channel exponents of axis 1 (NCHW), tensor.py
+    group_layout: Optional[tuple] = None      # (KV, HD): a [C][KV * HD] cache stored group-major
 
     @property
     def numel(self) -> int:
@@ -148,6 +150,48 @@ class RowOpsNode:
     win_hi: int = 0xFFFFFFFF
 
 
+KEY_QUANTUM = 16
+
+
+def attn_keys(pos: int, n: int, T: int, C: int, q: int = KEY_QUANTUM):
+    """(valid rows n, keys) of a prefill-attention call: n clamped to 0 <= n <= T and
+    pos + n <= C; the kernels run over keys = roundup(pos + n, q), at least q, at most C
+    (llm_nodes.py:960-968)."""
+    n = max(0, min(int(n), T, C - int(pos))) if int(pos) < C else 0
+    k = -(-(int(pos) + n) // q) * q
+    return n, max(q, min(k, C))
+
+
+@dataclass
+class LlmAttnConvNode:
+    """One attention contraction of KV group ``group`` with a runtime key count
+    (llm_nodes.py:1183-1425, reference() :1407-1425):
+      kind "qk": s_g[j][p] = sum_d K_g[j][d] qx_g[d][p] for the cache rows j < keys,
+                 inputs [K cache [C][KV HD] (group-major), qx [KV][HD][G T], pos, n],
+                 output [C][G T] (rows >= keys zero);
+      kind "pv": o_g[p][d] = sum_{j < keys} P_g[p][j] V_g[j][d],
+                 inputs [P_g [G T][C], V cache [C][KV HD] (group-major), pos, n],
+                 output [G T][HD].
+    Raw integer sums, int32 wrap, floor(/ 2^8), saturated (_kernel_out :995-1001).
+    ``static``: no pos / n, keys = C."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    kind: str = "qk"
+    group: int = 0
+    T: int = 1
+    H: int = 1
+    KV: int = 1
+    HD: int = 16
+    C: int = 16
+    Q: int = KEY_QUANTUM
+    static: bool = False
+    has_n: bool = True
+
+    @property
+    def G(self) -> int:
+        return self.H // self.KV
+
+
 @dataclass
 class Graph:
     """Nodes in topological order plus the graph's inputs, outputs and weights."""
@@ -171,6 +215,7 @@ def conv_out(size: int, k: int, stride: int, pad_lo: int, pad_hi: int, dil: int 
 
 
 __all__ = ["SchedulerError", "TensorInfo", "ScheduledNode", "MatmulNode", "ConvNode", "PoolNode",
-           "ReshapeNode", "SoftmaxVopNode", "RowOpsNode", "Graph", "conv_out", "OP_ADD", "OP_SUB",
+           "ReshapeNode", "SoftmaxVopNode", "RowOpsNode", "LlmAttnConvNode", "attn_keys", "KEY_QUANTUM",
+           "Graph", "conv_out", "OP_ADD", "OP_SUB",
            "OP_MUL", "OP_DIV", "OP_RELU", "OP_RELU6", "OP_SOFTMAX", "OP_SOFTMAX_T", "POOL_MAX",
            "POOL_AVG", "POOL_LP"]

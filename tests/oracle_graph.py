@@ -9,7 +9,12 @@ import numpy as np
 
 from cormorant_amd import graph as G
 from cormorant_amd.dtype import AP_FIXED_16_8 as DT
+from cormorant_amd.rowops_nodes import RowOpsAdapter
 from oracle import cm
+
+F = DT.frac_bits
+_NP = {"i16": np.int16, "i32": np.int32, "f32": np.float32}
+_KB = {"i16": 2, "i32": 4, "f32": 4}
 
 
 def _conv_int(x, w, sh, sw, pt, pl, dh, dw, oh, ow, dwise):
@@ -32,7 +37,109 @@ def _conv_int(x, w, sh, sw, pt, pl, dh, dw, oh, ow, dwise):
 
 
 def _weight(t):
-    return DT.quantize(np.asarray(t.data, np.float64).reshape(t.shape))
+    """_weight_value (_simulate.py:531-539): quantized data, times 2^(F - wexp) when encoded."""
+    v = DT.quantize(np.asarray(t.data, np.float64).reshape(t.shape))
+    if t.wexp is not None:
+        v = v * np.power(2.0, F - np.asarray(t.wexp, np.float64))
+    return v
+
+
+def _pow2(*ts):
+    return any(t is not None and (t.exp is not None or t.wexp is not None or t.chexp is not None) for t in ts)
+
+
+def _wrap_floor(acc):
+    """The ap_fixed<32,16> accumulator: wrap to int32, floor(/ 2^F), saturate (_simulate.py:826-831)."""
+    big = np.abs(acc) >= 2.0 ** 31
+    if big.any():
+        acc = np.where(big, np.mod(acc + 2.0 ** 31, 2.0 ** 32) - 2.0 ** 31, acc)
+    return np.clip(np.floor(acc / float(1 << F)), -32768, 32767)
+
+
+def _matmul_exp(sn, a, b):
+    """_simulate.py:814-835."""
+    fo = np.asarray(F if sn.output.exp is None else sn.output.exp, np.float64)
+    acc = np.matmul(a, b) * np.power(2.0, fo + F)
+    assert np.array_equal(acc, np.round(acc)), "accumulator not on the 2^-(f_out+F) grid"
+    return _wrap_floor(acc) / np.power(2.0, fo)
+
+
+def _conv_exp(sn, x, w, bias):
+    """_simulate.py:784-812."""
+    xt, wt, yt = sn.inputs[0], sn.inputs[1], sn.output
+    fx = (np.asarray(xt.chexp, np.float64).reshape(1, -1, 1, 1) if xt.chexp is not None
+          else float(np.asarray(F if xt.exp is None else xt.exp)))
+    fy = (np.asarray(yt.chexp, np.float64).reshape(1, -1, 1, 1) if yt.chexp is not None
+          else float(np.asarray(F if yt.exp is None else yt.exp)))
+    fw = np.asarray(F if wt.wexp is None else wt.wexp, np.float64)
+    x_raw = np.asarray(x, np.float64).reshape(sn.batch, sn.in_ch, sn.in_h, sn.in_w) * np.power(2.0, fx)
+    w_raw = np.asarray(w, np.float64).reshape(sn.out_ch, 1 if sn.is_depthwise else sn.in_ch, sn.kh, sn.kw) \
+        * np.power(2.0, fw)
+    acc = _conv_int(x_raw, w_raw, sn.stride_h, sn.stride_w, sn.pad_top, sn.pad_left, sn.dilation_h,
+                    sn.dilation_w, sn.out_h, sn.out_w, sn.is_depthwise)
+    if bias is not None:
+        acc = acc + (np.asarray(bias, np.float64).reshape(1, -1, 1, 1) * np.power(2.0, fy)) * 2.0 ** F
+    assert np.array_equal(acc, np.round(acc)), "conv operands off their grids"
+    return _wrap_floor(acc) / np.power(2.0, fy)
+
+
+def _raw_of(t, v):
+    """Raw integers of a tensor's values (per-channel exponents of the last axis or axis 1)."""
+    if t.chexp is not None:
+        e = np.asarray(t.chexp, np.float64).reshape((1, -1) + (1,) * (len(t.shape) - 2))
+    else:
+        e = np.asarray(F if t.exp is None else t.exp, np.float64)
+    return np.rint(np.asarray(v, np.float64).reshape(t.shape) * np.power(2.0, e)).astype(np.int64)
+
+
+def _attn_conv(sn, w, x, pos, n):
+    """LlmAttnConvNode.reference (llm_nodes.py:1407-1425) on logical arrays; raw integers."""
+    keys = sn.C if sn.static else G.attn_keys(int(pos), int(n) if sn.has_n else sn.T, sn.T, sn.C, sn.Q)[1]
+    g, HD = sn.group, sn.HD
+    if sn.kind == "qk":
+        kc = _raw_of(sn.inputs[0], w)[:keys, g * HD:(g + 1) * HD].astype(np.float64)
+        B = np.asarray(x, np.float64).reshape(sn.KV, HD, sn.G * sn.T)[g]
+        out = np.zeros((sn.C, sn.G * sn.T))
+        out[:keys] = _wrap_floor(kc @ B)
+        return out
+    P = np.asarray(w, np.float64).reshape(sn.G * sn.T, sn.C)[:, :keys]
+    vc = _raw_of(sn.inputs[1], x)[:keys, g * HD:(g + 1) * HD].astype(np.float64)
+    return _wrap_floor(P @ vc)
+
+
+def _rows16(x2d, kind):
+    rows, w = x2d.shape
+    stride = (_KB[kind] * w + 15) & ~15
+    img = np.zeros((rows, stride), np.uint8)
+    img[:, :_KB[kind] * w] = np.ascontiguousarray(x2d.astype(_NP[kind])).view(np.uint8).reshape(rows, -1)
+    return img.reshape(-1), stride
+
+
+def run_adapter(node, raw_of):
+    """A row-ops adapter's jobs through the C oracle with the Simulator's row re-layout:
+    ``raw_of(tensor)`` gives the raw lanes of an input; returns the raw output."""
+    at, ot = node.inputs[0], node.output
+    bt = getattr(node, "table", None) or (node.inputs[1] if len(node.inputs) > 1 else None)
+    jobs = node.jobs()
+    width = max(j.col0 + j.n for j in jobs)
+    rows = at.numel // width
+    a2d = np.asarray(raw_of(at)).reshape(rows, width)
+    out = np.zeros((rows, width), _NP[ot.kind])
+    for j in jobs:
+        a_img, a_s1 = _rows16(a2d[:, j.col0:j.col0 + j.n], at.kind)
+        b_img, b_s1 = None, 0
+        if bt is not None:
+            if j.b_row0 is None:
+                b2d = np.asarray(raw_of(bt)).reshape(rows, width)[:, j.col0:j.col0 + j.n]
+            else:
+                b2d = np.asarray(bt.data).reshape(-1, bt.shape[-1])[j.b_row0:j.b_row0 + rows]
+            b_img, b_s1 = _rows16(b2d, bt.kind)
+        c_img, c_s1 = _rows16(np.zeros((rows, j.n), _NP[ot.kind]), ot.kind)
+        cm.rowops_reset_params()
+        cm.rowops(a_img, b_img, c_img, j.params, j.op, j.n, rows, 1, a_s1, 0, b_s1, 0, c_s1, 0, j.eps, j.aux,
+                  j.bq_sh)
+        out[:, j.col0:j.col0 + j.n] = c_img.reshape(rows, c_s1)[:, :_KB[ot.kind] * j.n].copy().view(_NP[ot.kind])
+    return out
 
 
 def forward(graph, inputs):
@@ -42,7 +149,29 @@ def forward(graph, inputs):
         out = sn.output
         if isinstance(sn, G.MatmulNode):
             a, b = get(sn.inputs[0]), get(sn.inputs[1])
-            vals[out.onnx_name] = DT.truncate(np.matmul(a, b)).reshape(out.shape)
+            if _pow2(sn.inputs[0], sn.inputs[1], out):
+                vals[out.onnx_name] = _matmul_exp(sn, a, b).reshape(out.shape)
+            else:
+                vals[out.onnx_name] = DT.truncate(np.matmul(a, b)).reshape(out.shape)
+        elif isinstance(sn, G.ConvNode) and _pow2(*sn.inputs[:2], out):
+            vals[out.onnx_name] = _conv_exp(sn, get(sn.inputs[0]), get(sn.inputs[1]),
+                                            get(sn.inputs[2]) if sn.has_bias else None).reshape(out.shape)
+        elif isinstance(sn, G.LlmAttnConvNode):
+            pos = get(sn.inputs[2]) if not sn.static else 0
+            n = get(sn.inputs[3]) if not sn.static and sn.has_n else sn.T
+            vals[out.onnx_name] = _attn_conv(sn, get(sn.inputs[0]), get(sn.inputs[1]), np.asarray(pos).reshape(-1)[0],
+                                             np.asarray(n).reshape(-1)[0]).reshape(out.shape)
+        elif isinstance(sn, RowOpsAdapter):
+            def raw_of(t):
+                if t.kind == "f32":
+                    return np.asarray(get(t), np.float32)
+                return _raw_of(t, get(t))
+            y = run_adapter(sn, raw_of).reshape(out.shape)
+            if out.kind == "f32":
+                vals[out.onnx_name] = y.astype(np.float64)
+            else:
+                e = np.asarray(F if out.exp is None else out.exp, np.float64)
+                vals[out.onnx_name] = y.astype(np.float64) / np.power(2.0, e)
         elif isinstance(sn, G.ConvNode):
             x, w = get(sn.inputs[0]), get(sn.inputs[1])
             acc = _conv_int(x * 256, w * 256, sn.stride_h, sn.stride_w, sn.pad_top, sn.pad_left,
