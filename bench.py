@@ -94,6 +94,109 @@ def calibrate(units, torch):
                       "bytes_written": CAL_ELEMS * 2, "launches": 3}), flush=True)
 
 
+HBM_PEAK_GBS = 8000.0
+
+
+def hbm_kernels(torch, units, reps: int = 20):
+    """The HBM-bound units at shapes of the reference's configurations, each a workload of
+    tens of MB: algorithmic bytes (each tensor once; 2 B int16, 4 B int32 / float32) over the
+    mean time of ``reps`` back-to-back launches.  One JSON line per workload."""
+    import numpy as np
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    i16 = lambda n, lo=-32768, hi=32768: torch.randint(lo, hi, (n,), dtype=torch.int16, device=dev, generator=g)  # noqa: E731
+    i32 = lambda n, lo=-2 ** 30, hi=2 ** 30: torch.randint(lo, hi, (n,), dtype=torch.int32, device=dev, generator=g)  # noqa: E731
+    u8 = lambda t: t.view(torch.uint8)   # noqa: E731
+    lines = []
+
+    def run(name, shape, nbytes, fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        us = s.elapsed_time(e) / reps * 1e3
+        gbs = nbytes / (us * 1e-6) / 1e9
+        line = {"kernel": name, "shape": shape, "bytes": int(nbytes), "us": round(us, 2), "GB/s": round(gbs, 1),
+                "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        print(json.dumps(line), flush=True)
+        lines.append(line)
+
+    units.init()
+    # element-wise VectorOP: one run of the whole tensor
+    def elementwise(name, shape, op, binary, act=0):
+        n = int(np.prod(shape))
+        a, b, c = i16(n), i16(n) if binary else None, torch.empty(n, dtype=torch.int16, device=dev)
+        run(name, shape, (6 if binary else 4) * n, lambda: units.vectorop(a, b, c, n, op, act=act))
+    elementwise("vectorop_kernel RELU6 (MobileNetV2 expand output)", [32, 96, 112, 112], units.OP_RELU6, False)
+    elementwise("vectorop_kernel ADD (MobileNetV2 residual)", [32, 144, 56, 56], units.OP_ADD, True)
+    elementwise("vectorop_kernel GELU erf (BERT FFN)", [3072, 3072], units.OP_GELU, False)
+    # softmax: keys-major (BERT attention, 96 heads of 384 keys x 384 queries) and row mode
+    heads, keys, q = 96, 384, 384
+    x = i16(heads * keys * q, -2000, 2000)
+    y = torch.empty(heads * q * keys, dtype=torch.int16, device=dev)
+    def smx_cols():
+        for h in range(heads):
+            units.vectorop(x[h * keys * q:(h + 1) * keys * q], None, y[h * q * keys:(h + 1) * q * keys], keys,
+                           units.OP_SOFTMAX_T, outer=q, a_inc=q, b_inc=keys, smx_cm=12102203, smx_cfg=0x0813,
+                           smx_mask=keys)
+    run("softmax_cols_kernel (BERT, 96 heads)", [heads, keys, q], 4 * heads * keys * q, smx_cols)
+    rows = heads * q
+    run("softmax_rows_kernel (BERT row mode)", [rows, keys], 4 * rows * keys,
+        lambda: units.vectorop(x, None, y, keys, units.OP_SOFTMAX, outer=rows, a_inc=keys, b_inc=keys,
+                               smx_cm=12102203, smx_cfg=0x0813, smx_mask=keys))
+    # pooling
+    N, C, H = 32, 64, 112
+    xp, yp = i16(N * C * H * H), torch.empty(N * C * (H // 2) ** 2, dtype=torch.int16, device=dev)
+    run("pool_kernel MAX 2x2 s2", [N, C, H, H], 2 * N * C * H * H + 2 * N * C * (H // 2) ** 2,
+        lambda: units.pool(xp, yp, N, C, H, H, H // 2, H // 2, 2, 2, 2, 2))
+    N, C, H = 32, 1280, 7
+    xg, yg = i16(N * C * H * H), torch.empty(N * C, dtype=torch.int16, device=dev)
+    run("pool_global_kernel AVG (MobileNetV2 head)", [N, C, H, H], 2 * N * C * H * H + 2 * N * C,
+        lambda: units.pool(xg, yg, N, C, H, H, 1, 1, H, H, 1, 1, pool_type=units.POOL_AVG))
+    # depthwise 3x3 conv (MobileNetV2 block)
+    N, C, H = 32, 144, 56
+    xd, yd = i16(N * C * H * H, -2048, 2048), torch.empty(N * C * H * H, dtype=torch.int16, device=dev)
+    wd = i16(units.conv_weight_numel(C, C, 3, 3, True), -512, 512)
+    bd = i16(C, -512, 512)
+    run("conv_dw_kernel 3x3 s1 (MobileNetV2)", [N, C, H, H], 4 * N * C * H * H,
+        lambda: units.conv(xd, wd, bd, yd, N, C, H, H, C, H, H, 3, 3, pad_top=1, pad_left=1, has_bias=1,
+                           is_depthwise=1))
+    # row-ops jobs on contiguous rows (one broadcast parameter entry)
+    p0 = torch.zeros(16, dtype=torch.uint8, device=dev)
+    def rowjob(name, rows, n, op, ak, ck, bk=None, aux=0, nbytes=None, rope_hd=0):
+        kb = {units.K_I16: 2, units.K_I32: 4, units.K_F32: 4}
+        a = i32(rows * n) if ak == units.K_I32 else i16(rows * n, -4096, 4096)
+        b, b_s1 = None, 0
+        if rope_hd:                       # one cos / sin position row (2 HD int32) per row
+            b, b_s1 = i32(rows * 2 * rope_hd, -2 ** 23, 2 ** 23), 8 * rope_hd
+        elif bk is not None:
+            b = i32(rows * n) if bk == units.K_I32 else i16(rows * n, -4096, 4096)
+            b_s1 = kb[bk] * n
+        c = torch.empty(rows * n * kb[ck], dtype=torch.uint8, device=dev)
+        opw = op | (ak << 4) | ((bk or 0) << 6) | (ck << 8) | units.F_P_BCAST | (units.F_B_EN if bk is not None else 0)
+        run(name, [rows, n], nbytes, lambda: units.rowops(u8(a), u8(b) if b is not None else None, c, p0, opw, n,
+                                                           rows, 1, kb[ak] * n, 0, b_s1, 0, kb[ck] * n, 0, 1 << 20,
+                                                           aux, 0))
+    rowjob("ro_norm_kernel LayerNorm i32->i16 (BERT)", 3072 * 8, 768, units.RO_NORM | units.F_NORM_LN, units.K_I32,
+           units.K_I16, nbytes=6 * 3072 * 8 * 768)
+    rowjob("ro_norm_kernel RMSNorm i32->i16 (SmolLM2 rows)", 16384, 960, units.RO_NORM, units.K_I32, units.K_I16,
+           nbytes=6 * 16384 * 960)
+    rowjob("ro_stream_kernel ADDX i32+i16->i32", 3072 * 8, 768, units.RO_ADDX, units.K_I32, units.K_I32,
+           bk=units.K_I16, nbytes=10 * 3072 * 8 * 768)
+    rowjob("ro_stream_kernel MULACT (SiLU x up)", 8192, 2560, units.RO_MULACT, units.K_I16, units.K_I16,
+           bk=units.K_I16, nbytes=6 * 8192 * 2560)
+    rowjob("ro_stream_kernel DEQUANT i16->f32 (logits)", 4096, 4096, units.RO_DEQUANT, units.K_I16, units.K_F32,
+           nbytes=6 * 4096 * 4096)
+    rowjob("ro_stream_kernel ROPE (SmolLM2 q, HD 64)", 16384, 960, units.RO_ROPE, units.K_I16, units.K_I16,
+           bk=units.K_I32, aux=64, rope_hd=64, nbytes=4 * 16384 * 960 + 8 * 64 * 16384)
+    return lines
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -103,6 +206,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--hbm", action="store_true",
+                    help="measure the HBM-bound units (VectorOP, softmax, pooling, depthwise conv, "
+                         "row-ops) against the 8 TB/s roofline instead of the matmul step")
     ap.add_argument("--calibrate", action="store_true",
                     help="run only the copy used to scale HBM counters: a RELU over 256 MiB of "
                          "non-negative int16 (reads and writes exactly 256 MiB each)")
@@ -118,6 +224,9 @@ def main():
 
     if args.calibrate:
         calibrate(units, torch)
+        return
+    if args.hbm:
+        hbm_kernels(torch, units)
         return
     a, b, bp = make_inputs(args.seed)
     dev = torch.device("cuda:0")
