@@ -139,12 +139,9 @@ def hbm_kernels(torch, units, reps: int = 20):
     heads, keys, q = 96, 384, 384
     x = i16(heads * keys * q, -2000, 2000)
     y = torch.empty(heads * q * keys, dtype=torch.int16, device=dev)
-    def smx_cols():
-        for h in range(heads):
-            units.vectorop(x[h * keys * q:(h + 1) * keys * q], None, y[h * q * keys:(h + 1) * q * keys], keys,
-                           units.OP_SOFTMAX_T, outer=q, a_inc=q, b_inc=keys, smx_cm=12102203, smx_cfg=0x0813,
-                           smx_mask=keys)
-    run("softmax_cols_kernel (BERT, 96 heads)", [heads, keys, q], 4 * heads * keys * q, smx_cols)
+    run("softmax_cols_kernel (BERT, 96 heads)", [heads, keys, q], 4 * heads * keys * q,
+        lambda: units.softmax(x, y, keys, units.OP_SOFTMAX_T, q, q, keys, 12102203, 0x0813, keys, batch=heads,
+                              a_bs=keys * q, c_bs=q * keys))
     rows = heads * q
     run("softmax_rows_kernel (BERT row mode)", [rows, keys], 4 * rows * keys,
         lambda: units.vectorop(x, None, y, keys, units.OP_SOFTMAX, outer=rows, a_inc=keys, b_inc=keys,

@@ -42,6 +42,9 @@ struct DeviceState {
     bool pram_valid = false, pram_bcast = false;
     void* ws = nullptr;              // grow-only workspace
     size_t ws_size = 0;
+    int cus = 0;                     // compute units
+    size_t lds_per_cu = 0;           // LDS bytes per compute unit
+    size_t lds_per_block = 0;        // LDS bytes one workgroup may hold (dynamic attribute raised to it)
 };
 
 // The calling thread's current device, prepared (tables built) on first use.
@@ -83,5 +86,7 @@ inline size_t round_up(size_t a, size_t b) { return (a + b - 1) / b * b; }
 void build_act_tables_full(int16_t (*full)[65536]);   // [3][65536] SiLU, GELU, GELU-tanh
 void build_smx_table(int32_t* tab4096);
 void build_rowops_table_image(uint8_t* img65536);
+// Per-device set-up of the softmax kernels (their dynamic-LDS limit), with that device current.
+int prepare_softmax(DeviceState* st);
 
 }  // namespace cm

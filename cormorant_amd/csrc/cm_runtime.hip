@@ -1,4 +1,5 @@
 // cm_runtime.hip -- library runtime: error reporting, per-device tables and workspace.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -114,6 +115,21 @@ static int prepare(DeviceState* st, int dev) {
     CM_HIP_CHECK(hipMemcpy(st->smx_tab, smx, sizeof(smx), hipMemcpyHostToDevice));
     CM_HIP_CHECK(hipMemcpy(st->ro_tables, img.data(), 65536, hipMemcpyHostToDevice));
     CM_HIP_CHECK(hipMemset(st->ro_pram, 0, 4096 * 16));
+    int cus = 0, lds_cu = 0, lds_blk = 0, lds_optin = 0;
+    CM_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    CM_HIP_CHECK(hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev));
+    CM_HIP_CHECK(hipDeviceGetAttribute(&lds_blk, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
+    if (hipDeviceGetAttribute(&lds_optin, hipDeviceAttributeSharedMemPerBlockOptin, dev) != hipSuccess) {
+        lds_optin = 0;                                   // not reported: the per-block limit stands
+        (void)hipGetLastError();
+    }
+    st->cus = cus > 0 ? cus : 1;
+    st->lds_per_cu = lds_cu > 0 ? (size_t)lds_cu : 65536;
+    st->lds_per_block = std::min((size_t)std::max({lds_blk, lds_optin, 65536}), st->lds_per_cu);
+    {
+        int rc = prepare_softmax(st);
+        if (rc) return rc;
+    }
     st->device = dev;
     st->ready = true;
     return CM_OK;

@@ -82,6 +82,21 @@ def vectorop(a: torch.Tensor, b: Optional[torch.Tensor], c: torch.Tensor, size: 
 
 
 # ---------------------------------------------------------------- Matmul
+def softmax(a: torch.Tensor, c: torch.Tensor, size: int, op: int, outer: int, a_inc: int, c_inc: int,
+            smx_cm: int, smx_cfg: int, smx_mask: int, batch: int = 1, a_bs: int = 0,
+            c_bs: int = 0) -> torch.Tensor:
+    """The softmax unit over ``batch`` matrices (cm_softmax): matrix i at a + i a_bs, c + i c_bs,
+    each the VectorOP softmax call (op 10 rows, 11 keys-major)."""
+    if batch and size and outer:
+        na, _, nc = vectorop_extent(size, op, outer, a_inc, c_inc)
+        _require(a, "a", torch.int16, (batch - 1) * a_bs + na)
+        _require(c, "c", torch.int16, (batch - 1) * c_bs + nc)
+    rc = _lib.lib().cm_softmax(_ptr(a), _ptr(c), size, op, outer, a_inc, c_inc, smx_cm, smx_cfg, smx_mask,
+                               batch, a_bs, c_bs, _stream())
+    _lib.check(rc, "cm_softmax")
+    return c
+
+
 def matmul_b_extent(k: int, m: int, b_packed: int, gemv_kw: int) -> int:
     if gemv_kw:
         return k * m

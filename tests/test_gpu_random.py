@@ -241,6 +241,81 @@ def test_softmax_cols_random(U, oracle_lib, keys, queries, mask):
     np.testing.assert_array_equal(host(c), want)
 
 
+@pytest.mark.parametrize("op,size,outer,mask,batch", [
+    (11, 384, 384, 384, 5), (11, 1024, 64, 1024, 3), (11, 96, 48, 1 | (96 << 16), 4), (11, 37, 16, 37, 2),
+    (10, 384, 96, 384, 6), (10, 2048, 8, 2048, 3), (10, 2056, 5, 2056, 2), (10, 100, 33, 1 | (100 << 16), 4)])
+def test_softmax_batched(U, oracle_lib, op, size, outer, mask, batch):
+    """cm_softmax over `batch` matrices at strides = one VectorOP softmax call per matrix
+    (rows longer than 2048 take the re-reading path)."""
+    rng = np.random.default_rng(size * 7 + outer + batch)
+    s8 = (size + 7) & ~7
+    if op == 11:
+        a_inc, c_inc, na, nc = outer, s8, size * outer, (outer & ~15) * s8
+    else:
+        a_inc, c_inc, na, nc = s8, s8, outer * s8, outer * s8
+    a_bs, c_bs = na + 8, nc + 16                     # strided matrices with gaps
+    a = rint16(rng, batch * a_bs, -4000, 4000)
+    want = np.full(batch * c_bs + 8, 0x5A5A, np.int16)
+    for i in range(batch):
+        part = np.full(c_bs, 0x5A5A, np.int16)
+        oracle_lib.vectorop(a[i * a_bs:i * a_bs + na], None, c_bs, size, op, outer, a_inc, c_inc, 0, 0, 12102203,
+                            0x0C1A, mask, c=part)
+        want[i * c_bs:(i + 1) * c_bs] = part
+    c = poisoned16(batch * c_bs + 8)
+    U.softmax(dev16(a), c, size, op, outer, a_inc, c_inc, 12102203, 0x0C1A, mask, batch=batch, a_bs=a_bs, c_bs=c_bs)
+    np.testing.assert_array_equal(host(c), want)
+
+
+# (Cm, cfg): the exponential's scale Cm / 2^Cs decides where e vanishes (dlim, the least
+# max - x with (d Cm) >> Cs >= 17 * 4096) and so whether e is tabulated per d (dlim up to
+# 16383) or computed from the 4096-entry table: Cm 17410 / 17409 at Cs = 12 put dlim at
+# 16383 and 16384; Cm = 0 never decays; Cs = 46 / 47 straddle the host's shortcut for huge
+# shifts; f_p = 31 (cfg 0x1Fxx) lets e R 2^(f_p - 40) + 1/2 reach 2^31 before saturating.
+SMX_PARAMS = [(12102203, 0x0813), (0, 0x0813), (1, 0x0000), (0xFFFFFF, 0x0F00), (0xFFFFFF, 0x003F),
+              (17410, 0x0F0C), (17409, 0x0F0C), (3, 0x1F2E), (3, 0x1F2F), (12102203, 0x1F13)]
+
+
+def _smx_scores(rng, n):
+    a = rint16(rng, n)
+    a[: n // 7] = rng.choice(np.array([-32768, 32767, 0, -1], np.int16), n // 7)
+    return a
+
+
+@pytest.mark.parametrize("cm,cfg", SMX_PARAMS)
+@pytest.mark.parametrize("n", [1, 129, 384, 1000, 1025])
+def test_softmax_rows_params(U, oracle_lib, cm, cfg, n):
+    """Row mode over the exponential's parameter range and every row length form (1..8
+    words per lane of a 16-lane row, and the three-pass form past 1024), full-range scores
+    (max - x up to 65535), one row of equal scores, a causal valid count."""
+    rows, n8 = 37, (n + 7) & ~7
+    rng = np.random.default_rng(cm + cfg + n)
+    a = _smx_scores(rng, rows * n8)
+    a[:n8] = -32768
+    for mask in (n, 1 | (min(n, 40) << 16)):
+        want = np.full(rows * n8 + 8, 0x5A5A, np.int16)
+        oracle_lib.vectorop(a, None, rows * n8 + 8, n, 10, rows, n8, n8, 0, 0, cm, cfg, mask, c=want)
+        c = poisoned16(rows * n8 + 8)
+        U.vectorop(dev16(a), None, c, n, 10, rows, n8, n8, smx_cm=cm, smx_cfg=cfg, smx_mask=mask)
+        np.testing.assert_array_equal(host(c), want, err_msg=f"mask {mask:#x}")
+
+
+@pytest.mark.parametrize("cm,cfg", SMX_PARAMS)
+@pytest.mark.parametrize("keys,queries", [(37, 48), (384, 80), (1024, 64)])
+def test_softmax_cols_params(U, oracle_lib, cm, cfg, keys, queries):
+    """Column mode over the same parameters; 1024 keys with the largest tabulated e leaves
+    room in LDS for narrower query tiles only."""
+    rng = np.random.default_rng(cm + cfg + keys)
+    k8 = (keys + 7) & ~7
+    a = _smx_scores(rng, keys * queries)
+    c_len = queries * k8 + 8
+    for mask in (keys, 3 | (min(keys, 20) << 16)):
+        want = np.full(c_len, 0x5A5A, np.int16)
+        oracle_lib.vectorop(a, None, c_len, keys, 11, queries, queries, k8, 0, 0, cm, cfg, mask, c=want)
+        c = poisoned16(c_len)
+        U.vectorop(dev16(a), None, c, keys, 11, queries, queries, k8, smx_cm=cm, smx_cfg=cfg, smx_mask=mask)
+        np.testing.assert_array_equal(host(c), want, err_msg=f"mask {mask:#x}")
+
+
 POOL_CASES = [  # N, C, H, W, ph, pw, sh, sw, pt, pl, pb, pr, dh, dw, type, lp, cip
     (2, 5, 17, 19, 3, 3, 2, 2, 1, 1, 1, 1, 1, 1, 0, 2, 0),
     (1, 7, 13, 11, 3, 2, 1, 2, 1, 0, 1, 1, 2, 1, 1, 2, 0),
