@@ -95,7 +95,7 @@ __global__ __launch_bounds__(256) void vectorop_kernel(const int16_t* __restrict
             int r = act_lane(act, op_lane<OP>(x, y), alpha16, tab, act_len);
             cl[l] = (int16_t)(live ? r : 0);
         }
-        *reinterpret_cast<int4*>(c + o * (a_inc + b_inc) + base) = cv;
+        store_stream(c + o * (a_inc + b_inc) + base, cv);
     }
 }
 
@@ -177,29 +177,42 @@ __host__ __device__ constexpr uint32_t smx_tab_words(bool etab, uint32_t dlim) {
     return etab ? ((dlim + 1 + 3) & ~3u) : 4096u;
 }
 
-// Fills the workgroup's table: e(d) for d <= dlim (ETAB), else a copy of TAB.
-template <bool ETAB>
-__device__ __forceinline__ void smx_stage(uint32_t* tab, const int32_t* __restrict__ gtab, const SmxRegs& r) {
-    const uint32_t nt = blockDim.x;
-    if constexpr (ETAB) {
-        for (uint32_t d0 = threadIdx.x; d0 <= r.dlim; d0 += 4 * nt) {
-            uint32_t v[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {                 // four gathers in flight per thread
-                const uint32_t d = d0 + u * nt;
-                const uint32_t y = (uint32_t)(((uint64_t)(d & 0x1FFFFu) * r.cm) >> r.cs);
-                v[u] = (uint32_t)gtab[y & 4095] >> ((y >> 12) & 31);   // d < dlim: y < 17 * 4096
-            }
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const uint32_t d = d0 + u * nt;
-                if (d <= r.dlim) tab[d] = d < r.dlim ? v[u] : 0u;
-            }
-        }
-    } else {
-        for (uint32_t i = threadIdx.x; i < 1024; i += nt)
-            reinterpret_cast<int4*>(tab)[i] = reinterpret_cast<const int4*>(gtab)[i];
+// e(d) for d < dlim of one (Cm, Cs), zero from dlim to the table's end (`words` entries):
+// the per-(Cm, Cs) table the kernels stage, built once on the device.
+__global__ void smx_etab_kernel(uint32_t* __restrict__ out, uint32_t words, const int32_t* __restrict__ gtab,
+                                SmxRegs r) {
+    for (uint32_t d = blockIdx.x * blockDim.x + threadIdx.x; d < words; d += gridDim.x * blockDim.x) {
+        const uint32_t y = (uint32_t)(((uint64_t)d * r.cm) >> r.cs);
+        out[d] = d < r.dlim ? (uint32_t)gtab[y & 4095] >> ((y >> 12) & 31) : 0u;   // d < dlim: y < 17 * 4096
     }
+}
+
+// A workgroup's exponential table is n4 16-byte words at tsrc (the e(d) table or TAB).  Its
+// loads issue first, up to kStageWords per lane into registers, so that they return ahead
+// of the loads the kernel issues next; smx_stage_store then writes them to LDS.
+constexpr int kStageWords = 4;
+
+struct SmxStage {
+    int4 v[kStageWords];
+};
+
+__device__ __forceinline__ void smx_stage_load(SmxStage& st, const int4* __restrict__ tsrc, uint32_t n4) {
+#pragma unroll
+    for (int j = 0; j < kStageWords; j++) {
+        const uint32_t i = threadIdx.x + j * blockDim.x;
+        st.v[j] = i < n4 ? tsrc[i] : make_int4(0, 0, 0, 0);
+    }
+}
+
+__device__ __forceinline__ void smx_stage_store(const SmxStage& st, uint32_t* tab, const int4* __restrict__ tsrc,
+                                                uint32_t n4) {
+    int4* t4 = reinterpret_cast<int4*>(tab);
+#pragma unroll
+    for (int j = 0; j < kStageWords; j++) {
+        const uint32_t i = threadIdx.x + j * blockDim.x;
+        if (i < n4) t4[i] = st.v[j];
+    }
+    for (uint32_t i = threadIdx.x + kStageWords * blockDim.x; i < n4; i += blockDim.x) t4[i] = tsrc[i];
 }
 
 // e(d), d <= 65536 (kSmxDead gives 0).
@@ -283,9 +296,8 @@ __device__ __forceinline__ void smx_store(const uint32_t (&e)[KW][8], double rs,
     for (int k = 0; k < KW; k++) {
         const uint32_t w = l16 + 16 * k;
         if (w < words)
-            *reinterpret_cast<int4*>(out + 8 * w) =
-                make_int4(smx_p2<CLAMP>(e[k][0], e[k][1], rs), smx_p2<CLAMP>(e[k][2], e[k][3], rs),
-                          smx_p2<CLAMP>(e[k][4], e[k][5], rs), smx_p2<CLAMP>(e[k][6], e[k][7], rs));
+            store_stream(out + 8 * w, make_int4(smx_p2<CLAMP>(e[k][0], e[k][1], rs), smx_p2<CLAMP>(e[k][2], e[k][3], rs),
+                                                smx_p2<CLAMP>(e[k][4], e[k][5], rs), smx_p2<CLAMP>(e[k][6], e[k][7], rs)));
     }
 }
 
@@ -328,33 +340,42 @@ __device__ __forceinline__ void smx_row16(const int4 (&xv)[KW], uint32_t words, 
 
 // Row mode over `total` rows (row g of matrix g / rows, at a + (g / rows) a_bs + (g mod
 // rows) a_inc, its index for the valid count row0 + g mod rows).  Workgroups stay resident
-// and take groups of 16 lanes' rows in turn, so the table is built once per workgroup;
-// 1024 lanes per workgroup keep that build small beside the rows.  A group steps by the
-// grid's row slots with the matrix / row split and both offsets carried, not divided.
+// and take groups of 16 lanes' rows in turn, so the table is staged once per workgroup, its
+// loads ahead of the first rows'.  A group steps by the grid's row slots with the matrix /
+// row split and both offsets carried, not divided.
 template <int KW, bool ETAB>
 __global__ __launch_bounds__(1024, KW <= 3 ? 8 : 4) void softmax_rows_kernel(
     const int16_t* __restrict__ a, int16_t* __restrict__ c, uint32_t n, uint32_t rows, uint32_t total, uint32_t row0,
-    uint64_t a_inc, uint64_t c_inc, uint64_t a_bs, uint64_t c_bs, SmxRegs r, const int32_t* __restrict__ gtab) {
+    uint64_t a_inc, uint64_t c_inc, uint64_t a_bs, uint64_t c_bs, SmxRegs r, const int4* __restrict__ tsrc,
+    uint32_t tab_n4) {
     extern __shared__ __attribute__((aligned(16))) uint32_t smx_lds[];
-    smx_stage<ETAB>(smx_lds, gtab, r);
-    __syncthreads();
+    SmxStage stg;
+    smx_stage_load(stg, tsrc, tab_n4);
     const uint32_t l16 = threadIdx.x & 15, words = (n + 7) >> 3;
     const uint32_t per_wg = blockDim.x >> 4, slots = gridDim.x * per_wg;
     uint32_t g = blockIdx.x * per_wg + (threadIdx.x >> 4);
-    if (g >= total) return;                              // no barrier follows
     const uint32_t sdiv = slots / rows, smod = slots - sdiv * rows;
     const uint32_t bt = g / rows;
     uint32_t row = g - bt * rows;
     uint64_t oa = bt * a_bs + row * a_inc, oc = bt * c_bs + row * c_inc;
     const uint64_t da = sdiv * a_bs + smod * a_inc, dc = sdiv * c_bs + smod * c_inc;
     const uint64_t wa = a_bs - rows * a_inc, wc = c_bs - rows * c_inc;   // the step into the next matrix (mod 2^64)
-    for (; g < total; g += slots) {
-        int4 xv[KW];
+    int4 xv[KW];
+    auto load_row = [&]() {
 #pragma unroll
         for (int k = 0; k < KW; k++) {
             const uint32_t w = l16 + 16 * k;
             xv[k] = w < words ? *reinterpret_cast<const int4*>(a + oa + 8 * w) : make_int4(0, 0, 0, 0);
         }
+    };
+    // the first rows' loads follow the table's (rows of up to 3 words a lane: longer rows
+    // would hold too many registers across the staging)
+    constexpr bool kEarly = KW <= 3;
+    if (kEarly && g < total) load_row();
+    smx_stage_store(stg, smx_lds, tsrc, tab_n4);
+    __syncthreads();
+    for (bool first = kEarly; g < total; g += slots, first = false) {
+        if (!first) load_row();
         smx_row16<KW, ETAB>(xv, words, smx_valid(row0 + row, n, r), r, smx_lds, c + oc, l16);
         row += smod;
         oa += da;
@@ -374,9 +395,11 @@ __global__ __launch_bounds__(1024) void softmax_long_kernel(const int16_t* __res
                                                             int16_t* __restrict__ c, uint32_t n, uint32_t rows,
                                                             uint32_t total, uint32_t row0, uint64_t a_inc,
                                                             uint64_t c_inc, uint64_t a_bs, uint64_t c_bs, SmxRegs r,
-                                                            const int32_t* __restrict__ gtab) {
+                                                            const int4* __restrict__ tsrc, uint32_t tab_n4) {
     extern __shared__ __attribute__((aligned(16))) uint32_t smx_lds[];
-    smx_stage<ETAB>(smx_lds, gtab, r);
+    SmxStage stg;
+    smx_stage_load(stg, tsrc, tab_n4);
+    smx_stage_store(stg, smx_lds, tsrc, tab_n4);
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63, words = (n + 7) >> 3;
     const uint32_t slots = gridDim.x * (blockDim.x >> 6);
@@ -409,7 +432,7 @@ __global__ __launch_bounds__(1024) void softmax_long_kernel(const int16_t* __res
 #pragma unroll
             for (int l = 0; l < 8; l++)
                 e[l] = smx_e<ETAB>(8 * w + l < v ? (uint32_t)(m - (int)xl[l]) : kSmxDead, r, smx_lds);
-            *reinterpret_cast<int4*>(p + 8 * w) = smx_pack(e, rs);
+            store_stream(p + 8 * w, smx_pack(e, rs));
         }
     }
 }
@@ -431,7 +454,7 @@ __global__ __launch_bounds__(1024, KW <= 3 ? 8 : 4) void softmax_cols_kernel(con
                                                             uint32_t qt, uint32_t tiles_q, uint32_t tiles,
                                                             uint64_t a_inc, uint64_t c_inc, uint64_t a_bs,
                                                             uint64_t c_bs, SmxRegs r,
-                                                            const int32_t* __restrict__ gtab) {
+                                                            const int4* __restrict__ tsrc, uint32_t tab_n4) {
     extern __shared__ __attribute__((aligned(16))) uint32_t smx_lds[];
     const uint32_t per_xcd = (tiles + 7) >> 3;
     const uint32_t tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
@@ -439,19 +462,30 @@ __global__ __launch_bounds__(1024, KW <= 3 ? 8 : 4) void softmax_cols_kernel(con
     const uint32_t h = tile / tiles_q, q0 = (tile - h * tiles_q) * qt;
     const uint32_t t = threadIdx.x, nt = blockDim.x;
     const uint32_t pitch = cols_pitch(n), words = (n + 7) >> 3;
-    int16_t* blk = reinterpret_cast<int16_t*>(smx_lds + smx_tab_words(ETAB, r.dlim));   // [qt][pitch]
+    int16_t* blk = reinterpret_cast<int16_t*>(smx_lds + tab_n4 * 4);   // [qt][pitch]
     const int16_t* sh = s + h * a_bs;
-    smx_stage<ETAB>(smx_lds, gtab, r);
+    SmxStage stg;
+    smx_stage_load(stg, tsrc, tab_n4);
     if ((a_inc & 7) == 0) {
-        // 8 queries (16 bytes) of key row j per thread, written transposed: blk[q][j]
-        const uint32_t chunks = qt >> 3;
-        for (uint32_t i = t; i < n * chunks; i += nt) {
-            const uint32_t j = i / chunks, ch = i - j * chunks;
-            const uint32_t q = q0 + 8 * ch;
-            const int4 v = q < nq ? *reinterpret_cast<const int4*>(sh + j * a_inc + q) : make_int4(0, 0, 0, 0);
-            const int16_t* vl = reinterpret_cast<const int16_t*>(&v);
+        // 8 queries (16 bytes) of key row j per lane, written transposed: blk[q][j].  The
+        // qt / 8 chunks of a key row go to consecutive lanes and a workgroup (16 qt lanes)
+        // covers 128 key rows a step, so n <= 1024 keys take at most 8 loads per lane, all
+        // issued before the first write.
+        const uint32_t chunks = qt >> 3, ch = t % chunks, j0 = t / chunks, q = q0 + 8 * ch;
+        int4 bv[8];
 #pragma unroll
-            for (int l = 0; l < 8; l++) blk[(8 * ch + l) * pitch + j] = vl[l];
+        for (int u = 0; u < 8; u++) {
+            const uint32_t j = j0 + 128 * u;
+            bv[u] = (j < n && q < nq) ? *reinterpret_cast<const int4*>(sh + j * a_inc + q) : make_int4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t j = j0 + 128 * u;
+            const int16_t* vl = reinterpret_cast<const int16_t*>(&bv[u]);
+            if (j < n) {
+#pragma unroll
+                for (int l = 0; l < 8; l++) blk[(8 * ch + l) * pitch + j] = vl[l];
+            }
         }
     } else {
         for (uint32_t i = t; i < n * qt; i += nt) {
@@ -462,6 +496,7 @@ __global__ __launch_bounds__(1024, KW <= 3 ? 8 : 4) void softmax_cols_kernel(con
     // keys n .. pitch of every row are zero (their P lanes are written as 0)
     const uint32_t pad = pitch - n;
     for (uint32_t i = t; i < qt * pad; i += nt) blk[(i / pad) * pitch + n + i % pad] = 0;
+    smx_stage_store(stg, smx_lds, tsrc, tab_n4);
     __syncthreads();
     const uint32_t l16 = t & 15;
     for (uint32_t qq = t >> 4; qq < qt; qq += nt >> 4) {
@@ -497,9 +532,48 @@ int blocks_per_cu(const void* kernel, int block, size_t lds) {
 }
 
 using SmxRowsFn = void (*)(const int16_t*, int16_t*, uint32_t, uint32_t, uint32_t, uint32_t, uint64_t, uint64_t,
-                           uint64_t, uint64_t, SmxRegs, const int32_t*);
+                           uint64_t, uint64_t, SmxRegs, const int4*, uint32_t);
 using SmxColsFn = void (*)(const int16_t*, int16_t*, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, uint64_t,
-                           uint64_t, uint64_t, uint64_t, SmxRegs, const int32_t*);
+                           uint64_t, uint64_t, uint64_t, SmxRegs, const int4*, uint32_t);
+
+// The workgroups' table: e(d) for this (Cm, Cs) from the device's cache, built on `s` by the
+// first call that needs it (later calls on other streams wait for that build until it is
+// seen complete); nullptr when the cache is full (the caller then stages TAB).
+constexpr size_t kEtabCacheEntries = 1024;
+
+int smx_etab(DeviceState* st, const SmxRegs& r, hipStream_t s, const uint32_t** out) {
+    std::lock_guard<std::mutex> lk(st->smx_mu);
+    *out = nullptr;
+    for (SmxEtab& e : st->smx_etabs) {
+        if (e.cm != r.cm || e.cs != r.cs) continue;
+        if (!e.done) {
+            const hipError_t q = hipEventQuery(e.ready);
+            if (q == hipSuccess) {
+                e.done = true;
+            } else if (q == hipErrorNotReady) {
+                (void)hipGetLastError();
+                CM_HIP_CHECK(hipStreamWaitEvent(s, e.ready, 0));
+            } else {
+                return hip_fail(q, "hipEventQuery (softmax table)");
+            }
+        }
+        *out = e.table;
+        return CM_OK;
+    }
+    if (st->smx_etabs.size() >= kEtabCacheEntries) return CM_OK;
+    SmxEtab e;
+    e.cm = r.cm;
+    e.cs = r.cs;
+    const uint32_t words = smx_tab_words(true, r.dlim);
+    CM_HIP_CHECK(hipMalloc(&e.table, (size_t)words * 4));
+    CM_HIP_CHECK(hipEventCreateWithFlags(&e.ready, hipEventDisableTiming));
+    CM_LAUNCH("smx_etab_kernel", smx_etab_kernel, dim3(ceil_div(words, 256)), dim3(256), 0, s, e.table, words,
+              st->smx_tab, r);
+    CM_HIP_CHECK(hipEventRecord(e.ready, s));
+    st->smx_etabs.push_back(e);
+    *out = e.table;
+    return CM_OK;
+}
 
 template <bool ETAB>
 SmxRowsFn rows_kernel(uint32_t kw) {
@@ -528,9 +602,10 @@ SmxColsFn cols_kernel(uint32_t kw) {
 
 template <bool ETAB>
 int launch_rows(const int16_t* a, int16_t* c, uint32_t n, uint32_t rows, uint32_t total, uint32_t row0,
-                uint64_t a_inc, uint64_t c_inc, uint64_t a_bs, uint64_t c_bs, const SmxRegs& r,
+                uint64_t a_inc, uint64_t c_inc, uint64_t a_bs, uint64_t c_bs, const SmxRegs& r, const int4* tsrc,
                 const DeviceState* st, hipStream_t s) {
-    const size_t lds = (size_t)smx_tab_words(ETAB, r.dlim) * 4;
+    const uint32_t tab_n4 = smx_tab_words(ETAB, r.dlim) / 4;
+    const size_t lds = (size_t)tab_n4 * 16;
     const uint32_t kw = smx_kw((n + 7) >> 3);
     const SmxRowsFn k = rows_kernel<ETAB>(kw);
     const uint32_t per_wg = kw ? 64 : 16;                              // rows per workgroup pass
@@ -538,21 +613,22 @@ int launch_rows(const int16_t* a, int16_t* c, uint32_t n, uint32_t rows, uint32_
     const unsigned blocks = (unsigned)std::min<uint64_t>(ceil_div(total, per_wg), resident);
     if (kw) {
         CM_LAUNCH("softmax_rows_kernel", k, dim3(blocks), dim3(1024), lds, s, a, c, n, rows, total, row0, a_inc, c_inc,
-                  a_bs, c_bs, r, st->smx_tab);
+                  a_bs, c_bs, r, tsrc, tab_n4);
     } else {
         CM_LAUNCH("softmax_long_kernel", k, dim3(blocks), dim3(1024), lds, s, a, c, n, rows, total, row0, a_inc, c_inc,
-                  a_bs, c_bs, r, st->smx_tab);
+                  a_bs, c_bs, r, tsrc, tab_n4);
     }
     return CM_OK;
 }
 
 template <bool ETAB>
 int launch_cols(const int16_t* a, int16_t* c, uint32_t n, uint32_t nq, uint32_t batch, uint64_t a_inc,
-                uint64_t c_inc, uint64_t a_bs, uint64_t c_bs, const SmxRegs& r, const DeviceState* st,
-                hipStream_t s) {
+                uint64_t c_inc, uint64_t a_bs, uint64_t c_bs, const SmxRegs& r, const int4* tsrc,
+                const DeviceState* st, hipStream_t s) {
     // queries per tile: the fewest rounds of resident workgroups times the tile height, ties
     // to the wider tile (longer contiguous key-row reads)
-    const size_t tab = (size_t)smx_tab_words(ETAB, r.dlim) * 4;
+    const uint32_t tab_n4 = smx_tab_words(ETAB, r.dlim) / 4;
+    const size_t tab = (size_t)tab_n4 * 16;
     const SmxColsFn k = cols_kernel<ETAB>(smx_kw((n + 7) >> 3));
     uint32_t qt = 0;
     uint64_t best = ~0ull;
@@ -575,7 +651,7 @@ int launch_cols(const int16_t* a, int16_t* c, uint32_t n, uint32_t nq, uint32_t 
     const size_t lds = tab + (size_t)qt * cols_pitch(n) * sizeof(int16_t);
     if (lds > st->lds_per_block) return fail(CM_EINVAL, "softmax columns: %u keys do not fit the LDS", n);
     CM_LAUNCH("softmax_cols_kernel", k, dim3(grid), dim3(16 * qt), lds, s, a, c, n, nq, qt, tiles_q,
-              (uint32_t)tiles, a_inc, c_inc, a_bs, c_bs, r, st->smx_tab);
+              (uint32_t)tiles, a_inc, c_inc, a_bs, c_bs, r, tsrc, tab_n4);
     return CM_OK;
 }
 
@@ -586,12 +662,21 @@ int launch_softmax(const int16_t* a, int16_t* c, uint32_t size, uint32_t op, uin
                    uint64_t a_bs, uint64_t c_bs, DeviceState* st, hipStream_t s) {
     SmxRegs r{smx_cm & 0xFFFFFFu, smx_cfg & 63u, (smx_cfg >> 8) & 31u, smx_mask & 0xFFFFu, smx_mask >> 16, 0};
     r.dlim = smx_dlim(r.cm, r.cs);
-    const bool etab = r.dlim <= kEtabMax;
     if (size > 65535) return fail(CM_EINVAL, "softmax: %u elements per vector", size);
     if (c_inc & 7) return fail(CM_EALIGN, "softmax: output stride %u not a multiple of 8", c_inc);
     if (!aligned16(a) || !aligned16(c)) return fail(CM_EALIGN, "softmax: a and c must be 16-byte aligned");
     if (batch > 1 && ((a_bs & 7) || (c_bs & 7)))
         return fail(CM_EALIGN, "softmax: batch strides must be multiples of 8 elements");
+    if (op == OP_SOFTMAX_T && (outer & ~15u) == 0) return CM_OK;
+    if (op == OP_SOFTMAX_T && size > kColsMaxKeys)
+        return fail(CM_EINVAL, "softmax columns: %u keys above %u", size, kColsMaxKeys);
+    const uint32_t* etab_src = nullptr;
+    if (r.dlim <= kEtabMax) {
+        const int rc = smx_etab(st, r, s, &etab_src);
+        if (rc) return rc;
+    }
+    const bool etab = etab_src != nullptr;
+    const int4* tsrc = reinterpret_cast<const int4*>(etab ? etab_src : reinterpret_cast<const uint32_t*>(st->smx_tab));
     if (op == OP_SOFTMAX) {
         if (a_inc & 7) return fail(CM_EALIGN, "softmax rows: input stride %u not a multiple of 8", a_inc);
         // launches of at most 2^30 rows: whole matrices, or row ranges of one matrix
@@ -604,9 +689,9 @@ int launch_softmax(const int16_t* a, int16_t* c, uint32_t size, uint32_t op, uin
                 int16_t* cb = c + b0 * c_bs + r0 * c_inc;
                 const uint32_t total = (uint32_t)(nr * nb);
                 const int rc = etab ? launch_rows<true>(ab, cb, size, nr, total, (uint32_t)r0, a_inc, c_inc, a_bs,
-                                                        c_bs, r, st, s)
+                                                        c_bs, r, tsrc, st, s)
                                     : launch_rows<false>(ab, cb, size, nr, total, (uint32_t)r0, a_inc, c_inc, a_bs,
-                                                         c_bs, r, st, s);
+                                                         c_bs, r, tsrc, st, s);
                 if (rc) return rc;
             }
             b0 += nb;
@@ -614,10 +699,8 @@ int launch_softmax(const int16_t* a, int16_t* c, uint32_t size, uint32_t op, uin
         return CM_OK;
     }
     const uint32_t nq = outer & ~15u;
-    if (nq == 0) return CM_OK;
-    if (size > kColsMaxKeys) return fail(CM_EINVAL, "softmax columns: %u keys above %u", size, kColsMaxKeys);
-    return etab ? launch_cols<true>(a, c, size, nq, batch, a_inc, c_inc, a_bs, c_bs, r, st, s)
-                : launch_cols<false>(a, c, size, nq, batch, a_inc, c_inc, a_bs, c_bs, r, st, s);
+    return etab ? launch_cols<true>(a, c, size, nq, batch, a_inc, c_inc, a_bs, c_bs, r, tsrc, st, s)
+                : launch_cols<false>(a, c, size, nq, batch, a_inc, c_inc, a_bs, c_bs, r, tsrc, st, s);
 }
 
 template <uint32_t OP>
