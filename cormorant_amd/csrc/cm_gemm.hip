@@ -664,6 +664,209 @@ __global__ __launch_bounds__(256) void conv_dw_kernel(const int16_t* __restrict_
     }
 }
 
+// Depthwise 3x3, dilation 1, stride SH x SW (the MobileNet blocks): each lane computes R
+// output rows of one column (a vertical strip) from the (R - 1) SH + 3 input rows' three
+// taps held in registers.  Lanes of a wavefront sit on neighbouring columns, so each load
+// is one contiguous run of an input row and the L1 serves the overlap between neighbours.
+// Sums are int32 where they are exact: the wrap path, or a channel whose bound
+// sum |w| 2^15 + |bias| 2^8 stays below 2^31; int64 otherwise.
+template <int SH, int SW, int R>
+__global__ __launch_bounds__(256) void conv_dw3_kernel(const int16_t* __restrict__ x, const int16_t* __restrict__ w,
+                                                       const int16_t* __restrict__ bias, int16_t* __restrict__ y,
+                                                       uint32_t items, uint32_t strips, uint32_t ch, uint32_t in_h,
+                                                       uint32_t in_w, uint32_t out_h, uint32_t out_w, uint32_t pt,
+                                                       uint32_t pl, uint32_t dws, uint32_t cs, uint32_t cn,
+                                                       uint32_t gs, uint32_t wrap) {
+    constexpr int NR = (R - 1) * SH + 3;
+    const uint32_t per_plane = strips * out_w;
+    for (uint32_t it = blockIdx.x * blockDim.x + threadIdx.x; it < items; it += gridDim.x * blockDim.x) {
+        const uint32_t p = it / per_plane, rem = it - p * per_plane;
+        const uint32_t sidx = rem / out_w, ow = rem - sidx * out_w;
+        const uint32_t nb = p / ch, c = p - nb * ch;
+        const int16_t* xp = x + (uint64_t)p * in_h * in_w;
+        const int16_t* wp = w + (uint64_t)c * dws;
+        int wv[9];
+        uint32_t wabs = 0;
+#pragma unroll
+        for (int i = 0; i < 9; i++) {
+            wv[i] = wp[i];
+            wabs += (uint32_t)(wv[i] < 0 ? -wv[i] : wv[i]);
+        }
+        const int b0 = bias ? (int)bias[c] : 0;
+        const int oh0 = (int)(sidx * R);
+        const int ih0 = oh0 * SH - (int)pt, iw0 = (int)(ow * SW) - (int)pl;
+        bool cv[3];
+#pragma unroll
+        for (int b = 0; b < 3; b++) cv[b] = (uint32_t)(iw0 + b) < in_w;
+        int v[NR][3];
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            const int ih = ih0 + r;
+            const bool rv = (uint32_t)ih < in_h;
+            const int16_t* xr = xp + (int64_t)ih * in_w + iw0;
+#pragma unroll
+            for (int b = 0; b < 3; b++) v[r][b] = (rv && cv[b]) ? (int)xr[b] : 0;
+        }
+        const uint64_t bound = (uint64_t)wabs * 32768u + (uint64_t)(b0 < 0 ? -b0 : b0) * 256u;
+        int out[R];
+        if (wrap || bound < ((uint64_t)1 << 31)) {
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                uint32_t acc = (uint32_t)b0 << 8;
+#pragma unroll
+                for (int a = 0; a < 3; a++)
+#pragma unroll
+                    for (int b = 0; b < 3; b++) acc += (uint32_t)(v[i * SH + a][b] * wv[a * 3 + b]);
+                const int q = (int)acc >> 8;
+                out[i] = q > 32767 ? 32767 : (q < -32768 ? -32768 : q);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                long long acc = (long long)b0 * 256;
+#pragma unroll
+                for (int a = 0; a < 3; a++)
+#pragma unroll
+                    for (int b = 0; b < 3; b++) acc += (long long)v[i * SH + a][b] * wv[a * 3 + b];
+                const long long q = acc >> 8;
+                out[i] = (int)(q > 32767 ? 32767 : (q < -32768 ? -32768 : q));
+            }
+        }
+        const uint64_t plane = (uint64_t)out_h * out_w;
+        const uint64_t base = cn ? (uint64_t)(c % cn) * cs + (uint64_t)(c / cn) * gs : (uint64_t)c * cs;
+        int16_t* yp = y + (uint64_t)nb * ch * plane + base + ow;
+#pragma unroll
+        for (int i = 0; i < R; i++)
+            if ((uint32_t)(oh0 + i) < out_h) yp[(uint64_t)(oh0 + i) * out_w] = (int16_t)out[i];
+    }
+}
+
+// Depthwise 3x3 stride 1 on rows of a multiple of 8 columns: a lane computes 8 columns x R
+// rows.  Per input row it loads the 16-byte word of its 8 columns and the dwords either side
+// (columns 8j - 2 .. 8j + 9, zero past the row), and every output takes its row's three
+// taps as two v_dot2_i32_i16 against packed weight pairs, so no 16-bit value is unpacked.
+// PL (the left pad, 0..2) fixes which pairs line up.  Exact int32 sums as in
+// conv_dw3_kernel; a channel whose bound leaves int32 takes int64 per value.
+typedef short cm_s16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ int dot2(uint32_t x, uint32_t w, int acc) {
+    return __builtin_amdgcn_sdot2(__builtin_bit_cast(cm_s16x2, x), __builtin_bit_cast(cm_s16x2, w), acc, false);
+}
+
+__device__ __forceinline__ uint32_t pack16(int lo, int hi) { return (uint32_t)(uint16_t)lo | ((uint32_t)hi << 16); }
+
+template <int PL, int R>
+__global__ __launch_bounds__(256) void conv_dw3v_kernel(const int16_t* __restrict__ x, const int16_t* __restrict__ w,
+                                                        const int16_t* __restrict__ bias, int16_t* __restrict__ y,
+                                                        uint32_t items, uint32_t strips, uint32_t groups, uint32_t ch,
+                                                        uint32_t in_h, uint32_t in_w, uint32_t out_h, uint32_t out_w,
+                                                        uint32_t pt, uint32_t dws, uint32_t cs, uint32_t cn,
+                                                        uint32_t gs, uint32_t wrap) {
+    const uint32_t per_plane = strips * groups;
+    for (uint32_t it = blockIdx.x * blockDim.x + threadIdx.x; it < items; it += gridDim.x * blockDim.x) {
+        const uint32_t p = it / per_plane, rem = it - p * per_plane;
+        const uint32_t sidx = rem / groups, j = rem - sidx * groups;
+        const uint32_t nb = p / ch, c = p - nb * ch;
+        const int16_t* xp = x + (uint64_t)p * in_h * in_w;
+        const int16_t* wp = w + (uint64_t)c * dws;
+        int wv[9];
+        uint32_t wabs = 0;
+#pragma unroll
+        for (int i = 0; i < 9; i++) {
+            wv[i] = wp[i];
+            wabs += (uint32_t)(wv[i] < 0 ? -wv[i] : wv[i]);
+        }
+        const int b0 = bias ? (int)bias[c] : 0;
+        const uint64_t bound = (uint64_t)wabs * 32768u + (uint64_t)(b0 < 0 ? -b0 : b0) * 256u;
+        const bool exact32 = wrap || bound < ((uint64_t)1 << 31);
+        const int oh0 = (int)(sidx * R);
+        const uint32_t c0 = 8 * j;                                   // first output column
+        const uint64_t plane = (uint64_t)out_h * out_w;
+        const uint64_t base = cn ? (uint64_t)(c % cn) * cs + (uint64_t)(c / cn) * gs : (uint64_t)c * cs;
+        int16_t* yp = y + (uint64_t)nb * ch * plane + base + c0;
+        if (!exact32) {
+            // int64 per value (weights too large for an int32 bound): each tap loaded alone
+            for (int i = 0; i < R && (uint32_t)(oh0 + i) < out_h; i++) {
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    long long a64 = (long long)b0 * 256;
+                    for (int a = 0; a < 3; a++) {
+                        const int ih = oh0 + i - (int)pt + a;
+                        if ((uint32_t)ih >= in_h) continue;
+                        for (int b = 0; b < 3; b++) {
+                            const int iw = (int)c0 + t - PL + b;
+                            if ((uint32_t)iw < in_w) a64 += (long long)xp[(uint64_t)ih * in_w + iw] * wv[3 * a + b];
+                        }
+                    }
+                    const long long v = a64 >> 8;
+                    yp[(uint64_t)(oh0 + i) * out_w + t] = (int16_t)(v > 32767 ? 32767 : (v < -32768 ? -32768 : v));
+                }
+            }
+            continue;
+        }
+        // weight pairs per kernel row: (w0, w1), (w2, 0) for an even first tap; (0, w0), (w1, w2) odd
+        uint32_t wA[3], wB[3], wC[3], wD[3];
+#pragma unroll
+        for (int a = 0; a < 3; a++) {
+            wA[a] = pack16(wv[3 * a], wv[3 * a + 1]);
+            wB[a] = pack16(wv[3 * a + 2], 0);
+            wC[a] = pack16(0, wv[3 * a]);
+            wD[a] = pack16(wv[3 * a + 1], wv[3 * a + 2]);
+        }
+        int acc[R][8];
+#pragma unroll
+        for (int i = 0; i < R; i++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) acc[i][t] = b0 * 256;
+#pragma unroll
+        for (int r = 0; r < R + 2; r++) {
+            const int ih = oh0 - (int)pt + r;
+            uint32_t W[6] = {0, 0, 0, 0, 0, 0};                      // columns c0 - 2 .. c0 + 9
+            if ((uint32_t)ih < in_h) {
+                const int16_t* xr = xp + (uint64_t)ih * in_w + c0;
+                if (c0 + 8 <= in_w) {
+                    const int4 mid = *reinterpret_cast<const int4*>(xr);
+                    W[1] = (uint32_t)mid.x;
+                    W[2] = (uint32_t)mid.y;
+                    W[3] = (uint32_t)mid.z;
+                    W[4] = (uint32_t)mid.w;
+                }
+                if (c0 >= 2) W[0] = *reinterpret_cast<const uint32_t*>(xr - 2);
+                if (c0 + 10 <= in_w) W[5] = *reinterpret_cast<const uint32_t*>(xr + 8);
+            }
+#pragma unroll
+            for (int a = 0; a < 3; a++) {
+                const int i = r - a;                                   // the output row fed at tap row a
+                if (i < 0 || i >= R) continue;
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    const int q0 = t - PL + 2;                         // window index of tap b = 0
+                    if ((q0 & 1) == 0) {
+                        acc[i][t] = dot2(W[q0 >> 1], wA[a], acc[i][t]);
+                        acc[i][t] = dot2(W[(q0 >> 1) + 1], wB[a], acc[i][t]);
+                    } else {
+                        acc[i][t] = dot2(W[q0 >> 1], wC[a], acc[i][t]);
+                        acc[i][t] = dot2(W[(q0 >> 1) + 1], wD[a], acc[i][t]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            if ((uint32_t)(oh0 + i) >= out_h) break;
+            int q[8];
+#pragma unroll
+            for (int t = 0; t < 8; t++) q[t] = acc[i][t] >> 8;
+            int4 o;
+            o.x = __builtin_bit_cast(int, __builtin_amdgcn_cvt_pk_i16(q[0], q[1]));
+            o.y = __builtin_bit_cast(int, __builtin_amdgcn_cvt_pk_i16(q[2], q[3]));
+            o.z = __builtin_bit_cast(int, __builtin_amdgcn_cvt_pk_i16(q[4], q[5]));
+            o.w = __builtin_bit_cast(int, __builtin_amdgcn_cvt_pk_i16(q[6], q[7]));
+            store_stream(yp + (uint64_t)(oh0 + i) * out_w, o);
+        }
+    }
+}
+
 // ---------------------------------------------------------------- drivers
 // Byte planes [slices][lines_p][kp] of one operand and its partial line sums
 // [slices][nslab][lines_p].
@@ -796,6 +999,43 @@ extern "C" int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, 
     const uint32_t plane = out_h * out_w;
     const uint32_t cs = y_cs ? y_cs : plane;
     const int16_t* bptr = has_bias ? bias : nullptr;
+    const bool dw3 = is_depthwise && kh == 3 && kw == 3 && dilation_h == 1 && dilation_w == 1;
+    if (dw3 && stride_h == 1 && stride_w == 1 && pad_left <= 2 && (in_w & 7) == 0 && (out_w & 7) == 0 &&
+        aligned16(x) && aligned16(y) && (cs & 7) == 0 && (!y_cn || (y_gs & 7) == 0)) {
+        constexpr uint32_t R = 4;
+        const uint32_t strips = (out_h + R - 1) / R, groups = out_w / 8;
+        const uint64_t items = (uint64_t)batch * out_ch * strips * groups;
+        if (items < ((uint64_t)1 << 31)) {
+            const unsigned blocks = (unsigned)std::min<uint64_t>((items + 255) / 256, 65536ull * 8);
+#define CM_DW3V(PL)                                                                                              \
+    CM_LAUNCH("conv_dw3v_kernel", (conv_dw3v_kernel<PL, R>), dim3(blocks), dim3(256), 0, s, x, w, bptr, y,       \
+              (uint32_t)items, strips, groups, out_ch, in_h, in_w, out_h, out_w, pad_top, 16u, cs, y_cn, y_gs, \
+              wrap32 ? 1u : 0u)
+            if (pad_left == 0) { CM_DW3V(0); }
+            else if (pad_left == 1) { CM_DW3V(1); }
+            else { CM_DW3V(2); }
+#undef CM_DW3V
+            return CM_OK;
+        }
+    }
+    if (dw3 && stride_h == stride_w && stride_h <= 2) {
+        const uint32_t R = stride_h == 1 ? 8 : 4;
+        const uint32_t strips = (out_h + R - 1) / R;
+        const uint64_t items = (uint64_t)batch * out_ch * strips * out_w;
+        if (items < ((uint64_t)1 << 31)) {
+            const unsigned blocks = (unsigned)std::min<uint64_t>((items + 255) / 256, 65536ull * 8);
+            if (stride_h == 1) {
+                CM_LAUNCH("conv_dw3_kernel", (conv_dw3_kernel<1, 1, 8>), dim3(blocks), dim3(256), 0, s, x, w, bptr, y,
+                          (uint32_t)items, strips, out_ch, in_h, in_w, out_h, out_w, pad_top, pad_left, 16u, cs, y_cn,
+                          y_gs, wrap32 ? 1u : 0u);
+            } else {
+                CM_LAUNCH("conv_dw3_kernel", (conv_dw3_kernel<2, 2, 4>), dim3(blocks), dim3(256), 0, s, x, w, bptr, y,
+                          (uint32_t)items, strips, out_ch, in_h, in_w, out_h, out_w, pad_top, pad_left, 16u, cs, y_cn,
+                          y_gs, wrap32 ? 1u : 0u);
+            }
+            return CM_OK;
+        }
+    }
     if (is_depthwise) {
         const uint64_t total = (uint64_t)batch * out_ch * plane;
         uint64_t blocks = (total + 255) / 256;

@@ -149,6 +149,22 @@ CONV_CASES = [  # batch, C, H, W, M, kh, kw, sh, sw, dh, dw, pt, pl, pb, pr, bia
     (2, 24, 15, 17, 24, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, True, False),
     (1, 16, 20, 20, 16, 5, 5, 2, 2, 1, 1, 2, 2, 2, 2, 0, 1, True, True),
     (32, 3, 16, 16, 32, 3, 3, 2, 2, 1, 1, 1, 1, 1, 1, 1, 0, False, False),
+    # depthwise 3x3 strips: int32 sums (small operands, wrap) and int64 (full range), s1 / s2,
+    # asymmetric pads, strips cut by the plane's last rows
+    (2, 24, 15, 17, 24, 3, 3, 2, 2, 1, 1, 1, 1, 1, 1, 1, 1, False, False),
+    (2, 24, 15, 17, 24, 3, 3, 2, 2, 1, 1, 1, 1, 1, 1, 1, 1, True, False),
+    (3, 8, 9, 33, 8, 3, 3, 1, 1, 1, 1, 0, 2, 1, 0, 1, 1, False, True),
+    (3, 8, 9, 33, 8, 3, 3, 1, 1, 1, 1, 0, 2, 1, 0, 1, 1, True, True),
+    (1, 32, 56, 56, 32, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, False, False),
+    (2, 16, 112, 112, 16, 3, 3, 2, 2, 1, 1, 0, 0, 1, 1, 0, 1, False, False),
+    (4, 40, 7, 7, 40, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, False, False),
+    # depthwise 3x3 s1 on rows of 8k columns (16-byte words, v_dot2 pairs): left pads 0 / 1 / 2,
+    # strips cut by the plane's end, int64 sums (full range) and wrap
+    (2, 16, 13, 24, 16, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, False, False),
+    (1, 8, 10, 16, 8, 3, 3, 1, 1, 1, 1, 0, 0, 0, 2, 0, 1, False, True),
+    (1, 8, 12, 16, 8, 3, 3, 1, 1, 1, 1, 2, 2, 0, 0, 1, 1, True, False),
+    (1, 8, 20, 56, 8, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, True, False),
+    (2, 8, 9, 32, 8, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, True, True),
 ]
 
 
