@@ -7,6 +7,8 @@
 // 64 lanes at a time and reduced across the wavefront.
 #include "cm_common.h"
 
+#include <algorithm>
+
 namespace cm {
 namespace {
 
@@ -52,6 +54,10 @@ __device__ __forceinline__ void tap(const PoolGeom& g, long long v, long long& m
     mx = v > mx ? v : mx;
     if (g.type == 1) sum += v;
     else if (g.type == 2) sum += g.lp == 1 ? (v < 0 ? -v : v) : v * v;
+}
+
+__device__ __forceinline__ uint32_t pack_i16(int lo, int hi) {
+    return (uint32_t)(uint16_t)lo | ((uint32_t)(uint16_t)hi << 16);
 }
 
 __global__ __launch_bounds__(256) void pool_kernel(const int16_t* __restrict__ x,
@@ -100,6 +106,78 @@ __global__ __launch_bounds__(256) void pool_global_kernel(const int16_t* __restr
     if (lane == 0) y[nc] = (int16_t)finish(g, mx, sum, hw);
 }
 
+// Global pool over small planes (hw <= kSmallPlane): a lane owns a plane.  A workgroup's
+// planes are contiguous, so it copies their elements into LDS with coalesced loads and
+// each lane then reduces its own plane from LDS; the outputs leave as one contiguous run.
+constexpr uint32_t kSmallPlane = 64;
+
+__global__ __launch_bounds__(64) void pool_global_small_kernel(const int16_t* __restrict__ x,
+                                                               int16_t* __restrict__ y, uint64_t planes,
+                                                               PoolGeom g) {
+    __shared__ __attribute__((aligned(16))) int16_t buf[64 * kSmallPlane];
+    const uint32_t hw = g.in_h * g.in_w;
+    const uint64_t p0 = (uint64_t)blockIdx.x * 64;
+    const uint32_t np = (uint32_t)(planes - p0 < 64 ? planes - p0 : 64);
+    const int16_t* xs = x + p0 * hw;
+    if (np == 64 && aligned16(x)) {
+        // 64 whole planes: 8 hw 16-byte words (128 hw bytes from a 16-byte aligned start), all
+        // loads in flight before the LDS writes
+        const uint32_t n4 = 8 * hw;
+        int4 v[kSmallPlane / 8];
+#pragma unroll
+        for (uint32_t u = 0; u < kSmallPlane / 8; u++) {
+            const uint32_t i = threadIdx.x + 64 * u;
+            if (i < n4) v[u] = reinterpret_cast<const int4*>(xs)[i];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kSmallPlane / 8; u++) {
+            const uint32_t i = threadIdx.x + 64 * u;
+            if (i < n4) reinterpret_cast<int4*>(buf)[i] = v[u];
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < np * hw; i += 64) buf[i] = xs[i];
+    }
+    __syncthreads();
+    if (threadIdx.x >= np) return;
+    const int16_t* xp = buf + threadIdx.x * hw;
+    long long mx = INT64_MIN, sum = 0;
+    for (uint32_t i = 0; i < hw; i++) tap(g, xp[i], mx, sum);
+    y[p0 + threadIdx.x] = (int16_t)finish(g, mx, sum, hw);
+}
+
+// MAX / AVG 2x2 stride 2 without padding or dilation, on rows of 16k columns: a lane makes 8
+// outputs of one row from two 16-byte words of each of its two input rows and writes them as
+// one 16-byte word.  AVG divides by the window's 4 taps: (sum * round(2^23 / 4)) >> 23.
+__global__ __launch_bounds__(256) void pool2x2_kernel(const int16_t* __restrict__ x, int16_t* __restrict__ y,
+                                                      uint64_t items, uint32_t groups, PoolGeom g) {
+    for (uint64_t it = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; it < items;
+         it += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t row = it / groups;                       // plane * out_h + oh
+        const uint32_t j = (uint32_t)(it - row * groups);
+        const uint64_t plane = row / g.out_h;
+        const uint32_t oh = (uint32_t)(row - plane * g.out_h);
+        const int16_t* r0 = x + (plane * g.in_h + 2 * oh) * g.in_w + 16 * j;
+        const int16_t* r1 = r0 + g.in_w;
+        int4 v[4] = {*reinterpret_cast<const int4*>(r0), *reinterpret_cast<const int4*>(r0 + 8),
+                     *reinterpret_cast<const int4*>(r1), *reinterpret_cast<const int4*>(r1 + 8)};
+        const int16_t* a = reinterpret_cast<const int16_t*>(&v[0]);   // row 2 oh, 16 columns
+        const int16_t* b = reinterpret_cast<const int16_t*>(&v[2]);   // row 2 oh + 1
+        int q[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const int x0 = a[2 * t], x1 = a[2 * t + 1], x2 = b[2 * t], x3 = b[2 * t + 1];
+            if (g.type == 0) q[t] = max(max(x0, x1), max(x2, x3));
+            else q[t] = (x0 + x1 + x2 + x3) >> 2;                    // (sum * 2^21) >> 23, in range
+        }
+        int4 o;
+        o.x = (int)pack_i16(q[0], q[1]);
+        o.y = (int)pack_i16(q[2], q[3]);
+        o.z = (int)pack_i16(q[4], q[5]);
+        o.w = (int)pack_i16(q[6], q[7]);
+        store_stream(y + row * g.out_w + 8 * j, o);
+    }
+}
+
 }  // namespace
 }  // namespace cm
 
@@ -124,6 +202,20 @@ extern "C" int cm_pool(const int16_t* x, int16_t* y, uint32_t batch, uint32_t ch
     hipStream_t s = as_stream(stream);
     const bool global = out_h == 1 && out_w == 1 && pool_h == in_h && pool_w == in_w &&
                         pad_top == 0 && pad_left == 0 && dil_h == 1 && dil_w == 1;
+    if (global && (uint64_t)in_h * in_w <= kSmallPlane) {
+        CM_LAUNCH("pool_global_kernel", pool_global_small_kernel, dim3((unsigned)((planes + 63) / 64)), dim3(64), 0,
+                  s, x, y, planes, g);
+        return CM_OK;
+    }
+    if (pool_type <= 1 && pool_h == 2 && pool_w == 2 && stride_h == 2 && stride_w == 2 && dil_h == 1 &&
+        dil_w == 1 && pad_top == 0 && pad_left == 0 && (in_w & 15) == 0 && out_w == in_w / 2 &&
+        out_h <= in_h / 2 && aligned16(x) && aligned16(y)) {
+        const uint32_t groups = out_w / 8;
+        const uint64_t items = planes * out_h * groups;
+        const unsigned blocks = (unsigned)std::min<uint64_t>((items + 255) / 256, 65536ull * 8);
+        CM_LAUNCH("pool2x2_kernel", pool2x2_kernel, dim3(blocks), dim3(256), 0, s, x, y, items, groups, g);
+        return CM_OK;
+    }
     if (global) {
         CM_LAUNCH("pool_global_kernel", pool_global_kernel, dim3((unsigned)((planes + 3) / 4)), dim3(256), 0, s,
                            x, y, planes, g);

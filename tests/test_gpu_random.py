@@ -341,6 +341,12 @@ POOL_CASES = [  # N, C, H, W, ph, pw, sh, sw, pt, pl, pb, pr, dh, dw, type, lp, 
     (32, 64, 7, 7, 7, 7, 1, 1, 0, 0, 0, 0, 1, 1, 1, 2, 0),
     (4, 32, 6, 6, 6, 6, 1, 1, 0, 0, 0, 0, 1, 1, 0, 2, 0),
     (3, 16, 5, 5, 5, 5, 1, 1, 0, 0, 0, 0, 1, 1, 2, 2, 0),
+    (2, 7, 9, 9, 9, 9, 1, 1, 0, 0, 0, 0, 1, 1, 1, 2, 0),       # global, plane above 64
+    # MAX / AVG 2x2 s2 on rows of 16k columns (16-byte words); odd heights drop the last row
+    (2, 5, 8, 32, 2, 2, 2, 2, 0, 0, 0, 0, 1, 1, 0, 2, 0),
+    (2, 5, 9, 32, 2, 2, 2, 2, 0, 0, 0, 0, 1, 1, 1, 2, 1),
+    (1, 3, 16, 112, 2, 2, 2, 2, 0, 0, 0, 0, 1, 1, 1, 2, 0),
+    (1, 3, 16, 112, 2, 2, 2, 2, 0, 0, 0, 0, 1, 1, 0, 2, 0),
 ]
 
 
