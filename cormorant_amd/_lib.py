@@ -40,6 +40,7 @@ SIGNATURES = {
     "cm_rowops": (_I32, [_P, _P, _P, _P] + [_U32] * 10 + [_I64] + [_U32] * 4 + [_P]),
     "cm_rowops_chain": (_I32, [ctypes.POINTER(CmRowopsDesc), _U32, _P]),
     "cm_softmax": (_I32, [_P, _P] + [_U32] * 9 + [ctypes.c_uint64, ctypes.c_uint64, _P]),
+    "cm_permute16": (_I32, [_P, _P] + [_U32] * 4 + [ctypes.c_uint64] * 4 + [_P]),
     "cm_timing_enable": (_I32, [_I32]),
     "cm_timing_read": (_I32, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                               ctypes.POINTER(ctypes.c_uint64)]),

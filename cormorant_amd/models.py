@@ -9,11 +9,15 @@ SoftmaxVopNode; _simulate.py:617-765).
 """
 from __future__ import annotations
 
+import math
+from dataclasses import dataclass
+
 import numpy as np
 
 from . import units
-from .graph import (ConvNode, Graph, MatmulNode, PoolNode, ReshapeNode, ScheduledNode,
-                    SoftmaxVopNode, TensorInfo)
+from .graph import (AttnContractNode, ConvNode, Graph, MatmulNode, PermuteNode, PoolNode, ReshapeNode, ScheduledNode,
+                    SoftmaxVopNode, TensorInfo, softmax_regs)
+from .rowops_nodes import LayerNorm32RoNode, ResAddBiasRoNode
 
 
 def small_cnn(seed: int = 0):
@@ -52,3 +56,193 @@ def small_cnn(seed: int = 0):
     g = Graph(nodes, input_tensors=[x], output_tensors=[sm])
     inputs = {"input": np.round(rng.uniform(0.0, 1.0, (1, 1, 28, 28)) * 256) / 256}
     return g, inputs
+
+
+# ---------------------------------------------------------------- BERT-base-shaped encoder
+RES_BITS = 15        # the int32 residual's exponent (graph_builder.py:35)
+F_Q88 = 8            # the element grid of Q8.8 tensors (the activation unit's input)
+
+
+def _fit_exp(maxabs: float, margin: float = 1.25, lo: int = -8, hi: int = 24) -> int:
+    """The largest f with maxabs * margin * 2^f <= 32767 (a per-tensor pow2 exponent)."""
+    if maxabs <= 0:
+        return hi
+    return int(max(lo, min(hi, math.floor(math.log2(32767.0 / (maxabs * margin))))))
+
+
+def _gelu(x):
+    return x * 0.5 * (1.0 + np.vectorize(math.erf)(x / math.sqrt(2.0)))
+
+
+def _layer_norm(h, gamma, beta, eps):
+    mu = h.mean(axis=-1, keepdims=True)
+    var = ((h - mu) ** 2).mean(axis=-1, keepdims=True)
+    return (h - mu) / np.sqrt(var + eps) * gamma + beta
+
+
+@dataclass
+class BertShape:
+    layers: int = 12
+    batch: int = 8
+    seq: int = 384
+    d: int = 768
+    heads: int = 12
+    ff: int = 3072
+    vocab: int = 30522
+    eps: float = 1e-12
+
+    @property
+    def hd(self) -> int:
+        return self.d // self.heads
+
+    def macs(self) -> int:
+        """Multiply-accumulates of one forward: the linears and the attention contractions."""
+        rows = self.batch * self.seq
+        lin = rows * (3 * self.d * self.d + self.d * self.d + 2 * self.d * self.ff)
+        att = 2 * self.batch * self.heads * self.seq * self.seq * self.hd
+        return self.layers * (lin + att)
+
+
+def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int = 1):
+    """(graph, inputs, exps): the BERT-base-shaped encoder in per-tensor power-of-two numerics.
+
+    Token ids U{0 .. vocab-1} and embedding rows N(0, 1) (the embedding lookup is the host
+    op whose result, the int32 residual at 2^-15, is the graph's input); per layer, in the
+    arrangement of the reference's encoder template (vit.py:19-32):
+
+        x  = LayerNorm32(h)                          row-ops NORM, int32 -> int16
+        qkv = x . Wqkv                               MatMul (pow2, int32 wrap)
+        q^T, K, V per head                           Permute (the head split)
+        s  = K . q^T   [B H][keys][queries]          batched MatMul, f_s = f_q + f_k - 8
+        P  = softmax over keys (column mode)         VectorOP softmax, logit scale 1/sqrt(hd)
+        o  = P . V     [B H][queries][hd]            batched MatMul, f_o = f_p + f_v - 8
+        h1 = ResAddBias(h, merge(o) . Wo, bo)        Permute, MatMul, row-ops ADDX
+        x2 = LayerNorm32(h1);  f = x2 . W1  (at 2^-8)
+        a  = GELU(f + b1)                            VectorOP ADD with the GELU act
+        h  = ResAddBias(h1, a . W2, b2)
+
+    Weights N(0, 0.02), biases N(0, 0.02), LayerNorm gamma N(1, 0.02), beta N(0, 0.02).
+    Exponents: a float64 run of the first ``calib_seqs`` sequences gives each tensor's
+    largest |value|, and each tensor takes the largest exponent that keeps it below 32767
+    with a 1.25 margin; the contractions' output exponents follow from their operands', the
+    q / v exponents are lowered where the scores or P.V would not fit.  ``exps`` records them.
+    """
+    from .numeric import encode_matmul_weights
+    from .dtype import AP_FIXED_16_8
+
+    S = shape
+    rng = np.random.default_rng(seed)
+    ids = rng.integers(0, S.vocab, (S.batch, S.seq))
+    emb = rng.standard_normal((S.vocab, S.d), dtype=np.float32)
+    h0 = emb[ids].astype(np.float64).reshape(S.batch * S.seq, S.d)
+    del emb
+    h0 = np.round(h0 * 2.0 ** RES_BITS) / 2.0 ** RES_BITS
+    norm = lambda *sh: (rng.standard_normal(sh, dtype=np.float32) * 0.02)       # noqa: E731
+    Ls = []
+    for _ in range(S.layers):
+        Ls.append(dict(g1=1.0 + norm(S.d).astype(np.float64), be1=norm(S.d).astype(np.float64),
+                       wqkv=norm(S.d, 3 * S.d), wo=norm(S.d, S.d), bo=norm(S.d).astype(np.float64),
+                       g2=1.0 + norm(S.d).astype(np.float64), be2=norm(S.d).astype(np.float64),
+                       w1=norm(S.d, S.ff), b1=norm(S.ff).astype(np.float64), w2=norm(S.ff, S.d),
+                       b2=norm(S.d).astype(np.float64)))
+
+    # ---- calibration: a float64 forward of the first sequences, the largest |value| per tensor
+    H, hd, T = S.heads, S.hd, S.seq
+    cal = []
+    h = h0[:calib_seqs * T]
+    for L in Ls:
+        m = {}
+        x = _layer_norm(h, L["g1"], L["be1"], S.eps)
+        qkv = x @ L["wqkv"].astype(np.float64)
+        q, k, v = qkv[:, :S.d], qkv[:, S.d:2 * S.d], qkv[:, 2 * S.d:]
+        m.update(x1=np.abs(x).max(), q=np.abs(q).max(), k=np.abs(k).max(), v=np.abs(v).max())
+        qh = q.reshape(-1, T, H, hd).transpose(0, 2, 1, 3)
+        kh = k.reshape(-1, T, H, hd).transpose(0, 2, 1, 3)
+        vh = v.reshape(-1, T, H, hd).transpose(0, 2, 1, 3)
+        s = kh @ qh.transpose(0, 1, 3, 2)                       # [b][h][keys][queries]
+        p = np.exp((s - s.max(axis=2, keepdims=True)) / math.sqrt(hd))
+        p = p / p.sum(axis=2, keepdims=True)
+        o = p.transpose(0, 1, 3, 2) @ vh                        # [b][h][queries][hd]
+        m.update(s=np.abs(s).max(), o=np.abs(o).max())
+        om = o.transpose(0, 2, 1, 3).reshape(-1, S.d)
+        ao = om @ L["wo"].astype(np.float64)
+        h1 = h + ao + L["bo"]
+        x2 = _layer_norm(h1, L["g2"], L["be2"], S.eps)
+        f = x2 @ L["w1"].astype(np.float64)
+        a = _gelu(f + L["b1"])
+        dd = a @ L["w2"].astype(np.float64)
+        h = h1 + dd + L["b2"]
+        m.update(ao=np.abs(ao).max(), x2=np.abs(x2).max(), f=np.abs(f + L["b1"]).max(), dd=np.abs(dd).max())
+        cal.append(m)
+
+    exps = []
+    for m in cal:
+        e = {key: _fit_exp(val) for key, val in m.items()}
+        e["p"] = 14                                             # P <= 1: 2^14 fits int16
+        # scores s at f_q + f_k - 8: lower the larger of q / k until s fits
+        while e["q"] + e["k"] - F_Q88 > e["s"]:
+            if e["q"] >= e["k"]:
+                e["q"] -= 1
+            else:
+                e["k"] -= 1
+        e["s"] = e["q"] + e["k"] - F_Q88
+        # P.V at f_p + f_v - 8 must fit: v no finer than the output allows
+        e["v"] = min(e["v"], e["o"] - e["p"] + F_Q88)
+        e["o"] = e["p"] + e["v"] - F_Q88
+        e["f"] = F_Q88                                          # the act unit's grid
+        e["ao"] = min(e["ao"], RES_BITS)                        # residual deltas: no finer than 2^-15
+        e["dd"] = min(e["dd"], RES_BITS)
+        exps.append(e)
+
+    # ---- the integer graph
+    T_ = TensorInfo
+    rows, D = S.batch * S.seq, S.d
+    BH = S.batch * H
+    nodes = []
+    h_in = T_("h0", [rows, D], exp=RES_BITS, kind="i32")
+    hcur = h_in
+    for li, (L, e) in enumerate(zip(Ls, exps)):
+        p = f"l{li}."
+        x1 = T_(p + "x1", [rows, D], exp=e["x1"])
+        nodes.append(LayerNorm32RoNode([hcur], x1, gamma=L["g1"], beta=L["be1"], eps=S.eps))
+        wqkv = T_(p + "wqkv", [D, 3 * D], data=L["wqkv"])
+        qkv = T_(p + "qkv", [rows, 3 * D], exp=np.repeat([e["q"], e["k"], e["v"]], D))
+        nodes.append(MatmulNode([x1, wqkv], qkv))
+        ld = 3 * D
+        qT = T_(p + "qT", [BH, hd, T], exp=e["q"])
+        kh = T_(p + "kh", [BH, T, hd], exp=e["k"])
+        vh = T_(p + "vh", [BH, T, hd], exp=e["v"])
+        nodes.append(PermuteNode([qkv], qT, dims=(S.batch, H, hd, T), strides=(T * ld, hd, 1, ld), offset=0))
+        nodes.append(PermuteNode([qkv], kh, dims=(S.batch, H, T, hd), strides=(T * ld, hd, ld, 1), offset=D))
+        nodes.append(PermuteNode([qkv], vh, dims=(S.batch, H, T, hd), strides=(T * ld, hd, ld, 1), offset=2 * D))
+        sc = T_(p + "s", [BH, T, T], exp=e["s"])
+        nodes.append(AttnContractNode([kh, qT], sc))
+        cmr, cfg = softmax_regs(e["s"], 1.0 / math.sqrt(hd), e["p"])
+        pr = T_(p + "P", [BH, T, T], exp=e["p"])
+        nodes.append(SoftmaxVopNode([sc], pr, cm=cmr, cfg=cfg, keys_major=True))
+        o = T_(p + "o", [BH, T, hd], exp=e["o"])
+        nodes.append(AttnContractNode([pr, vh], o))
+        om = T_(p + "om", [rows, D], exp=e["o"])
+        nodes.append(PermuteNode([o], om, dims=(S.batch, T, H, hd), strides=(H * T * hd, hd, T * hd, 1)))
+        wo = T_(p + "wo", [D, D], data=L["wo"])
+        ao = T_(p + "ao", [rows, D], exp=e["ao"])
+        nodes.append(MatmulNode([om, wo], ao))
+        h1 = T_(p + "h1", [rows, D], exp=RES_BITS, kind="i32")
+        nodes.append(ResAddBiasRoNode([hcur, ao], h1, bias=L["bo"]))
+        x2 = T_(p + "x2", [rows, D], exp=e["x2"])
+        nodes.append(LayerNorm32RoNode([h1], x2, gamma=L["g2"], beta=L["be2"], eps=S.eps))
+        w1 = T_(p + "w1", [D, S.ff], data=L["w1"])
+        f = T_(p + "f", [rows, S.ff], exp=F_Q88)
+        nodes.append(MatmulNode([x2, w1], f))
+        b1 = T_(p + "b1", [S.ff], data=L["b1"])
+        a = T_(p + "a", [rows, S.ff], exp=F_Q88)
+        nodes.append(ScheduledNode([f, b1], a, units.OP_ADD, act=units.ACT_GELU))
+        w2 = T_(p + "w2", [S.ff, D], data=L["w2"])
+        dd = T_(p + "dd", [rows, D], exp=e["dd"])
+        nodes.append(MatmulNode([a, w2], dd))
+        hn = T_(p + "h", [rows, D], exp=RES_BITS, kind="i32")
+        nodes.append(ResAddBiasRoNode([h1, dd], hn, bias=L["b2"]))
+        hcur = hn
+    g = Graph(nodes, input_tensors=[h_in], output_tensors=[hcur])
+    encode_matmul_weights(g.nodes, AP_FIXED_16_8)
+    return g, {"h0": h0}, exps

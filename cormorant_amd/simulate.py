@@ -16,8 +16,8 @@ import torch
 
 from . import units
 from .dtype import AP_FIXED_16_8, ApFixed16
-from .graph import (ConvNode, Graph, LlmAttnConvNode, MatmulNode, PoolNode, ReshapeNode, RowOpsNode,
-                    ScheduledNode, SchedulerError, SoftmaxVopNode, TensorInfo, attn_keys)
+from .graph import (AttnContractNode, ConvNode, Graph, LlmAttnConvNode, MatmulNode, PermuteNode, PoolNode,
+                    ReshapeNode, RowOpsNode, ScheduledNode, SchedulerError, SoftmaxVopNode, TensorInfo, attn_keys)
 from .packing import conv_bias_image, conv_weight_image, pack_matmul_b
 from .rowops_nodes import RoJob, RowOpsAdapter
 
@@ -84,6 +84,10 @@ class Simulator:
                 raw[sn.output.onnx_name] = self._adapter(sn, raw)
             elif isinstance(sn, LlmAttnConvNode):
                 raw[sn.output.onnx_name] = self._attn_conv(sn, raw)
+            elif isinstance(sn, PermuteNode):
+                raw[sn.output.onnx_name] = self._permute(sn, raw)
+            elif isinstance(sn, AttnContractNode):
+                raw[sn.output.onnx_name] = self._attn_contract(sn, raw)
             elif isinstance(sn, ScheduledNode):
                 raw[sn.output.onnx_name] = self._vectorop(sn, raw)
             else:
@@ -353,6 +357,29 @@ class Simulator:
         vc = self._get(x, raw).reshape(sn.KV, C, HD)[g, :keys]
         out = torch.empty(GT * HD, dtype=torch.int16, device=self.device)
         units.matmul(p.reshape(-1), vc.reshape(-1), out, GT, keys, HD, wrap32=True)
+        return out
+
+    def _attn_contract(self, sn: AttnContractNode, raw) -> torch.Tensor:
+        at, bt, ot = sn.inputs[0], sn.inputs[1], sn.output
+        batch, n, k = at.shape
+        if len(bt.shape) != 3 or bt.shape[0] != batch or bt.shape[1] != k or list(ot.shape) != [batch, n, bt.shape[2]]:
+            raise SchedulerError(f"attention contraction '{ot.onnx_name}': [b][n][k] x [b][k][m] -> [b][n][m]")
+        fa, fb, fo = (np.asarray(self._exp(t)).reshape(-1) for t in (at, bt, ot))
+        if fa.size != 1 or fb.size != 1 or fo.size != 1 or int(fo[0]) != int(fa[0]) + int(fb[0]) - self._dtype.frac_bits:
+            raise SchedulerError(f"attention contraction '{ot.onnx_name}': output exponent is not f_a + f_b - 8")
+        m = int(bt.shape[2])
+        c = self._new(ot)
+        units.matmul(self._get(at, raw).reshape(-1).contiguous(), self._get(bt, raw).reshape(-1).contiguous(), c,
+                     n, k, m, batch=batch, a_bs=n * k, b_bs=k * m, c_bs=n * m, wrap32=True)
+        return c
+
+    def _permute(self, sn: PermuteNode, raw) -> torch.Tensor:
+        xt, ot = sn.inputs[0], sn.output
+        if xt.kind != "i16" or ot.kind != "i16" or int(np.prod(sn.dims)) != ot.numel:
+            raise SchedulerError(f"Permute '{ot.onnx_name}': int16 tensors, dims covering the output")
+        x = self._get(xt, raw).reshape(-1)
+        out = self._new(ot)
+        units.permute16(x[int(sn.offset):], out, sn.dims, sn.strides)
         return out
 
     def _rows16(self, x2d: torch.Tensor, kind: str):

@@ -97,6 +97,22 @@ def softmax(a: torch.Tensor, c: torch.Tensor, size: int, op: int, outer: int, a_
     return c
 
 
+def permute16(src: torch.Tensor, dst: torch.Tensor, dims, strides) -> torch.Tensor:
+    """dst[i0][i1][i2][i3] = src[sum i_k s_k] (cm_permute16): ``dims`` the 4 dst extents,
+    ``strides`` the src strides of those dimensions, in elements."""
+    d = [int(v) for v in dims]
+    st = [int(v) for v in strides]
+    if len(d) != 4 or len(st) != 4 or min(d) < 0 or min(st) < 0:
+        raise ValueError("permute16: 4 dims and 4 non-negative strides")
+    total = d[0] * d[1] * d[2] * d[3]
+    if total:
+        _require(src, "src", torch.int16, 1 + sum((dk - 1) * sk for dk, sk in zip(d, st)))
+        _require(dst, "dst", torch.int16, total)
+    rc = _lib.lib().cm_permute16(_ptr(src), _ptr(dst), *d, *st, _stream())
+    _lib.check(rc, "cm_permute16")
+    return dst
+
+
 def matmul_b_extent(k: int, m: int, b_packed: int, gemv_kw: int) -> int:
     if gemv_kw:
         return k * m

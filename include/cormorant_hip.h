@@ -169,6 +169,15 @@ typedef struct cm_rowops_desc {
  * the previous ones wrote (ROWOPS_RTL_KERNEL.md section 1.6; no 16-job cap). */
 int cm_rowops_chain(const cm_rowops_desc* jobs, uint32_t n_jobs, void* stream);
 
+/* ---------------------------------------------------------------- Layout
+ * The attention's operand moves between the projection MatMuls and the contractions (the
+ * reference does them on the host / by DMA: VitAttnPrep and LlmAttnMerge, vit.py:19-32,
+ * llm_nodes.py AttnPrep / Merge): a 4-D strided int16 gather,
+ *   dst[i0][i1][i2][i3] (contiguous) = src[i0 * s0 + i1 * s1 + i2 * s2 + i3 * s3]
+ * (strides in elements).  No unit of the reference's five; the exact copy of its moves. */
+int cm_permute16(const int16_t* src, int16_t* dst, uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3,
+                 uint64_t s0, uint64_t s1, uint64_t s2, uint64_t s3, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,54 @@
+"""The encoder builder and its graph pieces on the CPU: the softmax registers (the small
+CNN's regs(8, 1.0, 8) known answer), the permute gather against numpy's transpose, the
+exponent rules the contractions impose, and the MAC count of the full-size shape."""
+import math
+
+import numpy as np
+
+from cormorant_amd import models
+from cormorant_amd.graph import AttnContractNode, PermuteNode, SoftmaxVopNode, TensorInfo, softmax_regs
+
+SMALL = models.BertShape(layers=2, batch=2, seq=64, d=128, heads=2, ff=512, vocab=1000)
+
+
+def test_softmax_regs_known_answers():
+    assert softmax_regs(8, 1.0, 8) == (12102203, 0x0813)     # SoftmaxVopNode's C1 default
+    cm, cfg = softmax_regs(13, 0.125, 14)
+    c = math.log2(math.e) * 0.125 * 2.0 ** -13 * 4096
+    assert cfg >> 8 == 14 and 2 ** 23 <= cm < 2 ** 24
+    assert abs(cm * 2.0 ** -(cfg & 63) - c) <= 2.0 ** -(cfg & 63)
+
+
+def test_permute_gather_is_the_transpose():
+    B, T, H, hd = 2, 5, 3, 4
+    x = np.arange(B * T * 3 * H * hd).reshape(B, T, 3 * H * hd)
+    ld = 3 * H * hd
+    q = PermuteNode([TensorInfo("x", list(x.shape))], TensorInfo("q", [B * H, hd, T]), dims=(B, H, hd, T),
+                    strides=(T * ld, hd, 1, ld))
+    want_q = x[:, :, :H * hd].reshape(B, T, H, hd).transpose(0, 2, 3, 1).reshape(-1)
+    assert np.array_equal(x.reshape(-1)[q.gather_index()], want_q)
+    v = PermuteNode([TensorInfo("x", list(x.shape))], TensorInfo("v", [B * H, T, hd]), dims=(B, H, T, hd),
+                    strides=(T * ld, hd, ld, 1), offset=2 * H * hd)
+    want_v = x[:, :, 2 * H * hd:].reshape(B, T, H, hd).transpose(0, 2, 1, 3).reshape(-1)
+    assert np.array_equal(x.reshape(-1)[v.gather_index()], want_v)
+
+
+def test_encoder_exponents_and_structure():
+    g, inputs, exps = models.bert_encoder(SMALL, seed=1)
+    assert inputs["h0"].shape == (SMALL.batch * SMALL.seq, SMALL.d)
+    assert np.array_equal(inputs["h0"] * 2 ** 15, np.round(inputs["h0"] * 2 ** 15))
+    for e in exps:
+        assert e["s"] == e["q"] + e["k"] - 8 and e["o"] == e["p"] + e["v"] - 8
+        assert e["f"] == 8 and e["ao"] <= 15 and e["dd"] <= 15
+    contract = [sn for sn in g.nodes if isinstance(sn, AttnContractNode)]
+    assert len(contract) == 2 * SMALL.layers
+    for sn in contract:
+        a, b = sn.inputs
+        assert sn.output.exp == a.exp + b.exp - 8
+    smx = [sn for sn in g.nodes if isinstance(sn, SoftmaxVopNode)]
+    assert all(sn.keys_major for sn in smx) and len(smx) == SMALL.layers
+
+
+def test_full_shape_macs():
+    # 12 x 3072 x (4 x 768^2 + 2 x 768 x 3072) + 2 x 8 x 12 x 384^2 x 64 x 12
+    assert models.BertShape().macs() == 260_919_263_232 + 21_743_271_936
