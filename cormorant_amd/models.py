@@ -131,12 +131,15 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
     from .dtype import AP_FIXED_16_8
 
     S = shape
-    rng = np.random.default_rng(seed)
-    ids = rng.integers(0, S.vocab, (S.batch, S.seq))
-    emb = rng.standard_normal((S.vocab, S.d), dtype=np.float32)
+    # ids / embeddings and weights from their own generators: a smaller batch of the same seed
+    # is the leading sequences of a larger one, with the same weights and exponents
+    rng_in = np.random.default_rng([seed, 0])
+    emb = rng_in.standard_normal((S.vocab, S.d), dtype=np.float32)
+    ids = rng_in.integers(0, S.vocab, (S.batch, S.seq))
     h0 = emb[ids].astype(np.float64).reshape(S.batch * S.seq, S.d)
     del emb
     h0 = np.round(h0 * 2.0 ** RES_BITS) / 2.0 ** RES_BITS
+    rng = np.random.default_rng([seed, 1])
     norm = lambda *sh: (rng.standard_normal(sh, dtype=np.float32) * 0.02)       # noqa: E731
     Ls = []
     for _ in range(S.layers):

@@ -40,6 +40,7 @@ class Simulator:
         self._weights: Dict[str, torch.Tensor] = {}      # raw device copies of the weights
         self._images: Dict[str, torch.Tensor] = {}       # packed weight images
         self._infos: Dict[str, TensorInfo] = {}
+        self._params: Dict[int, list] = {}                # row-ops parameter blocks on the device
         for t in graph.input_tensors + graph.output_tensors:
             self._infos[t.onnx_name] = t
         for sn in graph.nodes:
@@ -382,6 +383,14 @@ class Simulator:
         units.permute16(x[int(sn.offset):], out, sn.dims, sn.strides)
         return out
 
+    @staticmethod
+    def _rows_whole(sn: RowOpsAdapter, width: int) -> bool:
+        """Every tensor of the adapter has rows of whole 16-byte words."""
+        ts = [sn.inputs[0], sn.output] + ([sn.inputs[1]] if len(sn.inputs) > 1 else [])
+        if getattr(sn, "table", None) is not None:
+            return False
+        return all((width * _KB[t.kind]) % 16 == 0 and int(t.shape[-1]) == width for t in ts)
+
     def _rows16(self, x2d: torch.Tensor, kind: str):
         """[rows][w] lanes re-laid at a 16-byte row stride: (buffer, stride bytes, lanes per row)."""
         rows, w = x2d.shape
@@ -402,7 +411,20 @@ class Simulator:
         out = torch.empty((rows, width), dtype=_TORCH[ot.kind], device=self.device)
         b_all = self._get(bt, raw) if bt is not None else None
         u8 = lambda t: t.reshape(-1).view(torch.uint8) if t is not None else None   # noqa: E731
-        for j in jobs:
+        params = self._params.get(id(sn))
+        if params is None:
+            params = [torch.from_numpy(np.ascontiguousarray(j.params, np.uint8)).to(self.device) for j in jobs]
+            self._params[id(sn)] = params
+        if len(jobs) == 1 and jobs[0].col0 == 0 and jobs[0].b_row0 is None and self._rows_whole(sn, width):
+            # rows already whole 16-byte multiples: the jobs run on the tensors themselves
+            j = jobs[0]
+            b2d = b_all.reshape(rows, width) if b_all is not None else None
+            units.rowops(u8(a2d.contiguous()), u8(b2d.contiguous() if b2d is not None else None), u8(out), params[0],
+                         j.op, j.n, rows, 1, width * _KB[at.kind], 0,
+                         width * _KB[bt.kind] if bt is not None else 0, 0, width * _KB[ot.kind], 0,
+                         j.eps, j.aux, j.bq_sh, 0, 0xFFFFFFFF)
+            return out.reshape(-1)
+        for ji, j in enumerate(jobs):
             a_buf, a_s1, _ = self._rows16(a2d[:, j.col0:j.col0 + j.n], at.kind)
             b_buf, b_s1 = None, 0
             if b_all is not None:
@@ -416,9 +438,8 @@ class Simulator:
                 b_buf, b_s1, _ = self._rows16(b2d, bt.kind)
             c_buf, c_s1, c_per = self._rows16(torch.zeros((rows, j.n), dtype=_TORCH[ot.kind], device=self.device),
                                               ot.kind)
-            p = torch.from_numpy(np.ascontiguousarray(j.params, np.uint8)).to(self.device)
-            units.rowops(u8(a_buf), u8(b_buf), u8(c_buf), p, j.op, j.n, rows, 1, a_s1, 0, b_s1, 0, c_s1, 0,
-                         j.eps, j.aux, j.bq_sh, 0, 0xFFFFFFFF)
+            units.rowops(u8(a_buf), u8(b_buf), u8(c_buf), params[ji], j.op, j.n, rows, 1, a_s1, 0, b_s1, 0, c_s1,
+                         0, j.eps, j.aux, j.bq_sh, 0, 0xFFFFFFFF)
             out[:, j.col0:j.col0 + j.n] = c_buf[:, :j.n]
         return out.reshape(-1)
 

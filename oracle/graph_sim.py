@@ -3,7 +3,7 @@
 with numpy float64, the way the reference computes: np.matmul / per-tap conv sums (exact for
 on-grid operands), then ``truncate`` (clip + floor).  Pooling, the activation unit, softmax
 and row-ops use the C oracle on raw lanes.  Test infrastructure only: the graph-level check
-of cormorant_amd.simulate.Simulator.
+of cormorant_amd.simulate.Simulator, and the CPU baseline bench.py times.
 """
 import numpy as np
 

@@ -7,7 +7,7 @@ import pytest
 
 from cormorant_amd import models
 from cormorant_amd.simulate import Simulator
-import oracle_graph
+from oracle import graph_sim as oracle_graph
 
 pytestmark = pytest.mark.gpu
 

@@ -10,7 +10,7 @@ from cormorant_amd.dtype import AP_FIXED_16_8 as DT
 from cormorant_amd.graph import ConvNode, Graph, LlmAttnConvNode, MatmulNode, TensorInfo
 from cormorant_amd.numeric import encode_conv_weights, encode_matmul_weights
 from cormorant_amd.simulate import Simulator
-import oracle_graph
+from oracle import graph_sim as oracle_graph
 
 pytestmark = pytest.mark.gpu
 

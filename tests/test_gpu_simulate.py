@@ -18,7 +18,7 @@ def torch_gpu():
 def test_small_cnn_matches_reference_forward(torch_gpu, seed):
     from cormorant_amd import models
     from cormorant_amd.simulate import Simulator
-    import oracle_graph
+    from oracle import graph_sim as oracle_graph
     g, inputs = models.small_cnn(seed)
     sim = Simulator(g)
     got = sim._forward_pass(inputs)
@@ -35,7 +35,7 @@ def test_matmul_node_batched_broadcast_b(torch_gpu):
     """MatMul with A [3, 5, 70] and a shared weight B [70, 33] (packed once)."""
     from cormorant_amd import graph as G
     from cormorant_amd.simulate import Simulator
-    import oracle_graph
+    from oracle import graph_sim as oracle_graph
     rng = np.random.default_rng(4)
     a = G.TensorInfo("a", [3, 5, 70])
     w = G.TensorInfo("w", [70, 33], data=rng.uniform(-2, 2, (70, 33)))
@@ -50,7 +50,7 @@ def test_vectorop_broadcast_bias_unaligned(torch_gpu):
     [4, 16] (one that is): both broadcast paths."""
     from cormorant_amd import graph as G
     from cormorant_amd.simulate import Simulator
-    import oracle_graph
+    from oracle import graph_sim as oracle_graph
     rng = np.random.default_rng(5)
     for rows, n in ((6, 10), (4, 16)):
         x = G.TensorInfo("x", [rows, n])

@@ -9,7 +9,7 @@ import pytest
 from cormorant_amd.dtype import AP_FIXED_16_8 as DT
 from cormorant_amd.graph import ConvNode, MatmulNode, TensorInfo, attn_keys
 from cormorant_amd.numeric import NumericError, encode_conv_weights, encode_matmul_weights
-import oracle_graph
+from oracle import graph_sim as oracle_graph
 
 F = 8
 

@@ -4,7 +4,7 @@ nodes' closed forms: pins the parameter derivation and the job registers without
 import numpy as np
 import pytest
 
-from oracle_graph import run_adapter
+from oracle.graph_sim import run_adapter
 from rowops_node_cases import CASES, same
 
 
