@@ -443,7 +443,7 @@ __device__ __forceinline__ void lds_copy16(const int8_t* g, int8_t* lds_wave_bas
 }
 
 template <int WR, int NST, class Epi>
-__global__ __launch_bounds__(128 * WR, 8 / (2 * WR)) void gemm_planes_kernel(
+__global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_planes_kernel(
     const int8_t* __restrict__ Ahi, const int8_t* __restrict__ Alo, const int32_t* __restrict__ rpart,
     uint64_t a_slice, uint64_t rp_slice, uint32_t a_lines, const int8_t* __restrict__ Bhi,
     const int8_t* __restrict__ Blo, const int32_t* __restrict__ cpart, uint64_t b_slice, uint64_t cp_slice,
@@ -531,9 +531,12 @@ __global__ __launch_bounds__(128 * WR, 8 / (2 * WR)) void gemm_planes_kernel(
             lds_copy16(bl_src + ((q) - 4 - BCP) * kp16 + k_, &SM[2 * A_T + B_T + b_dst + 1024 * ((q) - 4 - BCP)]); \
     }
     // The copies of slot s (after the s-th group of four MFMAs, 0..7): waves of copy group
-    // g issue theirs in slots 4g .. 4g + 3, two, two, then the rest.
+    // g issue theirs in slots 4g .. 4g + 3, two, two, then the rest; with 2 waves (12 copies)
+    // the one group issues two in each of slots 0 .. 5.
 #define CM_COPIES(SM, step, slot)                                                 \
-    if (((slot) >> 2) == cgrp) {                                                  \
+    if (NW == 2) {                                                                \
+        if ((slot) < 6) { CM_COPY(SM, step, 2 * (slot)) CM_COPY(SM, step, 2 * (slot) + 1) } \
+    } else if (((slot) >> 2) == cgrp) {                                           \
         constexpr int s_ = (slot) & 3;                                            \
         if (s_ < 2) { CM_COPY(SM, step, 2 * s_) CM_COPY(SM, step, 2 * s_ + 1) }   \
         else if (NC == 6) { CM_COPY(SM, step, 2 + s_) }                           \
@@ -874,6 +877,7 @@ struct Planes {
     int8_t *hi, *lo;
     int32_t* part;
     uint32_t lines_p, kp, nslab, slices;
+    uint32_t tile = 128;                 // GEMM tile rows when this is the A operand
     size_t bytes() const {
         return (size_t)slices * lines_p * kp * 2 + (size_t)slices * nslab * lines_p * 4 + 1024;
     }
@@ -892,12 +896,20 @@ int run_split(const Src& src, uint64_t src_slice, Planes& pl, hipStream_t s) {
     return CM_OK;
 }
 
-// Tile rows of the GEMM for an A operand of `lines` rows: 256 once there are that many.
-uint32_t gemm_tile_rows(uint32_t lines) { return lines >= 256 ? 256 : 128; }
+// Tile rows of the GEMM for an n x m output of `batch` slices.  A 256-row tile (8 waves, one
+// workgroup per compute unit) has the most operand reuse, but a grid of them that does not
+// fill the compute units in whole rounds leaves most of the last round idle; 128-row tiles
+// (two workgroups per unit) then finish sooner.  Outputs of at most 64 rows take 64-row tiles.
+uint32_t gemm_tile_rows(uint32_t n, uint32_t m, uint32_t batch, uint32_t cus) {
+    if (n <= 64) return 64;
+    if (n <= 128) return 128;
+    const uint64_t tiles = (uint64_t)ceil_div(n, 256) * ceil_div(m, BN) * batch;
+    return (tiles % cus == 0 || tiles >= 4ull * cus) ? 256 : 128;
+}
 
 template <class Epi>
 int run_gemm(const Planes& A, const Planes& B, uint32_t batch, uint32_t k, Epi epi, hipStream_t s) {
-    const uint32_t tm = gemm_tile_rows(A.lines_p);
+    const uint32_t tm = A.tile;
     if (A.lines_p % tm) return fail(CM_EINVAL, "gemm: %u planes rows not a multiple of %u", A.lines_p, tm);
     const uint32_t tiles_r = A.lines_p / tm, tiles_c = B.lines_p / BN;
     const uint64_t a_slice = A.slices > 1 ? (uint64_t)A.lines_p * A.kp : 0;
@@ -908,6 +920,10 @@ int run_gemm(const Planes& A, const Planes& B, uint32_t batch, uint32_t k, Epi e
     const dim3 grid(tiles_r * tiles_c, batch);
     if (tm == 256) {
         CM_LAUNCH("gemm_planes_kernel", (gemm_planes_kernel<4, 3, Epi>), grid, dim3(512), 0, s, A.hi, A.lo, A.part,
+                  a_slice, rp_slice, A.lines_p, B.hi, B.lo, B.part, b_slice, cp_slice, B.lines_p, A.nslab, tiles_r,
+                  tiles_c, A.kp, (int32_t)(64 * k), mode, epi);
+    } else if (tm == 64) {
+        CM_LAUNCH("gemm_planes_kernel", (gemm_planes_kernel<1, 2, Epi>), grid, dim3(128), 0, s, A.hi, A.lo, A.part,
                   a_slice, rp_slice, A.lines_p, B.hi, B.lo, B.part, b_slice, cp_slice, B.lines_p, A.nslab, tiles_r,
                   tiles_c, A.kp, (int32_t)(64 * k), mode, epi);
     } else {
@@ -924,7 +940,56 @@ Planes make_planes(uint32_t lines, uint32_t kp, uint32_t slices, uint32_t align 
     p.kp = kp;
     p.nslab = ceil_div(kp, SLAB);
     p.slices = slices;
+    p.tile = align;
     return p;
+}
+
+}  // namespace
+}  // namespace cm
+
+namespace cm {
+namespace {
+
+int matmul_check(uint32_t k, uint32_t gemv_kw, int64_t a_bs, int64_t b_bs, int64_t c_bs) {
+    // the limb sums HL + LH stay exact in int32 for k <= 32768
+    if (k == 0 || k > 32768) return fail(CM_EINVAL, "matmul: k = %u outside 1 .. 32768", k);
+    if (gemv_kw && gemv_kw != 1 && gemv_kw != 2 && gemv_kw != 4 && gemv_kw != 8)
+        return fail(CM_EINVAL, "matmul: gemv_kw %u", gemv_kw);
+    if (gemv_kw > 1 && (k % (16 * gemv_kw)))
+        return fail(CM_EINVAL, "matmul: k %u not a multiple of 16 * gemv_kw", k);
+    if (a_bs < 0 || b_bs < 0 || c_bs < 0) return fail(CM_EINVAL, "matmul: negative batch stride");
+    return CM_OK;
+}
+
+// A's planes: row-major [n][k] slices at a_slice elements (0: one slice).
+int split_a(const int16_t* a, uint64_t a_slice, uint32_t n, uint32_t k, Planes& A, hipStream_t s) {
+    if (aligned16(a) && (k & 7) == 0 && (a_slice & 7) == 0) {
+        CM_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(A.lines_p / 4, A.nslab, A.slices), dim3(256), 0, s,
+                  a, a_slice, (uint64_t)k, n, k, A.hi, A.lo, A.part, A.lines_p, A.kp, A.nslab);
+        return CM_OK;
+    }
+    return run_split<SrcRowMajor, true>(SrcRowMajor{a, n, k, k}, a_slice, A, s);
+}
+
+// B's planes from its image (row-major, packed 32-column tiles or the GEMV image).
+int split_b(const int16_t* b, uint64_t b_slice, uint32_t k, uint32_t m, uint32_t b_packed, uint32_t gemv_kw,
+            Planes& B, hipStream_t s) {
+    const uint32_t layout = gemv_kw ? 2 : (b_packed ? 1 : 0);
+    const bool fast_b = aligned16(b) && (b_slice & 7) == 0 &&
+                        (layout == 1 || (layout == 0 && (m & 7) == 0) || (layout == 2 && gemv_kw == 1 && (m & 7) == 0));
+    if (fast_b) {
+        CM_LAUNCH("split_cols_kernel", split_cols_kernel, dim3(B.lines_p / 32, B.nslab, B.slices), dim3(256), 0, s,
+                  b, b_slice, layout == 1 ? 1u : 0u, m, k, B.hi, B.lo, B.part, B.lines_p, B.kp, B.nslab);
+        return CM_OK;
+    }
+    return run_split<SrcMatB, false>(SrcMatB{b, m, k, m, layout, gemv_kw}, b_slice, B, s);
+}
+
+int gemm_out(const Planes& A, const Planes& B, int16_t* c, uint32_t n, uint32_t k, uint32_t m, uint32_t batch,
+             int64_t c_bs, uint32_t wrap32, hipStream_t s) {
+    const bool pairs = (reinterpret_cast<uintptr_t>(c) & 3) == 0 && (m & 1) == 0 && (c_bs & 1) == 0;
+    EpiMatmul epi{c, (uint64_t)c_bs, n, m, wrap32 ? 1u : 0u, pairs ? 1u : 0u};
+    return run_gemm(A, B, batch, k, epi, s);
 }
 
 }  // namespace
@@ -938,17 +1003,12 @@ extern "C" int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_
     int rc = state(&st);
     if (rc) return rc;
     if (n == 0 || m == 0 || batch == 0) return CM_OK;
-    // the limb sums HL + LH stay exact in int32 for k <= 32768
-    if (k == 0 || k > 32768) return fail(CM_EINVAL, "matmul: k = %u outside 1 .. 32768", k);
-    if (gemv_kw && gemv_kw != 1 && gemv_kw != 2 && gemv_kw != 4 && gemv_kw != 8)
-        return fail(CM_EINVAL, "matmul: gemv_kw %u", gemv_kw);
-    if (gemv_kw > 1 && (k % (16 * gemv_kw)))
-        return fail(CM_EINVAL, "matmul: k %u not a multiple of 16 * gemv_kw", k);
-    if (a_bs < 0 || b_bs < 0 || c_bs < 0) return fail(CM_EINVAL, "matmul: negative batch stride");
+    rc = matmul_check(k, gemv_kw, a_bs, b_bs, c_bs);
+    if (rc) return rc;
     hipStream_t s = as_stream(stream);
     const uint32_t kp = (uint32_t)round_up(k, BK);
     const uint32_t sa = (batch > 1 && a_bs != 0) ? batch : 1, sb = (batch > 1 && b_bs != 0) ? batch : 1;
-    Planes A = make_planes(n, kp, sa, gemm_tile_rows(n)), B = make_planes(m, kp, sb);
+    Planes A = make_planes(n, kp, sa, gemm_tile_rows(n, m, batch, st->cus)), B = make_planes(m, kp, sb);
     void* ws;
     rc = workspace(st, A.bytes() + B.bytes(), &ws);
     if (rc) return rc;
@@ -956,26 +1016,61 @@ extern "C" int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_
     A.carve(p);
     B.carve(p);
     const uint64_t a_slice = sa > 1 ? (uint64_t)a_bs : 0, b_slice = sb > 1 ? (uint64_t)b_bs : 0;
-    if (aligned16(a) && (k & 7) == 0 && (a_slice & 7) == 0) {
-        CM_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(A.lines_p / 4, A.nslab, A.slices), dim3(256), 0, s,
-                  a, a_slice, (uint64_t)k, n, k, A.hi, A.lo, A.part, A.lines_p, A.kp, A.nslab);
-    } else {
-        rc = run_split<SrcRowMajor, true>(SrcRowMajor{a, n, k, k}, a_slice, A, s);
-    }
+    rc = split_a(a, a_slice, n, k, A, s);
     if (rc) return rc;
-    const uint32_t layout = gemv_kw ? 2 : (b_packed ? 1 : 0);
-    const bool fast_b = aligned16(b) && (b_slice & 7) == 0 &&
-                        (layout == 1 || (layout == 0 && (m & 7) == 0) || (layout == 2 && gemv_kw == 1 && (m & 7) == 0));
-    if (fast_b) {
-        CM_LAUNCH("split_cols_kernel", split_cols_kernel, dim3(B.lines_p / 32, B.nslab, B.slices), dim3(256), 0, s,
-                  b, b_slice, layout == 1 ? 1u : 0u, m, k, B.hi, B.lo, B.part, B.lines_p, B.kp, B.nslab);
-    } else {
-        rc = run_split<SrcMatB, false>(SrcMatB{b, m, k, m, layout, gemv_kw}, b_slice, B, s);
-    }
+    rc = split_b(b, b_slice, k, m, b_packed, gemv_kw, B, s);
     if (rc) return rc;
-    const bool pairs = (reinterpret_cast<uintptr_t>(c) & 3) == 0 && (m & 1) == 0 && (c_bs & 1) == 0;
-    EpiMatmul epi{c, (uint64_t)c_bs, n, m, wrap32 ? 1u : 0u, pairs ? 1u : 0u};
-    return run_gemm(A, B, batch, k, epi, s);
+    return gemm_out(A, B, c, n, k, m, batch, c_bs, wrap32, s);
+}
+
+extern "C" size_t cm_matmul_b_planes_bytes(uint32_t k, uint32_t m, uint32_t b_slices) {
+    using namespace cm;
+    if (k == 0 || m == 0 || b_slices == 0) return 0;
+    return make_planes(m, (uint32_t)round_up(k, BK), b_slices).bytes();
+}
+
+extern "C" int cm_matmul_split_b(const int16_t* b, void* planes, uint32_t k, uint32_t m, uint32_t b_slices,
+                                 int64_t b_bs, uint32_t b_packed, uint32_t gemv_kw, void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    if (m == 0 || b_slices == 0) return CM_OK;
+    rc = matmul_check(k, gemv_kw, 0, b_bs, 0);
+    if (rc) return rc;
+    if (reinterpret_cast<uintptr_t>(planes) & 255) return fail(CM_EALIGN, "matmul: b planes not 256-byte aligned");
+    Planes B = make_planes(m, (uint32_t)round_up(k, BK), b_slices);
+    char* p = static_cast<char*>(planes);
+    B.carve(p);
+    return split_b(b, b_slices > 1 ? (uint64_t)b_bs : 0, k, m, b_packed, gemv_kw, B, as_stream(stream));
+}
+
+extern "C" int cm_matmul_planes(const int16_t* a, const void* b_planes, int16_t* c, uint32_t n, uint32_t k,
+                                uint32_t m, uint32_t batch, int64_t a_bs, uint32_t b_slices, int64_t c_bs,
+                                uint32_t wrap32, void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    if (n == 0 || m == 0 || batch == 0) return CM_OK;
+    rc = matmul_check(k, 0, a_bs, 0, c_bs);
+    if (rc) return rc;
+    if (b_slices != 1 && b_slices != batch) return fail(CM_EINVAL, "matmul: %u b slices for batch %u", b_slices, batch);
+    if (reinterpret_cast<uintptr_t>(b_planes) & 255) return fail(CM_EALIGN, "matmul: b planes not 256-byte aligned");
+    hipStream_t s = as_stream(stream);
+    const uint32_t kp = (uint32_t)round_up(k, BK);
+    const uint32_t sa = (batch > 1 && a_bs != 0) ? batch : 1;
+    Planes A = make_planes(n, kp, sa, gemm_tile_rows(n, m, batch, st->cus)), B = make_planes(m, kp, b_slices);
+    void* ws;
+    rc = workspace(st, A.bytes(), &ws);
+    if (rc) return rc;
+    char* p = static_cast<char*>(ws);
+    A.carve(p);
+    char* q = static_cast<char*>(const_cast<void*>(b_planes));
+    B.carve(q);
+    rc = split_a(a, sa > 1 ? (uint64_t)a_bs : 0, n, k, A, s);
+    if (rc) return rc;
+    return gemm_out(A, B, c, n, k, m, batch, c_bs, wrap32, s);
 }
 
 extern "C" int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
@@ -1053,7 +1148,8 @@ extern "C" int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, 
         return fail(CM_EINVAL, "conv: in_ch * kh * kw = %u above 32768", in_ch * kh * kw);
     const uint32_t kpad = tiles * kh * kw * 16;
     const uint32_t kp = (uint32_t)round_up(kpad, BK);
-    Planes A = make_planes(out_ch, kp, 1, gemm_tile_rows(out_ch)), B = make_planes(plane, kp, batch);
+    Planes A = make_planes(out_ch, kp, 1, gemm_tile_rows(out_ch, plane, batch, st->cus)),
+           B = make_planes(plane, kp, batch);
     void* ws;
     rc = workspace(st, A.bytes() + B.bytes(), &ws);
     if (rc) return rc;

@@ -192,13 +192,14 @@ class Simulator:
             self._check_exponents(at, bt, ot)
         c = self._new(ot, batch * n * m)
         if bt.data is not None and b_batch == 1:
-            # a shared weight: the packed image once (the scheduler's packing)
-            img = self._images.get(bt.onnx_name)
-            if img is None:
+            # a shared weight: the packed image (the scheduler's packing), split once
+            planes = self._images.get(bt.onnx_name)
+            if planes is None:
                 img = torch.from_numpy(pack_matmul_b(b.cpu().numpy().reshape(k, m))).to(self.device)
-                self._images[bt.onnx_name] = img
-            units.matmul(a.reshape(-1), img, c, n, k, m, batch=batch, a_bs=n * k if a_batch > 1 else 0,
-                         b_bs=0, c_bs=n * m, b_packed=1, wrap32=wrap)
+                planes = units.matmul_b_planes(img, k, m, b_packed=1)
+                self._images[bt.onnx_name] = planes
+            units.matmul_planes(a.reshape(-1).contiguous(), planes, c, n, k, m, batch=batch,
+                                a_bs=n * k if a_batch > 1 else 0, c_bs=n * m, wrap32=wrap)
         else:
             units.matmul(a.reshape(-1).contiguous(), b.reshape(-1).contiguous(), c, n, k, m, batch=batch,
                          a_bs=n * k if a_batch > 1 else 0, b_bs=k * m if b_batch > 1 else 0,

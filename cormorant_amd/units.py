@@ -137,6 +137,39 @@ def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, n: int, k: int, m:
     return c
 
 
+def matmul_b_planes(b: torch.Tensor, k: int, m: int, b_slices: int = 1, b_bs: int = 0, b_packed: int = 0,
+                    gemv_kw: int = 0) -> torch.Tensor:
+    """B's split image (cm_matmul_split_b) in a new uint8 device tensor, for matmul_planes."""
+    nbytes = int(_lib.lib().cm_matmul_b_planes_bytes(k, m, b_slices))
+    planes = torch.empty(nbytes + 256, dtype=torch.uint8, device=b.device)
+    off = (-planes.data_ptr()) % 256
+    planes = planes[off:off + nbytes]
+    if b_slices and m:
+        _require(b, "b", torch.int16, (b_slices - 1) * b_bs + matmul_b_extent(k, m, b_packed, gemv_kw))
+    rc = _lib.lib().cm_matmul_split_b(_ptr(b), _ptr(planes), k, m, b_slices, b_bs, int(b_packed), int(gemv_kw),
+                                      _stream())
+    _lib.check(rc, "cm_matmul_split_b")
+    return planes
+
+
+def matmul_planes(a: torch.Tensor, b_planes: torch.Tensor, c: torch.Tensor, n: int, k: int, m: int,
+                  batch: int = 1, a_bs: int = 0, b_slices: int = 1, c_bs: Optional[int] = None,
+                  wrap32: bool = False) -> torch.Tensor:
+    """cm_matmul with B's split image from matmul_b_planes."""
+    if c_bs is None:
+        c_bs = n * m
+    if batch and n and m:
+        _require(a, "a", torch.int16, (batch - 1) * a_bs + n * k)
+        _require(c, "c", torch.int16, (batch - 1) * c_bs + n * m)
+        need = int(_lib.lib().cm_matmul_b_planes_bytes(k, m, b_slices))
+        if b_planes.dtype != torch.uint8 or b_planes.numel() < need or b_planes.data_ptr() % 256:
+            raise ValueError("b_planes: the uint8 image of matmul_b_planes for these k, m, b_slices")
+    rc = _lib.lib().cm_matmul_planes(_ptr(a), _ptr(b_planes), _ptr(c), n, k, m, batch, a_bs, b_slices, c_bs,
+                                     int(bool(wrap32)), _stream())
+    _lib.check(rc, "cm_matmul_planes")
+    return c
+
+
 # ---------------------------------------------------------------- Conv
 def conv_weight_numel(out_ch: int, in_ch: int, kh: int, kw: int, depthwise: bool) -> int:
     """Elements of the packed weight image (ConvKernel.h:142-150)."""

@@ -107,6 +107,19 @@ int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32
               uint32_t m, uint32_t batch, int64_t a_bs, int64_t b_bs, int64_t c_bs,
               uint32_t b_packed, uint32_t gemv_kw, uint32_t wrap32, void* stream);
 
+/* A constant B (a weight read by many calls) split once: cm_matmul_split_b writes B's byte
+ * planes and line sums -- what every cm_matmul call otherwise derives from b on the fly --
+ * into `planes` (cm_matmul_b_planes_bytes(k, m, b_slices) bytes, 256-byte aligned), from the
+ * same b image, layout and b_bs as cm_matmul; cm_matmul_planes then computes exactly
+ * cm_matmul(a, b, c, n, k, m, batch, a_bs, b_slices > 1 ? b_bs : 0, c_bs, ...) with b_slices
+ * 1 (shared) or batch.  No counterpart in the reference's units: a cache of the operand split
+ * that this build's GEMM performs. */
+size_t cm_matmul_b_planes_bytes(uint32_t k, uint32_t m, uint32_t b_slices);
+int cm_matmul_split_b(const int16_t* b, void* planes, uint32_t k, uint32_t m, uint32_t b_slices, int64_t b_bs,
+                      uint32_t b_packed, uint32_t gemv_kw, void* stream);
+int cm_matmul_planes(const int16_t* a, const void* b_planes, int16_t* c, uint32_t n, uint32_t k, uint32_t m,
+                     uint32_t batch, int64_t a_bs, uint32_t b_slices, int64_t c_bs, uint32_t wrap32, void* stream);
+
 /* ---------------------------------------------------------------- Conv
  * Replaces ConvKernel (kernels/conv_rtl/model/include/ConvKernel.h:229-259) and the
  * simulator's Conv branches (_simulate.py:121-220, 643-660, 784-812): NCHW x, packed

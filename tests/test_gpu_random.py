@@ -113,6 +113,32 @@ def test_matmul_random(U, oracle_lib, case):
     assert (got[batch * n * m:] == POISON16).all()
 
 
+@pytest.mark.parametrize("case", [c for c in MM_CASES if c[0] * c[1] * c[2] <= 2 ** 22], ids=lambda c: "n%d_k%d_m%d_b%d_%s%d_%s" % (
+    c[0], c[1], c[2], c[3], c[6], c[7], "wrap" if c[9] else "sat"))
+def test_matmul_planes_equals_matmul(U, case):
+    """B split once (cm_matmul_split_b) then cm_matmul_planes: the same output as cm_matmul,
+    shared and per-slice B, every B image, reused for a second A."""
+    n, k, m, batch, am, bm, layout, kw, full, wrap = case
+    rng = np.random.default_rng(n + k + m + 3)
+    lim = 32768 if full else 2048
+    a_bs = n * k if am else 0
+    bl = [rint16(rng, k * m, -lim, lim) for _ in range(batch if bm else 1)]
+    imgs = [pack_b(x, k, m) for x in bl] if layout == "packed" else (
+        [gemv_image(x, k, m, kw) for x in bl] if layout == "gemv" else bl)
+    b = dev16(np.concatenate(imgs))
+    slices = batch if bm else 1
+    b_bs = len(imgs[0]) if bm else 0
+    planes = U.matmul_b_planes(b, k, m, slices, b_bs, int(layout == "packed"), kw if layout == "gemv" else 0)
+    for rep in range(2):
+        a = dev16(rint16(rng, max(batch - 1, 0) * a_bs + n * k, -lim, lim))
+        want = poisoned16(batch * n * m + 8)
+        U.matmul(a, b, want, n, k, m, batch, a_bs, b_bs, n * m, int(layout == "packed"),
+                 kw if layout == "gemv" else 0, wrap)
+        got = poisoned16(batch * n * m + 8)
+        U.matmul_planes(a, planes, got, n, k, m, batch, a_bs, slices, n * m, wrap)
+        np.testing.assert_array_equal(host(got), host(want))
+
+
 def test_matmul_q88_saturates_where_int32_would_wrap(U, oracle_lib):
     """acc = 16 * 32767^2 exceeds int32: the Q8.8 path saturates the true sum, the
     power-of-two path wraps it (_simulate.py:620-633 vs 814-835; test_numeric.py:148-184)."""
