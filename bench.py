@@ -165,9 +165,9 @@ def hbm_kernels(torch, units, reps: int = 20):
                            is_depthwise=1))
     # row-ops jobs on contiguous rows (one broadcast parameter entry)
     p0 = torch.zeros(16, dtype=torch.uint8, device=dev)
-    def rowjob(name, rows, n, op, ak, ck, bk=None, aux=0, nbytes=None, rope_hd=0):
+    def rowjob(name, rows, n, op, ak, ck, bk=None, aux=0, nbytes=None, rope_hd=0, a32_range=2 ** 30, per_col=False):
         kb = {units.K_I16: 2, units.K_I32: 4, units.K_F32: 4}
-        a = i32(rows * n) if ak == units.K_I32 else i16(rows * n, -4096, 4096)
+        a = i32(rows * n, -a32_range, a32_range) if ak == units.K_I32 else i16(rows * n, -4096, 4096)
         b, b_s1 = None, 0
         if rope_hd:                       # one cos / sin position row (2 HD int32) per row
             b, b_s1 = i32(rows * 2 * rope_hd, -2 ** 23, 2 ** 23), 8 * rope_hd
@@ -175,16 +175,24 @@ def hbm_kernels(torch, units, reps: int = 20):
             b = i32(rows * n) if bk == units.K_I32 else i16(rows * n, -4096, 4096)
             b_s1 = kb[bk] * n
         c = torch.empty(rows * n * kb[ck], dtype=torch.uint8, device=dev)
-        opw = op | (ak << 4) | ((bk or 0) << 6) | (ck << 8) | units.F_P_BCAST | (units.F_B_EN if bk is not None else 0)
-        run(name, [rows, n], nbytes, lambda: units.rowops(u8(a), u8(b) if b is not None else None, c, p0, opw, n,
+        opw = op | (ak << 4) | ((bk or 0) << 6) | (ck << 8) | (units.F_B_EN if bk is not None else 0)
+        p = torch.zeros(16 * n, dtype=torch.uint8, device=dev) if per_col else p0
+        opw |= 0 if per_col else units.F_P_BCAST
+        run(name, [rows, n], nbytes, lambda: units.rowops(u8(a), u8(b) if b is not None else None, c, p, opw, n,
                                                            rows, 1, kb[ak] * n, 0, b_s1, 0, kb[ck] * n, 0, 1 << 20,
                                                            aux, 0))
+    # norm inputs in a residual stream's range (|x| < 2^20, 32 at 2^-15)
     rowjob("ro_norm_kernel LayerNorm i32->i16 (BERT)", 3072 * 8, 768, units.RO_NORM | units.F_NORM_LN, units.K_I32,
-           units.K_I16, nbytes=6 * 3072 * 8 * 768)
+           units.K_I16, nbytes=6 * 3072 * 8 * 768, a32_range=2 ** 20)
+    rowjob("ro_norm_kernel LayerNorm i32->i16 (BERT, one forward's 3072 rows, per-column G / B)", 3072, 768,
+           units.RO_NORM | units.F_NORM_LN, units.K_I32, units.K_I16, nbytes=6 * 3072 * 768, a32_range=2 ** 20,
+           per_col=True)
     rowjob("ro_norm_kernel RMSNorm i32->i16 (SmolLM2 rows)", 16384, 960, units.RO_NORM, units.K_I32, units.K_I16,
-           nbytes=6 * 16384 * 960)
+           nbytes=6 * 16384 * 960, a32_range=2 ** 20)
     rowjob("ro_stream_kernel ADDX i32+i16->i32", 3072 * 8, 768, units.RO_ADDX, units.K_I32, units.K_I32,
            bk=units.K_I16, nbytes=10 * 3072 * 8 * 768)
+    rowjob("ro_stream_kernel ADDX i32+i16->i32 (BERT residual, 3072 rows, per-column bias)", 3072, 768, units.RO_ADDX,
+           units.K_I32, units.K_I32, bk=units.K_I16, nbytes=10 * 3072 * 768, per_col=True)
     rowjob("ro_stream_kernel MULACT (SiLU x up)", 8192, 2560, units.RO_MULACT, units.K_I16, units.K_I16,
            bk=units.K_I16, nbytes=6 * 8192 * 2560)
     rowjob("ro_stream_kernel DEQUANT i16->f32 (logits)", 4096, 4096, units.RO_DEQUANT, units.K_I16, units.K_F32,

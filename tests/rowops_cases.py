@@ -24,6 +24,14 @@ RO_CASES = [  # label, op word, n, rows, blocks, kinds (a, b, c bytes), param ra
     ("norm_ln_i16", 5 | (1 << 16), 768, 7, 1),
     ("norm_ln_i32_4096", 5 | (1 << 4) | (1 << 16), 4096, 2, 1),
     ("rope_hd64", 6 | (2 << 6), 320, 4, 1),
+    # rows of whole 8-element units (the 16-byte kernels): COPY from int32, ADDX with an int32 B,
+    # the scale flag (128-bit path), broadcast parameters with relu, LN / RMS over 8 .. 2048 lanes
+    ("copy_i32_i16_u8", 1 | (1 << 4) | (1 << 12), 256, 3, 2),
+    ("addx_i16_i32_i32_u8", 2 | (1 << 6) | (1 << 8) | (1 << 12), 512, 4, 2),
+    ("copy_scale_u8", 1 | (1 << 17), 264, 3, 1),
+    ("addx_relu_bcast_u8", 2 | (1 << 12) | (1 << 13) | (1 << 15), 104, 4, 3),
+    ("norm_ln_i16_64", 5 | (1 << 16), 64, 9, 1),
+    ("norm_rms_i16_2048", 5, 2048, 3, 1),
 ]
 
 
