@@ -202,53 +202,44 @@ def hbm_kernels(torch, units, reps: int = 20):
     return lines
 
 
-# ---------------------------------------------------------------- config 4: BERT-base L384
-BERT_KERNELS = ("gemm_planes_kernel", "split_rows_kernel", "split_cols_kernel", "split_kernel",
-                "softmax_cols_kernel", "ro_norm_kernel", "ro_stream_kernel", "vectorop_kernel",
-                "permute_words_kernel", "permute_tile_kernel")
+# ---------------------------------------------------------------- graph workloads
+GRAPH_KERNELS = ("gemm_planes_kernel", "split_rows_kernel", "split_cols_kernel", "split_kernel",
+                 "softmax_cols_kernel", "softmax_rows_kernel", "ro_norm_kernel", "ro_stream_kernel",
+                 "vectorop_kernel", "permute_words_kernel", "permute_tile_kernel", "conv_dw_kernel",
+                 "conv_dw3_kernel", "conv_dw3v_kernel", "pool_kernel", "pool_global_kernel", "pool2x2_kernel",
+                 "softmax_long_kernel", "smx_etab_kernel")
 
 
-def bert_bench(args, torch, np):
-    """One step = one forward of the 12-layer encoder over the batch of 8 x 384 tokens, the
-    int32 residual input resident on the GPU, replayed as a captured HIP graph."""
-    from cormorant_amd import _lib, models
-    from cormorant_amd.simulate import Simulator
-
-    shape = models.BertShape()
-    t0 = time.time()
-    g, inputs, exps = models.bert_encoder(shape, seed=args.seed)
-    build_s = time.time() - t0
-    sim = Simulator(g)
-    out_name = g.output_tensors[0].onnx_name
-    h0 = sim._to_device(sim._tensor("h0"), inputs["h0"])
+def run_graph(args, torch, sim, feeds, out_name):
+    """Warm the simulator up, time every launch of one eager forward (per-kernel times), then
+    capture the forward as a HIP graph and time ``args.steps`` replays after ``args.warmup``.
+    Returns (ms per step, {kernel: {ms, launches}}, the output tensor of the graph)."""
+    from cormorant_amd import _lib
     for _ in range(2):                        # weights, packed images, tables, workspace
-        sim.forward_raw({"h0": h0})
+        sim.forward_raw(feeds)
     torch.cuda.synchronize()
-
-    # per-kernel times of one forward (eager, every launch timed)
     _lib.timing_reset()
     _lib.timing_select("")
     _lib.timing_enable(True)
-    sim.forward_raw({"h0": h0})
+    sim.forward_raw(feeds)
     torch.cuda.synchronize()
     _lib.timing_enable(False)
     per_kernel = {}
-    for k in BERT_KERNELS:
+    for k in GRAPH_KERNELS:
         ms_k, n_k = _lib.timing_read(k)
         if n_k:
             per_kernel[k] = {"ms": round(ms_k, 4), "launches": n_k}
     _lib.timing_reset()
 
-    # the step as a HIP graph
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        sim.forward_raw({"h0": h0})
+        sim.forward_raw(feeds)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     hg = torch.cuda.CUDAGraph()
     with torch.cuda.graph(hg):
-        out = sim.forward_raw({"h0": h0})[out_name]
+        out = sim.forward_raw(feeds)[out_name]
     for _ in range(args.warmup):
         hg.replay()
     torch.cuda.synchronize()
@@ -258,23 +249,48 @@ def bert_bench(args, torch, np):
         hg.replay()
     stop.record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(stop) / args.steps
-    macs = shape.macs()
-    gemm_ms = per_kernel.get("gemm_planes_kernel", {}).get("ms", float("nan"))
+    return start.elapsed_time(stop) / args.steps, per_kernel, out
+
+
+def step_fields(args, ms):
+    return {"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int16"}
+
+
+def gemm_roofline(per_kernel, macs):
+    gemm_ms = per_kernel.get(GEMM_KERNEL, {}).get("ms", float("nan"))
     achieved = 8.0 * macs / (gemm_ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(achieved, 1), "peak": I8_PEAK_TOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / I8_PEAK_TOPS, 4), "traffic": None, "kernel": GEMM_KERNEL,
+            "kernel_ms_per_step": gemm_ms, "ops_per_step": 8 * macs}
+
+
+def cores():
+    return len(os.sched_getaffinity(0))
+
+
+# ---------------------------------------------------------------- config 4: BERT-base L384
+def bert_bench(args, torch, np):
+    """One step = one forward of the 12-layer encoder over the batch of 8 x 384 tokens, the
+    int32 residual input resident on the GPU, replayed as a captured HIP graph."""
+    from cormorant_amd import models
+    from cormorant_amd.simulate import Simulator
+
+    shape = models.BertShape()
+    t0 = time.time()
+    g, inputs, exps = models.bert_encoder(shape, seed=args.seed)
+    build_s = time.time() - t0
+    sim = Simulator(g)
+    out_name = g.output_tensors[0].onnx_name
+    h0 = sim._to_device(sim._tensor("h0"), inputs["h0"])
+    ms, per_kernel, out = run_graph(args, torch, sim, {"h0": h0}, out_name)
+    macs = shape.macs()
     result = {
         "metric": "bit-exact fixed-point GMAC/s + inferences/s (BERT-base L384) vs CPU simulator",
         "value": round(macs / (ms * 1e-3) / 1e9, 1),
         "unit": "GMAC/s",
         "inferences_per_s": round(shape.batch / (ms * 1e-3), 1),
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int16",
+        **step_fields(args, ms),
         "data": f"synthetic (seed {args.seed}): token ids U(0, 30522), embedding rows N(0,1), weights / "
                 "biases N(0,0.02), LayerNorm gamma N(1,0.02), beta N(0,0.02); per-tensor pow2 exponents "
                 "from a float64 calibration of the first sequence",
@@ -282,9 +298,7 @@ def bert_bench(args, torch, np):
                                "768, 12 heads x 64, FFN 3072 GELU(erf), pre-LN on an int32 residual at 2^-15",
                    "layers": shape.layers, "batch": shape.batch, "seq": shape.seq, "hidden": shape.d,
                    "heads": shape.heads, "ffn": shape.ff, "macs_per_step": macs},
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": I8_PEAK_TOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / I8_PEAK_TOPS, 4), "traffic": None, "kernel": GEMM_KERNEL,
-                     "kernel_ms_per_step": gemm_ms, "ops_per_step": 8 * macs},
+        "roofline": gemm_roofline(per_kernel, macs),
         "kernels_ms_per_step": per_kernel,
         "graph_build_s": round(build_s, 1),
     }
@@ -297,13 +311,106 @@ def bert_bench(args, torch, np):
         dt = time.time() - t1
         got = sim._to_values(sim._tensor(out_name), out)[:shape.seq]
         result["cpu_baseline"] = {"value": round(one.macs() / dt / 1e9, 2), "unit": "GMAC/s",
-                                  "cores": len(os.sched_getaffinity(0)), "kind": "port",
+                                  "cores": cores(), "kind": "port",
                                   "sample": f"sequence 0 through all 12 layers ({one.macs() / 1e9:.1f} GMAC) in "
                                             f"{dt:.1f} s: the reference simulator's algorithms restated "
                                             "(float64 BLAS contractions, the C oracle's softmax / row-ops / "
                                             "activation unit)"}
         result["parity"] = ("sequence 0's output bit-exact vs the CPU simulator algorithm"
                             if exps1 == exps and np.array_equal(got, want.reshape(got.shape))
+                            else "MISMATCH vs the CPU simulator algorithm")
+    print(json.dumps(result), flush=True)
+
+
+# ---------------------------------------------------------------- config 3: MobileNetV2, batch 32
+def mobilenet_bench(args, torch, np):
+    """One step = one forward of MobileNetV2 1.0 over 32 images of 3 x 224 x 224 (Q8.8), the
+    input resident on the GPU, replayed as a captured HIP graph."""
+    from cormorant_amd import models
+    from cormorant_amd.simulate import Simulator
+
+    batch = 32
+    g, inputs, macs = models.mobilenet_v2(batch=batch, seed=args.seed)
+    sim = Simulator(g)
+    out_name = g.output_tensors[0].onnx_name
+    x = sim._to_device(sim._tensor("input"), inputs["input"])
+    ms, per_kernel, out = run_graph(args, torch, sim, {"input": x}, out_name)
+    result = {
+        "metric": "bit-exact fixed-point images/s (MobileNetV2 batch 32, 224x224, Q8.8)",
+        "value": round(batch / (ms * 1e-3), 1),
+        "unit": "images/s",
+        "gmacs_per_s": round(macs / (ms * 1e-3) / 1e9, 1),
+        **step_fields(args, ms),
+        "data": f"synthetic (seed {args.seed}): input U[0,1), He-normal weights, every tensor Q8.8 (RNE, saturated)",
+        "config": {"workload": "MobileNetV2 1.0 forward, batch 32 x 3 x 224 x 224, 17 inverted residual blocks, "
+                               "1x1 320->1280, global average pool, 1280x1000 classifier",
+                   "batch": batch, "res": 224, "macs_per_step": macs},
+        "kernels_ms_per_step": per_kernel,
+    }
+    # the GEMM's share of the MACs: standard / pointwise convolutions and the classifier
+    dw_macs = sum(sn.batch * sn.out_ch * sn.out_h * sn.out_w * sn.kh * sn.kw for sn in g.nodes
+                  if type(sn).__name__ == "ConvNode" and sn.is_depthwise)
+    result["roofline"] = gemm_roofline(per_kernel, macs - dw_macs)
+    result["roofline"]["macs_on_mfma"] = macs - dw_macs
+    if not args.no_cpu_baseline:
+        from oracle import graph_sim
+        g1, in1, macs1 = models.mobilenet_v2(batch=1, seed=args.seed)
+        reps, t1 = 0, time.time()
+        while reps == 0 or time.time() - t1 < 10.0:
+            want = graph_sim.forward(g1, in1)[out_name]
+            reps += 1
+        dt = (time.time() - t1) / reps
+        got = sim._to_values(sim._tensor(out_name), out)[:1]
+        result["cpu_baseline"] = {"value": round(1.0 / dt, 2), "unit": "images/s", "cores": cores(),
+                                  "kind": "port",
+                                  "sample": f"image 0 ({macs1 / 1e6:.0f} M MAC) {reps} times in {dt * reps:.1f} s: "
+                                            "the reference simulator's algorithms restated (float64 im2col "
+                                            "contractions, the C oracle's pooling / VectorOP)"}
+        result["parity"] = ("image 0's logits bit-exact vs the CPU simulator algorithm"
+                            if np.array_equal(got, want.reshape(got.shape))
+                            else "MISMATCH vs the CPU simulator algorithm")
+    print(json.dumps(result), flush=True)
+
+
+# ---------------------------------------------------------------- config 1: small CNN, batch 1
+def cnn_bench(args, torch, np):
+    """One step = one forward of the small CNN (batch 1, 28 x 28, Q8.8): latency-bound, so
+    the figure is inferences/s of the replayed graph."""
+    from cormorant_amd import models
+    from cormorant_amd.simulate import Simulator
+
+    g, inputs = models.small_cnn(args.seed)
+    macs = 290080
+    sim = Simulator(g)
+    out_name = g.output_tensors[0].onnx_name
+    x = sim._to_device(sim._tensor("input"), inputs["input"])
+    ms, per_kernel, out = run_graph(args, torch, sim, {"input": x}, out_name)
+    result = {
+        "metric": "bit-exact fixed-point inferences/s (small CNN, batch 1, Q8.8)",
+        "value": round(1.0 / (ms * 1e-3), 1),
+        "unit": "inferences/s",
+        "us_per_inference": round(ms * 1e3, 2),
+        **step_fields(args, ms),
+        "data": f"synthetic (seed {args.seed}): input U[0,1), weights U(+-0.25), biases U(+-0.1), Q8.8",
+        "config": {"workload": "small CNN forward, batch 1: Conv3x3 1->8 + RELU + MaxPool, Conv3x3 8->16 + RELU "
+                               "+ MaxPool, MatMul 784x10 + bias, Softmax", "batch": 1, "macs_per_step": macs},
+        "roofline": gemm_roofline(per_kernel, macs),
+        "kernels_ms_per_step": per_kernel,
+    }
+    result["roofline"]["note"] = "latency-bound: the fraction is not meaningful at 290 k MAC"
+    if not args.no_cpu_baseline:
+        from oracle import graph_sim
+        reps, t1 = 0, time.time()
+        while reps == 0 or time.time() - t1 < 10.0:
+            want = graph_sim.forward(g, inputs)[out_name]
+            reps += 1
+        dt = (time.time() - t1) / reps
+        got = sim._to_values(sim._tensor(out_name), out)
+        result["cpu_baseline"] = {"value": round(1.0 / dt, 1), "unit": "inferences/s", "cores": cores(),
+                                  "kind": "port",
+                                  "sample": f"the whole forward {reps} times in {dt * reps:.1f} s"}
+        result["parity"] = ("output bit-exact vs the CPU simulator algorithm"
+                            if np.array_equal(got, want.reshape(got.shape))
                             else "MISMATCH vs the CPU simulator algorithm")
     print(json.dumps(result), flush=True)
 
@@ -320,9 +427,10 @@ def main():
     ap.add_argument("--hbm", action="store_true",
                     help="measure the HBM-bound units (VectorOP, softmax, pooling, depthwise conv, "
                          "row-ops) against the 8 TB/s roofline instead of the matmul step")
-    ap.add_argument("--config", default="bert", choices=["bert", "matmul"],
+    ap.add_argument("--config", default="bert", choices=["bert", "matmul", "mobilenet", "cnn"],
                     help="bert: config 4, the BERT-base L384 encoder forward (the headline metric); "
-                         "matmul: config 2, the batched Q8.8 MatMul")
+                         "matmul: config 2, the batched Q8.8 MatMul; mobilenet: config 3, MobileNetV2 "
+                         "batch 32; cnn: config 1, the small CNN at batch 1")
     ap.add_argument("--calibrate", action="store_true",
                     help="run only the copy used to scale HBM counters: a RELU over 256 MiB of "
                          "non-negative int16 (reads and writes exactly 256 MiB each)")
@@ -344,6 +452,12 @@ def main():
         return
     if args.config == "bert":
         bert_bench(args, torch, np)
+        return
+    if args.config == "mobilenet":
+        mobilenet_bench(args, torch, np)
+        return
+    if args.config == "cnn":
+        cnn_bench(args, torch, np)
         return
     a, b, bp = make_inputs(args.seed)
     dev = torch.device("cuda:0")

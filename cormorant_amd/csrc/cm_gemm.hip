@@ -312,10 +312,107 @@ __global__ __launch_bounds__(256) void split_cols_kernel(const int16_t* __restri
             csum[0][threadIdx.x] + csum[1][threadIdx.x] + csum[2][threadIdx.x] + csum[3][threadIdx.x];
 }
 
+// 1x1 stride-1 convolutions with the images folded into the GEMM's columns: line
+// j = img * plane + p is pixel p of image img, k the input channel, B(c, j) = x[img][c][p].
+// For planes that are not a multiple of 8 pixels.  A workgroup takes 64 lines and one SLAB
+// of k, each of its waves (up to 16) 64 k in 16-k chunks: lane = line, 16 loads of 2 bytes
+// (the 64 lanes of one load read 128 consecutive bytes of one channel row where the lines
+// stay in one image), packed into one 16-byte word per plane.  Grid (lines_p / 64, nslab).
+__global__ __launch_bounds__(1024) void split_fold_kernel(const int16_t* __restrict__ x, uint32_t in_ch,
+                                                          uint32_t plane, uint64_t img_elems, uint32_t cols,
+                                                          int8_t* __restrict__ hi, int8_t* __restrict__ lo,
+                                                          int32_t* __restrict__ part, uint32_t lines_p, uint32_t kp) {
+    __shared__ int32_t wsum[16][64];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    const uint32_t j = blockIdx.x * 64 + lane, slab = blockIdx.y;
+    const bool real = j < cols;
+    const uint32_t img = real ? j / plane : 0, p = real ? j - img * plane : 0;
+    const int16_t* src = x + img * img_elems + p;
+    int32_t sum = 0;
+    const uint32_t kb = slab * SLAB + 64 * wave, ke = min(kb + 64, kp);
+#pragma unroll 2
+    for (uint32_t k0 = kb; k0 < ke; k0 += 16) {
+        int16_t e[16];
+        if (real && k0 + 16 <= in_ch) {
+#pragma unroll
+            for (int q = 0; q < 16; q++) e[q] = src[(uint64_t)(k0 + q) * plane];
+#pragma unroll
+            for (int q = 0; q < 16; q++) sum += e[q];
+        } else {
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const bool r = real && k0 + q < in_ch;
+                e[q] = r ? src[(uint64_t)(k0 + q) * plane] : kPad;
+                sum += r ? e[q] : 0;
+            }
+        }
+        uint2 h0, l0, h1, l1;
+        split8(*reinterpret_cast<const int4*>(e), h0, l0);
+        split8(*reinterpret_cast<const int4*>(e + 8), h1, l1);
+        const uint64_t off = (uint64_t)j * kp + k0;
+        *reinterpret_cast<uint4*>(hi + off) = make_uint4(h0.x, h0.y, h1.x, h1.y);
+        *reinterpret_cast<uint4*>(lo + off) = make_uint4(l0.x, l0.y, l1.x, l1.y);
+    }
+    wsum[wave][lane] = sum;
+    __syncthreads();
+    if (wave == 0) {
+        int32_t t = 0;
+        for (uint32_t w = 0; w < waves; w++) t += wsum[w][lane];
+        part[(uint64_t)slab * lines_p + j] = t;
+    }
+}
+
+// The same operand for planes with many lines: a workgroup takes 64 lines and one SLAB of
+// k in 64 x 64 tiles through LDS.  Thread t loads line t % 64 at 16 k (2-byte loads, the 64
+// lanes of one load on consecutive lines), then packs 16 consecutive k of line t / 4 into
+// 16-byte words: the four threads of a line write 64 contiguous bytes of each plane.
+// Grid (lines_p / 64, nslab).
+__global__ __launch_bounds__(256) void split_fold_lds_kernel(const int16_t* __restrict__ x, uint32_t in_ch,
+                                                             uint32_t plane, uint64_t img_elems, uint32_t cols,
+                                                             int8_t* __restrict__ hi, int8_t* __restrict__ lo,
+                                                             int32_t* __restrict__ part, uint32_t lines_p,
+                                                             uint32_t kp) {
+    __shared__ int16_t tile[64][64 + 2];
+    const uint32_t t = threadIdx.x, la = t & 63, kr = t >> 6;
+    const uint32_t l0 = blockIdx.x * 64, slab = blockIdx.y;
+    const uint32_t ja = l0 + la;
+    const bool real_a = ja < cols;
+    const uint32_t img = real_a ? ja / plane : 0, pa = real_a ? ja - img * plane : 0;
+    const int16_t* src = x + img * img_elems + pa;
+    const uint32_t my_line = t >> 2, part_k = (t & 3) * 16;
+    int32_t sum = 0;
+    const uint32_t k_end = min(kp, (slab + 1) * SLAB);
+    for (uint32_t k0 = slab * SLAB; k0 < k_end; k0 += 64) {
+#pragma unroll
+        for (uint32_t r = 0; r < 16; r++) {
+            const uint32_t kk = k0 + 4 * r + kr;
+            tile[la][4 * r + kr] = (real_a && kk < in_ch) ? src[(uint64_t)kk * plane] : kPad;
+        }
+        __syncthreads();
+        int16_t e[16];
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            e[q] = tile[my_line][part_k + q];
+            sum += (l0 + my_line < cols && k0 + part_k + q < in_ch) ? e[q] : 0;
+        }
+        uint2 h0, lw0, h1, lw1;
+        split8(*reinterpret_cast<const int4*>(e), h0, lw0);
+        split8(*reinterpret_cast<const int4*>(e + 8), h1, lw1);
+        const uint64_t off = (uint64_t)(l0 + my_line) * kp + k0 + part_k;
+        *reinterpret_cast<uint4*>(hi + off) = make_uint4(h0.x, h0.y, h1.x, h1.y);
+        *reinterpret_cast<uint4*>(lo + off) = make_uint4(lw0.x, lw0.y, lw1.x, lw1.y);
+        __syncthreads();
+    }
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    if ((t & 3) == 0) part[(uint64_t)slab * lines_p + l0 + my_line] = sum;
+}
+
 // ---------------------------------------------------------------- epilogues
 // An epilogue names where output row `i` of slice `bt` starts (nullptr past the last row),
-// the raw per-row bias (added to the sum as bias << 8), and whether every row start and the
-// column count are even (then two adjacent results go out as one 4-byte store).
+// the raw per-row bias (added to the sum as bias << 8), the offset of column `j` from a row
+// start, and whether every row start and the column count are even (then two adjacent
+// results go out as one 4-byte store).
 struct EpiMatmul {              // C[bt][i][j] = c + bt * c_bs + i * m + j
     int16_t* c;
     uint64_t c_bs;
@@ -324,17 +421,24 @@ struct EpiMatmul {              // C[bt][i][j] = c + bt * c_bs + i * m + j
     __device__ int16_t* row_ptr(uint32_t bt, uint32_t i) const {
         return i < rows ? c + bt * c_bs + (uint64_t)i * cols : nullptr;
     }
+    __device__ uint64_t col_off(uint32_t j) const { return j; }
 };
 struct EpiConv {                // y pattern (ConvKernel.h:250-258); acc seeded with bias << 8
     int16_t* y;
     const int16_t* bias;
     uint64_t img;               // elements per image (out_ch * plane)
     uint32_t rows, cols, cs, cn, gs, wrap, pairs;
+    uint32_t fold;              // pixels per image when the images are folded into the columns, else 0
     __device__ int32_t row_bias(uint32_t i) const { return bias && i < rows ? (int32_t)bias[i] : 0; }
     __device__ int16_t* row_ptr(uint32_t bt, uint32_t i) const {
         if (i >= rows) return nullptr;
         const uint64_t base = cn ? (uint64_t)(i % cn) * cs + (uint64_t)(i / cn) * gs : (uint64_t)i * cs;
         return y + bt * img + base;
+    }
+    __device__ uint64_t col_off(uint32_t j) const {
+        if (!fold) return j;
+        const uint32_t im = j / fold;
+        return (uint64_t)im * img + (j - im * fold);
     }
 };
 
@@ -402,12 +506,13 @@ __device__ __forceinline__ void store_wave_tile(const v16i (&hh)[2][2], const v1
                     const uint32_t hi = (uint32_t)(odd ? q1 : got) << 16;
                     int16_t* dst = epi.row_ptr(bt, row0 + rl + odd);
                     if (dst != nullptr && col - odd < epi.cols)
-                        *reinterpret_cast<uint32_t*>(dst + col - odd) = lo | hi;
+                        *reinterpret_cast<uint32_t*>(dst + epi.col_off(col - odd)) = lo | hi;
                 } else if (col < epi.cols) {
                     int16_t* d0 = epi.row_ptr(bt, row0 + rl);
                     int16_t* d1 = epi.row_ptr(bt, row0 + rl + 1);
-                    if (d0 != nullptr) d0[col] = (int16_t)q0;
-                    if (d1 != nullptr) d1[col] = (int16_t)q1;
+                    const uint64_t co = epi.col_off(col);
+                    if (d0 != nullptr) d0[co] = (int16_t)q0;
+                    if (d1 != nullptr) d1[co] = (int16_t)q1;
                 }
                 // one row pair at a time: hoisting the term loads of later pairs would
                 // need more registers than the accumulators leave
@@ -878,6 +983,7 @@ struct Planes {
     int32_t* part;
     uint32_t lines_p, kp, nslab, slices;
     uint32_t tile = 128;                 // GEMM tile rows when this is the A operand
+    uint32_t rows = 0;                   // real lines (the rest up to lines_p are padding)
     size_t bytes() const {
         return (size_t)slices * lines_p * kp * 2 + (size_t)slices * nslab * lines_p * 4 + 1024;
     }
@@ -910,8 +1016,9 @@ uint32_t gemm_tile_rows(uint32_t n, uint32_t m, uint32_t batch, uint32_t cus) {
 template <class Epi>
 int run_gemm(const Planes& A, const Planes& B, uint32_t batch, uint32_t k, Epi epi, hipStream_t s) {
     const uint32_t tm = A.tile;
-    if (A.lines_p % tm) return fail(CM_EINVAL, "gemm: %u planes rows not a multiple of %u", A.lines_p, tm);
-    const uint32_t tiles_r = A.lines_p / tm, tiles_c = B.lines_p / BN;
+    const uint32_t tiles_r = ceil_div(A.rows, tm), tiles_c = B.lines_p / BN;
+    if (tm != 64 && tm != 128 && tm != 256) return fail(CM_EINVAL, "gemm: tile rows %u", tm);
+    if ((uint64_t)tiles_r * tm > A.lines_p) return fail(CM_EINVAL, "gemm: %u tile rows past %u plane rows", tm, A.lines_p);
     const uint64_t a_slice = A.slices > 1 ? (uint64_t)A.lines_p * A.kp : 0;
     const uint64_t b_slice = B.slices > 1 ? (uint64_t)B.lines_p * B.kp : 0;
     const uint64_t rp_slice = A.slices > 1 ? (uint64_t)A.nslab * A.lines_p : 0;
@@ -937,6 +1044,7 @@ int run_gemm(const Planes& A, const Planes& B, uint32_t batch, uint32_t k, Epi e
 Planes make_planes(uint32_t lines, uint32_t kp, uint32_t slices, uint32_t align = 128) {
     Planes p{};
     p.lines_p = (uint32_t)round_up(lines, align);
+    p.rows = lines;
     p.kp = kp;
     p.nslab = ceil_div(kp, SLAB);
     p.slices = slices;
@@ -1073,6 +1181,76 @@ extern "C" int cm_matmul_planes(const int16_t* a, const void* b_planes, int16_t*
     return gemm_out(A, B, c, n, k, m, batch, c_bs, wrap32, s);
 }
 
+namespace cm {
+namespace {
+
+struct ConvGeom {
+    uint32_t batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, sh, sw, dh, dw, pt, pl;
+    uint32_t cs, cn, gs, wrap;          // the y pattern (cs = plane without one), int32 wrap
+    uint32_t plane() const { return out_h * out_w; }
+    // 1x1 stride-1 unpadded, same plane in and out, no y pattern: the images fold into the
+    // GEMM's columns (one slice of batch * plane lines)
+    bool fold() const {
+        return kh == 1 && kw == 1 && sh == 1 && sw == 1 && pt == 0 && pl == 0 && out_h == in_h && out_w == in_w &&
+               cn == 0 && cs == plane() && (uint64_t)batch * plane() < ((uint64_t)1 << 31);
+    }
+};
+
+// k of the GEMM: 16-channel tiles x kernel positions (the packed weight order), in BK steps.
+uint32_t conv_kp(uint32_t in_ch, uint32_t kh, uint32_t kw) {
+    return (uint32_t)round_up((uint64_t)((in_ch + 15) / 16) * kh * kw * 16, BK);
+}
+
+Planes conv_b_planes(const ConvGeom& g, uint32_t kp) {
+    return g.fold() ? make_planes(g.batch * g.plane(), kp, 1) : make_planes(g.plane(), kp, g.batch);
+}
+
+uint32_t conv_tile(const ConvGeom& g, const Planes& B, const DeviceState* st) {
+    return gemm_tile_rows(g.out_ch, B.rows, B.slices, st->cus);
+}
+
+// The weights' planes: rows = output channels in the packed tile-major order (ConvKernel.h:136-159).
+int conv_split_w(const int16_t* w, Planes& A, uint32_t out_ch, uint32_t in_ch, uint32_t kh, uint32_t kw,
+                 hipStream_t s) {
+    const uint32_t tiles = (in_ch + 15) / 16;
+    const uint32_t rem = in_ch - (tiles - 1) * 16, last = rem <= 8 ? 8 : 16;
+    const uint32_t per_m = kh * kw * ((tiles - 1) * 16 + last);
+    return run_split<SrcConvW, true>(SrcConvW{w, out_ch, in_ch, kh, kw, tiles, per_m, last}, 0, A, s);
+}
+
+// The input's planes (im2col, or the folded 1x1 form) and the GEMM with the weights' planes A.
+int conv_gemm(const int16_t* x, const Planes& A, Planes& B, const int16_t* bptr, int16_t* y, const ConvGeom& g,
+              const DeviceState* st, hipStream_t s) {
+    const uint32_t plane = g.plane();
+    const uint64_t img = (uint64_t)g.out_ch * plane;
+    if (g.fold()) {
+        const uint32_t cols = g.batch * plane;
+        if (B.lines_p / 64 >= 4 * st->cus) {
+            // lines enough for the workgroups of whole slabs to fill the chip
+            CM_LAUNCH("split_fold_kernel", split_fold_lds_kernel, dim3(B.lines_p / 64, B.nslab), dim3(256), 0, s, x,
+                      g.in_ch, plane, (uint64_t)g.in_ch * plane, cols, B.hi, B.lo, B.part, B.lines_p, B.kp);
+        } else {
+            // one wave per 64 k of the slab
+            const uint32_t waves = std::min<uint32_t>(16, ceil_div(std::min<uint32_t>(B.kp, SLAB), 64));
+            CM_LAUNCH("split_fold_kernel", split_fold_kernel, dim3(B.lines_p / 64, B.nslab), dim3(64 * waves), 0, s,
+                      x, g.in_ch, plane, (uint64_t)g.in_ch * plane, cols, B.hi, B.lo, B.part, B.lines_p, B.kp);
+        }
+        const bool pairs = (reinterpret_cast<uintptr_t>(y) & 3) == 0 && (plane & 1) == 0;
+        EpiConv epi{y, bptr, img, g.out_ch, cols, plane, 0, 0, g.wrap, pairs ? 1u : 0u, plane};
+        return run_gemm(A, B, 1, g.in_ch * g.kh * g.kw, epi, s);
+    }
+    SrcIm2col im{x, g.in_ch, g.in_h, g.in_w, g.out_w, g.kh, g.kw, g.sh, g.sw, g.dh, g.dw, g.pt, g.pl, plane};
+    int rc = run_split<SrcIm2col, false>(im, (uint64_t)g.in_ch * g.in_h * g.in_w, B, s);
+    if (rc) return rc;
+    const bool pairs = (reinterpret_cast<uintptr_t>(y) & 3) == 0 && (plane & 1) == 0 && (g.cs & 1) == 0 &&
+                       (g.gs & 1) == 0 && (img & 1) == 0;
+    EpiConv epi{y, bptr, img, g.out_ch, plane, g.cs, g.cn, g.gs, g.wrap, pairs ? 1u : 0u, 0};
+    return run_gemm(A, B, g.batch, g.in_ch * g.kh * g.kw, epi, s);
+}
+
+}  // namespace
+}  // namespace cm
+
 extern "C" int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
                        uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
                        uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
@@ -1141,30 +1319,81 @@ extern "C" int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, 
                            wrap32 ? 1u : 0u);
         return CM_OK;
     }
-    const uint32_t tiles = (in_ch + 15) / 16;
-    const uint32_t rem = in_ch - (tiles - 1) * 16, last = rem <= 8 ? 8 : 16;
-    const uint32_t per_m = kh * kw * ((tiles - 1) * 16 + last);
     if ((uint64_t)in_ch * kh * kw > 32768)
         return fail(CM_EINVAL, "conv: in_ch * kh * kw = %u above 32768", in_ch * kh * kw);
-    const uint32_t kpad = tiles * kh * kw * 16;
-    const uint32_t kp = (uint32_t)round_up(kpad, BK);
-    Planes A = make_planes(out_ch, kp, 1, gemm_tile_rows(out_ch, plane, batch, st->cus)),
-           B = make_planes(plane, kp, batch);
+    const ConvGeom g{batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w, dilation_h,
+                     dilation_w, pad_top, pad_left, cs, y_cn, y_gs, wrap32 ? 1u : 0u};
+    const uint32_t kp = conv_kp(in_ch, kh, kw);
+    Planes B = conv_b_planes(g, kp);
+    Planes A = make_planes(out_ch, kp, 1, conv_tile(g, B, st));
     void* ws;
     rc = workspace(st, A.bytes() + B.bytes(), &ws);
     if (rc) return rc;
     char* p = static_cast<char*>(ws);
     A.carve(p);
     B.carve(p);
-    rc = run_split<SrcConvW, true>(SrcConvW{w, out_ch, in_ch, kh, kw, tiles, per_m, last}, 0, A, s);
+    rc = conv_split_w(w, A, out_ch, in_ch, kh, kw, s);
     if (rc) return rc;
-    SrcIm2col im{x, in_ch, in_h, in_w, out_w, kh, kw, stride_h, stride_w, dilation_h, dilation_w,
-                 pad_top, pad_left, plane};
-    rc = run_split<SrcIm2col, false>(im, (uint64_t)in_ch * in_h * in_w, B, s);
+    return conv_gemm(x, A, B, bptr, y, g, st, s);
+}
+
+extern "C" size_t cm_conv_w_planes_bytes(uint32_t out_ch, uint32_t in_ch, uint32_t kh, uint32_t kw) {
+    using namespace cm;
+    if (out_ch == 0 || in_ch == 0 || kh == 0 || kw == 0) return 0;
+    return make_planes(out_ch, conv_kp(in_ch, kh, kw), 1, 256).bytes();
+}
+
+extern "C" int cm_conv_split_w(const int16_t* w, void* planes, uint32_t out_ch, uint32_t in_ch, uint32_t kh,
+                               uint32_t kw, void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
     if (rc) return rc;
-    const uint64_t img = (uint64_t)out_ch * plane;
-    const bool pairs = (reinterpret_cast<uintptr_t>(y) & 3) == 0 && (plane & 1) == 0 && (cs & 1) == 0 &&
-                       (y_gs & 1) == 0 && (img & 1) == 0;
-    EpiConv epi{y, bptr, img, out_ch, plane, cs, y_cn, y_gs, wrap32 ? 1u : 0u, pairs ? 1u : 0u};
-    return run_gemm(A, B, batch, in_ch * kh * kw, epi, s);
+    if (out_ch == 0) return CM_OK;
+    if (in_ch == 0 || kh == 0 || kw == 0 || kh > 7 || kw > 7) return fail(CM_EINVAL, "conv: weights %ux%ux%u", in_ch, kh, kw);
+    if ((uint64_t)in_ch * kh * kw > 32768)
+        return fail(CM_EINVAL, "conv: in_ch * kh * kw = %u above 32768", in_ch * kh * kw);
+    if (reinterpret_cast<uintptr_t>(planes) & 255) return fail(CM_EALIGN, "conv: weight planes not 256-byte aligned");
+    Planes A = make_planes(out_ch, conv_kp(in_ch, kh, kw), 1, 256);
+    char* p = static_cast<char*>(planes);
+    A.carve(p);
+    return conv_split_w(w, A, out_ch, in_ch, kh, kw, as_stream(stream));
+}
+
+extern "C" int cm_conv_planes(const int16_t* x, const void* w_planes, const int16_t* bias, int16_t* y,
+                              uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
+                              uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
+                              uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
+                              uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise, uint32_t y_cs,
+                              uint32_t y_cn, uint32_t y_gs, uint32_t wrap32, void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    if (batch == 0 || out_ch == 0 || out_h == 0 || out_w == 0) return CM_OK;
+    if (is_depthwise) return fail(CM_EINVAL, "conv: weight planes are for standard convolutions");
+    if (kh == 0 || kw == 0 || kh > 7 || kw > 7) return fail(CM_EINVAL, "conv: kernel %ux%u outside 1..7", kh, kw);
+    if (stride_h == 0 || stride_w == 0 || dilation_h == 0 || dilation_w == 0)
+        return fail(CM_EINVAL, "conv: zero stride or dilation");
+    if ((y_cs || y_cn) && batch != 1) return fail(CM_EINVAL, "conv: y pattern needs batch 1");
+    if (in_ch == 0) return fail(CM_EINVAL, "conv: in_ch 0");
+    if ((uint64_t)in_ch * kh * kw > 32768)
+        return fail(CM_EINVAL, "conv: in_ch * kh * kw = %u above 32768", in_ch * kh * kw);
+    if (reinterpret_cast<uintptr_t>(w_planes) & 255) return fail(CM_EALIGN, "conv: weight planes not 256-byte aligned");
+    hipStream_t s = as_stream(stream);
+    const uint32_t plane = out_h * out_w;
+    const ConvGeom g{batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w, dilation_h,
+                     dilation_w, pad_top, pad_left, y_cs ? y_cs : plane, y_cn, y_gs, wrap32 ? 1u : 0u};
+    const uint32_t kp = conv_kp(in_ch, kh, kw);
+    Planes B = conv_b_planes(g, kp);
+    Planes A = make_planes(out_ch, kp, 1, 256);
+    char* q = static_cast<char*>(const_cast<void*>(w_planes));
+    A.carve(q);
+    A.tile = conv_tile(g, B, st);
+    void* ws;
+    rc = workspace(st, B.bytes(), &ws);
+    if (rc) return rc;
+    char* p = static_cast<char*>(ws);
+    B.carve(p);
+    return conv_gemm(x, A, B, has_bias ? bias : nullptr, y, g, st, s);
 }

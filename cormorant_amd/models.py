@@ -16,7 +16,7 @@ import numpy as np
 
 from . import units
 from .graph import (AttnContractNode, ConvNode, Graph, MatmulNode, PermuteNode, PoolNode, ReshapeNode, ScheduledNode,
-                    SoftmaxVopNode, TensorInfo, softmax_regs)
+                    SoftmaxVopNode, TensorInfo, conv_out, softmax_regs)
 from .rowops_nodes import LayerNorm32RoNode, ResAddBiasRoNode
 
 
@@ -56,6 +56,85 @@ def small_cnn(seed: int = 0):
     g = Graph(nodes, input_tensors=[x], output_tensors=[sm])
     inputs = {"input": np.round(rng.uniform(0.0, 1.0, (1, 1, 28, 28)) * 256) / 256}
     return g, inputs
+
+
+# ---------------------------------------------------------------- MobileNetV2-style CNN
+# (expansion t, output channels c, repeats n, first stride s) of the 17 inverted residual blocks
+MOBILENET_V2_BLOCKS = ((1, 16, 1, 1), (6, 24, 2, 2), (6, 32, 3, 2), (6, 64, 4, 2), (6, 96, 3, 1),
+                       (6, 160, 3, 2), (6, 320, 1, 1))
+
+
+def mobilenet_v2(batch: int = 32, res: int = 224, seed: int = 0, classes: int = 1000):
+    """(graph, inputs, macs): MobileNetV2 1.0 in Q8.8, NCHW, batch ``batch`` at ``res`` x ``res``.
+
+    Stem Conv 3x3 s2 3->32 pad 1 + RELU6; the 17 inverted residual blocks (1x1 expand x t +
+    RELU6 where t > 1, depthwise 3x3 stride s pad 1 + RELU6, 1x1 project, residual ADD where
+    stride 1 and the channels match); Conv 1x1 320->1280 + RELU6; global AVG pool over the
+    final plane; flatten; MatMul 1280 x ``classes``.  The node kinds are the reference's
+    mapping of these ONNX ops (Conv -> ConvNode, Clip(0, 6) -> VectorOP RELU6, Add -> VectorOP
+    ADD, GlobalAveragePool -> PoolNode AVG, Flatten -> ReshapeNode, MatMul -> MatmulNode;
+    graph.py:1005-1069, _simulate.py:617-765).  Convolutions carry no bias (a folded
+    batch-norm's bias is a plain VectorOP ADD in the reference's mapping, left out here).
+
+    He-normal weights (std sqrt(2 / fan_in)), the input U[0, 1); every tensor Q8.8.  Weights
+    come from their own generator, so a smaller batch of the same seed is the leading images
+    of a larger one.  ``macs`` counts the convolutions' and the classifier's multiply-adds."""
+    T = TensorInfo
+    rng_in = np.random.default_rng([seed, 0])
+    x_val = np.round(rng_in.random((batch, 3, res, res)) * 256) / 256
+    rng = np.random.default_rng([seed, 1])
+    nodes, macs = [], [0]
+    x_t = T("input", [batch, 3, res, res])
+    cur = x_t
+    count = [0]
+
+    def name(tag):
+        count[0] += 1
+        return f"n{count[0]}.{tag}"
+
+    def conv(x, cout, k, stride, depthwise=False):
+        cin, h, w = x.shape[1], x.shape[2], x.shape[3]
+        pad = k // 2
+        oh, ow = conv_out(h, k, stride, pad, pad), conv_out(w, k, stride, pad, pad)
+        fan_in = (1 if depthwise else cin) * k * k
+        wt = T(name("w"), [cout, 1 if depthwise else cin, k, k],
+               data=rng.standard_normal((cout, 1 if depthwise else cin, k, k)) * math.sqrt(2.0 / fan_in))
+        y = T(name("conv"), [batch, cout, oh, ow])
+        nodes.append(ConvNode([x, wt], y, stride_h=stride, stride_w=stride, pad_top=pad, pad_left=pad,
+                              is_depthwise=depthwise))
+        macs[0] += batch * cout * oh * ow * fan_in
+        return y
+
+    def relu6(x):
+        y = T(name("relu6"), list(x.shape))
+        nodes.append(ScheduledNode([x], y, units.OP_RELU6))
+        return y
+
+    cur = relu6(conv(cur, 32, 3, 2))
+    for t, c, n, s in MOBILENET_V2_BLOCKS:
+        for i in range(n):
+            stride = s if i == 0 else 1
+            inp = cur
+            h = inp
+            if t != 1:
+                h = relu6(conv(h, inp.shape[1] * t, 1, 1))
+            h = relu6(conv(h, h.shape[1], 3, stride, depthwise=True))
+            h = conv(h, c, 1, 1)
+            if stride == 1 and inp.shape[1] == c:
+                y = T(name("add"), list(h.shape))
+                nodes.append(ScheduledNode([h, inp], y, units.OP_ADD))
+                h = y
+            cur = h
+    cur = relu6(conv(cur, 1280, 1, 1))
+    pooled = T("pool", [batch, 1280, 1, 1])
+    nodes.append(PoolNode([cur], pooled, units.POOL_AVG, cur.shape[2], cur.shape[3], 1, 1))
+    flat = T("flat", [batch, 1280])
+    nodes.append(ReshapeNode([pooled], flat))
+    wf = T("fc.w", [1280, classes], data=rng.standard_normal((1280, classes)) * math.sqrt(2.0 / 1280))
+    logits = T("logits", [batch, classes])
+    nodes.append(MatmulNode([flat, wf], logits))
+    macs[0] += batch * 1280 * classes
+    return Graph(nodes, input_tensors=[x_t], output_tensors=[logits]), {"input": x_val}, macs[0]
 
 
 # ---------------------------------------------------------------- BERT-base-shaped encoder

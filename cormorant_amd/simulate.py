@@ -224,6 +224,9 @@ class Simulator:
         if img is None:
             w = self._get(wt, raw).cpu().numpy().reshape(wt.shape)
             img = torch.from_numpy(conv_weight_image(w, sn.is_depthwise)).to(self.device)
+            if not sn.is_depthwise and wt.data is not None:
+                # a constant weight of a standard convolution: its GEMM operand split once
+                img = units.conv_w_planes(img, sn.out_ch, sn.in_ch, sn.kh, sn.kw)
             self._images[wt.onnx_name] = img
         bias = None
         if bias_t is not None:
@@ -233,6 +236,12 @@ class Simulator:
                 bias = torch.from_numpy(conv_bias_image(self._get(bias_t, raw).cpu().numpy())).to(self.device)
                 self._images[key] = bias
         y = self._new(ot)
+        if img.dtype == torch.uint8:
+            units.conv_planes(x.reshape(-1).contiguous(), img, bias, y, sn.batch, sn.in_ch, sn.in_h, sn.in_w,
+                              sn.out_ch, sn.out_h, sn.out_w, sn.kh, sn.kw, sn.stride_h, sn.stride_w, sn.dilation_h,
+                              sn.dilation_w, sn.pad_top, sn.pad_left, int(bias is not None),
+                              wrap32=self._pow2(xt, wt, ot))
+            return y
         units.conv(x.reshape(-1).contiguous(), img, bias, y, sn.batch, sn.in_ch, sn.in_h, sn.in_w, sn.out_ch,
                    sn.out_h, sn.out_w, sn.kh, sn.kw, sn.stride_h, sn.stride_w, sn.dilation_h, sn.dilation_w,
                    sn.pad_top, sn.pad_left, int(bias is not None), int(sn.is_depthwise),

@@ -214,6 +214,44 @@ def conv(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], y: torc
     return y
 
 
+def conv_w_planes(w: torch.Tensor, out_ch: int, in_ch: int, kh: int, kw: int) -> torch.Tensor:
+    """The split image of a standard convolution's packed weights (cm_conv_split_w) in a new
+    uint8 device tensor, for conv_planes."""
+    nbytes = int(_lib.lib().cm_conv_w_planes_bytes(out_ch, in_ch, kh, kw))
+    planes = torch.empty(nbytes + 256, dtype=torch.uint8, device=w.device)
+    off = (-planes.data_ptr()) % 256
+    planes = planes[off:off + nbytes]
+    if out_ch:
+        _require(w, "w", torch.int16, conv_weight_numel(out_ch, in_ch, kh, kw, False))
+    rc = _lib.lib().cm_conv_split_w(_ptr(w), _ptr(planes), out_ch, in_ch, kh, kw, _stream())
+    _lib.check(rc, "cm_conv_split_w")
+    return planes
+
+
+def conv_planes(x: torch.Tensor, w_planes: torch.Tensor, bias: Optional[torch.Tensor], y: torch.Tensor,
+                batch: int, in_ch: int, in_h: int, in_w: int, out_ch: int, out_h: int, out_w: int,
+                kh: int, kw: int, stride_h: int = 1, stride_w: int = 1, dilation_h: int = 1,
+                dilation_w: int = 1, pad_top: int = 0, pad_left: int = 0, has_bias: int = 0,
+                y_cs: int = 0, y_cn: int = 0, y_gs: int = 0, wrap32: bool = False) -> torch.Tensor:
+    """cm_conv of a standard convolution with the weights' split image from conv_w_planes."""
+    if batch and out_ch and out_h and out_w:
+        _require(x, "x", torch.int16, batch * in_ch * in_h * in_w)
+        if has_bias:
+            _require(bias, "bias", torch.int16, out_ch)
+        _require(y, "y", torch.int16, conv_y_extent(batch, out_ch, out_h, out_w, y_cs, y_cn, y_gs))
+        need = int(_lib.lib().cm_conv_w_planes_bytes(out_ch, in_ch, kh, kw))
+        if w_planes.dtype != torch.uint8 or w_planes.numel() < need or w_planes.data_ptr() % 256:
+            raise ValueError("w_planes: the uint8 image of conv_w_planes for these out_ch, in_ch, kh, kw")
+        if stride_h == 0 or stride_w == 0 or dilation_h == 0 or dilation_w == 0:
+            raise ValueError("conv: zero stride / dilation")
+    rc = _lib.lib().cm_conv_planes(_ptr(x), _ptr(w_planes), _ptr(bias) if has_bias else None, _ptr(y), batch,
+                                   in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w,
+                                   dilation_h, dilation_w, pad_top, pad_left, int(has_bias), 0, y_cs, y_cn, y_gs,
+                                   int(bool(wrap32)), _stream())
+    _lib.check(rc, "cm_conv_planes")
+    return y
+
+
 # ---------------------------------------------------------------- Pool
 def pool(x: torch.Tensor, y: torch.Tensor, batch: int, channels: int, in_h: int, in_w: int,
          out_h: int, out_w: int, pool_h: int, pool_w: int, stride_h: int = 1, stride_w: int = 1,

@@ -136,6 +136,22 @@ int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
             uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise, uint32_t y_cs,
             uint32_t y_cn, uint32_t y_gs, uint32_t wrap32, void* stream);
 
+/* Constant weights of a standard (not depthwise) convolution split once: cm_conv_split_w
+ * writes the byte planes and row sums of the packed weights w -- what every cm_conv call
+ * otherwise derives from w on the fly -- into `planes` (cm_conv_w_planes_bytes(out_ch, in_ch,
+ * kh, kw) bytes, 256-byte aligned); cm_conv_planes, with cm_conv's arguments otherwise
+ * (is_depthwise 0), then computes exactly cm_conv.  No counterpart in the reference's units:
+ * a cache of the operand split that this build's GEMM performs. */
+size_t cm_conv_w_planes_bytes(uint32_t out_ch, uint32_t in_ch, uint32_t kh, uint32_t kw);
+int cm_conv_split_w(const int16_t* w, void* planes, uint32_t out_ch, uint32_t in_ch, uint32_t kh, uint32_t kw,
+                    void* stream);
+int cm_conv_planes(const int16_t* x, const void* w_planes, const int16_t* bias, int16_t* y,
+                   uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
+                   uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
+                   uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
+                   uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise, uint32_t y_cs,
+                   uint32_t y_cn, uint32_t y_gs, uint32_t wrap32, void* stream);
+
 /* ---------------------------------------------------------------- Pooling
  * Replaces PoolingKernel (kernels/pool_rtl/model/include/PoolingKernel.h:120-140) and the
  * simulator's pool reference (_simulate.py:230-358, 701-719): pool_type 0 MAX, 1 AVG

@@ -191,6 +191,18 @@ CONV_CASES = [  # batch, C, H, W, M, kh, kw, sh, sw, dh, dw, pt, pl, pb, pr, bia
     (1, 8, 12, 16, 8, 3, 3, 1, 1, 1, 1, 2, 2, 0, 0, 1, 1, True, False),
     (1, 8, 20, 56, 8, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, True, False),
     (2, 8, 9, 32, 8, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, True, True),
+    # 1x1 stride 1 unpadded: the images folded into the GEMM's columns (even / odd planes,
+    # line groups across images, 1280 rows, two k slabs), and 1x1 convs that do not fold
+    (32, 24, 14, 14, 144, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 1, 0, False, False),
+    (5, 96, 7, 7, 160, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 0, 0, True, False),
+    (2, 320, 8, 8, 1280, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 1, 0, False, True),
+    (2, 1100, 4, 6, 40, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 1, 0, True, False),
+    (3, 16, 33, 35, 24, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 0, 0, False, False),
+    (2, 16, 9, 9, 24, 1, 1, 2, 2, 1, 1, 0, 0, 0, 0, 1, 0, False, False),
+    (2, 16, 9, 9, 24, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 0, False, False),
+    # folded 1x1 with 2^16 lines and more (the LDS-tiled split): an even and an odd plane
+    (4, 24, 128, 128, 40, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 1, 0, False, False),
+    (3, 20, 151, 149, 24, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 0, 0, True, False),
 ]
 
 
@@ -215,6 +227,30 @@ def test_conv_random(U, oracle_lib, case):
     got = host(y)
     np.testing.assert_array_equal(got[:bt * M * oh * ow], want)
     assert (got[bt * M * oh * ow:] == POISON16).all()
+
+
+@pytest.mark.parametrize("case", [c for c in CONV_CASES if not c[16]], ids=lambda c: "b%d_c%d_%dx%d_m%d_k%dx%d_s%d%d" % (
+    c[0], c[1], c[2], c[3], c[4], c[5], c[6], c[7], c[8]))
+def test_conv_planes_equals_conv(U, case):
+    """Weights split once (cm_conv_split_w) then cm_conv_planes: the same output as cm_conv,
+    for two inputs through the same planes."""
+    from cormorant_amd.packing import conv_bias_image, conv_weight_image
+    (bt, C, H, W, M, kh, kw, sh, sw, dh, dw, pt, pl, pb, pr, has_b, dwise, full, wrap) = case
+    rng = np.random.default_rng(C * 17 + M)
+    lim = 32768 if full else 1024
+    oh = (H + pt + pb - dh * (kh - 1) - 1) // sh + 1
+    ow = (W + pl + pr - dw * (kw - 1) - 1) // sw + 1
+    w = dev16(conv_weight_image(rint16(rng, M * C * kh * kw, -lim, lim).reshape(M, C, kh, kw), False))
+    bias = dev16(conv_bias_image(rint16(rng, M, -lim, lim)))
+    planes = U.conv_w_planes(w, M, C, kh, kw)
+    for rep in range(2):
+        x = dev16(rint16(rng, bt * C * H * W, -lim, lim))
+        want = poisoned16(bt * M * oh * ow + 8)
+        U.conv(x, w, bias, want, bt, C, H, W, M, oh, ow, kh, kw, sh, sw, dh, dw, pt, pl, has_b, 0, wrap32=wrap)
+        got = poisoned16(bt * M * oh * ow + 8)
+        U.conv_planes(x, planes, bias, got, bt, C, H, W, M, oh, ow, kh, kw, sh, sw, dh, dw, pt, pl, has_b,
+                      wrap32=wrap)
+        np.testing.assert_array_equal(host(got), host(want))
 
 
 @pytest.mark.parametrize("op", range(10))
