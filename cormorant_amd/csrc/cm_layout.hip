@@ -5,6 +5,8 @@
 // token rows: the moves the reference's VitAttnPrep / LlmAttnMerge make between the
 // projection MatMuls and the attention contractions.
 //
+// cm_copy16 is the same gather into a strided destination (the KV-cache row writes).
+//
 // Three kernels by the strides:
 //   * the innermost dimension contiguous in src (s3 == 1), rows of whole 16-byte words: one
 //     lane per 16-byte word, loads and stores both whole words;
@@ -79,6 +81,22 @@ __global__ __launch_bounds__(256) void permute_elems_kernel(const int16_t* __res
     }
 }
 
+// dst[i0 t0 + i1 t1 + i2 t2 + i3 t3] = src[i0 s0 + i1 s1 + i2 s2 + i3 s3]: a lane per element.
+__global__ __launch_bounds__(256) void copy_elems_kernel(const int16_t* __restrict__ src, int16_t* __restrict__ dst,
+                                                         uint64_t total, Perm p, Perm q) {
+    for (uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (uint64_t)gridDim.x * blockDim.x) {
+        uint64_t r = e;
+        const uint32_t i3 = (uint32_t)(r % p.d3);
+        r /= p.d3;
+        const uint32_t i2 = (uint32_t)(r % p.d2);
+        r /= p.d2;
+        const uint32_t i1 = (uint32_t)(r % p.d1);
+        const uint64_t i0 = r / p.d1;
+        dst[i0 * q.s0 + i1 * q.s1 + i2 * q.s2 + i3 * q.s3] = src[i0 * p.s0 + i1 * p.s1 + i2 * p.s2 + i3 * p.s3];
+    }
+}
+
 unsigned grid_of(uint64_t items) {
     return (unsigned)std::max<uint64_t>(1, std::min<uint64_t>((items + 255) / 256, 65536ull * 8));
 }
@@ -111,5 +129,20 @@ extern "C" int cm_permute16(const int16_t* src, int16_t* dst, uint32_t d0, uint3
         }
     }
     CM_LAUNCH("permute_elems_kernel", permute_elems_kernel, dim3(grid_of(total)), dim3(256), 0, s, src, dst, total, p);
+    return CM_OK;
+}
+
+extern "C" int cm_copy16(const int16_t* src, int16_t* dst, uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3,
+                         uint64_t s0, uint64_t s1, uint64_t s2, uint64_t s3, uint64_t t0, uint64_t t1, uint64_t t2,
+                         uint64_t t3, void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    const uint64_t total = (uint64_t)d0 * d1 * d2 * d3;
+    if (total == 0) return CM_OK;
+    const Perm p{d0, d1, d2, d3, s0, s1, s2, s3}, q{d0, d1, d2, d3, t0, t1, t2, t3};
+    CM_LAUNCH("copy_elems_kernel", copy_elems_kernel, dim3(grid_of(total)), dim3(256), 0, as_stream(stream), src, dst,
+              total, p, q);
     return CM_OK;
 }

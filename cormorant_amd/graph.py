@@ -240,6 +240,18 @@ class AttnContractNode:
 
 
 @dataclass
+class KvWriteNode:
+    """The step's K or V rows into the KV caches: x [B][KV * HD] (row b = sequence b's new
+    row) -> cache [B][KV][C][HD] (each sequence's cache group-major) at row ``pos``, the
+    cache written in place and returned as the output (the cache row writes of
+    LlmAttnPrep / AttnPrepRoNode, llm_nodes.py:1012-1030 and :1155-1159).  The row is
+    copied raw: x and the cache share one exponent."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    pos: int = 0
+
+
+@dataclass
 class Graph:
     """Nodes in topological order plus the graph's inputs, outputs and weights."""
     nodes: List[object] = field(default_factory=list)
@@ -262,7 +274,7 @@ def conv_out(size: int, k: int, stride: int, pad_lo: int, pad_hi: int, dil: int 
 
 
 __all__ = ["SchedulerError", "TensorInfo", "ScheduledNode", "MatmulNode", "ConvNode", "PoolNode",
-           "ReshapeNode", "SoftmaxVopNode", "RowOpsNode", "LlmAttnConvNode", "attn_keys", "KEY_QUANTUM",
+           "ReshapeNode", "SoftmaxVopNode", "RowOpsNode", "LlmAttnConvNode", "KvWriteNode", "attn_keys", "KEY_QUANTUM",
            "Graph", "conv_out", "OP_ADD", "OP_SUB",
            "OP_MUL", "OP_DIV", "OP_RELU", "OP_RELU6", "OP_SOFTMAX", "OP_SOFTMAX_T", "POOL_MAX",
            "POOL_AVG", "POOL_LP"]

@@ -328,3 +328,288 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
     g = Graph(nodes, input_tensors=[h_in], output_tensors=[hcur])
     encode_matmul_weights(g.nodes, AP_FIXED_16_8)
     return g, {"h0": h0}, exps
+
+
+# ---------------------------------------------------------------- SmolLM2-360M-shaped decode step
+@dataclass
+class LlamaShape:
+    """A Llama-architecture decoder (SmolLM2-360M's by default: config.json of the checkpoint
+    the reference's llama.py front end reads) and the decode step's batch / cache."""
+    layers: int = 32
+    batch: int = 16
+    d: int = 960
+    heads: int = 15
+    kv: int = 5
+    hd: int = 64
+    ff: int = 2560
+    vocab: int = 49152
+    ctx: int = 1024
+    theta: float = 100000.0
+    eps: float = 1e-5
+
+    @property
+    def group(self) -> int:
+        return self.heads // self.kv
+
+    def macs(self, keys: int = None) -> int:
+        """Multiply-accumulates of one step: the linears (q, k, v, o, gate, up, down and the
+        tied head) for every sequence, and q.K^T / P.V over ``keys`` cache rows."""
+        keys = self.ctx if keys is None else keys
+        D, A, K = self.d, self.heads * self.hd, self.kv * self.hd
+        lin = self.layers * (D * A + 2 * D * K + A * D + 3 * D * self.ff) + D * self.vocab
+        att = self.layers * 2 * self.heads * keys * self.hd
+        return self.batch * (lin + att)
+
+    def weight_bytes(self) -> int:
+        D, A, K = self.d, self.heads * self.hd, self.kv * self.hd
+        return 2 * (self.layers * (D * A + 2 * D * K + A * D + 3 * D * self.ff) + D * self.vocab)
+
+
+def rope_half_tables(theta: float, hd: int, n: int):
+    """float32 cos / sin [n][hd/2] as the reference's rope.half_tables (rope.py:51-58,
+    133-146): inv_j = float32(1 / theta^(2j/hd)) from float64, a = float32(float32(pos) * inv_j),
+    cos = float32(cos(double(a)))."""
+    inv = np.array([1.0 / (theta ** (2 * j / hd)) for j in range(hd // 2)], np.float64).astype(np.float32)
+    ang = (np.arange(n, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float32)
+    c = np.cos(ang.astype(np.float64)).astype(np.float32)
+    s = np.sin(ang.astype(np.float64)).astype(np.float32)
+    return c, s
+
+
+def _rms(h, gamma, eps):
+    return h / np.sqrt((h * h).mean(axis=-1, keepdims=True) + eps) * gamma
+
+
+def _rope_f(x, heads, hd, cos, sin):
+    """Rotate-half RoPE of rows [T][heads * hd] at one position (cos / sin [hd / 2])."""
+    x = x.reshape(-1, heads, hd)
+    half = hd // 2
+    x1, x2 = x[..., :half], x[..., half:]
+    c, s = cos.astype(np.float64), sin.astype(np.float64)
+    return np.concatenate([x1 * c - x2 * s, x2 * c + x1 * s], axis=-1).reshape(-1, heads * hd)
+
+
+KV_SIGMA = 0.6       # std of the synthetic cache rows: about a projection's (sqrt(960) x 0.02)
+
+
+def smollm2_weights(shape: LlamaShape = LlamaShape(), seed: int = 0):
+    """The synthetic float32 weights of ``shape`` (the decode step's ``weights``): the tied
+    embedding [vocab][d], per layer the linears (wq [d][heads hd], wk / wv [d][kv hd], wo,
+    wg / wu [d][ff], wd [ff][d]) N(0, 0.02) and the RMSNorm gammas 1 + N(0, 0.02), the final
+    gamma."""
+    S = shape
+    A, KD = S.heads * S.hd, S.kv * S.hd
+    rng = np.random.default_rng([seed, 1])
+    nrm = lambda *sh: rng.standard_normal(sh, dtype=np.float32) * np.float32(0.02)     # noqa: E731
+    emb = nrm(S.vocab, S.d)
+    Ls = [dict(g1=1.0 + nrm(S.d).astype(np.float64), wq=nrm(S.d, A), wk=nrm(S.d, KD), wv=nrm(S.d, KD),
+               wo=nrm(A, S.d), g2=1.0 + nrm(S.d).astype(np.float64), wg=nrm(S.d, S.ff), wu=nrm(S.d, S.ff),
+               wd=nrm(S.ff, S.d))
+          for _ in range(S.layers)]
+    gf = 1.0 + nrm(S.d).astype(np.float64)
+    return emb, Ls, gf
+
+
+def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: int = 1, weights=None):
+    """(graph, inputs, exps): one greedy decode step of ``shape.batch`` sequences, each at cache
+    position ctx - 1 (the cache full after the step's row: every cache row is a key), pow2
+    numerics on the units as the reference's llama.py front end lays out a layer with the
+    row-ops policy (llama.py:140-400, ``rowops`` + ``drope``):
+
+        x  = RMSNorm(h)                    row-ops NORM, int32 residual at 2^-15 -> int16
+        q, k, v = x Wq, x Wk, x Wv         MatMul (pow2, int32 wrap)
+        q, k = RoPE(q), RoPE(k)            row-ops ROPE at position pos
+        cache rows pos <- k, v             the attention prep's cache writes
+        qx = q per KV group [d][heads]     the q image (permute)
+        s  = K_cache . qx                  batched contraction per (sequence, group)
+        P  = softmax over keys             VectorOP softmax (row mode over s transposed), keys <= pos
+        o  = P . V_cache                   batched contraction
+        h1 = ResAdd(h, o Wo)               row-ops ADDX
+        x2 = RMSNorm(h1); m = SiluMul(x2 Wg, x2 Wu); h = ResAdd(h1, m Wd)
+    then RMSNorm, the tied head (x E^T) and Dequant to float32 logits.
+
+    Synthetic data (no checkpoint): the tied embedding, every linear N(0, 0.02), RMSNorm
+    gammas 1 + N(0, 0.02); the step's residual h0 = embedding rows of random ids; the cache
+    rows before ``pos`` N(0, KV_SIGMA) in place of a prefill; every draw is per sequence, so a
+    smaller batch of the same seed is the leading sequences of a larger one.  Exponents from a
+    float64 run of the step over the first ``calib_seqs`` sequences (``_fit_exp``), with the
+    pow2 rules: f_s = f_q + f_k - 8 (q / k lowered until
+    s fits), P at 2^-14, f_o = f_p + f_v - 8, deltas at <= 2^-15, the gate at <= 2^-14, and
+    every weight's exponent f_out + 8 - f_in at least 10.  ``weights``: smollm2_weights(shape,
+    seed) made once for several builds (they depend on the shape's sizes, not its batch)."""
+    from .dtype import AP_FIXED_16_8
+    from .numeric import encode_matmul_weights
+    from .rowops_nodes import DequantRoNode, RMSNormRoNode, ResAddRoNode, RopeRoNode, SiluMulRoNode
+    from .graph import KvWriteNode
+
+    S = shape
+    if S.ctx % 16 or S.heads % S.kv or S.hd % 16:
+        raise ValueError("ctx and head_dim multiples of 16, heads a multiple of the KV heads")
+    pos = S.ctx - 1
+    B, D, H, KV, HD, G = S.batch, S.d, S.heads, S.kv, S.hd, S.group
+    A, KD = H * HD, KV * HD
+    keys = S.ctx
+    emb, Ls, gf = smollm2_weights(S, seed) if weights is None else weights
+    rng_in = np.random.default_rng([seed, 0])
+    ids = rng_in.integers(0, S.vocab, B * 64)[::64]            # sequence b's id: one draw per sequence slot
+    h0 = np.round(emb[ids].astype(np.float64) * 2.0 ** RES_BITS) / 2.0 ** RES_BITS
+    cos, sin = rope_half_tables(S.theta, HD, S.ctx)
+
+    def cache_rows(layer, which):
+        """[B][KV][ctx][HD] float values of the synthetic rows before pos (zeros after)."""
+        c = np.zeros((B, KV, S.ctx, HD), np.float32)
+        for b in range(B):
+            r = np.random.default_rng([seed, 2, layer, which, b])
+            c[b, :, :pos, :] = r.standard_normal((KV, pos, HD), dtype=np.float32) * np.float32(KV_SIGMA)
+        return c
+
+    # ---- calibration: the step in float64 over the first sequences
+    cb = max(1, min(calib_seqs, B))
+    cal, caches = [], []
+    h = h0[:cb]
+    for li, L in enumerate(Ls):
+        m = {}
+        x = _rms(h, L["g1"], S.eps)
+        q = x @ L["wq"].astype(np.float64)
+        k = x @ L["wk"].astype(np.float64)
+        v = x @ L["wv"].astype(np.float64)
+        qr = _rope_f(q, H, HD, cos[pos], sin[pos])
+        kr = _rope_f(k, KV, HD, cos[pos], sin[pos])
+        kc, vc = cache_rows(li, 0), cache_rows(li, 1)
+        caches.append((kc, vc))
+        kc, vc = kc[:cb], vc[:cb]
+        kfull, vfull = kc.copy(), vc.copy()
+        kfull[:, :, pos, :] = kr.reshape(cb, KV, HD)
+        vfull[:, :, pos, :] = v.reshape(cb, KV, HD)
+        qh = qr.reshape(cb, KV, G, HD)
+        s = np.einsum("bgjd,bgpd->bgjp", kfull[:, :, :pos + 1], qh)            # [B][KV][keys][G]
+        p = np.exp((s - s.max(axis=2, keepdims=True)) / math.sqrt(HD))
+        p = p / p.sum(axis=2, keepdims=True)
+        o = np.einsum("bgjp,bgjd->bgpd", p, vfull[:, :, :pos + 1]).reshape(cb, A)
+        a = o @ L["wo"].astype(np.float64)
+        h1 = h + a
+        x2 = _rms(h1, L["g2"], S.eps)
+        gt = x2 @ L["wg"].astype(np.float64)
+        up = x2 @ L["wu"].astype(np.float64)
+        mm = gt / (1.0 + np.exp(-gt)) * up
+        dd = mm @ L["wd"].astype(np.float64)
+        h = h1 + dd
+        m.update(x=np.abs(x).max(), q=max(np.abs(q).max(), np.abs(qr).max()),
+                 k=max(np.abs(k).max(), np.abs(kr).max(), np.abs(kc).max()),
+                 v=max(np.abs(v).max(), np.abs(vc).max()), s=np.abs(s).max(), o=np.abs(o).max(), a=np.abs(a).max(),
+                 x2=np.abs(x2).max(), g=np.abs(gt).max(), u=np.abs(up).max(), m=np.abs(mm).max(),
+                 d=np.abs(dd).max())
+        cal.append(m)
+    xf = _rms(h, gf, S.eps)
+    logits = xf @ emb.T.astype(np.float64)
+    fin = dict(xf=_fit_exp(np.abs(xf).max()), logits=_fit_exp(np.abs(logits).max()))
+
+    # the largest exponents that fit, lowered where a rule ties them: a weight's rank-1
+    # exponent f_out + 8 - f_in kept >= W_MIN (N(0, 0.02) weights then keep >= 5 bits)
+    W_MIN = 10
+    exps = []
+    for m in cal:
+        f = {key: _fit_exp(val) for key, val in m.items()}
+        e = {"p": 14, "q": f["q"], "k": f["k"]}
+        while e["q"] + e["k"] - F_Q88 > f["s"]:                 # s = K . q at f_q + f_k - 8
+            if e["q"] >= e["k"]:
+                e["q"] -= 1
+            else:
+                e["k"] -= 1
+        e["s"] = e["q"] + e["k"] - F_Q88
+        e["a"] = min(f["a"], RES_BITS)                          # residual deltas at <= 2^-15
+        e["v"] = min(f["v"], f["o"] - e["p"] + F_Q88, e["a"] + F_Q88 - W_MIN - e["p"] + F_Q88)
+        e["o"] = e["p"] + e["v"] - F_Q88                        # o = P . V at f_p + f_v - 8
+        e["x"] = min(f["x"], e["q"] + F_Q88 - W_MIN, e["k"] + F_Q88 - W_MIN, e["v"] + F_Q88 - W_MIN)
+        e["g"] = min(f["g"], 14)                                # the gate at <= 2^-14 (MULACT)
+        e["u"] = f["u"]
+        e["d"] = min(f["d"], RES_BITS)
+        e["m"] = min(f["m"], e["d"] + F_Q88 - W_MIN)
+        e["x2"] = min(f["x2"], e["g"] + F_Q88 - W_MIN, e["u"] + F_Q88 - W_MIN)
+        exps.append(e)
+    fin["xf"] = min(fin["xf"], fin["logits"] + F_Q88 - W_MIN)
+    exps.append(fin)
+
+    # ---- the integer graph
+    T_ = TensorInfo
+    nodes = []
+    h_in = T_("h0", [B, D], exp=RES_BITS, kind="i32")
+    inputs = {"h0": h0}
+    cache_ts = []
+    hcur = h_in
+    for li, (L, e) in enumerate(zip(Ls, exps)):
+        p = f"l{li}."
+        kc_t = T_(p + "kc", [B, KV, S.ctx, HD], exp=e["k"])
+        vc_t = T_(p + "vc", [B, KV, S.ctx, HD], exp=e["v"])
+        cache_ts += [kc_t, vc_t]
+        kc, vc = caches[li]
+        inputs[kc_t.onnx_name] = np.round(kc.astype(np.float64) * 2.0 ** e["k"]) / 2.0 ** e["k"]
+        inputs[vc_t.onnx_name] = np.round(vc.astype(np.float64) * 2.0 ** e["v"]) / 2.0 ** e["v"]
+        x = T_(p + "x", [B, D], exp=e["x"])
+        nodes.append(RMSNormRoNode([hcur], x, gamma=L["g1"], eps=S.eps))
+        q = T_(p + "q", [B, A], exp=e["q"])
+        nodes.append(MatmulNode([x, T_(p + "wq", [D, A], data=L["wq"])], q))
+        k = T_(p + "k", [B, KD], exp=e["k"])
+        nodes.append(MatmulNode([x, T_(p + "wk", [D, KD], data=L["wk"])], k))
+        v = T_(p + "v", [B, KD], exp=e["v"])
+        nodes.append(MatmulNode([x, T_(p + "wv", [D, KD], data=L["wv"])], v))
+        qr = T_(p + "qr", [B, A], exp=e["q"])
+        nodes.append(RopeRoNode([q], qr, heads=H, head_dim=HD, cos=cos, sin=sin, pos=pos, same_pos=True))
+        kr = T_(p + "kr", [B, KD], exp=e["k"])
+        nodes.append(RopeRoNode([k], kr, heads=KV, head_dim=HD, cos=cos, sin=sin, pos=pos, same_pos=True))
+        kc2 = T_(p + "kc1", [B, KV, S.ctx, HD], exp=e["k"])
+        nodes.append(KvWriteNode([kr, kc_t], kc2, pos=pos))
+        vc2 = T_(p + "vc1", [B, KV, S.ctx, HD], exp=e["v"])
+        nodes.append(KvWriteNode([v, vc_t], vc2, pos=pos))
+        # q image per (sequence, group): qx[b g][d][h'] = qr[b][(g G + h') HD + d]
+        qx = T_(p + "qx", [B * KV, HD, G], exp=e["q"])
+        nodes.append(PermuteNode([qr], qx, dims=(B * KV, HD, G, 1), strides=(G * HD, 1, HD, 1)))
+        kview = T_(p + "kc1v", [B * KV, S.ctx, HD], exp=e["k"])
+        nodes.append(ReshapeNode([kc2], kview))
+        sc = T_(p + "s", [B * KV, keys, G], exp=e["s"])
+        nodes.append(AttnContractNode([kview, qx], sc))
+        # the unit's column mode takes query blocks of 16: the G queries of a decode step go
+        # query-major through its row mode (VitAttnSoftmax's query_major calls, smx_nodes.py:250-253)
+        st = T_(p + "sT", [B * KV, G, keys], exp=e["s"])
+        nodes.append(PermuteNode([sc], st, dims=(B * KV, G, keys, 1), strides=(keys * G, 1, G, 1)))
+        cmr, cfg = softmax_regs(e["s"], 1.0 / math.sqrt(HD), e["p"])
+        pr = T_(p + "P", [B * KV, G, keys], exp=e["p"])
+        nodes.append(SoftmaxVopNode([st], pr, cm=cmr, cfg=cfg, mask=pos + 1))
+        vview = T_(p + "vc1v", [B * KV, S.ctx, HD], exp=e["v"])
+        nodes.append(ReshapeNode([vc2], vview))
+        o = T_(p + "o", [B * KV, G, HD], exp=e["o"])
+        nodes.append(AttnContractNode([pr, vview], o))
+        om = T_(p + "om", [B, A], exp=e["o"])
+        nodes.append(ReshapeNode([o], om))
+        a = T_(p + "a", [B, D], exp=e["a"])
+        nodes.append(MatmulNode([om, T_(p + "wo", [A, D], data=L["wo"])], a))
+        h1 = T_(p + "h1", [B, D], exp=RES_BITS, kind="i32")
+        nodes.append(ResAddRoNode([hcur, a], h1))
+        x2 = T_(p + "x2", [B, D], exp=e["x2"])
+        nodes.append(RMSNormRoNode([h1], x2, gamma=L["g2"], eps=S.eps))
+        gt = T_(p + "g", [B, S.ff], exp=e["g"])
+        nodes.append(MatmulNode([x2, T_(p + "wg", [D, S.ff], data=L["wg"])], gt))
+        up = T_(p + "u", [B, S.ff], exp=e["u"])
+        nodes.append(MatmulNode([x2, T_(p + "wu", [D, S.ff], data=L["wu"])], up))
+        mm = T_(p + "m", [B, S.ff], exp=e["m"])
+        nodes.append(SiluMulRoNode([gt, up], mm))
+        dd = T_(p + "d", [B, D], exp=e["d"])
+        nodes.append(MatmulNode([mm, T_(p + "wd", [S.ff, D], data=L["wd"])], dd))
+        hn = T_(p + "h", [B, D], exp=RES_BITS, kind="i32")
+        nodes.append(ResAddRoNode([h1, dd], hn))
+        hcur = hn
+    xf = T_("xf", [B, D], exp=fin["xf"])
+    nodes.append(RMSNormRoNode([hcur], xf, gamma=gf, eps=S.eps))
+    lq = T_("logits_q", [B, S.vocab], exp=fin["logits"])
+    nodes.append(MatmulNode([xf, T_("w.lm_head", [D, S.vocab], data=np.ascontiguousarray(emb.T))], lq))
+    # the dequant's jobs take rows of at most 4096: the logits as [B * vocab / chunk][chunk]
+    chunk = next(c for c in range(4096, 0, -8) if S.vocab % c == 0)
+    lr = T_("logits_rows", [B * S.vocab // chunk, chunk], exp=fin["logits"])
+    nodes.append(ReshapeNode([lq], lr))
+    lf = T_("logits_f32", [B * S.vocab // chunk, chunk], kind="f32")
+    nodes.append(DequantRoNode([lr], lf))
+    lo = T_("logits", [B, S.vocab], kind="f32")
+    nodes.append(ReshapeNode([lf], lo))
+    g = Graph(nodes, input_tensors=[h_in] + cache_ts, output_tensors=[lo])
+    encode_matmul_weights(g.nodes, AP_FIXED_16_8)
+    return g, inputs, exps

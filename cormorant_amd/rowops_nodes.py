@@ -183,6 +183,7 @@ class RoJob:
     aux: int = 0
     bq_sh: int = 0
     b_row0: Optional[int] = None     # B is a table: job row t reads table row b_row0 + t
+    b_same: bool = False             # ... or every job row reads table row b_row0 (B row stride 0)
 
 
 def _exps(t: TensorInfo, F: int, n: int) -> np.ndarray:
@@ -490,7 +491,8 @@ class RopeRoNode(RowOpsAdapter):
     output's per-head exponents, position pos + t for row t -- one ROPE job with the cos / sin
     table as B (rowops_spec.rope; the RoPE jobs of AttnPrepRoNode, rowops_nodes.py:1008-1014
     and from_llm_attn_prep's rope_params :1181-1191).  ``table`` is the float32 [C][HD/2]
-    cos / sin pair."""
+    cos / sin pair.  ``same_pos``: every row at position pos (the rows of a batch of
+    sequences decoding at one position; the job's B row stride 0)."""
     inputs: List[TensorInfo]
     output: TensorInfo
     heads: int = 1
@@ -499,6 +501,7 @@ class RopeRoNode(RowOpsAdapter):
     sin: np.ndarray = None
     pos: int = 0
     F: int = 8
+    same_pos: bool = False
     table: Optional[TensorInfo] = field(default=None, init=False)
 
     def __post_init__(self):
@@ -516,14 +519,15 @@ class RopeRoNode(RowOpsAdapter):
         _require((sa <= 63).all() and (sb <= 63).all() and (sc >= 0).all() and (sc <= 63).all(), what,
                  "RoPE exponents beyond the shifts")
         tab = rope_table(self.cos, self.sin)
-        _require(tab.shape[1] == 2 * HD and 0 <= self.pos and self.pos + self.rows <= tab.shape[0], what,
-                 "cos / sin tables [C][HD/2] covering pos .. pos + rows")
+        last = self.pos + (1 if self.same_pos else self.rows)
+        _require(tab.shape[1] == 2 * HD and 0 <= self.pos and last <= tab.shape[0], what,
+                 "cos / sin tables [C][HD/2] covering the rows' positions")
         self.table = TensorInfo(f"{y.onnx_name}__rope_table", list(tab.shape), data=tab, kind="i32", raw=True)
         self._params, self.bcast = pblock(0, 0, sa.reshape(-1), sb.reshape(-1), sc.reshape(-1), n)
 
     def jobs(self):
         return [RoJob(opword(RO_ROPE, K_I16, K_I32, K_I16, b_en=True, p_bcast=self.bcast), self._params, self.n,
-                      aux=self.head_dim, b_row0=self.pos)]
+                      aux=self.head_dim, b_row0=self.pos, b_same=self.same_pos)]
 
 
 ADAPTERS = (LayerNormRoNode, LayerNorm32RoNode, RMSNormRoNode, ResAddRoNode, ResAddBiasRoNode, WidenRoNode,

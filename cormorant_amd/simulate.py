@@ -16,8 +16,9 @@ import torch
 
 from . import units
 from .dtype import AP_FIXED_16_8, ApFixed16
-from .graph import (AttnContractNode, ConvNode, Graph, LlmAttnConvNode, MatmulNode, PermuteNode, PoolNode,
-                    ReshapeNode, RowOpsNode, ScheduledNode, SchedulerError, SoftmaxVopNode, TensorInfo, attn_keys)
+from .graph import (AttnContractNode, ConvNode, Graph, KvWriteNode, LlmAttnConvNode, MatmulNode, PermuteNode,
+                    PoolNode, ReshapeNode, RowOpsNode, ScheduledNode, SchedulerError, SoftmaxVopNode, TensorInfo,
+                    attn_keys)
 from .packing import conv_bias_image, conv_weight_image, pack_matmul_b
 from .rowops_nodes import RoJob, RowOpsAdapter
 
@@ -89,6 +90,8 @@ class Simulator:
                 raw[sn.output.onnx_name] = self._permute(sn, raw)
             elif isinstance(sn, AttnContractNode):
                 raw[sn.output.onnx_name] = self._attn_contract(sn, raw)
+            elif isinstance(sn, KvWriteNode):
+                raw[sn.output.onnx_name] = self._kv_write(sn, raw)
             elif isinstance(sn, ScheduledNode):
                 raw[sn.output.onnx_name] = self._vectorop(sn, raw)
             else:
@@ -409,6 +412,21 @@ class Simulator:
         buf[:, :w] = x2d
         return buf, per * _KB[kind], per
 
+    def _kv_write(self, sn: KvWriteNode, raw) -> torch.Tensor:
+        """Row ``pos`` of every sequence's group-major cache from the step's rows, in place."""
+        xt, ct = sn.inputs[0], sn.inputs[1]
+        B, KV, C, HD = (int(v) for v in ct.shape)
+        if list(xt.shape) != [B, KV * HD] or not 0 <= sn.pos < C:
+            raise SchedulerError(f"KV write: rows {list(xt.shape)} into a cache {list(ct.shape)} at {sn.pos}")
+        if not np.array_equal(np.broadcast_to(self._exp_b(xt), (KV * HD,)),
+                              np.broadcast_to(np.asarray(self._exp_b(ct)).reshape(-1), (KV * HD,))):
+            raise SchedulerError("KV write: the rows and the cache at different exponents")
+        x = self._get(xt, raw).reshape(-1).contiguous()
+        cache = self._get(ct, raw)
+        units.copy16(x, cache.reshape(-1)[sn.pos * HD:], (B, KV, HD, 1), (KV * HD, HD, 1, 0),
+                     (KV * C * HD, C * HD, 1, 0))
+        return cache
+
     def _adapter(self, sn: RowOpsAdapter, raw) -> torch.Tensor:
         """A row-ops adapter: its jobs over row views of the tensors (rows of ``n`` = the job
         width; a job covers the columns [col0, col0 + n) of every row)."""
@@ -442,10 +460,12 @@ class Simulator:
                     b2d = b_all.reshape(rows, width)[:, j.col0:j.col0 + j.n]
                 else:
                     tab = b_all.reshape(-1, int(bt.shape[-1]))
-                    if j.b_row0 + rows > tab.shape[0]:
+                    if j.b_row0 + (1 if j.b_same else rows) > tab.shape[0]:
                         raise SchedulerError("row-ops job: table rows past the table")
-                    b2d = tab[j.b_row0:j.b_row0 + rows]
+                    b2d = tab[j.b_row0:j.b_row0 + (1 if j.b_same else rows)]
                 b_buf, b_s1, _ = self._rows16(b2d, bt.kind)
+                if j.b_same:
+                    b_s1 = 0
             c_buf, c_s1, c_per = self._rows16(torch.zeros((rows, j.n), dtype=_TORCH[ot.kind], device=self.device),
                                               ot.kind)
             units.rowops(u8(a_buf), u8(b_buf), u8(c_buf), params[ji], j.op, j.n, rows, 1, a_s1, 0, b_s1, 0, c_s1,

@@ -113,6 +113,21 @@ def permute16(src: torch.Tensor, dst: torch.Tensor, dims, strides) -> torch.Tens
     return dst
 
 
+def copy16(src: torch.Tensor, dst: torch.Tensor, dims, src_strides, dst_strides) -> torch.Tensor:
+    """dst[sum i_k t_k] = src[sum i_k s_k] over the 4 ``dims`` (cm_copy16), in elements."""
+    d = [int(v) for v in dims]
+    ss = [int(v) for v in src_strides]
+    ts = [int(v) for v in dst_strides]
+    if len(d) != 4 or len(ss) != 4 or len(ts) != 4 or min(d) < 0 or min(ss) < 0 or min(ts) < 0:
+        raise ValueError("copy16: 4 dims and 4 non-negative strides on each side")
+    if d[0] * d[1] * d[2] * d[3]:
+        _require(src, "src", torch.int16, 1 + sum((dk - 1) * sk for dk, sk in zip(d, ss)))
+        _require(dst, "dst", torch.int16, 1 + sum((dk - 1) * tk for dk, tk in zip(d, ts)))
+    rc = _lib.lib().cm_copy16(_ptr(src), _ptr(dst), *d, *ss, *ts, _stream())
+    _lib.check(rc, "cm_copy16")
+    return dst
+
+
 def matmul_b_extent(k: int, m: int, b_packed: int, gemv_kw: int) -> int:
     if gemv_kw:
         return k * m

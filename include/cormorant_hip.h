@@ -207,6 +207,14 @@ int cm_rowops_chain(const cm_rowops_desc* jobs, uint32_t n_jobs, void* stream);
 int cm_permute16(const int16_t* src, int16_t* dst, uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3,
                  uint64_t s0, uint64_t s1, uint64_t s2, uint64_t s3, void* stream);
 
+/* dst[i0 t0 + i1 t1 + i2 t2 + i3 t3] = src[i0 s0 + i1 s1 + i2 s2 + i3 s3] for i_k < d_k (elements):
+ * cm_permute16 into a strided destination, e.g. the step's K / V rows into the group-major
+ * caches [KV][C][HD] at row pos (the cache writes of LlmAttnPrep / AttnPrepRoNode,
+ * llm_nodes.py:1012-1030, rowops_nodes.py:1114).  src and dst must not overlap. */
+int cm_copy16(const int16_t* src, int16_t* dst, uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3,
+              uint64_t s0, uint64_t s1, uint64_t s2, uint64_t s3, uint64_t t0, uint64_t t1, uint64_t t2,
+              uint64_t t3, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -132,8 +132,10 @@ def run_adapter(node, raw_of):
             if j.b_row0 is None:
                 b2d = np.asarray(raw_of(bt)).reshape(rows, width)[:, j.col0:j.col0 + j.n]
             else:
-                b2d = np.asarray(bt.data).reshape(-1, bt.shape[-1])[j.b_row0:j.b_row0 + rows]
+                b2d = np.asarray(bt.data).reshape(-1, bt.shape[-1])[j.b_row0:j.b_row0 + (1 if j.b_same else rows)]
             b_img, b_s1 = _rows16(b2d, bt.kind)
+            if j.b_same:
+                b_s1 = 0
         c_img, c_s1 = _rows16(np.zeros((rows, j.n), _NP[ot.kind]), ot.kind)
         cm.rowops_reset_params()
         cm.rowops(a_img, b_img, c_img, j.params, j.op, j.n, rows, 1, a_s1, 0, b_s1, 0, c_s1, 0, j.eps, j.aux,
@@ -143,7 +145,7 @@ def run_adapter(node, raw_of):
 
 
 def forward(graph, inputs):
-    vals = {k: np.asarray(v, np.float64) for k, v in inputs.items()}
+    vals = {k: np.array(v, np.float64) for k, v in inputs.items()}      # copies: states change in place
     get = lambda t: vals[t.onnx_name] if t.onnx_name in vals else _weight(t)
     for sn in graph.nodes:
         out = sn.output
@@ -179,6 +181,12 @@ def forward(graph, inputs):
             if sn.has_bias:
                 acc = acc + get(sn.inputs[2]).reshape(1, -1, 1, 1)
             vals[out.onnx_name] = DT.truncate(acc).reshape(out.shape)
+        elif isinstance(sn, G.KvWriteNode):
+            xt, ct = sn.inputs[0], sn.inputs[1]
+            B, KV, C, HD = (int(v) for v in ct.shape)
+            cache = vals[ct.onnx_name].reshape(B, KV, C, HD)          # the state, written in place
+            cache[:, :, sn.pos, :] = get(xt).reshape(B, KV, HD)
+            vals[out.onnx_name] = cache
         elif isinstance(sn, G.ReshapeNode):
             vals[out.onnx_name] = get(sn.inputs[0]).reshape(out.shape)
         elif isinstance(sn, G.PoolNode):
