@@ -49,10 +49,11 @@ struct SrcRowMajor {             // A[i][kk] = a[i * lda + kk]
 // B side: columns of the output; B(kk, j) for the three matmul images.
 struct SrcMatB {
     const int16_t* p;
-    uint32_t cols, k, m, layout, kw;   // layout 0 row-major, 1 packed, 2 gemv
+    uint32_t cols, k, m, layout, kw;   // layout 0 row-major, 1 packed, 2 gemv, 3 transposed [m][k]
     __device__ bool real(uint32_t j, uint32_t kk) const { return j < cols && kk < k; }
     __device__ int16_t at(uint32_t j, uint32_t kk) const {
         if (layout == 1) return p[((uint64_t)(j >> 5) * k + kk) * 32 + (j & 31)];
+        if (layout == 3) return p[(uint64_t)j * k + kk];
         if (layout == 2 && kw > 1) {
             uint32_t c = (kk / (16 * kw)) * 16 + (kk & 15), jj = (kk >> 4) % kw;
             return p[((uint64_t)c * m + j) * kw + jj];
@@ -975,6 +976,128 @@ __global__ __launch_bounds__(256) void conv_dw3v_kernel(const int16_t* __restric
     }
 }
 
+// ---------------------------------------------------------------- skinny products (int32 wrap)
+// C = sat16(wrap32(A . B) >> 8) for A of at most 32 rows: the decode step's linears, where a
+// 128-column MFMA tile would be mostly padding and the plane split would cost more than the
+// product.  The wrap rule makes the int32 sum mod 2^32 exact in any order, so v_dot2_i32_i16
+// (two products per lane-op, no clamp) accumulates it directly and split k needs no care.
+// A wavefront takes 128 columns (a pair per lane) and one slice of kSkinnyKc k; A's rows of
+// the slice sit in LDS as k pairs, read as broadcasts.  B layouts (BL): 0 row-major [k][m]
+// and 1 the packed 32-column tiles (one 4-byte load per k row for the lane's two columns,
+// paired by byte permutes); 2 transposed [m][k] (a column's k contiguous: 16-byte loads of
+// 8 k).  Every B load of the slice is issued before the first product.  With several slices
+// each wavefront writes its int32 partials [slice][ks][n][m] for skinny_reduce_kernel.
+constexpr uint32_t kSkinnyKc = 64;
+
+template <int NR, int BL>
+__global__ __launch_bounds__(64) void skinny_wrap_kernel(const int16_t* __restrict__ a, uint64_t a_bs,
+                                                          const int16_t* __restrict__ b, uint64_t b_bs,
+                                                          int16_t* __restrict__ c, uint64_t c_bs,
+                                                          int32_t* __restrict__ part, uint32_t n, uint32_t k,
+                                                          uint32_t m) {
+    constexpr uint32_t KP = kSkinnyKc / 2;                                // k pairs per slice
+    __shared__ __attribute__((aligned(16))) uint32_t sa[NR][KP];
+    const uint32_t lane = threadIdx.x, cb = blockIdx.x, ks = blockIdx.y, bt = blockIdx.z, nks = gridDim.y;
+    const uint32_t k0 = ks * kSkinnyKc, k1 = min(k, k0 + kSkinnyKc);
+    const int16_t* ab = a + bt * a_bs;
+    const int16_t* bb = b + bt * b_bs;
+    const uint32_t j0 = cb * 128 + 2 * lane;
+    const bool live = j0 < m;
+    // B's pairs (B[kk][j], B[kk+1][j]) of the slice for columns j0 and j0 + 1
+    uint32_t p0[KP], p1[KP];
+    if (BL == 2) {
+#pragma unroll
+        for (uint32_t q = 0; q < KP / 4; q++) {
+            const uint32_t kk = k0 + 8 * q;
+            int4 x = make_int4(0, 0, 0, 0), y = make_int4(0, 0, 0, 0);
+            if (live && kk < k1) {                          // k1 - k0 is a multiple of 8 here
+                x = *reinterpret_cast<const int4*>(bb + (uint64_t)j0 * k + kk);
+                y = *reinterpret_cast<const int4*>(bb + (uint64_t)(j0 + 1) * k + kk);
+            }
+            p0[4 * q] = x.x; p0[4 * q + 1] = x.y; p0[4 * q + 2] = x.z; p0[4 * q + 3] = x.w;
+            p1[4 * q] = y.x; p1[4 * q + 1] = y.y; p1[4 * q + 2] = y.z; p1[4 * q + 3] = y.w;
+        }
+    } else {
+#pragma unroll
+        for (uint32_t i = 0; i < KP; i++) {
+            const uint32_t kk = k0 + 2 * i;
+            uint32_t w0 = 0, w1 = 0;
+            if (live && kk < k1) {                          // k1 - k0 is even
+                const uint64_t o0 = BL == 1 ? ((uint64_t)(j0 >> 5) * k + kk) * 32 + (j0 & 31) : (uint64_t)kk * m + j0;
+                const uint64_t o1 = BL == 1 ? o0 + 32 : o0 + m;
+                w0 = *reinterpret_cast<const uint32_t*>(bb + o0);
+                w1 = *reinterpret_cast<const uint32_t*>(bb + o1);
+            }
+            p0[i] = __builtin_amdgcn_perm(w1, w0, 0x05040100u);
+            p1[i] = __builtin_amdgcn_perm(w1, w0, 0x07060302u);
+        }
+    }
+    // A's rows of the slice (zero past n and past k)
+    for (uint32_t e = lane; e < NR * KP; e += 64) {
+        const uint32_t r = e / KP, kk = k0 + 2 * (e - r * KP);
+        sa[r][e - r * KP] = (r < n && kk < k1) ? *reinterpret_cast<const uint32_t*>(ab + (uint64_t)r * k + kk) : 0u;
+    }
+    __syncthreads();
+    typedef short v2s __attribute__((ext_vector_type(2)));
+    int acc0[NR], acc1[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) acc0[r] = acc1[r] = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < KP; i += 4) {
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            const uint4 av = *reinterpret_cast<const uint4*>(&sa[r][i]);
+            const uint32_t a4[4] = {av.x, av.y, av.z, av.w};
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                acc0[r] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, a4[t]), __builtin_bit_cast(v2s, p0[i + t]),
+                                                 acc0[r], false);
+                acc1[r] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, a4[t]), __builtin_bit_cast(v2s, p1[i + t]),
+                                                 acc1[r], false);
+            }
+        }
+    }
+    int16_t* cbt = c + bt * c_bs;
+    auto store = [&](uint32_t r, int s0, int s1) {
+        const int q0 = min(max(s0 >> 8, -32768), 32767), q1 = min(max(s1 >> 8, -32768), 32767);
+        *reinterpret_cast<uint32_t*>(cbt + (uint64_t)r * m + j0) = (uint32_t)(uint16_t)q0 | ((uint32_t)q1 << 16);
+    };
+    if (nks == 1) {
+        if (live) {
+#pragma unroll
+            for (int r = 0; r < NR; r++)
+                if ((uint32_t)r < n) store(r, acc0[r], acc1[r]);
+        }
+        return;
+    }
+    if (!live) return;
+    const uint64_t per = (uint64_t)n * m;
+    int32_t* pp = part + ((uint64_t)bt * nks + ks) * per;
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+        if ((uint32_t)r < n) *reinterpret_cast<int2*>(pp + (uint64_t)r * m + j0) = make_int2(acc0[r], acc1[r]);
+}
+
+// Sums the int32 partials of the k slices (wrapping) and applies the output rule: a lane per
+// pair of outputs.
+__global__ __launch_bounds__(256) void skinny_reduce_kernel(const int32_t* __restrict__ part, int16_t* __restrict__ c,
+                                                            uint64_t c_bs, uint32_t n, uint32_t m, uint32_t nks,
+                                                            uint32_t batch) {
+    const uint64_t per = (uint64_t)n * m, pairs = per / 2, total = pairs * batch;
+    for (uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t bt = e / pairs, i = 2 * (e - bt * pairs);
+        const int32_t* pp = part + bt * nks * per + i;
+        uint32_t s0 = 0, s1 = 0;
+        for (uint32_t q = 0; q < nks; q++) {
+            const int2 v = *reinterpret_cast<const int2*>(pp + (uint64_t)q * per);
+            s0 += (uint32_t)v.x;
+            s1 += (uint32_t)v.y;
+        }
+        const int q0 = min(max((int)s0 >> 8, -32768), 32767), q1 = min(max((int)s1 >> 8, -32768), 32767);
+        *reinterpret_cast<uint32_t*>(c + bt * c_bs + i) = (uint32_t)(uint16_t)q0 | ((uint32_t)q1 << 16);
+    }
+}
+
 // ---------------------------------------------------------------- drivers
 // Byte planes [slices][lines_p][kp] of one operand and its partial line sums
 // [slices][nslab][lines_p].
@@ -1058,13 +1181,14 @@ Planes make_planes(uint32_t lines, uint32_t kp, uint32_t slices, uint32_t align 
 namespace cm {
 namespace {
 
-int matmul_check(uint32_t k, uint32_t gemv_kw, int64_t a_bs, int64_t b_bs, int64_t c_bs) {
+int matmul_check(uint32_t k, uint32_t gemv_kw, int64_t a_bs, int64_t b_bs, int64_t c_bs, uint32_t b_packed = 0) {
     // the limb sums HL + LH stay exact in int32 for k <= 32768
     if (k == 0 || k > 32768) return fail(CM_EINVAL, "matmul: k = %u outside 1 .. 32768", k);
     if (gemv_kw && gemv_kw != 1 && gemv_kw != 2 && gemv_kw != 4 && gemv_kw != 8)
         return fail(CM_EINVAL, "matmul: gemv_kw %u", gemv_kw);
     if (gemv_kw > 1 && (k % (16 * gemv_kw)))
         return fail(CM_EINVAL, "matmul: k %u not a multiple of 16 * gemv_kw", k);
+    if (b_packed > 2 || (b_packed && gemv_kw)) return fail(CM_EINVAL, "matmul: b_packed %u with gemv_kw %u", b_packed, gemv_kw);
     if (a_bs < 0 || b_bs < 0 || c_bs < 0) return fail(CM_EINVAL, "matmul: negative batch stride");
     return CM_OK;
 }
@@ -1082,7 +1206,13 @@ int split_a(const int16_t* a, uint64_t a_slice, uint32_t n, uint32_t k, Planes& 
 // B's planes from its image (row-major, packed 32-column tiles or the GEMV image).
 int split_b(const int16_t* b, uint64_t b_slice, uint32_t k, uint32_t m, uint32_t b_packed, uint32_t gemv_kw,
             Planes& B, hipStream_t s) {
-    const uint32_t layout = gemv_kw ? 2 : (b_packed ? 1 : 0);
+    const uint32_t layout = gemv_kw ? 2 : (b_packed == 2 ? 3 : (b_packed ? 1 : 0));
+    if (layout == 3 && aligned16(b) && (b_slice & 7) == 0 && (k & 7) == 0) {
+        // the transposed image: B's lines are rows with k contiguous, like A's
+        CM_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(B.lines_p / 4, B.nslab, B.slices), dim3(256), 0, s,
+                  b, b_slice, (uint64_t)k, m, k, B.hi, B.lo, B.part, B.lines_p, B.kp, B.nslab);
+        return CM_OK;
+    }
     const bool fast_b = aligned16(b) && (b_slice & 7) == 0 &&
                         (layout == 1 || (layout == 0 && (m & 7) == 0) || (layout == 2 && gemv_kw == 1 && (m & 7) == 0));
     if (fast_b) {
@@ -1091,6 +1221,36 @@ int split_b(const int16_t* b, uint64_t b_slice, uint32_t k, uint32_t m, uint32_t
         return CM_OK;
     }
     return run_split<SrcMatB, false>(SrcMatB{b, m, k, m, layout, gemv_kw}, b_slice, B, s);
+}
+
+// The skinny path of cm_matmul (wrap32, n <= 32): slices of kSkinnyKc k.
+int skinny_wrap(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k, uint32_t m, uint32_t batch,
+                int64_t a_bs, int64_t b_bs, int64_t c_bs, uint32_t b_packed, DeviceState* st, hipStream_t s) {
+    const uint32_t cbs = ceil_div(m, 128), nks = ceil_div(k, kSkinnyKc);
+    if (nks > 65535 || batch > 65535) return fail(CM_EINVAL, "matmul: skinny grid %u x %u x %u", cbs, nks, batch);
+    int32_t* part = nullptr;
+    if (nks > 1) {
+        void* ws;
+        int rc = workspace(st, (size_t)batch * nks * n * m * 4, &ws);
+        if (rc) return rc;
+        part = static_cast<int32_t*>(ws);
+    }
+    const dim3 grid(cbs, nks, batch);
+#define CM_SKINNY(NR, BL)                                                                                         \
+    CM_LAUNCH("skinny_wrap_kernel", (skinny_wrap_kernel<NR, BL>), grid, dim3(64), 0, s, a, (uint64_t)a_bs, b,       \
+              (uint64_t)b_bs, c, (uint64_t)c_bs, part, n, k, m)
+#define CM_SKINNY_BL(NR) \
+    if (b_packed == 2) { CM_SKINNY(NR, 2); } else if (b_packed) { CM_SKINNY(NR, 1); } else { CM_SKINNY(NR, 0); }
+    if (n <= 8) { CM_SKINNY_BL(8) } else if (n <= 16) { CM_SKINNY_BL(16) } else { CM_SKINNY_BL(32) }
+#undef CM_SKINNY_BL
+#undef CM_SKINNY
+    if (nks > 1) {
+        const uint64_t pairs = (uint64_t)batch * n * m / 2;
+        const unsigned blocks = (unsigned)std::min<uint64_t>((pairs + 255) / 256, (uint64_t)st->cus * 8);
+        CM_LAUNCH("skinny_reduce_kernel", skinny_reduce_kernel, dim3(blocks), dim3(256), 0, s, part, c,
+                  (uint64_t)c_bs, n, m, nks, batch);
+    }
+    return CM_OK;
 }
 
 int gemm_out(const Planes& A, const Planes& B, int16_t* c, uint32_t n, uint32_t k, uint32_t m, uint32_t batch,
@@ -1111,9 +1271,14 @@ extern "C" int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_
     int rc = state(&st);
     if (rc) return rc;
     if (n == 0 || m == 0 || batch == 0) return CM_OK;
-    rc = matmul_check(k, gemv_kw, a_bs, b_bs, c_bs);
+    rc = matmul_check(k, gemv_kw, a_bs, b_bs, c_bs, b_packed);
     if (rc) return rc;
     hipStream_t s = as_stream(stream);
+    if (wrap32 && n <= 32 && gemv_kw == 0 && (m & 1) == 0 && (k & 1) == 0 && (reinterpret_cast<uintptr_t>(a) & 3) == 0 &&
+        (reinterpret_cast<uintptr_t>(b) & 3) == 0 && (reinterpret_cast<uintptr_t>(c) & 3) == 0 && (a_bs & 1) == 0 &&
+        (b_bs & 1) == 0 && (c_bs & 1) == 0 && (b_packed != 1 || (m & 31) == 0) &&
+        (b_packed != 2 || ((k & 7) == 0 && aligned16(b) && (b_bs & 7) == 0)))
+        return skinny_wrap(a, b, c, n, k, m, batch, a_bs, b_bs, c_bs, b_packed, st, s);
     const uint32_t kp = (uint32_t)round_up(k, BK);
     const uint32_t sa = (batch > 1 && a_bs != 0) ? batch : 1, sb = (batch > 1 && b_bs != 0) ? batch : 1;
     Planes A = make_planes(n, kp, sa, gemm_tile_rows(n, m, batch, st->cus)), B = make_planes(m, kp, sb);
@@ -1144,7 +1309,7 @@ extern "C" int cm_matmul_split_b(const int16_t* b, void* planes, uint32_t k, uin
     int rc = state(&st);
     if (rc) return rc;
     if (m == 0 || b_slices == 0) return CM_OK;
-    rc = matmul_check(k, gemv_kw, 0, b_bs, 0);
+    rc = matmul_check(k, gemv_kw, 0, b_bs, 0, b_packed);
     if (rc) return rc;
     if (reinterpret_cast<uintptr_t>(planes) & 255) return fail(CM_EALIGN, "matmul: b planes not 256-byte aligned");
     Planes B = make_planes(m, (uint32_t)round_up(k, BK), b_slices);

@@ -234,9 +234,12 @@ class AttnContractNode:
     out[i] = sat16(floor(wrap32(A[i] . B[i]) / 2^8)) for the raw int16 operands A [batch][n][k]
     and B [batch][k][m], the math of LlmAttnConvNode (q.K^T with A = K rows, B = the q image;
     P.V with A = P, B = V rows; llm_nodes.py:995-1001, 1407-1425) over static keys, one call
-    for all pairs.  Output exponent f_a + f_b - 8 (score_exp / pv_exp, graph_builder.py:197-208)."""
+    for all pairs.  Output exponent f_a + f_b - 8 (score_exp / pv_exp, graph_builder.py:197-208).
+    ``b_trans``: B given as [batch][m][k] (out = A . B^T), e.g. q rows against a K cache's rows,
+    the scores then query-major."""
     inputs: List[TensorInfo]
     output: TensorInfo
+    b_trans: bool = False
 
 
 @dataclass

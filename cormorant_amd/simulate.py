@@ -194,6 +194,17 @@ class Simulator:
         if wrap:
             self._check_exponents(at, bt, ot)
         c = self._new(ot, batch * n * m)
+        if bt.data is not None and b_batch == 1 and wrap and n <= 32 and m % 2 == 0 and k % 8 == 0:
+            # a decode-sized product: the library's skinny path reads the weight itself, kept
+            # as its transposed image [m][k] (each column's k contiguous)
+            img = self._images.get(bt.onnx_name + "#trans")
+            if img is None:
+                wt = np.ascontiguousarray(b.cpu().numpy().reshape(k, m).T)
+                img = torch.from_numpy(wt).to(self.device)
+                self._images[bt.onnx_name + "#trans"] = img
+            units.matmul(a.reshape(-1).contiguous(), img, c, n, k, m, batch=batch, a_bs=n * k if a_batch > 1 else 0,
+                         b_bs=0, c_bs=n * m, b_packed=2, wrap32=True)
+            return c
         if bt.data is not None and b_batch == 1:
             # a shared weight: the packed image (the scheduler's packing), split once
             planes = self._images.get(bt.onnx_name)
@@ -376,15 +387,17 @@ class Simulator:
     def _attn_contract(self, sn: AttnContractNode, raw) -> torch.Tensor:
         at, bt, ot = sn.inputs[0], sn.inputs[1], sn.output
         batch, n, k = at.shape
-        if len(bt.shape) != 3 or bt.shape[0] != batch or bt.shape[1] != k or list(ot.shape) != [batch, n, bt.shape[2]]:
+        kb, m = (2, 1) if sn.b_trans else (1, 2)
+        if len(bt.shape) != 3 or bt.shape[0] != batch or bt.shape[kb] != k or list(ot.shape) != [batch, n, bt.shape[m]]:
             raise SchedulerError(f"attention contraction '{ot.onnx_name}': [b][n][k] x [b][k][m] -> [b][n][m]")
         fa, fb, fo = (np.asarray(self._exp(t)).reshape(-1) for t in (at, bt, ot))
         if fa.size != 1 or fb.size != 1 or fo.size != 1 or int(fo[0]) != int(fa[0]) + int(fb[0]) - self._dtype.frac_bits:
             raise SchedulerError(f"attention contraction '{ot.onnx_name}': output exponent is not f_a + f_b - 8")
-        m = int(bt.shape[2])
+        m = int(bt.shape[m])
         c = self._new(ot)
         units.matmul(self._get(at, raw).reshape(-1).contiguous(), self._get(bt, raw).reshape(-1).contiguous(), c,
-                     n, k, m, batch=batch, a_bs=n * k, b_bs=k * m, c_bs=n * m, wrap32=True)
+                     n, k, m, batch=batch, a_bs=n * k, b_bs=k * m, c_bs=n * m, b_packed=2 if sn.b_trans else 0,
+                     wrap32=True)
         return c
 
     def _permute(self, sn: PermuteNode, raw) -> torch.Tensor:

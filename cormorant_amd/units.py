@@ -129,7 +129,7 @@ def copy16(src: torch.Tensor, dst: torch.Tensor, dims, src_strides, dst_strides)
 
 
 def matmul_b_extent(k: int, m: int, b_packed: int, gemv_kw: int) -> int:
-    if gemv_kw:
+    if gemv_kw or b_packed == 2:
         return k * m
     if b_packed:
         return ((m + 31) // 32) * k * 32

@@ -221,7 +221,8 @@ int oracle_vectorop(const int16_t* a, const int16_t* b, int16_t* c, unsigned siz
 
 /* ------------------------------------------------------------------ Matmul */
 /* B[kk][j] of one batch slice in one of the three images (MatmulKernel.h:91-156):
- * row-major [k][m]; packed tile-major (kTileM = 32): ((j/32)*k + kk)*32 + j%32;
+ * row-major [k][m]; packed tile-major (kTileM = 32): ((j/32)*k + kk)*32 + j%32 (packed 2: the
+ * library's transposed image [m][k], j*k + kk);
  * GEMV kernel-width image kw: (c*m + j)*kw + jj with c = (kk/(16kw))*16 + kk%16,
  * jj = (kk/16) % kw (matmul_gemv_index). */
 static i64 mm_b(const int16_t* b, unsigned kk, unsigned j, unsigned k, unsigned m,
@@ -231,6 +232,7 @@ static i64 mm_b(const int16_t* b, unsigned kk, unsigned j, unsigned k, unsigned 
         unsigned c = (kk / (16 * kw)) * 16 + kk % 16, jj = (kk / 16) % kw;
         return b[((size_t)c * m + j) * kw + jj];
     }
+    if (packed == 2) return b[(size_t)j * k + kk];          /* this build's transposed image [m][k] */
     if (packed) return b[((size_t)(j / 32) * k + kk) * 32 + (j % 32)];
     return b[(size_t)kk * m + j];
 }

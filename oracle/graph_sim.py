@@ -223,7 +223,10 @@ def forward(graph, inputs):
         elif isinstance(sn, G.AttnContractNode):
             at, bt = sn.inputs
             ra, rb = _raw_of(at, get(at)), _raw_of(bt, get(bt))
-            acc = np.matmul(ra.astype(np.float64), rb.astype(np.float64))   # |sums| < 2^53: exact
+            rb = rb.reshape(bt.shape)
+            if sn.b_trans:
+                rb = rb.transpose(0, 2, 1)
+            acc = np.matmul(ra.reshape(at.shape).astype(np.float64), rb.astype(np.float64))   # |sums| < 2^53: exact
             fo = float(F if out.exp is None else out.exp)
             vals[out.onnx_name] = (_wrap_floor(acc) / 2.0 ** fo).reshape(out.shape)
         elif isinstance(sn, G.PermuteNode):

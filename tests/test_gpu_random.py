@@ -61,6 +61,24 @@ MM_CASES = [  # n, k, m, batch, a_bs_mode, b_bs_mode, layout, kw, full_range, wr
     (9, 9000, 17, 1, 1, 1, "packed", 0, True, False),      # int64 recombination
     (3, 32768, 5, 1, 1, 1, "row", 0, True, False),
     (3, 32768, 5, 1, 1, 1, "row", 0, True, True),
+    # wrap32 with at most 32 rows: the skinny path (v_dot2 over pairs of k, k split over the grid)
+    (1, 960, 960, 1, 1, 1, "packed", 0, True, True),
+    (16, 2560, 960, 1, 1, 1, "row", 0, True, True),
+    (3, 1024, 64, 80, 1, 1, "row", 0, True, True),
+    (32, 4096, 256, 2, 1, 0, "packed", 0, True, True),
+    (16, 32768, 64, 1, 1, 1, "row", 0, True, True),
+    (5, 2, 32, 1, 1, 1, "packed", 0, True, True),
+    (17, 96, 2, 3, 0, 1, "row", 0, True, True),
+    (9, 200, 640, 1, 1, 1, "row", 0, False, True),
+    # the transposed image [m][k] (b_packed 2): skinny (wrap, <= 32 rows) and plane paths
+    (3, 64, 1024, 80, 1, 1, "trans", 0, True, True),
+    (16, 960, 320, 2, 1, 0, "trans", 0, True, True),
+    (40, 72, 100, 3, 1, 1, "trans", 0, True, True),
+    (64, 256, 96, 2, 1, 1, "trans", 0, True, False),
+    (7, 100, 33, 1, 1, 1, "trans", 0, False, False),
+    (5, 70, 64, 2, 1, 1, "trans", 0, True, True),
+    (32, 136, 258, 2, 0, 1, "trans", 0, True, True),
+    (2, 8, 2, 1, 1, 1, "trans", 0, True, True),
 ]
 
 
@@ -98,16 +116,20 @@ def test_matmul_random(U, oracle_lib, case):
         imgs = [pack_b(x, k, m) for x in bl]
     elif layout == "gemv":
         imgs = [gemv_image(x, k, m, kw) for x in bl]
+    elif layout == "trans":
+        imgs = [np.ascontiguousarray(x.reshape(k, m).T).reshape(-1) for x in bl]
     else:
         imgs = bl
     img_len = len(imgs[0])
     b = np.concatenate(imgs)
     b_bs_img = img_len if bm else 0
-    want = oracle_lib.matmul(a, b, n, k, m, batch, a_bs, b_bs_img, n * m, int(layout == "packed"),
-                             kw if layout == "gemv" else 0, wrap)
+    bp = {"packed": 1, "trans": 2}.get(layout, 0)
+    want = oracle_lib.matmul(a, b, n, k, m, batch, a_bs, b_bs_img, n * m, bp, kw if layout == "gemv" else 0, wrap)
+    if layout == "trans":      # the oracle's transposed image against the row-major product
+        ref = oracle_lib.matmul(a, np.concatenate(bl), n, k, m, batch, a_bs, k * m if bm else 0, n * m, 0, 0, wrap)
+        np.testing.assert_array_equal(want, ref)
     c = poisoned16(batch * n * m + 8)
-    U.matmul(dev16(a), dev16(b), c, n, k, m, batch, a_bs, b_bs_img, n * m, int(layout == "packed"),
-             kw if layout == "gemv" else 0, wrap)
+    U.matmul(dev16(a), dev16(b), c, n, k, m, batch, a_bs, b_bs_img, n * m, bp, kw if layout == "gemv" else 0, wrap)
     got = host(c)
     np.testing.assert_array_equal(got[:batch * n * m], want)
     assert (got[batch * n * m:] == POISON16).all()
