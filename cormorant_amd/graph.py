@@ -243,6 +243,28 @@ class AttnContractNode:
 
 
 @dataclass
+class AttentionNode:
+    """An encoder layer's attention as one node: for each of ``batch`` sequences of ``seq``
+    tokens and each head, Q / K / V from the fused projection ``inputs[0]`` [batch seq][ld]
+    (columns q_off / k_off / v_off + head_dim h), the scores s = K . Q^T keys-major at
+    f_q + f_k - 8, P = the softmax unit's keys-major call with ``cm`` / ``cfg`` (every key
+    valid), o = P . V at f_p + f_v - 8, merged into the output rows [batch seq][heads head_dim]:
+    exactly the reference's chain VitAttnPrep, the q.K^T contraction, VitAttnSoftmaxVopNode,
+    P.V and the merge (vit.py:19-32; llm_nodes.py:995-1001, 1407-1425; smx_nodes.py:121-248)."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    batch: int = 1
+    seq: int = 64
+    heads: int = 1
+    head_dim: int = 64
+    q_off: int = 0
+    k_off: int = 0
+    v_off: int = 0
+    cm: int = 12102203
+    cfg: int = 0x0813
+
+
+@dataclass
 class KvWriteNode:
     """The step's K or V rows into the KV caches: x [B][KV * HD] (row b = sequence b's new
     row) -> cache [B][KV][C][HD] (each sequence's cache group-major) at row ``pos``, the
@@ -277,7 +299,8 @@ def conv_out(size: int, k: int, stride: int, pad_lo: int, pad_hi: int, dil: int 
 
 
 __all__ = ["SchedulerError", "TensorInfo", "ScheduledNode", "MatmulNode", "ConvNode", "PoolNode",
-           "ReshapeNode", "SoftmaxVopNode", "RowOpsNode", "LlmAttnConvNode", "KvWriteNode", "attn_keys", "KEY_QUANTUM",
+           "ReshapeNode", "SoftmaxVopNode", "RowOpsNode", "LlmAttnConvNode", "KvWriteNode", "AttentionNode", "attn_keys",
+           "KEY_QUANTUM",
            "Graph", "conv_out", "OP_ADD", "OP_SUB",
            "OP_MUL", "OP_DIV", "OP_RELU", "OP_RELU6", "OP_SOFTMAX", "OP_SOFTMAX_T", "POOL_MAX",
            "POOL_AVG", "POOL_LP"]

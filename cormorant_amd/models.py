@@ -15,8 +15,8 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import units
-from .graph import (AttnContractNode, ConvNode, Graph, MatmulNode, PermuteNode, PoolNode, ReshapeNode, ScheduledNode,
-                    SoftmaxVopNode, TensorInfo, conv_out, softmax_regs)
+from .graph import (AttentionNode, AttnContractNode, ConvNode, Graph, MatmulNode, PermuteNode, PoolNode, ReshapeNode,
+                    ScheduledNode, SoftmaxVopNode, TensorInfo, conv_out, softmax_regs)
 from .rowops_nodes import LayerNorm32RoNode, ResAddBiasRoNode
 
 
@@ -182,7 +182,7 @@ class BertShape:
         return self.layers * (lin + att)
 
 
-def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int = 1):
+def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int = 1, fused_attention: bool = False):
     """(graph, inputs, exps): the BERT-base-shaped encoder in per-tensor power-of-two numerics.
 
     Token ids U{0 .. vocab-1} and embedding rows N(0, 1) (the embedding lookup is the host
@@ -205,6 +205,9 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
     largest |value|, and each tensor takes the largest exponent that keeps it below 32767
     with a 1.25 margin; the contractions' output exponents follow from their operands', the
     q / v exponents are lowered where the scores or P.V would not fit.  ``exps`` records them.
+    ``fused_attention``: the head split, q.K^T, the softmax, P.V and the merge as one
+    AttentionNode (the same arithmetic in one call, cm_attention); False (faster on the
+    MI355X at this shape): node by node on the plane GEMM.
     """
     from .numeric import encode_matmul_weights
     from .dtype import AP_FIXED_16_8
@@ -291,21 +294,26 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
         qkv = T_(p + "qkv", [rows, 3 * D], exp=np.repeat([e["q"], e["k"], e["v"]], D))
         nodes.append(MatmulNode([x1, wqkv], qkv))
         ld = 3 * D
-        qT = T_(p + "qT", [BH, hd, T], exp=e["q"])
-        kh = T_(p + "kh", [BH, T, hd], exp=e["k"])
-        vh = T_(p + "vh", [BH, T, hd], exp=e["v"])
-        nodes.append(PermuteNode([qkv], qT, dims=(S.batch, H, hd, T), strides=(T * ld, hd, 1, ld), offset=0))
-        nodes.append(PermuteNode([qkv], kh, dims=(S.batch, H, T, hd), strides=(T * ld, hd, ld, 1), offset=D))
-        nodes.append(PermuteNode([qkv], vh, dims=(S.batch, H, T, hd), strides=(T * ld, hd, ld, 1), offset=2 * D))
-        sc = T_(p + "s", [BH, T, T], exp=e["s"])
-        nodes.append(AttnContractNode([kh, qT], sc))
         cmr, cfg = softmax_regs(e["s"], 1.0 / math.sqrt(hd), e["p"])
-        pr = T_(p + "P", [BH, T, T], exp=e["p"])
-        nodes.append(SoftmaxVopNode([sc], pr, cm=cmr, cfg=cfg, keys_major=True))
-        o = T_(p + "o", [BH, T, hd], exp=e["o"])
-        nodes.append(AttnContractNode([pr, vh], o))
         om = T_(p + "om", [rows, D], exp=e["o"])
-        nodes.append(PermuteNode([o], om, dims=(S.batch, T, H, hd), strides=(H * T * hd, hd, T * hd, 1)))
+        if fused_attention:
+            nodes.append(AttentionNode([qkv], om, batch=S.batch, seq=T, heads=H, head_dim=hd, q_off=0, k_off=D,
+                                       v_off=2 * D, cm=cmr, cfg=cfg))
+        else:
+            qT = T_(p + "qT", [BH, hd, T], exp=e["q"])
+            kh = T_(p + "kh", [BH, T, hd], exp=e["k"])
+            vh = T_(p + "vh", [BH, T, hd], exp=e["v"])
+            nodes.append(PermuteNode([qkv], qT, dims=(S.batch, H, hd, T), strides=(T * ld, hd, 1, ld), offset=0))
+            nodes.append(PermuteNode([qkv], kh, dims=(S.batch, H, T, hd), strides=(T * ld, hd, ld, 1), offset=D))
+            nodes.append(PermuteNode([qkv], vh, dims=(S.batch, H, T, hd), strides=(T * ld, hd, ld, 1),
+                                     offset=2 * D))
+            sc = T_(p + "s", [BH, T, T], exp=e["s"])
+            nodes.append(AttnContractNode([kh, qT], sc))
+            pr = T_(p + "P", [BH, T, T], exp=e["p"])
+            nodes.append(SoftmaxVopNode([sc], pr, cm=cmr, cfg=cfg, keys_major=True))
+            o = T_(p + "o", [BH, T, hd], exp=e["o"])
+            nodes.append(AttnContractNode([pr, vh], o))
+            nodes.append(PermuteNode([o], om, dims=(S.batch, T, H, hd), strides=(H * T * hd, hd, T * hd, 1)))
         wo = T_(p + "wo", [D, D], data=L["wo"])
         ao = T_(p + "ao", [rows, D], exp=e["ao"])
         nodes.append(MatmulNode([om, wo], ao))

@@ -16,9 +16,9 @@ import torch
 
 from . import units
 from .dtype import AP_FIXED_16_8, ApFixed16
-from .graph import (AttnContractNode, ConvNode, Graph, KvWriteNode, LlmAttnConvNode, MatmulNode, PermuteNode,
-                    PoolNode, ReshapeNode, RowOpsNode, ScheduledNode, SchedulerError, SoftmaxVopNode, TensorInfo,
-                    attn_keys)
+from .graph import (AttentionNode, AttnContractNode, ConvNode, Graph, KvWriteNode, LlmAttnConvNode, MatmulNode,
+                    PermuteNode, PoolNode, ReshapeNode, RowOpsNode, ScheduledNode, SchedulerError, SoftmaxVopNode,
+                    TensorInfo, attn_keys)
 from .packing import conv_bias_image, conv_weight_image, pack_matmul_b
 from .rowops_nodes import RoJob, RowOpsAdapter
 
@@ -92,6 +92,8 @@ class Simulator:
                 raw[sn.output.onnx_name] = self._attn_contract(sn, raw)
             elif isinstance(sn, KvWriteNode):
                 raw[sn.output.onnx_name] = self._kv_write(sn, raw)
+            elif isinstance(sn, AttentionNode):
+                raw[sn.output.onnx_name] = self._attention(sn, raw)
             elif isinstance(sn, ScheduledNode):
                 raw[sn.output.onnx_name] = self._vectorop(sn, raw)
             else:
@@ -424,6 +426,50 @@ class Simulator:
         buf = torch.zeros((rows, per), dtype=_TORCH[kind], device=self.device)
         buf[:, :w] = x2d
         return buf, per * _KB[kind], per
+
+    def _attention(self, sn: AttentionNode, raw) -> torch.Tensor:
+        """An encoder layer's attention: one cm_attention call, or (shapes it does not take) the
+        head split, the two contractions and the softmax unit call by call."""
+        xt, ot = sn.inputs[0], sn.output
+        B, T, H, hd = sn.batch, sn.seq, sn.heads, sn.head_dim
+        ld, cols = int(xt.shape[-1]), sn.heads * sn.head_dim
+        if list(xt.shape) != [B * T, ld] or list(ot.shape) != [B * T, cols]:
+            raise SchedulerError(f"attention '{ot.onnx_name}': qkv [{B * T}][ld] -> o [{B * T}][{cols}]")
+        fx = np.broadcast_to(np.asarray(self._exp(xt)).reshape(-1), (ld,))
+        f = {}
+        for key, off in (("q", sn.q_off), ("k", sn.k_off), ("v", sn.v_off)):
+            e = fx[off:off + cols]
+            if e.size != cols or (e != e[0]).any():
+                raise SchedulerError(f"attention '{ot.onnx_name}': {key} columns at one exponent")
+            f[key] = int(e[0])
+        fo = np.asarray(self._exp(ot)).reshape(-1)
+        fp = (sn.cfg >> 8) & 31
+        if fo.size != 1 or int(fo[0]) != fp + f["v"] - self._dtype.frac_bits:
+            raise SchedulerError(f"attention '{ot.onnx_name}': output exponent is not f_p + f_v - 8")
+        x = self._get(xt, raw).reshape(-1)
+        o = self._new(ot)
+        if (hd == 64 and T in (64, 128, 256, 384) and ld % 8 == 0 and cols % 8 == 0
+                and sn.q_off % 8 == 0 and sn.k_off % 8 == 0 and sn.v_off % 8 == 0):
+            units.attention(x, o, B, T, H, hd, ld, sn.q_off, sn.k_off, sn.v_off, cols, sn.cm, sn.cfg)
+            return o
+        if T % 16:
+            raise SchedulerError(f"attention '{ot.onnx_name}': the keys-major softmax takes query blocks of 16")
+        BH, dev = B * H, self.device
+        qT = torch.empty(BH * hd * T, dtype=torch.int16, device=dev)
+        kh = torch.empty(BH * T * hd, dtype=torch.int16, device=dev)
+        vh = torch.empty(BH * T * hd, dtype=torch.int16, device=dev)
+        units.permute16(x[sn.q_off:], qT, (B, H, hd, T), (T * ld, hd, 1, ld))
+        units.permute16(x[sn.k_off:], kh, (B, H, T, hd), (T * ld, hd, ld, 1))
+        units.permute16(x[sn.v_off:], vh, (B, H, T, hd), (T * ld, hd, ld, 1))
+        sc = torch.empty(BH * T * T, dtype=torch.int16, device=dev)
+        units.matmul(kh, qT, sc, T, hd, T, batch=BH, a_bs=T * hd, b_bs=hd * T, c_bs=T * T, wrap32=True)
+        kp = _pad8(T)
+        pr = torch.empty(BH * T * kp, dtype=torch.int16, device=dev)
+        units.softmax(sc, pr, T, units.OP_SOFTMAX_T, T, T, kp, sn.cm, sn.cfg, T, batch=BH, a_bs=T * T, c_bs=T * kp)
+        oh = torch.empty(BH * T * hd, dtype=torch.int16, device=dev)
+        units.matmul(pr, vh, oh, T, T, hd, batch=BH, a_bs=T * kp, b_bs=T * hd, c_bs=T * hd, wrap32=True)
+        units.permute16(oh, o, (B, T, H, hd), (H * T * hd, hd, T * hd, 1))
+        return o
 
     def _kv_write(self, sn: KvWriteNode, raw) -> torch.Tensor:
         """Row ``pos`` of every sequence's group-major cache from the step's rows, in place."""

@@ -128,6 +128,23 @@ def copy16(src: torch.Tensor, dst: torch.Tensor, dims, src_strides, dst_strides)
     return dst
 
 
+def attention(qkv: torch.Tensor, o: torch.Tensor, batch: int, seq: int, heads: int, head_dim: int, ld: int,
+              q_off: int, k_off: int, v_off: int, o_ld: int, smx_cm: int, smx_cfg: int) -> torch.Tensor:
+    """An encoder layer's attention in one call (cm_attention): q.K^T, the keys-major softmax and
+    P.V per (sequence, head), Q / K / V read from the fused projection's rows, o merged."""
+    if batch and heads:
+        cols = heads * head_dim
+        for off in (q_off, k_off, v_off):
+            if off < 0 or off + cols > ld:
+                raise ValueError("attention: head columns past the row")
+        _require(qkv, "qkv", torch.int16, (batch * seq - 1) * ld + max(q_off, k_off, v_off) + cols)
+        _require(o, "o", torch.int16, (batch * seq - 1) * o_ld + cols)
+    rc = _lib.lib().cm_attention(_ptr(qkv), _ptr(o), batch, seq, heads, head_dim, ld, q_off, k_off, v_off, o_ld,
+                                 smx_cm, smx_cfg, _stream())
+    _lib.check(rc, "cm_attention")
+    return o
+
+
 def matmul_b_extent(k: int, m: int, b_packed: int, gemv_kw: int) -> int:
     if gemv_kw or b_packed == 2:
         return k * m

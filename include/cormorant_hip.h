@@ -217,6 +217,22 @@ int cm_copy16(const int16_t* src, int16_t* dst, uint32_t d0, uint32_t d1, uint32
               uint64_t s0, uint64_t s1, uint64_t s2, uint64_t s3, uint64_t t0, uint64_t t1, uint64_t t2,
               uint64_t t3, void* stream);
 
+/* ---------------------------------------------------------------- Attention (composed)
+ * The attention of an encoder layer in one call -- no counterpart among the reference's
+ * units: the composition of VitAttnPrep (head split), the q.K^T contraction (the arithmetic
+ * of LlmAttnConvNode, int32 wrap), VitAttnSoftmaxVopNode's keys-major softmax (VectorOP op 11,
+ * every key valid), the P.V contraction and the head merge (vit.py:19-32,
+ * llm_nodes.py:995-1001 and 1407-1425, smx_nodes.py:121-248), exactly as those calls in turn
+ * compute it.  For sequence b of `batch` (seq tokens, rows of qkv ld elements apart from
+ * qkv + b*seq*ld) and head h of `heads` (head_dim 64): Q, K, V at columns q_off, k_off, v_off
+ * + 64 h; s[j][i] = sat16(wrap32(K[j].Q[i]) >> 8); P[i][.] = the softmax unit over the keys of
+ * query i with smx_cm / smx_cfg; o[i][d] = sat16(wrap32(sum_j P[i][j] V[j][d]) >> 8), written to
+ * o + (b*seq + i)*o_ld + 64 h + d.  seq in {64, 128, 256, 384}; 16-byte aligned rows and
+ * column offsets. */
+int cm_attention(const int16_t* qkv, int16_t* o, uint32_t batch, uint32_t seq, uint32_t heads, uint32_t head_dim,
+                 uint64_t ld, uint32_t q_off, uint32_t k_off, uint32_t v_off, uint64_t o_ld, uint32_t smx_cm,
+                 uint32_t smx_cfg, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -6,7 +6,7 @@ import math
 import numpy as np
 
 from cormorant_amd import models
-from cormorant_amd.graph import AttnContractNode, PermuteNode, SoftmaxVopNode, TensorInfo, softmax_regs
+from cormorant_amd.graph import AttentionNode, AttnContractNode, PermuteNode, SoftmaxVopNode, TensorInfo, softmax_regs
 
 SMALL = models.BertShape(layers=2, batch=2, seq=64, d=128, heads=2, ff=512, vocab=1000)
 
@@ -34,7 +34,7 @@ def test_permute_gather_is_the_transpose():
 
 
 def test_encoder_exponents_and_structure():
-    g, inputs, exps = models.bert_encoder(SMALL, seed=1)
+    g, inputs, exps = models.bert_encoder(SMALL, seed=1, fused_attention=False)
     assert inputs["h0"].shape == (SMALL.batch * SMALL.seq, SMALL.d)
     assert np.array_equal(inputs["h0"] * 2 ** 15, np.round(inputs["h0"] * 2 ** 15))
     for e in exps:
@@ -47,8 +47,28 @@ def test_encoder_exponents_and_structure():
         assert sn.output.exp == a.exp + b.exp - 8
     smx = [sn for sn in g.nodes if isinstance(sn, SoftmaxVopNode)]
     assert all(sn.keys_major for sn in smx) and len(smx) == SMALL.layers
+    gf, _, ef = models.bert_encoder(SMALL, seed=1, fused_attention=True)
+    att = [sn for sn in gf.nodes if isinstance(sn, AttentionNode)]
+    assert ef == exps and len(att) == SMALL.layers
+    for sn, sm in zip(att, smx):
+        assert (sn.cm, sn.cfg) == (sm.cm, sm.cfg) and (sn.q_off, sn.k_off, sn.v_off) == (0, SMALL.d, 2 * SMALL.d)
 
 
 def test_full_shape_macs():
     # 12 x 3072 x (4 x 768^2 + 2 x 768 x 3072) + 2 x 8 x 12 x 384^2 x 64 x 12
     assert models.BertShape().macs() == 260_919_263_232 + 21_743_271_936
+
+
+def test_fused_attention_oracle_equals_node_by_node():
+    """The oracle's AttentionNode (one composed step) against the node-by-node chain (head
+    split, q.K^T contraction, keys-major softmax, P.V, merge): the same output bits."""
+    from oracle import graph_sim
+    shape = models.BertShape(layers=1, batch=2, seq=32, d=128, heads=2, ff=256, vocab=500)
+    gf, inf, ef = models.bert_encoder(shape, seed=5, fused_attention=True)
+    gu, inu, eu = models.bert_encoder(shape, seed=5, fused_attention=False)
+    assert ef == eu
+    of = graph_sim.forward(gf, inf)
+    ou = graph_sim.forward(gu, inu)
+    name = gf.output_tensors[0].onnx_name
+    np.testing.assert_array_equal(of[name], ou[name])
+    np.testing.assert_array_equal(of["l0.om"], ou["l0.om"])

@@ -12,12 +12,16 @@ from oracle import graph_sim as oracle_graph
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("shape,seed", [
-    (models.BertShape(layers=2, batch=2, seq=64, d=128, heads=2, ff=512, vocab=1000), 1),
-    (models.BertShape(layers=1, batch=1, seq=384, d=768, heads=12, ff=3072, vocab=30522), 2),
+@pytest.mark.parametrize("shape,seed,fused", [
+    (models.BertShape(layers=2, batch=2, seq=64, d=128, heads=2, ff=512, vocab=1000), 1, True),
+    (models.BertShape(layers=2, batch=2, seq=64, d=128, heads=2, ff=512, vocab=1000), 1, False),
+    (models.BertShape(layers=1, batch=3, seq=128, d=192, heads=3, ff=256, vocab=1000), 3, True),
+    (models.BertShape(layers=1, batch=1, seq=256, d=128, heads=2, ff=256, vocab=1000), 4, True),
+    (models.BertShape(layers=1, batch=1, seq=384, d=768, heads=12, ff=3072, vocab=30522), 2, True),
+    (models.BertShape(layers=1, batch=1, seq=384, d=768, heads=12, ff=3072, vocab=30522), 2, False),
 ])
-def test_encoder_every_tensor(shape, seed):
-    g, inputs, _ = models.bert_encoder(shape, seed=seed)
+def test_encoder_every_tensor(shape, seed, fused):
+    g, inputs, _ = models.bert_encoder(shape, seed=seed, fused_attention=fused)
     got = Simulator(g)._forward_pass(inputs)
     want = oracle_graph.forward(g, inputs)
     for name, v in got.items():
