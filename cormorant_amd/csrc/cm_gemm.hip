@@ -220,6 +220,50 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const int16_t* __restri
     if (lane == 0) part[((uint64_t)bt * nslab + slab) * lines_p + row] = sum;
 }
 
+// Rows of at most 256 k (kp in {64, 128, 192, 256}: one slab): G lanes per row (kp / 8, and 32
+// for kp 192 with the last 8 idle), one 16-byte load each, 64 / G rows per wavefront, the row
+// sum over the row's lane group.
+// Grid (ceil(lines_p / (4 * 64 / G)), 1, slices).
+template <uint32_t G>
+__global__ __launch_bounds__(256) void split_rows_short_kernel(const int16_t* __restrict__ src, uint64_t slice,
+                                                               uint64_t lda, uint32_t rows, uint32_t k,
+                                                               int8_t* __restrict__ hi, int8_t* __restrict__ lo,
+                                                               int32_t* __restrict__ part, uint32_t lines_p,
+                                                               uint32_t kp) {
+    constexpr uint32_t RPW = 64 / G;                       // rows per wavefront
+    const uint32_t lane = threadIdx.x & 63, g = lane % G;
+    const uint32_t row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / G, bt = blockIdx.z;
+    const uint32_t k0 = 8 * g;
+    const bool in = row < lines_p && k0 < kp, real_row = row < rows;
+    int4 v = make_int4(0, 0, 0, 0);
+    int32_t sum = 0;
+    if (in) {
+        const int16_t* r = src + bt * slice + (uint64_t)row * lda;
+        if (real_row && k0 + 8 <= k) {
+            v = *reinterpret_cast<const int4*>(r + k0);
+            sum = sum8(v);
+        } else {
+            int16_t e[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const bool re = real_row && k0 + q < k;
+                e[q] = re ? r[k0 + q] : kPad;
+                sum += re ? e[q] : 0;
+            }
+            v = *reinterpret_cast<const int4*>(e);
+        }
+    }
+#pragma unroll
+    for (uint32_t off = 1; off < G; off <<= 1) sum += __shfl_xor(sum, off, 64);
+    if (!in) return;
+    uint2 h, l;
+    split8(v, h, l);
+    const uint64_t po = ((uint64_t)bt * lines_p + row) * kp + k0;
+    *reinterpret_cast<uint2*>(hi + po) = h;
+    *reinterpret_cast<uint2*>(lo + po) = l;
+    if (g == 0) part[(uint64_t)bt * lines_p + row] = sum;
+}
+
 // Columns of a k-major image (row-major B [k][m] with m % 8 == 0, or the packed 32-column
 // tiles).  A wavefront takes 32 columns and 256 k of one SLAB: lane = (r4, c8) with
 // r4 = lane / 4 picking 4 consecutive k of each 64-k group and c8 = lane % 4 picking 8
@@ -1193,13 +1237,26 @@ int matmul_check(uint32_t k, uint32_t gemv_kw, int64_t a_bs, int64_t b_bs, int64
     return CM_OK;
 }
 
-// A's planes: row-major [n][k] slices at a_slice elements (0: one slice).
-int split_a(const int16_t* a, uint64_t a_slice, uint32_t n, uint32_t k, Planes& A, hipStream_t s) {
-    if (aligned16(a) && (k & 7) == 0 && (a_slice & 7) == 0) {
-        CM_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(A.lines_p / 4, A.nslab, A.slices), dim3(256), 0, s,
-                  a, a_slice, (uint64_t)k, n, k, A.hi, A.lo, A.part, A.lines_p, A.kp, A.nslab);
+// Planes of rows with k contiguous (lda elements apart, 16-byte aligned): the short-row
+// kernel for kp <= 256, else a wavefront per row and slab.
+int split_row_lines(const int16_t* a, uint64_t a_slice, uint64_t lda, uint32_t n, uint32_t k, Planes& P,
+                    hipStream_t s) {
+    if (P.kp <= 256) {
+#define CM_SHORT(G)                                                                                            \
+    CM_LAUNCH("split_rows_kernel", split_rows_short_kernel<G>, dim3(ceil_div(P.lines_p, 4 * (64 / G)), 1, P.slices), \
+              dim3(256), 0, s, a, a_slice, lda, n, k, P.hi, P.lo, P.part, P.lines_p, P.kp)
+        if (P.kp == 64) { CM_SHORT(8); } else if (P.kp == 128) { CM_SHORT(16); } else { CM_SHORT(32); }
+#undef CM_SHORT
         return CM_OK;
     }
+    CM_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(P.lines_p / 4, P.nslab, P.slices), dim3(256), 0, s, a,
+              a_slice, lda, n, k, P.hi, P.lo, P.part, P.lines_p, P.kp, P.nslab);
+    return CM_OK;
+}
+
+// A's planes: row-major [n][k] slices at a_slice elements (0: one slice).
+int split_a(const int16_t* a, uint64_t a_slice, uint32_t n, uint32_t k, Planes& A, hipStream_t s) {
+    if (aligned16(a) && (k & 7) == 0 && (a_slice & 7) == 0) return split_row_lines(a, a_slice, k, n, k, A, s);
     return run_split<SrcRowMajor, true>(SrcRowMajor{a, n, k, k}, a_slice, A, s);
 }
 
@@ -1207,12 +1264,8 @@ int split_a(const int16_t* a, uint64_t a_slice, uint32_t n, uint32_t k, Planes& 
 int split_b(const int16_t* b, uint64_t b_slice, uint32_t k, uint32_t m, uint32_t b_packed, uint32_t gemv_kw,
             Planes& B, hipStream_t s) {
     const uint32_t layout = gemv_kw ? 2 : (b_packed == 2 ? 3 : (b_packed ? 1 : 0));
-    if (layout == 3 && aligned16(b) && (b_slice & 7) == 0 && (k & 7) == 0) {
-        // the transposed image: B's lines are rows with k contiguous, like A's
-        CM_LAUNCH("split_rows_kernel", split_rows_kernel, dim3(B.lines_p / 4, B.nslab, B.slices), dim3(256), 0, s,
-                  b, b_slice, (uint64_t)k, m, k, B.hi, B.lo, B.part, B.lines_p, B.kp, B.nslab);
-        return CM_OK;
-    }
+    if (layout == 3 && aligned16(b) && (b_slice & 7) == 0 && (k & 7) == 0)
+        return split_row_lines(b, b_slice, k, m, k, B, s);    // B's lines are rows with k contiguous
     const bool fast_b = aligned16(b) && (b_slice & 7) == 0 &&
                         (layout == 1 || (layout == 0 && (m & 7) == 0) || (layout == 2 && gemv_kw == 1 && (m & 7) == 0));
     if (fast_b) {

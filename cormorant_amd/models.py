@@ -191,8 +191,8 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
 
         x  = LayerNorm32(h)                          row-ops NORM, int32 -> int16
         qkv = x . Wqkv                               MatMul (pow2, int32 wrap)
-        q^T, K, V per head                           Permute (the head split)
-        s  = K . q^T   [B H][keys][queries]          batched MatMul, f_s = f_q + f_k - 8
+        q, K, V rows per head                        Permute (the head split)
+        s  = K . q^T   [B H][keys][queries]          batched MatMul (q rows as B^T), f_s = f_q + f_k - 8
         P  = softmax over keys (column mode)         VectorOP softmax, logit scale 1/sqrt(hd)
         o  = P . V     [B H][queries][hd]            batched MatMul, f_o = f_p + f_v - 8
         h1 = ResAddBias(h, merge(o) . Wo, bo)        Permute, MatMul, row-ops ADDX
@@ -300,15 +300,16 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
             nodes.append(AttentionNode([qkv], om, batch=S.batch, seq=T, heads=H, head_dim=hd, q_off=0, k_off=D,
                                        v_off=2 * D, cm=cmr, cfg=cfg))
         else:
-            qT = T_(p + "qT", [BH, hd, T], exp=e["q"])
+            qh = T_(p + "qh", [BH, T, hd], exp=e["q"])
             kh = T_(p + "kh", [BH, T, hd], exp=e["k"])
             vh = T_(p + "vh", [BH, T, hd], exp=e["v"])
-            nodes.append(PermuteNode([qkv], qT, dims=(S.batch, H, hd, T), strides=(T * ld, hd, 1, ld), offset=0))
+            nodes.append(PermuteNode([qkv], qh, dims=(S.batch, H, T, hd), strides=(T * ld, hd, ld, 1), offset=0))
             nodes.append(PermuteNode([qkv], kh, dims=(S.batch, H, T, hd), strides=(T * ld, hd, ld, 1), offset=D))
             nodes.append(PermuteNode([qkv], vh, dims=(S.batch, H, T, hd), strides=(T * ld, hd, ld, 1),
                                      offset=2 * D))
+            # s[j][i] = K[j] . Q[i]: the q rows as the transposed B image (no q transpose)
             sc = T_(p + "s", [BH, T, T], exp=e["s"])
-            nodes.append(AttnContractNode([kh, qT], sc))
+            nodes.append(AttnContractNode([kh, qh], sc, b_trans=True))
             pr = T_(p + "P", [BH, T, T], exp=e["p"])
             nodes.append(SoftmaxVopNode([sc], pr, cm=cmr, cfg=cfg, keys_major=True))
             o = T_(p + "o", [BH, T, hd], exp=e["o"])

@@ -79,6 +79,12 @@ MM_CASES = [  # n, k, m, batch, a_bs_mode, b_bs_mode, layout, kw, full_range, wr
     (5, 70, 64, 2, 1, 1, "trans", 0, True, True),
     (32, 136, 258, 2, 0, 1, "trans", 0, True, True),
     (2, 8, 2, 1, 1, 1, "trans", 0, True, True),
+    # rows of at most 256 k through the short-row split (kp 64 / 128 / 192 / 256), both operands
+    (100, 64, 96, 2, 1, 1, "row", 0, True, False),
+    (70, 184, 40, 2, 1, 1, "trans", 0, True, True),
+    (48, 120, 136, 3, 1, 1, "trans", 0, False, False),
+    (33, 256, 64, 2, 1, 0, "row", 0, True, True),
+    (130, 192, 72, 1, 1, 1, "trans", 0, True, False),
 ]
 
 
