@@ -497,7 +497,9 @@ struct EpiConv {                // y pattern (ConvKernel.h:250-258); acc seeded 
 //     int32 and cannot change a saturated result (|2^8 HH| > 2^30 then decides the sign);
 //   kWrap: the sum wrapped to int32 first, i.e. floor(acc / 2^8) mod 2^24, sign-extended;
 //   kSatWide (K > 8192, saturating): the sum in int64.
-enum : uint32_t { kSatNarrow = 0, kWrap = 1, kSatWide = 2 };
+//   kPartial (wrap products split over k): the slice's 2^16 HH + 2^8 MID + LL mod 2^32 as an
+//     int32 partial; gemm_reduce_kernel adds the slices, the sum terms and the output rule.
+enum : uint32_t { kSatNarrow = 0, kWrap = 1, kSatWide = 2, kPartial = 3 };
 
 __device__ __forceinline__ int32_t clamp_i32(int32_t v, int32_t lo, int32_t hi) {   // v_med3_i32
     return min(max(v, lo), hi);
@@ -567,8 +569,81 @@ __device__ __forceinline__ void store_wave_tile(const v16i (&hh)[2][2], const v1
     }
 }
 
+// One wave's 64 x 64 int32 partials (layout as store_wave_tile) into [rows][cols] at `out`.
+__device__ __forceinline__ void store_wave_partial(const v16i (&hh)[2][2], const v16i (&mid)[2][2],
+                                                   const v16i (&ll)[2][2], int32_t* __restrict__ out, uint32_t rows,
+                                                   uint32_t cols, uint32_t row0, uint32_t col0, uint32_t wr,
+                                                   uint32_t wc, uint32_t l32, uint32_t lh) {
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const uint32_t col = col0 + wc * 64 + j * 32 + l32;
+        if (col >= cols) continue;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t row = row0 + wr * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (row < rows)
+                    out[(uint64_t)row * cols + col] =
+                        (int32_t)(((uint32_t)hh[i][j][r] << 16) + ((uint32_t)mid[i][j][r] << 8) + (uint32_t)ll[i][j][r]);
+            }
+    }
+}
+
+// The wrap products split over k: sum of the slices' partials (mod 2^32) + 128 rowsum + 128
+// colsum - 16384 K, then sat16(>> 8) -- the kWrap rule of the unsplit kernel.  A lane per 8
+// outputs of a row (m % 8 == 0, 16-byte aligned C rows) or per output.
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const int32_t* __restrict__ part, const int32_t* __restrict__ rpart,
+                                                          uint64_t rp_slice, uint32_t a_lines,
+                                                          const int32_t* __restrict__ cpart, uint64_t cp_slice,
+                                                          uint32_t b_lines, uint32_t nslab, int16_t* __restrict__ c,
+                                                          uint64_t c_bs, uint32_t n, uint32_t m, uint32_t nz,
+                                                          uint32_t batch, uint32_t k, uint32_t vec) {
+    const uint64_t per = (uint64_t)n * m;
+    const uint32_t w = vec ? 8u : 1u;
+    const uint64_t total = per / w * batch;
+    for (uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t bt = e / (per / w), i = (e - bt * (per / w)) * w;
+        const uint32_t row = (uint32_t)(i / m), col = (uint32_t)(i - (uint64_t)row * m);
+        int32_t rs = 0;
+        for (uint32_t q = 0; q < nslab; q++) rs += rpart[bt * rp_slice + (uint64_t)q * a_lines + row];
+        const uint32_t base = 128u * (uint32_t)rs - 16384u * k;
+        if (vec) {
+            uint32_t acc[8];
+#pragma unroll
+            for (int t = 0; t < 8; t++) acc[t] = base;
+            for (uint32_t z = 0; z < nz; z++) {
+                const int4* pz = reinterpret_cast<const int4*>(part + (bt * nz + z) * per + i);
+                const int4 u = pz[0], v = pz[1];
+                acc[0] += u.x; acc[1] += u.y; acc[2] += u.z; acc[3] += u.w;
+                acc[4] += v.x; acc[5] += v.y; acc[6] += v.z; acc[7] += v.w;
+            }
+            for (uint32_t q = 0; q < nslab; q++) {
+                const int4* cz = reinterpret_cast<const int4*>(cpart + bt * cp_slice + (uint64_t)q * b_lines + col);
+                const int4 u = cz[0], v = cz[1];
+                acc[0] += 128u * u.x; acc[1] += 128u * u.y; acc[2] += 128u * u.z; acc[3] += 128u * u.w;
+                acc[4] += 128u * v.x; acc[5] += 128u * v.y; acc[6] += 128u * v.z; acc[7] += 128u * v.w;
+            }
+            uint32_t o[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int q0 = min(max((int32_t)acc[2 * t] >> 8, -32768), 32767);
+                const int q1 = min(max((int32_t)acc[2 * t + 1] >> 8, -32768), 32767);
+                o[t] = (uint32_t)(uint16_t)q0 | ((uint32_t)q1 << 16);
+            }
+            *reinterpret_cast<uint4*>(c + bt * c_bs + (uint64_t)row * m + col) = make_uint4(o[0], o[1], o[2], o[3]);
+        } else {
+            uint32_t acc = base;
+            for (uint32_t z = 0; z < nz; z++) acc += (uint32_t)part[(bt * nz + z) * per + i];
+            for (uint32_t q = 0; q < nslab; q++) acc += 128u * (uint32_t)cpart[bt * cp_slice + (uint64_t)q * b_lines + col];
+            c[bt * c_bs + (uint64_t)row * m + col] = (int16_t)min(max((int32_t)acc >> 8, -32768), 32767);
+        }
+    }
+}
+
 // ---------------------------------------------------------------- the plane GEMM
-// Grid: x = output tiles of one slice (XCD-aware order), y = batch slice.  a_slice /
+// Grid: x = output tiles of one slice (XCD-aware order), y = batch slice, z = k slice (with
+// `ksteps` k steps each; 0: no split).  a_slice /
 // b_slice: plane bytes per slice (0 = broadcast); the row / column partial sums per SLAB of
 // k sit at part[(slice * nslab + s) * lines + line] (slice stride 0 = broadcast).
 //
@@ -598,7 +673,7 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
     uint64_t a_slice, uint64_t rp_slice, uint32_t a_lines, const int8_t* __restrict__ Bhi,
     const int8_t* __restrict__ Blo, const int32_t* __restrict__ cpart, uint64_t b_slice, uint64_t cp_slice,
     uint32_t b_lines, uint32_t nslab, uint32_t tiles_r, uint32_t tiles_c, uint32_t kp, int32_t k64,
-    uint32_t mode, Epi epi) {
+    uint32_t mode, int32_t* __restrict__ pout, uint32_t ksteps, Epi epi) {
     constexpr int TM = 64 * WR;                  // tile rows
     constexpr int NT = 128 * WR;                 // threads
     constexpr int NW = 2 * WR;                   // waves
@@ -622,14 +697,15 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
     uint32_t g = blockIdx.x;
     if ((ntiles & 7) == 0) g = (g & 7) * (ntiles >> 3) + (g >> 3);
     const uint32_t tr = g % tiles_r, tc = g / tiles_r;
-    const uint32_t bt = blockIdx.y;
+    const uint32_t bt = blockIdx.y, kz = blockIdx.z;
+    const uint32_t kbeg = ksteps ? kz * ksteps : 0;
 
     const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const uint32_t wr = wave >> 1, wc = wave & 1, l32 = lane & 31, lh = lane >> 5;
 
     // row / column terms of the epilogue, summed from the slab partials now so that their
     // loads overlap the first copies
-    for (uint32_t e = t; e < TM + BN; e += NT) {
+    for (uint32_t e = t; e < (mode == kPartial ? 0u : TM + BN); e += NT) {
         const bool is_row = e < TM;
         const uint32_t line = is_row ? tr * TM + e : tc * BN + (e - TM);
         const int32_t* pp = is_row ? rpart + bt * rp_slice + line : cpart + bt * cp_slice + line;
@@ -644,7 +720,8 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
     // from BCP w of each B plane; lane l takes row 16 b + l / 4, physical chunk l % 4 =
     // logical chunk (l % 4) ^ swizzle (the swizzle depends on l / 4 only)
     const uint32_t lrow = lane >> 2, cchunk = ((lane & 3) ^ ((lrow >> 2) & 3)) * 16;
-    const uint64_t a_base = bt * a_slice + (uint64_t)tr * TM * kp, b_base = bt * b_slice + (uint64_t)tc * BN * kp;
+    const uint64_t a_base = bt * a_slice + (uint64_t)tr * TM * kp + (uint64_t)kbeg * BK;
+    const uint64_t b_base = bt * b_slice + (uint64_t)tc * BN * kp + (uint64_t)kbeg * BK;
     const int8_t* ah_src = Ahi + a_base + (uint64_t)(32 * wave + lrow) * kp + cchunk;
     const int8_t* al_src = Alo + a_base + (uint64_t)(32 * wave + lrow) * kp + cchunk;
     const int8_t* bh_src = Bhi + b_base + (uint64_t)(16 * BCP * wave + lrow) * kp + cchunk;
@@ -665,7 +742,7 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
         for (int j = 0; j < 2; j++) hh[i][j] = mid[i][j] = ll[i][j] = v16i{};
     v4i ah[2], al[2], bh[2], bl[2];
 
-    const uint32_t nk = kp / BK;
+    const uint32_t nk = ksteps ? min(ksteps, kp / BK - kbeg) : kp / BK;
     // Copy group: the two waves sharing a SIMD (w and w + 4 of 8, as dispatched) issue
     // their copies in different substeps.  With 4 waves per workgroup all are group 0.
     const uint32_t cgrp = NW == 8 ? __builtin_amdgcn_readfirstlane((wave >> 2) & 1) : 0;
@@ -767,7 +844,10 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
     // ---- epilogue: one uniform dispatch to the store routine of this mode
     const uint32_t row0 = tr * TM, col0 = tc * BN;
 #define CM_STORE(M, P) store_wave_tile<M, P>(hh, mid, ll, rterm, cterm, bt, row0, col0, wr, wc, l32, lh, epi)
-    if (mode == kSatNarrow) {
+    if (mode == kPartial) {
+        store_wave_partial(hh, mid, ll, pout + ((uint64_t)bt * gridDim.z + kz) * epi.rows * epi.cols, epi.rows,
+                           epi.cols, row0, col0, wr, wc, l32, lh);
+    } else if (mode == kSatNarrow) {
         if (epi.pairs) CM_STORE(kSatNarrow, true); else CM_STORE(kSatNarrow, false);
     } else if (mode == kWrap) {
         if (epi.pairs) CM_STORE(kWrap, true); else CM_STORE(kWrap, false);
@@ -1181,7 +1261,8 @@ uint32_t gemm_tile_rows(uint32_t n, uint32_t m, uint32_t batch, uint32_t cus) {
 }
 
 template <class Epi>
-int run_gemm(const Planes& A, const Planes& B, uint32_t batch, uint32_t k, Epi epi, hipStream_t s) {
+int run_gemm(const Planes& A, const Planes& B, uint32_t batch, uint32_t k, Epi epi, hipStream_t s,
+             int32_t* pout = nullptr, uint32_t ksteps = 0) {
     const uint32_t tm = A.tile;
     const uint32_t tiles_r = ceil_div(A.rows, tm), tiles_c = B.lines_p / BN;
     if (tm != 64 && tm != 128 && tm != 256) return fail(CM_EINVAL, "gemm: tile rows %u", tm);
@@ -1190,22 +1271,33 @@ int run_gemm(const Planes& A, const Planes& B, uint32_t batch, uint32_t k, Epi e
     const uint64_t b_slice = B.slices > 1 ? (uint64_t)B.lines_p * B.kp : 0;
     const uint64_t rp_slice = A.slices > 1 ? (uint64_t)A.nslab * A.lines_p : 0;
     const uint64_t cp_slice = B.slices > 1 ? (uint64_t)B.nslab * B.lines_p : 0;
-    const uint32_t mode = epi.wrap ? kWrap : (k <= 8192 ? kSatNarrow : kSatWide);
-    const dim3 grid(tiles_r * tiles_c, batch);
+    const uint32_t mode = ksteps ? kPartial : (epi.wrap ? kWrap : (k <= 8192 ? kSatNarrow : kSatWide));
+    const uint32_t nz = ksteps ? ceil_div(A.kp / BK, ksteps) : 1;
+    const dim3 grid(tiles_r * tiles_c, batch, nz);
     if (tm == 256) {
         CM_LAUNCH("gemm_planes_kernel", (gemm_planes_kernel<4, 3, Epi>), grid, dim3(512), 0, s, A.hi, A.lo, A.part,
                   a_slice, rp_slice, A.lines_p, B.hi, B.lo, B.part, b_slice, cp_slice, B.lines_p, A.nslab, tiles_r,
-                  tiles_c, A.kp, (int32_t)(64 * k), mode, epi);
+                  tiles_c, A.kp, (int32_t)(64 * k), mode, pout, ksteps, epi);
     } else if (tm == 64) {
         CM_LAUNCH("gemm_planes_kernel", (gemm_planes_kernel<1, 2, Epi>), grid, dim3(128), 0, s, A.hi, A.lo, A.part,
                   a_slice, rp_slice, A.lines_p, B.hi, B.lo, B.part, b_slice, cp_slice, B.lines_p, A.nslab, tiles_r,
-                  tiles_c, A.kp, (int32_t)(64 * k), mode, epi);
+                  tiles_c, A.kp, (int32_t)(64 * k), mode, pout, ksteps, epi);
     } else {
         CM_LAUNCH("gemm_planes_kernel", (gemm_planes_kernel<2, 2, Epi>), grid, dim3(256), 0, s, A.hi, A.lo, A.part,
                   a_slice, rp_slice, A.lines_p, B.hi, B.lo, B.part, b_slice, cp_slice, B.lines_p, A.nslab, tiles_r,
-                  tiles_c, A.kp, (int32_t)(64 * k), mode, epi);
+                  tiles_c, A.kp, (int32_t)(64 * k), mode, pout, ksteps, epi);
     }
     return CM_OK;
+}
+
+// k steps per slice for a wrap-mode matmul whose output tiles leave most workgroup slots
+// idle (0: no split): slices until the grid about fills the slots, at least 4 steps each.
+uint32_t gemm_ksteps(uint32_t tm, uint32_t tiles, uint32_t kp, const DeviceState* st) {
+    const uint32_t slots = st->cus * (tm == 256 ? 1u : 2u), nk = kp / BK;
+    if (tiles * 2 > slots || nk < 16) return 0;
+    const uint32_t nz = std::min(slots / tiles, nk / 4);
+    if (nz < 2) return 0;
+    return ceil_div(nk, nz);
 }
 
 Planes make_planes(uint32_t lines, uint32_t kp, uint32_t slices, uint32_t align = 128) {
@@ -1306,11 +1398,33 @@ int skinny_wrap(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint
     return CM_OK;
 }
 
+// The wrap-mode split over k for a matmul of this shape: k steps per slice (0: none) and the
+// bytes of its int32 partials.
+uint32_t matmul_ksteps(const Planes& A, const Planes& B, uint32_t n, uint32_t m, uint32_t batch, uint32_t wrap32,
+                       const DeviceState* st, size_t* bytes) {
+    const uint32_t tiles = ceil_div(n, A.tile) * (B.lines_p / BN) * batch;
+    const uint32_t ks = wrap32 ? gemm_ksteps(A.tile, tiles, A.kp, st) : 0;
+    *bytes = ks ? (size_t)batch * ceil_div(A.kp / BK, ks) * n * m * 4 : 0;
+    return ks;
+}
+
 int gemm_out(const Planes& A, const Planes& B, int16_t* c, uint32_t n, uint32_t k, uint32_t m, uint32_t batch,
-             int64_t c_bs, uint32_t wrap32, hipStream_t s) {
+             int64_t c_bs, uint32_t wrap32, hipStream_t s, int32_t* pout = nullptr, uint32_t ksteps = 0) {
     const bool pairs = (reinterpret_cast<uintptr_t>(c) & 3) == 0 && (m & 1) == 0 && (c_bs & 1) == 0;
     EpiMatmul epi{c, (uint64_t)c_bs, n, m, wrap32 ? 1u : 0u, pairs ? 1u : 0u};
-    return run_gemm(A, B, batch, k, epi, s);
+    int rc = run_gemm(A, B, batch, k, epi, s, pout, ksteps);
+    if (rc || !ksteps) return rc;
+    const uint32_t nz = ceil_div(A.kp / BK, ksteps);
+    const uint64_t rp_slice = A.slices > 1 ? (uint64_t)A.nslab * A.lines_p : 0;
+    const uint64_t cp_slice = B.slices > 1 ? (uint64_t)B.nslab * B.lines_p : 0;
+    // 8 outputs a lane where C's rows and the column sums are whole 16-byte words
+    const bool vec = (m & 7) == 0 && aligned16(c) && (c_bs & 7) == 0 && (B.lines_p & 3) == 0 &&
+                     (cp_slice & 3) == 0 && (reinterpret_cast<uintptr_t>(B.part) & 15) == 0;
+    const uint64_t total = (uint64_t)batch * n * m / (vec ? 8 : 1);
+    const unsigned blocks = (unsigned)std::min<uint64_t>((total + 255) / 256, 65536ull * 8);
+    CM_LAUNCH("gemm_reduce_kernel", gemm_reduce_kernel, dim3(blocks), dim3(256), 0, s, pout, A.part, rp_slice,
+              A.lines_p, B.part, cp_slice, B.lines_p, A.nslab, c, (uint64_t)c_bs, n, m, nz, batch, k, vec ? 1u : 0u);
+    return CM_OK;
 }
 
 }  // namespace
@@ -1335,8 +1449,10 @@ extern "C" int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_
     const uint32_t kp = (uint32_t)round_up(k, BK);
     const uint32_t sa = (batch > 1 && a_bs != 0) ? batch : 1, sb = (batch > 1 && b_bs != 0) ? batch : 1;
     Planes A = make_planes(n, kp, sa, gemm_tile_rows(n, m, batch, st->cus)), B = make_planes(m, kp, sb);
+    size_t pbytes;
+    const uint32_t ksteps = matmul_ksteps(A, B, n, m, batch, wrap32, st, &pbytes);
     void* ws;
-    rc = workspace(st, A.bytes() + B.bytes(), &ws);
+    rc = workspace(st, A.bytes() + B.bytes() + pbytes, &ws);
     if (rc) return rc;
     char* p = static_cast<char*>(ws);
     A.carve(p);
@@ -1346,7 +1462,7 @@ extern "C" int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_
     if (rc) return rc;
     rc = split_b(b, b_slice, k, m, b_packed, gemv_kw, B, s);
     if (rc) return rc;
-    return gemm_out(A, B, c, n, k, m, batch, c_bs, wrap32, s);
+    return gemm_out(A, B, c, n, k, m, batch, c_bs, wrap32, s, reinterpret_cast<int32_t*>(p), ksteps);
 }
 
 extern "C" size_t cm_matmul_b_planes_bytes(uint32_t k, uint32_t m, uint32_t b_slices) {
@@ -1387,8 +1503,10 @@ extern "C" int cm_matmul_planes(const int16_t* a, const void* b_planes, int16_t*
     const uint32_t kp = (uint32_t)round_up(k, BK);
     const uint32_t sa = (batch > 1 && a_bs != 0) ? batch : 1;
     Planes A = make_planes(n, kp, sa, gemm_tile_rows(n, m, batch, st->cus)), B = make_planes(m, kp, b_slices);
+    size_t pbytes;
+    const uint32_t ksteps = matmul_ksteps(A, B, n, m, batch, wrap32, st, &pbytes);
     void* ws;
-    rc = workspace(st, A.bytes(), &ws);
+    rc = workspace(st, A.bytes() + pbytes, &ws);
     if (rc) return rc;
     char* p = static_cast<char*>(ws);
     A.carve(p);
@@ -1396,7 +1514,7 @@ extern "C" int cm_matmul_planes(const int16_t* a, const void* b_planes, int16_t*
     B.carve(q);
     rc = split_a(a, sa > 1 ? (uint64_t)a_bs : 0, n, k, A, s);
     if (rc) return rc;
-    return gemm_out(A, B, c, n, k, m, batch, c_bs, wrap32, s);
+    return gemm_out(A, B, c, n, k, m, batch, c_bs, wrap32, s, reinterpret_cast<int32_t*>(p), ksteps);
 }
 
 namespace cm {

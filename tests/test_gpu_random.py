@@ -85,6 +85,13 @@ MM_CASES = [  # n, k, m, batch, a_bs_mode, b_bs_mode, layout, kw, full_range, wr
     (48, 120, 136, 3, 1, 1, "trans", 0, False, False),
     (33, 256, 64, 2, 1, 0, "row", 0, True, True),
     (130, 192, 72, 1, 1, 1, "trans", 0, True, False),
+    # wrap products of few output tiles split over k (int32 partials + the reduce kernel)
+    (512, 1024, 256, 1, 1, 1, "row", 0, True, True),
+    (300, 2048, 200, 2, 1, 1, "row", 0, True, True),
+    (200, 1280, 96, 1, 1, 1, "packed", 0, True, True),
+    (64, 4096, 64, 1, 1, 1, "row", 0, True, True),
+    (129, 1536, 130, 1, 1, 1, "trans", 0, False, True),
+    (96, 1536, 40, 3, 1, 0, "row", 0, True, True),
 ]
 
 
