@@ -28,6 +28,16 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int BN = 128, BK = 64;               // output tile columns; k step in elements (= plane bytes)
 constexpr int SLAB = 1024;                     // k per partial-sum slab
 
+// Where batch slice bt of an operand starts: (bt / inner) s1 + (bt % inner) s2 elements (the
+// (sequence, head) pairs of an attention's operands inside one projection), or bt s1.
+struct Slices {
+    uint64_t s1 = 0, s2 = 0;
+    uint32_t inner = 1;
+    __host__ __device__ uint64_t off(uint32_t bt) const {
+        return inner > 1 ? (uint64_t)(bt / inner) * s1 + (uint64_t)(bt % inner) * s2 : (uint64_t)bt * s1;
+    }
+};
+
 __device__ __forceinline__ uint32_t pack_hi(const int16_t* v) {   // 4 high bytes
     return (uint32_t)(uint8_t)(v[0] >> 8) | ((uint32_t)(uint8_t)(v[1] >> 8) << 8) |
            ((uint32_t)(uint8_t)(v[2] >> 8) << 16) | ((uint32_t)(uint8_t)(v[3] >> 8) << 24);
@@ -172,7 +182,7 @@ __device__ __forceinline__ int32_t sum8(const int4 v) {   // sum of the 8 int16 
 // Rows with k contiguous (the matmul A, row stride lda, 16-byte aligned rows): one wavefront
 // per row and SLAB of k, 8 k per lane per 16-byte load, the slab's loads all in flight
 // before the first is used; grid (ceil(lines_p / 4), nslab, slices).
-__global__ __launch_bounds__(256) void split_rows_kernel(const int16_t* __restrict__ src, uint64_t slice,
+__global__ __launch_bounds__(256) void split_rows_kernel(const int16_t* __restrict__ src, Slices slice,
                                                          uint64_t lda, uint32_t rows, uint32_t k,
                                                          int8_t* __restrict__ hi, int8_t* __restrict__ lo,
                                                          int32_t* __restrict__ part, uint32_t lines_p,
@@ -181,7 +191,7 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const int16_t* __restri
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6), slab = blockIdx.y, bt = blockIdx.z;
     if (row >= lines_p) return;
-    const int16_t* r = src + bt * slice + (uint64_t)row * lda;
+    const int16_t* r = src + slice.off(bt) + (uint64_t)row * lda;
     const uint64_t po = ((uint64_t)bt * lines_p + row) * kp;
     const bool real_row = row < rows;
     int4 v[U];
@@ -225,7 +235,7 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const int16_t* __restri
 // sum over the row's lane group.
 // Grid (ceil(lines_p / (4 * 64 / G)), 1, slices).
 template <uint32_t G>
-__global__ __launch_bounds__(256) void split_rows_short_kernel(const int16_t* __restrict__ src, uint64_t slice,
+__global__ __launch_bounds__(256) void split_rows_short_kernel(const int16_t* __restrict__ src, Slices slice,
                                                                uint64_t lda, uint32_t rows, uint32_t k,
                                                                int8_t* __restrict__ hi, int8_t* __restrict__ lo,
                                                                int32_t* __restrict__ part, uint32_t lines_p,
@@ -238,7 +248,7 @@ __global__ __launch_bounds__(256) void split_rows_short_kernel(const int16_t* __
     int4 v = make_int4(0, 0, 0, 0);
     int32_t sum = 0;
     if (in) {
-        const int16_t* r = src + bt * slice + (uint64_t)row * lda;
+        const int16_t* r = src + slice.off(bt) + (uint64_t)row * lda;
         if (real_row && k0 + 8 <= k) {
             v = *reinterpret_cast<const int4*>(r + k0);
             sum = sum8(v);
@@ -272,8 +282,8 @@ __global__ __launch_bounds__(256) void split_rows_short_kernel(const int16_t* __
 // (byte permutes) into one dword of 4 k per column and plane.  A workgroup is the four
 // 256-k quarters of one slab; their column sums meet in LDS.  Grid (ceil(lines_p / 32),
 // nslab, slices).
-__global__ __launch_bounds__(256) void split_cols_kernel(const int16_t* __restrict__ src, uint64_t slice,
-                                                         uint32_t packed, uint32_t m, uint32_t k,
+__global__ __launch_bounds__(256) void split_cols_kernel(const int16_t* __restrict__ src, Slices slice,
+                                                         uint64_t ldb, uint32_t packed, uint32_t m, uint32_t k,
                                                          int8_t* __restrict__ hi, int8_t* __restrict__ lo,
                                                          int32_t* __restrict__ part, uint32_t lines_p,
                                                          uint32_t kp, uint32_t nslab) {
@@ -282,17 +292,17 @@ __global__ __launch_bounds__(256) void split_cols_kernel(const int16_t* __restri
     const uint32_t r4 = lane >> 2, c8 = lane & 3;
     const uint32_t jg = blockIdx.x * 32, slab = blockIdx.y, bt = blockIdx.z;
     const uint32_t j0 = jg + 8 * c8;                       // this lane's first column
-    const int16_t* b = src + bt * slice;
+    const int16_t* b = src + slice.off(bt);
     const uint32_t kq = slab * SLAB + 256 * wave;          // this wave's first k
     const bool cols_real = j0 + 8 <= m;
     // element (kk, j) of the image
     auto at = [&](uint32_t kk, uint32_t j) -> uint64_t {
-        return packed ? ((uint64_t)(j >> 5) * k + kk) * 32 + (j & 31) : (uint64_t)kk * m + j;
+        return packed ? ((uint64_t)(j >> 5) * k + kk) * 32 + (j & 31) : (uint64_t)kk * ldb + j;
     };
     int4 v[4][4];
     if (cols_real && kq + 256 <= k) {                  // every load is real: no branches
         const int16_t* p0 = b + at(kq + 4 * r4, j0);
-        const uint64_t rs = packed ? 32 : m;           // elements per k row
+        const uint64_t rs = packed ? 32 : ldb;         // elements per k row
 #pragma unroll
         for (int g = 0; g < 4; g++)
 #pragma unroll
@@ -458,13 +468,18 @@ __global__ __launch_bounds__(256) void split_fold_lds_kernel(const int16_t* __re
 // the raw per-row bias (added to the sum as bias << 8), the offset of column `j` from a row
 // start, and whether every row start and the column count are even (then two adjacent
 // results go out as one 4-byte store).
-struct EpiMatmul {              // C[bt][i][j] = c + bt * c_bs + i * m + j
+struct EpiMatmul {              // C[bt][i][j] = c + off(bt) + i * ldc + j
     int16_t* c;
     uint64_t c_bs;
     uint32_t rows, cols, wrap, pairs;
+    uint64_t ldc = 0;           // row stride (0: cols)
+    uint64_t c_bs2 = 0;         // with `inner` > 1: slice bt at (bt / inner) c_bs + (bt % inner) c_bs2
+    uint32_t inner = 1;
     __device__ int32_t row_bias(uint32_t) const { return 0; }
     __device__ int16_t* row_ptr(uint32_t bt, uint32_t i) const {
-        return i < rows ? c + bt * c_bs + (uint64_t)i * cols : nullptr;
+        if (i >= rows) return nullptr;
+        const uint64_t off = inner > 1 ? (uint64_t)(bt / inner) * c_bs + (uint64_t)(bt % inner) * c_bs2 : bt * c_bs;
+        return c + off + (uint64_t)i * (ldc ? ldc : cols);
     }
     __device__ uint64_t col_off(uint32_t j) const { return j; }
 };
@@ -1331,7 +1346,7 @@ int matmul_check(uint32_t k, uint32_t gemv_kw, int64_t a_bs, int64_t b_bs, int64
 
 // Planes of rows with k contiguous (lda elements apart, 16-byte aligned): the short-row
 // kernel for kp <= 256, else a wavefront per row and slab.
-int split_row_lines(const int16_t* a, uint64_t a_slice, uint64_t lda, uint32_t n, uint32_t k, Planes& P,
+int split_row_lines(const int16_t* a, Slices a_slice, uint64_t lda, uint32_t n, uint32_t k, Planes& P,
                     hipStream_t s) {
     if (P.kp <= 256) {
 #define CM_SHORT(G)                                                                                            \
@@ -1348,7 +1363,7 @@ int split_row_lines(const int16_t* a, uint64_t a_slice, uint64_t lda, uint32_t n
 
 // A's planes: row-major [n][k] slices at a_slice elements (0: one slice).
 int split_a(const int16_t* a, uint64_t a_slice, uint32_t n, uint32_t k, Planes& A, hipStream_t s) {
-    if (aligned16(a) && (k & 7) == 0 && (a_slice & 7) == 0) return split_row_lines(a, a_slice, k, n, k, A, s);
+    if (aligned16(a) && (k & 7) == 0 && (a_slice & 7) == 0) return split_row_lines(a, Slices{a_slice}, k, n, k, A, s);
     return run_split<SrcRowMajor, true>(SrcRowMajor{a, n, k, k}, a_slice, A, s);
 }
 
@@ -1357,12 +1372,13 @@ int split_b(const int16_t* b, uint64_t b_slice, uint32_t k, uint32_t m, uint32_t
             Planes& B, hipStream_t s) {
     const uint32_t layout = gemv_kw ? 2 : (b_packed == 2 ? 3 : (b_packed ? 1 : 0));
     if (layout == 3 && aligned16(b) && (b_slice & 7) == 0 && (k & 7) == 0)
-        return split_row_lines(b, b_slice, k, m, k, B, s);    // B's lines are rows with k contiguous
+        return split_row_lines(b, Slices{b_slice}, k, m, k, B, s);    // B's lines are rows with k contiguous
     const bool fast_b = aligned16(b) && (b_slice & 7) == 0 &&
                         (layout == 1 || (layout == 0 && (m & 7) == 0) || (layout == 2 && gemv_kw == 1 && (m & 7) == 0));
     if (fast_b) {
         CM_LAUNCH("split_cols_kernel", split_cols_kernel, dim3(B.lines_p / 32, B.nslab, B.slices), dim3(256), 0, s,
-                  b, b_slice, layout == 1 ? 1u : 0u, m, k, B.hi, B.lo, B.part, B.lines_p, B.kp, B.nslab);
+                  b, Slices{b_slice}, (uint64_t)m, layout == 1 ? 1u : 0u, m, k, B.hi, B.lo, B.part, B.lines_p, B.kp,
+                  B.nslab);
         return CM_OK;
     }
     return run_split<SrcMatB, false>(SrcMatB{b, m, k, m, layout, gemv_kw}, b_slice, B, s);
@@ -1732,4 +1748,44 @@ extern "C" int cm_conv_planes(const int16_t* x, const void* w_planes, const int1
     char* p = static_cast<char*>(ws);
     B.carve(p);
     return conv_gemm(x, A, B, has_bias ? bias : nullptr, y, g, st, s);
+}
+
+extern "C" int cm_matmul_strided(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k, uint32_t m,
+                                 uint32_t batch, uint32_t inner, uint64_t lda, uint64_t a_bs, uint64_t a_bs2,
+                                 uint64_t ldb, uint64_t b_bs, uint64_t b_bs2, uint32_t b_trans, uint64_t ldc,
+                                 uint64_t c_bs, uint64_t c_bs2, uint32_t wrap32, void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    if (n == 0 || m == 0 || batch == 0) return CM_OK;
+    if (k == 0 || k > 32768) return fail(CM_EINVAL, "matmul: k = %u outside 1 .. 32768", k);
+    if (inner == 0) return fail(CM_EINVAL, "matmul: inner 0");
+    const bool a_ok = aligned16(a) && (lda & 7) == 0 && (a_bs & 7) == 0 && (a_bs2 & 7) == 0 && (k & 7) == 0;
+    const bool b_ok = aligned16(b) && (ldb & 7) == 0 && (b_bs & 7) == 0 && (b_bs2 & 7) == 0 &&
+                      (b_trans ? (k & 7) == 0 : (m & 7) == 0);
+    if (!a_ok || !b_ok) return fail(CM_EALIGN, "matmul: strided operands need 16-byte rows and slices");
+    if (lda < k || ldb < (b_trans ? k : m) || ldc < m) return fail(CM_EINVAL, "matmul: row strides below the rows");
+    hipStream_t s = as_stream(stream);
+    const uint32_t kp = (uint32_t)round_up(k, BK);
+    Planes A = make_planes(n, kp, batch, gemm_tile_rows(n, m, batch, st->cus)), B = make_planes(m, kp, batch);
+    void* ws;
+    rc = workspace(st, A.bytes() + B.bytes(), &ws);
+    if (rc) return rc;
+    char* p = static_cast<char*>(ws);
+    A.carve(p);
+    B.carve(p);
+    rc = split_row_lines(a, Slices{a_bs, a_bs2, inner}, lda, n, k, A, s);
+    if (rc) return rc;
+    if (b_trans) {
+        rc = split_row_lines(b, Slices{b_bs, b_bs2, inner}, ldb, m, k, B, s);
+        if (rc) return rc;
+    } else {
+        CM_LAUNCH("split_cols_kernel", split_cols_kernel, dim3(B.lines_p / 32, B.nslab, B.slices), dim3(256), 0, s,
+                  b, (Slices{b_bs, b_bs2, inner}), ldb, 0u, m, k, B.hi, B.lo, B.part, B.lines_p, B.kp, B.nslab);
+    }
+    const bool pairs = (reinterpret_cast<uintptr_t>(c) & 3) == 0 && (m & 1) == 0 && (ldc & 1) == 0 &&
+                       (c_bs & 1) == 0 && (c_bs2 & 1) == 0;
+    EpiMatmul epi{c, c_bs, n, m, wrap32 ? 1u : 0u, pairs ? 1u : 0u, ldc, c_bs2, inner};
+    return run_gemm(A, B, batch, k, epi, s);
 }

@@ -228,6 +228,36 @@ class LlmAttnConvNode:
         return self.H // self.KV
 
 
+@dataclass(frozen=True)
+class HeadView:
+    """Per-head blocks of a token-major tensor [batch seq][ld] as the slices [batch heads][seq]
+    [width] of a contraction: slice b heads + h is rows b seq .. b seq + seq - 1, columns
+    col + h width .. col + (h + 1) width - 1 (the q / K / V rows VitAttnPrep copies out of
+    the fused projection, and the rows LlmAttnMerge copies o back into; vit.py:19-32), read
+    or written in place."""
+    col: int
+    heads: int
+    width: int
+    seq: int
+
+    def strides(self, ld: int) -> Tuple[int, int, int, int]:
+        """(offset, row stride, slice stride over sequences, slice stride over heads) in elements."""
+        return self.col, ld, self.seq * ld, self.width
+
+    def gather(self, x: np.ndarray) -> np.ndarray:
+        """[batch seq][ld] -> [batch heads][seq][width]."""
+        ld = x.shape[-1]
+        x = x.reshape(-1, self.seq, ld)[:, :, self.col:self.col + self.heads * self.width]
+        return x.reshape(-1, self.seq, self.heads, self.width).transpose(0, 2, 1, 3).reshape(-1, self.seq, self.width)
+
+    def scatter(self, y: np.ndarray, ld: int) -> np.ndarray:
+        """[batch heads][seq][width] -> [batch seq][ld] (col 0, heads width == ld: every element)."""
+        if self.col != 0 or self.heads * self.width != ld:
+            raise ValueError("an output head view covers its tensor's rows")
+        y = y.reshape(-1, self.heads, self.seq, self.width).transpose(0, 2, 1, 3)
+        return y.reshape(-1, ld)
+
+
 @dataclass
 class AttnContractNode:
     """The attention contractions of ``batch`` (sequence, head) pairs with every key valid:
@@ -236,10 +266,27 @@ class AttnContractNode:
     P.V with A = P, B = V rows; llm_nodes.py:995-1001, 1407-1425) over static keys, one call
     for all pairs.  Output exponent f_a + f_b - 8 (score_exp / pv_exp, graph_builder.py:197-208).
     ``b_trans``: B given as [batch][m][k] (out = A . B^T), e.g. q rows against a K cache's rows,
-    the scores then query-major."""
+    the scores then query-major.  ``a_view`` / ``b_view`` / ``c_view``: the operand (B as
+    given, i.e. [batch][m][k] with ``b_trans``) or the output as a HeadView of a token-major
+    tensor instead of a [batch][rows][cols] tensor of its own."""
     inputs: List[TensorInfo]
     output: TensorInfo
     b_trans: bool = False
+    a_view: Optional[HeadView] = None
+    b_view: Optional[HeadView] = None
+    c_view: Optional[HeadView] = None
+
+    def operand_shape(self, i: int) -> Tuple[int, int, int]:
+        """[slices][rows][cols] of input ``i`` (0: A, 1: B as given) or 2: the output."""
+        t = self.output if i == 2 else self.inputs[i]
+        v = (self.a_view, self.b_view, self.c_view)[i]
+        if v is None:
+            if len(t.shape) != 3:
+                raise SchedulerError(f"attention contraction '{self.output.onnx_name}': operand {i} not 3-d")
+            return tuple(int(d) for d in t.shape)
+        if len(t.shape) != 2 or int(t.shape[0]) % v.seq or v.col + v.heads * v.width > int(t.shape[1]):
+            raise SchedulerError(f"attention contraction '{self.output.onnx_name}': head view outside its tensor")
+        return int(t.shape[0]) // v.seq * v.heads, v.seq, v.width
 
 
 @dataclass
@@ -298,7 +345,7 @@ def conv_out(size: int, k: int, stride: int, pad_lo: int, pad_hi: int, dil: int 
     return (size + pad_lo + pad_hi - dil * (k - 1) - 1) // stride + 1
 
 
-__all__ = ["SchedulerError", "TensorInfo", "ScheduledNode", "MatmulNode", "ConvNode", "PoolNode",
+__all__ = ["SchedulerError", "TensorInfo", "HeadView", "ScheduledNode", "MatmulNode", "ConvNode", "PoolNode",
            "ReshapeNode", "SoftmaxVopNode", "RowOpsNode", "LlmAttnConvNode", "KvWriteNode", "AttentionNode", "attn_keys",
            "KEY_QUANTUM",
            "Graph", "conv_out", "OP_ADD", "OP_SUB",

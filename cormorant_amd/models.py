@@ -15,7 +15,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import units
-from .graph import (AttentionNode, AttnContractNode, ConvNode, Graph, MatmulNode, PermuteNode, PoolNode, ReshapeNode,
+from .graph import (AttentionNode, AttnContractNode, ConvNode, Graph, HeadView, MatmulNode, PoolNode, ReshapeNode,
                     ScheduledNode, SoftmaxVopNode, TensorInfo, conv_out, softmax_regs)
 from .rowops_nodes import LayerNorm32RoNode, ResAddBiasRoNode
 
@@ -191,11 +191,12 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
 
         x  = LayerNorm32(h)                          row-ops NORM, int32 -> int16
         qkv = x . Wqkv                               MatMul (pow2, int32 wrap)
-        q, K, V rows per head                        Permute (the head split)
-        s  = K . q^T   [B H][keys][queries]          batched MatMul (q rows as B^T), f_s = f_q + f_k - 8
+        s  = K . q^T   [B H][keys][queries]          batched MatMul, K and q rows per head read in
+                                                     place from qkv (q as B^T), f_s = f_q + f_k - 8
         P  = softmax over keys (column mode)         VectorOP softmax, logit scale 1/sqrt(hd)
-        o  = P . V     [B H][queries][hd]            batched MatMul, f_o = f_p + f_v - 8
-        h1 = ResAddBias(h, merge(o) . Wo, bo)        Permute, MatMul, row-ops ADDX
+        o  = P . V     [B H][queries][hd]            batched MatMul, V rows read in place, o written
+                                                     per head into its columns of om, f_o = f_p + f_v - 8
+        h1 = ResAddBias(h, om . Wo, bo)              MatMul, row-ops ADDX
         x2 = LayerNorm32(h1);  f = x2 . W1  (at 2^-8)
         a  = GELU(f + b1)                            VectorOP ADD with the GELU act
         h  = ResAddBias(h1, a . W2, b2)
@@ -300,21 +301,14 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
             nodes.append(AttentionNode([qkv], om, batch=S.batch, seq=T, heads=H, head_dim=hd, q_off=0, k_off=D,
                                        v_off=2 * D, cm=cmr, cfg=cfg))
         else:
-            qh = T_(p + "qh", [BH, T, hd], exp=e["q"])
-            kh = T_(p + "kh", [BH, T, hd], exp=e["k"])
-            vh = T_(p + "vh", [BH, T, hd], exp=e["v"])
-            nodes.append(PermuteNode([qkv], qh, dims=(S.batch, H, T, hd), strides=(T * ld, hd, ld, 1), offset=0))
-            nodes.append(PermuteNode([qkv], kh, dims=(S.batch, H, T, hd), strides=(T * ld, hd, ld, 1), offset=D))
-            nodes.append(PermuteNode([qkv], vh, dims=(S.batch, H, T, hd), strides=(T * ld, hd, ld, 1),
-                                     offset=2 * D))
+            # the per-head q / K / V rows read in place from qkv, o written in place into om
+            hv = lambda col: HeadView(col, H, hd, T)                                 # noqa: E731
             # s[j][i] = K[j] . Q[i]: the q rows as the transposed B image (no q transpose)
             sc = T_(p + "s", [BH, T, T], exp=e["s"])
-            nodes.append(AttnContractNode([kh, qh], sc, b_trans=True))
+            nodes.append(AttnContractNode([qkv, qkv], sc, b_trans=True, a_view=hv(D), b_view=hv(0)))
             pr = T_(p + "P", [BH, T, T], exp=e["p"])
             nodes.append(SoftmaxVopNode([sc], pr, cm=cmr, cfg=cfg, keys_major=True))
-            o = T_(p + "o", [BH, T, hd], exp=e["o"])
-            nodes.append(AttnContractNode([pr, vh], o))
-            nodes.append(PermuteNode([o], om, dims=(S.batch, T, H, hd), strides=(H * T * hd, hd, T * hd, 1)))
+            nodes.append(AttnContractNode([pr, qkv], om, b_view=hv(2 * D), c_view=hv(0)))
         wo = T_(p + "wo", [D, D], data=L["wo"])
         ao = T_(p + "ao", [rows, D], exp=e["ao"])
         nodes.append(MatmulNode([om, wo], ao))

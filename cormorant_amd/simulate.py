@@ -388,19 +388,41 @@ class Simulator:
 
     def _attn_contract(self, sn: AttnContractNode, raw) -> torch.Tensor:
         at, bt, ot = sn.inputs[0], sn.inputs[1], sn.output
-        batch, n, k = at.shape
-        kb, m = (2, 1) if sn.b_trans else (1, 2)
-        if len(bt.shape) != 3 or bt.shape[0] != batch or bt.shape[kb] != k or list(ot.shape) != [batch, n, bt.shape[m]]:
+        batch, n, k = sn.operand_shape(0)
+        b3 = sn.operand_shape(1)
+        kb, mb = (2, 1) if sn.b_trans else (1, 2)
+        m = b3[mb]
+        if b3[0] != batch or b3[kb] != k or sn.operand_shape(2) != (batch, n, m):
             raise SchedulerError(f"attention contraction '{ot.onnx_name}': [b][n][k] x [b][k][m] -> [b][n][m]")
-        fa, fb, fo = (np.asarray(self._exp(t)).reshape(-1) for t in (at, bt, ot))
-        if fa.size != 1 or fb.size != 1 or fo.size != 1 or int(fo[0]) != int(fa[0]) + int(fb[0]) - self._dtype.frac_bits:
+        fa, fb, fo = (self._view_exp(t, v, ot) for t, v in ((at, sn.a_view), (bt, sn.b_view), (ot, sn.c_view)))
+        if fo != fa + fb - self._dtype.frac_bits:
             raise SchedulerError(f"attention contraction '{ot.onnx_name}': output exponent is not f_a + f_b - 8")
-        m = int(bt.shape[m])
+        a, b = self._get(at, raw).reshape(-1), self._get(bt, raw).reshape(-1)
         c = self._new(ot)
-        units.matmul(self._get(at, raw).reshape(-1).contiguous(), self._get(bt, raw).reshape(-1).contiguous(), c,
-                     n, k, m, batch=batch, a_bs=n * k, b_bs=k * m, c_bs=n * m, b_packed=2 if sn.b_trans else 0,
-                     wrap32=True)
+        if sn.a_view is None and sn.b_view is None and sn.c_view is None:
+            units.matmul(a.contiguous(), b.contiguous(), c, n, k, m, batch=batch, a_bs=n * k, b_bs=k * m,
+                         c_bs=n * m, b_packed=2 if sn.b_trans else 0, wrap32=True)
+            return c
+        inner = next(v.heads for v in (sn.a_view, sn.b_view, sn.c_view) if v is not None)
+        def view(t, v, rows, cols):
+            if v is None:
+                return (0, cols, inner * rows * cols, rows * cols)   # slice bt at bt rows cols
+            if v.heads != inner:
+                raise SchedulerError(f"attention contraction '{ot.onnx_name}': head views of different head counts")
+            return v.strides(int(t.shape[-1]))
+        units.matmul_strided(a, b, c, n, k, m, batch, inner, view(at, sn.a_view, n, k),
+                             view(bt, sn.b_view, *((m, k) if sn.b_trans else (k, m))), view(ot, sn.c_view, n, m),
+                             b_trans=sn.b_trans, wrap32=True)
         return c
+
+    def _view_exp(self, t: TensorInfo, v, ot: TensorInfo) -> int:
+        """The one exponent of a contraction operand: the tensor's, or a head view's columns'."""
+        e = np.asarray(self._exp(t)).reshape(-1)
+        if v is not None and e.size > 1:
+            e = np.broadcast_to(e, (int(t.shape[-1]),))[v.col:v.col + v.heads * v.width]
+        if e.size == 0 or (e != e[0]).any():
+            raise SchedulerError(f"attention contraction '{ot.onnx_name}': operand '{t.onnx_name}' at one exponent")
+        return int(e[0])
 
     def _permute(self, sn: PermuteNode, raw) -> torch.Tensor:
         xt, ot = sn.inputs[0], sn.output

@@ -169,6 +169,25 @@ def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, n: int, k: int, m:
     return c
 
 
+def matmul_strided(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, n: int, k: int, m: int, batch: int,
+                   inner: int, a_view, b_view, c_view, b_trans: bool = False, wrap32: bool = False) -> torch.Tensor:
+    """cm_matmul_strided: each view is (offset, ld, bs, bs2) in elements of its tensor; slice bt
+    starts at offset + (bt // inner) bs + (bt % inner) bs2."""
+    def extent(view, r, cols):
+        off, ld, bs, bs2 = view
+        return off + ((batch - 1) // inner) * bs + (min(batch, inner) - 1) * bs2 + (r - 1) * ld + cols
+    if n and m and batch:
+        _require(a, "a", torch.int16, extent(a_view, n, k))
+        _require(b, "b", torch.int16, extent(b_view, m, k) if b_trans else extent(b_view, k, m))
+        _require(c, "c", torch.int16, extent(c_view, n, m))
+    (ao, lda, abs1, abs2), (bo, ldb, bbs1, bbs2), (co, ldc, cbs1, cbs2) = a_view, b_view, c_view
+    rc = _lib.lib().cm_matmul_strided(_ptr(a) + 2 * ao, _ptr(b) + 2 * bo, _ptr(c) + 2 * co, n, k, m, batch, inner,
+                                      lda, abs1, abs2, ldb, bbs1, bbs2, int(bool(b_trans)), ldc, cbs1, cbs2,
+                                      int(bool(wrap32)), _stream())
+    _lib.check(rc, "cm_matmul_strided")
+    return c
+
+
 def matmul_b_planes(b: torch.Tensor, k: int, m: int, b_slices: int = 1, b_bs: int = 0, b_packed: int = 0,
                     gemv_kw: int = 0) -> torch.Tensor:
     """B's split image (cm_matmul_split_b) in a new uint8 device tensor, for matmul_planes."""

@@ -109,6 +109,18 @@ int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32
               uint32_t m, uint32_t batch, int64_t a_bs, int64_t b_bs, int64_t c_bs,
               uint32_t b_packed, uint32_t gemv_kw, uint32_t wrap32, void* stream);
 
+/* cm_matmul over strided operands (no counterpart in the reference's units: the per-head
+ * operands that VitAttnPrep / LlmAttnMerge would copy out and back, read and written in place):
+ * slice bt of `batch` starts at (bt / inner) x_bs + (bt % inner) x_bs2 elements of each
+ * operand (bt x_bs with inner 1); A[i][kk] = a[.. + i lda + kk]; B[kk][j] = b[.. + kk ldb + j],
+ * or b[.. + j ldb + kk] with b_trans; C[i][j] at c[.. + i ldc + j]; the arithmetic of
+ * cm_matmul.  16-byte aligned operands and strides (elements multiples of 8), k % 8 == 0, and
+ * m % 8 == 0 without b_trans. */
+int cm_matmul_strided(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k, uint32_t m,
+                      uint32_t batch, uint32_t inner, uint64_t lda, uint64_t a_bs, uint64_t a_bs2, uint64_t ldb,
+                      uint64_t b_bs, uint64_t b_bs2, uint32_t b_trans, uint64_t ldc, uint64_t c_bs, uint64_t c_bs2,
+                      uint32_t wrap32, void* stream);
+
 /* A constant B (a weight read by many calls) split once: cm_matmul_split_b writes B's byte
  * planes and line sums -- what every cm_matmul call otherwise derives from b on the fly --
  * into `planes` (cm_matmul_b_planes_bytes(k, m, b_slices) bytes, 256-byte aligned), from the

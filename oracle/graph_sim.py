@@ -241,13 +241,18 @@ def forward(graph, inputs):
                 vals[out.onnx_name] = (c.reshape(rows, n8)[:, :n].astype(np.float64) / 2.0 ** fp).reshape(out.shape)
         elif isinstance(sn, G.AttnContractNode):
             at, bt = sn.inputs
-            ra, rb = _raw_of(at, get(at)), _raw_of(bt, get(bt))
-            rb = rb.reshape(bt.shape)
+            # operands as [slices][rows][cols]: their own 3-d shape or a head view's gather
+            ops = [_raw_of(t, get(t)).reshape(t.shape) if v is None else v.gather(_raw_of(t, get(t)))
+                   for t, v in ((at, sn.a_view), (bt, sn.b_view))]
+            ra, rb = ops
             if sn.b_trans:
                 rb = rb.transpose(0, 2, 1)
-            acc = np.matmul(ra.reshape(at.shape).astype(np.float64), rb.astype(np.float64))   # |sums| < 2^53: exact
+            acc = np.matmul(ra.astype(np.float64), rb.astype(np.float64))   # |sums| < 2^53: exact
             fo = float(F if out.exp is None else out.exp)
-            vals[out.onnx_name] = (_wrap_floor(acc) / 2.0 ** fo).reshape(out.shape)
+            r = _wrap_floor(acc)
+            if sn.c_view is not None:
+                r = sn.c_view.scatter(r, int(out.shape[-1]))
+            vals[out.onnx_name] = (r / 2.0 ** fo).reshape(out.shape)
         elif isinstance(sn, G.PermuteNode):
             vals[out.onnx_name] = get(sn.inputs[0]).reshape(-1)[sn.gather_index()].reshape(out.shape)
         elif isinstance(sn, G.ScheduledNode):

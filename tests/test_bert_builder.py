@@ -6,7 +6,7 @@ import math
 import numpy as np
 
 from cormorant_amd import models
-from cormorant_amd.graph import AttentionNode, AttnContractNode, PermuteNode, SoftmaxVopNode, TensorInfo, softmax_regs
+from cormorant_amd.graph import AttentionNode, AttnContractNode, HeadView, PermuteNode, SoftmaxVopNode, TensorInfo, softmax_regs
 
 SMALL = models.BertShape(layers=2, batch=2, seq=64, d=128, heads=2, ff=512, vocab=1000)
 
@@ -42,9 +42,13 @@ def test_encoder_exponents_and_structure():
         assert e["f"] == 8 and e["ao"] <= 15 and e["dd"] <= 15
     contract = [sn for sn in g.nodes if isinstance(sn, AttnContractNode)]
     assert len(contract) == 2 * SMALL.layers
+    assert not any(isinstance(sn, PermuteNode) for sn in g.nodes)       # head views, no copies
     for sn in contract:
         a, b = sn.inputs
-        assert sn.output.exp == a.exp + b.exp - 8
+        ea, eb = (np.unique(np.broadcast_to(t.exp, (t.shape[-1],))[v.col:v.col + v.heads * v.width])
+                  if v is not None else np.unique(t.exp) for t, v in ((a, sn.a_view), (b, sn.b_view)))
+        assert ea.size == 1 and eb.size == 1 and sn.output.exp == ea[0] + eb[0] - 8
+        assert sn.operand_shape(2) == (SMALL.batch * SMALL.heads, SMALL.seq, sn.operand_shape(1)[1 if sn.b_trans else 2])
     smx = [sn for sn in g.nodes if isinstance(sn, SoftmaxVopNode)]
     assert all(sn.keys_major for sn in smx) and len(smx) == SMALL.layers
     gf, _, ef = models.bert_encoder(SMALL, seed=1, fused_attention=True)
@@ -52,6 +56,22 @@ def test_encoder_exponents_and_structure():
     assert ef == exps and len(att) == SMALL.layers
     for sn, sm in zip(att, smx):
         assert (sn.cm, sn.cfg) == (sm.cm, sm.cfg) and (sn.q_off, sn.k_off, sn.v_off) == (0, SMALL.d, 2 * SMALL.d)
+
+
+def test_head_view_gather_scatter():
+    B, T, H, hd, ld = 2, 5, 3, 4, 40
+    x = np.arange(B * T * ld).reshape(B * T, ld)
+    v = HeadView(col=8, heads=H, width=hd, seq=T)
+    want = x.reshape(B, T, ld)[:, :, 8:8 + H * hd].reshape(B, T, H, hd).transpose(0, 2, 1, 3).reshape(B * H, T, hd)
+    assert np.array_equal(v.gather(x), want)
+    off, lda, bs, bs2 = v.strides(ld)
+    for bt in range(B * H):                                   # the strides cm_matmul_strided reads
+        for i in range(T):
+            base = off + (bt // H) * bs + (bt % H) * bs2 + i * lda
+            assert np.array_equal(x.reshape(-1)[base:base + hd], want[bt, i])
+    o = HeadView(col=0, heads=H, width=hd, seq=T)
+    y = np.arange(B * H * T * hd).reshape(B * H, T, hd)
+    assert np.array_equal(o.gather(o.scatter(y, H * hd)), y)
 
 
 def test_full_shape_macs():

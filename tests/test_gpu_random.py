@@ -174,6 +174,66 @@ def test_matmul_planes_equals_matmul(U, case):
         np.testing.assert_array_equal(host(got), host(want))
 
 
+STRIDED_CASES = [  # B, T, H, hd, ld, a (col or None), b (col or None), b_trans, c (ldc or None), full, wrap
+    (2, 64, 3, 64, 576, 192, 0, True, None, True, True),       # K . q^T from a fused projection
+    (2, 64, 3, 64, 576, None, 384, False, 192, True, True),    # P . V into the merged rows
+    (1, 384, 2, 64, 384, None, 256, False, 136, False, True),  # 384 keys; o rows wider than the heads
+    (3, 40, 2, 24, 160, 16, 112, True, None, True, False),     # ragged rows, saturating
+    (2, 72, 1, 32, 48, 8, None, False, 40, True, True),        # one head, padded rows
+]
+
+
+@pytest.mark.parametrize("case", STRIDED_CASES, ids=lambda c: "B%d_T%d_H%d_hd%d_%s_%s_%s" % (
+    c[0], c[1], c[2], c[3], "av" if c[5] is not None else "a", ("btv" if c[7] else "bv") if c[6] is not None else "b",
+    "cv" if c[8] else "c"))
+def test_matmul_strided_random(U, oracle_lib, case):
+    """cm_matmul_strided against cm_matmul's oracle on the gathered operands: per-head rows
+    read in place from a token-major tensor (A, B and B^T), the output written per head into
+    the columns of token-major rows (the columns between left untouched), or plain slices."""
+    from cormorant_amd.graph import HeadView
+    B, T, H, hd, ld, acol, bcol, btr, ldc, full, wrap = case
+    rng = np.random.default_rng(B * 1000 + T * 10 + hd)
+    lim = 32768 if full else 2048
+    x = rint16(rng, B * T * ld, -lim, lim).reshape(B * T, ld)
+    BH = B * H
+    # the logical contraction: A [BH][n][k], B [BH][k][m]
+    if acol is not None:                       # A = per-head rows of x: n = T, k = hd
+        n, k = T, hd
+        av = HeadView(acol, H, hd, T)
+        a_log, a_src, a_view = av.gather(x), x.reshape(-1), av.strides(ld)
+    else:                                      # A = plain [BH][T][T] (probabilities)
+        n, k = T, T
+        a_log = rint16(rng, BH * T * T, -lim, lim).reshape(BH, T, T)
+        a_src, a_view = a_log.reshape(-1), (0, T, H * T * T, T * T)
+    if bcol is not None:
+        bv = HeadView(bcol, H, hd, T)
+        g = bv.gather(x)                       # [BH][T][hd]
+        b_log = g.transpose(0, 2, 1) if btr else g
+        b_src, b_view = x.reshape(-1), bv.strides(ld)
+    else:
+        b_log = rint16(rng, BH * k * hd, -lim, lim).reshape(BH, k, hd)
+        b_src, b_view = b_log.reshape(-1), (0, hd, H * k * hd, k * hd)
+    m = b_log.shape[2]
+    assert b_log.shape[1] == k
+    want = oracle_lib.matmul(np.ascontiguousarray(a_log).reshape(-1), np.ascontiguousarray(b_log).reshape(-1),
+                             n, k, m, BH, n * k, k * m, n * m, 0, 0, wrap).reshape(BH, n, m)
+    if ldc is None:
+        c_len, c_view = BH * n * m, (0, m, H * n * m, n * m)
+        full_want = want.reshape(-1)
+    else:
+        c_len, c_view = B * T * ldc, (0, ldc, T * ldc, m)
+        full_want = np.full(c_len, POISON16, np.int16)
+        for bt in range(BH):
+            for i in range(n):
+                base = (bt // H) * T * ldc + (bt % H) * m + i * ldc
+                full_want[base:base + m] = want[bt, i]
+    c = poisoned16(c_len + 8)
+    U.matmul_strided(dev16(a_src), dev16(b_src), c, n, k, m, BH, H, a_view, b_view, c_view, b_trans=btr, wrap32=wrap)
+    got = host(c)
+    np.testing.assert_array_equal(got[:c_len], full_want)
+    assert (got[c_len:] == POISON16).all()
+
+
 def test_matmul_q88_saturates_where_int32_would_wrap(U, oracle_lib):
     """acc = 16 * 32767^2 exceeds int32: the Q8.8 path saturates the true sum, the
     power-of-two path wraps it (_simulate.py:620-633 vs 814-835; test_numeric.py:148-184)."""
