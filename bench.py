@@ -301,11 +301,11 @@ def bert_bench(args, torch, np):
                                "768, 12 heads x 64, FFN 3072 GELU(erf), pre-LN on an int32 residual at 2^-15",
                    "layers": shape.layers, "batch": shape.batch, "seq": shape.seq, "hidden": shape.d,
                    "heads": shape.heads, "ffn": shape.ff, "macs_per_step": macs},
-        "roofline": gemm_roofline(per_kernel, macs),
+        "roofline": gemm_roofline(per_kernel, shape.linear_macs()),
         "kernels_ms_per_step": per_kernel,
         "graph_build_s": round(build_s, 1),
     }
-    # the GEMM launches' HBM bytes per forward (72 launches), from the committed --pmc summary
+    # the GEMM launches' HBM bytes per forward, from the committed --pmc summary
     result["roofline"]["traffic"] = read_traffic(BERT_TRAFFIC_FILE, "traffic_bytes_per_step")
     if not args.no_cpu_baseline:
         from oracle import graph_sim

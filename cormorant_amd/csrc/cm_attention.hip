@@ -8,18 +8,24 @@
 // VitAttnSoftmax keys-major call, the P.V contraction and the head merge (vit.py:19-32,
 // llm_nodes.py:995-1001, vectorop_smx.py:50-66), without materializing s or P.
 //
-// The int32 wrap makes every sum exact in any order, so v_dot2_i32_i16 (two products per
-// lane-op, no clamp) forms them directly.  Workgroup: 4 wavefronts, lane = query, wavefront w
-// = keys [w T/4, (w+1) T/4).
-//   phase 1: the lane's Q row in registers, K rows read at wavefront-uniform addresses;
-//   phase 2: the softmax: row max and sum across the four wavefronts through LDS,
+// Both contractions run on v_mfma_i32_16x16x64_i8 over byte limbs: x - 128 = 256 h + l with
+// h = x >> 8 and l = (x & 255) - 128, so that
+//   sum a b = 2^16 HH + 2^8 (HL + LH) + LL + 128 sum a + 128 sum b - 16384 K   (mod 2^32),
+// the int32-wrapped sum exactly (the wrap makes every term's order free).
+//
+// Workgroup: 4 wavefronts, wavefront w owns queries q0 + 16 w .. + 15 end to end.  MFMA
+// layouts (16 x 16 blocks): operand lane l holds row / column l % 16 and 16 bytes of k slot
+// group l / 16; result lane l holds column l % 16, rows 4 (l / 16) .. + 3.
+//   phase 1: s for key block kb (16 keys) = K rows (A, from the projection rows, split in
+//            registers) x Q rows (B, loaded once): lane (query l % 16, g = l / 16) ends up
+//            with the scores of keys 16 kb + 4 g + r, r < 4, for all T / 16 blocks;
+//   phase 2: the softmax per query over its lane group (shuffles across g; no LDS):
 //            e = TAB[y & 4095] >> (y >> 12), y = (max - s) Cm >> Cs, R = floor(2^40 / S),
 //            P = min((e R + 2^(39 - fp)) >> (40 - fp), 32767) (the unit's integer rule);
-//   phase 3: o partials over the wavefront's keys from V transposed in LDS (k pairs of one
-//            d contiguous: 16-byte broadcast reads of 4 key pairs), summed across the
-//            wavefronts through LDS (the region V used), then the output rule.
-// LDS: TAB (16 KiB) + one 64 KiB region (V^T [64][T] and the max / sum exchange, then the
-// partials [4][64][64]): two workgroups per compute unit.  T <= 384.
+//   phase 3: o^T = V^T P^T: P stays in registers as the B operand, its k slots the lane's own
+//            keys (slot 16 g + 4 q + r of k step ks = key 16 (4 ks + q) + 4 g + r); V^T is
+//            split into byte planes in LDS once per workgroup in that key order.
+// LDS: TAB (16 KiB) + V^T hi / lo planes [64][T + 16] + the V column-sum partials.
 #include "cm_common.h"
 
 #include <algorithm>
@@ -29,8 +35,8 @@ namespace {
 
 constexpr uint32_t kHd = 64;                 // head dimension
 constexpr uint32_t kQb = 64;                 // queries per workgroup
-constexpr uint32_t kRegion = 65536;          // bytes: V^T (T <= 384) + exchange, or the partials
 
+typedef int v4i __attribute__((ext_vector_type(4)));
 typedef short v2s __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ int dot2(uint32_t a, uint32_t b, int c) {
@@ -39,142 +45,227 @@ __device__ __forceinline__ int dot2(uint32_t a, uint32_t b, int c) {
 
 __device__ __forceinline__ int sat16_shr8(int acc) { return min(max(acc >> 8, -32768), 32767); }
 
-// NK = keys per wavefront (T / 4).  qkv rows: ld elements apart; Q / K / V of head h at
-// columns q_off / k_off / v_off + 64 h.  o rows: o_ld apart, head h at columns 64 h.
-template <uint32_t NK>
+// 8 int16 -> their high bytes and low bytes ^ 0x80 (two dwords each) and their sum
+__device__ __forceinline__ void limbs8(const int4 v, uint32_t& h0, uint32_t& h1, uint32_t& l0, uint32_t& l1, int& sum) {
+    const uint32_t x = (uint32_t)v.x, y = (uint32_t)v.y, z = (uint32_t)v.z, u = (uint32_t)v.w;
+    h0 = __builtin_amdgcn_perm(y, x, 0x07050301u);
+    h1 = __builtin_amdgcn_perm(u, z, 0x07050301u);
+    l0 = __builtin_amdgcn_perm(y, x, 0x06040200u) ^ 0x80808080u;
+    l1 = __builtin_amdgcn_perm(u, z, 0x06040200u) ^ 0x80808080u;
+    sum = dot2(u, 0x00010001u, dot2(z, 0x00010001u, dot2(y, 0x00010001u, dot2(x, 0x00010001u, sum))));
+}
+
+// 16 consecutive int16 at p (16-byte aligned) -> the hi / lo limb operands and their sum
+__device__ __forceinline__ void limbs16(const int16_t* p, v4i& hi, v4i& lo, int& sum) {
+    const int4 a = *reinterpret_cast<const int4*>(p), b = *reinterpret_cast<const int4*>(p + 8);
+    uint32_t h0, h1, h2, h3, l0, l1, l2, l3;
+    sum = 0;
+    limbs8(a, h0, h1, l0, l1, sum);
+    limbs8(b, h2, h3, l2, l3, sum);
+    hi = v4i{(int)h0, (int)h1, (int)h2, (int)h3};
+    lo = v4i{(int)l0, (int)l1, (int)l2, (int)l3};
+}
+
+__device__ __forceinline__ uint32_t dword(const int4& v, uint32_t q) {
+    return (uint32_t)(q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w);
+}
+
+__device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// the wrapped sum from the limb accumulators and the row + column term 128 (ra + cb) - 16384 K
+__device__ __forceinline__ int32_t wrap_sum(int32_t hh, int32_t mid, int32_t ll, uint32_t term) {
+    return (int32_t)(((uint32_t)hh << 16) + ((uint32_t)mid << 8) + (uint32_t)ll + term);
+}
+
+// T = keys per sequence (a multiple of 64, at most 384).  qkv rows: ld elements apart; Q / K /
+// V of head h at columns q_off / k_off / v_off + 64 h.  o rows: o_ld apart, head h at 64 h.
+template <uint32_t T>
 __global__ __launch_bounds__(256, 2) void attention_kernel(const int16_t* __restrict__ qkv, int16_t* __restrict__ o,
                                                            const int32_t* __restrict__ tab, uint32_t heads,
                                                            uint64_t ld, uint32_t q_off, uint32_t k_off,
                                                            uint32_t v_off, uint64_t o_ld, uint32_t cm, uint32_t cfg) {
-    constexpr uint32_t T = 4 * NK;
+    constexpr uint32_t KB = T / 16;          // key blocks of phase 1
+    constexpr uint32_t KS = T / 64;          // k steps of phase 3
+    constexpr uint32_t VS = T + 16;          // V^T plane row stride, bytes (rows 4 banks apart)
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    int32_t* stab = reinterpret_cast<int32_t*>(lds);                     // [4096]
-    uint8_t* region = lds + 16384;
-    int16_t* vt = reinterpret_cast<int16_t*>(region);                     // [64][T]
-    uint32_t* xch = reinterpret_cast<uint32_t*>(region + 2 * kHd * T);    // [2][4][64], past V^T
-    int32_t* red = reinterpret_cast<int32_t*>(region);                    // [4][64][64]
+    int32_t* stab = reinterpret_cast<int32_t*>(lds);                      // [4096]
+    uint8_t* vth = lds + 16384;                                           // [64][VS]
+    uint8_t* vtl = vth + kHd * VS;                                        // [64][VS]
+    int32_t* vsw = reinterpret_cast<int32_t*>(vtl + kHd * VS);            // [4][64]
 
-    const uint32_t t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const uint32_t t = threadIdx.x, lane = t & 63, w = t >> 6, c16 = lane & 15, g = lane >> 4;
     const uint32_t bh = blockIdx.y, b = bh / heads, h = bh - b * heads;
     const uint32_t q0 = blockIdx.x * kQb;
     const int16_t* seq = qkv + (uint64_t)b * T * ld;
 
-    // ---- staging: TAB, V^T, the lane's Q row
+    // ---- staging: TAB; V^T planes (task = 4 keys x 8 d: keys 4 qd + r, d 8 c ..); the
+    // per-wavefront V column sums
     for (uint32_t e = t; e < 1024; e += 256)
         reinterpret_cast<int4*>(stab)[e] = reinterpret_cast<const int4*>(tab)[e];
-    for (uint32_t e = t; e < T * (kHd / 8); e += 256) {
-        const uint32_t j = e >> 3, d0 = (e & 7) * 8;
-        const int4 v = *reinterpret_cast<const int4*>(seq + (uint64_t)j * ld + v_off + kHd * h + d0);
-        const int16_t* vv = reinterpret_cast<const int16_t*>(&v);
-#pragma unroll
-        for (uint32_t q = 0; q < 8; q++) vt[(d0 + q) * T + j] = vv[q];
-    }
-    const uint32_t qi = q0 + lane;
-    const bool qlive = qi < T;
-    uint32_t qr[kHd / 2];
     {
-        const int16_t* qrow = seq + (uint64_t)(qlive ? qi : 0) * ld + q_off + kHd * h;
+        const uint32_t c = t & 7;
+        int vpart[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-        for (uint32_t c = 0; c < kHd / 8; c++) {
-            const int4 v = *reinterpret_cast<const int4*>(qrow + 8 * c);
-            qr[4 * c] = v.x; qr[4 * c + 1] = v.y; qr[4 * c + 2] = v.z; qr[4 * c + 3] = v.w;
+        for (uint32_t it = 0; it < (T / 4 + 31) / 32; it++) {
+            const uint32_t qd = (t >> 3) + 32 * it;
+            if (qd >= T / 4) break;
+            const int16_t* vp = seq + (uint64_t)(4 * qd) * ld + v_off + kHd * h + 8 * c;
+            int4 x[4];
+#pragma unroll
+            for (uint32_t r = 0; r < 4; r++) x[r] = *reinterpret_cast<const int4*>(vp + (uint64_t)r * ld);
+            // key 16 kb + 4 g' + r sits at position 64 (kb / 4) + 16 g' + 4 (kb % 4) + r
+            const uint32_t p0 = 64 * (qd >> 4) + 16 * (qd & 3) + 4 * ((qd >> 2) & 3);
+#pragma unroll
+            for (uint32_t q = 0; q < 4; q++) {
+                const uint32_t a0 = dword(x[0], q), a1 = dword(x[1], q), a2 = dword(x[2], q), a3 = dword(x[3], q);
+                const uint32_t th01 = __builtin_amdgcn_perm(a1, a0, 0x07030501u);
+                const uint32_t th23 = __builtin_amdgcn_perm(a3, a2, 0x07030501u);
+                const uint32_t tl01 = __builtin_amdgcn_perm(a1, a0, 0x06020400u);
+                const uint32_t tl23 = __builtin_amdgcn_perm(a3, a2, 0x06020400u);
+                const uint32_t d0 = 8 * c + 2 * q;
+                // th01 = (a0.b1, a1.b1, a0.b3, a1.b3): the even element's high bytes of keys
+                // 0, 1 in its low half, the odd element's in its high half
+                *reinterpret_cast<uint32_t*>(vth + d0 * VS + p0) = __builtin_amdgcn_perm(th23, th01, 0x05040100u);
+                *reinterpret_cast<uint32_t*>(vth + (d0 + 1) * VS + p0) = __builtin_amdgcn_perm(th23, th01, 0x07060302u);
+                *reinterpret_cast<uint32_t*>(vtl + d0 * VS + p0) =
+                    __builtin_amdgcn_perm(tl23, tl01, 0x05040100u) ^ 0x80808080u;
+                *reinterpret_cast<uint32_t*>(vtl + (d0 + 1) * VS + p0) =
+                    __builtin_amdgcn_perm(tl23, tl01, 0x07060302u) ^ 0x80808080u;
+                vpart[2 * q] += (int)(int16_t)a0 + (int)(int16_t)a1 + (int)(int16_t)a2 + (int)(int16_t)a3;
+                vpart[2 * q + 1] += ((int)a0 >> 16) + ((int)a1 >> 16) + ((int)a2 >> 16) + ((int)a3 >> 16);
+            }
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < 8; q++) {
+            int x = vpart[q];
+            x += __shfl_xor(x, 8, 64);
+            x += __shfl_xor(x, 16, 64);
+            x += __shfl_xor(x, 32, 64);
+            vpart[q] = x;
+        }
+        if (lane < 8) {
+#pragma unroll
+            for (uint32_t q = 0; q < 8; q++) vsw[w * 64 + 8 * c + q] = vpart[q];
         }
     }
 
-    // ---- phase 1: scores of the wavefront's keys (K rows at wavefront-uniform addresses:
-    // scalar loads)
-    const uint32_t j0 = __builtin_amdgcn_readfirstlane(w * NK);
-    int32_t sv[NK];                    // register arrays: every index a constant (loops unrolled)
-#pragma unroll
-    for (uint32_t n = 0; n < NK; n++) {
-        const int16_t* krow = seq + (uint64_t)(j0 + n) * ld + k_off + kHd * h;
-        int acc = 0;
-#pragma unroll
-        for (uint32_t c = 0; c < kHd / 8; c++) {
-            const int4 kv = *reinterpret_cast<const int4*>(krow + 8 * c);
-            acc = dot2(qr[4 * c], kv.x, acc);
-            acc = dot2(qr[4 * c + 1], kv.y, acc);
-            acc = dot2(qr[4 * c + 2], kv.z, acc);
-            acc = dot2(qr[4 * c + 3], kv.w, acc);
-        }
-        sv[n] = sat16_shr8(acc);
-    }
+    // ---- the wavefront's Q rows (B of phase 1): query qi, d 16 g .. 16 g + 15
+    const uint32_t qi = q0 + 16 * w + c16;
+    v4i qh, ql;
+    int qsum;
+    limbs16(seq + (uint64_t)qi * ld + q_off + kHd * h + 16 * g, qh, ql, qsum);
+    qsum += __shfl_xor(qsum, 16, 64);
+    qsum += __shfl_xor(qsum, 32, 64);                  // sum_d Q[qi][d]
 
-    // ---- phase 2: the softmax over all T keys of the lane's query
+    // ---- phase 1: the scores, key block by key block
+    int32_t sv[4 * KB];                 // register arrays: every index a constant (loops unrolled)
+#pragma unroll
+    for (uint32_t kb = 0; kb < KB; kb++) {
+        v4i kh, kl;
+        int ksum;
+        limbs16(seq + (uint64_t)(16 * kb + c16) * ld + k_off + kHd * h + 16 * g, kh, kl, ksum);
+        ksum += __shfl_xor(ksum, 16, 64);
+        ksum += __shfl_xor(ksum, 32, 64);              // sum_d K[16 kb + c16][d] in every lane of c16
+        const v4i zero = {0, 0, 0, 0};
+        const v4i hh = mfma(kh, qh, zero);
+        v4i mid = mfma(kh, ql, zero);
+        mid = mfma(kl, qh, mid);
+        const v4i ll = mfma(kl, ql, zero);
+#pragma unroll
+        for (uint32_t r = 0; r < 4; r++) {
+            const int rs = __shfl(ksum, 4 * g + r, 64);  // key 16 kb + 4 g + r
+            const uint32_t term = 128u * (uint32_t)(rs + qsum) - 16384u * kHd;
+            sv[4 * kb + r] = sat16_shr8(wrap_sum(hh[r], mid[r], ll[r], term));
+        }
+    }
+    __syncthreads();                                   // TAB, V^T planes and V sums staged
+
+    // ---- phase 2: the softmax over the T keys of the lane's query (its lane group g = 0..3)
     int32_t mx = -32768;
 #pragma unroll
-    for (uint32_t n = 0; n < NK; n++) mx = max(mx, sv[n]);
-    xch[w * 64 + lane] = (uint32_t)mx;
-    __syncthreads();                                                     // also: TAB and V^T staged
-    mx = max(max((int32_t)xch[lane], (int32_t)xch[64 + lane]), max((int32_t)xch[128 + lane], (int32_t)xch[192 + lane]));
+    for (uint32_t n = 0; n < 4 * KB; n++) mx = max(mx, sv[n]);
+    mx = max(mx, __shfl_xor(mx, 16, 64));
+    mx = max(mx, __shfl_xor(mx, 32, 64));
     const uint32_t cs = cfg & 63u, fp = (cfg >> 8) & 31u;
     const uint64_t cm24 = cm & 0xFFFFFFu;
     uint32_t part = 0;
 #pragma unroll
-    for (uint32_t n = 0; n < NK; n++) {
+    for (uint32_t n = 0; n < 4 * KB; n++) {
         const uint64_t y = ((uint64_t)(uint32_t)(mx - sv[n]) * cm24) >> cs;
         const uint64_t sh = y >> 12;
         const uint32_t e = sh >= 63 ? 0u : (uint32_t)((uint64_t)(uint32_t)stab[y & 4095] >> sh);
         sv[n] = (int32_t)e;
         part += e;
     }
-    xch[256 + w * 64 + lane] = part;
-    __syncthreads();
-    const uint32_t S = xch[256 + lane] + xch[320 + lane] + xch[384 + lane] + xch[448 + lane];
-    const uint64_t R = ((uint64_t)1 << 40) / (uint64_t)(S ? S : 1u);
+    part += __shfl_xor(part, 16, 64);
+    part += __shfl_xor(part, 32, 64);
+    const uint64_t R = ((uint64_t)1 << 40) / (uint64_t)(part ? part : 1u);
     const uint32_t psh = 40 - fp;
     const uint64_t half = (uint64_t)1 << (psh - 1);
-    uint32_t pp[NK / 2];                                                 // (P[j], P[j+1]) pairs
+    int psum = 0;
 #pragma unroll
-    for (uint32_t n = 0; n < NK; n += 2) {
+    for (uint32_t n = 0; n < 4 * KB; n++) {
         const uint64_t a = ((uint64_t)(uint32_t)sv[n] * R + half) >> psh;
-        const uint64_t c = ((uint64_t)(uint32_t)sv[n + 1] * R + half) >> psh;
-        const uint32_t pa = a > 32767 ? 32767u : (uint32_t)a, pc = c > 32767 ? 32767u : (uint32_t)c;
-        pp[n / 2] = pa | (pc << 16);
+        sv[n] = a > 32767 ? 32767 : (int32_t)a;
+        psum += sv[n];
     }
+    psum += __shfl_xor(psum, 16, 64);
+    psum += __shfl_xor(psum, 32, 64);                  // sum_j P[qi][j]
 
-    // ---- phase 3: o over the wavefront's keys from V^T (k pairs of one d contiguous)
-    int32_t acc[kHd];
+    // ---- phase 3: o^T[d][qi] over 4 blocks of 16 d
+    v4i ohh[4], omid[4], oll[4];
 #pragma unroll
-    for (uint32_t d = 0; d < kHd; d++) acc[d] = 0;
+    for (uint32_t mb = 0; mb < 4; mb++) ohh[mb] = omid[mb] = oll[mb] = v4i{0, 0, 0, 0};
 #pragma unroll
-    for (uint32_t g = 0; g < NK / 8; g++) {
-        const uint32_t p0 = pp[4 * g], p1 = pp[4 * g + 1], p2 = pp[4 * g + 2], p3 = pp[4 * g + 3];
-        const int16_t* vcol = vt + j0 + 8 * g;
+    for (uint32_t ks = 0; ks < KS; ks++) {
+        // B: the lane's P of key blocks 4 ks + q, byte 4 q + r = key 16 (4 ks + q) + 4 g + r
+        uint32_t ph[4], pl[4];
 #pragma unroll
-        for (uint32_t d = 0; d < kHd; d++) {
-            const uint4 v = *reinterpret_cast<const uint4*>(vcol + d * T);
-            acc[d] = dot2(p3, v.w, dot2(p2, v.z, dot2(p1, v.y, dot2(p0, v.x, acc[d]))));
+        for (uint32_t q = 0; q < 4; q++) {
+            const uint32_t n = 4 * (4 * ks + q);
+            const uint32_t p01 = (uint32_t)sv[n] | ((uint32_t)sv[n + 1] << 16);      // P in [0, 32767]
+            const uint32_t p23 = (uint32_t)sv[n + 2] | ((uint32_t)sv[n + 3] << 16);
+            ph[q] = __builtin_amdgcn_perm(p23, p01, 0x07050301u);
+            pl[q] = __builtin_amdgcn_perm(p23, p01, 0x06040200u) ^ 0x80808080u;
+        }
+        const v4i bh4 = {(int)ph[0], (int)ph[1], (int)ph[2], (int)ph[3]};
+        const v4i bl4 = {(int)pl[0], (int)pl[1], (int)pl[2], (int)pl[3]};
+#pragma unroll
+        for (uint32_t mb = 0; mb < 4; mb++) {
+            const uint32_t off = (16 * mb + c16) * VS + 64 * ks + 16 * g;
+            const v4i vh = *reinterpret_cast<const v4i*>(vth + off);
+            const v4i vl = *reinterpret_cast<const v4i*>(vtl + off);
+            ohh[mb] = mfma(vh, bh4, ohh[mb]);
+            omid[mb] = mfma(vh, bl4, omid[mb]);
+            omid[mb] = mfma(vl, bh4, omid[mb]);
+            oll[mb] = mfma(vl, bl4, oll[mb]);
         }
     }
-    __syncthreads();                                                     // V^T done: the region is the partials
+    // result lane: query qi, d = 16 mb + 4 g + r
+    int16_t* orow = o + ((uint64_t)b * T + qi) * o_ld + kHd * h;
 #pragma unroll
-    for (uint32_t d = 0; d < kHd; d += 4)
-        *reinterpret_cast<int4*>(red + (w * 64 + lane) * kHd + d) = make_int4(acc[d], acc[d + 1], acc[d + 2], acc[d + 3]);
-    __syncthreads();
-    // thread t: query t / 4, 16 d from 16 (t % 4)
-    const uint32_t i = t >> 2, d0 = (t & 3) * 16;
-    if (q0 + i < T) {
-        uint32_t out[8];
+    for (uint32_t mb = 0; mb < 4; mb++) {
+        uint32_t pk[2];
 #pragma unroll
-        for (uint32_t d = 0; d < 16; d += 2) {
-            uint32_t s0 = 0, s1 = 0;
-#pragma unroll
-            for (uint32_t ww = 0; ww < 4; ww++) {
-                s0 += (uint32_t)red[(ww * 64 + i) * kHd + d0 + d];
-                s1 += (uint32_t)red[(ww * 64 + i) * kHd + d0 + d + 1];
-            }
-            out[d / 2] = (uint32_t)(uint16_t)sat16_shr8((int)s0) | ((uint32_t)(uint16_t)sat16_shr8((int)s1) << 16);
+        for (uint32_t r = 0; r < 4; r += 2) {
+            const uint32_t d = 16 * mb + 4 * g + r;
+            const int32_t vs0 = vsw[d] + vsw[64 + d] + vsw[128 + d] + vsw[192 + d];
+            const int32_t vs1 = vsw[d + 1] + vsw[65 + d] + vsw[129 + d] + vsw[193 + d];
+            const uint32_t t0 = 128u * (uint32_t)(vs0 + psum) - 16384u * T;
+            const uint32_t t1 = 128u * (uint32_t)(vs1 + psum) - 16384u * T;
+            const int o0 = sat16_shr8(wrap_sum(ohh[mb][r], omid[mb][r], oll[mb][r], t0));
+            const int o1 = sat16_shr8(wrap_sum(ohh[mb][r + 1], omid[mb][r + 1], oll[mb][r + 1], t1));
+            pk[r / 2] = (uint32_t)(uint16_t)o0 | ((uint32_t)(uint16_t)o1 << 16);
         }
-        int16_t* orow = o + ((uint64_t)b * T + q0 + i) * o_ld + kHd * h + d0;
-        *reinterpret_cast<uint4*>(orow) = make_uint4(out[0], out[1], out[2], out[3]);
-        *reinterpret_cast<uint4*>(orow + 8) = make_uint4(out[4], out[5], out[6], out[7]);
+        *reinterpret_cast<uint2*>(orow + 16 * mb + 4 * g) = make_uint2(pk[0], pk[1]);
     }
 }
 
-template <uint32_t NK>
+template <uint32_t T>
 void* attention_fn() {
-    return reinterpret_cast<void*>(&attention_kernel<NK>);
+    return reinterpret_cast<void*>(&attention_kernel<T>);
 }
 
 }  // namespace
@@ -196,24 +287,24 @@ extern "C" int cm_attention(const int16_t* qkv, int16_t* o, uint32_t batch, uint
     if (((smx_cfg >> 8) & 31u) > 39u || ((smx_cfg >> 8) & 31u) == 0u)
         return fail(CM_EINVAL, "attention: softmax output bits %u", (smx_cfg >> 8) & 31u);
     if ((uint64_t)batch * heads > 65535) return fail(CM_EINVAL, "attention: %u sequence-head pairs", batch * heads);
-    const size_t lds = 16384 + kRegion;
+    const size_t lds = 16384 + 2 * (size_t)kHd * (seq + 16) + 4 * 64 * sizeof(int32_t);
     if (lds > st->lds_per_block) return fail(CM_EINVAL, "attention: %zu bytes of LDS per workgroup", lds);
     hipStream_t s = as_stream(stream);
-    const dim3 grid((seq + kQb - 1) / kQb, batch * heads);
-#define CM_ATT(NK)                                                                                              \
-    case 4 * NK: {                                                                                              \
+    const dim3 grid(seq / kQb, batch * heads);
+#define CM_ATT(T)                                                                                               \
+    case T: {                                                                                                   \
         static bool attr = false;                                                                               \
         if (!attr) {                                                                                            \
-            CM_HIP_CHECK(hipFuncSetAttribute(attention_fn<NK>(), hipFuncAttributeMaxDynamicSharedMemorySize,    \
+            CM_HIP_CHECK(hipFuncSetAttribute(attention_fn<T>(), hipFuncAttributeMaxDynamicSharedMemorySize,     \
                                              (int)lds));                                                        \
             attr = true;                                                                                        \
         }                                                                                                       \
-        CM_LAUNCH("attention_kernel", attention_kernel<NK>, grid, dim3(256), lds, s, qkv, o, st->smx_tab,      \
+        CM_LAUNCH("attention_kernel", attention_kernel<T>, grid, dim3(256), lds, s, qkv, o, st->smx_tab,       \
                   heads, ld, q_off, k_off, v_off, o_ld, smx_cm, smx_cfg);                                       \
         return CM_OK;                                                                                           \
     }
     switch (seq) {
-        CM_ATT(16) CM_ATT(32) CM_ATT(64) CM_ATT(96)
+        CM_ATT(64) CM_ATT(128) CM_ATT(256) CM_ATT(384)
     default: break;
     }
 #undef CM_ATT

@@ -718,18 +718,33 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
     const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const uint32_t wr = wave >> 1, wc = wave & 1, l32 = lane & 31, lh = lane >> 5;
 
-    // row / column terms of the epilogue, summed from the slab partials now so that their
-    // loads overlap the first copies
-    for (uint32_t e = t; e < (mode == kPartial ? 0u : TM + BN); e += NT) {
-        const bool is_row = e < TM;
-        const uint32_t line = is_row ? tr * TM + e : tc * BN + (e - TM);
-        const int32_t* pp = is_row ? rpart + bt * rp_slice + line : cpart + bt * cp_slice + line;
-        const uint32_t stride = is_row ? a_lines : b_lines;
-        int32_t sum = 0;
-        for (uint32_t q = 0; q < nslab; q++) sum += pp[(uint64_t)q * stride];
-        if (is_row) rterm[e] = make_int2(epi.row_bias(line) - k64 + (sum >> 1), (sum & 1) << 7);
-        else cterm[e - TM] = make_int2(sum >> 1, (sum & 1) << 7);
+    // Row / column terms of the epilogue from the slab partials: the first slab's loads are
+    // issued here and used only after the first copies have been issued, so that the two
+    // latencies overlap; the other slabs and the LDS writes follow the copies.
+    constexpr int TE = (TM + BN + NT - 1) / NT;  // term elements per thread
+    int32_t tsum[TE];
+#pragma unroll
+    for (int q = 0; q < TE; q++) {
+        const uint32_t e = t + q * NT;
+        tsum[q] = 0;
+        if (mode != kPartial && e < TM + BN)
+            tsum[q] = e < TM ? rpart[bt * rp_slice + tr * TM + e] : cpart[bt * cp_slice + tc * BN + (e - TM)];
     }
+    auto finish_terms = [&]() {
+#pragma unroll
+        for (int q = 0; q < TE; q++) {
+            const uint32_t e = t + q * NT;
+            if (mode == kPartial || e >= TM + BN) continue;
+            const bool is_row = e < TM;
+            const uint32_t line = is_row ? tr * TM + e : tc * BN + (e - TM);
+            const int32_t* pp = is_row ? rpart + bt * rp_slice + line : cpart + bt * cp_slice + line;
+            const uint32_t stride = is_row ? a_lines : b_lines;
+            int32_t sum = tsum[q];
+            for (uint32_t sl = 1; sl < nslab; sl++) sum += pp[(uint64_t)sl * stride];
+            if (is_row) rterm[e] = make_int2(epi.row_bias(line) - k64 + (sum >> 1), (sum & 1) << 7);
+            else cterm[e - TM] = make_int2(sum >> 1, (sum & 1) << 7);
+        }
+    };
 
     // copy assignment: wave w fills 16-row blocks 2w, 2w + 1 of each A plane and BCP blocks
     // from BCP w of each B plane; lane l takes row 16 b + l / 4, physical chunk l % 4 =
@@ -776,7 +791,8 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
     // g issue theirs in slots 4g .. 4g + 3, two, two, then the rest; with 2 waves (12 copies)
     // the one group issues two in each of slots 0 .. 5.
 #define CM_COPIES(SM, step, slot)                                                 \
-    if (NW == 2) {                                                                \
+    if (!cp_) {                                                                   \
+    } else if (NW == 2) {                                                         \
         if ((slot) < 6) { CM_COPY(SM, step, 2 * (slot)) CM_COPY(SM, step, 2 * (slot) + 1) } \
     } else if (((slot) >> 2) == cgrp) {                                           \
         constexpr int s_ = (slot) & 3;                                            \
@@ -799,8 +815,7 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
         ACC[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(X[i], Y[j], ACC[i][j], 0, 0, 0);       \
     __builtin_amdgcn_sched_barrier(0);
     // One k step on stage SMC while later steps land in the others; SMI receives step
-    // kt + NST - 1 (past the last step the copy repeats step nk - 1, so every step has the
-    // same shape).  Two 32-k substeps of 16 MFMAs (hh, mid = h l, ll, mid = l h: no MFMA
+    // kt + NST - 1 when there is one (a wave-uniform branch around each copy).  Two 32-k substeps of 16 MFMAs (hh, mid = h l, ll, mid = l h: no MFMA
     // waits on the one before); the step's copies sit between MFMA groups of the substep
     // of the wave's copy group, so that while one wave of a SIMD spends issue cycles on
     // copies the other has MFMAs to issue, and the sched_barriers keep the compiler from
@@ -815,10 +830,12 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
     CM_MFMA4(mid, al, bh) CM_COPIES(SMI, st, S0 + 3)
 #define CM_STEP(kt, SMC, SMI)                                                     \
     {                                                                             \
-        const uint32_t st_ = min((kt) + NST - 1, nk - 1);                         \
+        const uint32_t st_ = (kt) + NST - 1;                                      \
+        const bool cp_ = st_ < nk;                                                \
         CM_SUBSTEP(SMC, SMI, st_, ch0, 0)                                         \
         CM_SUBSTEP(SMC, SMI, st_, ch1, 4)                                         \
-        __builtin_amdgcn_s_waitcnt(NST == 3 ? (0x0070 | NC) : 0x0070);            \
+        if (NST == 3 && cp_) __builtin_amdgcn_s_waitcnt(0x0070 | NC);             \
+        else __builtin_amdgcn_s_waitcnt(0x0070);                                  \
         __builtin_amdgcn_s_barrier();                                             \
     }
 #define CM_ISSUE(SM, step)                                                        \
@@ -827,8 +844,14 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
     uint32_t kt = 0;
     if constexpr (NST == 3) {
         CM_ISSUE(sm0, 0)
-        CM_ISSUE(sm1, min(1u, nk - 1))
-        __builtin_amdgcn_s_waitcnt(0x0070 | NC);
+        if (nk > 1) {
+            CM_ISSUE(sm1, 1)
+            finish_terms();
+            __builtin_amdgcn_s_waitcnt(0x0070 | NC);
+        } else {
+            finish_terms();
+            __builtin_amdgcn_s_waitcnt(0x0070);
+        }
         __builtin_amdgcn_s_barrier();
         for (; kt + 3 <= nk; kt += 3) {
             CM_STEP(kt, sm0, sm2)
@@ -839,6 +862,7 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
         if (kt + 1 < nk) CM_STEP(kt + 1, sm1, sm0)
     } else {
         CM_ISSUE(sm0, 0)
+        finish_terms();
         __builtin_amdgcn_s_waitcnt(0x0070);
         __builtin_amdgcn_s_barrier();
         for (; kt + 2 <= nk; kt += 2) {

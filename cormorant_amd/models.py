@@ -181,8 +181,12 @@ class BertShape:
         att = 2 * self.batch * self.heads * self.seq * self.seq * self.hd
         return self.layers * (lin + att)
 
+    def linear_macs(self) -> int:
+        """Multiply-accumulates of the linears alone (the plane GEMM's share of a forward)."""
+        return self.layers * self.batch * self.seq * (4 * self.d * self.d + 2 * self.d * self.ff)
 
-def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int = 1, fused_attention: bool = False):
+
+def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int = 1, fused_attention: bool = True):
     """(graph, inputs, exps): the BERT-base-shaped encoder in per-tensor power-of-two numerics.
 
     Token ids U{0 .. vocab-1} and embedding rows N(0, 1) (the embedding lookup is the host
@@ -206,9 +210,9 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
     largest |value|, and each tensor takes the largest exponent that keeps it below 32767
     with a 1.25 margin; the contractions' output exponents follow from their operands', the
     q / v exponents are lowered where the scores or P.V would not fit.  ``exps`` records them.
-    ``fused_attention``: the head split, q.K^T, the softmax, P.V and the merge as one
-    AttentionNode (the same arithmetic in one call, cm_attention); False (faster on the
-    MI355X at this shape): node by node on the plane GEMM.
+    ``fused_attention`` (default): the head split, q.K^T, the softmax, P.V and the merge as
+    one AttentionNode (the same arithmetic in one call, cm_attention on MFMA); False: node by
+    node, the contractions on the plane GEMM reading and writing per-head views in place.
     """
     from .numeric import encode_matmul_weights
     from .dtype import AP_FIXED_16_8

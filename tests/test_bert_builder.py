@@ -77,6 +77,7 @@ def test_head_view_gather_scatter():
 def test_full_shape_macs():
     # 12 x 3072 x (4 x 768^2 + 2 x 768 x 3072) + 2 x 8 x 12 x 384^2 x 64 x 12
     assert models.BertShape().macs() == 260_919_263_232 + 21_743_271_936
+    assert models.BertShape().linear_macs() == 260_919_263_232
 
 
 def test_fused_attention_oracle_equals_node_by_node():

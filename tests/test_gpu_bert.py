@@ -1,7 +1,8 @@
 """The BERT-shaped encoder on the GPU (Simulator) against the value-domain restatement of
 the reference simulator (oracle_graph), every tensor of every layer bit for bit: LayerNorm32
-and ResAddBias on row-ops, the fused QKV projection, the head split / merge permutes, the
-batched attention contractions (int32 wrap), the keys-major softmax, GELU on the act unit."""
+and ResAddBias on row-ops, the fused QKV projection, the attention (one fused node, or the
+batched contractions on per-head views, int32 wrap, with the keys-major softmax), GELU on the
+act unit."""
 import numpy as np
 import pytest
 
