@@ -11,7 +11,9 @@
 // Both contractions run on v_mfma_i32_16x16x64_i8 over byte limbs: x - 128 = 256 h + l with
 // h = x >> 8 and l = (x & 255) - 128, so that
 //   sum a b = 2^16 HH + 2^8 (HL + LH) + LL + 128 sum a + 128 sum b - 16384 K   (mod 2^32),
-// the int32-wrapped sum exactly (the wrap makes every term's order free).
+// the int32-wrapped sum exactly (the wrap makes every term's order free).  Phase 1 takes the
+// operand sums as limb sums from MFMAs against an all-ones operand, already in the result
+// layout; phase 3 takes them from the staging and a lane-group reduction.
 //
 // Workgroup: 4 wavefronts, wavefront w owns queries q0 + 16 w .. + 15 end to end.  MFMA
 // layouts (16 x 16 blocks): operand lane l holds row / column l % 16 and 16 bytes of k slot
@@ -21,11 +23,14 @@
 //            with the scores of keys 16 kb + 4 g + r, r < 4, for all T / 16 blocks;
 //   phase 2: the softmax per query over its lane group (shuffles across g; no LDS):
 //            e = TAB[y & 4095] >> (y >> 12), y = (max - s) Cm >> Cs, R = floor(2^40 / S),
-//            P = min((e R + 2^(39 - fp)) >> (40 - fp), 32767) (the unit's integer rule);
+//            P = min((e R + 2^(39 - fp)) >> (40 - fp), 32767) (the unit's integer rule; y in
+//            32 bits below dlim, P through an exact double);
 //   phase 3: o^T = V^T P^T: P stays in registers as the B operand, its k slots the lane's own
 //            keys (slot 16 g + 4 q + r of k step ks = key 16 (4 ks + q) + 4 g + r); V^T is
-//            split into byte planes in LDS once per workgroup in that key order.
-// LDS: TAB (16 KiB) + V^T hi / lo planes [64][T + 16] + the V column-sum partials.
+//            split into byte planes in LDS in that key order, 32 d at a time (the first half
+//            staged before phase 1, the second after the first half's products).
+// LDS: TAB (16 KiB) + V^T hi / lo planes [32][T + 16] + the V column-sum partials, 42.6 KiB at
+// T = 384: three workgroups per compute unit, so that BERT's 576 workgroups are resident at once.
 #include "cm_common.h"
 
 #include <algorithm>
@@ -37,31 +42,23 @@ constexpr uint32_t kHd = 64;                 // head dimension
 constexpr uint32_t kQb = 64;                 // queries per workgroup
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef short v2s __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ int dot2(uint32_t a, uint32_t b, int c) {
-    return __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, a), __builtin_bit_cast(v2s, b), c, false);
-}
-
 __device__ __forceinline__ int sat16_shr8(int acc) { return min(max(acc >> 8, -32768), 32767); }
 
-// 8 int16 -> their high bytes and low bytes ^ 0x80 (two dwords each) and their sum
-__device__ __forceinline__ void limbs8(const int4 v, uint32_t& h0, uint32_t& h1, uint32_t& l0, uint32_t& l1, int& sum) {
+// 8 int16 -> their high bytes and low bytes ^ 0x80 (two dwords each)
+__device__ __forceinline__ void limbs8(const int4 v, uint32_t& h0, uint32_t& h1, uint32_t& l0, uint32_t& l1) {
     const uint32_t x = (uint32_t)v.x, y = (uint32_t)v.y, z = (uint32_t)v.z, u = (uint32_t)v.w;
     h0 = __builtin_amdgcn_perm(y, x, 0x07050301u);
     h1 = __builtin_amdgcn_perm(u, z, 0x07050301u);
     l0 = __builtin_amdgcn_perm(y, x, 0x06040200u) ^ 0x80808080u;
     l1 = __builtin_amdgcn_perm(u, z, 0x06040200u) ^ 0x80808080u;
-    sum = dot2(u, 0x00010001u, dot2(z, 0x00010001u, dot2(y, 0x00010001u, dot2(x, 0x00010001u, sum))));
 }
 
-// 16 consecutive int16 at p (16-byte aligned) -> the hi / lo limb operands and their sum
-__device__ __forceinline__ void limbs16(const int16_t* p, v4i& hi, v4i& lo, int& sum) {
+// 16 consecutive int16 at p (16-byte aligned) -> the hi / lo limb operands
+__device__ __forceinline__ void limbs16(const int16_t* p, v4i& hi, v4i& lo) {
     const int4 a = *reinterpret_cast<const int4*>(p), b = *reinterpret_cast<const int4*>(p + 8);
     uint32_t h0, h1, h2, h3, l0, l1, l2, l3;
-    sum = 0;
-    limbs8(a, h0, h1, l0, l1, sum);
-    limbs8(b, h2, h3, l2, l3, sum);
+    limbs8(a, h0, h1, l0, l1);
+    limbs8(b, h2, h3, l2, l3);
     hi = v4i{(int)h0, (int)h1, (int)h2, (int)h3};
     lo = v4i{(int)l0, (int)l1, (int)l2, (int)l3};
 }
@@ -82,36 +79,36 @@ __device__ __forceinline__ int32_t wrap_sum(int32_t hh, int32_t mid, int32_t ll,
 // T = keys per sequence (a multiple of 64, at most 384).  qkv rows: ld elements apart; Q / K /
 // V of head h at columns q_off / k_off / v_off + 64 h.  o rows: o_ld apart, head h at 64 h.
 template <uint32_t T>
-__global__ __launch_bounds__(256, 2) void attention_kernel(const int16_t* __restrict__ qkv, int16_t* __restrict__ o,
+__global__ __launch_bounds__(256, 3) void attention_kernel(const int16_t* __restrict__ qkv, int16_t* __restrict__ o,
                                                            const int32_t* __restrict__ tab, uint32_t heads,
                                                            uint64_t ld, uint32_t q_off, uint32_t k_off,
-                                                           uint32_t v_off, uint64_t o_ld, uint32_t cm, uint32_t cfg) {
+                                                           uint32_t v_off, uint64_t o_ld, uint32_t cm, uint32_t cfg,
+                                                           uint32_t dlim) {
     constexpr uint32_t KB = T / 16;          // key blocks of phase 1
     constexpr uint32_t KS = T / 64;          // k steps of phase 3
     constexpr uint32_t VS = T + 16;          // V^T plane row stride, bytes (rows 4 banks apart)
+    constexpr uint32_t HD = kHd / 2;         // d per staged half
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int32_t* stab = reinterpret_cast<int32_t*>(lds);                      // [4096]
-    uint8_t* vth = lds + 16384;                                           // [64][VS]
-    uint8_t* vtl = vth + kHd * VS;                                        // [64][VS]
-    int32_t* vsw = reinterpret_cast<int32_t*>(vtl + kHd * VS);            // [4][64]
+    uint8_t* vth = lds + 16384;                                           // [32][VS]
+    uint8_t* vtl = vth + HD * VS;                                         // [32][VS]
+    int32_t* vsw = reinterpret_cast<int32_t*>(vtl + HD * VS);             // [4][64]
 
     const uint32_t t = threadIdx.x, lane = t & 63, w = t >> 6, c16 = lane & 15, g = lane >> 4;
     const uint32_t bh = blockIdx.y, b = bh / heads, h = bh - b * heads;
     const uint32_t q0 = blockIdx.x * kQb;
     const int16_t* seq = qkv + (uint64_t)b * T * ld;
 
-    // ---- staging: TAB; V^T planes (task = 4 keys x 8 d: keys 4 qd + r, d 8 c ..); the
-    // per-wavefront V column sums
-    for (uint32_t e = t; e < 1024; e += 256)
-        reinterpret_cast<int4*>(stab)[e] = reinterpret_cast<const int4*>(tab)[e];
-    {
-        const uint32_t c = t & 7;
+    // V^T planes of d 32 half .. + 31 (task = 4 keys x 8 d: keys 4 qd + r, d 8 (4 half + c) ..)
+    // and the per-wavefront column sums of those d
+    auto stage_v = [&](uint32_t half) {
+        const uint32_t c = t & 3;
         int vpart[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-        for (uint32_t it = 0; it < (T / 4 + 31) / 32; it++) {
-            const uint32_t qd = (t >> 3) + 32 * it;
+        for (uint32_t it = 0; it < (T / 4 + 63) / 64; it++) {
+            const uint32_t qd = (t >> 2) + 64 * it;
             if (qd >= T / 4) break;
-            const int16_t* vp = seq + (uint64_t)(4 * qd) * ld + v_off + kHd * h + 8 * c;
+            const int16_t* vp = seq + (uint64_t)(4 * qd) * ld + v_off + kHd * h + HD * half + 8 * c;
             int4 x[4];
 #pragma unroll
             for (uint32_t r = 0; r < 4; r++) x[r] = *reinterpret_cast<const int4*>(vp + (uint64_t)r * ld);
@@ -140,44 +137,51 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const int16_t* __rest
 #pragma unroll
         for (uint32_t q = 0; q < 8; q++) {
             int x = vpart[q];
+            x += __shfl_xor(x, 4, 64);
             x += __shfl_xor(x, 8, 64);
             x += __shfl_xor(x, 16, 64);
             x += __shfl_xor(x, 32, 64);
             vpart[q] = x;
         }
-        if (lane < 8) {
+        if (lane < 4) {
 #pragma unroll
-            for (uint32_t q = 0; q < 8; q++) vsw[w * 64 + 8 * c + q] = vpart[q];
+            for (uint32_t q = 0; q < 8; q++) vsw[w * 64 + HD * half + 8 * c + q] = vpart[q];
         }
-    }
+    };
+
+    // ---- staging: TAB and the first half of V^T
+    for (uint32_t e = t; e < 1024; e += 256)
+        reinterpret_cast<int4*>(stab)[e] = reinterpret_cast<const int4*>(tab)[e];
+    stage_v(0);
 
     // ---- the wavefront's Q rows (B of phase 1): query qi, d 16 g .. 16 g + 15
     const uint32_t qi = q0 + 16 * w + c16;
     v4i qh, ql;
-    int qsum;
-    limbs16(seq + (uint64_t)qi * ld + q_off + kHd * h + 16 * g, qh, ql, qsum);
-    qsum += __shfl_xor(qsum, 16, 64);
-    qsum += __shfl_xor(qsum, 32, 64);                  // sum_d Q[qi][d]
+    limbs16(seq + (uint64_t)qi * ld + q_off + kHd * h + 16 * g, qh, ql);
+    // The offset terms from MFMAs against ones (A' = A - 128 = 256 h + l):
+    //   sum_d K Q = 2^16 HH + 2^8 MID + LL + 2^15 (sum h_K + sum h_Q) + 2^7 (sum l_K + sum l_Q) + 2^20,
+    // the limb sums of Q (columns) once, those of K (rows) per key block on top of them.
+    const v4i zero = {0, 0, 0, 0};
+    const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+    const v4i c20 = {1 << 20, 1 << 20, 1 << 20, 1 << 20};
+    const v4i qh1 = mfma(ones, qh, zero), ql1 = mfma(ones, ql, zero);
 
     // ---- phase 1: the scores, key block by key block
     int32_t sv[4 * KB];                 // register arrays: every index a constant (loops unrolled)
 #pragma unroll
     for (uint32_t kb = 0; kb < KB; kb++) {
         v4i kh, kl;
-        int ksum;
-        limbs16(seq + (uint64_t)(16 * kb + c16) * ld + k_off + kHd * h + 16 * g, kh, kl, ksum);
-        ksum += __shfl_xor(ksum, 16, 64);
-        ksum += __shfl_xor(ksum, 32, 64);              // sum_d K[16 kb + c16][d] in every lane of c16
-        const v4i zero = {0, 0, 0, 0};
+        limbs16(seq + (uint64_t)(16 * kb + c16) * ld + k_off + kHd * h + 16 * g, kh, kl);
         const v4i hh = mfma(kh, qh, zero);
         v4i mid = mfma(kh, ql, zero);
         mid = mfma(kl, qh, mid);
-        const v4i ll = mfma(kl, ql, zero);
+        const v4i ll = mfma(kl, ql, c20);
+        const v4i ha = mfma(kh, ones, qh1), la = mfma(kl, ones, ql1);
 #pragma unroll
         for (uint32_t r = 0; r < 4; r++) {
-            const int rs = __shfl(ksum, 4 * g + r, 64);  // key 16 kb + 4 g + r
-            const uint32_t term = 128u * (uint32_t)(rs + qsum) - 16384u * kHd;
-            sv[4 * kb + r] = sat16_shr8(wrap_sum(hh[r], mid[r], ll[r], term));
+            const uint32_t acc = ((uint32_t)hh[r] << 16) + ((uint32_t)mid[r] << 8) + (uint32_t)ll[r] +
+                                 ((uint32_t)ha[r] << 15) + ((uint32_t)la[r] << 7);
+            sv[4 * kb + r] = sat16_shr8((int32_t)acc);
         }
     }
     __syncthreads();                                   // TAB, V^T planes and V sums staged
@@ -188,78 +192,89 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(const int16_t* __rest
     for (uint32_t n = 0; n < 4 * KB; n++) mx = max(mx, sv[n]);
     mx = max(mx, __shfl_xor(mx, 16, 64));
     mx = max(mx, __shfl_xor(mx, 32, 64));
+    // e(d), d = max - s: below dlim y = (d Cm) >> Cs < 2^17 and e = TAB[y & 4095] >> (y >> 12);
+    // from dlim on e = 0 (TAB <= 2^16)
     const uint32_t cs = cfg & 63u, fp = (cfg >> 8) & 31u;
     const uint64_t cm24 = cm & 0xFFFFFFu;
     uint32_t part = 0;
 #pragma unroll
     for (uint32_t n = 0; n < 4 * KB; n++) {
-        const uint64_t y = ((uint64_t)(uint32_t)(mx - sv[n]) * cm24) >> cs;
-        const uint64_t sh = y >> 12;
-        const uint32_t e = sh >= 63 ? 0u : (uint32_t)((uint64_t)(uint32_t)stab[y & 4095] >> sh);
+        const uint32_t d = (uint32_t)(mx - sv[n]);
+        const uint32_t y = (uint32_t)(((uint64_t)d * cm24) >> cs);
+        const uint32_t e = ((uint32_t)stab[y & 4095] >> ((y >> 12) & 31)) & (d < dlim ? ~0u : 0u);   // no branch
         sv[n] = (int32_t)e;
         part += e;
     }
     part += __shfl_xor(part, 16, 64);
     part += __shfl_xor(part, 32, 64);
+    // P = min(floor(e R 2^(fp - 40) + 1/2), 32767), R = floor(2^40 / S): e <= S, so e R <= 2^40
+    // and e R 2^(fp - 40) + 1/2 has at most 41 significant bits, exact in double; the
+    // conversion truncates (the floor of a positive value) and saturates
     const uint64_t R = ((uint64_t)1 << 40) / (uint64_t)(part ? part : 1u);
-    const uint32_t psh = 40 - fp;
-    const uint64_t half = (uint64_t)1 << (psh - 1);
+    const double rd = __builtin_ldexp((double)R, (int)fp - 40);
     int psum = 0;
 #pragma unroll
     for (uint32_t n = 0; n < 4 * KB; n++) {
-        const uint64_t a = ((uint64_t)(uint32_t)sv[n] * R + half) >> psh;
-        sv[n] = a > 32767 ? 32767 : (int32_t)a;
+        sv[n] = (int32_t)__builtin_fmin(__builtin_fma((double)(uint32_t)sv[n], rd, 0.5), 32767.0);
         psum += sv[n];
     }
     psum += __shfl_xor(psum, 16, 64);
     psum += __shfl_xor(psum, 32, 64);                  // sum_j P[qi][j]
 
-    // ---- phase 3: o^T[d][qi] over 4 blocks of 16 d
-    v4i ohh[4], omid[4], oll[4];
+    // ---- phase 3: o^T[d][qi] over 4 blocks of 16 d, two per staged half of V^T
+    int16_t* orow = o + ((uint64_t)b * T + qi) * o_ld + kHd * h;      // result lane: d = 16 mb + 4 g + r
 #pragma unroll
-    for (uint32_t mb = 0; mb < 4; mb++) ohh[mb] = omid[mb] = oll[mb] = v4i{0, 0, 0, 0};
-#pragma unroll
-    for (uint32_t ks = 0; ks < KS; ks++) {
-        // B: the lane's P of key blocks 4 ks + q, byte 4 q + r = key 16 (4 ks + q) + 4 g + r
-        uint32_t ph[4], pl[4];
-#pragma unroll
-        for (uint32_t q = 0; q < 4; q++) {
-            const uint32_t n = 4 * (4 * ks + q);
-            const uint32_t p01 = (uint32_t)sv[n] | ((uint32_t)sv[n + 1] << 16);      // P in [0, 32767]
-            const uint32_t p23 = (uint32_t)sv[n + 2] | ((uint32_t)sv[n + 3] << 16);
-            ph[q] = __builtin_amdgcn_perm(p23, p01, 0x07050301u);
-            pl[q] = __builtin_amdgcn_perm(p23, p01, 0x06040200u) ^ 0x80808080u;
+    for (uint32_t half = 0; half < 2; half++) {
+        if (half == 1) {
+            __syncthreads();                           // every wavefront done with the first half
+            stage_v(1);
+            __syncthreads();
         }
-        const v4i bh4 = {(int)ph[0], (int)ph[1], (int)ph[2], (int)ph[3]};
-        const v4i bl4 = {(int)pl[0], (int)pl[1], (int)pl[2], (int)pl[3]};
+        v4i ohh[2], omid[2], oll[2];
 #pragma unroll
-        for (uint32_t mb = 0; mb < 4; mb++) {
-            const uint32_t off = (16 * mb + c16) * VS + 64 * ks + 16 * g;
-            const v4i vh = *reinterpret_cast<const v4i*>(vth + off);
-            const v4i vl = *reinterpret_cast<const v4i*>(vtl + off);
-            ohh[mb] = mfma(vh, bh4, ohh[mb]);
-            omid[mb] = mfma(vh, bl4, omid[mb]);
-            omid[mb] = mfma(vl, bh4, omid[mb]);
-            oll[mb] = mfma(vl, bl4, oll[mb]);
+        for (uint32_t m = 0; m < 2; m++) ohh[m] = omid[m] = oll[m] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (uint32_t ks = 0; ks < KS; ks++) {
+            // B: the lane's P of key blocks 4 ks + q, byte 4 q + r = key 16 (4 ks + q) + 4 g + r
+            uint32_t ph[4], pl[4];
+#pragma unroll
+            for (uint32_t q = 0; q < 4; q++) {
+                const uint32_t n = 4 * (4 * ks + q);
+                const uint32_t p01 = (uint32_t)sv[n] | ((uint32_t)sv[n + 1] << 16);      // P in [0, 32767]
+                const uint32_t p23 = (uint32_t)sv[n + 2] | ((uint32_t)sv[n + 3] << 16);
+                ph[q] = __builtin_amdgcn_perm(p23, p01, 0x07050301u);
+                pl[q] = __builtin_amdgcn_perm(p23, p01, 0x06040200u) ^ 0x80808080u;
+            }
+            const v4i bh4 = {(int)ph[0], (int)ph[1], (int)ph[2], (int)ph[3]};
+            const v4i bl4 = {(int)pl[0], (int)pl[1], (int)pl[2], (int)pl[3]};
+#pragma unroll
+            for (uint32_t m = 0; m < 2; m++) {
+                const uint32_t off = (16 * m + c16) * VS + 64 * ks + 16 * g;
+                const v4i vh = *reinterpret_cast<const v4i*>(vth + off);
+                const v4i vl = *reinterpret_cast<const v4i*>(vtl + off);
+                ohh[m] = mfma(vh, bh4, ohh[m]);
+                omid[m] = mfma(vh, bl4, omid[m]);
+                omid[m] = mfma(vl, bh4, omid[m]);
+                oll[m] = mfma(vl, bl4, oll[m]);
+            }
         }
-    }
-    // result lane: query qi, d = 16 mb + 4 g + r
-    int16_t* orow = o + ((uint64_t)b * T + qi) * o_ld + kHd * h;
 #pragma unroll
-    for (uint32_t mb = 0; mb < 4; mb++) {
-        uint32_t pk[2];
+        for (uint32_t m = 0; m < 2; m++) {
+            const uint32_t mb = 2 * half + m;
+            uint32_t pk[2];
 #pragma unroll
-        for (uint32_t r = 0; r < 4; r += 2) {
-            const uint32_t d = 16 * mb + 4 * g + r;
-            const int32_t vs0 = vsw[d] + vsw[64 + d] + vsw[128 + d] + vsw[192 + d];
-            const int32_t vs1 = vsw[d + 1] + vsw[65 + d] + vsw[129 + d] + vsw[193 + d];
-            const uint32_t t0 = 128u * (uint32_t)(vs0 + psum) - 16384u * T;
-            const uint32_t t1 = 128u * (uint32_t)(vs1 + psum) - 16384u * T;
-            const int o0 = sat16_shr8(wrap_sum(ohh[mb][r], omid[mb][r], oll[mb][r], t0));
-            const int o1 = sat16_shr8(wrap_sum(ohh[mb][r + 1], omid[mb][r + 1], oll[mb][r + 1], t1));
-            pk[r / 2] = (uint32_t)(uint16_t)o0 | ((uint32_t)(uint16_t)o1 << 16);
+            for (uint32_t r = 0; r < 4; r += 2) {
+                const uint32_t d = 16 * mb + 4 * g + r;
+                const int32_t vs0 = vsw[d] + vsw[64 + d] + vsw[128 + d] + vsw[192 + d];
+                const int32_t vs1 = vsw[d + 1] + vsw[65 + d] + vsw[129 + d] + vsw[193 + d];
+                const uint32_t t0 = 128u * (uint32_t)(vs0 + psum) - 16384u * T;
+                const uint32_t t1 = 128u * (uint32_t)(vs1 + psum) - 16384u * T;
+                const int o0 = sat16_shr8(wrap_sum(ohh[m][r], omid[m][r], oll[m][r], t0));
+                const int o1 = sat16_shr8(wrap_sum(ohh[m][r + 1], omid[m][r + 1], oll[m][r + 1], t1));
+                pk[r / 2] = (uint32_t)(uint16_t)o0 | ((uint32_t)(uint16_t)o1 << 16);
+            }
+            *reinterpret_cast<uint2*>(orow + 16 * mb + 4 * g) = make_uint2(pk[0], pk[1]);
         }
-        *reinterpret_cast<uint2*>(orow + 16 * mb + 4 * g) = make_uint2(pk[0], pk[1]);
     }
 }
 
@@ -287,9 +302,10 @@ extern "C" int cm_attention(const int16_t* qkv, int16_t* o, uint32_t batch, uint
     if (((smx_cfg >> 8) & 31u) > 39u || ((smx_cfg >> 8) & 31u) == 0u)
         return fail(CM_EINVAL, "attention: softmax output bits %u", (smx_cfg >> 8) & 31u);
     if ((uint64_t)batch * heads > 65535) return fail(CM_EINVAL, "attention: %u sequence-head pairs", batch * heads);
-    const size_t lds = 16384 + 2 * (size_t)kHd * (seq + 16) + 4 * 64 * sizeof(int32_t);
+    const size_t lds = 16384 + 2 * (size_t)(kHd / 2) * (seq + 16) + 4 * 64 * sizeof(int32_t);
     if (lds > st->lds_per_block) return fail(CM_EINVAL, "attention: %zu bytes of LDS per workgroup", lds);
     hipStream_t s = as_stream(stream);
+    const uint32_t dlim = smx_dlim(smx_cm & 0xFFFFFFu, smx_cfg & 63u);
     const dim3 grid(seq / kQb, batch * heads);
 #define CM_ATT(T)                                                                                               \
     case T: {                                                                                                   \
@@ -300,7 +316,7 @@ extern "C" int cm_attention(const int16_t* qkv, int16_t* o, uint32_t batch, uint
             attr = true;                                                                                        \
         }                                                                                                       \
         CM_LAUNCH("attention_kernel", attention_kernel<T>, grid, dim3(256), lds, s, qkv, o, st->smx_tab,       \
-                  heads, ld, q_off, k_off, v_off, o_ld, smx_cm, smx_cfg);                                       \
+                  heads, ld, q_off, k_off, v_off, o_ld, smx_cm, smx_cfg, dlim);                                 \
         return CM_OK;                                                                                           \
     }
     switch (seq) {

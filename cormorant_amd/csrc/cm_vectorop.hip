@@ -121,7 +121,6 @@ __global__ __launch_bounds__(256) void vectorop_kernel(const int16_t* __restrict
 // words l16 + 16 k, k < KW.  Max and sum reduce over the 16 lanes in four DPP steps that
 // leave the result in every lane; a wavefront works on four rows at once, so the per-row
 // arithmetic (the division) is shared by them.
-constexpr uint32_t kSmxYZero = 17u * 4096u;   // y from which e = 0
 constexpr uint32_t kEtabMax = 16383;          // largest dlim with e(d) tabulated in LDS (4 dlim < 2^16)
 constexpr uint32_t kSmxDead = 65536;          // d given to scores past v: e = 0 in both forms
 
@@ -129,13 +128,6 @@ struct SmxRegs {
     uint32_t cm, cs, fp, valid0, period, dlim;
 };
 
-// Least d in [0, 65536] with ((d Cm) >> Cs) >= 17 * 4096 (65536: none below 2^16).
-uint32_t smx_dlim(uint32_t cm, uint32_t cs) {
-    if (cm == 0 || cs > 46) return 65536;                      // d Cm < 2^40 <= 17 * 4096 * 2^Cs
-    const uint64_t thr = (uint64_t)kSmxYZero << cs;
-    const uint64_t d = (thr + cm - 1) / cm;
-    return d < 65536 ? (uint32_t)d : 65536u;
-}
 
 __device__ __forceinline__ uint32_t smx_valid(uint32_t q, uint32_t n, const SmxRegs& r) {
     const uint32_t v = r.valid0 + (r.period ? q % r.period : 0u);
