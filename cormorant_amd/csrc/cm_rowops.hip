@@ -323,6 +323,91 @@ __device__ __forceinline__ void norm_unit_wide(const int (&x)[8], uint32_t u, ui
     }
 }
 
+// One NORM row of the fast path: x[k] = unit lane + 64 k of the row (int32, zero past the
+// row), the staged parameters at lds; the int16 results to rc.  Wavefront-uniform control.
+template <int UPL>
+__device__ __forceinline__ void norm_row(const Job& j, const int (&x)[UPL][8], uint8_t* rc, const uint4* ro_lds,
+                                         bool bcast, const uint8_t* tab, uint32_t lane, uint32_t units, bool ln) {
+    i64 s1 = 0;
+    u64 lo = 0, hi = 0;
+    uint32_t amax = 0;
+#pragma unroll
+    for (int k = 0; k < UPL; k++) {
+#pragma unroll
+        for (int l = 0; l < 8; l++) {
+            const i64 v = x[k][l];
+            s1 += v;
+            const u64 sq = (u64)(v * v);                 // |x| <= 2^31: x^2 <= 2^62
+            lo += sq;
+            hi += lo < sq ? 1 : 0;
+            const uint32_t av = (uint32_t)(v < 0 ? -v : v);
+            amax = av > amax ? av : amax;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        s1 += (i64)shfl64((u64)s1, off);
+        const u64 olo = shfl64(lo, off), ohi = shfl64(hi, off);
+        const u64 nlo = lo + olo;
+        hi = hi + ohi + (nlo < lo ? 1 : 0);
+        lo = nlo;
+        const uint32_t om = (uint32_t)__shfl_xor((int)amax, off, 64);
+        amax = om > amax ? om : amax;
+    }
+    const i128 S1 = s1, S2 = (i128)(((unsigned __int128)hi << 64) | lo);
+    i128 D = ln ? ((i128)j.n * S2 - S1 * S1 + (i128)j.eps) : (S2 + (i128)j.eps);
+    if (D <= 0) D = 1;
+    u64 Rm;
+    int sh;
+    rsqrt_bf(D, Rm, sh, tab);
+    const int shp = sh - 24;                             // >= 7: sh >= 31
+    // A = n x - S1 (LN) or x in 32 bits for the whole row: A Rm < 2^63
+    const u64 abound = ln ? (u64)j.n * amax + (u64)(s1 < 0 ? -s1 : s1) : (u64)amax;
+    const bool a32 = abound < ((u64)1 << 31);
+    bool wide = !a32;
+#pragma unroll
+    for (int k = 0; k < UPL; k++) {
+        const uint32_t u = lane + 64 * k;
+        if (!a32 || u >= units) continue;           // a32 is uniform over the wavefront
+        int r[8];
+#pragma unroll
+        for (int l = 0; l < 8; l++) {
+            const uint4 e = ro_lds[bcast ? 0u : l * units + u];
+            const int32_t G = (int32_t)e.x;
+            const uint32_t sc = e.y;
+            const i64 bs = (i64)(((u64)e.w << 32) | e.z);
+            // A in 32 bits (a32): the low 32 bits of n x - S1 are A itself
+            const int32_t A = ln ? (int32_t)((uint32_t)j.n * (uint32_t)x[k][l] - (uint32_t)s1) : x[k][l];
+            const i64 P1 = ((i64)A * (i64)(uint32_t)Rm) >> shp;
+            wide |= !(P1 < ((i64)1 << 31) && P1 > -((i64)1 << 31) && sc <= 61);
+            const i64 v = rne_shr_fast((i64)(int32_t)P1 * G + bs, sc);
+            r[l] = v > 32767 ? 32767 : (v < -32768 ? -32768 : (int)v);
+        }
+        int4 o;
+        o.x = (int)((uint32_t)(uint16_t)r[0] | ((uint32_t)(uint16_t)r[1] << 16));
+        o.y = (int)((uint32_t)(uint16_t)r[2] | ((uint32_t)(uint16_t)r[3] << 16));
+        o.z = (int)((uint32_t)(uint16_t)r[4] | ((uint32_t)(uint16_t)r[5] << 16));
+        o.w = (int)((uint32_t)(uint16_t)r[6] | ((uint32_t)(uint16_t)r[7] << 16));
+        store_stream(rc + 16u * u, o);
+    }
+    // rows with a value outside the 64-bit bounds: the whole row again in 128 bits, over
+    // the stores above (a branch uniform over the wavefront)
+    if (__any(wide)) {
+        for (int k = 0; k < UPL; k++) {
+            const uint32_t u = lane + 64 * k;
+            if (u >= units) continue;
+            int r[8];
+            norm_unit_wide(x[k], u, units, ln, j.n, s1, Rm, shp, ro_lds, bcast, r);
+            int4 o;
+            o.x = (int)((uint32_t)(uint16_t)r[0] | ((uint32_t)(uint16_t)r[1] << 16));
+            o.y = (int)((uint32_t)(uint16_t)r[2] | ((uint32_t)(uint16_t)r[3] << 16));
+            o.z = (int)((uint32_t)(uint16_t)r[4] | ((uint32_t)(uint16_t)r[5] << 16));
+            o.w = (int)((uint32_t)(uint16_t)r[6] | ((uint32_t)(uint16_t)r[7] << 16));
+            store_stream(rc + 16u * u, o);
+        }
+    }
+}
+
 // NORM: a wavefront per row (rows in turn over the grid), the row held in registers between
 // the sums and the output: UPL units of 8 elements per lane, n <= 512 UPL.
 template <int AK, int UPL>
@@ -354,85 +439,7 @@ __global__ __launch_bounds__(256) void ro_norm_fast_kernel(Job j, const uint8_t*
     stage_norm_params(ro_lds, params, bcast ? 1u : j.n, units, j.bq_sh);
     for (; row < rows; row += stride) {
         const uint32_t i1 = (uint32_t)(row % j.c1), i2 = (uint32_t)(row / j.c1);
-        uint8_t* rc = j.c + (u64)i2 * j.c_s2 + (u64)i1 * j.c_s1;
-        i64 s1 = 0;
-        u64 lo = 0, hi = 0;
-        uint32_t amax = 0;
-#pragma unroll
-        for (int k = 0; k < UPL; k++) {
-#pragma unroll
-            for (int l = 0; l < 8; l++) {
-                const i64 v = x[k][l];
-                s1 += v;
-                const u64 sq = (u64)(v * v);                 // |x| <= 2^31: x^2 <= 2^62
-                lo += sq;
-                hi += lo < sq ? 1 : 0;
-                const uint32_t av = (uint32_t)(v < 0 ? -v : v);
-                amax = av > amax ? av : amax;
-            }
-        }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            s1 += (i64)shfl64((u64)s1, off);
-            const u64 olo = shfl64(lo, off), ohi = shfl64(hi, off);
-            const u64 nlo = lo + olo;
-            hi = hi + ohi + (nlo < lo ? 1 : 0);
-            lo = nlo;
-            const uint32_t om = (uint32_t)__shfl_xor((int)amax, off, 64);
-            amax = om > amax ? om : amax;
-        }
-        const i128 S1 = s1, S2 = (i128)(((unsigned __int128)hi << 64) | lo);
-        i128 D = ln ? ((i128)j.n * S2 - S1 * S1 + (i128)j.eps) : (S2 + (i128)j.eps);
-        if (D <= 0) D = 1;
-        u64 Rm;
-        int sh;
-        rsqrt_bf(D, Rm, sh, tab);
-        const int shp = sh - 24;                             // >= 7: sh >= 31
-        // A = n x - S1 (LN) or x in 32 bits for the whole row: A Rm < 2^63
-        const u64 abound = ln ? (u64)j.n * amax + (u64)(s1 < 0 ? -s1 : s1) : (u64)amax;
-        const bool a32 = abound < ((u64)1 << 31);
-        bool wide = !a32;
-#pragma unroll
-        for (int k = 0; k < UPL; k++) {
-            const uint32_t u = lane + 64 * k;
-            if (!a32 || u >= units) continue;           // a32 is uniform over the wavefront
-            int r[8];
-#pragma unroll
-            for (int l = 0; l < 8; l++) {
-                const uint4 e = ro_lds[bcast ? 0u : l * units + u];
-                const int32_t G = (int32_t)e.x;
-                const uint32_t sc = e.y;
-                const i64 bs = (i64)(((u64)e.w << 32) | e.z);
-                // A in 32 bits (a32): the low 32 bits of n x - S1 are A itself
-                const int32_t A = ln ? (int32_t)((uint32_t)j.n * (uint32_t)x[k][l] - (uint32_t)s1) : x[k][l];
-                const i64 P1 = ((i64)A * (i64)(uint32_t)Rm) >> shp;
-                wide |= !(P1 < ((i64)1 << 31) && P1 > -((i64)1 << 31) && sc <= 61);
-                const i64 v = rne_shr_fast((i64)(int32_t)P1 * G + bs, sc);
-                r[l] = v > 32767 ? 32767 : (v < -32768 ? -32768 : (int)v);
-            }
-            int4 o;
-            o.x = (int)((uint32_t)(uint16_t)r[0] | ((uint32_t)(uint16_t)r[1] << 16));
-            o.y = (int)((uint32_t)(uint16_t)r[2] | ((uint32_t)(uint16_t)r[3] << 16));
-            o.z = (int)((uint32_t)(uint16_t)r[4] | ((uint32_t)(uint16_t)r[5] << 16));
-            o.w = (int)((uint32_t)(uint16_t)r[6] | ((uint32_t)(uint16_t)r[7] << 16));
-            store_stream(rc + 16u * u, o);
-        }
-        // rows with a value outside the 64-bit bounds: the whole row again in 128 bits, over
-        // the stores above (a branch uniform over the wavefront)
-        if (__any(wide)) {
-            for (int k = 0; k < UPL; k++) {
-                const uint32_t u = lane + 64 * k;
-                if (u >= units) continue;
-                int r[8];
-                norm_unit_wide(x[k], u, units, ln, j.n, s1, Rm, shp, ro_lds, bcast, r);
-                int4 o;
-                o.x = (int)((uint32_t)(uint16_t)r[0] | ((uint32_t)(uint16_t)r[1] << 16));
-                o.y = (int)((uint32_t)(uint16_t)r[2] | ((uint32_t)(uint16_t)r[3] << 16));
-                o.z = (int)((uint32_t)(uint16_t)r[4] | ((uint32_t)(uint16_t)r[5] << 16));
-                o.w = (int)((uint32_t)(uint16_t)r[6] | ((uint32_t)(uint16_t)r[7] << 16));
-                store_stream(rc + 16u * u, o);
-            }
-        }
+        norm_row<UPL>(j, x, j.c + (u64)i2 * j.c_s2 + (u64)i1 * j.c_s1, ro_lds, bcast, tab, lane, units, ln);
         if (row + stride < rows) load_row(row + stride);
     }
 }
@@ -445,6 +452,34 @@ __device__ __forceinline__ void addx_unit_wide(const int (&x)[8], const int (&y)
         const i128 s = ((i128)x[l] << q.sa) + ((i128)(ben ? y[l] : 0) << q.sb) + ((i128)q.bq << bq_sh);
         const i128 v = rne_shr(scale ? s * (i128)q.g : s, q.sc);
         r[l] = (int)(ck == 0 ? sat16(v) : sat32(v));
+    }
+}
+
+// One COPY / ADDX unit: 64-bit arithmetic where the shifts keep every term below 2^61, else
+// the 128-bit form (a branch taken by the lanes that need it).
+template <int BK, int CK, bool BEN>
+__device__ __forceinline__ void addx_unit(const int (&x)[8], const int (&y)[8], uint32_t u, uint32_t units,
+                                          const Job& j, const uint4* ro_lds, bool bcast, bool scale, bool relu,
+                                          int (&r)[8]) {
+    bool wide = scale || j.bq_sh > 40;
+#pragma unroll
+    for (int l = 0; l < 8; l++) {
+        const Param q = param_of(ro_lds[bcast ? 0u : l * units + u]);
+        const i64 yv = BEN ? (i64)y[l] : 0;
+        // each term below 2^61 when: x (32 bits) << sa <= 30, y << sb (16 / 32 bits), Bq (22) << bq_sh <= 40
+        wide |= !(q.sa <= 30 && q.sb <= (BK == 0 ? 46 : 30) && q.sc <= 61);
+        i64 v = rne_shr_fast((i64)x[l] * (i64)((u64)1 << (q.sa & 31)) + yv * (i64)((u64)1 << (q.sb & 63)) +
+                                 q.bq * (i64)((u64)1 << (j.bq_sh & 63)), q.sc & 63);
+        v = CK == 0 ? (v > 32767 ? 32767 : (v < -32768 ? -32768 : v))
+                    : (v > 2147483647 ? 2147483647 : (v < -2147483647LL - 1 ? -2147483647LL - 1 : v));
+        r[l] = (int)v;
+    }
+    if (__any(wide)) {
+        if (wide) addx_unit_wide(x, y, BEN, CK, u, units, j.bq_sh, scale, ro_lds, bcast, r);
+    }
+    if (relu) {
+#pragma unroll
+        for (int l = 0; l < 8; l++) r[l] = r[l] < 0 ? 0 : r[l];
     }
 }
 
@@ -472,26 +507,7 @@ __global__ __launch_bounds__(256) void ro_addx_fast_kernel(Job j, const uint8_t*
         }
         if constexpr (BEN) ld_unit<BK>(j.b + (u64)i2 * j.b_s2 + (u64)i1 * j.b_s1, u, y);
         int r[8];
-        bool wide = scale || j.bq_sh > 40;
-#pragma unroll
-        for (int l = 0; l < 8; l++) {
-            const Param q = param_of(ro_lds[bcast ? 0u : l * units + u]);
-            const i64 yv = BEN ? (i64)y[l] : 0;
-            // each term below 2^61 when: x (32 bits) << sa <= 30, y << sb (16 / 32 bits), Bq (22) << bq_sh <= 40
-            wide |= !(q.sa <= 30 && q.sb <= (BK == 0 ? 46 : 30) && q.sc <= 61);
-            i64 v = rne_shr_fast((i64)x[l] * (i64)((u64)1 << (q.sa & 31)) + yv * (i64)((u64)1 << (q.sb & 63)) +
-                                     q.bq * (i64)((u64)1 << (j.bq_sh & 63)), q.sc & 63);
-            v = CK == 0 ? (v > 32767 ? 32767 : (v < -32768 ? -32768 : v))
-                        : (v > 2147483647 ? 2147483647 : (v < -2147483647LL - 1 ? -2147483647LL - 1 : v));
-            r[l] = (int)v;
-        }
-        if (__any(wide)) {
-            if (wide) addx_unit_wide(x, y, BEN, CK, u, units, j.bq_sh, scale, ro_lds, bcast, r);
-        }
-        if (relu) {
-#pragma unroll
-            for (int l = 0; l < 8; l++) r[l] = r[l] < 0 ? 0 : r[l];
-        }
+        addx_unit<BK, CK, BEN>(x, y, u, units, j, ro_lds, bcast, scale, relu, r);
         uint8_t* rc = j.c + (u64)i2 * j.c_s2 + (u64)i1 * j.c_s1;
         if constexpr (CK == 0) {
             int4 o;

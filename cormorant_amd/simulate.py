@@ -508,6 +508,19 @@ class Simulator:
                      (KV * C * HD, C * HD, 1, 0))
         return cache
 
+    def _whole_row_job(self, sn: RowOpsAdapter, a2d: torch.Tensor, b_all, out: torch.Tensor, p: torch.Tensor) -> dict:
+        """The single job of a whole-row adapter as rowops_jobs() takes it."""
+        at, ot = sn.inputs[0], sn.output
+        bt = getattr(sn, "table", None) or (sn.inputs[1] if len(sn.inputs) > 1 else None)
+        j = sn.jobs()[0]
+        rows, width = a2d.shape
+        u8 = lambda t: t.reshape(-1).view(torch.uint8) if t is not None else None   # noqa: E731
+        b2d = b_all.reshape(rows, width).contiguous() if b_all is not None else None
+        return dict(a=u8(a2d.contiguous()), b=u8(b2d), c=u8(out), p=p, op=j.op, n=j.n, c1=rows, c2=1,
+                    a_s1=width * _KB[at.kind], a_s2=0, b_s1=width * _KB[bt.kind] if bt is not None else 0, b_s2=0,
+                    c_s1=width * _KB[ot.kind], c_s2=0, eps=j.eps, aux=j.aux, bq_sh=j.bq_sh, win_lo=0,
+                    win_hi=0xFFFFFFFF)
+
     def _adapter(self, sn: RowOpsAdapter, raw) -> torch.Tensor:
         """A row-ops adapter: its jobs over row views of the tensors (rows of ``n`` = the job
         width; a job covers the columns [col0, col0 + n) of every row)."""
@@ -526,12 +539,7 @@ class Simulator:
             self._params[id(sn)] = params
         if len(jobs) == 1 and jobs[0].col0 == 0 and jobs[0].b_row0 is None and self._rows_whole(sn, width):
             # rows already whole 16-byte multiples: the jobs run on the tensors themselves
-            j = jobs[0]
-            b2d = b_all.reshape(rows, width) if b_all is not None else None
-            units.rowops(u8(a2d.contiguous()), u8(b2d.contiguous() if b2d is not None else None), u8(out), params[0],
-                         j.op, j.n, rows, 1, width * _KB[at.kind], 0,
-                         width * _KB[bt.kind] if bt is not None else 0, 0, width * _KB[ot.kind], 0,
-                         j.eps, j.aux, j.bq_sh, 0, 0xFFFFFFFF)
+            units.rowops_jobs([self._whole_row_job(sn, a2d, b_all, out, params[0])])
             return out.reshape(-1)
         for ji, j in enumerate(jobs):
             a_buf, a_s1, _ = self._rows16(a2d[:, j.col0:j.col0 + j.n], at.kind)

@@ -413,6 +413,34 @@ def rowops(a, b, c, p, op: int, n: int, c1: int, c2: int, a_s1: int, a_s2: int, 
     _lib.check(rc, "cm_rowops")
 
 
+def rowops_jobs(jobs: Sequence[dict]) -> None:
+    """Row-ops jobs in order through cm_rowops_chain, each job a dict of rowops()'s arguments
+    with its own tensors (a / b / c / p: GPU uint8 images or None)."""
+    descs = (_lib.CmRowopsDesc * len(jobs))()
+    for d, j in zip(descs, jobs):
+        ext = rowops_extents(j["op"], j["n"], j["c1"], j["c2"], j["a_s1"], j["a_s2"], j["b_s1"], j["b_s2"],
+                             j["c_s1"], j["c_s2"], j.get("aux", 0), j.get("win_lo", 0), j.get("win_hi", 0xFFFFFFFF))
+        if ext is not None:
+            (a_lo, a_hi), b_end, c_end, p_end = ext
+            for key, lo, hi in (("a", a_lo, a_hi), ("b", 0, b_end), ("c", 0, c_end), ("p", 0, p_end)):
+                if hi <= lo:
+                    continue
+                t = j.get(key)
+                if t is None or not t.is_cuda or t.dtype != torch.uint8 or not t.is_contiguous():
+                    raise ValueError(f"rowops: {key} must be a contiguous GPU uint8 tensor")
+                if lo < 0 or hi > t.numel():
+                    raise ValueError(f"rowops: {key} accesses bytes [{lo}, {hi}) of {t.numel()}")
+        for f in ("op", "n", "c1", "c2", "a_s1", "a_s2", "b_s1", "b_s2", "c_s1", "c_s2", "aux",
+                  "bq_sh", "win_lo", "win_hi"):
+            setattr(d, f, int(j.get(f, 0xFFFFFFFF if f == "win_hi" else 0)))
+        d.eps = int(j.get("eps", 0))
+        for key in ("a", "b", "c", "p"):
+            t = j.get(key)
+            setattr(d, key, t.data_ptr() if t is not None else 0)
+    rc = _lib.lib().cm_rowops_chain(descs, len(jobs), _stream())
+    _lib.check(rc, "cm_rowops_chain")
+
+
 def rowops_chain(seg: torch.Tensor, jobs: Sequence[dict]) -> None:
     """A descriptor chain over one GPU byte segment: each job's a / b / c / p are byte
     offsets into ``seg`` (the layout of the reference's chain fixtures)."""

@@ -561,6 +561,49 @@ def test_pool_random(U, oracle_lib, case):
     assert (got[N * C * oh * ow:] == POISON16).all()
 
 
+@pytest.mark.parametrize("n,rows,ln,bcast,lim,bq_sh", [
+    (768, 37, True, False, 1 << 20, 12),       # BERT's residual add + LayerNorm32
+    (960, 9, False, False, 1 << 20, 0),        # SmolLM2's residual add + RMSNorm
+    (64, 70, True, True, 1 << 30, 40),         # broadcast parameters, values past the 64-bit bounds
+    (4096, 3, True, False, 1 << 24, 20),
+    (256, 5, True, False, 1 << 16, 45),        # bq_sh past 40: the NORM's general kernel
+])
+def test_rowops_addx_norm_jobs(U, oracle_lib, n, rows, ln, bcast, lim, bq_sh):
+    """An ADDX job (int32 + int16 -> int32) and the NORM of its output as one job list
+    (rowops_jobs, cm_rowops_chain) against the oracle running the two jobs in turn: both
+    outputs, and the parameter RAM a later P_KEEP job reads."""
+    from rowops_cases import _params
+    rng = np.random.default_rng(n + rows + bq_sh)
+    a = rng.integers(-lim, lim, n * rows).astype(np.int32).view(np.uint8)
+    b = rng.integers(-32768, 32768, n * rows).astype(np.int16).view(np.uint8)
+    ent = 1 if bcast else n
+    pa = _params(rng, ent, sh=(0, 20), sb=(0, 20), sc=(0, 30))
+    pn = _params(rng, ent, g_lo=-(1 << 20), g_hi=1 << 20, sc=(20, 50))
+    op_a = 2 | (1 << 4) | (1 << 8) | (1 << 12) | ((1 << 13) if bcast else 0)
+    op_n = 5 | (1 << 4) | ((1 << 16) if ln else 0) | ((1 << 13) if bcast else 0)
+    eps = int(rng.integers(0, 1 << 20))
+    h_want = np.full(4 * n * rows, 0xDE, np.uint8)
+    x_want = np.full(2 * n * rows, 0xDE, np.uint8)
+    k_want = np.full(2 * n * rows, 0xDE, np.uint8)
+    oracle_lib.rowops_reset_params()
+    oracle_lib.rowops(a, b, h_want, pa, op_a, n, rows, 1, 4 * n, 0, 2 * n, 0, 4 * n, 0, 0, 0, 0)
+    oracle_lib.rowops(h_want, None, x_want, pn, op_n, n, rows, 1, 4 * n, 0, 0, 0, 2 * n, 0, eps, 0, bq_sh)
+    decoy = _params(rng, ent)              # what a P_KEEP job must not read
+    oracle_lib.rowops(h_want, None, k_want, decoy, op_n | (1 << 14), n, rows, 1, 4 * n, 0, 0, 0, 2 * n, 0, eps, 0,
+                      bq_sh)
+    ad, bd, pad, pnd = dev8(a), dev8(b), dev8(pa), dev8(pn)
+    hd, xd, kd = (dev8(np.full(m, 0xDE, np.uint8)) for m in (4 * n * rows, 2 * n * rows, 2 * n * rows))
+    common = dict(c1=rows, c2=1, a_s2=0, b_s2=0, c_s2=0, aux=0, win_lo=0, win_hi=0xFFFFFFFF)
+    U.rowops_jobs([dict(a=ad, b=bd, c=hd, p=pad, op=op_a, n=n, a_s1=4 * n, b_s1=2 * n, c_s1=4 * n, eps=0,
+                        bq_sh=0, **common),
+                   dict(a=hd, b=None, c=xd, p=pnd, op=op_n, n=n, a_s1=4 * n, b_s1=0, c_s1=2 * n, eps=eps,
+                        bq_sh=bq_sh, **common)])
+    U.rowops(hd, None, kd, dev8(decoy), op_n | (1 << 14), n, rows, 1, 4 * n, 0, 0, 0, 2 * n, 0, eps, 0, bq_sh)
+    np.testing.assert_array_equal(host(hd), h_want)
+    np.testing.assert_array_equal(host(xd), x_want)
+    np.testing.assert_array_equal(host(kd), k_want)
+
+
 @pytest.mark.parametrize("case", RO_CASES, ids=lambda c: c[0])
 def test_rowops_random(U, oracle_lib, case):
     a, b, p, c_len, r = make_job(case)
