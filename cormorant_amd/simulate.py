@@ -541,6 +541,18 @@ class Simulator:
             # rows already whole 16-byte multiples: the jobs run on the tensors themselves
             units.rowops_jobs([self._whole_row_job(sn, a2d, b_all, out, params[0])])
             return out.reshape(-1)
+        j0 = jobs[0]
+        if (len(jobs) == 1 and j0.col0 == 0 and j0.b_row0 is not None and b_all is not None
+                and all((width * _KB[t.kind]) % 16 == 0 and int(t.shape[-1]) == width for t in (at, ot))):
+            # a table job (RoPE) over whole rows: A, C and the table rows in place
+            tab = b_all.reshape(-1, int(bt.shape[-1]))
+            tb = int(bt.shape[-1]) * _KB[bt.kind]
+            n_tab = 1 if j0.b_same else rows
+            if tb % 16 == 0 and j0.b_row0 + n_tab <= tab.shape[0]:
+                units.rowops(u8(a2d.contiguous()), u8(tab[j0.b_row0:j0.b_row0 + n_tab]), u8(out), params[0], j0.op,
+                             j0.n, rows, 1, width * _KB[at.kind], 0, 0 if j0.b_same else tb, 0,
+                             width * _KB[ot.kind], 0, j0.eps, j0.aux, j0.bq_sh, 0, 0xFFFFFFFF)
+                return out.reshape(-1)
         for ji, j in enumerate(jobs):
             a_buf, a_s1, _ = self._rows16(a2d[:, j.col0:j.col0 + j.n], at.kind)
             b_buf, b_s1 = None, 0
