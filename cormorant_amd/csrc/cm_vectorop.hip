@@ -67,10 +67,11 @@ __global__ __launch_bounds__(256) void vectorop_kernel(const int16_t* __restrict
                                                        uint32_t act, uint32_t alpha,
                                                        const uint8_t* __restrict__ act_tab,
                                                        uint32_t act_len) {
-    __shared__ uint8_t tab[kActTabBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t tab[kActTabBytes];
     const bool table = act >= ACT_SILU && act <= ACT_GELU_TANH;
-    if (table) {
-        for (uint32_t i = threadIdx.x; i < act_len; i += blockDim.x) tab[i] = act_tab[i];
+    if (table) {                    // 16-byte loads of the table (act_len <= 4096, a 16-byte aligned image)
+        for (uint32_t i = threadIdx.x; i < (act_len + 15) / 16; i += blockDim.x)
+            reinterpret_cast<int4*>(tab)[i] = reinterpret_cast<const int4*>(act_tab)[i];
         __syncthreads();
     }
     const uint32_t wpr = (size + 7) >> 3;                                  // words per run
@@ -708,6 +709,8 @@ int launch_ew(const int16_t* a, const int16_t* b, int16_t* c, uint32_t size, uin
     if (act >= ACT_SILU && act <= ACT_GELU_TANH) {
         tab = st->act_tab + (act - ACT_SILU) * kActTabBytes;
         len = st->act_len[act - ACT_SILU];
+        // every workgroup stages the table: a few per compute unit, each over many words
+        blocks = std::min<uint64_t>(blocks, (uint64_t)st->cus * 4);
     }
     CM_LAUNCH("vectorop_kernel", vectorop_kernel<OP>, dim3((unsigned)blocks), dim3(threads), 0, s, a, b, c,
                        size, outer, (uint64_t)a_inc, (uint64_t)b_inc, act, alpha, tab, len);
