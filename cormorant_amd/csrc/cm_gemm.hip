@@ -1151,16 +1151,35 @@ __global__ __launch_bounds__(256) void conv_dw3v_kernel(const int16_t* __restric
 // 8 k).  Every B load of the slice is issued before the first product.  With several slices
 // each wavefront writes its int32 partials [slice][ks][n][m] for skinny_reduce_kernel.
 constexpr uint32_t kSkinnyKc = 64;
+constexpr uint32_t kSkinnySegs = 4;
+
+// The products of one skinny launch: up to kSkinnySegs B / C / m over the same A rows (batch 1),
+// or one product over `batch` slices.  Segment s owns column blocks [cb0[s], cb0[s + 1]) of
+// the grid and output pairs [pair0[s], pair0[s + 1]) of the reduce.
+struct SkinnySegs {
+    const int16_t* b[kSkinnySegs];
+    int16_t* c[kSkinnySegs];
+    int32_t* part[kSkinnySegs];
+    uint32_t m[kSkinnySegs], cb0[kSkinnySegs];
+    uint64_t pair0[kSkinnySegs];
+    uint32_t count;
+};
 
 template <int NR, int BL>
 __global__ __launch_bounds__(64) void skinny_wrap_kernel(const int16_t* __restrict__ a, uint64_t a_bs,
-                                                          const int16_t* __restrict__ b, uint64_t b_bs,
-                                                          int16_t* __restrict__ c, uint64_t c_bs,
-                                                          int32_t* __restrict__ part, uint32_t n, uint32_t k,
-                                                          uint32_t m) {
+                                                          SkinnySegs segs, uint64_t b_bs, uint64_t c_bs, uint32_t n,
+                                                          uint32_t k) {
     constexpr uint32_t KP = kSkinnyKc / 2;                                // k pairs per slice
     __shared__ __attribute__((aligned(16))) uint32_t sa[NR][KP];
-    const uint32_t lane = threadIdx.x, cb = blockIdx.x, ks = blockIdx.y, bt = blockIdx.z, nks = gridDim.y;
+    uint32_t si = 0;                                                      // this workgroup's segment
+    for (uint32_t i = 1; i < segs.count; i++)
+        if (blockIdx.x >= segs.cb0[i]) si = i;
+    const int16_t* __restrict__ b = segs.b[si];
+    int16_t* __restrict__ c = segs.c[si];
+    int32_t* __restrict__ part = segs.part[si];
+    const uint32_t m = segs.m[si];
+    const uint32_t lane = threadIdx.x, cb = blockIdx.x - segs.cb0[si], ks = blockIdx.y, bt = blockIdx.z,
+                   nks = gridDim.y;
     const uint32_t k0 = ks * kSkinnyKc, k1 = min(k, k0 + kSkinnyKc);
     const int16_t* ab = a + bt * a_bs;
     const int16_t* bb = b + bt * b_bs;
@@ -1243,13 +1262,16 @@ __global__ __launch_bounds__(64) void skinny_wrap_kernel(const int16_t* __restri
 
 // Sums the int32 partials of the k slices (wrapping) and applies the output rule: a lane per
 // pair of outputs.
-__global__ __launch_bounds__(256) void skinny_reduce_kernel(const int32_t* __restrict__ part, int16_t* __restrict__ c,
-                                                            uint64_t c_bs, uint32_t n, uint32_t m, uint32_t nks,
-                                                            uint32_t batch) {
-    const uint64_t per = (uint64_t)n * m, pairs = per / 2, total = pairs * batch;
+__global__ __launch_bounds__(256) void skinny_reduce_kernel(SkinnySegs segs, uint64_t c_bs, uint32_t n,
+                                                            uint32_t nks, uint32_t batch, uint64_t total) {
     for (uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (uint64_t)gridDim.x * blockDim.x) {
-        const uint64_t bt = e / pairs, i = 2 * (e - bt * pairs);
-        const int32_t* pp = part + bt * nks * per + i;
+        uint32_t si = 0;
+        for (uint32_t j = 1; j < segs.count; j++)
+            if (e >= segs.pair0[j]) si = j;
+        const uint64_t per = (uint64_t)n * segs.m[si], pairs = per / 2, el = e - segs.pair0[si];
+        const uint64_t bt = el / pairs, i = 2 * (el - bt * pairs);
+        int16_t* c = segs.c[si];
+        const int32_t* pp = segs.part[si] + bt * nks * per + i;
         uint32_t s0 = 0, s1 = 0;
         for (uint32_t q = 0; q < nks; q++) {
             const int2 v = *reinterpret_cast<const int2*>(pp + (uint64_t)q * per);
@@ -1409,33 +1431,58 @@ int split_b(const int16_t* b, uint64_t b_slice, uint32_t k, uint32_t m, uint32_t
 }
 
 // The skinny path of cm_matmul (wrap32, n <= 32): slices of kSkinnyKc k.
-int skinny_wrap(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k, uint32_t m, uint32_t batch,
-                int64_t a_bs, int64_t b_bs, int64_t c_bs, uint32_t b_packed, DeviceState* st, hipStream_t s) {
-    const uint32_t cbs = ceil_div(m, 128), nks = ceil_div(k, kSkinnyKc);
+// Skinny products of the same A (n rows, k) into `count` segments, or one product over
+// `batch` slices (count 1); the partials of all segments in one workspace, one reduce launch.
+int skinny_run(const int16_t* a, uint32_t n, uint32_t k, uint32_t batch, int64_t a_bs, int64_t b_bs, int64_t c_bs,
+               uint32_t count, const int16_t* const* b, int16_t* const* c, const uint32_t* m, uint32_t b_packed,
+               DeviceState* st, hipStream_t s) {
+    const uint32_t nks = ceil_div(k, kSkinnyKc);
+    SkinnySegs segs{};
+    segs.count = count;
+    uint32_t cbs = 0;
+    uint64_t pairs = 0;
+    size_t pbytes = 0;
+    for (uint32_t i = 0; i < count; i++) {
+        segs.b[i] = b[i];
+        segs.c[i] = c[i];
+        segs.m[i] = m[i];
+        segs.cb0[i] = cbs;
+        segs.pair0[i] = pairs;
+        cbs += ceil_div(m[i], 128);
+        pairs += (uint64_t)batch * n * m[i] / 2;
+        pbytes += (size_t)batch * nks * n * m[i] * 4;
+    }
     if (nks > 65535 || batch > 65535) return fail(CM_EINVAL, "matmul: skinny grid %u x %u x %u", cbs, nks, batch);
-    int32_t* part = nullptr;
     if (nks > 1) {
         void* ws;
-        int rc = workspace(st, (size_t)batch * nks * n * m * 4, &ws);
+        int rc = workspace(st, pbytes, &ws);
         if (rc) return rc;
-        part = static_cast<int32_t*>(ws);
+        int32_t* p = static_cast<int32_t*>(ws);
+        for (uint32_t i = 0; i < count; i++) {
+            segs.part[i] = p;
+            p += (size_t)batch * nks * n * m[i];
+        }
     }
     const dim3 grid(cbs, nks, batch);
 #define CM_SKINNY(NR, BL)                                                                                         \
-    CM_LAUNCH("skinny_wrap_kernel", (skinny_wrap_kernel<NR, BL>), grid, dim3(64), 0, s, a, (uint64_t)a_bs, b,       \
-              (uint64_t)b_bs, c, (uint64_t)c_bs, part, n, k, m)
+    CM_LAUNCH("skinny_wrap_kernel", (skinny_wrap_kernel<NR, BL>), grid, dim3(64), 0, s, a, (uint64_t)a_bs, segs,   \
+              (uint64_t)b_bs, (uint64_t)c_bs, n, k)
 #define CM_SKINNY_BL(NR) \
     if (b_packed == 2) { CM_SKINNY(NR, 2); } else if (b_packed) { CM_SKINNY(NR, 1); } else { CM_SKINNY(NR, 0); }
     if (n <= 8) { CM_SKINNY_BL(8) } else if (n <= 16) { CM_SKINNY_BL(16) } else { CM_SKINNY_BL(32) }
 #undef CM_SKINNY_BL
 #undef CM_SKINNY
     if (nks > 1) {
-        const uint64_t pairs = (uint64_t)batch * n * m / 2;
         const unsigned blocks = (unsigned)std::min<uint64_t>((pairs + 255) / 256, (uint64_t)st->cus * 8);
-        CM_LAUNCH("skinny_reduce_kernel", skinny_reduce_kernel, dim3(blocks), dim3(256), 0, s, part, c,
-                  (uint64_t)c_bs, n, m, nks, batch);
+        CM_LAUNCH("skinny_reduce_kernel", skinny_reduce_kernel, dim3(blocks), dim3(256), 0, s, segs, (uint64_t)c_bs,
+                  n, nks, batch, pairs);
     }
     return CM_OK;
+}
+
+int skinny_wrap(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k, uint32_t m, uint32_t batch,
+                int64_t a_bs, int64_t b_bs, int64_t c_bs, uint32_t b_packed, DeviceState* st, hipStream_t s) {
+    return skinny_run(a, n, k, batch, a_bs, b_bs, c_bs, 1, &b, &c, &m, b_packed, st, s);
 }
 
 // The wrap-mode split over k for a matmul of this shape: k steps per slice (0: none) and the
@@ -1812,4 +1859,25 @@ extern "C" int cm_matmul_strided(const int16_t* a, const int16_t* b, int16_t* c,
                        (c_bs & 1) == 0 && (c_bs2 & 1) == 0;
     EpiMatmul epi{c, c_bs, n, m, wrap32 ? 1u : 0u, pairs ? 1u : 0u, ldc, c_bs2, inner};
     return run_gemm(A, B, batch, k, epi, s);
+}
+
+extern "C" int cm_matmul_skinny_multi(const int16_t* a, uint32_t n, uint32_t k, uint32_t count,
+                                      const int16_t* const* b, int16_t* const* c, const uint32_t* m,
+                                      uint32_t b_packed, void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    if (count == 0 || count > kSkinnySegs) return fail(CM_EINVAL, "matmul: %u products (1 .. %u)", count, kSkinnySegs);
+    if (n == 0) return CM_OK;
+    if (n > 32 || k == 0 || k > 32768 || (k & 1) || b_packed > 2 || (b_packed == 2 && (k & 7)))
+        return fail(CM_EINVAL, "matmul: skinny products take n <= 32, even k <= 32768 (k %% 8 == 0 transposed)");
+    if (reinterpret_cast<uintptr_t>(a) & 3) return fail(CM_EALIGN, "matmul: a not 4-byte aligned");
+    for (uint32_t i = 0; i < count; i++) {
+        if (m[i] == 0 || (m[i] & 1) || (b_packed == 1 && (m[i] & 31)))
+            return fail(CM_EINVAL, "matmul: product %u: m = %u", i, m[i]);
+        if ((reinterpret_cast<uintptr_t>(b[i]) & (b_packed == 2 ? 15 : 3)) || (reinterpret_cast<uintptr_t>(c[i]) & 3))
+            return fail(CM_EALIGN, "matmul: product %u: b / c not aligned", i);
+    }
+    return skinny_run(a, n, k, 1, 0, 0, 0, count, b, c, m, b_packed, st, as_stream(stream));
 }

@@ -69,7 +69,21 @@ class Simulator:
     def forward_raw(self, raw_inputs: Dict[str, torch.Tensor]) -> Dict[str, torch.Tensor]:
         """The device-resident path: raw input tensors in, raw tensors of every node out."""
         raw: Dict[str, torch.Tensor] = dict(raw_inputs)
-        for sn in self._graph.nodes:
+        nodes = self._graph.nodes
+        i = 0
+        while i < len(nodes):
+            sn = nodes[i]
+            i += 1
+            if self._skinny_single(sn):
+                # the skinny MatMuls that follow on the same A: one launch for up to 4
+                group = [sn]
+                while (i < len(nodes) and len(group) < 4 and self._skinny_single(nodes[i])
+                       and nodes[i].inputs[0].onnx_name == sn.inputs[0].onnx_name):
+                    group.append(nodes[i])
+                    i += 1
+                if len(group) > 1:
+                    self._matmul_group(group, raw)
+                    continue
             if isinstance(sn, MatmulNode):
                 raw[sn.output.onnx_name] = self._matmul(sn, raw)
             elif isinstance(sn, ConvNode):
@@ -199,13 +213,8 @@ class Simulator:
         if bt.data is not None and b_batch == 1 and wrap and n <= 32 and m % 2 == 0 and k % 8 == 0:
             # a decode-sized product: the library's skinny path reads the weight itself, kept
             # as its transposed image [m][k] (each column's k contiguous)
-            img = self._images.get(bt.onnx_name + "#trans")
-            if img is None:
-                wt = np.ascontiguousarray(b.cpu().numpy().reshape(k, m).T)
-                img = torch.from_numpy(wt).to(self.device)
-                self._images[bt.onnx_name + "#trans"] = img
-            units.matmul(a.reshape(-1).contiguous(), img, c, n, k, m, batch=batch, a_bs=n * k if a_batch > 1 else 0,
-                         b_bs=0, c_bs=n * m, b_packed=2, wrap32=True)
+            units.matmul(a.reshape(-1).contiguous(), self._trans_image(bt, b, k, m), c, n, k, m, batch=batch,
+                         a_bs=n * k if a_batch > 1 else 0, b_bs=0, c_bs=n * m, b_packed=2, wrap32=True)
             return c
         if bt.data is not None and b_batch == 1:
             # a shared weight: the packed image (the scheduler's packing), split once
@@ -221,6 +230,43 @@ class Simulator:
                          a_bs=n * k if a_batch > 1 else 0, b_bs=k * m if b_batch > 1 else 0,
                          c_bs=n * m, wrap32=wrap)
         return c
+
+    def _trans_image(self, bt: TensorInfo, b: torch.Tensor, k: int, m: int) -> torch.Tensor:
+        """A weight's transposed image [m][k], built once."""
+        img = self._images.get(bt.onnx_name + "#trans")
+        if img is None:
+            wt = np.ascontiguousarray(b.cpu().numpy().reshape(k, m).T)
+            img = torch.from_numpy(wt).to(self.device)
+            self._images[bt.onnx_name + "#trans"] = img
+        return img
+
+    def _skinny_single(self, sn) -> bool:
+        """A MatMul of one slice the skinny path takes: a constant pow2 weight, at most 32 rows."""
+        if not isinstance(sn, MatmulNode):
+            return False
+        at, bt, ot = sn.inputs[0], sn.inputs[1], sn.output
+        if bt.data is None or len(at.shape) > 2 or len(bt.shape) > 2 or bt.shape[-2] != at.shape[-1]:
+            return False
+        n, k, m = int(at.shape[-2]), int(at.shape[-1]), int(bt.shape[-1])
+        return self._pow2(at, bt, ot) and n <= 32 and m % 2 == 0 and k % 8 == 0
+
+    def _matmul_group(self, group, raw) -> None:
+        """Consecutive skinny MatMuls of the same A (q / k / v, gate / up) in one launch, each
+        output as _matmul would give it."""
+        at = group[0].inputs[0]
+        a = self._get(at, raw).reshape(-1).contiguous()
+        n, k = int(at.shape[-2]), int(at.shape[-1])
+        bs, cs, ms = [], [], []
+        for sn in group:
+            bt, ot = sn.inputs[1], sn.output
+            self._check_exponents(at, bt, ot)
+            m = int(bt.shape[-1])
+            bs.append(self._trans_image(bt, self._get(bt, raw), k, m))
+            cs.append(self._new(ot, n * m))
+            ms.append(m)
+        units.matmul_skinny_multi(a, n, k, bs, cs, ms, b_packed=2)
+        for sn, c in zip(group, cs):
+            raw[sn.output.onnx_name] = c
 
     def _check_exponents(self, at: TensorInfo, bt: TensorInfo, ot: TensorInfo) -> None:
         """Every product of column j must sit at 2^-(f_out[j] + F) (_simulate.py:821-827)."""

@@ -11,6 +11,8 @@ from __future__ import annotations
 
 from typing import Iterable, Optional, Sequence
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -167,6 +169,22 @@ def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, n: int, k: int, m:
                               int(b_packed), int(gemv_kw), int(bool(wrap32)), _stream())
     _lib.check(rc, "cm_matmul")
     return c
+
+
+def matmul_skinny_multi(a: torch.Tensor, n: int, k: int, bs, cs, ms, b_packed: int = 0) -> None:
+    """cm_matmul_skinny_multi: C_i = sat16(wrap32(A . B_i) >> 8) for up to 4 B images of the
+    same A [n][k] (n <= 32) in one launch."""
+    count = len(bs)
+    if not (len(cs) == len(ms) == count):
+        raise ValueError("matmul_skinny_multi: one c and one m per b")
+    _require(a, "a", torch.int16, n * k)
+    for b, c, m in zip(bs, cs, ms):
+        _require(b, "b", torch.int16, matmul_b_extent(k, m, b_packed, 0))
+        _require(c, "c", torch.int16, n * m)
+    P = ctypes.c_void_p * max(count, 1)
+    rc = _lib.lib().cm_matmul_skinny_multi(_ptr(a), n, k, count, P(*[_ptr(b) for b in bs]), P(*[_ptr(c) for c in cs]),
+                                           (ctypes.c_uint32 * max(count, 1))(*ms), int(b_packed), _stream())
+    _lib.check(rc, "cm_matmul_skinny_multi")
 
 
 def matmul_strided(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, n: int, k: int, m: int, batch: int,

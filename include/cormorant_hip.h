@@ -109,6 +109,14 @@ int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32
               uint32_t m, uint32_t batch, int64_t a_bs, int64_t b_bs, int64_t c_bs,
               uint32_t b_packed, uint32_t gemv_kw, uint32_t wrap32, void* stream);
 
+/* Up to 4 int32-wrap products of the same A rows (n <= 32, the decode step's q / k / v or gate /
+ * up projections) in one launch (no counterpart in the reference's units: each product is
+ * cm_matmul(a, b[i], c[i], n, k, m[i], 1, 0, 0, n m[i], b_packed, 0, 1) of MatmulKernel.h:228-242,
+ * the same results): C_i = sat16(wrap32(A . B_i) >> 8).  b_packed 0 / 1 / 2 as cm_matmul; m[i]
+ * even (a multiple of 32 packed), k even (a multiple of 8 and 16-byte aligned B transposed). */
+int cm_matmul_skinny_multi(const int16_t* a, uint32_t n, uint32_t k, uint32_t count, const int16_t* const* b,
+                           int16_t* const* c, const uint32_t* m, uint32_t b_packed, void* stream);
+
 /* cm_matmul over strided operands (no counterpart in the reference's units: the per-head
  * operands that VitAttnPrep / LlmAttnMerge would copy out and back, read and written in place):
  * slice bt of `batch` starts at (bt / inner) x_bs + (bt % inner) x_bs2 elements of each

@@ -234,6 +234,30 @@ def test_matmul_strided_random(U, oracle_lib, case):
     assert (got[c_len:] == POISON16).all()
 
 
+@pytest.mark.parametrize("n,k,ms,bp", [
+    (16, 960, (960, 320, 320), 2),       # SmolLM2's q / k / v
+    (16, 960, (2560, 2560), 2),          # gate / up
+    (3, 64, (130, 64, 2, 66), 2),        # one k slice (no reduce), ragged column blocks
+    (32, 2560, (96, 512), 0),            # row-major B, 40 k slices
+    (9, 200, (64, 32, 160), 1),          # packed B
+])
+def test_matmul_skinny_multi(U, oracle_lib, n, k, ms, bp):
+    """cm_matmul_skinny_multi against the oracle's products one by one (and the outputs'
+    neighbours untouched): full-range operands, the int32 wrap."""
+    rng = np.random.default_rng(n + k + len(ms) + bp)
+    a = rint16(rng, n * k)
+    bl = [rint16(rng, k * m) for m in ms]
+    imgs = [pack_b(x, k, m) if bp == 1 else (np.ascontiguousarray(x.reshape(k, m).T).reshape(-1) if bp == 2 else x)
+            for x, m in zip(bl, ms)]
+    wants = [oracle_lib.matmul(a, x, n, k, m, 1, 0, 0, n * m, 0, 0, True) for x, m in zip(bl, ms)]
+    outs = [poisoned16(n * m + 8) for m in ms]
+    U.matmul_skinny_multi(dev16(a), n, k, [dev16(x) for x in imgs], outs, list(ms), b_packed=bp)
+    for got, want, m in zip(outs, wants, ms):
+        g = host(got)
+        np.testing.assert_array_equal(g[:n * m], want)
+        assert (g[n * m:] == POISON16).all()
+
+
 def _attention_regs():
     from cormorant_amd.graph import softmax_regs
     return [(12102203, 0x0813), softmax_regs(9, 0.125, 15), softmax_regs(12, 0.125, 14), softmax_regs(6, 1.0, 14)]
