@@ -33,6 +33,8 @@ SIGNATURES = {
     "cm_init": (_I32, []),
     "cm_host_act_table": (_I32, [_I32, _P]),
     "cm_host_rowops_table_image": (_I32, [_P]),
+    "cm_act_table_init": (_I32, [_P]),
+    "cm_rowops_tables_init": (_I32, [_P]),
     "cm_vectorop": (_I32, [_P, _P, _P] + [_U32] * 10 + [_P]),
     "cm_matmul": (_I32, [_P, _P, _P, _U32, _U32, _U32, _U32, _I64, _I64, _I64, _U32, _U32, _U32, _P]),
     "cm_conv": (_I32, [_P, _P, _P, _P] + [_U32] * 21 + [_P]),

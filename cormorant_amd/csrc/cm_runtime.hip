@@ -80,11 +80,10 @@ constexpr int kMaxDevices = 64;
 static DeviceState g_states[kMaxDevices];
 static std::mutex g_mu;
 
-static int prepare(DeviceState* st, int dev) {
-    // Activation tables -> the compact form, verified lossless over all 65 536 inputs.
-    static int16_t full[3][65536];
-    build_act_tables_full(full);
-    std::vector<uint8_t> compact(3 * kActTabBytes, 0);
+// Full activation tables (SiLU, GELU, GELU-tanh: f(x) at [x + 32768]) -> the compact form the
+// VectorOP kernel reads, f(x) = max(x, 0) - d[|x|] with d a byte table of lens[a] entries,
+// verified lossless over all 65 536 inputs; CM_EINVAL for a table without that form.
+static int compact_act_tables(const int16_t (*full)[65536], uint8_t* compact, uint32_t* lens) {
     for (int a = 0; a < 3; a++) {
         uint32_t len = 0;
         for (int t = 0; t < 32768; t++) {
@@ -100,8 +99,17 @@ static int prepare(DeviceState* st, int dev) {
             if (want != full[a][x + 32768])
                 return fail(CM_EINVAL, "activation table %d is not max(x,0) - d[|x|] at %d", a, x);
         }
-        st->act_len[a] = len;
+        lens[a] = len;
     }
+    return CM_OK;
+}
+
+static int prepare(DeviceState* st, int dev) {
+    static int16_t full[3][65536];
+    build_act_tables_full(full);
+    std::vector<uint8_t> compact(3 * kActTabBytes, 0);
+    int rc0 = compact_act_tables(full, compact.data(), st->act_len);
+    if (rc0) return rc0;
     int32_t smx[4096];
     build_smx_table(smx);
     std::vector<uint8_t> img(65536);
@@ -280,3 +288,28 @@ int cm_host_rowops_table_image(uint8_t* out65536) {
 }
 
 }  // extern "C"
+
+extern "C" int cm_act_table_init(const int16_t* tables) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    if (tables == nullptr) return fail(CM_EINVAL, "act tables: null");
+    std::vector<uint8_t> compact(3 * kActTabBytes, 0);
+    uint32_t lens[3];
+    rc = compact_act_tables(reinterpret_cast<const int16_t (*)[65536]>(tables), compact.data(), lens);
+    if (rc) return rc;
+    CM_HIP_CHECK(hipMemcpy(st->act_tab, compact.data(), compact.size(), hipMemcpyHostToDevice));
+    for (int a = 0; a < 3; a++) st->act_len[a] = lens[a];
+    return CM_OK;
+}
+
+extern "C" int cm_rowops_tables_init(const void* img64k) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    if (img64k == nullptr) return fail(CM_EINVAL, "row-ops tables: null");
+    CM_HIP_CHECK(hipMemcpy(st->ro_tables, img64k, 65536, hipMemcpyHostToDevice));
+    return CM_OK;
+}

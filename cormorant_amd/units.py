@@ -496,3 +496,18 @@ def host_rowops_table_image():
     out = np.zeros(65536, np.uint8)
     _lib.check(_lib.lib().cm_host_rowops_table_image(out.ctypes.data), "cm_host_rowops_table_image")
     return out
+
+
+def act_table_init(tables) -> None:
+    """cm_act_table_init: the current device's SiLU / GELU / GELU-tanh tables from int16
+    [3][65536] (f(x) at [x + 32768]); ValueError where a table lacks the unit's form."""
+    import numpy as np
+    t = np.ascontiguousarray(np.asarray(tables, np.int16).reshape(3, 65536))
+    _lib.check(_lib.lib().cm_act_table_init(t.ctypes.data), "cm_act_table_init")
+
+
+def rowops_tables_init(img) -> None:
+    """cm_rowops_tables_init: the current device's 64 KiB row-ops table image."""
+    import numpy as np
+    b = np.ascontiguousarray(np.asarray(img, np.uint8).reshape(65536))
+    _lib.check(_lib.lib().cm_rowops_tables_init(b.ctypes.data), "cm_rowops_tables_init")
