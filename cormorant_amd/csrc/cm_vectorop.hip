@@ -601,12 +601,17 @@ int launch_rows(const int16_t* a, int16_t* c, uint32_t n, uint32_t rows, uint32_
     const size_t lds = (size_t)tab_n4 * 16;
     const uint32_t kw = smx_kw((n + 7) >> 3);
     const SmxRowsFn k = rows_kernel<ETAB>(kw);
-    const uint32_t per_wg = kw ? 64 : 16;                              // rows per workgroup pass
-    const uint64_t resident = (uint64_t)st->cus * blocks_per_cu(reinterpret_cast<const void*>(k), 1024, lds);
+    // 16 lanes a row: 64 rows per 1024-thread workgroup pass; fewer rows than that per compute
+    // unit take smaller workgroups (down to 4 rows), so that they spread over the units
+    uint32_t threads = 1024;
+    if (kw && ceil_div(total, 64) < st->cus)
+        threads = std::min<uint32_t>(1024, std::max<uint32_t>(64, (uint32_t)round_up(16 * ceil_div(total, st->cus), 64)));
+    const uint32_t per_wg = kw ? threads / 16 : 16;                   // rows per workgroup pass
+    const uint64_t resident = (uint64_t)st->cus * blocks_per_cu(reinterpret_cast<const void*>(k), threads, lds);
     const unsigned blocks = (unsigned)std::min<uint64_t>(ceil_div(total, per_wg), resident);
     if (kw) {
-        CM_LAUNCH("softmax_rows_kernel", k, dim3(blocks), dim3(1024), lds, s, a, c, n, rows, total, row0, a_inc, c_inc,
-                  a_bs, c_bs, r, tsrc, tab_n4);
+        CM_LAUNCH("softmax_rows_kernel", k, dim3(blocks), dim3(threads), lds, s, a, c, n, rows, total, row0, a_inc,
+                  c_inc, a_bs, c_bs, r, tsrc, tab_n4);
     } else {
         CM_LAUNCH("softmax_long_kernel", k, dim3(blocks), dim3(1024), lds, s, a, c, n, rows, total, row0, a_inc, c_inc,
                   a_bs, c_bs, r, tsrc, tab_n4);
