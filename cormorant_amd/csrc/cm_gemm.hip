@@ -1273,7 +1273,18 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(SkinnySegs segs, uin
         int16_t* c = segs.c[si];
         const int32_t* pp = segs.part[si] + bt * nks * per + i;
         uint32_t s0 = 0, s1 = 0;
-        for (uint32_t q = 0; q < nks; q++) {
+        uint32_t q = 0;
+        for (; q + 8 <= nks; q += 8) {                 // eight slices' loads in flight at once
+            int2 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = *reinterpret_cast<const int2*>(pp + (uint64_t)(q + u) * per);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                s0 += (uint32_t)v[u].x;
+                s1 += (uint32_t)v[u].y;
+            }
+        }
+        for (; q < nks; q++) {
             const int2 v = *reinterpret_cast<const int2*>(pp + (uint64_t)q * per);
             s0 += (uint32_t)v.x;
             s1 += (uint32_t)v.y;
