@@ -54,6 +54,7 @@ struct DeviceState {
     bool pram_valid = false, pram_bcast = false;
     void* ws = nullptr;              // grow-only workspace
     size_t ws_size = 0;
+    std::vector<void*> ws_retired;   // buffers the workspace outgrew (kept: captured graphs may hold them)
     int cus = 0;                     // compute units
     size_t lds_per_cu = 0;           // LDS bytes per compute unit
     size_t lds_per_block = 0;        // LDS bytes one workgroup may hold (dynamic attribute raised to it)
@@ -63,10 +64,10 @@ struct DeviceState {
 
 // The calling thread's current device, prepared (tables built) on first use.
 int state(DeviceState** out);
-// At least `bytes` of workspace on the current device (stream-ordered reuse: every unit
-// call enqueues its work on one stream, so a later call that grows the buffer first waits
-// for the device).
-int workspace(DeviceState* st, size_t bytes, void** out);
+// At least `bytes` of workspace on the current device.  Growth allocates a larger buffer and
+// keeps the old one until the process ends (work already queued, or a captured graph, may
+// still use it); it is refused (CM_EINVAL) while the stream `s` is capturing a graph.
+int workspace(DeviceState* st, size_t bytes, void** out, hipStream_t s);
 
 // Records a HIP event pair around the launches in its scope while timing is enabled
 // (cm_timing_enable); `name` must be a string literal.

@@ -1466,7 +1466,7 @@ int skinny_run(const int16_t* a, uint32_t n, uint32_t k, uint32_t batch, int64_t
     if (nks > 65535 || batch > 65535) return fail(CM_EINVAL, "matmul: skinny grid %u x %u x %u", cbs, nks, batch);
     if (nks > 1) {
         void* ws;
-        int rc = workspace(st, pbytes, &ws);
+        int rc = workspace(st, pbytes, &ws, s);
         if (rc) return rc;
         int32_t* p = static_cast<int32_t*>(ws);
         for (uint32_t i = 0; i < count; i++) {
@@ -1550,7 +1550,7 @@ extern "C" int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_
     size_t pbytes;
     const uint32_t ksteps = matmul_ksteps(A, B, n, m, batch, wrap32, st, &pbytes);
     void* ws;
-    rc = workspace(st, A.bytes() + B.bytes() + pbytes, &ws);
+    rc = workspace(st, A.bytes() + B.bytes() + pbytes, &ws, s);
     if (rc) return rc;
     char* p = static_cast<char*>(ws);
     A.carve(p);
@@ -1604,7 +1604,7 @@ extern "C" int cm_matmul_planes(const int16_t* a, const void* b_planes, int16_t*
     size_t pbytes;
     const uint32_t ksteps = matmul_ksteps(A, B, n, m, batch, wrap32, st, &pbytes);
     void* ws;
-    rc = workspace(st, A.bytes() + pbytes, &ws);
+    rc = workspace(st, A.bytes() + pbytes, &ws, s);
     if (rc) return rc;
     char* p = static_cast<char*>(ws);
     A.carve(p);
@@ -1761,7 +1761,7 @@ extern "C" int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, 
     Planes B = conv_b_planes(g, kp);
     Planes A = make_planes(out_ch, kp, 1, conv_tile(g, B, st));
     void* ws;
-    rc = workspace(st, A.bytes() + B.bytes(), &ws);
+    rc = workspace(st, A.bytes() + B.bytes(), &ws, s);
     if (rc) return rc;
     char* p = static_cast<char*>(ws);
     A.carve(p);
@@ -1825,7 +1825,7 @@ extern "C" int cm_conv_planes(const int16_t* x, const void* w_planes, const int1
     A.carve(q);
     A.tile = conv_tile(g, B, st);
     void* ws;
-    rc = workspace(st, B.bytes(), &ws);
+    rc = workspace(st, B.bytes(), &ws, s);
     if (rc) return rc;
     char* p = static_cast<char*>(ws);
     B.carve(p);
@@ -1852,7 +1852,7 @@ extern "C" int cm_matmul_strided(const int16_t* a, const int16_t* b, int16_t* c,
     const uint32_t kp = (uint32_t)round_up(k, BK);
     Planes A = make_planes(n, kp, batch, gemm_tile_rows(n, m, batch, st->cus)), B = make_planes(m, kp, batch);
     void* ws;
-    rc = workspace(st, A.bytes() + B.bytes(), &ws);
+    rc = workspace(st, A.bytes() + B.bytes(), &ws, s);
     if (rc) return rc;
     char* p = static_cast<char*>(ws);
     A.carve(p);

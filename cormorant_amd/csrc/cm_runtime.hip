@@ -159,20 +159,23 @@ int state(DeviceState** out) {
     return CM_OK;
 }
 
-int workspace(DeviceState* st, size_t bytes, void** out) {
+int workspace(DeviceState* st, size_t bytes, void** out, hipStream_t s) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (bytes > st->ws_size) {
-        if (st->ws) {
-            CM_HIP_CHECK(hipDeviceSynchronize());
-            CM_HIP_CHECK(hipFree(st->ws));
-            st->ws = nullptr;
-            st->ws_size = 0;
-        }
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        CM_HIP_CHECK(hipStreamIsCapturing(s, &cap));
+        if (cap != hipStreamCaptureStatusNone)
+            return fail(CM_EINVAL, "workspace of %zu bytes needed while the stream captures a graph (%zu held): "
+                                   "run the call once before the capture", bytes, st->ws_size);
         size_t sz = round_up(bytes, (size_t)1 << 21);
-        if (hipMalloc(&st->ws, sz) != hipSuccess) {
-            st->ws = nullptr;
+        void* p = nullptr;
+        if (hipMalloc(&p, sz) != hipSuccess) {
+            (void)hipGetLastError();
             return fail(CM_ENOMEM, "workspace of %zu bytes", sz);
         }
+        // the old buffer stays allocated: queued work and captured graphs may still use it
+        if (st->ws) st->ws_retired.push_back(st->ws);
+        st->ws = p;
         st->ws_size = sz;
     }
     *out = st->ws;

@@ -10,7 +10,13 @@
  *   - Counts and strides are the reference unit's register values (elements unless a
  *     register is documented in bytes).
  *   - `stream` is a hipStream_t (NULL = the legacy default stream).  Calls are
- *     asynchronous on that stream; they are thread-safe per stream.
+ *     asynchronous on that stream.  The library keeps per-device state that calls share:
+ *     the unit tables, the row-ops parameter RAM and one grow-only workspace.  Calls that
+ *     overlap on one device -- from two host threads, or queued on two streams whose work
+ *     may run concurrently -- therefore race; order them (one stream, or events).
+ *   - Workspace growth allocates (and keeps every outgrown buffer until the process ends,
+ *     so graphs captured earlier stay valid); a call that would grow it while its stream
+ *     captures a HIP graph fails with CM_EINVAL -- run that call once before the capture.
  *   - Return value: CM_OK (0) or a negative CM_E* status; cm_last_error() describes the
  *     last failure of the calling thread.  Nothing throws across the ABI.
  *
