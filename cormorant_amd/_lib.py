@@ -37,6 +37,7 @@ SIGNATURES = {
     "cm_rowops_tables_init": (_I32, [_P]),
     "cm_vectorop": (_I32, [_P, _P, _P] + [_U32] * 10 + [_P]),
     "cm_matmul": (_I32, [_P, _P, _P, _U32, _U32, _U32, _U32, _I64, _I64, _I64, _U32, _U32, _U32, _P]),
+    "cm_matmul_noalloc": (_I32, [_P, _P, _P, _U32, _U32, _U32, _U32, _I64, _I64, _I64, _U32, _U32, _U32, _P]),
     "cm_conv": (_I32, [_P, _P, _P, _P] + [_U32] * 21 + [_P]),
     "cm_conv_w_planes_bytes": (ctypes.c_size_t, [_U32] * 4),
     "cm_conv_split_w": (_I32, [_P, _P, _U32, _U32, _U32, _U32, _P]),

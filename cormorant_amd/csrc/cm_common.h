@@ -55,6 +55,8 @@ struct DeviceState {
     void* ws = nullptr;              // grow-only workspace
     size_t ws_size = 0;
     std::vector<void*> ws_retired;   // buffers the workspace outgrew (kept: captured graphs may hold them)
+    void* scratch = nullptr;         // this device's copy of the no-allocation scratch (cm_gemm.hip)
+    size_t scratch_bytes = 0;
     int cus = 0;                     // compute units
     size_t lds_per_cu = 0;           // LDS bytes per compute unit
     size_t lds_per_block = 0;        // LDS bytes one workgroup may hold (dynamic attribute raised to it)
@@ -64,10 +66,25 @@ struct DeviceState {
 
 // The calling thread's current device, prepared (tables built) on first use.
 int state(DeviceState** out);
+// The calling thread's current device if cm_init (or any earlier call) has prepared it;
+// CM_EINVAL otherwise.  Allocates nothing.
+int state_ready(DeviceState** out);
 // At least `bytes` of workspace on the current device.  Growth allocates a larger buffer and
 // keeps the old one until the process ends (work already queued, or a captured graph, may
 // still use it); it is refused (CM_EINVAL) while the stream `s` is capturing a graph.
 int workspace(DeviceState* st, size_t bytes, void** out, hipStream_t s);
+
+// A call's workspace: the grow-only buffer above (fixed == nullptr) or a fixed region of
+// `cap` bytes that the caller provides (the no-allocation entry point's scratch).
+struct WsRegion {
+    void* base = nullptr;
+    size_t cap = 0;
+};
+int take_workspace(DeviceState* st, const WsRegion* fixed, size_t bytes, void** out, hipStream_t s);
+
+// Looks up this device's address of the no-allocation scratch (cm_gemm.hip); called once
+// per device by the set-up, with that device current.
+int gemm_scratch_setup(DeviceState* st);
 
 // Records a HIP event pair around the launches in its scope while timing is enabled
 // (cm_timing_enable); `name` must be a string literal.

@@ -1446,7 +1446,7 @@ int split_b(const int16_t* b, uint64_t b_slice, uint32_t k, uint32_t m, uint32_t
 // `batch` slices (count 1); the partials of all segments in one workspace, one reduce launch.
 int skinny_run(const int16_t* a, uint32_t n, uint32_t k, uint32_t batch, int64_t a_bs, int64_t b_bs, int64_t c_bs,
                uint32_t count, const int16_t* const* b, int16_t* const* c, const uint32_t* m, uint32_t b_packed,
-               DeviceState* st, hipStream_t s) {
+               DeviceState* st, hipStream_t s, const WsRegion* fixed = nullptr) {
     const uint32_t nks = ceil_div(k, kSkinnyKc);
     SkinnySegs segs{};
     segs.count = count;
@@ -1466,7 +1466,7 @@ int skinny_run(const int16_t* a, uint32_t n, uint32_t k, uint32_t batch, int64_t
     if (nks > 65535 || batch > 65535) return fail(CM_EINVAL, "matmul: skinny grid %u x %u x %u", cbs, nks, batch);
     if (nks > 1) {
         void* ws;
-        int rc = workspace(st, pbytes, &ws, s);
+        int rc = take_workspace(st, fixed, pbytes, &ws, s);
         if (rc) return rc;
         int32_t* p = static_cast<int32_t*>(ws);
         for (uint32_t i = 0; i < count; i++) {
@@ -1492,8 +1492,9 @@ int skinny_run(const int16_t* a, uint32_t n, uint32_t k, uint32_t batch, int64_t
 }
 
 int skinny_wrap(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k, uint32_t m, uint32_t batch,
-                int64_t a_bs, int64_t b_bs, int64_t c_bs, uint32_t b_packed, DeviceState* st, hipStream_t s) {
-    return skinny_run(a, n, k, batch, a_bs, b_bs, c_bs, 1, &b, &c, &m, b_packed, st, s);
+                int64_t a_bs, int64_t b_bs, int64_t c_bs, uint32_t b_packed, DeviceState* st, hipStream_t s,
+                const WsRegion* fixed) {
+    return skinny_run(a, n, k, batch, a_bs, b_bs, c_bs, 1, &b, &c, &m, b_packed, st, s, fixed);
 }
 
 // The wrap-mode split over k for a matmul of this shape: k steps per slice (0: none) and the
@@ -1528,29 +1529,28 @@ int gemm_out(const Planes& A, const Planes& B, int16_t* c, uint32_t n, uint32_t 
 }  // namespace
 }  // namespace cm
 
-extern "C" int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
-                         uint32_t m, uint32_t batch, int64_t a_bs, int64_t b_bs, int64_t c_bs,
-                         uint32_t b_packed, uint32_t gemv_kw, uint32_t wrap32, void* stream) {
-    using namespace cm;
-    DeviceState* st;
-    int rc = state(&st);
-    if (rc) return rc;
+namespace cm {
+namespace {
+
+// cm_matmul with its workspace from `fixed` (nullptr: the grow-only workspace).
+int matmul_run(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k, uint32_t m, uint32_t batch,
+               int64_t a_bs, int64_t b_bs, int64_t c_bs, uint32_t b_packed, uint32_t gemv_kw, uint32_t wrap32,
+               hipStream_t s, DeviceState* st, const WsRegion* fixed) {
     if (n == 0 || m == 0 || batch == 0) return CM_OK;
-    rc = matmul_check(k, gemv_kw, a_bs, b_bs, c_bs, b_packed);
+    int rc = matmul_check(k, gemv_kw, a_bs, b_bs, c_bs, b_packed);
     if (rc) return rc;
-    hipStream_t s = as_stream(stream);
     if (wrap32 && n <= 32 && gemv_kw == 0 && (m & 1) == 0 && (k & 1) == 0 && (reinterpret_cast<uintptr_t>(a) & 3) == 0 &&
         (reinterpret_cast<uintptr_t>(b) & 3) == 0 && (reinterpret_cast<uintptr_t>(c) & 3) == 0 && (a_bs & 1) == 0 &&
         (b_bs & 1) == 0 && (c_bs & 1) == 0 && (b_packed != 1 || (m & 31) == 0) &&
         (b_packed != 2 || ((k & 7) == 0 && aligned16(b) && (b_bs & 7) == 0)))
-        return skinny_wrap(a, b, c, n, k, m, batch, a_bs, b_bs, c_bs, b_packed, st, s);
+        return skinny_wrap(a, b, c, n, k, m, batch, a_bs, b_bs, c_bs, b_packed, st, s, fixed);
     const uint32_t kp = (uint32_t)round_up(k, BK);
     const uint32_t sa = (batch > 1 && a_bs != 0) ? batch : 1, sb = (batch > 1 && b_bs != 0) ? batch : 1;
     Planes A = make_planes(n, kp, sa, gemm_tile_rows(n, m, batch, st->cus)), B = make_planes(m, kp, sb);
     size_t pbytes;
     const uint32_t ksteps = matmul_ksteps(A, B, n, m, batch, wrap32, st, &pbytes);
     void* ws;
-    rc = workspace(st, A.bytes() + B.bytes() + pbytes, &ws, s);
+    rc = take_workspace(st, fixed, A.bytes() + B.bytes() + pbytes, &ws, s);
     if (rc) return rc;
     char* p = static_cast<char*>(ws);
     A.carve(p);
@@ -1561,6 +1561,51 @@ extern "C" int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_
     rc = split_b(b, b_slice, k, m, b_packed, gemv_kw, B, s);
     if (rc) return rc;
     return gemm_out(A, B, c, n, k, m, batch, c_bs, wrap32, s, reinterpret_cast<int32_t*>(p), ksteps);
+}
+
+// The no-allocation scratch: every call of cm_matmul_noalloc on a device takes its planes, line
+// sums and split-k partials from that device's copy of this array (the code object holds one
+// per device from load to process end).  Host code never passes `scratch` itself: its
+// device address per device comes from hipGetSymbolAddress at set-up (DeviceState::scratch).
+constexpr size_t kScratchBytes = CM_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+}  // namespace
+
+int gemm_scratch_setup(DeviceState* st) {
+    void* ptr = nullptr;
+    CM_HIP_CHECK(hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch)));
+    if (ptr == nullptr || (reinterpret_cast<uintptr_t>(ptr) & 255))
+        return fail(CM_EHIP, "no-allocation scratch: unusable device address %p", ptr);
+    st->scratch = ptr;
+    st->scratch_bytes = kScratchBytes;
+    return CM_OK;
+}
+
+}  // namespace cm
+
+extern "C" int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
+                         uint32_t m, uint32_t batch, int64_t a_bs, int64_t b_bs, int64_t c_bs,
+                         uint32_t b_packed, uint32_t gemv_kw, uint32_t wrap32, void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    return matmul_run(a, b, c, n, k, m, batch, a_bs, b_bs, c_bs, b_packed, gemv_kw, wrap32, as_stream(stream), st,
+                      nullptr);
+}
+
+extern "C" int cm_matmul_noalloc(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
+                                 uint32_t m, uint32_t batch, int64_t a_bs, int64_t b_bs, int64_t c_bs,
+                                 uint32_t b_packed, uint32_t gemv_kw, uint32_t wrap32, void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state_ready(&st);                       // no set-up here: that allocates the unit tables
+    if (rc) return rc;
+    if (st->scratch == nullptr) return fail(CM_EINVAL, "no-allocation scratch not set up on this device");
+    const WsRegion region{st->scratch, st->scratch_bytes};
+    return matmul_run(a, b, c, n, k, m, batch, a_bs, b_bs, c_bs, b_packed, gemv_kw, wrap32, as_stream(stream), st,
+                      &region);
 }
 
 extern "C" size_t cm_matmul_b_planes_bytes(uint32_t k, uint32_t m, uint32_t b_slices) {

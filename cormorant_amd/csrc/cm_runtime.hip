@@ -137,6 +137,8 @@ static int prepare(DeviceState* st, int dev) {
     {
         int rc = prepare_softmax(st);
         if (rc) return rc;
+        rc = gemm_scratch_setup(st);
+        if (rc) return rc;
     }
     st->device = dev;
     st->ready = true;
@@ -155,6 +157,16 @@ int state(DeviceState** out) {
             if (rc) return rc;
         }
     }
+    *out = st;
+    return CM_OK;
+}
+
+int state_ready(DeviceState** out) {
+    int dev = 0;
+    CM_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(CM_EINVAL, "device %d beyond %d", dev, kMaxDevices);
+    DeviceState* st = &g_states[dev];
+    if (!st->ready) return fail(CM_EINVAL, "device %d not initialised: call cm_init on it first", dev);
     *out = st;
     return CM_OK;
 }
@@ -179,6 +191,14 @@ int workspace(DeviceState* st, size_t bytes, void** out, hipStream_t s) {
         st->ws_size = sz;
     }
     *out = st->ws;
+    return CM_OK;
+}
+
+int take_workspace(DeviceState* st, const WsRegion* fixed, size_t bytes, void** out, hipStream_t s) {
+    if (fixed == nullptr) return workspace(st, bytes, out, s);
+    if (bytes > fixed->cap)
+        return fail(CM_EINVAL, "the call needs %zu bytes of scratch; the no-allocation maximum is %zu", bytes, fixed->cap);
+    *out = fixed->base;
     return CM_OK;
 }
 

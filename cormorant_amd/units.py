@@ -171,6 +171,26 @@ def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, n: int, k: int, m:
     return c
 
 
+NOALLOC_MAX_BYTES = 64 << 20       # CM_NOALLOC_MAX_BYTES of include/cormorant_hip.h
+
+
+def matmul_noalloc(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, n: int, k: int, m: int,
+                   batch: int = 1, a_bs: int = 0, b_bs: int = 0, c_bs: Optional[int] = None,
+                   b_packed: int = 0, gemv_kw: int = 0, wrap32: bool = False) -> torch.Tensor:
+    """cm_matmul_noalloc: ``matmul``'s result with no device allocation (the library's fixed
+    scratch; ValueError past its CM_NOALLOC_MAX_BYTES, or before ``init`` on this device)."""
+    if c_bs is None:
+        c_bs = n * m
+    if batch and n and m:
+        _require(a, "a", torch.int16, (batch - 1) * a_bs + n * k)
+        _require(b, "b", torch.int16, (batch - 1) * b_bs + matmul_b_extent(k, m, b_packed, gemv_kw))
+        _require(c, "c", torch.int16, (batch - 1) * c_bs + n * m)
+    rc = _lib.lib().cm_matmul_noalloc(_ptr(a), _ptr(b), _ptr(c), n, k, m, batch, a_bs, b_bs, c_bs,
+                                      int(b_packed), int(gemv_kw), int(bool(wrap32)), _stream())
+    _lib.check(rc, "cm_matmul_noalloc")
+    return c
+
+
 def matmul_skinny_multi(a: torch.Tensor, n: int, k: int, bs, cs, ms, b_packed: int = 0) -> None:
     """cm_matmul_skinny_multi: C_i = sat16(wrap32(A . B_i) >> 8) for up to 4 B images of the
     same A [n][k] (n <= 32) in one launch."""

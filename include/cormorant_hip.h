@@ -26,6 +26,7 @@
 #ifndef CORMORANT_HIP_H
 #define CORMORANT_HIP_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -124,6 +125,19 @@ int cm_softmax(const int16_t* a, int16_t* c, uint32_t size, uint32_t op, uint32_
 int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
               uint32_t m, uint32_t batch, int64_t a_bs, int64_t b_bs, int64_t c_bs,
               uint32_t b_packed, uint32_t gemv_kw, uint32_t wrap32, void* stream);
+
+/* cm_matmul without any allocation (no counterpart in the reference: for callers that cannot
+ * allocate device memory, e.g. code under HIP graph capture or a serving loop that forbids
+ * it).  Same arguments and results as cm_matmul; the operand planes, line sums and split-k
+ * partials live in a device array of CM_NOALLOC_MAX_BYTES that the library's code object
+ * holds on each device, and a call that needs more returns CM_EINVAL.  cm_init must have run
+ * on the current device (CM_EINVAL otherwise: set-up allocates the unit tables).  Every call
+ * on a device shares that device's array, so calls that overlap on one device race; no byte
+ * of it needs to start at zero (each call writes what it reads). */
+#define CM_NOALLOC_MAX_BYTES ((size_t)64 << 20)
+int cm_matmul_noalloc(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
+                      uint32_t m, uint32_t batch, int64_t a_bs, int64_t b_bs, int64_t c_bs,
+                      uint32_t b_packed, uint32_t gemv_kw, uint32_t wrap32, void* stream);
 
 /* Up to 4 int32-wrap products of the same A rows (n <= 32, the decode step's q / k / v or gate /
  * up projections) in one launch (no counterpart in the reference's units: each product is
