@@ -38,7 +38,8 @@ def _channels(t: TensorInfo, F: int, n: int) -> np.ndarray:
 
 def _encode(data: np.ndarray, f: np.ndarray, F: int):
     """raw / 2^F (float32) of data rounded half to even at 2^-f and saturated; the count."""
-    r = np.round(np.asarray(data, np.float64) * np.power(2.0, np.asarray(f, np.float64)))
+    # scaling by 2^f is exact (ldexp), so this is round(data * 2^f) without the power array
+    r = np.rint(np.ldexp(np.asarray(data, np.float64), np.asarray(f, np.int64)))
     n_sat = int(((r < I16_LO) | (r > I16_HI)).sum())
     return (np.clip(r, I16_LO, I16_HI) / float(1 << F)).astype(np.float32), n_sat
 

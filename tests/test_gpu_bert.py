@@ -20,6 +20,9 @@ pytestmark = pytest.mark.gpu
     (models.BertShape(layers=1, batch=1, seq=256, d=128, heads=2, ff=256, vocab=1000), 4, True),
     (models.BertShape(layers=1, batch=1, seq=384, d=768, heads=12, ff=3072, vocab=30522), 2, True),
     (models.BertShape(layers=1, batch=1, seq=384, d=768, heads=12, ff=3072, vocab=30522), 2, False),
+    # the configuration's own batch: 3072 rows through every linear (FFN2's split over k and its
+    # reduce), 96 (sequence, head) pairs of the fused attention; every sequence compared
+    (models.BertShape(layers=1, batch=8), 5, True),
 ])
 def test_encoder_every_tensor(shape, seed, fused):
     g, inputs, _ = models.bert_encoder(shape, seed=seed, fused_attention=fused)

@@ -16,6 +16,9 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize("shape,seed", [
     (models.LlamaShape(layers=2, batch=3, d=128, heads=4, kv=2, hd=32, ff=256, vocab=512, ctx=64), 1),
     (models.LlamaShape(layers=1, batch=2, vocab=4096, ctx=256), 2),
+    # the configuration's own step: 16 sequences (the 16-row skinny products and the grouped
+    # q / k / v and gate / up launches), 1024-row caches, the 49152-column tied head
+    (models.LlamaShape(layers=1, batch=16), 5),
 ])
 def test_decode_step_every_tensor(shape, seed):
     g, inputs, _ = models.smollm2_decode(shape, seed=seed)

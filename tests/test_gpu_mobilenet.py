@@ -12,7 +12,9 @@ from oracle import graph_sim as oracle_graph
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("batch,res,seed", [(1, 32, 0), (2, 64, 1), (1, 224, 2)])
+# (32, 224): the configuration's own batch -- the 1x1 convolutions fold 32 images into their
+# GEMM columns (up to 401 408 lines), every image compared
+@pytest.mark.parametrize("batch,res,seed", [(1, 32, 0), (2, 64, 1), (1, 224, 2), (32, 224, 5)])
 def test_mobilenet_every_tensor(batch, res, seed):
     g, inputs, _ = models.mobilenet_v2(batch=batch, res=res, seed=seed)
     got = Simulator(g)._forward_pass(inputs)
