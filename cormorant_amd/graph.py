@@ -37,6 +37,7 @@ class TensorInfo:
     raw: bool = False                 # ``data`` holds raw lanes of ``kind`` (a table), not values
     chexp: Optional[np.ndarray] = None        # per-channel exponents of axis 1 (NCHW), tensor.py
     group_layout: Optional[tuple] = None      # (KV, HD): a [C][KV * HD] cache stored group-major
+    state: bool = False               # a persistent state (a KV cache): updated in place, kept across passes
 
     @property
     def numel(self) -> int:
@@ -329,6 +330,17 @@ class Graph:
     nodes: List[object] = field(default_factory=list)
     input_tensors: List[TensorInfo] = field(default_factory=list)
     output_tensors: List[TensorInfo] = field(default_factory=list)
+
+    @property
+    def state_tensors(self) -> List[TensorInfo]:
+        """The persistent states the nodes read and update in place (numeric.py states; the
+        reference's Graph.state_tensors), in first-use order."""
+        seen, out = set(), []
+        for t in list(self.input_tensors) + [u for n in self.nodes for u in list(n.inputs) + [n.output]]:
+            if t is not None and t.state and t.onnx_name not in seen:
+                seen.add(t.onnx_name)
+                out.append(t)
+        return out
 
     @property
     def weight_tensors(self) -> List[TensorInfo]:

@@ -20,7 +20,7 @@ from .graph import (AttentionNode, AttnContractNode, ConvNode, Graph, KvWriteNod
                     PermuteNode, PoolNode, ReshapeNode, RowOpsNode, ScheduledNode, SchedulerError, SoftmaxVopNode,
                     TensorInfo, attn_keys)
 from .packing import conv_bias_image, conv_weight_image, pack_matmul_b
-from .rowops_nodes import RoJob, RowOpsAdapter
+from .rowops_nodes import RoCallNode, RoJob, RowOpsAdapter
 
 _TORCH = {"i16": torch.int16, "i32": torch.int32, "f32": torch.float32}
 _NP = {"i16": np.int16, "i32": np.int32, "f32": np.float32}
@@ -42,6 +42,7 @@ class Simulator:
         self._images: Dict[str, torch.Tensor] = {}       # packed weight images
         self._infos: Dict[str, TensorInfo] = {}
         self._params: Dict[int, list] = {}                # row-ops parameter blocks on the device
+        self._staging: Dict[tuple, torch.Tensor] = {}     # row-ops nodes' staging buffers
         for t in graph.input_tensors + graph.output_tensors:
             self._infos[t.onnx_name] = t
         for sn in graph.nodes:
@@ -56,14 +57,40 @@ class Simulator:
         arrays = self._forward_pass(inputs, keep=[t.onnx_name for t in self._graph.output_tensors])
         return {t.onnx_name: arrays[t.onnx_name] for t in self._graph.output_tensors}
 
+    def initial_states(self) -> Dict[str, np.ndarray]:
+        """Fresh float64 values of the graph's persistent states: a state's ``data``, else 0
+        (the reference's initial_states)."""
+        out = {}
+        for t in self._graph.state_tensors:
+            v = np.zeros(t.shape) if t.data is None else np.asarray(t.data, np.float64).reshape(t.shape)
+            out[t.onnx_name] = v.copy()
+        return out
+
     def _forward_pass(self, input_arrays: Dict[str, np.ndarray], errors_out=None, states=None,
                       keep: Optional[Iterable[str]] = None) -> Dict[str, np.ndarray]:
-        """Run every node; returns float64 values of every tensor visited, or only ``keep``
-        (the reference's lean mode, _simulate.py:541-592).  ``errors_out`` / ``states`` are
-        accepted for the reference's signature; residual statistics are not computed."""
-        raw = self.forward_raw({name: self._to_device(self._tensor(name), v)
-                                for name, v in input_arrays.items()})
-        wanted = set(raw) if keep is None else set(keep)
+        """Run every node; returns float64 values of every tensor visited, or only ``keep`` and
+        the states (the reference's lean mode, _simulate.py:541-592).  ``states`` ({name:
+        float64 array}, default fresh initial_states()) are the persistent state tensors: the
+        nodes update them in place on the device and the caller's arrays receive the new values,
+        so a caller can run several passes over the same states (_simulate.py:573-577,
+        609-611).  Inputs may also carry a state's value (it then replaces the array's).
+        ``errors_out`` (the residual statistics of _simulate.py:77-118) is not computed on the
+        GPU: passing one raises NotImplementedError."""
+        if errors_out is not None:
+            raise NotImplementedError("residual statistics (errors_out) are not computed by the GPU simulator")
+        st_names = [t.onnx_name for t in self._graph.state_tensors]
+        if states is None:
+            states = self.initial_states()
+        missing = [nm for nm in st_names if nm not in states and nm not in input_arrays]
+        if missing:
+            raise KeyError(f"states {missing} have no value")
+        feeds = {nm: self._to_device(self._tensor(nm), states[nm]) for nm in st_names if nm not in input_arrays}
+        feeds.update({name: self._to_device(self._tensor(name), v) for name, v in input_arrays.items()})
+        raw = self.forward_raw(feeds)
+        for nm in st_names:                      # the states as the pass left them, in place
+            if nm in states:
+                states[nm][...] = self._to_values(self._tensor(nm), feeds[nm]).reshape(np.shape(states[nm]))
+        wanted = set(raw) if keep is None else set(keep) | set(st_names)
         return {name: self._to_values(self._tensor(name), t) for name, t in raw.items() if name in wanted}
 
     def forward_raw(self, raw_inputs: Dict[str, torch.Tensor]) -> Dict[str, torch.Tensor]:
@@ -98,6 +125,8 @@ class Simulator:
                 raw[sn.output.onnx_name] = self._rowops(sn, raw)
             elif isinstance(sn, RowOpsAdapter):
                 raw[sn.output.onnx_name] = self._adapter(sn, raw)
+            elif isinstance(sn, RoCallNode):
+                raw[sn.output.onnx_name] = self._ro_calls(sn, raw)
             elif isinstance(sn, LlmAttnConvNode):
                 raw[sn.output.onnx_name] = self._attn_conv(sn, raw)
             elif isinstance(sn, PermuteNode):
@@ -553,6 +582,42 @@ class Simulator:
         units.copy16(x, cache.reshape(-1)[sn.pos * HD:], (B, KV, HD, 1), (KV * HD, HD, 1, 0),
                      (KV * C * HD, C * HD, 1, 0))
         return cache
+
+    def _ro_calls(self, sn: RoCallNode, raw) -> torch.Tensor:
+        """A node's unit calls over named buffers: the graph's tensors (the states written in
+        place), the node's staging buffers (zero at creation, kept across calls) and tables."""
+        host = {t.onnx_name: int(np.asarray(self._get(t, raw)).reshape(-1)[0]) for t in sn.host_inputs()}
+        out = self._new(sn.output)
+        bufs = {sn.output.onnx_name: out.view(torch.uint8)}
+        for t in sn.inputs:
+            if t is not None and t.kind != "host":
+                bufs[t.onnx_name] = self._get(t, raw).reshape(-1).view(torch.uint8)
+        key = id(sn)
+        for k, nbytes in sn.staging().items():
+            b = self._staging.get((key, k))
+            if b is None:
+                b = torch.zeros(nbytes + 16, dtype=torch.uint8, device=self.device)
+                self._staging[(key, k)] = b
+            bufs["node:" + k] = b
+        for k, lanes in sn.tables().items():
+            b = self._images.get(f"{key}:{k}")
+            if b is None:
+                b = torch.from_numpy(np.ascontiguousarray(lanes).reshape(-1).view(np.uint8).copy()).to(self.device)
+                self._images[f"{key}:{k}"] = b
+            bufs["node:" + k] = b
+        params = self._params.setdefault(key, {})
+        for j in sn.calls(host):
+            p = None
+            if j.p is not None:
+                pk = np.asarray(j.p, np.uint8).tobytes()
+                p = params.get(pk)
+                if p is None:
+                    p = torch.from_numpy(np.frombuffer(pk, np.uint8).copy()).to(self.device)
+                    params[pk] = p
+            units.rowops(bufs[j.a] if j.a else None, bufs[j.b] if j.b else None, bufs[j.c], p, j.op, j.n, j.rows,
+                         j.blocks, j.a_s1, j.a_s2, j.b_s1, j.b_s2, j.c_s1, j.c_s2, j.eps, j.aux, j.bq_sh, j.win_lo,
+                         j.win_hi, a_off=j.a_off, b_off=j.b_off, c_off=j.c_off)
+        return out
 
     def _whole_row_job(self, sn: RowOpsAdapter, a2d: torch.Tensor, b_all, out: torch.Tensor, p: torch.Tensor) -> dict:
         """The single job of a whole-row adapter as rowops_jobs() takes it."""

@@ -11,6 +11,7 @@ from cormorant_amd import graph as G
 from cormorant_amd.dtype import AP_FIXED_16_8 as DT
 from cormorant_amd.rowops_nodes import RowOpsAdapter
 from oracle import cm
+from oracle.attn_prep import attn_prep, transpose
 
 F = DT.frac_bits
 _NP = {"i16": np.int16, "i32": np.int32, "f32": np.float32}
@@ -144,8 +145,21 @@ def run_adapter(node, raw_of):
     return out
 
 
-def forward(graph, inputs):
+def _chan(t, n):
+    """Per-channel exponents of the last axis, n of them."""
+    return np.broadcast_to(np.asarray(F if t.exp is None else t.exp, np.int64).reshape(-1), (n,)).copy()
+
+
+def forward(graph, inputs, states=None):
+    """Every tensor's float64 values.  ``states`` ({name: float64 array}) are the persistent
+    states, updated in place (_simulate.py:573-577); default: zeros, or copies of the inputs
+    of those names."""
     vals = {k: np.array(v, np.float64) for k, v in inputs.items()}      # copies: states change in place
+    for t in getattr(graph, "state_tensors", []):
+        if states is not None and t.onnx_name in states:
+            vals[t.onnx_name] = states[t.onnx_name]
+        elif t.onnx_name not in vals:
+            vals[t.onnx_name] = np.zeros(t.shape)
     get = lambda t: vals[t.onnx_name] if t.onnx_name in vals else _weight(t)
     for sn in graph.nodes:
         out = sn.output
@@ -200,6 +214,22 @@ def forward(graph, inputs):
                     o[b, :, h * hd:(h + 1) * hd] = _wrap_floor(p_.astype(np.float64) @ v)
             fo = float(F if out.exp is None else out.exp)
             vals[out.onnx_name] = (o.astype(np.float64) / 2.0 ** fo).reshape(out.shape)
+        elif type(sn).__name__ == "TransposeRoNode":
+            xt = sn.inputs[0]
+            vals[out.onnx_name] = transpose(get(xt).reshape(xt.shape), sn.perm).reshape(out.shape)
+        elif type(sn).__name__ == "AttnPrepRoNode":
+            q0t, k0t, vt, pt = sn.inputs[:4]
+            ckt, cvt = sn.inputs[-2], sn.inputs[-1]
+            H, KV, HD = sn.heads, sn.kv_heads, sn.head_dim
+            T = q0t.numel // (H * HD)
+            pos = int(np.asarray(get(pt)).reshape(-1)[0])
+            n = int(np.asarray(get(sn.inputs[4])).reshape(-1)[0]) if len(sn.inputs) == 7 else T
+            ck = vals[ckt.onnx_name].reshape(ckt.shape)                # the states, in place
+            cv = vals[cvt.onnx_name].reshape(cvt.shape)
+            vals[out.onnx_name] = attn_prep(get(q0t), get(k0t), get(vt), pos, n, ck, cv, _chan(q0t, H * HD),
+                                            _chan(k0t, KV * HD), _chan(vt, KV * HD), _chan(ckt, KV * HD),
+                                            _chan(cvt, KV * HD), sn.fq, sn.cos, sn.sin, H, KV, HD,
+                                            sn.key_quantum).reshape(out.shape)
         elif isinstance(sn, G.KvWriteNode):
             xt, ct = sn.inputs[0], sn.inputs[1]
             B, KV, C, HD = (int(v) for v in ct.shape)
