@@ -69,6 +69,74 @@ class MatmulNode:
 
 
 @dataclass
+class MatmulConvNode:
+    """One MatMul C [.., n, m] = A [.., n, k] . B [.., k, m] run on the conv unit with the operands'
+    roles swapped (nodes.py:1627-1786, matmul_lowering.py): a 1 x kw conv of stride (1, kw), no
+    pad, out_ch n, in_ch k / kw, output out_h x out_w = m, weight = A (row-major [n][k] is the
+    packed tile-major weight when k % (16 kw) == 0), x = B in conv_lowered_b_image's layout (kw
+    1: B itself; kw > 1: a constant B re-laid once), y = C row-major.  The result is
+    MatmulNode's bit for bit (the simulator treats both alike, _simulate.py:620-633).
+
+    Batch (matmul_lowering._batch_mode, :123-143): A shared and B batched -> the conv's batch;
+    B shared and A batched -> the batch folded into the rows (out_ch = batch n); both batched ->
+    one call per item."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    kw: int = 1
+    out_w: int = 0               # 0: m (one output row)
+
+    def __post_init__(self):
+        a, b = self.inputs
+        n, k = int(a.shape[-2]), int(a.shape[-1])
+        m = int(b.shape[-1])
+        what = f"MatMul-on-conv '{self.output.onnx_name}'"
+        if int(b.shape[-2]) != k:
+            raise SchedulerError(f"{what}: A [.., {n}, {k}] x B {list(b.shape)}")
+        ab = int(np.prod(a.shape[:-2])) if len(a.shape) > 2 else 1
+        bb = int(np.prod(b.shape[:-2])) if len(b.shape) > 2 else 1
+        batch = max(ab, bb)
+        if ab not in (1, batch) or bb not in (1, batch):
+            raise SchedulerError(f"{what}: batch dimensions do not broadcast")
+        if n < 2 or k % 16 or m % 8:
+            raise SchedulerError(f"{what}: needs n >= 2, k % 16 == 0 and m % 8 == 0 (n {n}, k {k}, m {m})")
+        kw = int(self.kw)
+        if not 1 <= kw <= 7 or k % (16 * kw):
+            raise SchedulerError(f"{what}: kw {kw} (1 .. 7, k a multiple of 16 kw)")
+        if kw > 1 and b.data is None:
+            raise SchedulerError(f"{what}: kw > 1 re-lays a constant B only")
+        self.out_w = int(self.out_w) or m
+        if m % self.out_w:
+            raise SchedulerError(f"{what}: out_w {self.out_w} does not divide m {m}")
+        self.n, self.k, self.m, self.batch = n, k, m, batch
+        self.out_h = m // self.out_w
+        self.a_batch_stride = n * k if ab > 1 else 0
+        self.b_batch_stride = k * m if bb > 1 else 0
+        self.c_batch_stride = n * m
+        if batch == 1:
+            self.conv_n, self.conv_batch, self.calls = n, 1, 1
+        elif ab == 1:                              # shared weights: the conv's batch
+            self.conv_n, self.conv_batch, self.calls = n, batch, 1
+        elif bb == 1:                              # the batch folds into the rows
+            self.conv_n, self.conv_batch, self.calls = batch * n, 1, 1
+        else:                                      # one call per item
+            self.conv_n, self.conv_batch, self.calls = n, 1, batch
+        if self.output.numel != batch * n * m:
+            raise SchedulerError(f"{what}: output numel")
+
+    @property
+    def in_ch(self) -> int:
+        return self.k // self.kw
+
+    @property
+    def in_h(self) -> int:
+        return self.out_h
+
+    @property
+    def in_w(self) -> int:
+        return self.kw * self.out_w
+
+
+@dataclass
 class ConvNode:
     """NCHW Conv (nodes.py:1154): inputs x, w [M][C or 1][kh][kw], optional bias [M]."""
     inputs: List[TensorInfo]
@@ -357,7 +425,7 @@ def conv_out(size: int, k: int, stride: int, pad_lo: int, pad_hi: int, dil: int 
     return (size + pad_lo + pad_hi - dil * (k - 1) - 1) // stride + 1
 
 
-__all__ = ["SchedulerError", "TensorInfo", "HeadView", "ScheduledNode", "MatmulNode", "ConvNode", "PoolNode",
+__all__ = ["SchedulerError", "TensorInfo", "HeadView", "ScheduledNode", "MatmulNode", "MatmulConvNode", "ConvNode", "PoolNode",
            "ReshapeNode", "SoftmaxVopNode", "RowOpsNode", "LlmAttnConvNode", "KvWriteNode", "AttentionNode", "attn_keys",
            "KEY_QUANTUM",
            "Graph", "conv_out", "OP_ADD", "OP_SUB",

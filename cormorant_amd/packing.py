@@ -6,7 +6,8 @@ does when it emits a graph):
 * conv weights -- ``[M][ceil(C/16)][kh][kw][lanes]`` with 16-lane input-channel tiles, the
   last one 8 lanes when at most 8 channels remain, unused lanes zero; depthwise
   ``[M][roundup(kh*kw, 8)]``; bias ``[roundup(M, 8)]`` (ConvKernel.h:136-159;
-  nodes.py:1097-1150).
+  nodes.py:1097-1150);
+* a MatMul lowered onto the conv unit -- B as the conv's x image (nodes.py:1592-1624).
 """
 from __future__ import annotations
 
@@ -53,3 +54,28 @@ def conv_bias_image(bias: np.ndarray) -> np.ndarray:
     out = np.zeros((len(bias) + 7) & ~7, np.int16)
     out[:len(bias)] = bias
     return out
+
+
+CONV_TILE_IC = 16      # input channels per packed weight tile (ConvKernel.h)
+
+
+def conv_lowered_k_index(c, j, kw: int):
+    """K index of input channel c at kernel column j of a MatMul lowered onto the conv unit (1 x kw
+    kernel, in_ch = K / kw): A's row read as the packed weight [N][K/(16 kw)][1][kw][16] puts
+    channel c of column j at (c / 16) 16 kw + 16 j + c % 16 (nodes.py:1592-1599)."""
+    t = CONV_TILE_IC
+    return (c // t) * t * kw + j * t + c % t
+
+
+def conv_lowered_b_image(b: np.ndarray, k: int, m: int, kw: int) -> np.ndarray:
+    """The conv x image of a lowered MatMul's B [..., k, m] (one image per slice, concatenated):
+    x[s][c][kw p + j] = B[s][conv_lowered_k_index(c, j)][p] for c < k / kw, so that a 1 x kw
+    conv of stride (1, kw) over in_h x kw out_w reads B's column p at output position p; kw = 1
+    is B itself (nodes.py:1601-1624)."""
+    b3 = np.asarray(b).reshape(-1, k, m)
+    if kw == 1:
+        return np.ascontiguousarray(b3).reshape(-1)
+    c = np.arange(k // kw)[:, None]
+    j = np.arange(kw)[None, :]
+    img = b3[:, conv_lowered_k_index(c, j, kw), :]           # [s][in_ch][kw][m]
+    return np.ascontiguousarray(img.transpose(0, 1, 3, 2)).reshape(-1)

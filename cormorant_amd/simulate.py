@@ -16,10 +16,10 @@ import torch
 
 from . import units
 from .dtype import AP_FIXED_16_8, ApFixed16
-from .graph import (AttentionNode, AttnContractNode, ConvNode, Graph, KvWriteNode, LlmAttnConvNode, MatmulNode,
-                    PermuteNode, PoolNode, ReshapeNode, RowOpsNode, ScheduledNode, SchedulerError, SoftmaxVopNode,
+from .graph import (AttentionNode, AttnContractNode, ConvNode, Graph, KvWriteNode, LlmAttnConvNode, MatmulConvNode,
+                    MatmulNode, PermuteNode, PoolNode, ReshapeNode, RowOpsNode, ScheduledNode, SchedulerError, SoftmaxVopNode,
                     TensorInfo, attn_keys)
-from .packing import conv_bias_image, conv_weight_image, pack_matmul_b
+from .packing import conv_bias_image, conv_lowered_b_image, conv_weight_image, pack_matmul_b
 from .rowops_nodes import RoCallNode, RoJob, RowOpsAdapter
 
 _TORCH = {"i16": torch.int16, "i32": torch.int32, "f32": torch.float32}
@@ -113,6 +113,8 @@ class Simulator:
                     continue
             if isinstance(sn, MatmulNode):
                 raw[sn.output.onnx_name] = self._matmul(sn, raw)
+            elif isinstance(sn, MatmulConvNode):
+                raw[sn.output.onnx_name] = self._matmul_conv(sn, raw)
             elif isinstance(sn, ConvNode):
                 raw[sn.output.onnx_name] = self._conv(sn, raw)
             elif isinstance(sn, ReshapeNode):
@@ -258,6 +260,31 @@ class Simulator:
             units.matmul(a.reshape(-1).contiguous(), b.reshape(-1).contiguous(), c, n, k, m, batch=batch,
                          a_bs=n * k if a_batch > 1 else 0, b_bs=k * m if b_batch > 1 else 0,
                          c_bs=n * m, wrap32=wrap)
+        return c
+
+    def _matmul_conv(self, sn: MatmulConvNode, raw) -> torch.Tensor:
+        """A MatMul on the conv unit (nodes.py:1712-1756): weight = A's rows, x = B's conv image,
+        one call, or one per batch item when both operands are batched."""
+        at, bt, ot = sn.inputs[0], sn.inputs[1], sn.output
+        wrap = self._pow2(at, bt, ot)
+        if wrap:
+            self._check_exponents(at, bt, ot)
+        a = self._get(at, raw).reshape(-1).contiguous()
+        b = self._get(bt, raw).reshape(-1)
+        if sn.kw > 1:                              # a constant B re-laid once
+            key = f"{bt.onnx_name}#conv_kw{sn.kw}"
+            img = self._images.get(key)
+            if img is None:
+                img = torch.from_numpy(conv_lowered_b_image(b.cpu().numpy(), sn.k, sn.m, sn.kw)).to(self.device)
+                self._images[key] = img
+        else:
+            img = b.contiguous()
+        c = self._new(ot)
+        per = 1 if sn.calls > 1 else 0
+        for i in range(sn.calls):
+            units.conv(img[i * per * sn.b_batch_stride:], a[i * per * sn.a_batch_stride:], None,
+                       c[i * per * sn.c_batch_stride:], sn.conv_batch, sn.in_ch, sn.in_h, sn.in_w, sn.conv_n,
+                       sn.out_h, sn.out_w, 1, sn.kw, 1, sn.kw, wrap32=wrap)
         return c
 
     def _trans_image(self, bt: TensorInfo, b: torch.Tensor, k: int, m: int) -> torch.Tensor:

@@ -163,7 +163,9 @@ def forward(graph, inputs, states=None):
     get = lambda t: vals[t.onnx_name] if t.onnx_name in vals else _weight(t)
     for sn in graph.nodes:
         out = sn.output
-        if isinstance(sn, G.MatmulNode):
+        if isinstance(sn, (G.MatmulNode, G.MatmulConvNode)):
+            # a MatMul lowered onto the conv unit computes exactly MatmulNode's result
+            # (_simulate.py:620-633 treats both alike)
             a, b = get(sn.inputs[0]), get(sn.inputs[1])
             if _pow2(sn.inputs[0], sn.inputs[1], out):
                 vals[out.onnx_name] = _matmul_exp(sn, a, b).reshape(out.shape)

@@ -1,5 +1,6 @@
 """The host-side weight images (cormorant_amd.packing) against the reference's fixture images."""
 import numpy as np
+import pytest
 
 from cormorant_amd.packing import conv_bias_image, conv_weight_image, pack_matmul_b
 from golden_io import CONV_COLS, MM_COLS, arr, cases
@@ -49,3 +50,58 @@ def test_conv_weight_image_round_trips_every_fixture():
         if t["has_bias"]:
             b = arr("conv", t["idx"], "b")
             np.testing.assert_array_equal(conv_bias_image(b[:M]), b[:len(conv_bias_image(b[:M]))])
+
+
+def test_conv_lowered_b_image_explicit_loop():
+    """x[s][c][kw p + j] = B[s][(c / 16) 16 kw + 16 j + c % 16][p] (test_matmul_on_conv.py:137-153)."""
+    from cormorant_amd.packing import conv_lowered_b_image
+    rng = np.random.default_rng(1)
+    for kw in (1, 2, 3, 4, 6):
+        for slices, k, m in ((1, 16 * kw, 5), (3, 32 * kw, 12)):
+            b = rng.integers(-1000, 1000, (slices, k, m)).astype(np.float64)
+            img = conv_lowered_b_image(b, k, m, kw)
+            ref = np.zeros((slices, k // kw, m * kw))
+            for s_ in range(slices):
+                for c in range(k // kw):
+                    for p in range(m):
+                        for j in range(kw):
+                            ref[s_, c, kw * p + j] = b[s_, (c // 16) * 16 * kw + j * 16 + c % 16, p]
+            np.testing.assert_array_equal(img, ref.reshape(-1))
+
+
+def test_lowered_conv_of_the_image_is_the_matmul():
+    """A as the packed 1 x kw weight, B's image as NCHW x, a direct conv of stride (1, kw) = A B."""
+    from cormorant_amd.packing import conv_lowered_b_image, conv_weight_image
+    rng = np.random.default_rng(2)
+    for n, k, m, kw, out_w in ((20, 64, 48, 2, 16), (16, 96, 40, 3, 20), (33, 128, 24, 4, 8), (8, 192, 12, 6, 12)):
+        a = rng.integers(-50, 50, (n, k))
+        b = rng.integers(-50, 50, (k, m))
+        in_ch, out_h = k // kw, m // out_w
+        x = conv_lowered_b_image(b, k, m, kw).reshape(in_ch, out_h, kw * out_w)
+        t = 16
+        w = np.zeros((n, in_ch, 1, kw), np.int64)
+        for c in range(in_ch):
+            for j in range(kw):
+                w[:, c, 0, j] = a[:, (c // t) * kw * t + j * t + c % t]
+        y = np.zeros((n, out_h, out_w), np.int64)
+        for j in range(kw):
+            y += np.einsum("mc,chw->mhw", w[:, :, 0, j], x[:, :, j::kw])
+        np.testing.assert_array_equal(y.reshape(n, m), a @ b)
+        np.testing.assert_array_equal(conv_weight_image(w.astype(np.int16)), a.reshape(-1).astype(np.int16))
+
+
+def test_matmul_conv_batch_modes():
+    from cormorant_amd.graph import MatmulConvNode, SchedulerError, TensorInfo as T
+    one = MatmulConvNode([T("a", [16, 64]), T("b", [64, 40])], T("c", [16, 40]))
+    assert (one.conv_n, one.conv_batch, one.calls, one.out_h, one.out_w) == (16, 1, 1, 1, 40)
+    cb = MatmulConvNode([T("a", [16, 64]), T("b", [3, 64, 40])], T("c", [3, 16, 40]))
+    assert (cb.conv_n, cb.conv_batch, cb.calls) == (16, 3, 1)
+    fold = MatmulConvNode([T("a", [3, 16, 64]), T("b", [64, 40])], T("c", [3, 16, 40]))
+    assert (fold.conv_n, fold.conv_batch, fold.calls) == (48, 1, 1)
+    per = MatmulConvNode([T("a", [4, 16, 64]), T("b", [4, 64, 24])], T("c", [4, 16, 24]))
+    assert (per.conv_n, per.conv_batch, per.calls) == (16, 1, 4)
+    for bad in (dict(a=[1, 64], b=[64, 40]), dict(a=[16, 60], b=[60, 40]), dict(a=[16, 64], b=[64, 36])):
+        with pytest.raises(SchedulerError):
+            MatmulConvNode([T("a", bad["a"]), T("b", bad["b"])], T("c", [bad["a"][0], bad["b"][1]]))
+    with pytest.raises(SchedulerError):               # kw 2 re-lays a constant B only
+        MatmulConvNode([T("a", [16, 64]), T("b", [64, 40])], T("c", [16, 40]), kw=2)
