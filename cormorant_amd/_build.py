@@ -33,6 +33,26 @@ def _compile(src: str) -> str:
     return obj
 
 
+HOST_SRC = os.path.join(HERE, "csrc_host", "cm_host.cpp")
+HOST_LIB = os.path.join(HERE, "libcormo_host.so")
+# the host ops round where the reference's double arithmetic does: no contraction into fused
+# multiply-adds, no fast-math reassociation
+HOST_CFLAGS = ["-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra", "-ffp-contract=off", "-fno-fast-math"]
+
+
+def build_host(verbose: bool = True) -> str:
+    """libcormo_host.so from csrc_host with g++ (glibc's libm)."""
+    tmp = HOST_LIB + ".tmp"
+    r = subprocess.run(["g++", *HOST_CFLAGS, HOST_SRC, "-o", tmp, "-lm"], capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("g++ failed on the host ops")
+    os.replace(tmp, HOST_LIB)
+    if verbose:
+        print(f"built {HOST_LIB}")
+    return HOST_LIB
+
+
 def build(verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     srcs = sources()
@@ -47,6 +67,7 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources")
+    build_host(verbose)
     return LIB
 
 

@@ -146,3 +146,54 @@ extern "C" int cm_copy16(const int16_t* src, int16_t* dst, uint32_t d0, uint32_t
               total, p, q);
     return CM_OK;
 }
+
+// ---------------------------------------------------------------- embedding rows
+// out[t][0 .. d) = table[clamp(ids[t], 0, rows - 1)][0 .. d) as 32-bit lanes: a workgroup per id,
+// four lanes a thread per step (one 16-byte store); int16 table lanes are sign-extended.
+namespace cm {
+namespace {
+
+template <bool I16>
+__global__ __launch_bounds__(256) void embed_rows_kernel(const void* __restrict__ table, const int32_t* __restrict__ ids,
+                                                         int32_t* __restrict__ out, uint32_t rows, uint32_t d) {
+    const uint32_t t = blockIdx.x;
+    int32_t id = ids[t];
+    id = id < 0 ? 0 : (id >= (int32_t)rows ? (int32_t)rows - 1 : id);
+    int32_t* o = out + (uint64_t)t * d;
+    for (uint32_t c = 4 * threadIdx.x; c < d; c += 4 * blockDim.x) {
+        int4 v;
+        if (I16) {
+            const short4 s = *reinterpret_cast<const short4*>(static_cast<const int16_t*>(table) + (uint64_t)id * d + c);
+            v = make_int4(s.x, s.y, s.z, s.w);
+        } else {
+            v = *reinterpret_cast<const int4*>(static_cast<const int32_t*>(table) + (uint64_t)id * d + c);
+        }
+        *reinterpret_cast<int4*>(o + c) = v;
+    }
+}
+
+}  // namespace
+}  // namespace cm
+
+extern "C" int cm_embed_rows(const void* table, uint32_t table_i16, const int32_t* ids, void* out, uint32_t n_ids,
+                             uint32_t rows, uint32_t d, void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    if (n_ids == 0 || d == 0) return CM_OK;
+    if (rows == 0) return fail(CM_EINVAL, "embed: an empty table");
+    if (n_ids > 0x7FFFFFFFu) return fail(CM_EINVAL, "embed: %u ids", n_ids);
+    if ((d & 3) || !aligned16(out) || (reinterpret_cast<uintptr_t>(table) & (table_i16 ? 7 : 15)) ||
+        (reinterpret_cast<uintptr_t>(ids) & 3))
+        return fail(CM_EALIGN, "embed: rows of a multiple of 4 lanes, 16-byte aligned out and table rows");
+    hipStream_t s = as_stream(stream);
+    if (table_i16) {
+        CM_LAUNCH("embed_rows_kernel", embed_rows_kernel<true>, dim3(n_ids), dim3(256), 0, s, table, ids,
+                  static_cast<int32_t*>(out), rows, d);
+    } else {
+        CM_LAUNCH("embed_rows_kernel", embed_rows_kernel<false>, dim3(n_ids), dim3(256), 0, s, table, ids,
+                  static_cast<int32_t*>(out), rows, d);
+    }
+    return CM_OK;
+}

@@ -17,6 +17,7 @@ import numpy as np
 from . import units
 from .graph import (AttentionNode, AttnContractNode, ConvNode, Graph, HeadView, MatmulNode, PoolNode, ReshapeNode,
                     ScheduledNode, SoftmaxVopNode, TensorInfo, conv_out, softmax_regs)
+from .host_ops import LlmEmbedNode
 from .rowops_nodes import LayerNorm32RoNode, ResAddBiasRoNode
 
 
@@ -189,9 +190,9 @@ class BertShape:
 def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int = 1, fused_attention: bool = True):
     """(graph, inputs, exps): the BERT-base-shaped encoder in per-tensor power-of-two numerics.
 
-    Token ids U{0 .. vocab-1} and embedding rows N(0, 1) (the embedding lookup is the host
-    op whose result, the int32 residual at 2^-15, is the graph's input); per layer, in the
-    arrangement of the reference's encoder template (vit.py:19-32):
+    Token ids U{0 .. vocab-1} (the graph's input) and embedding rows N(0, 1), gathered on the
+    GPU into the int32 residual at 2^-15 (LlmEmbedNode); per layer, in the arrangement of the
+    reference's encoder template (vit.py:19-32):
 
         x  = LayerNorm32(h)                          row-ops NORM, int32 -> int16
         qkv = x . Wqkv                               MatMul (pow2, int32 wrap)
@@ -223,8 +224,7 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
     rng_in = np.random.default_rng([seed, 0])
     emb = rng_in.standard_normal((S.vocab, S.d), dtype=np.float32)
     ids = rng_in.integers(0, S.vocab, (S.batch, S.seq))
-    h0 = emb[ids].astype(np.float64).reshape(S.batch * S.seq, S.d)
-    del emb
+    h0 = emb[ids[:calib_seqs]].astype(np.float64).reshape(-1, S.d)
     h0 = np.round(h0 * 2.0 ** RES_BITS) / 2.0 ** RES_BITS
     rng = np.random.default_rng([seed, 1])
     norm = lambda *sh: (rng.standard_normal(sh, dtype=np.float32) * 0.02)       # noqa: E731
@@ -284,12 +284,14 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
         e["dd"] = min(e["dd"], RES_BITS)
         exps.append(e)
 
-    # ---- the integer graph
+    # ---- the integer graph: the token ids in, their embedding rows gathered into the int32
+    # residual at 2^-15 (LlmEmbedNode, the host op the reference runs before the encoder)
     T_ = TensorInfo
     rows, D = S.batch * S.seq, S.d
     BH = S.batch * H
-    nodes = []
+    ids_t = T_("ids", [rows], exp=0, kind="i32")
     h_in = T_("h0", [rows, D], exp=RES_BITS, kind="i32")
+    nodes = [LlmEmbedNode([ids_t], h_in, table=emb)]
     hcur = h_in
     for li, (L, e) in enumerate(zip(Ls, exps)):
         p = f"l{li}."
@@ -332,9 +334,9 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
         hn = T_(p + "h", [rows, D], exp=RES_BITS, kind="i32")
         nodes.append(ResAddBiasRoNode([h1, dd], hn, bias=L["b2"]))
         hcur = hn
-    g = Graph(nodes, input_tensors=[h_in], output_tensors=[hcur])
+    g = Graph(nodes, input_tensors=[ids_t], output_tensors=[hcur])
     encode_matmul_weights(g.nodes, AP_FIXED_16_8)
-    return g, {"h0": h0}, exps
+    return g, {"ids": ids.reshape(-1).astype(np.float64)}, exps
 
 
 # ---------------------------------------------------------------- SmolLM2-360M-shaped decode step
@@ -435,7 +437,8 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
     then RMSNorm, the tied head (x E^T) and Dequant to float32 logits.
 
     Synthetic data (no checkpoint): the tied embedding, every linear N(0, 0.02), RMSNorm
-    gammas 1 + N(0, 0.02); the step's residual h0 = embedding rows of random ids; the cache
+    gammas 1 + N(0, 0.02); the step's token ids (the graph's input) gathered on the GPU from the
+    tied embedding into the int32 residual (LlmEmbedNode); the cache
     rows before ``pos`` N(0, KV_SIGMA) in place of a prefill; every draw is per sequence, so a
     smaller batch of the same seed is the leading sequences of a larger one.  Exponents from a
     float64 run of the step over the first ``calib_seqs`` sequences (``_fit_exp``), with the
@@ -539,8 +542,10 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
     # ---- the integer graph
     T_ = TensorInfo
     nodes = []
+    ids_t = T_("ids", [B], exp=0, kind="i32")
     h_in = T_("h0", [B, D], exp=RES_BITS, kind="i32")
-    inputs = {"h0": h0}
+    nodes.append(LlmEmbedNode([ids_t], h_in, table=emb))
+    inputs = {"ids": ids.astype(np.float64)}
     cache_ts = []
     hcur = h_in
     for li, (L, e) in enumerate(zip(Ls, exps)):
@@ -615,6 +620,6 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
     nodes.append(DequantRoNode([lr], lf))
     lo = T_("logits", [B, S.vocab], kind="f32")
     nodes.append(ReshapeNode([lf], lo))
-    g = Graph(nodes, input_tensors=[h_in] + cache_ts, output_tensors=[lo])
+    g = Graph(nodes, input_tensors=[ids_t] + cache_ts, output_tensors=[lo])
     encode_matmul_weights(g.nodes, AP_FIXED_16_8)
     return g, inputs, exps

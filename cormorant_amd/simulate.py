@@ -20,6 +20,7 @@ from .graph import (AttentionNode, AttnContractNode, ConvNode, Graph, KvWriteNod
                     MatmulNode, PermuteNode, PoolNode, ReshapeNode, RowOpsNode, ScheduledNode, SchedulerError, SoftmaxVopNode,
                     TensorInfo, attn_keys)
 from .packing import conv_bias_image, conv_lowered_b_image, conv_weight_image, pack_matmul_b
+from .host_ops import HostNode, LlmEmbedNode
 from .rowops_nodes import RoCallNode, RoJob, RowOpsAdapter
 
 _TORCH = {"i16": torch.int16, "i32": torch.int32, "f32": torch.float32}
@@ -113,6 +114,10 @@ class Simulator:
                     continue
             if isinstance(sn, MatmulNode):
                 raw[sn.output.onnx_name] = self._matmul(sn, raw)
+            elif isinstance(sn, LlmEmbedNode):
+                raw[sn.output.onnx_name] = self._embed(sn, raw)
+            elif isinstance(sn, HostNode):
+                raw[sn.output.onnx_name] = self._host_node(sn, raw)
             elif isinstance(sn, MatmulConvNode):
                 raw[sn.output.onnx_name] = self._matmul_conv(sn, raw)
             elif isinstance(sn, ConvNode):
@@ -261,6 +266,32 @@ class Simulator:
                          a_bs=n * k if a_batch > 1 else 0, b_bs=k * m if b_batch > 1 else 0,
                          c_bs=n * m, wrap32=wrap)
         return c
+
+    def _embed(self, sn: LlmEmbedNode, raw) -> torch.Tensor:
+        """The embedding rows gathered on the device from the output-lane image of the table."""
+        key = f"{id(sn)}#embed"
+        img = self._images.get(key)
+        if img is None:
+            img = torch.from_numpy(sn.image()).to(self.device)
+            self._images[key] = img
+        ids = self._get(sn.inputs[0], raw).reshape(-1).contiguous()
+        out = self._new(sn.output)
+        units.embed_rows(img, ids, out, sn.rows, sn.d)
+        return out
+
+    def _host_node(self, sn: HostNode, raw) -> torch.Tensor:
+        """A host op (host_ops): host copies of its inputs' values, the node's reference(), the
+        result (and every state it updated in place) back on the device."""
+        ins = []
+        for t in sn.inputs:
+            v = self._get(t, raw)
+            ins.append(np.asarray(v) if t.kind == "host" else self._to_values(t, v))
+        y = sn.reference(ins, self._dtype)
+        for t, v in zip(sn.inputs, ins):
+            if t.state:
+                dev = self._get(t, raw)
+                dev.copy_(self._to_device(t, v).reshape(dev.shape))
+        return self._to_device(sn.output, y).reshape(-1)
 
     def _matmul_conv(self, sn: MatmulConvNode, raw) -> torch.Tensor:
         """A MatMul on the conv unit (nodes.py:1712-1756): weight = A's rows, x = B's conv image,

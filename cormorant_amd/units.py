@@ -130,6 +130,24 @@ def copy16(src: torch.Tensor, dst: torch.Tensor, dims, src_strides, dst_strides)
     return dst
 
 
+def embed_rows(table: torch.Tensor, ids: torch.Tensor, out: torch.Tensor, rows: int, d: int) -> torch.Tensor:
+    """cm_embed_rows: out[t] = table[clamp(ids[t], 0, rows - 1)] for every id, the table int16
+    (sign-extended) or 32-bit lanes, out 32-bit lanes [n_ids][d]."""
+    n = ids.numel()
+    if table.dtype not in (torch.int16, torch.int32, torch.float32) or not table.is_cuda or not table.is_contiguous():
+        raise ValueError("embed_rows: table must be a contiguous GPU int16 / int32 / float32 tensor")
+    if table.numel() < rows * d:
+        raise ValueError(f"embed_rows: table holds {table.numel()} lanes; [{rows}][{d}] needed")
+    _require(ids, "ids", torch.int32, n)
+    if out.dtype not in (torch.int32, torch.float32) or not out.is_cuda or not out.is_contiguous() \
+            or out.numel() < n * d:
+        raise ValueError(f"embed_rows: out must be a contiguous GPU 32-bit tensor of {n * d} lanes")
+    rc = _lib.lib().cm_embed_rows(_ptr(table), int(table.dtype == torch.int16), _ptr(ids), _ptr(out), n, rows, d,
+                                  _stream())
+    _lib.check(rc, "cm_embed_rows")
+    return out
+
+
 def attention(qkv: torch.Tensor, o: torch.Tensor, batch: int, seq: int, heads: int, head_dim: int, ld: int,
               q_off: int, k_off: int, v_off: int, o_ld: int, smx_cm: int, smx_cfg: int) -> torch.Tensor:
     """An encoder layer's attention in one call (cm_attention): q.K^T, the keys-major softmax and

@@ -267,6 +267,16 @@ int cm_copy16(const int16_t* src, int16_t* dst, uint32_t d0, uint32_t d1, uint32
               uint64_t s0, uint64_t s1, uint64_t s2, uint64_t s3, uint64_t t0, uint64_t t1, uint64_t t2,
               uint64_t t3, void* stream);
 
+/* The token-id embedding lookup of LlmEmbedNode (inference-scheduler/src/llm_nodes.py:466-570), a
+ * gather: out[t][0 .. d) = table[clamp(ids[t], 0, rows - 1)][0 .. d) for t < n_ids, out of 32-bit
+ * lanes.  `table` holds the output's own lanes for every row -- the int32 residual's raws
+ * (table_i16 = 0, or table_i16 = 1 for int16 raws that the gather sign-extends, the reference's
+ * int16 storage of a residual table whose raws fit) or float32 values (table_i16 = 0) -- so the
+ * gather is exact.  d a multiple of 4, `out` 16-byte aligned, table rows 16-byte (int16: 8-byte)
+ * aligned; ids int32 on the device. */
+int cm_embed_rows(const void* table, uint32_t table_i16, const int32_t* ids, void* out, uint32_t n_ids,
+                  uint32_t rows, uint32_t d, void* stream);
+
 /* ---------------------------------------------------------------- Attention (composed)
  * The attention of an encoder layer in one call -- no counterpart among the reference's
  * units: the composition of VitAttnPrep (head split), the q.K^T contraction (the arithmetic

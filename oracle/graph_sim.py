@@ -11,6 +11,7 @@ from cormorant_amd import graph as G
 from cormorant_amd.dtype import AP_FIXED_16_8 as DT
 from cormorant_amd.rowops_nodes import RowOpsAdapter
 from oracle import cm
+from oracle import host_ref
 from oracle.attn_prep import attn_prep, transpose
 
 F = DT.frac_bits
@@ -150,6 +151,42 @@ def _chan(t, n):
     return np.broadcast_to(np.asarray(F if t.exp is None else t.exp, np.int64).reshape(-1), (n,)).copy()
 
 
+_HOST_OPS = ("SoftmaxNode", "LayerNormNode", "GeluNode", "LlmRMSNormNode", "LlmSiluMulNode", "LlmResAddNode",
+             "LlmDequantNode", "LlmToHostNode", "LlmAttentionNode")
+
+
+def _host_op(sn, ins, vals):
+    """The host ops' reference() bodies (oracle/host_ref.py)."""
+    name, out = type(sn).__name__, sn.output
+    if name == "SoftmaxNode":
+        return host_ref.softmax(ins[0], int(sn.inputs[0].shape[-1]))
+    if name == "LayerNormNode":
+        return host_ref.layer_norm(ins[0], int(sn.inputs[0].shape[-1]), sn.gamma, sn.beta, sn.eps, sn.tf_form)
+    if name == "GeluNode":
+        return host_ref.gelu(ins[0], sn.approximate, sn.c1, sn.c2, sn.k, sn.div)
+    if name == "LlmRMSNormNode":
+        W = int(sn.inputs[0].shape[-1])
+        return host_ref.rms_norm(ins[0], sn.gamma, sn.eps, _chan(out, W), W)
+    if name == "LlmSiluMulNode":
+        n = int(sn.inputs[0].shape[-1])
+        return host_ref.silu_mul(ins[0], ins[1], _chan(sn.inputs[0], n), _chan(out, n))
+    if name == "LlmResAddNode":
+        return host_ref.f32(np.asarray(ins[0], np.float64) + np.asarray(ins[1], np.float64))
+    if name in ("LlmDequantNode", "LlmToHostNode"):
+        return host_ref.f32(ins[0])
+    # LlmAttentionNode: the caches (states) in place
+    H, KV, HD = sn.heads, sn.kv_heads, sn.head_dim
+    q0t, ckt, cvt = sn.inputs[0], sn.inputs[-2], sn.inputs[-1]
+    T = q0t.numel // (H * HD)
+    pos = int(np.asarray(ins[3]).reshape(-1)[0])
+    n = int(np.asarray(ins[4]).reshape(-1)[0]) if len(sn.inputs) == 7 else T
+    ck = vals[ckt.onnx_name].reshape(ckt.shape)
+    cv = vals[cvt.onnx_name].reshape(cvt.shape)
+    return host_ref.attention(ins[0], ins[1], ins[2], pos, n, ck, cv, _chan(ckt, KV * HD), _chan(cvt, KV * HD),
+                              _chan(out, H * HD), np.asarray(sn.cos, np.float32), np.asarray(sn.sin, np.float32),
+                              T, H, KV, HD)
+
+
 def forward(graph, inputs, states=None):
     """Every tensor's float64 values.  ``states`` ({name: float64 array}) are the persistent
     states, updated in place (_simulate.py:573-577); default: zeros, or copies of the inputs
@@ -216,6 +253,12 @@ def forward(graph, inputs, states=None):
                     o[b, :, h * hd:(h + 1) * hd] = _wrap_floor(p_.astype(np.float64) @ v)
             fo = float(F if out.exp is None else out.exp)
             vals[out.onnx_name] = (o.astype(np.float64) / 2.0 ** fo).reshape(out.shape)
+        elif type(sn).__name__ == "LlmEmbedNode":
+            fo = F if out.exp is None else np.asarray(out.exp).reshape(-1)[0]
+            vals[out.onnx_name] = host_ref.embed(get(sn.inputs[0]), sn.table, sn.scale, fo,
+                                                 out.kind == "i32").reshape(out.shape)
+        elif type(sn).__name__ in _HOST_OPS:
+            vals[out.onnx_name] = _host_op(sn, [get(t) for t in sn.inputs], vals).reshape(out.shape)
         elif type(sn).__name__ == "TransposeRoNode":
             xt = sn.inputs[0]
             vals[out.onnx_name] = transpose(get(xt).reshape(xt.shape), sn.perm).reshape(out.shape)

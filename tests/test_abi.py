@@ -9,14 +9,14 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def declared_symbols():
+def declared_symbols(prefix="cm_", header=None):
     names = set()
     inc = os.path.join(ROOT, "include")
     for f in os.listdir(inc):
-        if f.endswith(".h"):
+        if f.endswith(".h") and (header is None or f == header):
             text = open(os.path.join(inc, f)).read()
             text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-            names |= set(re.findall(r"\b(cm_\w+)\s*\(", text))
+            names |= set(re.findall(r"\b(" + prefix + r"\w+)\s*\(", text))
     return sorted(names)
 
 
@@ -59,3 +59,15 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "absent.so"))
     with pytest.raises(_lib.HipLibraryMissing):
         _lib.lib()
+
+
+def test_every_declared_host_symbol_is_exported():
+    """libcormo_host.so exports every cmh_ entry point include/cormorant_host.h declares."""
+    from cormorant_amd import host_ops
+    syms = declared_symbols("cmh_", "cormorant_host.h")
+    assert len(syms) >= 9
+    lib = host_ops.host_lib()
+    for s in syms:
+        assert hasattr(lib, s), s
+        assert s in host_ops.HOST_SIGNATURES, f"{s} has no ctypes signature"
+    assert lib.cmh_abi_version() == 100

@@ -35,8 +35,11 @@ def test_permute_gather_is_the_transpose():
 
 def test_encoder_exponents_and_structure():
     g, inputs, exps = models.bert_encoder(SMALL, seed=1, fused_attention=False)
-    assert inputs["h0"].shape == (SMALL.batch * SMALL.seq, SMALL.d)
-    assert np.array_equal(inputs["h0"] * 2 ** 15, np.round(inputs["h0"] * 2 ** 15))
+    from cormorant_amd.host_ops import LlmEmbedNode
+    assert set(inputs) == {"ids"} and inputs["ids"].shape == (SMALL.batch * SMALL.seq,)
+    assert ((inputs["ids"] >= 0) & (inputs["ids"] < SMALL.vocab)).all()
+    emb = g.nodes[0]
+    assert isinstance(emb, LlmEmbedNode) and emb.output.onnx_name == "h0" and emb.output.exp == 15
     for e in exps:
         assert e["s"] == e["q"] + e["k"] - 8 and e["o"] == e["p"] + e["v"] - 8
         assert e["f"] == 8 and e["ao"] <= 15 and e["dd"] <= 15

@@ -34,4 +34,4 @@ def test_smollm2_small_graph():
     for e in exps[:-1]:
         assert e["s"] == e["q"] + e["k"] - 8 and e["o"] == e["p"] + e["v"] - 8
         assert e["a"] <= 15 and e["d"] <= 15 and e["g"] <= 14
-    assert set(inputs) == {"h0"} | {f"l{i}.{c}" for i in range(2) for c in ("kc", "vc")}
+    assert set(inputs) == {"ids"} | {f"l{i}.{c}" for i in range(2) for c in ("kc", "vc")}
