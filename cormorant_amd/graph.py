@@ -198,8 +198,16 @@ class SoftmaxVopNode:
     cfg: int = 0x0813
     mask: Optional[int] = None
     keys_major: bool = False
+    mask_t: Optional[TensorInfo] = None      # a runtime mask: the host value of this tensor + mask_add
+    mask_add: int = 0
 
-    def mask_reg(self, n: int) -> int:
+    def mask_reg(self, n: int, host: Optional[int] = None) -> int:
+        """The mask register: a runtime one (host + mask_add, the valid keys of a decode step at
+        position host), the static one, or every element valid."""
+        if self.mask_t is not None:
+            if host is None:
+                raise SchedulerError(f"softmax '{self.output.onnx_name}': the runtime mask needs its host value")
+            return int(host) + self.mask_add
         return n if self.mask is None else self.mask
 
 
@@ -390,6 +398,14 @@ class KvWriteNode:
     inputs: List[TensorInfo]
     output: TensorInfo
     pos: int = 0
+    pos_t: Optional[TensorInfo] = None       # a runtime position: this host tensor's value
+
+    def position(self, host: Optional[int] = None) -> int:
+        if self.pos_t is not None:
+            if host is None:
+                raise SchedulerError(f"KV write '{self.output.onnx_name}': the runtime position needs its host value")
+            return int(host)
+        return self.pos
 
 
 @dataclass

@@ -419,7 +419,8 @@ def smollm2_weights(shape: LlamaShape = LlamaShape(), seed: int = 0):
     return emb, Ls, gf
 
 
-def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: int = 1, weights=None):
+def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: int = 1, weights=None,
+                   runtime_pos: bool = False):
     """(graph, inputs, exps): one greedy decode step of ``shape.batch`` sequences, each at cache
     position ctx - 1 (the cache full after the step's row: every cache row is a key), pow2
     numerics on the units as the reference's llama.py front end lays out a layer with the
@@ -445,7 +446,12 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
     pow2 rules: f_s = f_q + f_k - 8 (q / k lowered until
     s fits), P at 2^-14, f_o = f_p + f_v - 8, deltas at <= 2^-15, the gate at <= 2^-14, and
     every weight's exponent f_out + 8 - f_in at least 10.  ``weights``: smollm2_weights(shape,
-    seed) made once for several builds (they depend on the shape's sizes, not its batch)."""
+    seed) made once for several builds (they depend on the shape's sizes, not its batch).
+
+    ``runtime_pos``: the step's position is a host input "pos" (RoPE's table row, the cache row
+    written, the softmax's valid keys pos + 1) and the KV caches are persistent states, so one
+    graph runs successive decode steps over the same caches (_forward_pass with ``states``);
+    the inputs then carry "pos" = ctx - 1 and the caches' prefill as the states' first values."""
     from .dtype import AP_FIXED_16_8
     from .numeric import encode_matmul_weights
     from .rowops_nodes import DequantRoNode, RMSNormRoNode, ResAddRoNode, RopeRoNode, SiluMulRoNode
@@ -546,12 +552,15 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
     h_in = T_("h0", [B, D], exp=RES_BITS, kind="i32")
     nodes.append(LlmEmbedNode([ids_t], h_in, table=emb))
     inputs = {"ids": ids.astype(np.float64)}
+    pos_t = T_("pos", [1], kind="host") if runtime_pos else None
+    if runtime_pos:
+        inputs["pos"] = np.array([pos], np.float64)
     cache_ts = []
     hcur = h_in
     for li, (L, e) in enumerate(zip(Ls, exps)):
         p = f"l{li}."
-        kc_t = T_(p + "kc", [B, KV, S.ctx, HD], exp=e["k"])
-        vc_t = T_(p + "vc", [B, KV, S.ctx, HD], exp=e["v"])
+        kc_t = T_(p + "kc", [B, KV, S.ctx, HD], exp=e["k"], state=runtime_pos)
+        vc_t = T_(p + "vc", [B, KV, S.ctx, HD], exp=e["v"], state=runtime_pos)
         cache_ts += [kc_t, vc_t]
         kc, vc = caches[li]
         inputs[kc_t.onnx_name] = np.round(kc.astype(np.float64) * 2.0 ** e["k"]) / 2.0 ** e["k"]
@@ -565,13 +574,14 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
         v = T_(p + "v", [B, KD], exp=e["v"])
         nodes.append(MatmulNode([x, T_(p + "wv", [D, KD], data=L["wv"])], v))
         qr = T_(p + "qr", [B, A], exp=e["q"])
-        nodes.append(RopeRoNode([q], qr, heads=H, head_dim=HD, cos=cos, sin=sin, pos=pos, same_pos=True))
+        nodes.append(RopeRoNode([q], qr, heads=H, head_dim=HD, cos=cos, sin=sin, pos=pos, same_pos=True, pos_t=pos_t))
         kr = T_(p + "kr", [B, KD], exp=e["k"])
-        nodes.append(RopeRoNode([k], kr, heads=KV, head_dim=HD, cos=cos, sin=sin, pos=pos, same_pos=True))
+        nodes.append(RopeRoNode([k], kr, heads=KV, head_dim=HD, cos=cos, sin=sin, pos=pos, same_pos=True,
+                                pos_t=pos_t))
         kc2 = T_(p + "kc1", [B, KV, S.ctx, HD], exp=e["k"])
-        nodes.append(KvWriteNode([kr, kc_t], kc2, pos=pos))
+        nodes.append(KvWriteNode([kr, kc_t], kc2, pos=pos, pos_t=pos_t))
         vc2 = T_(p + "vc1", [B, KV, S.ctx, HD], exp=e["v"])
-        nodes.append(KvWriteNode([v, vc_t], vc2, pos=pos))
+        nodes.append(KvWriteNode([v, vc_t], vc2, pos=pos, pos_t=pos_t))
         # per (sequence, group): the group's G query rows against the cache's K rows, the scores
         # query-major s[b g][h'][j] (the unit's column mode takes query blocks of 16, so the
         # G queries of a decode step go through its row mode: VitAttnSoftmax's query_major
@@ -584,7 +594,7 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
         nodes.append(AttnContractNode([qrows, kview], st, b_trans=True))
         cmr, cfg = softmax_regs(e["s"], 1.0 / math.sqrt(HD), e["p"])
         pr = T_(p + "P", [B * KV, G, keys], exp=e["p"])
-        nodes.append(SoftmaxVopNode([st], pr, cm=cmr, cfg=cfg, mask=pos + 1))
+        nodes.append(SoftmaxVopNode([st], pr, cm=cmr, cfg=cfg, mask=pos + 1, mask_t=pos_t, mask_add=1))
         vview = T_(p + "vc1v", [B * KV, S.ctx, HD], exp=e["v"])
         nodes.append(ReshapeNode([vc2], vview))
         o = T_(p + "o", [B * KV, G, HD], exp=e["o"])
@@ -620,6 +630,6 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
     nodes.append(DequantRoNode([lr], lf))
     lo = T_("logits", [B, S.vocab], kind="f32")
     nodes.append(ReshapeNode([lf], lo))
-    g = Graph(nodes, input_tensors=[ids_t] + cache_ts, output_tensors=[lo])
+    g = Graph(nodes, input_tensors=[ids_t] + ([pos_t] if runtime_pos else []) + cache_ts, output_tensors=[lo])
     encode_matmul_weights(g.nodes, AP_FIXED_16_8)
     return g, inputs, exps

@@ -505,6 +505,7 @@ class RopeRoNode(RowOpsAdapter):
     pos: int = 0
     F: int = 8
     same_pos: bool = False
+    pos_t: Optional[TensorInfo] = None       # a runtime position (this host tensor's value) for pos
     table: Optional[TensorInfo] = field(default=None, init=False)
 
     def __post_init__(self):
@@ -522,15 +523,21 @@ class RopeRoNode(RowOpsAdapter):
         _require((sa <= 63).all() and (sb <= 63).all() and (sc >= 0).all() and (sc <= 63).all(), what,
                  "RoPE exponents beyond the shifts")
         tab = rope_table(self.cos, self.sin)
-        last = self.pos + (1 if self.same_pos else self.rows)
-        _require(tab.shape[1] == 2 * HD and 0 <= self.pos and last <= tab.shape[0], what,
+        self._span = 1 if self.same_pos else self.rows
+        _require(tab.shape[1] == 2 * HD and 0 <= self.pos and self.pos + self._span <= tab.shape[0], what,
                  "cos / sin tables [C][HD/2] covering the rows' positions")
         self.table = TensorInfo(f"{y.onnx_name}__rope_table", list(tab.shape), data=tab, kind="i32", raw=True)
         self._params, self.bcast = pblock(0, 0, sa.reshape(-1), sb.reshape(-1), sc.reshape(-1), n)
 
-    def jobs(self):
+    def jobs(self, pos: Optional[int] = None):
+        """The job at the static position, or at ``pos`` (the runtime position's host value)."""
+        p = self.pos if pos is None else int(pos)
+        if self.pos_t is not None and pos is None:
+            raise SchedulerError(f"RoPE '{self.output.onnx_name}': the runtime position needs its host value")
+        if not 0 <= p or p + self._span > self.table.shape[0]:
+            raise SchedulerError(f"RoPE '{self.output.onnx_name}': position {p} past the cos / sin tables")
         return [RoJob(opword(RO_ROPE, K_I16, K_I32, K_I16, b_en=True, p_bcast=self.bcast), self._params, self.n,
-                      aux=self.head_dim, b_row0=self.pos, b_same=self.same_pos)]
+                      aux=self.head_dim, b_row0=p, b_same=self.same_pos)]
 
 
 # ---------------------------------------------------------------- register-level job lists

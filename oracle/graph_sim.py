@@ -117,12 +117,19 @@ def _rows16(x2d, kind):
     return img.reshape(-1), stride
 
 
-def run_adapter(node, raw_of):
+def _mask(sn, n, get):
+    """The softmax node's mask register, a runtime one from its host tensor."""
+    if getattr(sn, "mask_t", None) is not None:
+        return int(np.asarray(get(sn.mask_t)).reshape(-1)[0]) + sn.mask_add
+    return n if sn.mask is None else sn.mask
+
+
+def run_adapter(node, raw_of, host_pos=None):
     """A row-ops adapter's jobs through the C oracle with the Simulator's row re-layout:
     ``raw_of(tensor)`` gives the raw lanes of an input; returns the raw output."""
     at, ot = node.inputs[0], node.output
     bt = getattr(node, "table", None) or (node.inputs[1] if len(node.inputs) > 1 else None)
-    jobs = node.jobs()
+    jobs = node.jobs(pos=host_pos) if getattr(node, "pos_t", None) is not None else node.jobs()
     width = max(j.col0 + j.n for j in jobs)
     rows = at.numel // width
     a2d = np.asarray(raw_of(at)).reshape(rows, width)
@@ -221,7 +228,9 @@ def forward(graph, inputs, states=None):
                 if t.kind == "f32":
                     return np.asarray(get(t), np.float32)
                 return _raw_of(t, get(t))
-            y = run_adapter(sn, raw_of).reshape(out.shape)
+            pt = getattr(sn, "pos_t", None)
+            y = run_adapter(sn, raw_of, None if pt is None else int(np.asarray(get(pt)).reshape(-1)[0])).reshape(
+                out.shape)
             if out.kind == "f32":
                 vals[out.onnx_name] = y.astype(np.float64)
             else:
@@ -279,7 +288,8 @@ def forward(graph, inputs, states=None):
             xt, ct = sn.inputs[0], sn.inputs[1]
             B, KV, C, HD = (int(v) for v in ct.shape)
             cache = vals[ct.onnx_name].reshape(B, KV, C, HD)          # the state, written in place
-            cache[:, :, sn.pos, :] = get(xt).reshape(B, KV, HD)
+            pos = sn.pos if sn.pos_t is None else int(np.asarray(get(sn.pos_t)).reshape(-1)[0])
+            cache[:, :, pos, :] = get(xt).reshape(B, KV, HD)
             vals[out.onnx_name] = cache
         elif isinstance(sn, G.ReshapeNode):
             vals[out.onnx_name] = get(sn.inputs[0]).reshape(out.shape)
@@ -302,7 +312,7 @@ def forward(graph, inputs, states=None):
                 ps = []
                 for m in mats:
                     c = cm.vectorop(np.ascontiguousarray(m.reshape(-1), np.int16), None, nq * k8, keys, 11, nq, nq, k8, 0, 0,
-                                    sn.cm, sn.cfg, sn.mask_reg(keys))
+                                    sn.cm, sn.cfg, _mask(sn, keys, get))
                     ps.append(c.reshape(nq, k8)[:, :keys])
                 vals[out.onnx_name] = (np.stack(ps).astype(np.float64) / 2.0 ** fp).reshape(out.shape)
             else:
@@ -312,7 +322,7 @@ def forward(graph, inputs, states=None):
                 xr = np.zeros((rows, n8), np.int16)
                 xr[:, :n] = x.reshape(rows, n)
                 c = cm.vectorop(xr.reshape(-1), None, rows * n8, n, 10, rows, n8, n8, 0, 0, sn.cm, sn.cfg,
-                                sn.mask_reg(n))
+                                _mask(sn, n, get))
                 vals[out.onnx_name] = (c.reshape(rows, n8)[:, :n].astype(np.float64) / 2.0 ** fp).reshape(out.shape)
         elif isinstance(sn, G.AttnContractNode):
             at, bt = sn.inputs
