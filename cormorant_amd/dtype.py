@@ -62,6 +62,38 @@ class ApFixed16:
         c = np.clip(np.asarray(x, np.float64), self.min_val, self.max_val)
         return np.round(c * self.scale).astype(np.int16).view(np.uint16)
 
+    def exp_to_storage(self, x, f) -> np.ndarray:
+        """The uint16 storage lanes of values at 2^-f: round half to even, saturate
+        (dtype.py:436-439)."""
+        s = np.power(2.0, np.asarray(f, np.float64))
+        r = np.clip(np.round(np.asarray(x, np.float64) * s), I16_LO, I16_HI)
+        return r.astype(np.int16).view(np.uint16)
+
+    def int_to_storage(self, x) -> np.ndarray:
+        """The uint16 lanes of integer values (ids, masks): the raw integers themselves,
+        truncated toward zero and saturated."""
+        r = np.clip(np.trunc(np.asarray(x, np.float64)), I16_LO, I16_HI)
+        return r.astype(np.int16).view(np.uint16)
+
+    def dat_bytes(self, data) -> bytes:
+        """The little-endian bytes of a .dat file: float_to_storage of the flattened values
+        (dtype.py:397-400)."""
+        return self.float_to_storage(np.asarray(data, np.float64).reshape(-1)).astype("<u2").tobytes()
+
+    def ramp_to_float(self, positions) -> np.ndarray:
+        """The value of the test harness's fill p[pos] = (Data_t)(pos & 0xFFFF) (dtype.py:385-389)."""
+        raw = (np.asarray(positions, np.int64) & 0xFFFF).astype(np.uint16).view(np.int16)
+        return raw.astype(np.float64) / self.scale
+
+    def ramp_to_float_exp(self, positions, f) -> np.ndarray:
+        """The ramp fill's value at 2^-f (dtype.py:441-443)."""
+        raw = (np.asarray(positions, np.int64) & 0xFFFF).astype(np.uint16).view(np.int16)
+        return raw.astype(np.float64) / np.power(2.0, np.asarray(f, np.float64))
+
+    def format_literal(self, storage_val) -> str:
+        """A storage lane as a C literal, 0x%04X (dtype.py:417-419)."""
+        return f"0x{int(storage_val) & 0xFFFF:04X}"
+
     def quantize_exp(self, x, f) -> np.ndarray:
         """round half to even at 2^-f, saturate, NaN -> 0 (dtype.py:278-285)."""
         s = np.power(2.0, np.asarray(f, np.float64))

@@ -38,6 +38,7 @@ class TensorInfo:
     chexp: Optional[np.ndarray] = None        # per-channel exponents of axis 1 (NCHW), tensor.py
     group_layout: Optional[tuple] = None      # (KV, HD): a [C][KV * HD] cache stored group-major
     state: bool = False               # a persistent state (a KV cache): updated in place, kept across passes
+    host: Optional[str] = None        # the reference's host-memory annotation ("f32", "i32", "i16"), if any
 
     @property
     def numel(self) -> int:
@@ -59,6 +60,52 @@ class ScheduledNode:
     @property
     def arity(self) -> int:
         return 2 if self.op_code < OP_RELU else 1
+
+    @property
+    def fusable_act(self) -> Optional[int]:
+        """The act register value this unary node would become in its producer (RELU -> act 1,
+        RELU6 -> 2, the activation unit's ops LeakyReLU / SiLU / GELU / GELU-tanh -> 3 .. 6;
+        nodes.py:347-353), else None."""
+        return _ACT_FOR_OP.get(self.op_code) if self.arity == 1 else None
+
+
+ACTIVATION_OPS = frozenset({6, 7, 8, 9})          # LeakyReLU, SiLU, GELU, GELU-tanh (nodes.py:156)
+_ACT_FOR_OP = {OP_RELU: 1, OP_RELU6: 2, 6: 3, 7: 4, 8: 5, 9: 6}
+
+
+def fuse_activations(graph: "Graph") -> int:
+    """Fold each unary activation into the VectorOP node producing its input (the reference's
+    OnnxGraph._fuse_activations, graph.py:1005-1058): when the producer is a VectorOP with no act
+    yet and is not itself an activation op, the intermediate is not a graph output, the
+    activation is its only reader and keeps its element count, the producer writes the
+    activation's output with ``act`` set and the activation node goes.  Returns the count."""
+    nodes = graph.nodes
+    readers: Dict[str, List[int]] = {}
+    for i, sn in enumerate(nodes):
+        for t in sn.inputs:
+            if t is not None:
+                readers.setdefault(t.onnx_name, []).append(i)
+    producer = {sn.output.onnx_name: i for i, sn in enumerate(nodes)}
+    outputs = {t.onnx_name for t in graph.output_tensors}
+    gone = set()
+    for i, sn in enumerate(nodes):
+        if not isinstance(sn, ScheduledNode) or sn.fusable_act is None:
+            continue
+        src = sn.inputs[0]
+        j = producer.get(src.onnx_name)
+        if j is None:
+            continue
+        prod = nodes[j]
+        if (not isinstance(prod, ScheduledNode) or prod.act != ACT_NONE or prod.op_code in ACTIVATION_OPS
+                or src.onnx_name in outputs or readers.get(src.onnx_name, []) != [i]
+                or src.numel != sn.output.numel):
+            continue
+        prod.act, prod.alpha, prod.output = sn.fusable_act, sn.alpha, sn.output
+        producer[sn.output.onnx_name] = j
+        gone.add(i)
+    if gone:
+        graph.nodes = [sn for i, sn in enumerate(nodes) if i not in gone]
+    return len(gone)
 
 
 @dataclass

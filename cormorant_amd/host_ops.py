@@ -326,8 +326,8 @@ class LlmEmbedNode:
         self.rows, self.d = int(tab.shape[0]), int(tab.shape[1])
         if y.numel != ids.numel * self.d or int(y.shape[-1]) != self.d:
             raise SchedulerError(f"{what}: output [{ids.numel}][{self.d}]")
-        if y.kind not in ("i32", "f32") or ids.kind != "i32":
-            raise SchedulerError(f"{what}: int32 ids into the int32 residual or float32 rows")
+        if y.kind not in ("i32", "f32") or ids.kind not in ("i32", "host"):
+            raise SchedulerError(f"{what}: int32 ids (device or host) into the int32 residual or float32 rows")
         if self.d % 4:
             raise SchedulerError(f"{what}: rows of a multiple of 4 lanes")
         if float(np.float32(self.scale)) != float(self.scale) or not self.scale > 0:

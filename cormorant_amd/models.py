@@ -323,10 +323,11 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
         x2 = T_(p + "x2", [rows, D], exp=e["x2"])
         nodes.append(LayerNorm32RoNode([h1], x2, gamma=L["g2"], beta=L["be2"], eps=S.eps))
         w1 = T_(p + "w1", [D, S.ff], data=L["w1"])
-        f = T_(p + "f", [rows, S.ff], exp=F_Q88)
+        # FFN1's output, the bias and the GELU run in the element type itself (Q8.8: no annotation)
+        f = T_(p + "f", [rows, S.ff])
         nodes.append(MatmulNode([x2, w1], f))
         b1 = T_(p + "b1", [S.ff], data=L["b1"])
-        a = T_(p + "a", [rows, S.ff], exp=F_Q88)
+        a = T_(p + "a", [rows, S.ff])
         nodes.append(ScheduledNode([f, b1], a, units.OP_ADD, act=units.ACT_GELU))
         w2 = T_(p + "w2", [S.ff, D], data=L["w2"])
         dd = T_(p + "dd", [rows, D], exp=e["dd"])

@@ -150,6 +150,72 @@ class Simulator:
                 raise SchedulerError(f"_forward_pass: unsupported node {type(sn).__name__}")
         return raw
 
+    # ------------------------------------------------------------------ expected outputs on disk
+    def _build_ramp_inputs(self) -> Dict[str, np.ndarray]:
+        """The inputs the reference's generated test writes into the buffers (_simulate.py:423-504):
+        an exponent tensor the ramp p[i] = (int16) i at its exponent(s); an integer tensor (ids)
+        i % R with R the smallest embedding table that reads it (else 2); a float32 host tensor
+        (i % 17 - 8) / 4; a host integer i % 2; a Q8.8 tensor the ramp at 2^-8."""
+        out = {}
+        dt = self._dtype
+        readers = {}
+        for sn in self._graph.nodes:
+            if isinstance(sn, LlmEmbedNode):
+                name = sn.inputs[0].onnx_name
+                readers[name] = min(readers.get(name, sn.rows), sn.rows)
+        for t in self._graph.input_tensors:
+            idx = np.arange(t.numel, dtype=np.int64)
+            if t.kind == "f32":
+                v = ((idx % 17) - 8).astype(np.float64) * 0.25
+            elif t.kind == "host" or (t.kind == "i32" and t.onnx_name in readers):
+                v = (idx % max(1, min(readers.get(t.onnx_name, 2), 32767))).astype(np.float64)
+            elif t.exp is not None:
+                e = np.broadcast_to(np.asarray(t.exp, np.float64).reshape(-1), (t.shape[-1],) if len(t.shape) else (1,))
+                v = dt.ramp_to_float_exp(idx, np.tile(e, t.numel // e.size))
+            else:
+                v = dt.ramp_to_float(idx)
+            out[t.onnx_name] = v.reshape(t.shape)
+        return out
+
+    def _simulate(self) -> Dict[str, np.ndarray]:
+        """The forward pass with the ramp inputs (_simulate.py:506-525)."""
+        return self._forward_pass(self._build_ramp_inputs())
+
+    def _expected_storage(self, name: str, logical: np.ndarray) -> np.ndarray:
+        """A tensor's values as the buffer lanes the board writes (_simulate.py:841-891): float32
+        for a float32 tensor, int32 for the int32 residual, else the uint16 storage at the
+        tensor's exponent(s) (integer tensors: their raw integers); contiguous (this simulator
+        keeps no broadcast strides)."""
+        t = self._tensor(name)
+        flat = np.asarray(logical, np.float64).reshape(-1)
+        if t.kind == "f32":
+            return flat.astype(np.float32)
+        if t.kind == "i32":
+            e = np.asarray(0 if t.exp is None else t.exp, np.float64).reshape(-1)
+            e = np.tile(e, flat.size // e.size) if e.size > 1 else e
+            return np.clip(np.rint(flat * np.power(2.0, e)), -2 ** 31, 2 ** 31 - 1).astype(np.int32)
+        if t.kind == "host":
+            return flat.astype(np.int32)
+        if t.exp is not None:
+            e = np.asarray(t.exp, np.float64).reshape(-1)
+            e = np.tile(e, flat.size // e.size) if e.size > 1 else e
+            return self._dtype.exp_to_storage(flat, e)
+        return self._dtype.float_to_storage(flat)
+
+    def _emit_expected_c(self, c_name: str, storage_buf: np.ndarray) -> str:
+        """``static const uint16_t expected_<c_name>[N]`` eight literals a row (_simulate.py:893-915)."""
+        buf = np.asarray(storage_buf).reshape(-1)
+        rows = ["    " + ", ".join(self._dtype.format_literal(v) for v in buf[i:i + 8]) for i in range(0, len(buf), 8)]
+        inner = ",\n".join(rows)
+        return f"static const uint16_t expected_{c_name}[{len(buf)}] = {{\n{inner}\n}};\n"
+
+    def generate_expected_dat(self, tensor: TensorInfo) -> bytes:
+        """The little-endian bytes of expected/<name>.dat: the tensor's ramp-input simulation as
+        the storage lanes (_simulate.py:950-964)."""
+        sim = self._simulate()
+        buf = self._expected_storage(tensor.onnx_name, sim[tensor.onnx_name])
+        return buf.astype(buf.dtype.newbyteorder("<")).tobytes()
+
     # ------------------------------------------------------------------ conversions
     def _tensor(self, name: str) -> TensorInfo:
         return self._infos[name]
@@ -274,7 +340,10 @@ class Simulator:
         if img is None:
             img = torch.from_numpy(sn.image()).to(self.device)
             self._images[key] = img
-        ids = self._get(sn.inputs[0], raw).reshape(-1).contiguous()
+        ids = self._get(sn.inputs[0], raw)
+        if not isinstance(ids, torch.Tensor):                 # host ids (an i32 host tensor)
+            ids = torch.from_numpy(np.asarray(ids, np.int64).reshape(-1).astype(np.int32)).to(self.device)
+        ids = ids.reshape(-1).contiguous()
         out = self._new(sn.output)
         units.embed_rows(img, ids, out, sn.rows, sn.d)
         return out

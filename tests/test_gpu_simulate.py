@@ -59,3 +59,23 @@ def test_vectorop_broadcast_bias_unaligned(torch_gpu):
         g = G.Graph([G.ScheduledNode([x, b], y, G.OP_ADD, act=1)], [x], [y])
         inputs = {"x": np.round(rng.uniform(-2, 2, (rows, n)) * 256) / 256}
         np.testing.assert_array_equal(Simulator(g).simulate(inputs)["y"], oracle_graph.forward(g, inputs)["y"])
+
+
+def test_expected_dat_of_the_small_cnn():
+    """generate_expected_dat: the ramp-input simulation's output as the little-endian storage
+    lanes, decoded back equal to the oracle's forward over the same ramp inputs."""
+    import numpy as np
+    from cormorant_amd import models
+    from cormorant_amd.dtype import AP_FIXED_16_8
+    from cormorant_amd.simulate import Simulator
+    from oracle import graph_sim
+    g, _ = models.small_cnn(0)
+    sim = Simulator(g)
+    ramp = sim._build_ramp_inputs()
+    assert ramp["input"].reshape(-1)[5] == 5 / 256
+    out = g.output_tensors[0]
+    dat = sim.generate_expected_dat(out)
+    got = np.frombuffer(dat, "<u2").view(np.int16) / 256.0
+    want = graph_sim.forward(g, ramp)[out.onnx_name].reshape(-1)
+    np.testing.assert_array_equal(got, want)
+    assert dat == AP_FIXED_16_8.dat_bytes(want)

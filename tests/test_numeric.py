@@ -117,3 +117,89 @@ def test_attn_keys_known_answers():
     assert attn_keys(3, 20, 8, 64, 16) == (8, 16)          # n clamped to T
     assert attn_keys(0, 0, 8, 64, 16) == (0, 16)           # at least one quantum
     assert attn_keys(5, -3, 8, 64, 16) == (0, 16)
+
+
+# ---------------------------------------------------------------- annotations, checks, fusion
+def test_annotations_parse_apply_round_trip():
+    from cormorant_amd.dtype import AP_FIXED_16_8
+    from cormorant_amd.graph import TensorInfo as T
+    from cormorant_amd.numeric import apply, empty, is_active, parse, to_metadata
+    meta = parse('{"version": 1, "exp": {"q": 11, "k": [9, 10, 11, 12]}, "host": {"h": "f32", "pos": "i32"}, '
+                 '"state": ["kc"], "layout": {"kc": [2, 8]}, "dma": {"r": "i32"}, "engine": {"q": "conv"}}')
+    assert is_active(meta) and not is_active(empty())
+    assert parse(to_metadata(meta)) == meta
+    ts = {n: T(n, s) for n, s in (("q", [4, 16]), ("k", [2, 4]), ("h", [1, 16]), ("pos", [1]), ("kc", [32, 16]),
+                                 ("r", [4, 16]))}
+    apply(ts, meta, AP_FIXED_16_8)
+    assert ts["q"].exp == 11 and list(ts["k"].exp) == [9, 10, 11, 12]
+    assert ts["h"].kind == "f32" and ts["h"].host == "f32" and ts["pos"].kind == "host"
+    assert ts["kc"].state and ts["kc"].group_layout == (2, 8) and ts["r"].kind == "i32"
+
+
+@pytest.mark.parametrize("meta,msg", [
+    ('{"host": {"q": "f64"}}', "kind"),
+    ('{"exp": {"q": [1, 2]}}', "last axis"),
+    ('{"exp": {"q": 50}}', "outside"),
+    ('{"host": {"q": "f32"}, "exp": {"q": 8}}', "host tensor"),
+    ('{"chexp": {"q": [8, 8, 8, 8]}}', "4-D"),
+    ('{"layout": {"q": [2, 8]}}', "2-D state"),
+    ('{"exp": {"nope": 8}}', "no tensor"),
+    ('{"bogus": 1}', "not known"),
+])
+def test_annotation_errors(meta, msg):
+    from cormorant_amd.dtype import AP_FIXED_16_8
+    from cormorant_amd.graph import TensorInfo as T
+    from cormorant_amd.numeric import NumericError, apply, parse
+    with pytest.raises(NumericError, match=msg):
+        apply({"q": T("q", [4, 16])}, parse(meta), AP_FIXED_16_8)
+
+
+def test_check_accepts_the_workload_graphs_and_refuses_misplaced_numerics():
+    from cormorant_amd import models, units
+    from cormorant_amd.dtype import AP_FIXED_16_8
+    from cormorant_amd.graph import ConvNode, ScheduledNode, TensorInfo as T
+    from cormorant_amd.numeric import NumericError, check
+    g, _, _ = models.bert_encoder(models.BertShape(layers=1, batch=1, seq=64, d=64, heads=1, ff=128, vocab=50))
+    check(g.nodes, AP_FIXED_16_8)
+    g, _, _ = models.smollm2_decode(models.LlamaShape(layers=1, batch=2, d=64, heads=4, kv=2, hd=16, ff=128,
+                                                      vocab=64, ctx=32), runtime_pos=True)
+    check(g.nodes, AP_FIXED_16_8)
+    check(models.small_cnn(0)[0].nodes, AP_FIXED_16_8)
+    with pytest.raises(NumericError, match="power-of-two"):
+        check([ScheduledNode([T("a", [8], exp=10), T("b", [8], exp=10)], T("c", [8], exp=10), units.OP_ADD)],
+              AP_FIXED_16_8)
+    with pytest.raises(NumericError, match="states"):
+        check([ScheduledNode([T("a", [8], state=True)], T("c", [8]), units.OP_RELU)], AP_FIXED_16_8)
+    with pytest.raises(NumericError, match="derived"):
+        check([ConvNode([T("x", [1, 1, 4, 4], exp=10), T("w", [1, 1, 1, 1], exp=3, data=np.ones((1, 1, 1, 1)))],
+                        T("y", [1, 1, 4, 4], exp=10))], AP_FIXED_16_8)
+
+
+def test_fuse_activations_rules():
+    from cormorant_amd import units
+    from cormorant_amd.graph import Graph, MatmulNode, ScheduledNode, TensorInfo as T, fuse_activations
+    a, b = T("a", [16]), T("b", [16])
+    s, r = T("s", [16]), T("r", [16])
+    m, g_ = T("m", [16]), T("g", [16])
+    x, out2 = T("x", [16]), T("o2", [16])
+    w = T("w", [16, 16], data=np.zeros((16, 16)))
+    mm, mr = T("mm", [1, 16]), T("mr", [1, 16])
+    nodes = [ScheduledNode([a, b], s, units.OP_ADD), ScheduledNode([s], r, units.OP_RELU),       # fused
+             ScheduledNode([a, b], m, units.OP_MUL), ScheduledNode([m], g_, units.OP_GELU),       # fused
+             ScheduledNode([a, b], x, units.OP_SUB), ScheduledNode([x], out2, units.OP_RELU6),   # x is read twice
+             ScheduledNode([x, x], T("x2", [16]), units.OP_ADD),
+             MatmulNode([T("a2", [1, 16]), w], mm), ScheduledNode([mm], mr, units.OP_RELU)]       # not a VectorOP
+    g = Graph(nodes, input_tensors=[a, b], output_tensors=[r, g_, out2, mr])
+    assert fuse_activations(g) == 2
+    assert [type(n).__name__ for n in g.nodes].count("ScheduledNode") == 6
+    assert g.nodes[0].output is r and g.nodes[0].act == units.ACT_RELU
+    assert g.nodes[1].output is g_ and g.nodes[1].act == units.ACT_GELU
+
+
+def test_engine_pins_lower_matmuls_to_the_conv_unit():
+    from cormorant_amd.graph import MatmulConvNode, MatmulNode, TensorInfo as T
+    from cormorant_amd.numeric import lower_engines, parse
+    nodes = [MatmulNode([T("a", [16, 64]), T("b", [64, 40], data=np.zeros((64, 40)))], T("c", [16, 40])),
+             MatmulNode([T("a", [16, 64]), T("b2", [64, 40], data=np.zeros((64, 40)))], T("d", [16, 40]))]
+    assert lower_engines(nodes, parse('{"engine": {"c": "conv", "d": "matmul"}}')) == 1
+    assert isinstance(nodes[0], MatmulConvNode) and isinstance(nodes[1], MatmulNode)
