@@ -11,6 +11,7 @@ from cormorant_amd.graph import ConvNode, Graph, LlmAttnConvNode, MatmulNode, Te
 from cormorant_amd.numeric import encode_conv_weights, encode_matmul_weights
 from cormorant_amd.simulate import Simulator
 from oracle import graph_sim as oracle_graph
+from oracle.attn_prep import clamp_n
 
 pytestmark = pytest.mark.gpu
 
@@ -88,7 +89,7 @@ def test_attention_contractions(pos, n):
               "qx": rng.integers(-32768, 32768, (KV, HD, G * T)).astype(np.float64),
               "pos": np.array([pos]), "n": np.array([n]), **prob_inputs}
     got = check(g, inputs)
-    keys = oracle_graph.G.attn_keys(pos, n, T, C)[1]
+    keys = clamp_n(pos, n, T, C)[1]
     assert (got["s0"][keys:] == 0).all()
 
 

@@ -1,5 +1,5 @@
 """Graph-level parity: cormorant_amd.simulate.Simulator (every node on the HIP units) against
-the value-domain restatement of the reference's _forward_pass (tests/oracle_graph.py)."""
+the value-domain restatement of the reference's _forward_pass (oracle/graph_sim.py)."""
 import numpy as np
 import pytest
 
