@@ -20,7 +20,7 @@ from typing import List, Optional
 
 import numpy as np
 
-from .graph import SchedulerError, TensorInfo
+from .graph import KernelNode, SchedulerError, TensorInfo
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 HOST_LIB_PATH = os.path.join(HERE, "libcormo_host.so")
@@ -303,7 +303,7 @@ class LlmAttentionNode(HostNode):
 
 # ---------------------------------------------------------------- the embedding (on the GPU)
 @dataclass
-class LlmEmbedNode:
+class LlmEmbedNode(KernelNode):
     """h[t] = table[clamp(ids[t], 0, rows - 1)] (llm_nodes.py:466-570): ids an int32 tensor, the
     table float32 [rows][d]; the output the int32 residual (kind "i32": each row's values rounded
     half to even at the residual's exponent and saturated, _res32 :297-303) or float32 rows

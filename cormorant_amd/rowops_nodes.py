@@ -18,7 +18,7 @@ from typing import List, Optional, Sequence
 
 import numpy as np
 
-from .graph import SchedulerError, TensorInfo, attn_keys
+from .graph import KernelNode, SchedulerError, TensorInfo, attn_keys
 from .units import (F_B_EN, F_NORM_LN, F_P_BCAST, F_RELU, RO_ADDX, RO_COPY, RO_DEQUANT, RO_MULACT,
                     RO_NORM, RO_ROPE, RO_XPOSE)
 
@@ -204,7 +204,7 @@ def _require(cond, what: str, msg: str):
         raise SchedulerError(f"{what}: {msg}")
 
 
-class RowOpsAdapter:
+class RowOpsAdapter(KernelNode):
     """Base of the adapters: ``inputs`` / ``output`` tensors and ``jobs()``."""
     inputs: List[TensorInfo]
     output: TensorInfo
@@ -570,7 +570,7 @@ class RoCall:
     win_hi: int = NO_WINDOW
 
 
-class RoCallNode:
+class RoCallNode(KernelNode):
     """Base of the nodes that lower to explicit unit calls over named buffers: ``staging()``
     the node's own buffers {key: bytes} (zero at creation, kept from call to call like the
     reference's DMA states), ``tables()`` constant buffers {key: raw lanes}, ``calls(host)``

@@ -23,6 +23,43 @@ from .packing import conv_bias_image, conv_lowered_b_image, conv_weight_image, p
 from .host_ops import HostNode, LlmEmbedNode
 from .rowops_nodes import RoCallNode, RoJob, RowOpsAdapter
 
+def node_reference(node, ins, dtype: Optional[ApFixed16] = None, device: str = "cuda",
+                   host: Optional[Dict[str, np.ndarray]] = None) -> np.ndarray:
+    """The output values of ``node`` alone for the input values ``ins`` (one per node input,
+    in order), computed by the HIP units: a one-node graph through ``Simulator._forward_pass``.
+    The per-node form of the reference's ``reference(ins, dtype)`` (_simulate.py:667-690).  A
+    constant input (a tensor with ``data`` that is not a state) reads its own data, as in the
+    graph; a state input whose value is a float64 array is updated in place (the node's write
+    into the persistent state), any other value seeds the state.  ``host`` holds the values of
+    runtime host tensors the node reads outside its inputs (``pos_t``, ``mask_t``)."""
+    if len(ins) != len(node.inputs):
+        raise ValueError(f"{type(node).__name__}.reference: {len(ins)} values for {len(node.inputs)} inputs")
+    feeds: Dict[str, np.ndarray] = {}
+    states: Dict[str, np.ndarray] = {}
+    graph_in = []
+    for t, v in zip(node.inputs, ins):
+        if t is None or t.onnx_name in feeds or t.onnx_name in states or (t.data is not None and not t.state):
+            continue
+        if v is None:
+            raise ValueError(f"{type(node).__name__}.reference: no value for input '{t.onnx_name}'")
+        if t.state and isinstance(v, np.ndarray) and v.dtype == np.float64 and v.size == t.numel:
+            states[t.onnx_name] = v              # updated in place, as the graph's state
+        else:
+            feeds[t.onnx_name] = np.asarray(v)
+        graph_in.append(t)
+    for field_name, t in vars(node).items():      # runtime host tensors outside the inputs
+        if isinstance(t, TensorInfo) and t.kind == "host" and t is not node.output and t.onnx_name not in feeds:
+            if host is None or t.onnx_name not in host:
+                raise ValueError(f"{type(node).__name__}.reference: the runtime tensor '{t.onnx_name}' "
+                                 f"({field_name}) needs its value in host")
+            feeds[t.onnx_name] = np.asarray(host[t.onnx_name])
+            graph_in.append(t)
+    g = Graph(nodes=[node], input_tensors=graph_in, output_tensors=[node.output])
+    out = node.output.onnx_name
+    sim = Simulator(g, dtype or AP_FIXED_16_8, device)
+    return sim._forward_pass(feeds, states={**sim.initial_states(), **states}, keep=[out])[out]
+
+
 _TORCH = {"i16": torch.int16, "i32": torch.int32, "f32": torch.float32}
 _NP = {"i16": np.int16, "i32": np.int32, "f32": np.float32}
 _KB = {"i16": 2, "i32": 4, "f32": 4}
