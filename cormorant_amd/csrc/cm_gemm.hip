@@ -468,6 +468,10 @@ __global__ __launch_bounds__(256) void split_fold_lds_kernel(const int16_t* __re
 // the raw per-row bias (added to the sum as bias << 8), the offset of column `j` from a row
 // start, and whether every row start and the column count are even (then two adjacent
 // results go out as one 4-byte store).
+struct TileBase {               // a tile's first output element and row stride (nullptr: none)
+    int16_t* base;
+    uint32_t ld;
+};
 struct EpiMatmul {              // C[bt][i][j] = c + off(bt) + i * ldc + j
     int16_t* c;
     uint64_t c_bs;
@@ -482,6 +486,14 @@ struct EpiMatmul {              // C[bt][i][j] = c + off(bt) + i * ldc + j
         return c + off + (uint64_t)i * (ldc ? ldc : cols);
     }
     __device__ uint64_t col_off(uint32_t j) const { return j; }
+    // The tile (row0, col0) of tm x tn wholly inside C with paired stores: its first element
+    // and the row stride, so that element (r, c) of the tile sits at base + r * ld + c.
+    __device__ __forceinline__ TileBase tile_base(uint32_t bt, uint32_t row0, uint32_t col0, uint32_t tm,
+                                                  uint32_t tn) const {
+        const uint64_t l = ldc ? ldc : cols;
+        if (!pairs || row0 + tm > rows || col0 + tn > cols || l * tm >= (1ull << 30)) return TileBase{nullptr, 0};
+        return TileBase{row_ptr(bt, row0) + col0, (uint32_t)l};
+    }
 };
 struct EpiConv {                // y pattern (ConvKernel.h:250-258); acc seeded with bias << 8
     int16_t* y;
@@ -499,6 +511,12 @@ struct EpiConv {                // y pattern (ConvKernel.h:250-258); acc seeded 
         if (!fold) return j;
         const uint32_t im = j / fold;
         return (uint64_t)im * img + (j - im * fold);
+    }
+    __device__ __forceinline__ TileBase tile_base(uint32_t bt, uint32_t row0, uint32_t col0, uint32_t tm,
+                                                  uint32_t tn) const {
+        if (!pairs || fold || cn || row0 + tm > rows || col0 + tn > cols || (uint64_t)cs * tm >= (1ull << 30))
+            return TileBase{nullptr, 0};
+        return TileBase{row_ptr(bt, row0) + col0, cs};
     }
 };
 
@@ -578,6 +596,39 @@ __device__ __forceinline__ void store_wave_tile(const v16i (&hh)[2][2], const v1
                 }
                 // one row pair at a time: hoisting the term loads of later pairs would
                 // need more registers than the accumulators leave
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+}
+
+// store_wave_tile for a tile wholly inside the output with plain rows (tile_base): the lane's
+// offset from the tile's first element in 32 bits, the row offsets uniform, no bounds checks.
+template <uint32_t MODE>
+__device__ __forceinline__ void store_wave_fast(const v16i (&hh)[2][2], const v16i (&mid)[2][2],
+                                                const v16i (&ll)[2][2], const int2* rterm, const int2* cterm,
+                                                int16_t* __restrict__ base, uint32_t ld, uint32_t wr, uint32_t wc,
+                                                uint32_t l32, uint32_t lh) {
+    const uint32_t odd = l32 & 1;
+    const uint32_t lane_off = (wr * 64 + 4 * lh + odd) * ld + wc * 64 + l32 - odd;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int2 ct = cterm[wc * 64 + j * 32 + l32];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const uint32_t rl = wr * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                const int2 r0 = rterm[rl], r1 = rterm[rl + 1];
+                const int32_t q0 = recombine<MODE>(hh[i][j][r], mid[i][j][r], ll[i][j][r], r0.x + ct.x, r0.y + ct.y);
+                const int32_t q1 = recombine<MODE>(hh[i][j][r + 1], mid[i][j][r + 1], ll[i][j][r + 1], r1.x + ct.x,
+                                                   r1.y + ct.y);
+                // the pair exchange of store_wave_tile: the even lane stores row r, the odd lane row r + 1
+                const int32_t give = odd ? q0 : q1;
+                const int32_t got = __builtin_amdgcn_mov_dpp(give, 0xB1, 0xF, 0xF, false);
+                const uint32_t lo = (uint32_t)(odd ? got : q0), hi = (uint32_t)(odd ? q1 : got);
+                const uint32_t roff = (uint32_t)(i * 32 + 8 * (r >> 2) + (r & 3)) * ld + j * 32;
+                *reinterpret_cast<uint32_t*>(base + lane_off + roff) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -883,7 +934,12 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
     // ---- epilogue: one uniform dispatch to the store routine of this mode
     const uint32_t row0 = tr * TM, col0 = tc * BN;
 #define CM_STORE(M, P) store_wave_tile<M, P>(hh, mid, ll, rterm, cterm, bt, row0, col0, wr, wc, l32, lh, epi)
-    if (mode == kPartial) {
+    const TileBase tb = mode != kPartial ? epi.tile_base(bt, row0, col0, TM, BN) : TileBase{nullptr, 0};
+    if (tb.base != nullptr) {           // a whole tile: the lean store
+        if (mode == kWrap) store_wave_fast<kWrap>(hh, mid, ll, rterm, cterm, tb.base, tb.ld, wr, wc, l32, lh);
+        else if (mode == kSatNarrow) store_wave_fast<kSatNarrow>(hh, mid, ll, rterm, cterm, tb.base, tb.ld, wr, wc, l32, lh);
+        else store_wave_fast<kSatWide>(hh, mid, ll, rterm, cterm, tb.base, tb.ld, wr, wc, l32, lh);
+    } else if (mode == kPartial) {
         store_wave_partial(hh, mid, ll, pout + ((uint64_t)bt * gridDim.z + kz) * epi.rows * epi.cols, epi.rows,
                            epi.cols, row0, col0, wr, wc, l32, lh);
     } else if (mode == kSatNarrow) {
