@@ -210,6 +210,7 @@ GRAPH_KERNELS = ("gemm_planes_kernel", "split_rows_kernel", "split_cols_kernel",
                  "conv_dw3_kernel", "conv_dw3v_kernel", "pool_kernel", "pool_global_kernel", "pool2x2_kernel",
                  "softmax_long_kernel", "smx_etab_kernel", "copy_elems_kernel", "permute_elems_kernel",
                  "split_fold_kernel", "split_fold_lds_kernel", "skinny_wrap_kernel", "skinny_reduce_kernel",
+                 "skinny_planes_kernel", "decode_attn_kernel",
                  "gemm_reduce_kernel", "attention_kernel", "embed_rows_kernel")
 
 
@@ -405,11 +406,10 @@ def smollm2_bench(args, torch, np):
     macs = shape.macs()
     kv_bytes = shape.layers * 2 * shape.batch * shape.kv * shape.ctx * shape.hd * 2
     step_bytes = shape.weight_bytes() + kv_bytes
-    # the skinny products read every weight and both caches once (q.K^T the K rows, P.V the V
-    # rows); their time is the product launches plus the reduces that finish them
-    sk_bytes = step_bytes
-    sk_ms = sum(per_kernel.get(k, {}).get("ms", 0.0) for k in ("skinny_wrap_kernel", "skinny_reduce_kernel"))
-    sk_ms = sk_ms or float("nan")
+    # the linears (7 per layer and the tied head) run as skinny_planes_kernel launches that read
+    # every weight's byte planes once: 2 bytes per weight, the column sums aside
+    sk_bytes = shape.weight_bytes()
+    sk_ms = per_kernel.get("skinny_planes_kernel", {}).get("ms", 0.0) or float("nan")
     result = {
         "metric": "bit-exact fixed-point tokens/s (SmolLM2-360M-shaped decode, batch 16, 1024-row KV cache)",
         "value": round(shape.batch / (ms * 1e-3), 1),
@@ -430,11 +430,10 @@ def smollm2_bench(args, torch, np):
         "roofline": {"bound": "hbm", "achieved": round(sk_bytes / (sk_ms * 1e-3) / 1e9, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(sk_bytes / (sk_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "skinny_wrap_kernel + skinny_reduce_kernel", "kernel_ms_per_step": sk_ms,
+                     "kernel": "skinny_planes_kernel", "kernel_ms_per_step": sk_ms,
                      "bytes_per_step": sk_bytes,
-                     "note": "the skinny products (the 7 linears of every layer, the tied head, q.K^T and P.V) "
-                             "and the reduces that finish them, against their algorithmic bytes: the int16 "
-                             "weights and the K and V caches once"},
+                     "note": "the linears (7 per layer and the tied head) against their algorithmic bytes: "
+                             "every int16 weight once (its two byte planes)"},
         "kernels_ms_per_step": per_kernel,
         "graph_build_s": round(build_s, 1),
     }

@@ -50,11 +50,14 @@ SIGNATURES = {
     "cm_copy16": (_I32, [_P, _P] + [_U32] * 4 + [ctypes.c_uint64] * 8 + [_P]),
     "cm_embed_rows": (_I32, [_P, _U32, _P, _P, _U32, _U32, _U32, _P]),
     "cm_attention": (_I32, [_P, _P] + [_U32] * 4 + [ctypes.c_uint64] + [_U32] * 3 + [ctypes.c_uint64] + [_U32] * 2 + [_P]),
+    "cm_decode_attention": (_I32, [_P, _P, _P, _P] + [_U32] * 7 + [_P]),
     "cm_matmul_b_planes_bytes": (ctypes.c_size_t, [_U32] * 3),
     "cm_matmul_split_b": (_I32, [_P, _P, _U32, _U32, _U32, ctypes.c_int64, _U32, _U32, _P]),
     "cm_matmul_planes": (_I32, [_P, _P, _P, _U32, _U32, _U32, _U32, ctypes.c_int64, _U32, ctypes.c_int64, _U32, _P]),
     "cm_matmul_strided": (_I32, [_P, _P, _P] + [_U32] * 5 + [ctypes.c_uint64] * 6 + [_U32] + [ctypes.c_uint64] * 3 + [_U32, _P]),
     "cm_matmul_skinny_multi": (_I32, [_P, _U32, _U32, _U32, _P, _P, _P, _U32, _P]),
+    "cm_matmul_skinny_planes": (_I32, [_P, _U32, _U32, _U32, _P, _P, _P, _P]),
+    "cm_matmul_skinny_planes_addx": (_I32, [_P, _U32, _U32, _P, _P, _U32, _P, _P, _U32, _U32, _P, _P]),
     "cm_timing_enable": (_I32, [_I32]),
     "cm_timing_read": (_I32, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                               ctypes.POINTER(ctypes.c_uint64)]),

@@ -19,6 +19,7 @@
 // per-1024-k partial row / column sums; the plane GEMM streams 64-k tiles of the four planes
 // into LDS with direct global -> LDS copies and sums the partials in its prologue.
 #include "cm_common.h"
+#include "cm_rowops_math.h"
 
 namespace cm {
 namespace {
@@ -1350,6 +1351,135 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(SkinnySegs segs, uin
     }
 }
 
+// ---------------------------------------------------------------- skinny products on split weights
+// C = sat16(wrap32(A . B) >> 8) for A of at most 16 rows against a weight already split into
+// byte planes (cm_matmul_split_b).  Sixteen rows are exactly one v_mfma_i32_16x16x64_i8
+// operand, so the products run on MFMA over limbs with the plane GEMM's recombination, and a
+// workgroup owns 32 columns for the whole k: its W wavefronts take the 64-k steps w, w + W, ..
+// (the loads of a chunk of kSpChunk steps all in flight before the chunk's products) and add
+// their wrapped partials in LDS, so there are no partial buffers and no second launch.  A is
+// split in registers, 16 k of row l % 16 per lane (the MFMA operand layout), its row sums
+// taken on the way; B's column sums come from the plane image.
+constexpr uint32_t kSpCols = 32;          // columns per workgroup: two 16-column MFMA blocks
+constexpr uint32_t kSpChunk = 4;          // 64-k steps whose loads a wavefront issues together
+constexpr uint32_t kSpMaxWaves = 8;
+
+struct SkinnyPlaneSegs {
+    const int8_t* hi[kSkinnySegs];
+    const int8_t* lo[kSkinnySegs];
+    const int32_t* part[kSkinnySegs];
+    int16_t* c[kSkinnySegs];
+    uint32_t m[kSkinnySegs], lines_p[kSkinnySegs], cb0[kSkinnySegs];
+    uint32_t count;
+};
+
+// A row-ops COPY / ADDX job applied to a one-product launch's output as it is stored: out[r][j]
+// = copy_addx(x[r][j], C[r][j]) with the job's op word (A kind, output kind, flags), its
+// parameter block and bq_sh (the residual add of a decode linear); out == nullptr: none.
+struct SkinnyAddx {
+    const uint8_t* x;
+    uint8_t* out;
+    const uint8_t* params;
+    uint32_t op, bq_sh;
+};
+
+__global__ __launch_bounds__(64 * kSpMaxWaves) void skinny_planes_kernel(const int16_t* __restrict__ a, uint32_t n,
+                                                                       uint32_t k, uint32_t kp, uint32_t nslab,
+                                                                       SkinnyPlaneSegs segs, SkinnyAddx ax) {
+    __shared__ uint32_t red[kSpMaxWaves][16][kSpCols];
+    __shared__ int32_t rsum[kSpMaxWaves][16];
+    uint32_t si = 0;
+    for (uint32_t i = 1; i < segs.count; i++)
+        if (blockIdx.x >= segs.cb0[i]) si = i;
+    const uint32_t c0 = (blockIdx.x - segs.cb0[si]) * kSpCols;
+    const int8_t* __restrict__ bhi = segs.hi[si];
+    const int8_t* __restrict__ blo = segs.lo[si];
+    const uint32_t W = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t r = lane & 15, g = lane >> 4;             // A row and B column of a block; k group
+    const uint32_t nsteps = kp / 64;
+    const bool row_ok = r < n;
+    const int16_t* arow = a + (uint64_t)(row_ok ? r : 0) * k;
+    const int4 pad8 = make_int4(0x00800080, 0x00800080, 0x00800080, 0x00800080);   // eight kPad: A' = 0
+    v4i hh[2], mid[2], ll[2];
+#pragma unroll
+    for (int b = 0; b < 2; b++) hh[b] = mid[b] = ll[b] = v4i{0, 0, 0, 0};
+    int32_t asum = 0;
+    for (uint32_t s0 = wave; s0 < nsteps; s0 += W * kSpChunk) {
+        int4 av[kSpChunk][2];
+        v4i bh[kSpChunk][2], bl[kSpChunk][2];
+#pragma unroll
+        for (uint32_t u = 0; u < kSpChunk; u++) {
+            const uint32_t st = s0 + u * W;
+            const bool live = st < nsteps;
+            const uint32_t kk = (live ? st : 0) * 64 + 16 * g;
+            // k % 8 == 0: each half of the lane's 16 k is wholly real or wholly past k
+            av[u][0] = (live && row_ok && kk + 8 <= k) ? *reinterpret_cast<const int4*>(arow + kk) : pad8;
+            av[u][1] = (live && row_ok && kk + 16 <= k) ? *reinterpret_cast<const int4*>(arow + kk + 8) : pad8;
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                const uint64_t off = (uint64_t)(c0 + 16 * b + r) * kp + kk;
+                bh[u][b] = *reinterpret_cast<const v4i*>(bhi + off);
+                bl[u][b] = *reinterpret_cast<const v4i*>(blo + off);
+            }
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kSpChunk; u++) {
+            if (s0 + u * W >= nsteps) break;                  // wave-uniform
+            const uint32_t kk = (s0 + u * W) * 64 + 16 * g;
+            if (row_ok && kk + 8 <= k) asum += sum8(av[u][0]);
+            if (row_ok && kk + 16 <= k) asum += sum8(av[u][1]);
+            uint2 h0, l0, h1, l1;
+            split8(av[u][0], h0, l0);
+            split8(av[u][1], h1, l1);
+            const v4i ah{(int)h0.x, (int)h0.y, (int)h1.x, (int)h1.y}, al{(int)l0.x, (int)l0.y, (int)l1.x, (int)l1.y};
+#pragma unroll
+            for (int b = 0; b < 2; b++) hh[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bh[u][b], hh[b], 0, 0, 0);
+#pragma unroll
+            for (int b = 0; b < 2; b++) mid[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bl[u][b], mid[b], 0, 0, 0);
+#pragma unroll
+            for (int b = 0; b < 2; b++) ll[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bl[u][b], ll[b], 0, 0, 0);
+#pragma unroll
+            for (int b = 0; b < 2; b++) mid[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bh[u][b], mid[b], 0, 0, 0);
+        }
+    }
+    // this wavefront's wrapped partials: lane l holds column l % 16 of each block, rows 4 g .. + 3
+#pragma unroll
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            red[wave][4 * g + i][16 * b + r] =
+                ((uint32_t)hh[b][i] << 16) + ((uint32_t)mid[b][i] << 8) + (uint32_t)ll[b][i];
+    asum += __shfl_xor(asum, 16, 64);
+    asum += __shfl_xor(asum, 32, 64);
+    if (g == 0) rsum[wave][r] = asum;
+    __syncthreads();
+    const uint32_t m = segs.m[si], lp = segs.lines_p[si];
+    const int32_t* __restrict__ part = segs.part[si];
+    int16_t* __restrict__ c = segs.c[si];
+    for (uint32_t e = threadIdx.x; e < 16 * kSpCols; e += blockDim.x) {
+        const uint32_t row = e / kSpCols, col = c0 + (e - row * kSpCols);
+        if (row >= n || col >= m) continue;
+        uint32_t acc = 0u - 16384u * k, rs = 0, cs = 0;
+        for (uint32_t w = 0; w < W; w++) {
+            acc += red[w][row][col - c0];
+            rs += (uint32_t)rsum[w][row];
+        }
+        for (uint32_t sl = 0; sl < nslab; sl++) cs += (uint32_t)part[(uint64_t)sl * lp + col];
+        acc += 128u * rs + 128u * cs;
+        const int16_t y = (int16_t)min(max((int32_t)acc >> 8, -32768), 32767);
+        c[(uint64_t)row * m + col] = y;
+        if (ax.out != nullptr) {
+            const uint32_t ak = (ax.op >> 4) & 3, ck = (ax.op >> 8) & 3;
+            const uint64_t e = (uint64_t)row * m + col;
+            const ro::i64 x = ro::ld_kind(ax.x + e * (ak == 0 ? 2 : 4), ak);
+            const ro::i64 r = ro::copy_addx(x, y, ro::ld_param(ax.params, col, (ax.op & ro::F_P_BCAST) != 0), ax.op,
+                                            ax.bq_sh, ck);
+            if (ck == 0) reinterpret_cast<int16_t*>(ax.out)[e] = (int16_t)r;
+            else reinterpret_cast<int32_t*>(ax.out)[e] = (int32_t)r;
+        }
+    }
+}
+
 // ---------------------------------------------------------------- drivers
 // Byte planes [slices][lines_p][kp] of one operand and its partial line sums
 // [slices][nslab][lines_p].
@@ -1992,4 +2122,77 @@ extern "C" int cm_matmul_skinny_multi(const int16_t* a, uint32_t n, uint32_t k, 
             return fail(CM_EALIGN, "matmul: product %u: b / c not aligned", i);
     }
     return skinny_run(a, n, k, 1, 0, 0, 0, count, b, c, m, b_packed, st, as_stream(stream));
+}
+
+namespace cm {
+namespace {
+
+int skinny_planes(const int16_t* a, uint32_t n, uint32_t k, uint32_t count, const void* const* b_planes,
+                  int16_t* const* c, const uint32_t* m, const SkinnyAddx& ax, hipStream_t s) {
+    if (count == 0 || count > kSkinnySegs) return fail(CM_EINVAL, "matmul: %u products (1 .. %u)", count, kSkinnySegs);
+    if (n == 0) return CM_OK;
+    if (n > 16 || k == 0 || k > 32768 || (k & 7))
+        return fail(CM_EINVAL, "matmul: skinny plane products take n <= 16 and k a multiple of 8 up to 32768");
+    if (!aligned16(a)) return fail(CM_EALIGN, "matmul: a not 16-byte aligned");
+    const uint32_t kp = (uint32_t)round_up(k, BK);
+    SkinnyPlaneSegs segs{};
+    segs.count = count;
+    uint64_t cbs = 0;
+    uint32_t nslab = 0;
+    for (uint32_t i = 0; i < count; i++) {
+        if (m[i] == 0) return fail(CM_EINVAL, "matmul: product %u: m = 0", i);
+        if (reinterpret_cast<uintptr_t>(b_planes[i]) & 255)
+            return fail(CM_EALIGN, "matmul: product %u: b planes not 256-byte aligned", i);
+        Planes B = make_planes(m[i], kp, 1);
+        char* q = static_cast<char*>(const_cast<void*>(b_planes[i]));
+        B.carve(q);
+        segs.hi[i] = B.hi;
+        segs.lo[i] = B.lo;
+        segs.part[i] = B.part;
+        segs.c[i] = c[i];
+        segs.m[i] = m[i];
+        segs.lines_p[i] = B.lines_p;
+        segs.cb0[i] = (uint32_t)cbs;
+        nslab = B.nslab;
+        cbs += ceil_div(m[i], kSpCols);
+    }
+    if (cbs > 0x7FFFFFFFull) return fail(CM_EINVAL, "matmul: %llu column blocks", (unsigned long long)cbs);
+    const uint32_t waves = std::min<uint32_t>(kSpMaxWaves, std::max<uint32_t>(1, ceil_div(kp / 64, kSpChunk)));
+    CM_LAUNCH("skinny_planes_kernel", skinny_planes_kernel, dim3((uint32_t)cbs), dim3(64 * waves), 0, s, a, n, k, kp,
+              nslab, segs, ax);
+    return CM_OK;
+}
+
+}  // namespace
+}  // namespace cm
+
+extern "C" int cm_matmul_skinny_planes(const int16_t* a, uint32_t n, uint32_t k, uint32_t count,
+                                       const void* const* b_planes, int16_t* const* c, const uint32_t* m,
+                                       void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    return skinny_planes(a, n, k, count, b_planes, c, m, SkinnyAddx{}, as_stream(stream));
+}
+
+extern "C" int cm_matmul_skinny_planes_addx(const int16_t* a, uint32_t n, uint32_t k, const void* b_planes,
+                                            int16_t* c, uint32_t m, const void* x, const void* params, uint32_t op,
+                                            uint32_t bq_sh, void* out, void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    const uint32_t code = op & 15, ak = (op >> 4) & 3, bk = (op >> 6) & 3, ck = (op >> 8) & 3;
+    if ((code != ro::RO_COPY && code != ro::RO_ADDX) || !(op & ro::F_B_EN) || (op & ro::F_P_KEEP) || ak > 1 ||
+        bk != 0 || ck > 1 || bq_sh > 63)
+        return fail(CM_EINVAL, "matmul: the output job must be a COPY / ADDX with B the int16 product (op 0x%x)", op);
+    if (x == nullptr || out == nullptr || params == nullptr)
+        return fail(CM_EINVAL, "matmul: the output job needs x, out and a parameter block");
+    if ((reinterpret_cast<uintptr_t>(x) & (ak ? 3 : 1)) || (reinterpret_cast<uintptr_t>(out) & (ck ? 3 : 1)) ||
+        (reinterpret_cast<uintptr_t>(params) & 15))
+        return fail(CM_EALIGN, "matmul: the output job's operands are not aligned");
+    const SkinnyAddx ax{static_cast<const uint8_t*>(x), static_cast<uint8_t*>(out), static_cast<const uint8_t*>(params),
+                        op, bq_sh};
+    return skinny_planes(a, n, k, 1, &b_planes, &c, &m, ax, as_stream(stream));
 }

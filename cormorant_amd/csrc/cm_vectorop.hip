@@ -152,6 +152,17 @@ __device__ __forceinline__ uint32_t row16_sum(uint32_t x) {
     return x;
 }
 
+// Sum over aligned groups of N consecutive lanes (N = 4, 8 or 16, within a DPP row); every lane
+// of a group gets the group's sum.
+template <uint32_t N>
+__device__ __forceinline__ int group_sum(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);          // quad_perm [1,0,3,2]
+    x += __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);          // quad_perm [2,3,0,1]
+    if constexpr (N >= 8) x += __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false);   // row_half_mirror
+    if constexpr (N >= 16) x += __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false);  // row_mirror
+    return x;
+}
+
 // The same over the whole wavefront (all 64 lanes active), uniform.
 __device__ __forceinline__ int wave_max(int x) {
     const int r = row16_max(x);
@@ -701,6 +712,224 @@ int launch_softmax(const int16_t* a, int16_t* c, uint32_t size, uint32_t op, uin
                 : launch_cols<false>(a, c, size, nq, batch, a_inc, c_inc, a_bs, c_bs, r, tsrc, st, s);
 }
 
+// ---------------------------------------------------------------- decode attention
+// One decode step's attention for a KV group (b, g) in one workgroup: the group's G query
+// rows against its cache of C rows, the chain of the unfused nodes
+//   s[i][j] = sat16(wrap32(sum_d q[i][d] K[j][d]) >> 8)        (q.K^T, MatmulKernel's wrap rule)
+//   P[i][.] = the softmax unit's row mode over s[i][.] (valid keys from the mask register)
+//   o[i][d] = sat16(wrap32(sum_j P[i][j] V[j][d]) >> 8)        (P.V)
+// without materializing s or P in HBM.  Phase 1: lane l reads word l % W4 of a key row (a
+// wavefront's loads cover whole rows), dots its 8 d with every query (v_dot2) and the W4 lanes
+// of a row sum by DPP; phase 2: the max and the sum of every query over the workgroup
+// (wavefront reductions, then LDS), e from the staged TAB and P by the rule of smx_row16
+// (scores past the valid count 0); phase 3: the consecutive lanes of a chunk of 8 d take pairs
+// of keys (v_dot2 over the pair) and sum by DPP, then over the wavefronts.  G is a template
+// argument, so every loop over the queries unrolls into independent chains.  Head dim HD (32
+// or 64): q rows of group bg at q + bg G HD, the caches' rows at kc / vc + bg C HD, o like q.
+constexpr uint32_t kDaThreads = 1024;          // four wavefronts a SIMD hide each other's latencies
+constexpr uint32_t kDaWaves = kDaThreads / 64;
+constexpr uint32_t kDaMaxG = 8;
+
+template <uint32_t HD, uint32_t G>
+__global__ __launch_bounds__(kDaThreads) void decode_attn_kernel(const int16_t* __restrict__ q,
+                                                                 const int16_t* __restrict__ kc,
+                                                                 const int16_t* __restrict__ vc,
+                                                                 int16_t* __restrict__ o, uint32_t C, SmxRegs r,
+                                                                 const int4* __restrict__ tsrc) {
+    constexpr uint32_t W4 = HD / 8;                         // 16-byte words of a row
+    constexpr uint32_t KPW = 64 / W4;                       // rows a wavefront load covers
+    extern __shared__ __attribute__((aligned(16))) uint32_t da_lds[];
+    uint32_t* tab = da_lds;                                 // TAB: 4096 words
+    uint32_t* qs = tab + 4096;                              // [G][HD / 2] d pairs
+    int32_t* red = reinterpret_cast<int32_t*>(qs + kDaMaxG * 32);       // [2][waves][8] reductions
+    uint32_t* oacc = reinterpret_cast<uint32_t*>(red + 2 * kDaWaves * kDaMaxG);   // [G][HD] sums of P V
+    int16_t* ps = reinterpret_cast<int16_t*>(oacc + kDaMaxG * 64);     // s, then P: [G][C]
+    const uint32_t bg = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int16_t* qg = q + (uint64_t)bg * G * HD;
+    const int16_t* kg = kc + (uint64_t)bg * C * HD;
+    const int16_t* vg = vc + (uint64_t)bg * C * HD;
+    typedef short v2s __attribute__((ext_vector_type(2)));
+
+    // ---- phase 1 loads first: KCH rounds of KR rows (one word a lane) in flight
+    constexpr uint32_t KR = kDaWaves * KPW, KCH = 8;
+    const uint32_t kw = t % W4, krow = t / W4;
+    int4 kv[KCH];
+    auto load_k = [&](uint32_t j0) {
+#pragma unroll
+        for (uint32_t u = 0; u < KCH; u++) {
+            const uint32_t j = j0 + u * KR + krow;
+            kv[u] = j < C ? reinterpret_cast<const int4*>(kg + (uint64_t)j * HD)[kw] : make_int4(0, 0, 0, 0);
+        }
+    };
+    load_k(0);
+    SmxStage stg;
+    smx_stage_load(stg, tsrc, 1024);
+    for (uint32_t e = t; e < G * HD / 2; e += kDaThreads) qs[e] = reinterpret_cast<const uint32_t*>(qg)[e];
+    for (uint32_t e = t; e < G * HD; e += kDaThreads) oacc[e] = 0u;
+    smx_stage_store(stg, tab, tsrc, 1024);
+    __syncthreads();
+    uint32_t qv[G][4];                                      // this lane's 8 d of every query
+#pragma unroll
+    for (uint32_t i = 0; i < G; i++)
+#pragma unroll
+        for (int w = 0; w < 4; w++) qv[i][w] = qs[i * (HD / 2) + 4 * kw + w];
+    for (uint32_t j0 = 0; j0 < C; j0 += KR * KCH) {
+        if (j0) load_k(j0);
+#pragma unroll
+        for (uint32_t u = 0; u < KCH; u++) {
+            int acc[G];
+#pragma unroll
+            for (uint32_t i = 0; i < G; i++) {
+                acc[i] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, qv[i][0]), __builtin_bit_cast(v2s, kv[u].x), 0, false);
+                acc[i] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, qv[i][1]), __builtin_bit_cast(v2s, kv[u].y), acc[i], false);
+                acc[i] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, qv[i][2]), __builtin_bit_cast(v2s, kv[u].z), acc[i], false);
+                acc[i] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, qv[i][3]), __builtin_bit_cast(v2s, kv[u].w), acc[i], false);
+                acc[i] = group_sum<W4>(acc[i]);
+            }
+            const uint32_t j = j0 + u * KR + krow;
+            if (kw == 0 && j < C) {
+#pragma unroll
+                for (uint32_t i = 0; i < G; i++) ps[i * C + j] = (int16_t)min(max(acc[i] >> 8, -32768), 32767);
+            }
+        }
+    }
+    // phase 3's lanes: the KPW consecutive lanes of d chunk dc take key pairs kp0 = wave KPW +
+    // slot; their first VCH pairs are loaded now, in flight across the softmax
+    constexpr uint32_t KPG = kDaThreads / W4, VCH = 4;
+    const uint32_t dc = lane / KPW, kp0 = wave * KPW + lane % KPW;
+    int4 va[VCH], vb[VCH];
+    auto load_v = [&](uint32_t j0) {
+#pragma unroll
+        for (uint32_t u = 0; u < VCH; u++) {
+            const uint32_t j = j0 + u * 2 * KPG;
+            va[u] = j < C ? *reinterpret_cast<const int4*>(vg + (uint64_t)j * HD + 8 * dc) : make_int4(0, 0, 0, 0);
+            vb[u] = j < C ? *reinterpret_cast<const int4*>(vg + (uint64_t)(j + 1) * HD + 8 * dc) : make_int4(0, 0, 0, 0);
+        }
+    };
+    load_v(2 * kp0);
+    __syncthreads();
+
+    // ---- phase 2: the softmax of every query row over its valid keys
+    uint32_t v[G];
+    int m[G];
+#pragma unroll
+    for (uint32_t i = 0; i < G; i++) {
+        v[i] = smx_valid(bg * G + i, C, r);
+        m[i] = -32768;
+    }
+    for (uint32_t j = t; j < C; j += kDaThreads) {
+#pragma unroll
+        for (uint32_t i = 0; i < G; i++) m[i] = max(m[i], j < v[i] ? (int)ps[i * C + j] : -32768);
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < G; i++) {
+        m[i] = wave_max(m[i]);
+        if (lane == 0) red[wave * kDaMaxG + i] = m[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t i = 0; i < G; i++) {
+        int x = red[i];
+#pragma unroll
+        for (uint32_t w = 1; w < kDaWaves; w++) x = max(x, red[w * kDaMaxG + i]);
+        m[i] = x;
+    }
+    uint32_t S[G];
+#pragma unroll
+    for (uint32_t i = 0; i < G; i++) S[i] = 0;
+    for (uint32_t j = t; j < C; j += kDaThreads) {
+#pragma unroll
+        for (uint32_t i = 0; i < G; i++)
+            S[i] += j < v[i] ? smx_e<false>((uint32_t)(m[i] - (int)ps[i * C + j]), r, tab) : 0u;
+    }
+    int32_t* red2 = red + kDaWaves * kDaMaxG;
+#pragma unroll
+    for (uint32_t i = 0; i < G; i++) {
+        S[i] = wave_sum(S[i]);
+        if (lane == 0) red2[wave * kDaMaxG + i] = (int32_t)S[i];
+    }
+    __syncthreads();
+    double rs[G];
+#pragma unroll
+    for (uint32_t i = 0; i < G; i++) {
+        uint32_t x = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < kDaWaves; w++) x += (uint32_t)red2[w * kDaMaxG + i];
+        rs[i] = smx_rscale(x, r);
+    }
+    // P in pairs of keys (C even): a thread reads the scores of its own pairs and overwrites
+    // them with P; the barrier above ended every other read of the scores
+    for (uint32_t j = 2 * t; j < C; j += 2 * kDaThreads) {
+#pragma unroll
+        for (uint32_t i = 0; i < G; i++) {
+            const uint32_t e0 = j < v[i] ? smx_e<false>((uint32_t)(m[i] - (int)ps[i * C + j]), r, tab) : 0u;
+            const uint32_t e1 = j + 1 < v[i] ? smx_e<false>((uint32_t)(m[i] - (int)ps[i * C + j + 1]), r, tab) : 0u;
+            *reinterpret_cast<int*>(&ps[i * C + j]) = smx_p2<true>(e0, e1, rs[i]);
+        }
+    }
+    __syncthreads();
+
+    // ---- phase 3: o = P . V, VCH key pairs of a lane in flight at a time
+    int acc[G][8];
+#pragma unroll
+    for (uint32_t i = 0; i < G; i++)
+#pragma unroll
+        for (int l = 0; l < 8; l++) acc[i][l] = 0;
+    for (uint32_t j0 = 2 * kp0; j0 < C; j0 += 2 * KPG * VCH) {
+        if (j0 != 2 * kp0) load_v(j0);
+#pragma unroll
+        for (uint32_t u = 0; u < VCH; u++) {
+            const uint32_t j = j0 + u * 2 * KPG;
+            if (j >= C) break;
+            const uint32_t wa[4] = {(uint32_t)va[u].x, (uint32_t)va[u].y, (uint32_t)va[u].z, (uint32_t)va[u].w};
+            const uint32_t wb[4] = {(uint32_t)vb[u].x, (uint32_t)vb[u].y, (uint32_t)vb[u].z, (uint32_t)vb[u].w};
+            uint32_t pr[8];                                 // (V[j][d], V[j + 1][d]) for the chunk's 8 d
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                pr[2 * w] = __builtin_amdgcn_perm(wb[w], wa[w], 0x05040100u);
+                pr[2 * w + 1] = __builtin_amdgcn_perm(wb[w], wa[w], 0x07060302u);
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < G; i++) {
+                const uint32_t pp = *reinterpret_cast<const uint32_t*>(&ps[i * C + j]);
+#pragma unroll
+                for (int l = 0; l < 8; l++)
+                    acc[i][l] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, pp), __builtin_bit_cast(v2s, pr[l]),
+                                                       acc[i][l], false);
+            }
+        }
+    }
+    // sum over the key-pair slots of a wavefront (a DPP group of KPW lanes), then over the
+    // wavefronts (LDS atomics: the sums wrap)
+#pragma unroll
+    for (uint32_t i = 0; i < G; i++)
+#pragma unroll
+        for (int l = 0; l < 8; l++) {
+            const int x = group_sum<KPW>(acc[i][l]);
+            if (lane % KPW == 0) atomicAdd(&oacc[i * HD + 8 * dc + l], (uint32_t)x);
+        }
+    __syncthreads();
+    for (uint32_t e = t; e < G * HD; e += kDaThreads)
+        o[(uint64_t)bg * G * HD + e] = (int16_t)min(max((int32_t)oacc[e] >> 8, -32768), 32767);
+}
+
+typedef void (*DecodeAttnFn)(const int16_t*, const int16_t*, const int16_t*, int16_t*, uint32_t, SmxRegs,
+                             const int4*);
+
+template <uint32_t HD>
+DecodeAttnFn decode_attn_fn(uint32_t g) {
+    switch (g) {
+    case 1: return decode_attn_kernel<HD, 1>;
+    case 2: return decode_attn_kernel<HD, 2>;
+    case 3: return decode_attn_kernel<HD, 3>;
+    case 4: return decode_attn_kernel<HD, 4>;
+    case 5: return decode_attn_kernel<HD, 5>;
+    case 6: return decode_attn_kernel<HD, 6>;
+    case 7: return decode_attn_kernel<HD, 7>;
+    default: return decode_attn_kernel<HD, 8>;
+    }
+}
+
 template <uint32_t OP>
 int launch_ew(const int16_t* a, const int16_t* b, int16_t* c, uint32_t size, uint32_t outer,
               uint32_t a_inc, uint32_t b_inc, uint32_t act, uint32_t alpha, DeviceState* st,
@@ -741,6 +970,12 @@ int prepare_softmax(DeviceState* st) {
         reinterpret_cast<const void*>(softmax_cols_kernel<6, false>), reinterpret_cast<const void*>(softmax_cols_kernel<8, false>)};
     for (const void* f : fns)
         CM_HIP_CHECK(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)st->lds_per_block));
+    for (uint32_t g = 1; g <= kDaMaxG; g++) {
+        CM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(decode_attn_fn<32>(g)),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)st->lds_per_block));
+        CM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(decode_attn_fn<64>(g)),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)st->lds_per_block));
+    }
     return CM_OK;
 }
 
@@ -787,4 +1022,29 @@ extern "C" int cm_softmax(const int16_t* a, int16_t* c, uint32_t size, uint32_t 
     if (size == 0 || outer == 0 || batch == 0) return CM_OK;
     return launch_softmax(a, c, size, op, outer, a_inc, c_inc, smx_cm, smx_cfg, smx_mask, batch, a_bs, c_bs, st,
                           as_stream(stream));
+}
+
+extern "C" int cm_decode_attention(const int16_t* q, const int16_t* kc, const int16_t* vc, int16_t* o,
+                                   uint32_t groups, uint32_t g, uint32_t c, uint32_t head_dim, uint32_t smx_cm,
+                                   uint32_t smx_cfg, uint32_t smx_mask, void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    if (groups == 0) return CM_OK;
+    if (head_dim != 32 && head_dim != 64)
+        return fail(CM_EINVAL, "decode attention: head_dim %u (the kernel takes 32 or 64)", head_dim);
+    if (g == 0 || g > kDaMaxG) return fail(CM_EINVAL, "decode attention: %u queries per group (1 .. %u)", g, kDaMaxG);
+    if (c == 0 || (c & 63) || c > 8192) return fail(CM_EINVAL, "decode attention: %u cache rows (a multiple of 64, <= 8192)", c);
+    if (groups > 0x7FFFFFFFu) return fail(CM_EINVAL, "decode attention: %u groups", groups);
+    if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || !aligned16(o))
+        return fail(CM_EALIGN, "decode attention: q, the caches and o must be 16-byte aligned");
+    SmxRegs r{smx_cm & 0xFFFFFFu, smx_cfg & 63u, (smx_cfg >> 8) & 31u, smx_mask & 0xFFFFu, smx_mask >> 16, 0};
+    r.dlim = smx_dlim(r.cm, r.cs);
+    const size_t lds = 4 * (4096 + kDaMaxG * 32 + 2 * kDaWaves * kDaMaxG + kDaMaxG * 64) + (size_t)2 * g * c;
+    if (lds > st->lds_per_block) return fail(CM_EINVAL, "decode attention: %zu bytes of LDS", lds);
+    const DecodeAttnFn fn = head_dim == 64 ? decode_attn_fn<64>(g) : decode_attn_fn<32>(g);
+    CM_LAUNCH("decode_attn_kernel", fn, dim3(groups), dim3(kDaThreads), lds, as_stream(stream), q, kc, vc, o, c, r,
+              reinterpret_cast<const int4*>(st->smx_tab));
+    return CM_OK;
 }

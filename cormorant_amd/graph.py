@@ -272,6 +272,47 @@ class SoftmaxVopNode(KernelNode):
         return n if self.mask is None else self.mask
 
 
+@dataclass
+class DecodeAttentionNode(KernelNode):
+    """One decode step's attention over the KV caches, fused: for every KV group (b, g) the
+    group's G = heads / kv_heads query rows of q [B][heads hd] against cache rows [C][hd] of
+    kc / vc [B][kv_heads][C][hd],
+        s = sat16(wrap32(q K^T) >> 8),  P = the softmax unit's row mode over s (valid keys from
+        the mask register),  o = sat16(wrap32(P V) >> 8),
+    o [B][heads hd] -- the chain the unfused graph runs as two AttnContractNodes around a
+    SoftmaxVopNode (LlmAttnConvNode's contractions, llm_nodes.py:1183-1425, and the row-mode
+    softmax, vectorop_smx.py:50-66), with s and P never leaving the workgroup.  ``cm`` / ``cfg``
+    / ``mask`` / ``mask_t`` / ``mask_add`` as SoftmaxVopNode's; the softmax's rows are the
+    (b, g, i) in order.  q, kc and o at exponents with f_o = f_p + f_v - 8 (f_p cfg's)."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    heads: int = 1
+    kv_heads: int = 1
+    head_dim: int = 64
+    cm: int = 12102203
+    cfg: int = 0x0813
+    mask: Optional[int] = None
+    mask_t: Optional[TensorInfo] = None
+    mask_add: int = 0
+
+    def mask_reg(self, n: int, host: Optional[int] = None) -> int:
+        if self.mask_t is not None:
+            if host is None:
+                raise SchedulerError(f"decode attention '{self.output.onnx_name}': the runtime mask needs its host value")
+            return int(host) + self.mask_add
+        return n if self.mask is None else self.mask
+
+    @property
+    def group(self) -> int:
+        return self.heads // self.kv_heads
+
+    @staticmethod
+    def supports(head_dim: int, ctx: int, group: int) -> bool:
+        """The fused kernel's geometry: head dim 32 or 64, a cache of a multiple of 64 rows (up
+        to 8192), at most 8 queries per KV group."""
+        return head_dim in (32, 64) and ctx % 64 == 0 and 0 < ctx <= 8192 and 0 < group <= 8
+
+
 def softmax_regs(f_s: int, sigma: float, f_p: int):
     """(smx_cm, smx_cfg) of scores at 2^-f_s with logit scale ``sigma`` and P at 2^-f_p
     (vectorop_smx.scale_regs + smx_nodes.regs, vectorop_smx.py:37-47, smx_nodes.py:64-76):
@@ -503,7 +544,7 @@ def conv_out(size: int, k: int, stride: int, pad_lo: int, pad_hi: int, dil: int 
 
 
 __all__ = ["SchedulerError", "KernelNode", "TensorInfo", "HeadView", "ScheduledNode", "MatmulNode", "MatmulConvNode", "ConvNode", "PoolNode",
-           "ReshapeNode", "SoftmaxVopNode", "RowOpsNode", "LlmAttnConvNode", "KvWriteNode", "AttentionNode", "attn_keys",
+           "ReshapeNode", "SoftmaxVopNode", "DecodeAttentionNode", "RowOpsNode", "LlmAttnConvNode", "KvWriteNode", "AttentionNode", "attn_keys",
            "KEY_QUANTUM",
            "Graph", "conv_out", "OP_ADD", "OP_SUB",
            "OP_MUL", "OP_DIV", "OP_RELU", "OP_RELU6", "OP_SOFTMAX", "OP_SOFTMAX_T", "POOL_MAX",

@@ -15,8 +15,8 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import units
-from .graph import (AttentionNode, AttnContractNode, ConvNode, Graph, HeadView, MatmulNode, PoolNode, ReshapeNode,
-                    ScheduledNode, SoftmaxVopNode, TensorInfo, conv_out, softmax_regs)
+from .graph import (AttentionNode, AttnContractNode, ConvNode, DecodeAttentionNode, Graph, HeadView, MatmulNode,
+                    PoolNode, ReshapeNode, ScheduledNode, SoftmaxVopNode, TensorInfo, conv_out, softmax_regs)
 from .host_ops import LlmEmbedNode
 from .rowops_nodes import LayerNorm32RoNode, ResAddBiasRoNode
 
@@ -421,7 +421,7 @@ def smollm2_weights(shape: LlamaShape = LlamaShape(), seed: int = 0):
 
 
 def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: int = 1, weights=None,
-                   runtime_pos: bool = False):
+                   runtime_pos: bool = False, fused_attention: bool = True):
     """(graph, inputs, exps): one greedy decode step of ``shape.batch`` sequences, each at cache
     position ctx - 1 (the cache full after the step's row: every cache row is a key), pow2
     numerics on the units as the reference's llama.py front end lays out a layer with the
@@ -452,7 +452,11 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
     ``runtime_pos``: the step's position is a host input "pos" (RoPE's table row, the cache row
     written, the softmax's valid keys pos + 1) and the KV caches are persistent states, so one
     graph runs successive decode steps over the same caches (_forward_pass with ``states``);
-    the inputs then carry "pos" = ctx - 1 and the caches' prefill as the states' first values."""
+    the inputs then carry "pos" = ctx - 1 and the caches' prefill as the states' first values.
+
+    ``fused_attention``: q.K^T, the softmax and P.V of a layer as one DecodeAttentionNode (the
+    same arithmetic, s and P not materialized) where its kernel takes the geometry; otherwise
+    as the two contractions and the softmax node."""
     from .dtype import AP_FIXED_16_8
     from .numeric import encode_matmul_weights
     from .rowops_nodes import DequantRoNode, RMSNormRoNode, ResAddRoNode, RopeRoNode, SiluMulRoNode
@@ -583,25 +587,14 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
         nodes.append(KvWriteNode([kr, kc_t], kc2, pos=pos, pos_t=pos_t))
         vc2 = T_(p + "vc1", [B, KV, S.ctx, HD], exp=e["v"])
         nodes.append(KvWriteNode([v, vc_t], vc2, pos=pos, pos_t=pos_t))
-        # per (sequence, group): the group's G query rows against the cache's K rows, the scores
-        # query-major s[b g][h'][j] (the unit's column mode takes query blocks of 16, so the
-        # G queries of a decode step go through its row mode: VitAttnSoftmax's query_major
-        # calls, smx_nodes.py:250-253)
-        qrows = T_(p + "qrows", [B * KV, G, HD], exp=e["q"])
-        nodes.append(ReshapeNode([qr], qrows))
-        kview = T_(p + "kc1v", [B * KV, S.ctx, HD], exp=e["k"])
-        nodes.append(ReshapeNode([kc2], kview))
-        st = T_(p + "s", [B * KV, G, keys], exp=e["s"])
-        nodes.append(AttnContractNode([qrows, kview], st, b_trans=True))
         cmr, cfg = softmax_regs(e["s"], 1.0 / math.sqrt(HD), e["p"])
-        pr = T_(p + "P", [B * KV, G, keys], exp=e["p"])
-        nodes.append(SoftmaxVopNode([st], pr, cm=cmr, cfg=cfg, mask=pos + 1, mask_t=pos_t, mask_add=1))
-        vview = T_(p + "vc1v", [B * KV, S.ctx, HD], exp=e["v"])
-        nodes.append(ReshapeNode([vc2], vview))
-        o = T_(p + "o", [B * KV, G, HD], exp=e["o"])
-        nodes.append(AttnContractNode([pr, vview], o))
         om = T_(p + "om", [B, A], exp=e["o"])
-        nodes.append(ReshapeNode([o], om))
+        if fused_attention and DecodeAttentionNode.supports(HD, S.ctx, G):
+            nodes.append(DecodeAttentionNode([qr, kc2, vc2], om, heads=H, kv_heads=KV, head_dim=HD, cm=cmr, cfg=cfg,
+                                             mask=pos + 1, mask_t=pos_t, mask_add=1))
+        else:
+            _decode_attention_unfused(nodes, T_, p, e, qr, kc2, vc2, om, B, KV, G, HD, keys, S.ctx, cmr, cfg, pos,
+                                      pos_t)
         a = T_(p + "a", [B, D], exp=e["a"])
         nodes.append(MatmulNode([om, T_(p + "wo", [A, D], data=L["wo"])], a))
         h1 = T_(p + "h1", [B, D], exp=RES_BITS, kind="i32")
@@ -634,3 +627,23 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
     g = Graph(nodes, input_tensors=[ids_t] + ([pos_t] if runtime_pos else []) + cache_ts, output_tensors=[lo])
     encode_matmul_weights(g.nodes, AP_FIXED_16_8)
     return g, inputs, exps
+
+def _decode_attention_unfused(nodes, T_, p, e, qr, kc2, vc2, om, B, KV, G, HD, keys, ctx, cmr, cfg, pos, pos_t):
+    """A decode layer's attention as the reference's nodes: per (sequence, group) the group's G
+    query rows against the cache's K rows, the scores query-major s[b g][h'][j] (the unit's
+    column mode takes query blocks of 16, so the G queries of a decode step go through its row
+    mode: VitAttnSoftmax's query_major calls, smx_nodes.py:250-253), the softmax, P.V."""
+    qrows = T_(p + "qrows", [B * KV, G, HD], exp=e["q"])
+    nodes.append(ReshapeNode([qr], qrows))
+    kview = T_(p + "kc1v", [B * KV, ctx, HD], exp=e["k"])
+    nodes.append(ReshapeNode([kc2], kview))
+    st = T_(p + "s", [B * KV, G, keys], exp=e["s"])
+    nodes.append(AttnContractNode([qrows, kview], st, b_trans=True))
+    pr = T_(p + "P", [B * KV, G, keys], exp=e["p"])
+    nodes.append(SoftmaxVopNode([st], pr, cm=cmr, cfg=cfg, mask=pos + 1, mask_t=pos_t, mask_add=1))
+    vview = T_(p + "vc1v", [B * KV, ctx, HD], exp=e["v"])
+    nodes.append(ReshapeNode([vc2], vview))
+    o = T_(p + "o", [B * KV, G, HD], exp=e["o"])
+    nodes.append(AttnContractNode([pr, vview], o))
+    nodes.append(ReshapeNode([o], om))
+

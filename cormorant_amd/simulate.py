@@ -16,7 +16,8 @@ import torch
 
 from . import units
 from .dtype import AP_FIXED_16_8, ApFixed16
-from .graph import (AttentionNode, AttnContractNode, ConvNode, Graph, KvWriteNode, LlmAttnConvNode, MatmulConvNode,
+from .graph import (AttentionNode, AttnContractNode, ConvNode, DecodeAttentionNode, Graph, KvWriteNode, LlmAttnConvNode,
+                    MatmulConvNode,
                     MatmulNode, PermuteNode, PoolNode, ReshapeNode, RowOpsNode, ScheduledNode, SchedulerError, SoftmaxVopNode,
                     TensorInfo, attn_keys)
 from .packing import conv_bias_image, conv_lowered_b_image, conv_weight_image, pack_matmul_b
@@ -149,6 +150,11 @@ class Simulator:
                 if len(group) > 1:
                     self._matmul_group(group, raw)
                     continue
+            if i < len(nodes) and self._output_job_fusable(sn, nodes[i]):
+                # a decode linear and the row-ops job on its output (the residual add): one launch
+                self._matmul_output_job(sn, nodes[i], raw)
+                i += 1
+                continue
             if isinstance(sn, MatmulNode):
                 raw[sn.output.onnx_name] = self._matmul(sn, raw)
             elif isinstance(sn, LlmEmbedNode):
@@ -179,6 +185,8 @@ class Simulator:
                 raw[sn.output.onnx_name] = self._attn_contract(sn, raw)
             elif isinstance(sn, KvWriteNode):
                 raw[sn.output.onnx_name] = self._kv_write(sn, raw)
+            elif isinstance(sn, DecodeAttentionNode):
+                raw[sn.output.onnx_name] = self._decode_attention(sn, raw)
             elif isinstance(sn, AttentionNode):
                 raw[sn.output.onnx_name] = self._attention(sn, raw)
             elif isinstance(sn, ScheduledNode):
@@ -349,6 +357,10 @@ class Simulator:
         if wrap:
             self._check_exponents(at, bt, ot)
         c = self._new(ot, batch * n * m)
+        if bt.data is not None and b_batch == 1 and batch == 1 and wrap and n <= 16 and k % 8 == 0:
+            # a decode-sized product: MFMA over the weight's split image, one launch
+            units.matmul_skinny_planes(a.reshape(-1).contiguous(), n, k, [self._row_planes(bt, b, k, m)], [c], [m])
+            return c
         if bt.data is not None and b_batch == 1 and wrap and n <= 32 and m % 2 == 0 and k % 8 == 0:
             # a decode-sized product: the library's skinny path reads the weight itself, kept
             # as its transposed image [m][k] (each column's k contiguous)
@@ -424,6 +436,63 @@ class Simulator:
                        sn.out_h, sn.out_w, 1, sn.kw, 1, sn.kw, wrap32=wrap)
         return c
 
+    def _skinny_planes_ok(self, sn) -> bool:
+        """A MatMul the skinny plane kernel takes: a constant 2-d pow2 weight, one slice of A of
+        at most 16 rows, k a multiple of 8."""
+        if not isinstance(sn, MatmulNode):
+            return False
+        at, bt, ot = sn.inputs[0], sn.inputs[1], sn.output
+        if bt.data is None or len(at.shape) > 2 or len(bt.shape) != 2 or bt.shape[0] != at.shape[-1]:
+            return False
+        return self._pow2(at, bt, ot) and int(at.shape[-2]) <= 16 and int(at.shape[-1]) % 8 == 0
+
+    def _output_job_fusable(self, sn, nxt) -> bool:
+        """``nxt`` is a one-job COPY / ADDX adapter over whole rows whose B is the skinny
+        MatMul ``sn``'s output (and whose A is another tensor): the pair runs as one launch."""
+        if not (self._skinny_planes_ok(sn) and isinstance(nxt, RowOpsAdapter) and len(nxt.inputs) == 2
+                and getattr(nxt, "pos_t", None) is None and getattr(nxt, "table", None) is None):
+            return False
+        xt, bt, ot = nxt.inputs[0], nxt.inputs[1], nxt.output
+        n, m = int(sn.inputs[0].shape[-2]), int(sn.inputs[1].shape[-1])
+        if bt.onnx_name != sn.output.onnx_name or xt.onnx_name == sn.output.onnx_name:
+            return False
+        if xt.kind not in ("i16", "i32") or ot.kind not in ("i16", "i32") or xt.numel != n * m or ot.numel != n * m:
+            return False
+        jobs = nxt.jobs()
+        if len(jobs) != 1:
+            return False
+        j = jobs[0]
+        code = j.op & 15
+        return (j.col0 == 0 and j.n == m and j.b_row0 is None and code in (units.RO_COPY, units.RO_ADDX)
+                and (j.op >> 6) & 3 == 0 and not (j.op & (1 << 14)))
+
+    def _matmul_output_job(self, sn: MatmulNode, nxt: RowOpsAdapter, raw) -> None:
+        """The skinny MatMul and its output's row-ops job in one launch; both outputs kept."""
+        at, bt, ot = sn.inputs[0], sn.inputs[1], sn.output
+        self._check_exponents(at, bt, ot)
+        n, k, m = int(at.shape[-2]), int(at.shape[-1]), int(bt.shape[-1])
+        a = self._get(at, raw).reshape(-1).contiguous()
+        c = self._new(ot, n * m)
+        j = nxt.jobs()[0]
+        params = self._params.get(id(nxt))
+        if params is None:
+            params = [torch.from_numpy(np.ascontiguousarray(j.params, np.uint8)).to(self.device)]
+            self._params[id(nxt)] = params
+        x = self._get(nxt.inputs[0], raw).reshape(-1).contiguous()
+        out = self._new(nxt.output)
+        units.matmul_skinny_planes_addx(a, n, k, self._row_planes(bt, self._get(bt, raw), k, m), c, m, x, params[0],
+                                        j.op, out, bq_sh=j.bq_sh)
+        raw[ot.onnx_name] = c
+        raw[nxt.output.onnx_name] = out
+
+    def _row_planes(self, bt: TensorInfo, b: torch.Tensor, k: int, m: int) -> torch.Tensor:
+        """A weight's split image (byte planes and column sums) from its row-major lanes, built once."""
+        img = self._images.get(bt.onnx_name + "#planes")
+        if img is None:
+            img = units.matmul_b_planes(b.reshape(-1).contiguous(), k, m)
+            self._images[bt.onnx_name + "#planes"] = img
+        return img
+
     def _trans_image(self, bt: TensorInfo, b: torch.Tensor, k: int, m: int) -> torch.Tensor:
         """A weight's transposed image [m][k], built once."""
         img = self._images.get(bt.onnx_name + "#trans")
@@ -449,15 +518,20 @@ class Simulator:
         at = group[0].inputs[0]
         a = self._get(at, raw).reshape(-1).contiguous()
         n, k = int(at.shape[-2]), int(at.shape[-1])
+        planes = n <= 16
         bs, cs, ms = [], [], []
         for sn in group:
             bt, ot = sn.inputs[1], sn.output
             self._check_exponents(at, bt, ot)
             m = int(bt.shape[-1])
-            bs.append(self._trans_image(bt, self._get(bt, raw), k, m))
+            b = self._get(bt, raw)
+            bs.append(self._row_planes(bt, b, k, m) if planes else self._trans_image(bt, b, k, m))
             cs.append(self._new(ot, n * m))
             ms.append(m)
-        units.matmul_skinny_multi(a, n, k, bs, cs, ms, b_packed=2)
+        if planes:
+            units.matmul_skinny_planes(a, n, k, bs, cs, ms)
+        else:
+            units.matmul_skinny_multi(a, n, k, bs, cs, ms, b_packed=2)
         for sn, c in zip(group, cs):
             raw[sn.output.onnx_name] = c
 
@@ -732,6 +806,28 @@ class Simulator:
         oh = torch.empty(BH * T * hd, dtype=torch.int16, device=dev)
         units.matmul(pr, vh, oh, T, T, hd, batch=BH, a_bs=T * kp, b_bs=T * hd, c_bs=T * hd, wrap32=True)
         units.permute16(oh, o, (B, T, H, hd), (H * T * hd, hd, T * hd, 1))
+        return o
+
+    def _decode_attention(self, sn: DecodeAttentionNode, raw) -> torch.Tensor:
+        """q.K^T, the row-mode softmax and P.V of every KV group in one launch."""
+        qt, kt, vt = sn.inputs[:3]
+        ot = sn.output
+        B, KV, C, HD = (int(v) for v in kt.shape)
+        G = sn.group
+        if (list(vt.shape) != [B, KV, C, HD] or sn.kv_heads != KV or sn.head_dim != HD or sn.heads != KV * G
+                or list(qt.shape) != [B, sn.heads * HD] or list(ot.shape) != [B, sn.heads * HD]):
+            raise SchedulerError(f"decode attention '{ot.onnx_name}': q {list(qt.shape)}, caches {list(kt.shape)}, "
+                                 f"o {list(ot.shape)}")
+        fq, fk, fv, fo = (np.asarray(self._exp_b(t)).reshape(-1) for t in (qt, kt, vt, ot))
+        if any((e != e[0]).any() for e in (fq, fk, fv, fo)):
+            raise SchedulerError(f"decode attention '{ot.onnx_name}': q, the caches and o at one exponent each")
+        fp = (sn.cfg >> 8) & 31
+        if int(fo[0]) != fp + int(fv[0]) - self._dtype.frac_bits:
+            raise SchedulerError(f"decode attention '{ot.onnx_name}': the output exponent is not f_p + f_v - 8")
+        o = self._new(ot)
+        units.decode_attention(self._get(qt, raw).reshape(-1).contiguous(), self._get(kt, raw).reshape(-1),
+                               self._get(vt, raw).reshape(-1), o, B * KV, G, C, sn.cm, sn.cfg,
+                               sn.mask_reg(C, self._host_int(sn.mask_t, raw)), head_dim=HD)
         return o
 
     def _kv_write(self, sn: KvWriteNode, raw) -> torch.Tensor:

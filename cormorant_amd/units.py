@@ -225,6 +225,58 @@ def matmul_skinny_multi(a: torch.Tensor, n: int, k: int, bs, cs, ms, b_packed: i
     _lib.check(rc, "cm_matmul_skinny_multi")
 
 
+def decode_attention(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, o: torch.Tensor, groups: int, g: int,
+                     c: int, smx_cm: int, smx_cfg: int, smx_mask: int, head_dim: int = 64) -> torch.Tensor:
+    """cm_decode_attention: per KV group the g query rows against c cache rows, q.K^T, the
+    row-mode softmax and P.V in one launch (o like q)."""
+    _require(q, "q", torch.int16, groups * g * head_dim)
+    _require(kc, "kc", torch.int16, groups * c * head_dim)
+    _require(vc, "vc", torch.int16, groups * c * head_dim)
+    _require(o, "o", torch.int16, groups * g * head_dim)
+    rc = _lib.lib().cm_decode_attention(_ptr(q), _ptr(kc), _ptr(vc), _ptr(o), groups, g, c, head_dim,
+                                        smx_cm & 0xFFFFFFFF, smx_cfg & 0xFFFFFFFF, smx_mask & 0xFFFFFFFF, _stream())
+    _lib.check(rc, "cm_decode_attention")
+    return o
+
+
+def matmul_skinny_planes(a: torch.Tensor, n: int, k: int, planes, cs, ms) -> None:
+    """cm_matmul_skinny_planes: C_i = sat16(wrap32(A . B_i) >> 8) for up to 4 weights given as
+    their split images (matmul_b_planes of the same k and m_i) and the same A [n][k], n <= 16."""
+    count = len(planes)
+    if not (len(cs) == len(ms) == count):
+        raise ValueError("matmul_skinny_planes: one c and one m per weight")
+    _require(a, "a", torch.int16, n * k)
+    for pl, c, m in zip(planes, cs, ms):
+        need = int(_lib.lib().cm_matmul_b_planes_bytes(k, m, 1))
+        if pl.dtype != torch.uint8 or pl.numel() < need or pl.data_ptr() % 256:
+            raise ValueError("matmul_skinny_planes: the uint8 image of matmul_b_planes for these k, m")
+        _require(c, "c", torch.int16, n * m)
+    P = ctypes.c_void_p * max(count, 1)
+    rc = _lib.lib().cm_matmul_skinny_planes(_ptr(a), n, k, count, P(*[_ptr(x) for x in planes]),
+                                            P(*[_ptr(c) for c in cs]), (ctypes.c_uint32 * max(count, 1))(*ms),
+                                            _stream())
+    _lib.check(rc, "cm_matmul_skinny_planes")
+
+
+def matmul_skinny_planes_addx(a: torch.Tensor, n: int, k: int, planes: torch.Tensor, c: torch.Tensor, m: int,
+                              x: torch.Tensor, params: torch.Tensor, op: int, out: torch.Tensor,
+                              bq_sh: int = 0) -> None:
+    """cm_matmul_skinny_planes_addx: C = sat16(wrap32(A . B) >> 8) for one weight's split image,
+    then the row-ops COPY / ADDX job ``op`` over x [n][m] and C into out [n][m] in the same launch."""
+    _require(a, "a", torch.int16, n * k)
+    need = int(_lib.lib().cm_matmul_b_planes_bytes(k, m, 1))
+    if planes.dtype != torch.uint8 or planes.numel() < need or planes.data_ptr() % 256:
+        raise ValueError("matmul_skinny_planes_addx: the uint8 image of matmul_b_planes for these k, m")
+    _require(c, "c", torch.int16, n * m)
+    if x.numel() * x.element_size() < n * m * (2 if (op >> 4) & 3 == 0 else 4):
+        raise ValueError("matmul_skinny_planes_addx: x smaller than [n][m] of the job's A kind")
+    if out.numel() * out.element_size() < n * m * (2 if (op >> 8) & 3 == 0 else 4):
+        raise ValueError("matmul_skinny_planes_addx: out smaller than [n][m] of the job's output kind")
+    rc = _lib.lib().cm_matmul_skinny_planes_addx(_ptr(a), n, k, _ptr(planes), _ptr(c), m, _ptr(x), _ptr(params),
+                                                 op & 0xFFFFFFFF, bq_sh, _ptr(out), _stream())
+    _lib.check(rc, "cm_matmul_skinny_planes_addx")
+
+
 def matmul_strided(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, n: int, k: int, m: int, batch: int,
                    inner: int, a_view, b_view, c_view, b_trans: bool = False, wrap32: bool = False) -> torch.Tensor:
     """cm_matmul_strided: each view is (offset, ld, bs, bs2) in elements of its tensor; slice bt

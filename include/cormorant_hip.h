@@ -147,6 +147,25 @@ int cm_matmul_noalloc(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n
 int cm_matmul_skinny_multi(const int16_t* a, uint32_t n, uint32_t k, uint32_t count, const int16_t* const* b,
                            int16_t* const* c, const uint32_t* m, uint32_t b_packed, void* stream);
 
+/* The products of cm_matmul_skinny_multi (n <= 16 rows, k a multiple of 8, a 16-byte aligned)
+ * against weights already split by cm_matmul_split_b (b_slices 1, the same k and m[i]): C_i =
+ * sat16(wrap32(A . B_i) >> 8), C_i row-major [n][m[i]].  No counterpart in the reference's
+ * units (each product is the MatmulKernel call of cm_matmul, MatmulKernel.h:228-242): one
+ * launch, no workspace, for the decode step's linears. */
+int cm_matmul_skinny_planes(const int16_t* a, uint32_t n, uint32_t k, uint32_t count, const void* const* b_planes,
+                            int16_t* const* c, const uint32_t* m, void* stream);
+
+/* One product of cm_matmul_skinny_planes followed, in the same launch, by a row-ops COPY /
+ * ADDX job on its output (the decode step's residual add): C = sat16(wrap32(A . B) >> 8) as
+ * there, then out[r][j] = the job of op word `op` (A kind int16 / int32, B the int16 C, output
+ * kind int16 / int32, F_P_BCAST / F_RELU / F_SCALE) over x[r][j] and C[r][j] with the 16-byte
+ * parameter block `params` and bq_sh -- the cm_rowops job (x, c, out, params, op, n = m, c1 = n)
+ * of ROWOPS_RTL_KERNEL.md section 1 on whole rows (x and out row-major [n][m]).  No
+ * counterpart in the reference's units; the results equal those two calls. */
+int cm_matmul_skinny_planes_addx(const int16_t* a, uint32_t n, uint32_t k, const void* b_planes, int16_t* c,
+                                 uint32_t m, const void* x, const void* params, uint32_t op, uint32_t bq_sh,
+                                 void* out, void* stream);
+
 /* cm_matmul over strided operands (no counterpart in the reference's units: the per-head
  * operands that VitAttnPrep / LlmAttnMerge would copy out and back, read and written in place):
  * slice bt of `batch` starts at (bt / inner) x_bs + (bt % inner) x_bs2 elements of each
@@ -292,6 +311,20 @@ int cm_embed_rows(const void* table, uint32_t table_i16, const int32_t* ids, voi
 int cm_attention(const int16_t* qkv, int16_t* o, uint32_t batch, uint32_t seq, uint32_t heads, uint32_t head_dim,
                  uint64_t ld, uint32_t q_off, uint32_t k_off, uint32_t v_off, uint64_t o_ld, uint32_t smx_cm,
                  uint32_t smx_cfg, void* stream);
+
+/* One decode step's attention, fused, for `groups` KV groups: group bg's g query rows q[bg g +
+ * i][0..hd) against its cache rows kc / vc[bg c + j][0..hd) (head_dim hd 32 or 64, c a
+ * multiple of 64 up to 8192, g <= 8),
+ *   s[i][j] = sat16(wrap32(sum_d q[i][d] kc[j][d]) >> 8),
+ *   P[i][.] = the softmax unit's row mode over s[i][.] (cm_vectorop op 10 with smx_cm / smx_cfg /
+ *             smx_mask; the softmax row index of (bg, i) is bg g + i),
+ *   o[bg g + i][d] = sat16(wrap32(sum_j P[i][j] vc[j][d]) >> 8).
+ * The chain of two cm_matmul wrap contractions around a cm_vectorop softmax, as the reference
+ * runs a decode step's q.K^T, softmax and P.V (llm_nodes.py:1183-1425, vectorop_smx.py:50-66);
+ * no counterpart as one unit call.  16-byte aligned operands. */
+int cm_decode_attention(const int16_t* q, const int16_t* kc, const int16_t* vc, int16_t* o, uint32_t groups,
+                        uint32_t g, uint32_t c, uint32_t head_dim, uint32_t smx_cm, uint32_t smx_cfg,
+                        uint32_t smx_mask, void* stream);
 
 #ifdef __cplusplus
 }

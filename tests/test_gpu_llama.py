@@ -22,6 +22,21 @@ pytestmark = pytest.mark.gpu
 ])
 def test_decode_step_every_tensor(shape, seed):
     g, inputs, _ = models.smollm2_decode(shape, seed=seed)
+    assert any(type(n).__name__ == "DecodeAttentionNode" for n in g.nodes)
+    got = Simulator(g)._forward_pass(inputs)
+    want = oracle_graph.forward(g, inputs)
+    for name, v in got.items():
+        np.testing.assert_array_equal(v, want[name].reshape(v.shape), err_msg=name)
+
+
+@pytest.mark.parametrize("shape,seed", [
+    (models.LlamaShape(layers=2, batch=3, d=128, heads=4, kv=2, hd=32, ff=256, vocab=512, ctx=64), 1),
+    (models.LlamaShape(layers=1, batch=16), 5),
+])
+def test_decode_step_unfused_attention(shape, seed):
+    """The same step with the attention as the two contractions around the softmax node (s and
+    P materialized and compared too)."""
+    g, inputs, _ = models.smollm2_decode(shape, seed=seed, fused_attention=False)
     got = Simulator(g)._forward_pass(inputs)
     want = oracle_graph.forward(g, inputs)
     for name, v in got.items():

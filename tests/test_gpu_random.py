@@ -258,6 +258,109 @@ def test_matmul_skinny_multi(U, oracle_lib, n, k, ms, bp):
         assert (g[n * m:] == POISON16).all()
 
 
+@pytest.mark.parametrize("n,k,ms", [
+    (16, 960, (960, 320, 320)),          # SmolLM2's q / k / v
+    (16, 960, (2560, 2560)),             # gate / up
+    (16, 2560, (960,)),                  # down: 40 k steps over 8 wavefronts
+    (16, 960, (49152,)),                 # the tied head
+    (1, 8, (1, 33, 64, 7)),              # one k group, ragged columns
+    (5, 200, (31, 100)),                 # k past a step, rows short of 16
+    (16, 4104, (40,)),                   # several chunks per wavefront, k past a slab
+])
+def test_matmul_skinny_planes(U, oracle_lib, n, k, ms):
+    """cm_matmul_skinny_planes against the oracle's products one by one (the outputs'
+    neighbours untouched): full-range operands, the int32 wrap, B from its split image."""
+    rng = np.random.default_rng(n + 3 * k + len(ms))
+    a = rint16(rng, n * k)
+    bl = [rint16(rng, k * m) for m in ms]
+    planes = [U.matmul_b_planes(dev16(x), k, m) for x, m in zip(bl, ms)]
+    wants = [oracle_lib.matmul(a, x, n, k, m, 1, 0, 0, n * m, 0, 0, True) for x, m in zip(bl, ms)]
+    outs = [poisoned16(n * m + 8) for m in ms]
+    U.matmul_skinny_planes(dev16(a), n, k, planes, outs, list(ms))
+    for got, want, m in zip(outs, wants, ms):
+        g = host(got)
+        np.testing.assert_array_equal(g[:n * m], want)
+        assert (g[n * m:] == POISON16).all()
+
+
+@pytest.mark.parametrize("n,k,m,kind", [
+    (16, 960, 960, "resadd"),            # SmolLM2's o projection and residual add (int32 x and out)
+    (16, 2560, 960, "resadd"),           # the down projection
+    (5, 200, 72, "copy_relu"),           # an int16 COPY with bias, shifts, ReLU (per-column block)
+    (1, 8, 24, "scale"),                 # F_SCALE, int16 x, int32 out, broadcast block
+])
+def test_matmul_skinny_planes_output_job(U, oracle_lib, n, k, m, kind):
+    """cm_matmul_skinny_planes_addx equals cm_matmul_skinny_planes followed by the cm_rowops job
+    on its output (both outputs), for the residual add and other COPY / ADDX jobs."""
+    import torch
+    from cormorant_amd import rowops_nodes as rn
+    rng = np.random.default_rng(n + k + m)
+    a = rint16(rng, n * k)
+    b = rint16(rng, k * m)
+    planes = U.matmul_b_planes(dev16(b), k, m)
+    if kind == "resadd":
+        ak, ck = rn.K_I32, rn.K_I32
+        blk, bc = rn.pblock(0, 0, 0, rng.integers(0, 10, m), 0, m)
+        op = rn.opword(rn.RO_ADDX, ak, rn.K_I16, ck, b_en=True, p_bcast=bc)
+        bq_sh = 0
+    elif kind == "copy_relu":
+        ak, ck = rn.K_I16, rn.K_I16
+        blk, bc = rn.pblock(0, rng.integers(-2 ** 21, 2 ** 21, m), rng.integers(0, 4, m), rng.integers(0, 4, m),
+                            rng.integers(0, 6, m), m)
+        op = rn.opword(rn.RO_ADDX, ak, rn.K_I16, ck, b_en=True, p_bcast=bc, relu=True)
+        bq_sh = 3
+    else:
+        ak, ck = rn.K_I16, rn.K_I32
+        blk, bc = rn.pblock(12345, 7, 2, 1, 9, m)
+        op = rn.opword(rn.RO_ADDX, ak, rn.K_I16, ck, b_en=True, p_bcast=bc) | U.F_SCALE
+        bq_sh = 5
+    xb = 2 if ak == rn.K_I16 else 4
+    cb = 2 if ck == rn.K_I16 else 4
+    x = torch.from_numpy(rng.integers(-2 ** (8 * xb - 2), 2 ** (8 * xb - 2), n * m).astype(np.int16 if xb == 2 else np.int32)).cuda()
+    p = torch.from_numpy(np.ascontiguousarray(blk, np.uint8)).cuda()
+    c = poisoned16(n * m + 8)
+    out = torch.full((n * m * cb + 16,), 0x5A, dtype=torch.uint8, device="cuda")
+    U.matmul_skinny_planes_addx(dev16(a), n, k, planes, c, m, x, p, op, out, bq_sh=bq_sh)
+    c2 = poisoned16(n * m + 8)
+    U.matmul_skinny_planes(dev16(a), n, k, [planes], [c2], [m])
+    out2 = torch.full((n * m * cb + 16,), 0x5A, dtype=torch.uint8, device="cuda")
+    U.rowops(x.view(torch.uint8), c2.view(torch.uint8), out2, p, op, m, n, 1, m * xb, 0, m * 2, 0, m * cb, 0,
+             bq_sh=bq_sh)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(c), host(c2))
+    np.testing.assert_array_equal(out.cpu().numpy(), out2.cpu().numpy())
+    np.testing.assert_array_equal(host(c2)[:n * m], oracle_lib.matmul(a, b, n, k, m, 1, 0, 0, n * m, 0, 0, True))
+
+
+@pytest.mark.parametrize("groups,G,C,mask,regs,lim", [
+    (80, 3, 1024, 1024, 2, 3000),        # SmolLM2's step: 16 sequences x 5 groups, every cache row a key
+    (10, 3, 1024, 700, 1, 3000),         # keys past the valid count
+    (4, 8, 2048, (100 | (3 << 16)), 3, 32768),   # a periodic mask (per-row valid counts), full range
+    (7, 1, 64, 0, 0, 32768),             # no valid key: P = 0, o = 0
+    (3, 5, 128, 128, 1, 32768),
+])
+def test_decode_attention(U, oracle_lib, groups, G, C, mask, regs, lim):
+    """cm_decode_attention against the oracle's chain per group: s = q K^T (int32 wrap), the
+    row-mode softmax (op 10, the softmax row index bg G + i), o = P V."""
+    rng = np.random.default_rng(groups + G + C)
+    smx_cm, smx_cfg = _attention_regs()[regs]
+    q = rng.integers(-lim, lim, (groups, G, 64)).astype(np.int16)
+    kc = rng.integers(-lim, lim, (groups, C, 64)).astype(np.int16)
+    vc = rng.integers(-32768, 32768, (groups, C, 64)).astype(np.int16)
+    s = np.stack([oracle_lib.matmul(q[b].reshape(-1), np.ascontiguousarray(kc[b].T).reshape(-1), G, 64, C, 1, 0, 0,
+                                    G * C, 0, 0, True).reshape(G, C) for b in range(groups)])
+    p = oracle_lib.vectorop(s.reshape(-1), None, groups * G * C, C, 10, groups * G, C, C, 0, 0, smx_cm, smx_cfg,
+                            mask).reshape(groups, G, C)
+    want = np.stack([oracle_lib.matmul(p[b].reshape(-1), vc[b].reshape(-1), G, C, 64, 1, 0, 0, G * 64, 0, 0,
+                                       True).reshape(G, 64) for b in range(groups)])
+    o = poisoned16(groups * G * 64 + 8)
+    U.decode_attention(dev16(q.reshape(-1)), dev16(kc.reshape(-1)), dev16(vc.reshape(-1)), o, groups, G, C, smx_cm,
+                       smx_cfg, mask)
+    got = host(o)
+    np.testing.assert_array_equal(got[:groups * G * 64].reshape(groups, G, 64), want)
+    assert (got[groups * G * 64:] == POISON16).all()
+
+
 def _attention_regs():
     from cormorant_amd.graph import softmax_regs
     return [(12102203, 0x0813), softmax_regs(9, 0.125, 15), softmax_regs(12, 0.125, 14), softmax_regs(6, 1.0, 14)]
