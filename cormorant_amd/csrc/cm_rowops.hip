@@ -91,14 +91,8 @@ __global__ __launch_bounds__(256) void ro_stream_kernel(Job j, const uint8_t* __
             const Param q = ld_param(params, col, bcast);
             i64 r = 0;
             if (code == RO_ROPE) {
-                const uint32_t HD = j.aux & 0xFFF, half = HD / 2, d = col % HD;
-                const i64 x = *reinterpret_cast<const int16_t*>(ra + 2u * col);
-                const i64 rot = d < half ? -(i64)*reinterpret_cast<const int16_t*>(ra + 2u * (col + half))
-                                         : (i64)*reinterpret_cast<const int16_t*>(ra + 2u * (col - half));
-                const i64 cs = *reinterpret_cast<const int32_t*>(rb + 4u * d);
-                const i64 sn = *reinterpret_cast<const int32_t*>(rb + 4u * (HD + d));
-                const i128 s = (((i128)x * cs) << q.sa) + (((i128)rot * sn) << q.sb);
-                r = sat16(rne_shr(s, q.sc));
+                r = rope_value(reinterpret_cast<const int16_t*>(ra), col, j.aux & 0xFFF,
+                               reinterpret_cast<const int32_t*>(rb), q);
             } else {
                 const i64 x = zero_a ? 0 : ld_kind(ra + (u64)abytes * col, ak);
                 const i64 y = (ben && code != RO_DEQUANT) ? ld_kind(rb + (u64)bbytes * col, bk) : 0;
@@ -542,6 +536,49 @@ __global__ __launch_bounds__(256) void ro_tload_kernel(Job j, uint8_t* __restric
     }
 }
 
+// ---------------------------------------------------------------- decode prep
+// A decode step's attention prep in one launch: q and k rows [B][heads HD] RoPE'd at one
+// position (the ROPE jobs of the two RopeRoNodes: their parameter blocks, the table row of the
+// position), q into qr, k straight into the K cache rows kc[b][g][pos] and v copied into the V
+// cache rows vc[b][g][pos] (caches [B][KV][C][HD]): the ROPE, ROPE and the two KV row writes of
+// the unfused step, with the same element rule (rope_value).  A thread per 16-byte output word.
+struct DecodePrep {
+    const int16_t *q, *k, *v;
+    int16_t *qr, *kc, *vc;
+    const int32_t* tab;                 // cos [HD] then sin [HD] of the position
+    const uint8_t *pq, *pk;             // the ROPE jobs' parameter blocks
+    uint32_t bcq, bck, B, H, KV, HD, C, pos;
+};
+
+__global__ __launch_bounds__(256) void decode_prep_kernel(DecodePrep d) {
+    const uint32_t qw = d.H * d.HD / 8, kw = d.KV * d.HD / 8, per = qw + 2 * kw;
+    const u64 total = (u64)d.B * per;
+    for (u64 w = (u64)blockIdx.x * blockDim.x + threadIdx.x; w < total; w += (u64)gridDim.x * blockDim.x) {
+        const uint32_t b = (uint32_t)(w / per), r = (uint32_t)(w - (u64)b * per);
+        int16_t* dst;
+        uint32_t out[4] = {0, 0, 0, 0};
+        if (r < qw + kw) {
+            const bool isq = r < qw;
+            const uint32_t col0 = (isq ? r : r - qw) * 8;
+            const int16_t* row = isq ? d.q + (u64)b * d.H * d.HD : d.k + (u64)b * d.KV * d.HD;
+#pragma unroll
+            for (uint32_t l = 0; l < 8; l++) {
+                const uint32_t col = col0 + l;
+                const Param p = ld_param(isq ? d.pq : d.pk, col, (isq ? d.bcq : d.bck) != 0);
+                out[l >> 1] |= ((uint32_t)(uint16_t)rope_value(row, col, d.HD, d.tab, p)) << (16 * (l & 1));
+            }
+            dst = isq ? d.qr + (u64)b * d.H * d.HD + col0
+                      : d.kc + (((u64)b * d.KV + col0 / d.HD) * d.C + d.pos) * d.HD + col0 % d.HD;
+        } else {
+            const uint32_t col0 = (r - qw - kw) * 8;
+            const uint4 x = *reinterpret_cast<const uint4*>(d.v + (u64)b * d.KV * d.HD + col0);
+            out[0] = x.x; out[1] = x.y; out[2] = x.z; out[3] = x.w;
+            dst = d.vc + (((u64)b * d.KV + col0 / d.HD) * d.C + d.pos) * d.HD + col0 % d.HD;
+        }
+        *reinterpret_cast<uint4*>(dst) = make_uint4(out[0], out[1], out[2], out[3]);
+    }
+}
+
 unsigned grid_for(u64 items, unsigned per_block = 256) {
     u64 b = (items + per_block - 1) / per_block;
     if (b > 65536ull * 8) b = 65536ull * 8;
@@ -676,5 +713,34 @@ extern "C" int cm_rowops_chain(const cm_rowops_desc* jobs, uint32_t n_jobs, void
                            d.win_lo, d.win_hi, stream);
         if (rc) return rc;
     }
+    return CM_OK;
+}
+
+extern "C" int cm_decode_prep(const int16_t* q, const int16_t* k, const int16_t* v, int16_t* qr, int16_t* kc,
+                              int16_t* vc, uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t head_dim,
+                              uint32_t cache_rows, uint32_t pos, const void* rope_row, const void* params_q,
+                              uint32_t op_q, const void* params_k, uint32_t op_k, void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    if (batch == 0) return CM_OK;
+    if (head_dim == 0 || (head_dim & 15) || head_dim > 128 || heads == 0 || kv_heads == 0)
+        return fail(CM_EINVAL, "decode prep: %u heads and %u KV heads of %u (a multiple of 16 up to 128)", heads,
+                    kv_heads, head_dim);
+    if (pos >= cache_rows) return fail(CM_EINVAL, "decode prep: position %u of %u cache rows", pos, cache_rows);
+    for (uint32_t op : {op_q, op_k})
+        if ((op & 15) != RO_ROPE || ((op >> 4) & 3) != 0 || ((op >> 8) & 3) != 0 || (op & F_P_KEEP))
+            return fail(CM_EINVAL, "decode prep: 0x%x is not an int16 ROPE job's op word", op);
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(qr) || !aligned16(kc) || !aligned16(vc) ||
+        (reinterpret_cast<uintptr_t>(rope_row) & 3) || (reinterpret_cast<uintptr_t>(params_q) & 15) ||
+        (reinterpret_cast<uintptr_t>(params_k) & 15))
+        return fail(CM_EALIGN, "decode prep: operands not aligned");
+    const DecodePrep d{q, k, v, qr, kc, vc, static_cast<const int32_t*>(rope_row),
+                       static_cast<const uint8_t*>(params_q), static_cast<const uint8_t*>(params_k),
+                       (op_q & F_P_BCAST) ? 1u : 0u, (op_k & F_P_BCAST) ? 1u : 0u, batch, heads, kv_heads, head_dim,
+                       cache_rows, pos};
+    const uint64_t words = (uint64_t)batch * (heads + 2 * kv_heads) * head_dim / 8;
+    CM_LAUNCH("decode_prep_kernel", decode_prep_kernel, dim3(grid_for(words)), dim3(256), 0, as_stream(stream), d);
     return CM_OK;
 }

@@ -65,5 +65,17 @@ __device__ __forceinline__ i64 copy_addx(i64 x, i64 y, const Param& q, uint32_t 
     return r;
 }
 
+// ROPE of element col of a row of heads of width HD (rowops_spec.rope): the rotate-half partner
+// from the same head, cos / sin (int32 at 2^-23) at tab[d] / tab[HD + d], d = col mod HD:
+// sat16(rne_shr(((x cos) << sa) + ((rot sin) << sb), sc)).
+__device__ __forceinline__ i64 rope_value(const int16_t* row, uint32_t col, uint32_t HD, const int32_t* tab,
+                                          const Param& q) {
+    const uint32_t half = HD / 2, d = col % HD;
+    const i64 x = row[col];
+    const i64 rot = d < half ? -(i64)row[col + half] : (i64)row[col - half];
+    const i128 s = (((i128)x * (i64)tab[d]) << q.sa) + (((i128)rot * (i64)tab[HD + d]) << q.sb);
+    return sat16(rne_shr(s, q.sc));
+}
+
 }  // namespace ro
 }  // namespace cm

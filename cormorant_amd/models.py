@@ -454,12 +454,13 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
     graph runs successive decode steps over the same caches (_forward_pass with ``states``);
     the inputs then carry "pos" = ctx - 1 and the caches' prefill as the states' first values.
 
-    ``fused_attention``: q.K^T, the softmax and P.V of a layer as one DecodeAttentionNode (the
-    same arithmetic, s and P not materialized) where its kernel takes the geometry; otherwise
-    as the two contractions and the softmax node."""
+    ``fused_attention``: the RoPE of q / k and the cache row writes as one DecodePrepNode, and
+    q.K^T, the softmax and P.V as one DecodeAttentionNode (the same arithmetic; the RoPE'd k rows,
+    s and P not materialized) where the kernels take the geometry; otherwise the RoPE and KV-write
+    nodes, the two contractions and the softmax node."""
     from .dtype import AP_FIXED_16_8
     from .numeric import encode_matmul_weights
-    from .rowops_nodes import DequantRoNode, RMSNormRoNode, ResAddRoNode, RopeRoNode, SiluMulRoNode
+    from .rowops_nodes import DecodePrepNode, DequantRoNode, RMSNormRoNode, ResAddRoNode, RopeRoNode, SiluMulRoNode
     from .graph import KvWriteNode
 
     S = shape
@@ -579,20 +580,24 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
         v = T_(p + "v", [B, KD], exp=e["v"])
         nodes.append(MatmulNode([x, T_(p + "wv", [D, KD], data=L["wv"])], v))
         qr = T_(p + "qr", [B, A], exp=e["q"])
-        nodes.append(RopeRoNode([q], qr, heads=H, head_dim=HD, cos=cos, sin=sin, pos=pos, same_pos=True, pos_t=pos_t))
-        kr = T_(p + "kr", [B, KD], exp=e["k"])
-        nodes.append(RopeRoNode([k], kr, heads=KV, head_dim=HD, cos=cos, sin=sin, pos=pos, same_pos=True,
-                                pos_t=pos_t))
-        kc2 = T_(p + "kc1", [B, KV, S.ctx, HD], exp=e["k"])
-        nodes.append(KvWriteNode([kr, kc_t], kc2, pos=pos, pos_t=pos_t))
-        vc2 = T_(p + "vc1", [B, KV, S.ctx, HD], exp=e["v"])
-        nodes.append(KvWriteNode([v, vc_t], vc2, pos=pos, pos_t=pos_t))
         cmr, cfg = softmax_regs(e["s"], 1.0 / math.sqrt(HD), e["p"])
         om = T_(p + "om", [B, A], exp=e["o"])
-        if fused_attention and DecodeAttentionNode.supports(HD, S.ctx, G):
-            nodes.append(DecodeAttentionNode([qr, kc2, vc2], om, heads=H, kv_heads=KV, head_dim=HD, cm=cmr, cfg=cfg,
+        if fused_attention and DecodeAttentionNode.supports(HD, S.ctx, G) and HD % 16 == 0:
+            # RoPE of q and k with the cache rows written in one launch, then the attention
+            nodes.append(DecodePrepNode([q, k, v, kc_t, vc_t], qr, heads=H, kv_heads=KV, head_dim=HD, cos=cos,
+                                        sin=sin, pos=pos, pos_t=pos_t))
+            nodes.append(DecodeAttentionNode([qr, kc_t, vc_t], om, heads=H, kv_heads=KV, head_dim=HD, cm=cmr, cfg=cfg,
                                              mask=pos + 1, mask_t=pos_t, mask_add=1))
         else:
+            nodes.append(RopeRoNode([q], qr, heads=H, head_dim=HD, cos=cos, sin=sin, pos=pos, same_pos=True,
+                                    pos_t=pos_t))
+            kr = T_(p + "kr", [B, KD], exp=e["k"])
+            nodes.append(RopeRoNode([k], kr, heads=KV, head_dim=HD, cos=cos, sin=sin, pos=pos, same_pos=True,
+                                    pos_t=pos_t))
+            kc2 = T_(p + "kc1", [B, KV, S.ctx, HD], exp=e["k"])
+            nodes.append(KvWriteNode([kr, kc_t], kc2, pos=pos, pos_t=pos_t))
+            vc2 = T_(p + "vc1", [B, KV, S.ctx, HD], exp=e["v"])
+            nodes.append(KvWriteNode([v, vc_t], vc2, pos=pos, pos_t=pos_t))
             _decode_attention_unfused(nodes, T_, p, e, qr, kc2, vc2, om, B, KV, G, HD, keys, S.ctx, cmr, cfg, pos,
                                       pos_t)
         a = T_(p + "a", [B, D], exp=e["a"])

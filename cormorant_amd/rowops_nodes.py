@@ -542,6 +542,50 @@ class RopeRoNode(RowOpsAdapter):
 
 # ---------------------------------------------------------------- register-level job lists
 @dataclass
+class DecodePrepNode(KernelNode):
+    """A decode step's attention prep, fused: RoPE of q [B][heads hd] into the output qr and of
+    k [B][kv_heads hd] straight into the K cache rows at the step's position, v's rows into the V
+    cache rows -- the two RopeRoNodes (same_pos) and the two KvWriteNodes of the unfused step, the
+    same jobs' arithmetic (their parameter blocks and table row) in one launch.  inputs: q, k, v,
+    kc, vc (caches [B][kv_heads][C][hd], written in place; k's RoPE output at kc's exponents and
+    v at vc's); ``pos`` or the runtime ``pos_t``."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    heads: int = 1
+    kv_heads: int = 1
+    head_dim: int = 64
+    cos: np.ndarray = None
+    sin: np.ndarray = None
+    pos: int = 0
+    pos_t: Optional[TensorInfo] = None
+    F: int = 8
+
+    def __post_init__(self):
+        q, k, v, kc, vc = self.inputs[:5]
+        B, KV, C, HD = (int(x) for x in kc.shape)
+        what = f"decode prep '{self.output.onnx_name}'"
+        _require(list(vc.shape) == [B, KV, C, HD] and KV == self.kv_heads and HD == self.head_dim
+                 and list(q.shape) == [B, self.heads * HD] and list(k.shape) == [B, KV * HD]
+                 and list(v.shape) == [B, KV * HD] and list(self.output.shape) == list(q.shape), what, "shapes")
+        _require(HD % 16 == 0 and HD <= 128, what, "a head dim of a multiple of 16 up to 128")
+        fk, fv = np.asarray(_exps(kc, self.F, 1)).reshape(-1), np.asarray(_exps(vc, self.F, 1)).reshape(-1)
+        _require((fk == fk[0]).all() and (fv == fv[0]).all(), what, "the caches at one exponent each")
+        _require((_exps(v, self.F, KV * HD) == fv[0]).all(), what, "v at the V cache's exponent")
+        self.rope_q = RopeRoNode([q], self.output, heads=self.heads, head_dim=HD, cos=self.cos, sin=self.sin,
+                                 pos=self.pos, F=self.F, same_pos=True, pos_t=self.pos_t)
+        kr = TensorInfo(self.output.onnx_name + "__k_rope", [B, KV * HD], exp=int(fk[0]))
+        self.rope_k = RopeRoNode([k], kr, heads=KV, head_dim=HD, cos=self.cos, sin=self.sin, pos=self.pos, F=self.F,
+                                 same_pos=True, pos_t=self.pos_t)
+
+    def position(self, host: Optional[int] = None) -> int:
+        if self.pos_t is not None:
+            if host is None:
+                raise SchedulerError(f"decode prep '{self.output.onnx_name}': the runtime position needs its host value")
+            return int(host)
+        return self.pos
+
+
+@dataclass
 class RoCall:
     """One run_rowops call (rowops_nodes.py:143-151): the register block, each stream's buffer
     named -- a graph tensor's onnx_name, or a staging buffer of the node ("node:<key>") -- with

@@ -22,7 +22,7 @@ from .graph import (AttentionNode, AttnContractNode, ConvNode, DecodeAttentionNo
                     TensorInfo, attn_keys)
 from .packing import conv_bias_image, conv_lowered_b_image, conv_weight_image, pack_matmul_b
 from .host_ops import HostNode, LlmEmbedNode
-from .rowops_nodes import RoCallNode, RoJob, RowOpsAdapter
+from .rowops_nodes import DecodePrepNode, RoCallNode, RoJob, RowOpsAdapter
 
 def node_reference(node, ins, dtype: Optional[ApFixed16] = None, device: str = "cuda",
                    host: Optional[Dict[str, np.ndarray]] = None) -> np.ndarray:
@@ -187,6 +187,8 @@ class Simulator:
                 raw[sn.output.onnx_name] = self._kv_write(sn, raw)
             elif isinstance(sn, DecodeAttentionNode):
                 raw[sn.output.onnx_name] = self._decode_attention(sn, raw)
+            elif isinstance(sn, DecodePrepNode):
+                raw[sn.output.onnx_name] = self._decode_prep(sn, raw)
             elif isinstance(sn, AttentionNode):
                 raw[sn.output.onnx_name] = self._attention(sn, raw)
             elif isinstance(sn, ScheduledNode):
@@ -829,6 +831,26 @@ class Simulator:
                                self._get(vt, raw).reshape(-1), o, B * KV, G, C, sn.cm, sn.cfg,
                                sn.mask_reg(C, self._host_int(sn.mask_t, raw)), head_dim=HD)
         return o
+
+    def _decode_prep(self, sn: DecodePrepNode, raw) -> torch.Tensor:
+        """RoPE of q (into the output) and k (into the K cache rows) and the V cache rows, one launch."""
+        q, k, v, kc, vc = sn.inputs[:5]
+        B, KV, C, HD = (int(x) for x in kc.shape)
+        pos = sn.position(self._host_int(sn.pos_t, raw))
+        if not 0 <= pos < C:
+            raise SchedulerError(f"decode prep '{sn.output.onnx_name}': position {pos} of {C} cache rows")
+        jq, jk = sn.rope_q.jobs(pos=pos)[0], sn.rope_k.jobs(pos=pos)[0]
+        params = self._params.get(id(sn))
+        if params is None:
+            params = [torch.from_numpy(np.ascontiguousarray(j.params, np.uint8)).to(self.device) for j in (jq, jk)]
+            self._params[id(sn)] = params
+        tab = self._get(sn.rope_q.table, raw).reshape(-1, 2 * HD)
+        qr = self._new(sn.output)
+        units.decode_prep(self._get(q, raw).reshape(-1).contiguous(), self._get(k, raw).reshape(-1).contiguous(),
+                          self._get(v, raw).reshape(-1).contiguous(), qr, self._get(kc, raw).reshape(-1), C,
+                          self._get(vc, raw).reshape(-1), B, sn.heads, KV, HD, pos, tab[jq.b_row0], params[0], jq.op,
+                          params[1], jk.op)
+        return qr
 
     def _kv_write(self, sn: KvWriteNode, raw) -> torch.Tensor:
         """Row ``pos`` of every sequence's group-major cache from the step's rows, in place."""

@@ -239,6 +239,24 @@ def decode_attention(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor, o: tor
     return o
 
 
+def decode_prep(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, qr: torch.Tensor, kc: torch.Tensor,
+                kc_rows: int, vc: torch.Tensor, batch: int, heads: int, kv_heads: int, head_dim: int, pos: int,
+                rope_row: torch.Tensor, params_q: torch.Tensor, op_q: int, params_k: torch.Tensor, op_k: int) -> None:
+    """cm_decode_prep: q / k RoPE'd at ``pos`` (q into qr, k into the K cache rows), v's rows into
+    the V cache rows; caches [batch][kv_heads][kc_rows][head_dim]."""
+    _require(q, "q", torch.int16, batch * heads * head_dim)
+    _require(k, "k", torch.int16, batch * kv_heads * head_dim)
+    _require(v, "v", torch.int16, batch * kv_heads * head_dim)
+    _require(qr, "qr", torch.int16, batch * heads * head_dim)
+    _require(kc, "kc", torch.int16, batch * kv_heads * kc_rows * head_dim)
+    _require(vc, "vc", torch.int16, batch * kv_heads * kc_rows * head_dim)
+    _require(rope_row, "rope_row", torch.int32, 2 * head_dim)
+    rc = _lib.lib().cm_decode_prep(_ptr(q), _ptr(k), _ptr(v), _ptr(qr), _ptr(kc), _ptr(vc), batch, heads, kv_heads,
+                                   head_dim, kc_rows, pos, _ptr(rope_row), _ptr(params_q), op_q & 0xFFFFFFFF,
+                                   _ptr(params_k), op_k & 0xFFFFFFFF, _stream())
+    _lib.check(rc, "cm_decode_prep")
+
+
 def matmul_skinny_planes(a: torch.Tensor, n: int, k: int, planes, cs, ms) -> None:
     """cm_matmul_skinny_planes: C_i = sat16(wrap32(A . B_i) >> 8) for up to 4 weights given as
     their split images (matmul_b_planes of the same k and m_i) and the same A [n][k], n <= 16."""

@@ -326,6 +326,20 @@ int cm_decode_attention(const int16_t* q, const int16_t* kc, const int16_t* vc, 
                         uint32_t g, uint32_t c, uint32_t head_dim, uint32_t smx_cm, uint32_t smx_cfg,
                         uint32_t smx_mask, void* stream);
 
+/* A decode step's attention prep in one launch (no counterpart as one unit call): the ROPE jobs
+ * of q [batch][heads hd] and k [batch][kv_heads hd] at one position -- op words op_q / op_k
+ * (int16 A and C, the int32 table as B), their 16-byte parameter blocks params_q / params_k,
+ * rope_row the table row of the position (cos [hd] then sin [hd], int32) -- with q's result
+ * into qr and k's straight into the K cache rows kc[b][g][pos][0..hd), and v's rows copied into
+ * vc[b][g][pos] (caches [batch][kv_heads][cache_rows][hd]): the cm_rowops ROPE jobs and the two
+ * KV row writes of the reference's attention prep (rowops_nodes.py:997-1047, llm_nodes.py:
+ * 1012-1030) with the same element rule.  hd a multiple of 16 up to 128, 16-byte aligned rows.
+ * The device's row-ops parameter RAM is left as it was. */
+int cm_decode_prep(const int16_t* q, const int16_t* k, const int16_t* v, int16_t* qr, int16_t* kc, int16_t* vc,
+                   uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t head_dim, uint32_t cache_rows,
+                   uint32_t pos, const void* rope_row, const void* params_q, uint32_t op_q, const void* params_k,
+                   uint32_t op_k, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,6 +10,8 @@ baseline bench.py times.  It reads a graph's declared fields (tensors, shapes, e
 parameters) and dispatches on the nodes' class names; it imports nothing from the product, so
 no arithmetic, rounding rule or job derivation is shared with what it checks.
 """
+from types import SimpleNamespace
+
 import numpy as np
 
 from oracle import cm
@@ -23,6 +25,13 @@ _NP = {"i16": np.int16, "i32": np.int32, "f32": np.float32}
 _KB = {"i16": 2, "i32": 4, "f32": 4}
 ADAPTERS = ("LayerNormRoNode", "LayerNorm32RoNode", "RMSNormRoNode", "ResAddRoNode", "ResAddBiasRoNode",
             "WidenRoNode", "SiluMulRoNode", "DequantRoNode", "BiasCopyRoNode", "RopeRoNode")
+
+
+class _RopeRoNode(SimpleNamespace):
+    """A RoPE adapter's declared fields, for the row-ops adapter restatement (dispatched by class name)."""
+
+
+_RopeRoNode.__name__ = "RopeRoNode"
 
 
 def _quantize(x):
@@ -350,6 +359,22 @@ def forward(graph, inputs, states=None):
                 c = cm.vectorop(xr.reshape(-1), None, rows * n8, n, 10, rows, n8, n8, 0, 0, sn.cm, sn.cfg,
                                 _mask(sn, n, get))
                 vals[out.onnx_name] = (c.reshape(rows, n8)[:, :n].astype(np.float64) / 2.0 ** fp).reshape(out.shape)
+        elif kind == "DecodePrepNode":
+            # RoPE of q (the output) and k (at the K cache's exponent) at the position, then the
+            # cache rows: the RoPE and KV-write nodes of the unfused step
+            qt, kt, vt, kct, vct = sn.inputs[:5]
+            B, KV, C, HD = (int(x) for x in kct.shape)
+            pos = sn.pos if sn.pos_t is None else int(np.asarray(get(sn.pos_t)).reshape(-1)[0])
+            kr = SimpleNamespace(onnx_name="k_rope", shape=list(kt.shape), exp=kct.exp, kind="i16")
+            rq = _RopeRoNode(inputs=[qt], output=out, heads=sn.heads, head_dim=HD, cos=sn.cos, sin=sn.sin,
+                             pos=pos, pos_t=None, same_pos=True, F=getattr(sn, "F", 8))
+            rk = _RopeRoNode(inputs=[kt], output=kr, heads=KV, head_dim=HD, cos=sn.cos, sin=sn.sin, pos=pos,
+                             pos_t=None, same_pos=True, F=getattr(sn, "F", 8))
+            vals[out.onnx_name] = rowops_adapt.adapter(rq, [get(qt)]).reshape(out.shape)
+            kcache = vals[kct.onnx_name].reshape(B, KV, C, HD)       # the states, written in place
+            vcache = vals[vct.onnx_name].reshape(B, KV, C, HD)
+            kcache[:, :, pos, :] = rowops_adapt.adapter(rk, [get(kt)]).reshape(B, KV, HD)
+            vcache[:, :, pos, :] = get(vt).reshape(B, KV, HD)
         elif kind == "DecodeAttentionNode":
             # per KV group: s = q K^T (wrap rule), the row-mode softmax (VectorOP op 10), o = P V
             qt, kt, vt = sn.inputs[:3]
