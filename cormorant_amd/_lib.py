@@ -45,6 +45,11 @@ SIGNATURES = {
     "cm_pool": (_I32, [_P, _P] + [_U32] * 17 + [_P]),
     "cm_rowops": (_I32, [_P, _P, _P, _P] + [_U32] * 10 + [_I64] + [_U32] * 4 + [_P]),
     "cm_rowops_chain": (_I32, [ctypes.POINTER(CmRowopsDesc), _U32, _P]),
+    "cm_rowops_chain_planes": (_I32, [ctypes.POINTER(CmRowopsDesc), _U32, _P, _P]),
+    "cm_vectorop_planes": (_I32, [_P, _P, _P] + [_U32] * 7 + [_P, _P]),
+    "cm_attention_planes": (_I32, [_P, _P] + [_U32] * 4 + [ctypes.c_uint64] + [_U32] * 5 + [_P, _P]),
+    "cm_matmul_a_planes_bytes": (ctypes.c_size_t, [_U32] * 3),
+    "cm_matmul_aplanes": (_I32, [_P, _U32, _P, _P, _U32, _U32, _U32, _U32, _P]),
     "cm_softmax": (_I32, [_P, _P] + [_U32] * 9 + [ctypes.c_uint64, ctypes.c_uint64, _P]),
     "cm_permute16": (_I32, [_P, _P] + [_U32] * 4 + [ctypes.c_uint64] * 4 + [_P]),
     "cm_copy16": (_I32, [_P, _P] + [_U32] * 4 + [ctypes.c_uint64] * 8 + [_P]),

@@ -78,12 +78,14 @@ __device__ __forceinline__ int32_t wrap_sum(int32_t hh, int32_t mid, int32_t ll,
 
 // T = keys per sequence (a multiple of 64, at most 384).  qkv rows: ld elements apart; Q / K /
 // V of head h at columns q_off / k_off / v_off + 64 h.  o rows: o_ld apart, head h at 64 h.
-template <uint32_t T>
+// PL: also the byte planes of o as the A operand of the output projection (rows b T + i, the
+// row sums of head h's 64 columns as partial sum h).
+template <uint32_t T, bool PL>
 __global__ __launch_bounds__(256, 3) void attention_kernel(const int16_t* __restrict__ qkv, int16_t* __restrict__ o,
                                                            const int32_t* __restrict__ tab, uint32_t heads,
                                                            uint64_t ld, uint32_t q_off, uint32_t k_off,
                                                            uint32_t v_off, uint64_t o_ld, uint32_t cm, uint32_t cfg,
-                                                           uint32_t dlim) {
+                                                           uint32_t dlim, APlanes po) {
     constexpr uint32_t KB = T / 16;          // key blocks of phase 1
     constexpr uint32_t KS = T / 64;          // k steps of phase 3
     constexpr uint32_t VS = T + 16;          // V^T plane row stride, bytes (rows 4 banks apart)
@@ -223,6 +225,8 @@ __global__ __launch_bounds__(256, 3) void attention_kernel(const int16_t* __rest
 
     // ---- phase 3: o^T[d][qi] over 4 blocks of 16 d, two per staged half of V^T
     int16_t* orow = o + ((uint64_t)b * T + qi) * o_ld + kHd * h;      // result lane: d = 16 mb + 4 g + r
+    const uint64_t prow = (uint64_t)b * T + qi;
+    int32_t osum = 0;                                                   // PL: the lane's 16 outputs' sum
 #pragma unroll
     for (uint32_t half = 0; half < 2; half++) {
         if (half == 1) {
@@ -274,22 +278,32 @@ __global__ __launch_bounds__(256, 3) void attention_kernel(const int16_t* __rest
                 pk[r / 2] = (uint32_t)(uint16_t)o0 | ((uint32_t)(uint16_t)o1 << 16);
             }
             *reinterpret_cast<uint2*>(orow + 16 * mb + 4 * g) = make_uint2(pk[0], pk[1]);
+            if constexpr (PL) {
+                const uint32_t col = kHd * h + 16 * mb + 4 * g;
+                *reinterpret_cast<uint32_t*>(po.hi + prow * po.k + col) = __builtin_amdgcn_perm(pk[1], pk[0], 0x07050301u);
+                *reinterpret_cast<uint32_t*>(po.lo + prow * po.k + col) =
+                    __builtin_amdgcn_perm(pk[1], pk[0], 0x06040200u) ^ 0x80808080u;
+                osum += (int32_t)(int16_t)(pk[0] & 0xFFFF) + ((int32_t)pk[0] >> 16) + (int32_t)(int16_t)(pk[1] & 0xFFFF) +
+                        ((int32_t)pk[1] >> 16);
+            }
         }
+    }
+    if constexpr (PL) {
+        // the four lane groups g of query c16 hold its 64 outputs of this head
+        osum += __shfl_xor(osum, 16, 64);
+        osum += __shfl_xor(osum, 32, 64);
+        if (g == 0) po.part[(uint64_t)h * po.lines + prow] = osum;
     }
 }
 
-template <uint32_t T>
+template <uint32_t T, bool PL>
 void* attention_fn() {
-    return reinterpret_cast<void*>(&attention_kernel<T>);
+    return reinterpret_cast<void*>(&attention_kernel<T, PL>);
 }
 
-}  // namespace
-}  // namespace cm
-
-extern "C" int cm_attention(const int16_t* qkv, int16_t* o, uint32_t batch, uint32_t seq, uint32_t heads,
-                            uint32_t head_dim, uint64_t ld, uint32_t q_off, uint32_t k_off, uint32_t v_off,
-                            uint64_t o_ld, uint32_t smx_cm, uint32_t smx_cfg, void* stream) {
-    using namespace cm;
+int run_attention(const int16_t* qkv, int16_t* o, uint32_t batch, uint32_t seq, uint32_t heads, uint32_t head_dim,
+                  uint64_t ld, uint32_t q_off, uint32_t k_off, uint32_t v_off, uint64_t o_ld, uint32_t smx_cm,
+                  uint32_t smx_cfg, void* planes, hipStream_t s) {
     DeviceState* st;
     int rc = state(&st);
     if (rc) return rc;
@@ -302,27 +316,51 @@ extern "C" int cm_attention(const int16_t* qkv, int16_t* o, uint32_t batch, uint
     if (((smx_cfg >> 8) & 31u) > 39u || ((smx_cfg >> 8) & 31u) == 0u)
         return fail(CM_EINVAL, "attention: softmax output bits %u", (smx_cfg >> 8) & 31u);
     if ((uint64_t)batch * heads > 65535) return fail(CM_EINVAL, "attention: %u sequence-head pairs", batch * heads);
+    if (planes != nullptr && (o_ld != (uint64_t)heads * kHd || heads > 64 || (reinterpret_cast<uintptr_t>(planes) & 255)))
+        return fail(CM_EINVAL, "attention planes: o rows of exactly heads x 64 (at most 64 heads), 256-byte aligned "
+                               "planes");
     const size_t lds = 16384 + 2 * (size_t)(kHd / 2) * (seq + 16) + 4 * 64 * sizeof(int32_t);
     if (lds > st->lds_per_block) return fail(CM_EINVAL, "attention: %zu bytes of LDS per workgroup", lds);
-    hipStream_t s = as_stream(stream);
     const uint32_t dlim = smx_dlim(smx_cm & 0xFFFFFFu, smx_cfg & 63u);
     const dim3 grid(seq / kQb, batch * heads);
-#define CM_ATT(T)                                                                                               \
-    case T: {                                                                                                   \
+    const APlanes po = planes != nullptr ? a_planes_view(planes, batch * seq, heads * kHd, heads) : APlanes{};
+#define CM_ATT(T, PL)                                                                                           \
+    {                                                                                                           \
         static bool attr = false;                                                                               \
         if (!attr) {                                                                                            \
-            CM_HIP_CHECK(hipFuncSetAttribute(attention_fn<T>(), hipFuncAttributeMaxDynamicSharedMemorySize,     \
+            CM_HIP_CHECK(hipFuncSetAttribute(attention_fn<T, PL>(), hipFuncAttributeMaxDynamicSharedMemorySize, \
                                              (int)lds));                                                        \
             attr = true;                                                                                        \
         }                                                                                                       \
-        CM_LAUNCH("attention_kernel", attention_kernel<T>, grid, dim3(256), lds, s, qkv, o, st->smx_tab,       \
-                  heads, ld, q_off, k_off, v_off, o_ld, smx_cm, smx_cfg, dlim);                                 \
+        CM_LAUNCH("attention_kernel", (attention_kernel<T, PL>), grid, dim3(256), lds, s, qkv, o, st->smx_tab,  \
+                  heads, ld, q_off, k_off, v_off, o_ld, smx_cm, smx_cfg, dlim, po);                             \
         return CM_OK;                                                                                           \
     }
+#define CM_ATT_T(T) \
+    case T: if (planes != nullptr) CM_ATT(T, true) else CM_ATT(T, false)
     switch (seq) {
-        CM_ATT(64) CM_ATT(128) CM_ATT(256) CM_ATT(384)
+        CM_ATT_T(64) CM_ATT_T(128) CM_ATT_T(256) CM_ATT_T(384)
     default: break;
     }
+#undef CM_ATT_T
 #undef CM_ATT
     return fail(CM_EINVAL, "attention: %u keys", seq);
+}
+
+}  // namespace
+}  // namespace cm
+
+extern "C" int cm_attention(const int16_t* qkv, int16_t* o, uint32_t batch, uint32_t seq, uint32_t heads,
+                            uint32_t head_dim, uint64_t ld, uint32_t q_off, uint32_t k_off, uint32_t v_off,
+                            uint64_t o_ld, uint32_t smx_cm, uint32_t smx_cfg, void* stream) {
+    return cm::run_attention(qkv, o, batch, seq, heads, head_dim, ld, q_off, k_off, v_off, o_ld, smx_cm, smx_cfg,
+                             nullptr, cm::as_stream(stream));
+}
+
+extern "C" int cm_attention_planes(const int16_t* qkv, int16_t* o, uint32_t batch, uint32_t seq, uint32_t heads,
+                                   uint32_t head_dim, uint64_t ld, uint32_t q_off, uint32_t k_off, uint32_t v_off,
+                                   uint32_t smx_cm, uint32_t smx_cfg, void* planes, void* stream) {
+    if (planes == nullptr) return cm::fail(CM_EINVAL, "attention planes: no planes buffer");
+    return cm::run_attention(qkv, o, batch, seq, heads, head_dim, ld, q_off, k_off, v_off, (uint64_t)heads * 64,
+                             smx_cm, smx_cfg, planes, cm::as_stream(stream));
 }

@@ -116,6 +116,53 @@ __device__ __forceinline__ void store_stream(void* p, int4 v) {
     __builtin_nontemporal_store(__builtin_bit_cast(cm_i32x4, v), reinterpret_cast<cm_i32x4*>(p));
 }
 
+// ---------------------------------------------------------------- byte planes
+// The byte planes of 8 int16 values (one 16-byte load), x - 128 = 256 h + l: high bytes (1, 3
+// of each dword) and low bytes (0, 2, top bit flipped) as two 8-byte words.
+__device__ __forceinline__ void split8(const int4 v, uint2& h, uint2& l) {
+    const uint32_t w0 = (uint32_t)v.x, w1 = (uint32_t)v.y, w2 = (uint32_t)v.z, w3 = (uint32_t)v.w;
+    h = make_uint2(__builtin_amdgcn_perm(w1, w0, 0x07050301u), __builtin_amdgcn_perm(w3, w2, 0x07050301u));
+    l = make_uint2(__builtin_amdgcn_perm(w1, w0, 0x06040200u) ^ 0x80808080u,
+                   __builtin_amdgcn_perm(w3, w2, 0x06040200u) ^ 0x80808080u);
+}
+
+__device__ __forceinline__ int32_t sum8(const int4 v) {   // sum of the 8 int16 lanes
+    const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+    int32_t s = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) s += (int32_t)(int16_t)(w[q] & 0xFFFF) + ((int32_t)w[q] >> 16);
+    return s;
+}
+
+// The A operand of a matmul as its producer writes it (cm_matmul_aplanes): for n rows of k
+// int16 values (k a multiple of 64), hi and lo byte planes [lines][k] (lines = n rounded up to
+// 256; the rows past n are never read into a stored result) and `nsum` arrays of partial row
+// sums part[s][lines] whose total over s is each row's sum.  One buffer: hi, then lo, then
+// part, each section 256-byte aligned.
+constexpr uint32_t kAPlanesRowAlign = 256;
+inline size_t a_planes_lines(uint32_t n) { return ((size_t)n + kAPlanesRowAlign - 1) / kAPlanesRowAlign * kAPlanesRowAlign; }
+inline size_t a_planes_bytes(uint32_t n, uint32_t k, uint32_t nsum) {
+    const size_t lines = a_planes_lines(n);
+    return 2 * lines * k + lines * 4 * nsum;    // k % 64 == 0 and lines % 256 == 0 keep the sections aligned
+}
+struct APlanes {                    // a producer's view of one A planes buffer
+    int8_t* hi = nullptr;
+    int8_t* lo = nullptr;
+    int32_t* part = nullptr;
+    uint32_t lines = 0, k = 0, nsum = 0;
+};
+inline APlanes a_planes_view(void* buf, uint32_t n, uint32_t k, uint32_t nsum) {
+    APlanes p;
+    const size_t lines = a_planes_lines(n);
+    p.hi = static_cast<int8_t*>(buf);
+    p.lo = p.hi + lines * k;
+    p.part = reinterpret_cast<int32_t*>(p.lo + lines * k);
+    p.lines = (uint32_t)lines;
+    p.k = k;
+    p.nsum = nsum;
+    return p;
+}
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 __host__ __device__ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }

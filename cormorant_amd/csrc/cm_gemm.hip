@@ -163,23 +163,6 @@ __global__ __launch_bounds__(256) void split_kernel(Src src, uint64_t src_slice,
 // Padding is written as the value 128 (A' = 0: the byte pair (0, 0)) and left out of the sums.
 constexpr int16_t kPad = 128;
 
-// The byte planes of 8 int16 values (one 16-byte load): high bytes (1, 3 of each dword) and
-// low bytes (0, 2, top bit flipped) as two 8-byte words.
-__device__ __forceinline__ void split8(const int4 v, uint2& h, uint2& l) {
-    const uint32_t w0 = (uint32_t)v.x, w1 = (uint32_t)v.y, w2 = (uint32_t)v.z, w3 = (uint32_t)v.w;
-    h = make_uint2(__builtin_amdgcn_perm(w1, w0, 0x07050301u), __builtin_amdgcn_perm(w3, w2, 0x07050301u));
-    l = make_uint2(__builtin_amdgcn_perm(w1, w0, 0x06040200u) ^ 0x80808080u,
-                   __builtin_amdgcn_perm(w3, w2, 0x06040200u) ^ 0x80808080u);
-}
-
-__device__ __forceinline__ int32_t sum8(const int4 v) {   // sum of the 8 int16 lanes
-    const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
-    int32_t s = 0;
-#pragma unroll
-    for (int q = 0; q < 4; q++) s += (int32_t)(int16_t)(w[q] & 0xFFFF) + ((int32_t)w[q] >> 16);
-    return s;
-}
-
 // Rows with k contiguous (the matmul A, row stride lda, 16-byte aligned rows): one wavefront
 // per row and SLAB of k, 8 k per lane per 16-byte load, the slab's loads all in flight
 // before the first is used; grid (ceil(lines_p / 4), nslab, slices).
@@ -661,7 +644,7 @@ __device__ __forceinline__ void store_wave_partial(const v16i (&hh)[2][2], const
 // colsum - 16384 K, then sat16(>> 8) -- the kWrap rule of the unsplit kernel.  A lane per 8
 // outputs of a row (m % 8 == 0, 16-byte aligned C rows) or per output.
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(const int32_t* __restrict__ part, const int32_t* __restrict__ rpart,
-                                                          uint64_t rp_slice, uint32_t a_lines,
+                                                          uint64_t rp_slice, uint32_t a_lines, uint32_t nsum_a,
                                                           const int32_t* __restrict__ cpart, uint64_t cp_slice,
                                                           uint32_t b_lines, uint32_t nslab, int16_t* __restrict__ c,
                                                           uint64_t c_bs, uint32_t n, uint32_t m, uint32_t nz,
@@ -673,7 +656,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const int32_t* __restr
         const uint64_t bt = e / (per / w), i = (e - bt * (per / w)) * w;
         const uint32_t row = (uint32_t)(i / m), col = (uint32_t)(i - (uint64_t)row * m);
         int32_t rs = 0;
-        for (uint32_t q = 0; q < nslab; q++) rs += rpart[bt * rp_slice + (uint64_t)q * a_lines + row];
+        for (uint32_t q = 0; q < nsum_a; q++) rs += rpart[bt * rp_slice + (uint64_t)q * a_lines + row];
         const uint32_t base = 128u * (uint32_t)rs - 16384u * k;
         if (vec) {
             uint32_t acc[8];
@@ -739,7 +722,7 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
     const int8_t* __restrict__ Ahi, const int8_t* __restrict__ Alo, const int32_t* __restrict__ rpart,
     uint64_t a_slice, uint64_t rp_slice, uint32_t a_lines, const int8_t* __restrict__ Bhi,
     const int8_t* __restrict__ Blo, const int32_t* __restrict__ cpart, uint64_t b_slice, uint64_t cp_slice,
-    uint32_t b_lines, uint32_t nslab, uint32_t tiles_r, uint32_t tiles_c, uint32_t kp, int32_t k64,
+    uint32_t b_lines, uint32_t nslab, uint32_t nsum_a, uint32_t tiles_r, uint32_t tiles_c, uint32_t kp, int32_t k64,
     uint32_t mode, int32_t* __restrict__ pout, uint32_t ksteps, Epi epi) {
     constexpr int TM = 64 * WR;                  // tile rows
     constexpr int NT = 128 * WR;                 // threads
@@ -792,7 +775,8 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
             const int32_t* pp = is_row ? rpart + bt * rp_slice + line : cpart + bt * cp_slice + line;
             const uint32_t stride = is_row ? a_lines : b_lines;
             int32_t sum = tsum[q];
-            for (uint32_t sl = 1; sl < nslab; sl++) sum += pp[(uint64_t)sl * stride];
+            const uint32_t ns = is_row ? nsum_a : nslab;
+            for (uint32_t sl = 1; sl < ns; sl++) sum += pp[(uint64_t)sl * stride];
             if (is_row) rterm[e] = make_int2(epi.row_bias(line) - k64 + (sum >> 1), (sum & 1) << 7);
             else cterm[e - TM] = make_int2(sum >> 1, (sum & 1) << 7);
         }
@@ -1489,6 +1473,8 @@ struct Planes {
     uint32_t lines_p, kp, nslab, slices;
     uint32_t tile = 128;                 // GEMM tile rows when this is the A operand
     uint32_t rows = 0;                   // real lines (the rest up to lines_p are padding)
+    uint32_t sums = 0;                   // partial line sums per line (0: one per slab)
+    uint32_t nsum() const { return sums ? sums : nslab; }
     size_t bytes() const {
         return (size_t)slices * lines_p * kp * 2 + (size_t)slices * nslab * lines_p * 4 + 1024;
     }
@@ -1534,16 +1520,16 @@ int run_gemm(const Planes& A, const Planes& B, uint32_t batch, uint32_t k, Epi e
     const dim3 grid(tiles_r * tiles_c, batch, nz);
     if (tm == 256) {
         CM_LAUNCH("gemm_planes_kernel", (gemm_planes_kernel<4, 3, Epi>), grid, dim3(512), 0, s, A.hi, A.lo, A.part,
-                  a_slice, rp_slice, A.lines_p, B.hi, B.lo, B.part, b_slice, cp_slice, B.lines_p, A.nslab, tiles_r,
-                  tiles_c, A.kp, (int32_t)(64 * k), mode, pout, ksteps, epi);
+                  a_slice, rp_slice, A.lines_p, B.hi, B.lo, B.part, b_slice, cp_slice, B.lines_p, B.nslab, A.nsum(),
+                  tiles_r, tiles_c, A.kp, (int32_t)(64 * k), mode, pout, ksteps, epi);
     } else if (tm == 64) {
         CM_LAUNCH("gemm_planes_kernel", (gemm_planes_kernel<1, 2, Epi>), grid, dim3(128), 0, s, A.hi, A.lo, A.part,
-                  a_slice, rp_slice, A.lines_p, B.hi, B.lo, B.part, b_slice, cp_slice, B.lines_p, A.nslab, tiles_r,
-                  tiles_c, A.kp, (int32_t)(64 * k), mode, pout, ksteps, epi);
+                  a_slice, rp_slice, A.lines_p, B.hi, B.lo, B.part, b_slice, cp_slice, B.lines_p, B.nslab, A.nsum(),
+                  tiles_r, tiles_c, A.kp, (int32_t)(64 * k), mode, pout, ksteps, epi);
     } else {
         CM_LAUNCH("gemm_planes_kernel", (gemm_planes_kernel<2, 2, Epi>), grid, dim3(256), 0, s, A.hi, A.lo, A.part,
-                  a_slice, rp_slice, A.lines_p, B.hi, B.lo, B.part, b_slice, cp_slice, B.lines_p, A.nslab, tiles_r,
-                  tiles_c, A.kp, (int32_t)(64 * k), mode, pout, ksteps, epi);
+                  a_slice, rp_slice, A.lines_p, B.hi, B.lo, B.part, b_slice, cp_slice, B.lines_p, B.nslab, A.nsum(),
+                  tiles_r, tiles_c, A.kp, (int32_t)(64 * k), mode, pout, ksteps, epi);
     }
     return CM_OK;
 }
@@ -1708,7 +1694,8 @@ int gemm_out(const Planes& A, const Planes& B, int16_t* c, uint32_t n, uint32_t 
     const uint64_t total = (uint64_t)batch * n * m / (vec ? 8 : 1);
     const unsigned blocks = (unsigned)std::min<uint64_t>((total + 255) / 256, 65536ull * 8);
     CM_LAUNCH("gemm_reduce_kernel", gemm_reduce_kernel, dim3(blocks), dim3(256), 0, s, pout, A.part, rp_slice,
-              A.lines_p, B.part, cp_slice, B.lines_p, A.nslab, c, (uint64_t)c_bs, n, m, nz, batch, k, vec ? 1u : 0u);
+              A.lines_p, A.nsum(), B.part, cp_slice, B.lines_p, B.nslab, c, (uint64_t)c_bs, n, m, nz, batch, k,
+              vec ? 1u : 0u);
     return CM_OK;
 }
 
@@ -1844,6 +1831,42 @@ extern "C" int cm_matmul_planes(const int16_t* a, const void* b_planes, int16_t*
     rc = split_a(a, sa > 1 ? (uint64_t)a_bs : 0, n, k, A, s);
     if (rc) return rc;
     return gemm_out(A, B, c, n, k, m, batch, c_bs, wrap32, s, reinterpret_cast<int32_t*>(p), ksteps);
+}
+
+extern "C" size_t cm_matmul_a_planes_bytes(uint32_t n, uint32_t k, uint32_t nsum) {
+    return cm::a_planes_bytes(n, k, nsum);
+}
+
+extern "C" int cm_matmul_aplanes(const void* a_planes, uint32_t nsum, const void* b_planes, int16_t* c, uint32_t n,
+                                 uint32_t k, uint32_t m, uint32_t wrap32, void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    if (n == 0 || m == 0) return CM_OK;
+    rc = matmul_check(k, 0, 0, 0, 0);
+    if (rc) return rc;
+    if ((k % BK) || nsum == 0 || nsum > 64) return fail(CM_EINVAL, "matmul: A planes of k %u (a multiple of 64), %u sums", k, nsum);
+    if ((reinterpret_cast<uintptr_t>(a_planes) & 255) || (reinterpret_cast<uintptr_t>(b_planes) & 255))
+        return fail(CM_EALIGN, "matmul: planes not 256-byte aligned");
+    hipStream_t s = as_stream(stream);
+    const APlanes ap = a_planes_view(const_cast<void*>(a_planes), n, k, nsum);
+    Planes A = make_planes(n, k, 1, gemm_tile_rows(n, m, 1, st->cus)), B = make_planes(m, k, 1);
+    A.hi = ap.hi;
+    A.lo = ap.lo;
+    A.part = ap.part;
+    A.lines_p = ap.lines;
+    A.sums = nsum;
+    char* q = static_cast<char*>(const_cast<void*>(b_planes));
+    B.carve(q);
+    size_t pbytes;
+    const uint32_t ksteps = matmul_ksteps(A, B, n, m, 1, wrap32, st, &pbytes);
+    void* ws = nullptr;
+    if (pbytes) {
+        rc = workspace(st, pbytes, &ws, s);
+        if (rc) return rc;
+    }
+    return gemm_out(A, B, c, n, k, m, 1, 0, wrap32, s, static_cast<int32_t*>(ws), ksteps);
 }
 
 namespace cm {

@@ -260,7 +260,7 @@ __device__ __forceinline__ u64 shfl64(u64 v, int off) {
 }
 
 // One unit's outputs in 128-bit arithmetic, for the rows or elements outside the 64-bit bounds.
-__device__ __forceinline__ void norm_unit_wide(const int (&x)[8], uint32_t u, uint32_t units, bool ln, uint32_t n,
+__device__ __noinline__ void norm_unit_wide(const int (&x)[8], uint32_t u, uint32_t units, bool ln, uint32_t n,
                                             i64 s1, u64 Rm,
                                             int shp, const uint4* lds, bool bcast, int (&r)[8]) {
     for (int l = 0; l < 8; l++) {
@@ -272,11 +272,62 @@ __device__ __forceinline__ void norm_unit_wide(const int (&x)[8], uint32_t u, ui
     }
 }
 
+// One COPY / ADDX unit in 128-bit arithmetic (the scale flag, or shifts past the 64-bit bounds).
+__device__ __noinline__ void addx_unit_wide(const int (&x)[8], const int (&y)[8], bool ben, int ck, uint32_t u,
+                                            uint32_t units, uint32_t bq_sh, bool scale, const uint4* lds, bool bcast, int (&r)[8]) {
+    for (int l = 0; l < 8; l++) {
+        const Param q = param_of(lds[bcast ? 0u : l * units + u]);
+        const i128 s = ((i128)x[l] << q.sa) + ((i128)(ben ? y[l] : 0) << q.sb) + ((i128)q.bq << bq_sh);
+        const i128 v = rne_shr(scale ? s * (i128)q.g : s, q.sc);
+        r[l] = (int)(ck == 0 ? sat16(v) : sat32(v));
+    }
+}
+
+// One COPY / ADDX unit: 64-bit arithmetic where the shifts keep every term below 2^61, else
+// the 128-bit form (a branch taken by the lanes that need it).
+template <int BK, int CK, bool BEN>
+__device__ __forceinline__ void addx_unit(const int (&x)[8], const int (&y)[8], uint32_t u, uint32_t units,
+                                          const Job& j, const uint4* ro_lds, bool bcast, bool scale, bool relu,
+                                          int (&r)[8]) {
+    bool wide = scale || j.bq_sh > 40;
+#pragma unroll
+    for (int l = 0; l < 8; l++) {
+        const Param q = param_of(ro_lds[bcast ? 0u : l * units + u]);
+        const i64 yv = BEN ? (i64)y[l] : 0;
+        // each term below 2^61 when: x (32 bits) << sa <= 30, y << sb (16 / 32 bits), Bq (22) << bq_sh <= 40
+        wide |= !(q.sa <= 30 && q.sb <= (BK == 0 ? 46 : 30) && q.sc <= 61);
+        i64 v = rne_shr_fast((i64)x[l] * (i64)((u64)1 << (q.sa & 31)) + yv * (i64)((u64)1 << (q.sb & 63)) +
+                                 q.bq * (i64)((u64)1 << (j.bq_sh & 63)), q.sc & 63);
+        v = CK == 0 ? (v > 32767 ? 32767 : (v < -32768 ? -32768 : v))
+                    : (v > 2147483647 ? 2147483647 : (v < -2147483647LL - 1 ? -2147483647LL - 1 : v));
+        r[l] = (int)v;
+    }
+    if (__any(wide)) {
+        if (wide) addx_unit_wide(x, y, BEN, CK, u, units, j.bq_sh, scale, ro_lds, bcast, r);
+    }
+    if (relu) {
+#pragma unroll
+        for (int l = 0; l < 8; l++) r[l] = r[l] < 0 ? 0 : r[l];
+    }
+}
+
+__device__ __forceinline__ int4 pack16(const int (&r)[8]) {
+    int4 o;
+    o.x = (int)((uint32_t)(uint16_t)r[0] | ((uint32_t)(uint16_t)r[1] << 16));
+    o.y = (int)((uint32_t)(uint16_t)r[2] | ((uint32_t)(uint16_t)r[3] << 16));
+    o.z = (int)((uint32_t)(uint16_t)r[4] | ((uint32_t)(uint16_t)r[5] << 16));
+    o.w = (int)((uint32_t)(uint16_t)r[6] | ((uint32_t)(uint16_t)r[7] << 16));
+    return o;
+}
+
 // One NORM row of the fast path: x[k] = unit lane + 64 k of the row (int32, zero past the
-// row), the staged parameters at lds; the int16 results to rc.  Wavefront-uniform control.
-template <int UPL>
+// row), the staged parameters at lds; the int16 results to rc and, with PL, their byte planes
+// and row sums per 1024 columns (unit u in sum u / 128 = k / 2) as row `prow` of `po`.
+// Wavefront-uniform control.
+template <int UPL, bool PL>
 __device__ __forceinline__ void norm_row(const Job& j, const int (&x)[UPL][8], uint8_t* rc, const uint4* ro_lds,
-                                         bool bcast, const uint8_t* tab, uint32_t lane, uint32_t units, bool ln) {
+                                         bool bcast, const uint8_t* tab, uint32_t lane, uint32_t units, bool ln,
+                                         const APlanes& po, u64 prow) {
     i64 s1 = 0;
     u64 lo = 0, hi = 0;
     uint32_t amax = 0;
@@ -314,9 +365,11 @@ __device__ __forceinline__ void norm_row(const Job& j, const int (&x)[UPL][8], u
     const u64 abound = ln ? (u64)j.n * amax + (u64)(s1 < 0 ? -s1 : s1) : (u64)amax;
     const bool a32 = abound < ((u64)1 << 31);
     bool wide = !a32;
+    int4 o[UPL];
 #pragma unroll
     for (int k = 0; k < UPL; k++) {
         const uint32_t u = lane + 64 * k;
+        o[k] = make_int4(0, 0, 0, 0);
         if (!a32 || u >= units) continue;           // a32 is uniform over the wavefront
         int r[8];
 #pragma unroll
@@ -332,103 +385,109 @@ __device__ __forceinline__ void norm_row(const Job& j, const int (&x)[UPL][8], u
             const i64 v = rne_shr_fast((i64)(int32_t)P1 * G + bs, sc);
             r[l] = v > 32767 ? 32767 : (v < -32768 ? -32768 : (int)v);
         }
-        int4 o;
-        o.x = (int)((uint32_t)(uint16_t)r[0] | ((uint32_t)(uint16_t)r[1] << 16));
-        o.y = (int)((uint32_t)(uint16_t)r[2] | ((uint32_t)(uint16_t)r[3] << 16));
-        o.z = (int)((uint32_t)(uint16_t)r[4] | ((uint32_t)(uint16_t)r[5] << 16));
-        o.w = (int)((uint32_t)(uint16_t)r[6] | ((uint32_t)(uint16_t)r[7] << 16));
-        store_stream(rc + 16u * u, o);
+        o[k] = pack16(r);
     }
-    // rows with a value outside the 64-bit bounds: the whole row again in 128 bits, over
-    // the stores above (a branch uniform over the wavefront)
+    // rows with a value outside the 64-bit bounds: the whole row in 128 bits (a branch uniform
+    // over the wavefront)
     if (__any(wide)) {
         for (int k = 0; k < UPL; k++) {
             const uint32_t u = lane + 64 * k;
             if (u >= units) continue;
             int r[8];
             norm_unit_wide(x[k], u, units, ln, j.n, s1, Rm, shp, ro_lds, bcast, r);
-            int4 o;
-            o.x = (int)((uint32_t)(uint16_t)r[0] | ((uint32_t)(uint16_t)r[1] << 16));
-            o.y = (int)((uint32_t)(uint16_t)r[2] | ((uint32_t)(uint16_t)r[3] << 16));
-            o.z = (int)((uint32_t)(uint16_t)r[4] | ((uint32_t)(uint16_t)r[5] << 16));
-            o.w = (int)((uint32_t)(uint16_t)r[6] | ((uint32_t)(uint16_t)r[7] << 16));
-            store_stream(rc + 16u * u, o);
+            o[k] = pack16(r);
+        }
+    }
+    int32_t ps[UPL];
+#pragma unroll
+    for (int k = 0; k < UPL; k++) {
+        const uint32_t u = lane + 64 * k;
+        ps[k] = 0;
+        if (u >= units) continue;
+        store_stream(rc + 16u * u, o[k]);
+        if constexpr (PL) {
+            uint2 h, l;
+            split8(o[k], h, l);
+            *reinterpret_cast<uint2*>(po.hi + prow * po.k + 8u * u) = h;
+            *reinterpret_cast<uint2*>(po.lo + prow * po.k + 8u * u) = l;
+            ps[k] = sum8(o[k]);
+        }
+    }
+    if constexpr (PL) {
+#pragma unroll
+        for (int sl = 0; sl < (UPL + 1) / 2; sl++) {
+            int32_t v = ps[2 * sl] + (2 * sl + 1 < UPL ? ps[2 * sl + 1] : 0);
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+            if (lane == 0 && (uint32_t)sl < po.nsum) po.part[(u64)sl * po.lines + prow] = v;
         }
     }
 }
 
 // NORM: a wavefront per row (rows in turn over the grid), the row held in registers between
-// the sums and the output: UPL units of 8 elements per lane, n <= 512 UPL.
-template <int AK, int UPL>
+// the sums and the output: UPL units of 8 elements per lane, n <= 512 UPL.  With ADDX the row
+// is first the output of the COPY / ADDX job `ja` (int32, AK int32 or int16 A, int16 B, its
+// parameters staged after the NORM's), stored to ja.c and normalised from the registers: the
+// two-job chain ADDX -> NORM with one read of each row.  PL: the byte planes of the output.
+template <int AK, int UPL, bool ADDX, bool PL>
 __global__ __launch_bounds__(256) void ro_norm_fast_kernel(Job j, const uint8_t* __restrict__ params,
                                                            uint8_t* pram_dst, uint32_t p_entries, bool bcast,
-                                                           const uint8_t* __restrict__ tab) {
+                                                           const uint8_t* __restrict__ tab, Job ja,
+                                                           const uint8_t* __restrict__ pa, bool bca, APlanes po) {
     extern __shared__ __attribute__((aligned(16))) uint4 ro_lds[];
     const uint32_t lane = threadIdx.x & 63;
     const u64 rows = (u64)j.c1 * j.c2;
     const bool ln = (j.op & F_NORM_LN) != 0;
     const uint32_t units = j.n / 8;
     const u64 stride = (u64)gridDim.x * (blockDim.x >> 6);
-    int x[UPL][8];
+    const uint32_t nsl = bcast ? 1u : j.n;
+    uint4* a_lds = ro_lds + nsl;                          // the ADDX job's parameters
+    int x[UPL][8], y[UPL][8];
     auto load_row = [&](u64 row) {
-        const uint8_t* ra = j.a + (u64)(uint32_t)(row / j.c1) * j.a_s2 + (u64)(uint32_t)(row % j.c1) * j.a_s1;
+        const Job& jl = ADDX ? ja : j;
+        const uint32_t i1 = (uint32_t)(row % jl.c1), i2 = (uint32_t)(row / jl.c1);
+        const uint8_t* ra = jl.a + (u64)i2 * jl.a_s2 + (u64)i1 * jl.a_s1;
 #pragma unroll
         for (int k = 0; k < UPL; k++) {
             const uint32_t u = lane + 64 * k;
-            if (u < units) ld_unit<AK>(ra, u, x[k]);
-            else {
+            if (u < units) {
+                ld_unit<AK>(ra, u, x[k]);
+                if constexpr (ADDX) ld_unit<0>(ja.b + (u64)i2 * ja.b_s2 + (u64)i1 * ja.b_s1, u, y[k]);
+            } else {
 #pragma unroll
-                for (int l = 0; l < 8; l++) x[k][l] = 0;
+                for (int l = 0; l < 8; l++) x[k][l] = y[k][l] = 0;
             }
         }
     };
     u64 row = (u64)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row < rows) load_row(row);                       // in flight while the parameters are staged
     pram_load(params, pram_dst, p_entries);
-    stage_norm_params(ro_lds, params, bcast ? 1u : j.n, units, j.bq_sh);
+    if constexpr (ADDX) {
+        for (uint32_t i = threadIdx.x; i < (bca ? 1u : ja.n); i += blockDim.x)
+            a_lds[pslot(i, units)] = reinterpret_cast<const uint4*>(pa)[i];
+    }
+    stage_norm_params(ro_lds, params, nsl, units, j.bq_sh);
+    const bool scale = (ja.op & F_SCALE) != 0, relu = (ja.op & F_RELU) != 0;
     for (; row < rows; row += stride) {
         const uint32_t i1 = (uint32_t)(row % j.c1), i2 = (uint32_t)(row / j.c1);
-        norm_row<UPL>(j, x, j.c + (u64)i2 * j.c_s2 + (u64)i1 * j.c_s1, ro_lds, bcast, tab, lane, units, ln);
+        if constexpr (ADDX) {
+            // the ADDX outputs (int32) replace the row in registers and go to ja.c
+            uint8_t* rc1 = ja.c + (u64)i2 * ja.c_s2 + (u64)i1 * ja.c_s1;
+#pragma unroll
+            for (int k = 0; k < UPL; k++) {
+                const uint32_t u = lane + 64 * k;
+                if (u >= units) continue;
+                int r[8];
+                addx_unit<0, 1, true>(x[k], y[k], u, units, ja, a_lds, bca, scale, relu, r);
+                store_stream(rc1 + 32u * u, make_int4(r[0], r[1], r[2], r[3]));
+                store_stream(rc1 + 32u * u + 16, make_int4(r[4], r[5], r[6], r[7]));
+#pragma unroll
+                for (int l = 0; l < 8; l++) x[k][l] = r[l];
+            }
+        }
+        norm_row<UPL, PL>(j, x, j.c + (u64)i2 * j.c_s2 + (u64)i1 * j.c_s1, ro_lds, bcast, tab, lane, units, ln, po,
+                          row);
         if (row + stride < rows) load_row(row + stride);
-    }
-}
-
-// One COPY / ADDX unit in 128-bit arithmetic (the scale flag, or shifts past the 64-bit bounds).
-__device__ __forceinline__ void addx_unit_wide(const int (&x)[8], const int (&y)[8], bool ben, int ck, uint32_t u,
-                                            uint32_t units, uint32_t bq_sh, bool scale, const uint4* lds, bool bcast, int (&r)[8]) {
-    for (int l = 0; l < 8; l++) {
-        const Param q = param_of(lds[bcast ? 0u : l * units + u]);
-        const i128 s = ((i128)x[l] << q.sa) + ((i128)(ben ? y[l] : 0) << q.sb) + ((i128)q.bq << bq_sh);
-        const i128 v = rne_shr(scale ? s * (i128)q.g : s, q.sc);
-        r[l] = (int)(ck == 0 ? sat16(v) : sat32(v));
-    }
-}
-
-// One COPY / ADDX unit: 64-bit arithmetic where the shifts keep every term below 2^61, else
-// the 128-bit form (a branch taken by the lanes that need it).
-template <int BK, int CK, bool BEN>
-__device__ __forceinline__ void addx_unit(const int (&x)[8], const int (&y)[8], uint32_t u, uint32_t units,
-                                          const Job& j, const uint4* ro_lds, bool bcast, bool scale, bool relu,
-                                          int (&r)[8]) {
-    bool wide = scale || j.bq_sh > 40;
-#pragma unroll
-    for (int l = 0; l < 8; l++) {
-        const Param q = param_of(ro_lds[bcast ? 0u : l * units + u]);
-        const i64 yv = BEN ? (i64)y[l] : 0;
-        // each term below 2^61 when: x (32 bits) << sa <= 30, y << sb (16 / 32 bits), Bq (22) << bq_sh <= 40
-        wide |= !(q.sa <= 30 && q.sb <= (BK == 0 ? 46 : 30) && q.sc <= 61);
-        i64 v = rne_shr_fast((i64)x[l] * (i64)((u64)1 << (q.sa & 31)) + yv * (i64)((u64)1 << (q.sb & 63)) +
-                                 q.bq * (i64)((u64)1 << (j.bq_sh & 63)), q.sc & 63);
-        v = CK == 0 ? (v > 32767 ? 32767 : (v < -32768 ? -32768 : v))
-                    : (v > 2147483647 ? 2147483647 : (v < -2147483647LL - 1 ? -2147483647LL - 1 : v));
-        r[l] = (int)v;
-    }
-    if (__any(wide)) {
-        if (wide) addx_unit_wide(x, y, BEN, CK, u, units, j.bq_sh, scale, ro_lds, bcast, r);
-    }
-    if (relu) {
-#pragma unroll
-        for (int l = 0; l < 8; l++) r[l] = r[l] < 0 ? 0 : r[l];
     }
 }
 
@@ -585,6 +644,45 @@ unsigned grid_for(u64 items, unsigned per_block = 256) {
     return (unsigned)(b ? b : 1);
 }
 
+bool norm_fast_ok(const Job& j) {
+    const uint32_t ak = (j.op >> 4) & 3;
+    const bool a_words = aligned16(j.a) && (j.a_s1 & 15) == 0 && (j.a_s2 & 15) == 0;
+    return (j.n & 7) == 0 && a_words && ak <= 1 && j.bq_sh <= 40;
+}
+
+// The fast NORM of job j (norm_fast_ok), after the ADDX job `ja` with parameters pa (ADDX),
+// writing the byte planes `po` of its output (PL).
+int run_norm_fast(DeviceState* st, const Job& j, const uint8_t* params, uint8_t* dst, uint32_t entries, bool bcast,
+                  const Job* ja, const uint8_t* pa, bool bca, const APlanes* po, hipStream_t s) {
+    const uint32_t units = j.n / 8;
+    const uint32_t upl = units <= 64 ? 1 : units <= 128 ? 2 : units <= 256 ? 4 : 8;
+    const unsigned blocks = (unsigned)std::min<u64>(((u64)j.c1 * j.c2 + 3) / 4, (u64)st->cus * 8);
+    const size_t plds = (size_t)((bcast ? 1 : j.n) + (ja != nullptr ? (bca ? 1 : ja->n) : 0)) * 16;
+    const uint32_t ak = ja != nullptr ? (ja->op >> 4) & 3 : (j.op >> 4) & 3;
+    const Job jx = ja != nullptr ? *ja : j;
+    const APlanes pv = po != nullptr ? *po : APlanes{};
+    const uint32_t sel = (ak ? 1u : 0u) | (ja != nullptr ? 2u : 0u) | (po != nullptr ? 4u : 0u);
+#define CM_NORM(AK, U, AX, PL)                                                                                     \
+    CM_LAUNCH("ro_norm_kernel", (ro_norm_fast_kernel<AK, U, AX, PL>), dim3(blocks), dim3(256), plds, s, j, params, \
+              dst, entries, bcast, st->ro_tables, jx, pa, bca, pv)
+#define CM_NORM_U(AK, AX, PL)                                                                                      \
+    if (upl == 1) { CM_NORM(AK, 1, AX, PL); } else if (upl == 2) { CM_NORM(AK, 2, AX, PL); }                        \
+    else if (upl == 4) { CM_NORM(AK, 4, AX, PL); } else { CM_NORM(AK, 8, AX, PL); }
+    switch (sel) {
+    case 0: { CM_NORM_U(0, false, false) } break;
+    case 1: { CM_NORM_U(1, false, false) } break;
+    case 4: { CM_NORM_U(0, false, true) } break;
+    case 5: { CM_NORM_U(1, false, true) } break;
+    case 2: { CM_NORM_U(0, true, false) } break;
+    case 3: { CM_NORM_U(1, true, false) } break;
+    case 6: { CM_NORM_U(0, true, true) } break;
+    default: { CM_NORM_U(1, true, true) } break;
+    }
+#undef CM_NORM_U
+#undef CM_NORM
+    return CM_OK;
+}
+
 int run_job(DeviceState* st, const Job& j, const uint8_t* p, hipStream_t s) {
     const uint32_t code = j.op & 15;
     if (code == RO_TLOAD) {
@@ -640,23 +738,7 @@ int run_job(DeviceState* st, const Job& j, const uint8_t* p, hipStream_t s) {
     const bool b_words = aligned16(j.b) && (j.b_s1 & 15) == 0 && (j.b_s2 & 15) == 0;
     const size_t plds = (size_t)(bcast ? 1 : j.n) * 16;
     if (code == RO_NORM) {
-        if ((j.n & 7) == 0 && a_words && ak <= 1 && j.bq_sh <= 40) {
-            const uint32_t units = j.n / 8;
-            const uint32_t upl = units <= 64 ? 1 : units <= 128 ? 2 : units <= 256 ? 4 : 8;
-            const unsigned blocks = (unsigned)std::min<u64>(((u64)j.c1 * j.c2 + 3) / 4, (u64)st->cus * 8);
-#define CM_NORM(AK, U)                                                                                        \
-    CM_LAUNCH("ro_norm_kernel", (ro_norm_fast_kernel<AK, U>), dim3(blocks), dim3(256), plds, s, j, params, dst, \
-              entries, bcast, st->ro_tables)
-            if (ak == 0) {
-                if (upl == 1) { CM_NORM(0, 1); } else if (upl == 2) { CM_NORM(0, 2); }
-                else if (upl == 4) { CM_NORM(0, 4); } else { CM_NORM(0, 8); }
-            } else {
-                if (upl == 1) { CM_NORM(1, 1); } else if (upl == 2) { CM_NORM(1, 2); }
-                else if (upl == 4) { CM_NORM(1, 4); } else { CM_NORM(1, 8); }
-            }
-#undef CM_NORM
-            return CM_OK;
-        }
+        if (norm_fast_ok(j)) return run_norm_fast(st, j, params, dst, entries, bcast, nullptr, nullptr, false, nullptr, s);
         CM_LAUNCH("ro_norm_kernel", ro_norm_kernel, dim3(grid_for((u64)j.c1 * j.c2, 4)), dim3(256), 0, s, j, params,
                            dst, entries, bcast, st->ro_tables);
         return CM_OK;
@@ -704,16 +786,102 @@ extern "C" int cm_rowops(const void* a, const void* b, void* c, const void* p, u
     return run_job(st, j, static_cast<const uint8_t*>(p), as_stream(stream));
 }
 
-extern "C" int cm_rowops_chain(const cm_rowops_desc* jobs, uint32_t n_jobs, void* stream) {
+namespace cm {
+namespace {
+
+Job job_of(const cm_rowops_desc& d) {
+    return Job{reinterpret_cast<const uint8_t*>(d.a), reinterpret_cast<const uint8_t*>(d.b),
+               reinterpret_cast<uint8_t*>(d.c), d.op, d.n, d.c1, d.c2, d.a_s1, d.a_s2, d.b_s1, d.b_s2, d.c_s1, d.c_s2,
+               d.eps, d.aux, d.bq_sh, d.win_lo, d.win_hi};
+}
+
+// The jobs' own parameter block, 16-byte aligned (P_KEEP jobs are not fused).
+bool own_params(const cm_rowops_desc& d) {
+    return !(d.op & F_P_KEEP) && d.p != 0 && (d.p & 15) == 0;
+}
+
+// Job b is a fast NORM of job a's int32 output over the same rows, and a is a COPY / ADDX of
+// whole 8-element units (int32 or int16 A, int16 B, no window): the pair runs as one launch.
+bool fusable_addx_norm(const cm_rowops_desc& a, const cm_rowops_desc& b) {
+    const uint32_t code = a.op & 15, ak = (a.op >> 4) & 3, bk = (a.op >> 6) & 3, ck = (a.op >> 8) & 3;
+    if ((code != RO_ADDX && code != RO_COPY) || !(a.op & F_B_EN) || ak > 1 || bk != 0 || ck != 1) return false;
+    if ((b.op & 15) != RO_NORM || ((b.op >> 4) & 3) != 1 || !own_params(a) || !own_params(b)) return false;
+    if (a.n != b.n || a.c1 != b.c1 || a.c2 != b.c2 || a.n == 0 || (a.n & 7) || a.n > 4096) return false;
+    if (b.a != a.c || b.a_s1 != a.c_s1 || b.a_s2 != a.c_s2 || a.win_lo != 0 || a.win_hi < a.c1) return false;
+    // both parameter blocks staged in the default 64 KiB of dynamic LDS
+    const size_t plds = 16 * (size_t)(((a.op & F_P_BCAST) ? 1 : a.n) + ((b.op & F_P_BCAST) ? 1 : b.n));
+    if (plds > 65536) return false;
+    const bool words = (a.a & 15) == 0 && (a.b & 15) == 0 && (a.c & 15) == 0 && (b.c & 15) == 0 &&
+                       ((a.a_s1 | a.a_s2 | a.b_s1 | a.b_s2 | a.c_s1 | a.c_s2 | b.c_s1 | b.c_s2) & 15) == 0;
+    return words && norm_fast_ok(job_of(b));
+}
+
+int run_chain(const cm_rowops_desc* jobs, uint32_t n_jobs, void* planes, hipStream_t s) {
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    if (planes != nullptr) {
+        if (n_jobs == 0) return fail(CM_EINVAL, "rowops chain: planes of no job");
+        const cm_rowops_desc& l = jobs[n_jobs - 1];
+        if ((l.op & 15) != RO_NORM || ((l.op >> 8) & 3) != 0 || (l.n % 64) || l.n > 4096 || !own_params(l) ||
+            !norm_fast_ok(job_of(l)) || (l.c & 15) || ((l.c_s1 | l.c_s2) & 15) ||
+            (reinterpret_cast<uintptr_t>(planes) & 255))
+            return fail(CM_EINVAL, "rowops chain: planes need a last NORM job of int16 rows of a multiple of 64 "
+                                   "(its own parameters, 256-byte aligned planes)");
+    }
     for (uint32_t i = 0; i < n_jobs; i++) {
-        const cm_rowops_desc& d = jobs[i];
-        int rc = cm_rowops(reinterpret_cast<const void*>(d.a), reinterpret_cast<const void*>(d.b),
-                           reinterpret_cast<void*>(d.c), reinterpret_cast<const void*>(d.p), d.op, d.n, d.c1,
-                           d.c2, d.a_s1, d.a_s2, d.b_s1, d.b_s2, d.c_s1, d.c_s2, d.eps, d.aux, d.bq_sh,
-                           d.win_lo, d.win_hi, stream);
+        const bool last = i + 1 == n_jobs;
+        const bool fuse = i + 1 < n_jobs && fusable_addx_norm(jobs[i], jobs[i + 1]);
+        const bool pl = planes != nullptr && (last || (fuse && i + 2 == n_jobs));
+        if (!fuse && !pl) {
+            const cm_rowops_desc& d = jobs[i];
+            rc = cm_rowops(reinterpret_cast<const void*>(d.a), reinterpret_cast<const void*>(d.b),
+                           reinterpret_cast<void*>(d.c), reinterpret_cast<const void*>(d.p), d.op, d.n, d.c1, d.c2,
+                           d.a_s1, d.a_s2, d.b_s1, d.b_s2, d.c_s1, d.c_s2, d.eps, d.aux, d.bq_sh, d.win_lo, d.win_hi,
+                           s);
+            if (rc) return rc;
+            continue;
+        }
+        const cm_rowops_desc& dn = jobs[fuse ? i + 1 : i];
+        const Job jn = job_of(dn);
+        if (jn.c1 == 0 || jn.c2 == 0) {
+            i += fuse ? 1 : 0;
+            continue;
+        }
+        Job ja{};
+        const uint8_t* pa = nullptr;
+        bool bca = false;
+        if (fuse) {
+            ja = job_of(jobs[i]);
+            pa = reinterpret_cast<const uint8_t*>(jobs[i].p);
+            bca = (jobs[i].op & F_P_BCAST) != 0;
+        }
+        const bool bcn = (dn.op & F_P_BCAST) != 0;
+        st->pram_valid = true;           // the NORM's block is the one the RAM keeps
+        st->pram_bcast = bcn;
+        APlanes pv{};
+        if (pl) {
+            const uint32_t rows = jn.c1 * jn.c2;
+            pv = a_planes_view(planes, rows, jn.n, (jn.n + 1023) / 1024);
+        }
+        rc = run_norm_fast(st, jn, reinterpret_cast<const uint8_t*>(dn.p), st->ro_pram, bcn ? 1u : jn.n, bcn,
+                           fuse ? &ja : nullptr, pa, bca, pl ? &pv : nullptr, s);
         if (rc) return rc;
+        i += fuse ? 1 : 0;
     }
     return CM_OK;
+}
+
+}  // namespace
+}  // namespace cm
+
+extern "C" int cm_rowops_chain(const cm_rowops_desc* jobs, uint32_t n_jobs, void* stream) {
+    return cm::run_chain(jobs, n_jobs, nullptr, cm::as_stream(stream));
+}
+
+extern "C" int cm_rowops_chain_planes(const cm_rowops_desc* jobs, uint32_t n_jobs, void* planes, void* stream) {
+    if (planes == nullptr) return cm::fail(CM_EINVAL, "rowops chain: no planes buffer");
+    return cm::run_chain(jobs, n_jobs, planes, cm::as_stream(stream));
 }
 
 extern "C" int cm_decode_prep(const int16_t* q, const int16_t* k, const int16_t* v, int16_t* qr, int16_t* kc,

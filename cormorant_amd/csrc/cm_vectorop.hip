@@ -100,6 +100,60 @@ __global__ __launch_bounds__(256) void vectorop_kernel(const int16_t* __restrict
     }
 }
 
+// vectorop_kernel over `outer` runs of `size` elements (size a multiple of 64) whose outputs
+// are the rows of a matmul's A (row o at c + o size), also writing the output's byte planes and
+// its row sums per 1024 columns (APlanes): a wavefront per (row, 1024-column slab), two
+// 8-element units per lane, the slab's sum by a wavefront reduction.  Few workgroups per
+// compute unit (grid-stride) when an activation table is staged.
+template <uint32_t OP>
+__global__ __launch_bounds__(256) void vectorop_planes_kernel(const int16_t* __restrict__ a,
+                                                              const int16_t* __restrict__ b,
+                                                              int16_t* __restrict__ c, uint32_t size,
+                                                              uint32_t outer, uint64_t a_inc, uint64_t b_inc,
+                                                              uint32_t act, uint32_t alpha,
+                                                              const uint8_t* __restrict__ act_tab,
+                                                              uint32_t act_len, APlanes po) {
+    __shared__ __attribute__((aligned(16))) uint8_t tab[kActTabBytes];
+    const bool table = act >= ACT_SILU && act <= ACT_GELU_TANH;
+    if (table) {
+        for (uint32_t i = threadIdx.x; i < (act_len + 15) / 16; i += blockDim.x)
+            reinterpret_cast<int4*>(tab)[i] = reinterpret_cast<const int4*>(act_tab)[i];
+        __syncthreads();
+    }
+    const uint32_t lane = threadIdx.x & 63, units = size / 8, nslab = (size + 1023) / 1024;
+    const uint32_t alpha16 = alpha & 0xFFFFu;
+    const uint64_t tasks = (uint64_t)outer * nslab;
+    for (uint64_t t = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6); t < tasks; t += (uint64_t)gridDim.x * 4) {
+        const uint64_t o = t / nslab;
+        const uint32_t sl = (uint32_t)(t - o * nslab);
+        int32_t sum = 0;
+#pragma unroll
+        for (uint32_t jj = 0; jj < 2; jj++) {
+            const uint32_t u = sl * 128 + jj * 64 + lane;
+            if (u >= units) continue;
+            const uint32_t base = u * 8;
+            const int4 av = *reinterpret_cast<const int4*>(a + o * a_inc + base);
+            int4 bv = make_int4(0, 0, 0, 0);
+            if constexpr (OP < OP_RELU) bv = *reinterpret_cast<const int4*>(b + o * b_inc + base);
+            const int16_t* al = reinterpret_cast<const int16_t*>(&av);
+            const int16_t* bl = reinterpret_cast<const int16_t*>(&bv);
+            int4 cv;
+            int16_t* cl = reinterpret_cast<int16_t*>(&cv);
+#pragma unroll
+            for (int l = 0; l < 8; l++) cl[l] = (int16_t)act_lane(act, op_lane<OP>(al[l], bl[l]), alpha16, tab, act_len);
+            store_stream(c + o * (a_inc + b_inc) + base, cv);
+            uint2 h, lw;
+            split8(cv, h, lw);
+            *reinterpret_cast<uint2*>(po.hi + o * po.k + base) = h;
+            *reinterpret_cast<uint2*>(po.lo + o * po.k + base) = lw;
+            sum += sum8(cv);
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+        if (lane == 0) po.part[(uint64_t)sl * po.lines + o] = sum;
+    }
+}
+
 // ---------------------------------------------------------------- softmax
 // One vector (vectorop_smx.py:50-66): over its first v scores x_j (v = smx_valid),
 //   m = max x_j,  d_j = m - x_j,  y_j = (d_j Cm) >> Cs,
@@ -933,10 +987,11 @@ DecodeAttnFn decode_attn_fn(uint32_t g) {
 template <uint32_t OP>
 int launch_ew(const int16_t* a, const int16_t* b, int16_t* c, uint32_t size, uint32_t outer,
               uint32_t a_inc, uint32_t b_inc, uint32_t act, uint32_t alpha, DeviceState* st,
-              hipStream_t s) {
+              hipStream_t s, void* planes = nullptr) {
     const uint64_t words = (uint64_t)((size + 7) >> 3) * outer;
     const unsigned threads = 256;
     uint64_t blocks = (words + threads - 1) / threads;
+    if (planes != nullptr) blocks = ((uint64_t)outer * ((size + 1023) / 1024) + 3) / 4;   // a wavefront per slab
     if (blocks > 65536ull * 8) blocks = 65536ull * 8;
     const uint8_t* tab = st->act_tab;
     uint32_t len = 0;
@@ -945,6 +1000,12 @@ int launch_ew(const int16_t* a, const int16_t* b, int16_t* c, uint32_t size, uin
         len = st->act_len[act - ACT_SILU];
         // every workgroup stages the table: a few per compute unit, each over many words
         blocks = std::min<uint64_t>(blocks, (uint64_t)st->cus * 4);
+    }
+    if (planes != nullptr) {
+        const APlanes po = a_planes_view(planes, outer, size, (size + 1023) / 1024);
+        CM_LAUNCH("vectorop_kernel", vectorop_planes_kernel<OP>, dim3((unsigned)blocks), dim3(threads), 0, s, a, b,
+                  c, size, outer, (uint64_t)a_inc, (uint64_t)b_inc, act, alpha, tab, len, po);
+        return CM_OK;
     }
     CM_LAUNCH("vectorop_kernel", vectorop_kernel<OP>, dim3((unsigned)blocks), dim3(threads), 0, s, a, b, c,
                        size, outer, (uint64_t)a_inc, (uint64_t)b_inc, act, alpha, tab, len);
@@ -980,6 +1041,34 @@ int prepare_softmax(DeviceState* st) {
 }
 
 }  // namespace cm
+
+extern "C" int cm_vectorop_planes(const int16_t* a, const int16_t* b, int16_t* c, uint32_t size, uint32_t op,
+                                  uint32_t outer, uint32_t a_inc, uint32_t b_inc, uint32_t act, uint32_t alpha,
+                                  void* planes, void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    hipStream_t s = as_stream(stream);
+    if (op > OP_GELU_TANH) return fail(CM_EINVAL, "vectorop planes: op %u (not a softmax)", op);
+    if (act > ACT_GELU_TANH) return fail(CM_EINVAL, "vectorop: act %u", act);
+    if (size % 64 || size > 32768 || a_inc + b_inc != size)
+        return fail(CM_EINVAL, "vectorop planes: runs of %u (a multiple of 64 up to 32768) onto contiguous rows "
+                               "(a_inc + b_inc = %u)", size, a_inc + b_inc);
+    if (!aligned16(a) || !aligned16(c) || (op < OP_RELU && !aligned16(b)) || (reinterpret_cast<uintptr_t>(planes) & 255))
+        return fail(CM_EALIGN, "vectorop planes: a, b, c 16-byte and planes 256-byte aligned");
+    if (outer == 0) return CM_OK;
+    uint32_t ja = (op >= OP_LEAKY && op <= OP_GELU_TANH) ? op - (OP_LEAKY - ACT_LEAKY) : act;
+    switch (op) {
+    case OP_ADD: return launch_ew<OP_ADD>(a, b, c, size, outer, a_inc, b_inc, ja, alpha, st, s, planes);
+    case OP_SUB: return launch_ew<OP_SUB>(a, b, c, size, outer, a_inc, b_inc, ja, alpha, st, s, planes);
+    case OP_MUL: return launch_ew<OP_MUL>(a, b, c, size, outer, a_inc, b_inc, ja, alpha, st, s, planes);
+    case OP_DIV: return launch_ew<OP_DIV>(a, b, c, size, outer, a_inc, b_inc, ja, alpha, st, s, planes);
+    case OP_RELU: return launch_ew<OP_RELU>(a, b, c, size, outer, a_inc, b_inc, ja, alpha, st, s, planes);
+    case OP_RELU6: return launch_ew<OP_RELU6>(a, b, c, size, outer, a_inc, b_inc, ja, alpha, st, s, planes);
+    default: return launch_ew<OP_LEAKY>(a, b, c, size, outer, a_inc, b_inc, ja, alpha, st, s, planes);
+    }
+}
 
 extern "C" int cm_vectorop(const int16_t* a, const int16_t* b, int16_t* c, uint32_t size,
                            uint32_t op, uint32_t outer, uint32_t a_inc, uint32_t b_inc,

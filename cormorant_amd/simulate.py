@@ -82,6 +82,7 @@ class Simulator:
         self._infos: Dict[str, TensorInfo] = {}
         self._params: Dict[int, list] = {}                # row-ops parameter blocks on the device
         self._staging: Dict[tuple, torch.Tensor] = {}     # row-ops nodes' staging buffers
+        self._plan = None                                  # MatMuls fed byte planes by their A's producer
         for t in graph.input_tensors + graph.output_tensors:
             self._infos[t.onnx_name] = t
         for sn in graph.nodes:
@@ -129,7 +130,8 @@ class Simulator:
         for nm in st_names:                      # the states as the pass left them, in place
             if nm in states:
                 states[nm][...] = self._to_values(self._tensor(nm), feeds[nm]).reshape(np.shape(states[nm]))
-        wanted = set(raw) if keep is None else set(keep) | set(st_names)
+        # (names with '#' are a producer's byte planes for a MatMul, not graph tensors)
+        wanted = {nm for nm in raw if "#" not in nm} if keep is None else set(keep) | set(st_names)
         return {name: self._to_values(self._tensor(name), t) for name, t in raw.items() if name in wanted}
 
     def forward_raw(self, raw_inputs: Dict[str, torch.Tensor]) -> Dict[str, torch.Tensor]:
@@ -154,6 +156,13 @@ class Simulator:
                 # a decode linear and the row-ops job on its output (the residual add): one launch
                 self._matmul_output_job(sn, nodes[i], raw)
                 i += 1
+                continue
+            if i < len(nodes) and self._addx_norm_fusable(sn, nodes[i]):
+                # a residual add and the LayerNorm of its output: one launch, both outputs kept
+                self._addx_norm(sn, nodes[i], raw)
+                i += 1
+                continue
+            if self._planes_out(sn) is not None and self._planes_node(sn, raw):
                 continue
             if isinstance(sn, MatmulNode):
                 raw[sn.output.onnx_name] = self._matmul(sn, raw)
@@ -345,6 +354,15 @@ class Simulator:
 
     def _matmul(self, sn: MatmulNode, raw) -> torch.Tensor:
         at, bt, ot = sn.inputs[0], sn.inputs[1], sn.output
+        use = self._plan_planes()[0].get(id(sn))
+        if use is not None and at.onnx_name + "#planes" in raw:
+            # A's producer wrote its byte planes: only B's (split once) remain
+            self._check_exponents(at, bt, ot)
+            n, k, m = int(at.shape[-2]), int(at.shape[-1]), int(bt.shape[-1])
+            c = self._new(ot, n * m)
+            units.matmul_aplanes(raw[at.onnx_name + "#planes"], use[1], self._shared_b_planes(bt, self._get(bt, raw)),
+                                 c, n, k, m, wrap32=self._pow2(at, bt, ot))
+            return c
         a, b = self._get(at, raw), self._get(bt, raw)
         n, k = at.shape[-2], at.shape[-1]
         m = bt.shape[-1]
@@ -371,11 +389,7 @@ class Simulator:
             return c
         if bt.data is not None and b_batch == 1:
             # a shared weight: the packed image (the scheduler's packing), split once
-            planes = self._images.get(bt.onnx_name)
-            if planes is None:
-                img = torch.from_numpy(pack_matmul_b(b.cpu().numpy().reshape(k, m))).to(self.device)
-                planes = units.matmul_b_planes(img, k, m, b_packed=1)
-                self._images[bt.onnx_name] = planes
+            planes = self._shared_b_planes(bt, b)
             units.matmul_planes(a.reshape(-1).contiguous(), planes, c, n, k, m, batch=batch,
                                 a_bs=n * k if a_batch > 1 else 0, c_bs=n * m, wrap32=wrap)
         else:
@@ -383,6 +397,153 @@ class Simulator:
                          a_bs=n * k if a_batch > 1 else 0, b_bs=k * m if b_batch > 1 else 0,
                          c_bs=n * m, wrap32=wrap)
         return c
+
+    def _shared_b_planes(self, bt: TensorInfo, b: torch.Tensor) -> torch.Tensor:
+        """A constant 2-d weight's split image, from its packed image (the scheduler's packing), built once."""
+        planes = self._images.get(bt.onnx_name)
+        if planes is None:
+            k, m = int(bt.shape[-2]), int(bt.shape[-1])
+            img = torch.from_numpy(pack_matmul_b(b.cpu().numpy().reshape(k, m))).to(self.device)
+            planes = units.matmul_b_planes(img, k, m, b_packed=1)
+            self._images[bt.onnx_name] = planes
+        return planes
+
+    # ------------------------------------------------------------------ operands split by their producers
+    def _plan_planes(self):
+        """({id(MatMul): (A's name, partial sums)}, {A's name: (n, k, partial sums)}): the
+        MatMuls of a constant 2-d weight on the plane path (not the skinny products) whose A,
+        n x k with k a multiple of 64, comes from a node that can write A's byte planes as it
+        writes A -- a whole-row NORM job, a VectorOP over rows of k, the fused attention."""
+        if self._plan is not None:
+            return self._plan
+        prod = {sn.output.onnx_name: sn for sn in self._graph.nodes if getattr(sn, "output", None) is not None}
+        consumers, producers = {}, {}
+        for sn in self._graph.nodes:
+            if not isinstance(sn, MatmulNode):
+                continue
+            at, bt, ot = sn.inputs[0], sn.inputs[1], sn.output
+            if bt.data is None or len(bt.shape) != 2 or len(at.shape) != 2 or int(bt.shape[0]) != int(at.shape[1]):
+                continue
+            n, k = int(at.shape[0]), int(at.shape[1])
+            if k % 64 or at.kind != "i16" or (self._pow2(at, bt, ot) and n <= 32):
+                continue
+            nsum = self._planes_sums(prod.get(at.onnx_name), n, k)
+            if nsum is None or producers.get(at.onnx_name, (n, k, nsum)) != (n, k, nsum):
+                continue
+            consumers[id(sn)] = (at.onnx_name, nsum)
+            producers[at.onnx_name] = (n, k, nsum)
+        self._plan = (consumers, producers)
+        return self._plan
+
+    def _planes_sums(self, p, n: int, k: int) -> Optional[int]:
+        """The partial row sums `p` would write with the planes of its n x k output, or None
+        where it cannot write them."""
+        if p is None:
+            return None
+        ot = p.output
+        if isinstance(p, RowOpsAdapter) and getattr(p, "pos_t", None) is None:
+            jobs = p.jobs()
+            if (len(jobs) == 1 and jobs[0].op & 15 == units.RO_NORM and jobs[0].col0 == 0 and jobs[0].n == k
+                    and jobs[0].b_row0 is None and not jobs[0].op & (1 << 14) and (jobs[0].op >> 8) & 3 == 0
+                    and ot.kind == "i16" and p.inputs[0].numel == n * k and self._rows_whole(p, k)):
+                return (k + 1023) // 1024
+            return None
+        if isinstance(p, AttentionNode):
+            cols = p.heads * p.head_dim
+            ok = (p.head_dim == 64 and p.seq in (64, 128, 256, 384) and cols == k and p.batch * p.seq == n
+                  and int(p.inputs[0].shape[-1]) % 8 == 0 and p.q_off % 8 == 0 and p.k_off % 8 == 0
+                  and p.v_off % 8 == 0 and p.heads <= 64)
+            return p.heads if ok else None
+        if isinstance(p, ScheduledNode) and p.op_code <= 9 and ot.numel == n * k and k <= 32768:
+            if p.arity == 1:
+                return (k + 1023) // 1024 if p.inputs[0].numel == n * k else None
+            na, nb = p.inputs[0].numel, p.inputs[1].numel
+            if max(na, nb) == n * k and min(na, nb) == k and n > 1:
+                return (k + 1023) // 1024
+        return None
+
+    def _planes_out(self, sn) -> Optional[tuple]:
+        """(n, k, partial sums) of the planes ``sn`` writes with its output, or None."""
+        out = getattr(sn, "output", None)
+        if out is None or isinstance(sn, MatmulNode):
+            return None
+        return self._plan_planes()[1].get(out.onnx_name)
+
+    def _planes_node(self, sn, raw) -> bool:
+        """Run ``sn`` with the byte planes of its output as well (raw[name + '#planes']); False
+        if it runs the plain way after all."""
+        n, k, nsum = self._planes_out(sn)
+        name = sn.output.onnx_name
+        planes = units.a_planes(n, k, nsum, self.device)
+        if isinstance(sn, RowOpsAdapter):
+            at, ot = sn.inputs[0], sn.output
+            a2d = self._get(at, raw).reshape(n, k)
+            out = torch.empty((n, k), dtype=_TORCH[ot.kind], device=self.device)
+            params = self._params.get(id(sn))
+            if params is None:
+                params = [torch.from_numpy(np.ascontiguousarray(sn.jobs()[0].params, np.uint8)).to(self.device)]
+                self._params[id(sn)] = params
+            units.rowops_jobs([self._whole_row_job(sn, a2d, None, out, params[0])], planes=planes)
+            raw[name] = out.reshape(-1)
+        elif isinstance(sn, AttentionNode):
+            self._attention(sn, raw, planes=planes)
+            raw[name] = self._attention_out
+        else:
+            a = self._get(sn.inputs[0], raw).reshape(-1).contiguous()
+            c = self._new(sn.output, n * k)
+            if sn.arity == 1:
+                units.vectorop_planes(a, None, c, k, sn.op_code, n, k, 0, planes, act=sn.act, alpha=sn.alpha)
+            else:
+                b = self._get(sn.inputs[1], raw).reshape(-1).contiguous()
+                a_inc, b_inc = (k, 0) if a.numel() == n * k else (0, k)
+                units.vectorop_planes(a, b, c, k, sn.op_code, n, a_inc, b_inc, planes, act=sn.act, alpha=sn.alpha)
+            raw[name] = c
+        raw[name + "#planes"] = planes
+        return True
+
+    def _addx_norm_fusable(self, sn, nxt) -> bool:
+        """``sn`` is a one-job COPY / ADDX adapter over whole rows writing int32 and ``nxt`` a
+        one-job NORM adapter over the same whole rows reading that output: one chain call
+        (cm_rowops_chain runs the pair as one launch)."""
+        if not (isinstance(sn, RowOpsAdapter) and isinstance(nxt, RowOpsAdapter) and len(sn.inputs) == 2
+                and len(nxt.inputs) == 1 and nxt.inputs[0].onnx_name == sn.output.onnx_name):
+            return False
+        if getattr(sn, "pos_t", None) is not None or getattr(nxt, "pos_t", None) is not None:
+            return False
+        ja, jn = sn.jobs(), nxt.jobs()
+        if len(ja) != 1 or len(jn) != 1:
+            return False
+        ja, jn = ja[0], jn[0]
+        width = sn.n
+        return (ja.op & 15 in (units.RO_COPY, units.RO_ADDX) and jn.op & 15 == units.RO_NORM and ja.col0 == 0
+                and jn.col0 == 0 and ja.n == width and jn.n == width and ja.b_row0 is None and jn.b_row0 is None
+                and sn.output.kind == "i32" and sn.inputs[1].kind == "i16" and sn.inputs[0].kind in ("i16", "i32")
+                and self._rows_whole(sn, width) and self._rows_whole(nxt, width) and width % 8 == 0
+                and sn.inputs[0].numel == sn.output.numel == nxt.output.numel)
+
+    def _addx_norm(self, sn: RowOpsAdapter, nxt: RowOpsAdapter, raw) -> None:
+        """The residual add and the NORM of its output as one chain (and the NORM's byte planes
+        when a MatMul takes its output as A)."""
+        width = sn.n
+        rows = sn.output.numel // width
+        jobs = []
+        for node in (sn, nxt):
+            params = self._params.get(id(node))
+            if params is None:
+                params = [torch.from_numpy(np.ascontiguousarray(node.jobs()[0].params, np.uint8)).to(self.device)]
+                self._params[id(node)] = params
+            a2d = (self._get(node.inputs[0], raw) if node is sn else out1).reshape(rows, width)
+            b_all = self._get(node.inputs[1], raw) if len(node.inputs) > 1 else None
+            out = torch.empty((rows, width), dtype=_TORCH[node.output.kind], device=self.device)
+            jobs.append(self._whole_row_job(node, a2d, b_all, out, params[0]))
+            if node is sn:
+                out1 = out
+            raw[node.output.onnx_name] = out.reshape(-1)
+        pl = self._planes_out(nxt)
+        planes = units.a_planes(*pl, self.device) if pl is not None else None
+        units.rowops_jobs(jobs, planes=planes)
+        if planes is not None:
+            raw[nxt.output.onnx_name + "#planes"] = planes
 
     def _embed(self, sn: LlmEmbedNode, raw) -> torch.Tensor:
         """The embedding rows gathered on the device from the output-lane image of the table."""
@@ -766,9 +927,10 @@ class Simulator:
         buf[:, :w] = x2d
         return buf, per * _KB[kind], per
 
-    def _attention(self, sn: AttentionNode, raw) -> torch.Tensor:
-        """An encoder layer's attention: one cm_attention call, or (shapes it does not take) the
-        head split, the two contractions and the softmax unit call by call."""
+    def _attention(self, sn: AttentionNode, raw, planes: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """An encoder layer's attention: one cm_attention call (with ``planes``, cm_attention_planes:
+        o's byte planes as well), or (shapes it does not take) the head split, the two
+        contractions and the softmax unit call by call."""
         xt, ot = sn.inputs[0], sn.output
         B, T, H, hd = sn.batch, sn.seq, sn.heads, sn.head_dim
         ld, cols = int(xt.shape[-1]), sn.heads * sn.head_dim
@@ -789,8 +951,14 @@ class Simulator:
         o = self._new(ot)
         if (hd == 64 and T in (64, 128, 256, 384) and ld % 8 == 0 and cols % 8 == 0
                 and sn.q_off % 8 == 0 and sn.k_off % 8 == 0 and sn.v_off % 8 == 0):
+            if planes is not None:
+                units.attention_planes(x, o, B, T, H, hd, ld, sn.q_off, sn.k_off, sn.v_off, sn.cm, sn.cfg, planes)
+                self._attention_out = o
+                return o
             units.attention(x, o, B, T, H, hd, ld, sn.q_off, sn.k_off, sn.v_off, cols, sn.cm, sn.cfg)
             return o
+        if planes is not None:
+            raise SchedulerError(f"attention '{ot.onnx_name}': no planes for this shape")
         if T % 16:
             raise SchedulerError(f"attention '{ot.onnx_name}': the keys-major softmax takes query blocks of 16")
         BH, dev = B * H, self.device

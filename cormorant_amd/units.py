@@ -539,9 +539,77 @@ def rowops(a, b, c, p, op: int, n: int, c1: int, c2: int, a_s1: int, a_s2: int, 
     _lib.check(rc, "cm_rowops")
 
 
-def rowops_jobs(jobs: Sequence[dict]) -> None:
+def a_planes(n: int, k: int, nsum: int, device) -> torch.Tensor:
+    """A new 256-byte aligned uint8 device buffer for the byte planes of an n x k matmul A
+    (cm_matmul_a_planes_bytes) with nsum partial row-sum arrays."""
+    nbytes = int(_lib.lib().cm_matmul_a_planes_bytes(n, k, nsum))
+    buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
+    off = (-buf.data_ptr()) % 256
+    return buf[off:off + nbytes]
+
+
+def _require_planes(planes: torch.Tensor, n: int, k: int, nsum: int) -> None:
+    need = int(_lib.lib().cm_matmul_a_planes_bytes(n, k, nsum))
+    if (not planes.is_cuda or planes.dtype != torch.uint8 or not planes.is_contiguous() or planes.numel() < need
+            or planes.data_ptr() % 256):
+        raise ValueError(f"planes: a 256-byte aligned uint8 GPU buffer of {need} bytes (a_planes)")
+
+
+def matmul_aplanes(a_planes: torch.Tensor, nsum: int, b_planes: torch.Tensor, c: torch.Tensor, n: int, k: int,
+                   m: int, wrap32: bool = False) -> torch.Tensor:
+    """cm_matmul_aplanes: C = A . B with A's planes from its producer (a_planes, nsum row-sum
+    arrays) and B's from matmul_b_planes."""
+    if n and m:
+        _require_planes(a_planes, n, k, nsum)
+        _require(c, "c", torch.int16, n * m)
+        need = int(_lib.lib().cm_matmul_b_planes_bytes(k, m, 1))
+        if b_planes.dtype != torch.uint8 or b_planes.numel() < need or b_planes.data_ptr() % 256:
+            raise ValueError("b_planes: the uint8 image of matmul_b_planes for these k, m")
+    rc = _lib.lib().cm_matmul_aplanes(_ptr(a_planes), nsum, _ptr(b_planes), _ptr(c), n, k, m, int(bool(wrap32)),
+                                      _stream())
+    _lib.check(rc, "cm_matmul_aplanes")
+    return c
+
+
+def vectorop_planes(a: torch.Tensor, b: Optional[torch.Tensor], c: torch.Tensor, size: int, op: int, outer: int,
+                    a_inc: int, b_inc: int, planes: torch.Tensor, act: int = 0, alpha: int = 0) -> torch.Tensor:
+    """cm_vectorop_planes: the VectorOP over `outer` runs of `size` (contiguous output rows) and
+    the byte planes of c for matmul_aplanes (n = outer, k = size, nsum = ceil(size / 1024))."""
+    if outer and size:
+        _require(a, "a", torch.int16, (outer - 1) * a_inc + size)
+        if op < OP_RELU:
+            _require(b, "b", torch.int16, (outer - 1) * b_inc + size)
+        _require(c, "c", torch.int16, outer * size)
+        _require_planes(planes, outer, size, (size + 1023) // 1024)
+    rc = _lib.lib().cm_vectorop_planes(_ptr(a), _ptr(b), _ptr(c), size, op, outer, a_inc, b_inc, act, alpha,
+                                       _ptr(planes), _stream())
+    _lib.check(rc, "cm_vectorop_planes")
+    return c
+
+
+def attention_planes(qkv: torch.Tensor, o: torch.Tensor, batch: int, seq: int, heads: int, head_dim: int, ld: int,
+                     q_off: int, k_off: int, v_off: int, smx_cm: int, smx_cfg: int,
+                     planes: torch.Tensor) -> torch.Tensor:
+    """cm_attention_planes: attention() with o's rows heads x head_dim wide, and o's byte planes
+    for matmul_aplanes (n = batch seq, k = heads head_dim, nsum = heads)."""
+    if batch and heads:
+        cols = heads * head_dim
+        for off in (q_off, k_off, v_off):
+            if off < 0 or off + cols > ld:
+                raise ValueError("attention: head columns past the row")
+        _require(qkv, "qkv", torch.int16, (batch * seq - 1) * ld + max(q_off, k_off, v_off) + cols)
+        _require(o, "o", torch.int16, batch * seq * cols)
+        _require_planes(planes, batch * seq, cols, heads)
+    rc = _lib.lib().cm_attention_planes(_ptr(qkv), _ptr(o), batch, seq, heads, head_dim, ld, q_off, k_off, v_off,
+                                        smx_cm, smx_cfg, _ptr(planes), _stream())
+    _lib.check(rc, "cm_attention_planes")
+    return o
+
+
+def rowops_jobs(jobs: Sequence[dict], planes: Optional[torch.Tensor] = None) -> None:
     """Row-ops jobs in order through cm_rowops_chain, each job a dict of rowops()'s arguments
-    with its own tensors (a / b / c / p: GPU uint8 images or None)."""
+    with its own tensors (a / b / c / p: GPU uint8 images or None); with ``planes``
+    (cm_rowops_chain_planes) also the byte planes of the last job's output."""
     descs = (_lib.CmRowopsDesc * len(jobs))()
     for d, j in zip(descs, jobs):
         ext = rowops_extents(j["op"], j["n"], j["c1"], j["c2"], j["a_s1"], j["a_s2"], j["b_s1"], j["b_s2"],
@@ -563,6 +631,12 @@ def rowops_jobs(jobs: Sequence[dict]) -> None:
         for key in ("a", "b", "c", "p"):
             t = j.get(key)
             setattr(d, key, t.data_ptr() if t is not None else 0)
+    if planes is not None:
+        last = jobs[-1]
+        _require_planes(planes, int(last["c1"]) * int(last["c2"]), int(last["n"]), (int(last["n"]) + 1023) // 1024)
+        rc = _lib.lib().cm_rowops_chain_planes(descs, len(jobs), _ptr(planes), _stream())
+        _lib.check(rc, "cm_rowops_chain_planes")
+        return
     rc = _lib.lib().cm_rowops_chain(descs, len(jobs), _stream())
     _lib.check(rc, "cm_rowops_chain")
 

@@ -100,6 +100,15 @@ int cm_vectorop(const int16_t* a, const int16_t* b, int16_t* c, uint32_t size, u
                 uint32_t outer, uint32_t a_inc, uint32_t b_inc, uint32_t act, uint32_t alpha,
                 uint32_t smx_cm, uint32_t smx_cfg, uint32_t smx_mask, void* stream);
 
+/* cm_vectorop for ops 0..9 over `outer` runs of `size` (a multiple of 64, up to 32768) whose
+ * outputs are contiguous rows (a_inc + b_inc == size), also writing the output's byte planes
+ * for a following cm_matmul_aplanes with A = c (n = outer, k = size): `planes` holds
+ * cm_matmul_a_planes_bytes(outer, size, ceil(size / 1024)) bytes, 256-byte aligned.  c is what
+ * cm_vectorop writes.  No counterpart in the reference: the operand split of this build's
+ * matmul, done by the VectorOP call that produces the operand. */
+int cm_vectorop_planes(const int16_t* a, const int16_t* b, int16_t* c, uint32_t size, uint32_t op, uint32_t outer,
+                       uint32_t a_inc, uint32_t b_inc, uint32_t act, uint32_t alpha, void* planes, void* stream);
+
 /* The softmax unit over a batch of matrices (the per-head VectorOPKernel softmax calls of
  * SoftmaxVopNode / VitAttnSoftmaxVopNode / LlmAttnSoftmaxVopNode, smx_nodes.py:121-338, in
  * one launch): matrix i reads a + i * a_bs and writes c + i * c_bs (elements), each exactly
@@ -191,6 +200,18 @@ int cm_matmul_split_b(const int16_t* b, void* planes, uint32_t k, uint32_t m, ui
 int cm_matmul_planes(const int16_t* a, const void* b_planes, int16_t* c, uint32_t n, uint32_t k, uint32_t m,
                      uint32_t batch, int64_t a_bs, uint32_t b_slices, int64_t c_bs, uint32_t wrap32, void* stream);
 
+/* cm_matmul_planes with A also split already, by the kernel that produced it
+ * (cm_rowops_chain_planes, cm_vectorop_planes, cm_attention_planes): one slice, k a multiple
+ * of 64, C = A . B as cm_matmul(a, b, c, n, k, m, 1, 0, 0, 0, ..., wrap32) computes it from the
+ * int16 A those planes came from.  a_planes: cm_matmul_a_planes_bytes(n, k, nsum) bytes, 256-byte
+ * aligned -- hi and lo byte planes [lines][k] (x - 128 = 256 hi + lo, lo with its top bit
+ * flipped; lines = n rounded up to 256) and nsum partial row-sum arrays [nsum][lines] adding
+ * up to each row's sum.  No counterpart in the reference: the operand split of this build's
+ * matmul, done by the operand's producer. */
+size_t cm_matmul_a_planes_bytes(uint32_t n, uint32_t k, uint32_t nsum);
+int cm_matmul_aplanes(const void* a_planes, uint32_t nsum, const void* b_planes, int16_t* c, uint32_t n, uint32_t k,
+                      uint32_t m, uint32_t wrap32, void* stream);
+
 /* ---------------------------------------------------------------- Conv
  * Replaces ConvKernel (kernels/conv_rtl/model/include/ConvKernel.h:229-259) and the
  * simulator's Conv branches (_simulate.py:121-220, 643-660, 784-812): NCHW x, packed
@@ -269,6 +290,17 @@ typedef struct cm_rowops_desc {
  * the previous ones wrote (ROWOPS_RTL_KERNEL.md section 1.6; no 16-job cap). */
 int cm_rowops_chain(const cm_rowops_desc* jobs, uint32_t n_jobs, void* stream);
 
+/* cm_rowops_chain that also writes the byte planes of the last job's output for a following
+ * cm_matmul_aplanes (A = that output): the last job is a NORM of int16 rows of n elements, n a
+ * multiple of 64, with its own parameter block; `planes` holds cm_matmul_a_planes_bytes(c1 c2,
+ * n, ceil(n / 1024)) bytes, 256-byte aligned (row r of the job grid = i2 c1 + i1).  In both
+ * chain calls a COPY / ADDX job with an int32 output that the next job, a NORM over the same
+ * rows, takes as its A runs with that NORM as one launch (each row read once; the parameter
+ * RAM ends as the NORM leaves it).  No counterpart in the reference: the chain of
+ * ROWOPS_RTL_KERNEL.md section 1.6, with the operand split of this build's matmul folded into
+ * the NORM that produces the operand. */
+int cm_rowops_chain_planes(const cm_rowops_desc* jobs, uint32_t n_jobs, void* planes, void* stream);
+
 /* ---------------------------------------------------------------- Layout
  * The attention's operand moves between the projection MatMuls and the contractions (the
  * reference does them on the host / by DMA: VitAttnPrep and LlmAttnMerge, vit.py:19-32,
@@ -311,6 +343,15 @@ int cm_embed_rows(const void* table, uint32_t table_i16, const int32_t* ids, voi
 int cm_attention(const int16_t* qkv, int16_t* o, uint32_t batch, uint32_t seq, uint32_t heads, uint32_t head_dim,
                  uint64_t ld, uint32_t q_off, uint32_t k_off, uint32_t v_off, uint64_t o_ld, uint32_t smx_cm,
                  uint32_t smx_cfg, void* stream);
+
+/* cm_attention with o's rows exactly heads x 64 wide (o_ld = heads * 64), also writing o's byte
+ * planes for the output projection (cm_matmul_aplanes with A = o: n = batch * seq, k = heads *
+ * 64, nsum = heads): `planes` holds cm_matmul_a_planes_bytes(batch * seq, heads * 64, heads)
+ * bytes, 256-byte aligned.  No counterpart in the reference: the operand split of this
+ * build's matmul, done by the attention that produces the operand. */
+int cm_attention_planes(const int16_t* qkv, int16_t* o, uint32_t batch, uint32_t seq, uint32_t heads,
+                        uint32_t head_dim, uint64_t ld, uint32_t q_off, uint32_t k_off, uint32_t v_off,
+                        uint32_t smx_cm, uint32_t smx_cfg, void* planes, void* stream);
 
 /* One decode step's attention, fused, for `groups` KV groups: group bg's g query rows q[bg g +
  * i][0..hd) against its cache rows kc / vc[bg c + j][0..hd) (head_dim hd 32 or 64, c a
