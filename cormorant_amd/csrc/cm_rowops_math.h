@@ -77,5 +77,165 @@ __device__ __forceinline__ i64 rope_value(const int16_t* row, uint32_t col, uint
     return sat16(rne_shr(s, q.sc));
 }
 
+
+// ---------------------------------------------------------------- NORM rows (fast path)
+// Shared by the row-ops unit's NORM kernels and the kernels that normalise their operand rows
+// themselves (the decode linears' RMSNorm): a wavefront per row, units of 8 elements.
+// rsqrt_bf (rowops_spec.py:104-121): 1/sqrt(D) ~= Rm 2^-sh.
+__device__ __forceinline__ void rsqrt_bf(i128 D, u64& Rm, int& sh, const uint8_t* tab) {
+    const u64 hi = (u64)(D >> 64), lo = (u64)D;
+    const int e = hi ? 128 - __clzll(hi) : (lo ? 64 - __clzll(lo) : 0);
+    int d = e - 32;
+    if (d & 1) d += 1;
+    const i128 Dm = d >= 0 ? (D >> d) : (D << (-d));
+    // Dm lies in [2^30, 2^32): the index is in [2048, 8192); the mask only guards the table
+    const u64 y0 = *reinterpret_cast<const uint32_t*>(tab + 32768 + 4 * ((uint32_t)(Dm >> 19) & 8191u));
+    const u64 t = (u64)(((i128)Dm * (i128)y0) >> 32);
+    const u64 u = (u64)(((i128)t * (i128)y0) >> 32);
+    i128 y1 = (i128)y0 + (((i128)y0 * ((i128)((i64)1 << 30) - (i128)u)) >> 31);
+    if (y1 < ((i128)1 << 31)) y1 = (i128)1 << 31;
+    if (y1 > ((i128)1 << 32) - 1) y1 = ((i128)1 << 32) - 1;
+    Rm = (u64)y1;
+    sh = 47 + d / 2;
+}
+
+__device__ __forceinline__ Param param_of(uint4 w) {
+    Param q;
+    q.g = (int32_t)w.x;
+    q.bq = (i64)((int32_t)(w.y << 10) >> 10);
+    q.sa = w.z & 63;
+    q.sb = (w.z >> 8) & 63;
+    q.sc = (w.z >> 16) & 63;
+    return q;
+}
+
+// The staged parameter blocks hold column 8u + l at slot l units + u, so that the lanes of a
+// wavefront (consecutive units u) read consecutive 16-byte slots; a broadcast block is slot 0.
+__device__ __forceinline__ uint32_t pslot(uint32_t col, uint32_t units) { return (col & 7) * units + (col >> 3); }
+
+// NORM parameters as the element loop uses them: G, the shift sc and Bq 2^bq_sh (bq_sh <= 40:
+// below 2^61), one 16-byte entry per column.
+__device__ __forceinline__ void stage_norm_params(uint4* lds, const uint8_t* params, uint32_t entries,
+                                                  uint32_t units, uint32_t bq_sh) {
+    for (uint32_t i = threadIdx.x; i < entries; i += blockDim.x) {
+        const Param q = param_of(reinterpret_cast<const uint4*>(params)[i]);
+        const u64 bs = (u64)(q.bq * ((i64)1 << bq_sh));
+        lds[pslot(i, units)] = make_uint4((uint32_t)q.g, (uint32_t)q.sc, (uint32_t)bs, (uint32_t)(bs >> 32));
+    }
+}
+
+// Round half to even of v / 2^k for 0 <= k <= 61 and |v| < 1.5 2^62:
+// (v + 2^(k-1) - 1 + bit k of v) >> k, the sum below 2^63.
+__device__ __forceinline__ i64 rne_shr_fast(i64 v, uint32_t k) {
+    if (k == 0) return v;
+    return (v + (((i64)1 << (k - 1)) - 1) + ((v >> k) & 1)) >> k;
+}
+
+__device__ __forceinline__ u64 shfl64(u64 v, int off) {
+    return ((u64)(uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), off, 64) << 32) |
+           (uint32_t)__shfl_xor((int)(uint32_t)v, off, 64);
+}
+
+// One unit's outputs in 128-bit arithmetic, for the rows or elements outside the 64-bit bounds.
+__device__ __noinline__ inline void norm_unit_wide(const int (&x)[8], uint32_t u, uint32_t units, bool ln, uint32_t n,
+                                            i64 s1, u64 Rm,
+                                            int shp, const uint4* lds, bool bcast, int (&r)[8]) {
+    for (int l = 0; l < 8; l++) {
+        const uint4 e = lds[bcast ? 0u : l * units + u];
+        const i128 A = ln ? (i128)n * x[l] - s1 : (i128)x[l];
+        const i128 P1 = (A * (i128)Rm) >> shp;
+        const i64 bs = (i64)(((u64)e.w << 32) | e.z);
+        r[l] = (int)sat16(rne_shr(P1 * (i128)(int32_t)e.x + (i128)bs, (int)e.y));
+    }
+}
+
+__device__ __forceinline__ int4 pack16(const int (&r)[8]) {
+    int4 o;
+    o.x = (int)((uint32_t)(uint16_t)r[0] | ((uint32_t)(uint16_t)r[1] << 16));
+    o.y = (int)((uint32_t)(uint16_t)r[2] | ((uint32_t)(uint16_t)r[3] << 16));
+    o.z = (int)((uint32_t)(uint16_t)r[4] | ((uint32_t)(uint16_t)r[5] << 16));
+    o.w = (int)((uint32_t)(uint16_t)r[6] | ((uint32_t)(uint16_t)r[7] << 16));
+    return o;
+}
+
+// The int16 results of one NORM row (n elements, eps, LN or RMS) of the fast path: x[k] = unit
+// lane + 64 k of the row (int32, zero past the row), the parameters staged by
+// stage_norm_params at lds; 64-bit arithmetic where every element's bounds allow, the whole
+// row in 128 bits otherwise (a branch uniform over the wavefront).
+template <int UPL>
+__device__ __forceinline__ void norm_row_vals(uint32_t n, i64 eps, const int (&x)[UPL][8], const uint4* ro_lds,
+                                              bool bcast, const uint8_t* tab, uint32_t lane, uint32_t units, bool ln,
+                                              int4 (&o)[UPL]) {
+    i64 s1 = 0;
+    u64 lo = 0, hi = 0;
+    uint32_t amax = 0;
+#pragma unroll
+    for (int k = 0; k < UPL; k++) {
+#pragma unroll
+        for (int l = 0; l < 8; l++) {
+            const i64 v = x[k][l];
+            s1 += v;
+            const u64 sq = (u64)(v * v);                 // |x| <= 2^31: x^2 <= 2^62
+            lo += sq;
+            hi += lo < sq ? 1 : 0;
+            const uint32_t av = (uint32_t)(v < 0 ? -v : v);
+            amax = av > amax ? av : amax;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        s1 += (i64)shfl64((u64)s1, off);
+        const u64 olo = shfl64(lo, off), ohi = shfl64(hi, off);
+        const u64 nlo = lo + olo;
+        hi = hi + ohi + (nlo < lo ? 1 : 0);
+        lo = nlo;
+        const uint32_t om = (uint32_t)__shfl_xor((int)amax, off, 64);
+        amax = om > amax ? om : amax;
+    }
+    const i128 S1 = s1, S2 = (i128)(((unsigned __int128)hi << 64) | lo);
+    i128 D = ln ? ((i128)n * S2 - S1 * S1 + (i128)eps) : (S2 + (i128)eps);
+    if (D <= 0) D = 1;
+    u64 Rm;
+    int sh;
+    rsqrt_bf(D, Rm, sh, tab);
+    const int shp = sh - 24;                             // >= 7: sh >= 31
+    // A = n x - S1 (LN) or x in 32 bits for the whole row: A Rm < 2^63
+    const u64 abound = ln ? (u64)n * amax + (u64)(s1 < 0 ? -s1 : s1) : (u64)amax;
+    const bool a32 = abound < ((u64)1 << 31);
+    bool wide = !a32;
+#pragma unroll
+    for (int k = 0; k < UPL; k++) {
+        const uint32_t u = lane + 64 * k;
+        o[k] = make_int4(0, 0, 0, 0);
+        if (!a32 || u >= units) continue;           // a32 is uniform over the wavefront
+        int r[8];
+#pragma unroll
+        for (int l = 0; l < 8; l++) {
+            const uint4 e = ro_lds[bcast ? 0u : l * units + u];
+            const int32_t G = (int32_t)e.x;
+            const uint32_t sc = e.y;
+            const i64 bs = (i64)(((u64)e.w << 32) | e.z);
+            // A in 32 bits (a32): the low 32 bits of n x - S1 are A itself
+            const int32_t A = ln ? (int32_t)((uint32_t)n * (uint32_t)x[k][l] - (uint32_t)s1) : x[k][l];
+            const i64 P1 = ((i64)A * (i64)(uint32_t)Rm) >> shp;
+            wide |= !(P1 < ((i64)1 << 31) && P1 > -((i64)1 << 31) && sc <= 61);
+            const i64 v = rne_shr_fast((i64)(int32_t)P1 * G + bs, sc);
+            r[l] = v > 32767 ? 32767 : (v < -32768 ? -32768 : (int)v);
+        }
+        o[k] = pack16(r);
+    }
+    // rows with a value outside the 64-bit bounds: the whole row in 128 bits (a branch uniform
+    // over the wavefront)
+    if (__any(wide)) {
+        for (int k = 0; k < UPL; k++) {
+            const uint32_t u = lane + 64 * k;
+            if (u >= units) continue;
+            int r[8];
+            norm_unit_wide(x[k], u, units, ln, n, s1, Rm, shp, ro_lds, bcast, r);
+            o[k] = pack16(r);
+        }
+    }
+}
+
 }  // namespace ro
 }  // namespace cm
