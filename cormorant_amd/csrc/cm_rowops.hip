@@ -199,7 +199,7 @@ __device__ __forceinline__ void stage_params(uint4* lds, const uint8_t* params, 
 }
 
 // One COPY / ADDX unit in 128-bit arithmetic (the scale flag, or shifts past the 64-bit bounds).
-__device__ __noinline__ void addx_unit_wide(const int (&x)[8], const int (&y)[8], bool ben, int ck, uint32_t u,
+__device__ __forceinline__ void addx_unit_wide(const int (&x)[8], const int (&y)[8], bool ben, int ck, uint32_t u,
                                             uint32_t units, uint32_t bq_sh, bool scale, const uint4* lds, bool bcast, int (&r)[8]) {
     for (int l = 0; l < 8; l++) {
         const Param q = param_of(lds[bcast ? 0u : l * units + u]);
@@ -377,6 +377,104 @@ __global__ __launch_bounds__(256) void ro_addx_fast_kernel(Job j, const uint8_t*
             store_stream(rc + 32u * u, make_int4(r[0], r[1], r[2], r[3]));
             store_stream(rc + 32u * u + 16, make_int4(r[4], r[5], r[6], r[7]));
         }
+    }
+}
+
+// ---------------------------------------------------------------- fast DEQUANT / MULACT / GATE / ROPE
+// The stream ops over rows of whole 8-element units with 16-byte aligned rows: a lane per unit
+// (units in turn over the grid), the parameter block staged in LDS, 16-byte loads and stores,
+// 64-bit arithmetic where an element's shifts keep every term below 2^62 (sa, sb <= 23 with
+// int16 operands, sc <= 61), the 128-bit rule of ro_stream_kernel otherwise.  DEQUANT goes
+// through float: float(x) 2^-sc is the double route's one rounding (the scaling is exact for
+// |x| < 2^31 and sc <= 63).  ROPE: the unit's rotate-half partner is the unit HD / 2 columns
+// away in the same head (HD a multiple of 16), the table row's cos / sin 8 at a time.  MULACT and
+// GATE come here with B enabled (int16).
+__device__ __forceinline__ i64 silu_fast(i64 gv, const uint8_t* tab) {       // |gv| < 2^39
+    return rne_shr_fast(gv * sig_q(gv, tab), 18);
+}
+
+template <uint32_t CODE>
+__global__ __launch_bounds__(256) void ro_unit_fast_kernel(Job j, const uint8_t* __restrict__ params,
+                                                           uint8_t* pram_dst, uint32_t p_entries, bool bcast,
+                                                           const uint8_t* __restrict__ tab) {
+    extern __shared__ __attribute__((aligned(16))) uint4 ro_lds[];
+    pram_load(params, pram_dst, p_entries);
+    const uint32_t units = j.n / 8;
+    stage_params(ro_lds, params, bcast ? 1u : j.n, units);
+    const u64 total = (u64)units * j.c1 * j.c2;
+    const uint32_t HD = j.aux & 0xFFF, half = HD / 2;
+    for (u64 w = (u64)blockIdx.x * blockDim.x + threadIdx.x; w < total; w += (u64)gridDim.x * blockDim.x) {
+        const uint32_t u = (uint32_t)(w % units);
+        const u64 row = w / units;
+        const uint32_t i1 = (uint32_t)(row % j.c1), i2 = (uint32_t)(row / j.c1);
+        const uint8_t* ra = j.a + (u64)i2 * j.a_s2 + (u64)i1 * j.a_s1;
+        const uint8_t* rb = j.b + (u64)i2 * j.b_s2 + (u64)i1 * j.b_s1;
+        uint8_t* rc = j.c + (u64)i2 * j.c_s2 + (u64)i1 * j.c_s1;
+        int x[8];
+        ld_unit<0>(ra, u, x);
+        if constexpr (CODE == RO_DEQUANT) {
+            float f[8];
+#pragma unroll
+            for (int l = 0; l < 8; l++) {
+                const Param q = param_of(ro_lds[bcast ? 0u : l * units + u]);
+                f[l] = ldexpf((float)x[l], -q.sc);
+            }
+            store_stream(rc + 32u * u, *reinterpret_cast<const int4*>(f));
+            store_stream(rc + 32u * u + 16, *reinterpret_cast<const int4*>(f + 4));
+            continue;
+        }
+        int r[8];
+        if constexpr (CODE == RO_ROPE) {
+            const uint32_t d0 = (8 * u) % HD;
+            const bool lo = d0 < half;
+            int p[8];
+            ld_unit<0>(ra, lo ? u + half / 8 : u - half / 8, p);
+            const int4 c0 = *reinterpret_cast<const int4*>(rb + 4u * d0);
+            const int4 c1 = *reinterpret_cast<const int4*>(rb + 4u * d0 + 16);
+            const int4 s0 = *reinterpret_cast<const int4*>(rb + 4u * (HD + d0));
+            const int4 s1 = *reinterpret_cast<const int4*>(rb + 4u * (HD + d0) + 16);
+            const int cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            const int sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+            for (int l = 0; l < 8; l++) {
+                const Param q = param_of(ro_lds[bcast ? 0u : l * units + u]);
+                const i64 rot = lo ? -(i64)p[l] : (i64)p[l];
+                // |x cos|, |rot sin| <= 2^38 for a table at 2^-23: both terms below 2^61
+                if (q.sa <= 23 && q.sb <= 23 && q.sc <= 61 && abs(cs[l]) <= (1 << 23) && abs(sn[l]) <= (1 << 23)) {
+                    const i64 v = (((i64)x[l] * cs[l]) << q.sa) + ((rot * sn[l]) << q.sb);
+                    r[l] = (int)sat16(rne_shr_fast(v, (uint32_t)q.sc));
+                } else {
+                    const i128 v = (((i128)x[l] * cs[l]) << q.sa) + (((i128)rot * sn[l]) << q.sb);
+                    r[l] = (int)sat16(rne_shr(v, q.sc));
+                }
+            }
+        } else {
+            int y[8];
+            ld_unit<0>(rb, u, y);
+#pragma unroll
+            for (int l = 0; l < 8; l++) {
+                const Param q = param_of(ro_lds[bcast ? 0u : l * units + u]);
+                if constexpr (CODE == RO_MULACT) {
+                    if (q.sa <= 23 && q.sc <= 61) {
+                        const i64 sl = silu_fast((i64)x[l] << q.sa, tab);      // |sl| < 2^37
+                        r[l] = (int)sat16(rne_shr_fast(sl * y[l], (uint32_t)q.sc));
+                    } else {
+                        r[l] = (int)sat16(rne_shr((i128)silu_q((i64)x[l] << q.sa, tab) * y[l], q.sc));
+                    }
+                } else {   // GATE
+                    if (q.sa <= 23 && q.sb <= 23 && q.sc <= 61) {
+                        const i64 th = 2 * sig_q((i64)x[l] << q.sa, tab) - ((i64)1 << 24);
+                        const i64 sg = sig_q((i64)y[l] << q.sb, tab);
+                        r[l] = (int)sat16(rne_shr_fast(th * sg, (uint32_t)q.sc));
+                    } else {
+                        const i64 th = 2 * sig_q((i64)x[l] << q.sa, tab) - ((i64)1 << 24);
+                        const i64 sg = sig_q((i64)y[l] << q.sb, tab);
+                        r[l] = (int)sat16(rne_shr((i128)th * sg, q.sc));
+                    }
+                }
+            }
+        }
+        store_stream(rc + 16u * u, pack16(r));
     }
 }
 
@@ -611,6 +709,22 @@ int run_job(DeviceState* st, const Job& j, const uint8_t* p, hipStream_t s) {
         default: break;
         }
 #undef CM_ADDX
+    }
+    const bool c_words = aligned16(j.c) && (j.c_s1 & 15) == 0 && (j.c_s2 & 15) == 0;
+    if ((code == RO_DEQUANT || code == RO_MULACT || code == RO_GATE || code == RO_ROPE) && (j.n & 7) == 0 &&
+        a_words && c_words && ak == 0 && (code == RO_DEQUANT || ck == 0) &&
+        (code == RO_DEQUANT || (b_words && (code == RO_ROPE || (bk == 0 && ben))))) {
+        const u64 units = (u64)(j.n / 8) * j.c1 * j.c2;
+        const unsigned blocks = (unsigned)std::min<u64>((units + 255) / 256, (u64)st->cus * 16);
+#define CM_UNIT(C)                                                                                                   \
+    CM_LAUNCH("ro_stream_kernel", ro_unit_fast_kernel<C>, dim3(blocks), dim3(256), plds, s, j, params, dst, entries, \
+              bcast, st->ro_tables);                                                                                 \
+    return CM_OK;
+        if (code == RO_DEQUANT) { CM_UNIT(RO_DEQUANT) }
+        if (code == RO_MULACT) { CM_UNIT(RO_MULACT) }
+        if (code == RO_GATE) { CM_UNIT(RO_GATE) }
+        CM_UNIT(RO_ROPE)
+#undef CM_UNIT
     }
     const uint32_t cb = code == RO_DEQUANT ? 4 : (((j.op >> 8) & 3) == 0 ? 2 : 4);
     const u64 words = (u64)((j.n * cb + 15) / 16) * j.c1 * j.c2;

@@ -137,7 +137,7 @@ __device__ __forceinline__ u64 shfl64(u64 v, int off) {
 }
 
 // One unit's outputs in 128-bit arithmetic, for the rows or elements outside the 64-bit bounds.
-__device__ __noinline__ inline void norm_unit_wide(const int (&x)[8], uint32_t u, uint32_t units, bool ln, uint32_t n,
+__device__ __forceinline__ void norm_unit_wide(const int (&x)[8], uint32_t u, uint32_t units, bool ln, uint32_t n,
                                             i64 s1, u64 Rm,
                                             int shp, const uint4* lds, bool bcast, int (&r)[8]) {
     for (int l = 0; l < 8; l++) {

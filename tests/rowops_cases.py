@@ -32,7 +32,19 @@ RO_CASES = [  # label, op word, n, rows, blocks, kinds (a, b, c bytes), param ra
     ("addx_relu_bcast_u8", 2 | (1 << 12) | (1 << 13) | (1 << 15), 104, 4, 3),
     ("norm_ln_i16_64", 5 | (1 << 16), 64, 9, 1),
     ("norm_rms_i16_2048", 5, 2048, 3, 1),
+    # the 16-byte unit kernel of DEQUANT / MULACT / GATE / ROPE: shifts on both sides of its 64-bit
+    # bounds (sa, sb <= 23, sc <= 61), extreme int16 operands, RoPE tables past 2^23
+    ("dequant_i16_u8", 3 | (2 << 8), 512, 4, 2),
+    ("mulact_u8", 4 | (1 << 12), 2560, 3, 2),
+    ("mulact_u8_wide", 4 | (1 << 12), 512, 4, 1),
+    ("gate_u8", 10 | (1 << 12), 512, 3, 2),
+    ("rope_hd64_u8", 6 | (1 << 6), 320, 4, 2),
+    ("rope_hd32_u8_wide", 6 | (1 << 6), 256, 3, 1),
 ]
+
+# parameter / operand ranges of the cases above that differ from their op's defaults
+_WIDE = {"dequant_i16_u8": dict(sc=(0, 63)), "mulact_u8_wide": dict(sh=(15, 40), sc=(20, 63)),
+         "gate_u8": dict(sh=(0, 30), sb=(0, 30), sc=(20, 63)), "rope_hd32_u8_wide": dict(sh=(18, 30), sb=(18, 30), sc=(20, 63))}
 
 
 
@@ -57,10 +69,14 @@ def make_job(case):
         for i1 in range(c1):
             off = i2 * a_s2 + i1 * a_s1
             vals = rng.integers(-lim_a, lim_a, n).astype(np.int16 if ak == 0 else np.int32)
+            if label.endswith("_u8") or "_u8_" in label:
+                vals[:2] = [-lim_a, lim_a - 1]
             a[off:off + kb(ak) * n] = vals.view(np.uint8)
             boff = i2 * b_s2 + i1 * b_s1
             if code == 6:
-                cs = rng.integers(-(1 << 23), 1 << 23, 128).astype(np.int32)
+                tb = 1 << 25 if "wide" in label else 1 << 23
+                cs = rng.integers(-tb, tb, 128).astype(np.int32)
+                cs[:4] = [1 << 23, -(1 << 23), tb - 1, -tb]
                 b[boff:boff + 512] = cs.view(np.uint8)
             else:
                 bv = rng.integers(-32768, 32768, n).astype(np.int16 if bk == 0 else np.int32)
@@ -70,14 +86,14 @@ def make_job(case):
         p = _params(rng, n, 1 << 29, 1 << 31, 1 << 20, sc=(30, 45))
         eps, bq_sh = int(rng.integers(0, 1 << 20)), 20
     elif code == 6:
-        aux = 64
-        p = _params(rng, n, sh=(0, 2), sb=(0, 2), sc=(20, 26))
+        aux = 32 if "hd32" in label else 64
+        p = _params(rng, n, **_WIDE.get(label, dict(sh=(0, 2), sb=(0, 2), sc=(20, 26))))
     elif code == 4:
-        p = _params(rng, n, sh=(0, 6), sc=(14, 30))
+        p = _params(rng, n, **_WIDE.get(label, dict(sh=(0, 6), sc=(14, 30))))
     elif code == 10:
-        p = _params(rng, n, sh=(0, 5), sb=(0, 5), sc=(30, 40))
+        p = _params(rng, n, **_WIDE.get(label, dict(sh=(0, 5), sb=(0, 5), sc=(30, 40))))
     elif code == 3:
-        p = _params(rng, n, sc=(0, 30))
+        p = _params(rng, n, **_WIDE.get(label, dict(sc=(0, 30))))
     elif op & (1 << 17):
         p = _params(rng, n, 0, 1 << 25, 1 << 10, sh=(0, 4), sb=(0, 4), sc=(10, 30))
     else:
