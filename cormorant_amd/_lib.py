@@ -57,6 +57,7 @@ SIGNATURES = {
     "cm_attention": (_I32, [_P, _P] + [_U32] * 4 + [ctypes.c_uint64] + [_U32] * 3 + [ctypes.c_uint64] + [_U32] * 2 + [_P]),
     "cm_decode_attention": (_I32, [_P, _P, _P, _P] + [_U32] * 7 + [_P]),
     "cm_decode_prep": (_I32, [_P] * 6 + [_U32] * 6 + [_P, _P, _U32, _P, _U32, _P]),
+    "cm_decode_attention_prep": (_I32, [_P] * 7 + [_U32] * 6 + [_P, _P, _U32, _P, _U32] + [_U32] * 3 + [_P]),
     "cm_matmul_b_planes_bytes": (ctypes.c_size_t, [_U32] * 3),
     "cm_matmul_split_b": (_I32, [_P, _P, _U32, _U32, _U32, ctypes.c_int64, _U32, _U32, _P]),
     "cm_matmul_planes": (_I32, [_P, _P, _P, _U32, _U32, _U32, _U32, ctypes.c_int64, _U32, ctypes.c_int64, _U32, _P]),

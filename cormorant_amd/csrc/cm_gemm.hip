@@ -1339,14 +1339,20 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(SkinnySegs segs, uin
 // C = sat16(wrap32(A . B) >> 8) for A of at most 16 rows against a weight already split into
 // byte planes (cm_matmul_split_b).  Sixteen rows are exactly one v_mfma_i32_16x16x64_i8
 // operand, so the products run on MFMA over limbs with the plane GEMM's recombination, and a
-// workgroup owns 32 columns for the whole k: its W wavefronts take the 64-k steps w, w + W, ..
-// (the loads of a chunk of kSpChunk steps all in flight before the chunk's products) and add
-// their wrapped partials in LDS, so there are no partial buffers and no second launch.  A is
-// split in registers, 16 k of row l % 16 per lane (the MFMA operand layout), its row sums
-// taken on the way; B's column sums come from the plane image.
-constexpr uint32_t kSpCols = 32;          // columns per workgroup: two 16-column MFMA blocks
-constexpr uint32_t kSpChunk = 4;          // 64-k steps whose loads a wavefront issues together
-constexpr uint32_t kSpMaxWaves = 8;
+// workgroup owns NB 16-column blocks for the whole k: its W wavefronts take the 64-k steps w,
+// w + W, .. (the loads of a chunk of sp_chunk(NB) steps all in flight before the chunk's products)
+// and add their wrapped partials in LDS, so there are no partial buffers and no second launch.
+// A is split in registers, 16 k of row l % 16 per lane (the MFMA operand layout), its row sums
+// taken on the way; B's column sums come from the plane image.  Everything the stores of a
+// thread's first kSpPre output elements read besides the product (B's column sums, the output
+// job's parameter entry and x) is loaded before the products, under the weight loads.  NB
+// trades the workgroups a weight's columns give (one MFMA block each: narrow weights) against
+// the A rows every workgroup reads again (wide ones).
+// 64-k steps whose loads a wavefront issues together, wavefronts of an NB-block workgroup (the
+// register budget of its launch bounds), and the output elements a thread prefetches for
+__host__ __device__ constexpr uint32_t sp_chunk(uint32_t nb) { return nb == 4 ? 2u : 4u; }
+__host__ __device__ constexpr uint32_t sp_max_waves(uint32_t nb) { return nb == 1 ? 16u : 8u; }
+__host__ __device__ constexpr uint32_t sp_pre(uint32_t nb) { return nb == 1 ? 1u : 2u; }
 
 struct SkinnyPlaneSegs {
     const int8_t* hi[kSkinnySegs];
@@ -1367,47 +1373,90 @@ struct SkinnyAddx {
     uint32_t op, bq_sh;
 };
 
-__global__ __launch_bounds__(64 * kSpMaxWaves) void skinny_planes_kernel(const int16_t* __restrict__ a, uint32_t n,
+// The operands of one output element's store other than the product, as loaded (nothing
+// waits for them before the weight loads go out): B's column sums of the first kSpSlabs slabs,
+// the output job's parameter entry and x (int16 or int32).
+constexpr uint32_t kSpSlabs = 4;
+struct SkinnyEpiIn {
+    uint32_t cs[kSpSlabs] = {0, 0, 0, 0};
+    uint4 prm{};
+    int32_t x = 0;
+};
+
+// XK: the output job's x kind (0: no job, 1: int16, 2: int32).
+template <uint32_t NB, uint32_t XK>
+__global__ __launch_bounds__(64 * sp_max_waves(NB)) void skinny_planes_kernel(const int16_t* __restrict__ a, uint32_t n,
                                                                        uint32_t k, uint32_t kp, uint32_t nslab,
                                                                        SkinnyPlaneSegs segs, SkinnyAddx ax) {
-    __shared__ uint32_t red[kSpMaxWaves][16][kSpCols];
-    __shared__ int32_t rsum[kSpMaxWaves][16];
+    constexpr uint32_t COLS = 16 * NB;
+    extern __shared__ __attribute__((aligned(16))) uint32_t sp_lds[];
+    const uint32_t W = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    uint32_t* red = sp_lds;                                  // [W][16][COLS] wrapped partials
+    int32_t* rsum = reinterpret_cast<int32_t*>(sp_lds + W * 16 * COLS);   // [W][16] A row sums
     uint32_t si = 0;
     for (uint32_t i = 1; i < segs.count; i++)
         if (blockIdx.x >= segs.cb0[i]) si = i;
-    const uint32_t c0 = (blockIdx.x - segs.cb0[si]) * kSpCols;
+    const uint32_t c0 = (blockIdx.x - segs.cb0[si]) * COLS;
     const int8_t* __restrict__ bhi = segs.hi[si];
     const int8_t* __restrict__ blo = segs.lo[si];
-    const uint32_t W = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t m = segs.m[si], lp = segs.lines_p[si];
+    const int32_t* __restrict__ part = segs.part[si];
     const uint32_t r = lane & 15, g = lane >> 4;             // A row and B column of a block; k group
     const uint32_t nsteps = kp / 64;
     const bool row_ok = r < n;
     const int16_t* arow = a + (uint64_t)(row_ok ? r : 0) * k;
     const int4 pad8 = make_int4(0x00800080, 0x00800080, 0x00800080, 0x00800080);   // eight kPad: A' = 0
-    v4i hh[2], mid[2], ll[2];
+    const uint32_t ck = (ax.op >> 8) & 3;
+    const bool pb = (ax.op & ro::F_P_BCAST) != 0;
+    // element e of the tile: row e / COLS, column c0 + e % COLS
+    auto epi_in = [&](uint32_t e) {
+        SkinnyEpiIn in;
+        const uint32_t row = e / COLS, col = c0 + e % COLS;
+        if (row >= n || col >= m) return in;
 #pragma unroll
-    for (int b = 0; b < 2; b++) hh[b] = mid[b] = ll[b] = v4i{0, 0, 0, 0};
+        for (uint32_t sl = 0; sl < kSpSlabs; sl++)
+            if (sl < nslab) in.cs[sl] = (uint32_t)part[(uint64_t)sl * lp + col];
+        if constexpr (XK != 0) {
+            in.prm = *reinterpret_cast<const uint4*>(ax.params + 16u * (pb ? 0u : col));
+            const uint64_t ex = (uint64_t)row * m + col;
+            if constexpr (XK == 1) in.x = reinterpret_cast<const int16_t*>(ax.x)[ex];
+            else in.x = reinterpret_cast<const int32_t*>(ax.x)[ex];
+        }
+        return in;
+    };
+    constexpr uint32_t PRE = sp_pre(NB);
+    SkinnyEpiIn pre[PRE];
+#pragma unroll
+    for (uint32_t i = 0; i < PRE; i++) pre[i] = epi_in(threadIdx.x + i * blockDim.x);
+    v4i hh[NB], mid[NB], ll[NB];
+#pragma unroll
+    for (uint32_t b = 0; b < NB; b++) hh[b] = mid[b] = ll[b] = v4i{0, 0, 0, 0};
     int32_t asum = 0;
-    for (uint32_t s0 = wave; s0 < nsteps; s0 += W * kSpChunk) {
-        int4 av[kSpChunk][2];
-        v4i bh[kSpChunk][2], bl[kSpChunk][2];
+    constexpr uint32_t CH = sp_chunk(NB);
+    for (uint32_t s0 = wave; s0 < nsteps; s0 += W * CH) {
+        int4 av[CH][2];
+        v4i bh[CH][NB], bl[CH][NB];
 #pragma unroll
-        for (uint32_t u = 0; u < kSpChunk; u++) {
+        for (uint32_t u = 0; u < CH; u++) {
             const uint32_t st = s0 + u * W;
             const bool live = st < nsteps;
             const uint32_t kk = (live ? st : 0) * 64 + 16 * g;
-            // k % 8 == 0: each half of the lane's 16 k is wholly real or wholly past k
-            av[u][0] = (live && row_ok && kk + 8 <= k) ? *reinterpret_cast<const int4*>(arow + kk) : pad8;
-            av[u][1] = (live && row_ok && kk + 16 <= k) ? *reinterpret_cast<const int4*>(arow + kk + 8) : pad8;
+            // k % 8 == 0: each half of the lane's 16 k is wholly real or wholly past k; a half past
+            // k loads row 0's first 8 (in bounds) and takes the pad instead
+            const bool h0 = live && row_ok && kk + 8 <= k, h1 = live && row_ok && kk + 16 <= k;
+            const int4 a0 = *reinterpret_cast<const int4*>(arow + (h0 ? kk : 0));
+            const int4 a1 = *reinterpret_cast<const int4*>(arow + (h1 ? kk + 8 : 0));
+            av[u][0] = h0 ? a0 : pad8;
+            av[u][1] = h1 ? a1 : pad8;
 #pragma unroll
-            for (int b = 0; b < 2; b++) {
+            for (uint32_t b = 0; b < NB; b++) {
                 const uint64_t off = (uint64_t)(c0 + 16 * b + r) * kp + kk;
                 bh[u][b] = *reinterpret_cast<const v4i*>(bhi + off);
                 bl[u][b] = *reinterpret_cast<const v4i*>(blo + off);
             }
         }
 #pragma unroll
-        for (uint32_t u = 0; u < kSpChunk; u++) {
+        for (uint32_t u = 0; u < CH; u++) {
             if (s0 + u * W >= nsteps) break;                  // wave-uniform
             const uint32_t kk = (s0 + u * W) * 64 + 16 * g;
             if (row_ok && kk + 8 <= k) asum += sum8(av[u][0]);
@@ -1417,51 +1466,52 @@ __global__ __launch_bounds__(64 * kSpMaxWaves) void skinny_planes_kernel(const i
             split8(av[u][1], h1, l1);
             const v4i ah{(int)h0.x, (int)h0.y, (int)h1.x, (int)h1.y}, al{(int)l0.x, (int)l0.y, (int)l1.x, (int)l1.y};
 #pragma unroll
-            for (int b = 0; b < 2; b++) hh[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bh[u][b], hh[b], 0, 0, 0);
+            for (uint32_t b = 0; b < NB; b++) hh[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bh[u][b], hh[b], 0, 0, 0);
 #pragma unroll
-            for (int b = 0; b < 2; b++) mid[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bl[u][b], mid[b], 0, 0, 0);
+            for (uint32_t b = 0; b < NB; b++) mid[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bl[u][b], mid[b], 0, 0, 0);
 #pragma unroll
-            for (int b = 0; b < 2; b++) ll[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bl[u][b], ll[b], 0, 0, 0);
+            for (uint32_t b = 0; b < NB; b++) ll[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bl[u][b], ll[b], 0, 0, 0);
 #pragma unroll
-            for (int b = 0; b < 2; b++) mid[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bh[u][b], mid[b], 0, 0, 0);
+            for (uint32_t b = 0; b < NB; b++) mid[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bh[u][b], mid[b], 0, 0, 0);
         }
     }
     // this wavefront's wrapped partials: lane l holds column l % 16 of each block, rows 4 g .. + 3
 #pragma unroll
-    for (int b = 0; b < 2; b++)
+    for (uint32_t b = 0; b < NB; b++)
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            red[wave][4 * g + i][16 * b + r] =
+            red[(wave * 16 + 4 * g + i) * COLS + 16 * b + r] =
                 ((uint32_t)hh[b][i] << 16) + ((uint32_t)mid[b][i] << 8) + (uint32_t)ll[b][i];
     asum += __shfl_xor(asum, 16, 64);
     asum += __shfl_xor(asum, 32, 64);
-    if (g == 0) rsum[wave][r] = asum;
+    if (g == 0) rsum[wave * 16 + r] = asum;
     __syncthreads();
-    const uint32_t m = segs.m[si], lp = segs.lines_p[si];
-    const int32_t* __restrict__ part = segs.part[si];
     int16_t* __restrict__ c = segs.c[si];
-    for (uint32_t e = threadIdx.x; e < 16 * kSpCols; e += blockDim.x) {
-        const uint32_t row = e / kSpCols, col = c0 + (e - row * kSpCols);
-        if (row >= n || col >= m) continue;
+    auto store = [&](uint32_t e, const SkinnyEpiIn& in) {
+        const uint32_t row = e / COLS, cl = e - row * COLS, col = c0 + cl;
+        if (row >= n || col >= m) return;
         uint32_t acc = 0u - 16384u * k, rs = 0, cs = 0;
         for (uint32_t w = 0; w < W; w++) {
-            acc += red[w][row][col - c0];
-            rs += (uint32_t)rsum[w][row];
+            acc += red[(w * 16 + row) * COLS + cl];
+            rs += (uint32_t)rsum[w * 16 + row];
         }
-        for (uint32_t sl = 0; sl < nslab; sl++) cs += (uint32_t)part[(uint64_t)sl * lp + col];
+#pragma unroll
+        for (uint32_t sl = 0; sl < kSpSlabs; sl++) cs += in.cs[sl];
+        for (uint32_t sl = kSpSlabs; sl < nslab; sl++) cs += (uint32_t)part[(uint64_t)sl * lp + col];
         acc += 128u * rs + 128u * cs;
         const int16_t y = (int16_t)min(max((int32_t)acc >> 8, -32768), 32767);
-        c[(uint64_t)row * m + col] = y;
-        if (ax.out != nullptr) {
-            const uint32_t ak = (ax.op >> 4) & 3, ck = (ax.op >> 8) & 3;
-            const uint64_t e = (uint64_t)row * m + col;
-            const ro::i64 x = ro::ld_kind(ax.x + e * (ak == 0 ? 2 : 4), ak);
-            const ro::i64 r = ro::copy_addx(x, y, ro::ld_param(ax.params, col, (ax.op & ro::F_P_BCAST) != 0), ax.op,
-                                            ax.bq_sh, ck);
-            if (ck == 0) reinterpret_cast<int16_t*>(ax.out)[e] = (int16_t)r;
-            else reinterpret_cast<int32_t*>(ax.out)[e] = (int32_t)r;
+        const uint64_t eo = (uint64_t)row * m + col;
+        c[eo] = y;
+        if constexpr (XK != 0) {
+            const ro::i64 o = ro::copy_addx(in.x, y, ro::param_of(in.prm), ax.op, ax.bq_sh, ck);
+            if (ck == 0) reinterpret_cast<int16_t*>(ax.out)[eo] = (int16_t)o;
+            else reinterpret_cast<int32_t*>(ax.out)[eo] = (int32_t)o;
         }
-    }
+    };
+#pragma unroll
+    for (uint32_t i = 0; i < PRE; i++)
+        if (threadIdx.x + i * blockDim.x < 16 * COLS) store(threadIdx.x + i * blockDim.x, pre[i]);
+    for (uint32_t e = threadIdx.x + PRE * blockDim.x; e < 16 * COLS; e += blockDim.x) store(e, epi_in(e));
 }
 
 // ---------------------------------------------------------------- drivers
@@ -2150,6 +2200,12 @@ extern "C" int cm_matmul_skinny_multi(const int16_t* a, uint32_t n, uint32_t k, 
 namespace cm {
 namespace {
 
+// 16-column blocks a skinny workgroup owns, for a launch of blocks16 blocks over k.
+uint32_t skinny_blocks(uint64_t blocks16, uint32_t k) {
+    (void)k;
+    return blocks16 >= 2048 ? 4u : (blocks16 >= 256 ? 2u : 1u);
+}
+
 int skinny_planes(const int16_t* a, uint32_t n, uint32_t k, uint32_t count, const void* const* b_planes,
                   int16_t* const* c, const uint32_t* m, const SkinnyAddx& ax, hipStream_t s) {
     if (count == 0 || count > kSkinnySegs) return fail(CM_EINVAL, "matmul: %u products (1 .. %u)", count, kSkinnySegs);
@@ -2160,7 +2216,7 @@ int skinny_planes(const int16_t* a, uint32_t n, uint32_t k, uint32_t count, cons
     const uint32_t kp = (uint32_t)round_up(k, BK);
     SkinnyPlaneSegs segs{};
     segs.count = count;
-    uint64_t cbs = 0;
+    uint64_t blocks16 = 0;
     uint32_t nslab = 0;
     for (uint32_t i = 0; i < count; i++) {
         if (m[i] == 0) return fail(CM_EINVAL, "matmul: product %u: m = 0", i);
@@ -2175,14 +2231,37 @@ int skinny_planes(const int16_t* a, uint32_t n, uint32_t k, uint32_t count, cons
         segs.c[i] = c[i];
         segs.m[i] = m[i];
         segs.lines_p[i] = B.lines_p;
-        segs.cb0[i] = (uint32_t)cbs;
         nslab = B.nslab;
-        cbs += ceil_div(m[i], kSpCols);
+        blocks16 += ceil_div(m[i], 16);
+    }
+    const uint32_t nb = skinny_blocks(blocks16, k);
+    uint64_t cbs = 0;
+    for (uint32_t i = 0; i < count; i++) {
+        segs.cb0[i] = (uint32_t)cbs;
+        cbs += ceil_div(m[i], 16 * nb);
     }
     if (cbs > 0x7FFFFFFFull) return fail(CM_EINVAL, "matmul: %llu column blocks", (unsigned long long)cbs);
-    const uint32_t waves = std::min<uint32_t>(kSpMaxWaves, std::max<uint32_t>(1, ceil_div(kp / 64, kSpChunk)));
-    CM_LAUNCH("skinny_planes_kernel", skinny_planes_kernel, dim3((uint32_t)cbs), dim3(64 * waves), 0, s, a, n, k, kp,
-              nslab, segs, ax);
+    const uint32_t waves = std::min<uint32_t>(sp_max_waves(nb), std::max<uint32_t>(1, ceil_div(kp / 64, sp_chunk(nb))));
+    const size_t lds = (size_t)waves * 16 * (16 * nb + 1) * 4;
+    const dim3 grid((uint32_t)cbs), block(64 * waves);
+    const uint32_t xk = ax.out == nullptr ? 0u : (((ax.op >> 4) & 3) == 0 ? 1u : 2u);
+#define CM_SP_LAUNCH(NB_, XK_)                                                                                  \
+    CM_LAUNCH("skinny_planes_kernel", (skinny_planes_kernel<NB_, XK_>), grid, block, lds, s, a, n, k, kp, nslab, \
+              segs, ax)
+    if (xk == 0) {
+        if (nb == 1) { CM_SP_LAUNCH(1, 0); }
+        else if (nb == 2) { CM_SP_LAUNCH(2, 0); }
+        else { CM_SP_LAUNCH(4, 0); }
+    } else if (xk == 1) {
+        if (nb == 1) { CM_SP_LAUNCH(1, 1); }
+        else if (nb == 2) { CM_SP_LAUNCH(2, 1); }
+        else { CM_SP_LAUNCH(4, 1); }
+    } else {
+        if (nb == 1) { CM_SP_LAUNCH(1, 2); }
+        else if (nb == 2) { CM_SP_LAUNCH(2, 2); }
+        else { CM_SP_LAUNCH(4, 2); }
+    }
+#undef CM_SP_LAUNCH
     return CM_OK;
 }
 

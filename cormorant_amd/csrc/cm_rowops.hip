@@ -438,15 +438,7 @@ __global__ __launch_bounds__(256) void ro_unit_fast_kernel(Job j, const uint8_t*
 #pragma unroll
             for (int l = 0; l < 8; l++) {
                 const Param q = param_of(ro_lds[bcast ? 0u : l * units + u]);
-                const i64 rot = lo ? -(i64)p[l] : (i64)p[l];
-                // |x cos|, |rot sin| <= 2^38 for a table at 2^-23: both terms below 2^61
-                if (q.sa <= 23 && q.sb <= 23 && q.sc <= 61 && abs(cs[l]) <= (1 << 23) && abs(sn[l]) <= (1 << 23)) {
-                    const i64 v = (((i64)x[l] * cs[l]) << q.sa) + ((rot * sn[l]) << q.sb);
-                    r[l] = (int)sat16(rne_shr_fast(v, (uint32_t)q.sc));
-                } else {
-                    const i128 v = (((i128)x[l] * cs[l]) << q.sa) + (((i128)rot * sn[l]) << q.sb);
-                    r[l] = (int)sat16(rne_shr(v, q.sc));
-                }
+                r[l] = rope_elem(x[l], lo ? -(i64)p[l] : (i64)p[l], cs[l], sn[l], q);
             }
         } else {
             int y[8];
@@ -565,14 +557,14 @@ __global__ __launch_bounds__(256) void decode_prep_kernel(DecodePrep d) {
         uint32_t out[4] = {0, 0, 0, 0};
         if (r < qw + kw) {
             const bool isq = r < qw;
-            const uint32_t col0 = (isq ? r : r - qw) * 8;
+            const uint32_t col0 = (isq ? r : r - qw) * 8, d0 = col0 % d.HD;
             const int16_t* row = isq ? d.q + (u64)b * d.H * d.HD : d.k + (u64)b * d.KV * d.HD;
-#pragma unroll
-            for (uint32_t l = 0; l < 8; l++) {
-                const uint32_t col = col0 + l;
-                const Param p = ld_param(isq ? d.pq : d.pk, col, (isq ? d.bcq : d.bck) != 0);
-                out[l >> 1] |= ((uint32_t)(uint16_t)rope_value(row, col, d.HD, d.tab, p)) << (16 * (l & 1));
-            }
+            const uint8_t* prm = isq ? d.pq : d.pk;
+            const bool bc = (isq ? d.bcq : d.bck) != 0;
+            const int4 xw = *reinterpret_cast<const int4*>(row + col0);
+            const int4 pw = *reinterpret_cast<const int4*>(row + (d0 < d.HD / 2 ? col0 + d.HD / 2 : col0 - d.HD / 2));
+            const uint4 o = rope_unit8(xw, pw, d.tab, d.HD, d0, [&](uint32_t l) { return ld_param(prm, col0 + l, bc); });
+            out[0] = o.x; out[1] = o.y; out[2] = o.z; out[3] = o.w;
             dst = isq ? d.qr + (u64)b * d.H * d.HD + col0
                       : d.kc + (((u64)b * d.KV + col0 / d.HD) * d.C + d.pos) * d.HD + col0 % d.HD;
         } else {
@@ -864,7 +856,7 @@ extern "C" int cm_decode_prep(const int16_t* q, const int16_t* k, const int16_t*
         if ((op & 15) != RO_ROPE || ((op >> 4) & 3) != 0 || ((op >> 8) & 3) != 0 || (op & F_P_KEEP))
             return fail(CM_EINVAL, "decode prep: 0x%x is not an int16 ROPE job's op word", op);
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(qr) || !aligned16(kc) || !aligned16(vc) ||
-        (reinterpret_cast<uintptr_t>(rope_row) & 3) || (reinterpret_cast<uintptr_t>(params_q) & 15) ||
+        !aligned16(rope_row) || (reinterpret_cast<uintptr_t>(params_q) & 15) ||
         (reinterpret_cast<uintptr_t>(params_k) & 15))
         return fail(CM_EALIGN, "decode prep: operands not aligned");
     const DecodePrep d{q, k, v, qr, kc, vc, static_cast<const int32_t*>(rope_row),

@@ -131,6 +131,42 @@ __device__ __forceinline__ i64 rne_shr_fast(i64 v, uint32_t k) {
     return (v + (((i64)1 << (k - 1)) - 1) + ((v >> k) & 1)) >> k;
 }
 
+// rope_value's element rule on loaded operands (x, its rotate-half partner already negated
+// for the low half, cos, sin): 64-bit when |x cos|, |rot sin| <= 2^38 (table at 2^-23, int16
+// operands) keep both shifted terms below 2^61, 128-bit otherwise.
+__device__ __forceinline__ int rope_elem(i64 x, i64 rot, int c, int s, const Param& q) {
+    if (q.sa <= 23 && q.sb <= 23 && q.sc <= 61 && abs(c) <= (1 << 23) && abs(s) <= (1 << 23)) {
+        const i64 v = ((x * c) << q.sa) + ((rot * s) << q.sb);
+        return (int)sat16(rne_shr_fast(v, (uint32_t)q.sc));
+    }
+    const i128 v = (((i128)x * c) << q.sa) + (((i128)rot * s) << q.sb);
+    return (int)sat16(rne_shr(v, q.sc));
+}
+
+// RoPE of one 16-byte unit of 8 int16 elements at head column d0 (8 | d0): xw the unit, pw
+// its partner unit HD / 2 columns away in the same head, tab the position's cos [HD] then
+// sin [HD], prm(l) the parameter of element l.  Returns the 8 results packed in 4 words.
+template <typename PF>
+__device__ __forceinline__ uint4 rope_unit8(const int4 xw, const int4 pw, const int32_t* tab, uint32_t HD,
+                                            uint32_t d0, PF prm) {
+    const bool lo = d0 < HD / 2;
+    const int4 c0 = *reinterpret_cast<const int4*>(tab + d0);
+    const int4 c1 = *reinterpret_cast<const int4*>(tab + d0 + 4);
+    const int4 s0 = *reinterpret_cast<const int4*>(tab + HD + d0);
+    const int4 s1 = *reinterpret_cast<const int4*>(tab + HD + d0 + 4);
+    const int cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    const int sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    const int16_t* xv = reinterpret_cast<const int16_t*>(&xw);
+    const int16_t* pv = reinterpret_cast<const int16_t*>(&pw);
+    uint32_t out[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (uint32_t l = 0; l < 8; l++) {
+        const i64 rot = lo ? -(i64)pv[l] : (i64)pv[l];
+        out[l >> 1] |= ((uint32_t)(uint16_t)rope_elem(xv[l], rot, cs[l], sn[l], prm(l))) << (16 * (l & 1));
+    }
+    return make_uint4(out[0], out[1], out[2], out[3]);
+}
+
 __device__ __forceinline__ u64 shfl64(u64 v, int off) {
     return ((u64)(uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), off, 64) << 32) |
            (uint32_t)__shfl_xor((int)(uint32_t)v, off, 64);

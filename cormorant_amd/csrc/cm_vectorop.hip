@@ -11,6 +11,7 @@
 // (keys-major rows, up to 128 contiguous bytes each) and transposes it through LDS into
 // query rows, written whole.
 #include "cm_common.h"
+#include "cm_rowops_math.h"
 
 #include <algorithm>
 
@@ -784,12 +785,26 @@ constexpr uint32_t kDaThreads = 1024;          // four wavefronts a SIMD hide ea
 constexpr uint32_t kDaWaves = kDaThreads / 64;
 constexpr uint32_t kDaMaxG = 8;
 
-template <uint32_t HD, uint32_t G>
+// The decode step's attention prep of the group, done by its attention workgroup first (the
+// decode_prep launch of the row-ops unit, one group's share, the same element rule): q's G
+// heads RoPE'd at the position into qr and into the workgroup's query staging, k's head
+// RoPE'd into the K cache row at pos, v's head copied into the V cache row; q / k / v rows of
+// sequence b at q + b H HD, k / v + b KV HD; the ROPE jobs' parameter blocks (per column of
+// those rows, or one entry) and the position's table row (cos [HD], sin [HD]).
+struct DaPrep {
+    const int16_t *q, *k, *v;
+    int16_t *qr, *kc, *vc;
+    const int32_t* tab;
+    const uint8_t *pq, *pk;
+    uint32_t bcq, bck, KV, pos;
+};
+
+template <uint32_t HD, uint32_t G, bool PREP>
 __global__ __launch_bounds__(kDaThreads) void decode_attn_kernel(const int16_t* __restrict__ q,
                                                                  const int16_t* __restrict__ kc,
                                                                  const int16_t* __restrict__ vc,
                                                                  int16_t* __restrict__ o, uint32_t C, SmxRegs r,
-                                                                 const int4* __restrict__ tsrc) {
+                                                                 const int4* __restrict__ tsrc, DaPrep pp) {
     constexpr uint32_t W4 = HD / 8;                         // 16-byte words of a row
     constexpr uint32_t KPW = 64 / W4;                       // rows a wavefront load covers
     extern __shared__ __attribute__((aligned(16))) uint32_t da_lds[];
@@ -808,27 +823,67 @@ __global__ __launch_bounds__(kDaThreads) void decode_attn_kernel(const int16_t* 
     constexpr uint32_t KR = kDaWaves * KPW, KCH = 8;
     const uint32_t kw = t % W4, krow = t / W4;
     int4 kv[KCH];
-    auto load_k = [&](uint32_t j0) {
+    auto load_k = [&](uint32_t j0, uint32_t skip) {      // row `skip` is not read
 #pragma unroll
         for (uint32_t u = 0; u < KCH; u++) {
             const uint32_t j = j0 + u * KR + krow;
-            kv[u] = j < C ? reinterpret_cast<const int4*>(kg + (uint64_t)j * HD)[kw] : make_int4(0, 0, 0, 0);
+            kv[u] = j < C && j != skip ? reinterpret_cast<const int4*>(kg + (uint64_t)j * HD)[kw] : make_int4(0, 0, 0, 0);
         }
     };
-    load_k(0);
+    load_k(0, PREP ? pp.pos : 0xFFFFFFFFu);
     SmxStage stg;
     smx_stage_load(stg, tsrc, 1024);
-    for (uint32_t e = t; e < G * HD / 2; e += kDaThreads) qs[e] = reinterpret_cast<const uint32_t*>(qg)[e];
+    if constexpr (PREP) {
+        // the prep, under the loads above: a thread per 8-element word: the group's q words, then k's, then v's
+        const uint32_t b = bg / pp.KV, g = bg - b * pp.KV, H = pp.KV * G;
+        constexpr uint32_t QW = G * HD / 8, KW = HD / 8;
+        for (uint32_t w = t; w < QW + 2 * KW; w += kDaThreads) {
+            uint32_t out[4] = {0, 0, 0, 0};
+            if (w < QW + KW) {
+                const bool isq = w < QW;
+                const uint32_t col0 = isq ? g * G * HD + 8 * w : g * HD + 8 * (w - QW);
+                const int16_t* row = isq ? pp.q + (uint64_t)b * H * HD : pp.k + (uint64_t)b * pp.KV * HD;
+                const uint8_t* prm = isq ? pp.pq : pp.pk;
+                const bool bc = (isq ? pp.bcq : pp.bck) != 0;
+                const uint32_t d0 = col0 % HD;
+                const int4 xw = *reinterpret_cast<const int4*>(row + col0);
+                const int4 pw = *reinterpret_cast<const int4*>(row + (d0 < HD / 2 ? col0 + HD / 2 : col0 - HD / 2));
+                const uint4 ow = ro::rope_unit8(xw, pw, pp.tab, HD, d0, [&](uint32_t l) { return ro::ld_param(prm, col0 + l, bc); });
+                out[0] = ow.x; out[1] = ow.y; out[2] = ow.z; out[3] = ow.w;
+                if (isq) {
+                    *reinterpret_cast<uint4*>(pp.qr + (uint64_t)b * H * HD + col0) = make_uint4(out[0], out[1], out[2], out[3]);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) qs[4 * w + e] = out[e];
+                } else {
+                    *reinterpret_cast<uint4*>(pp.kc + ((uint64_t)bg * C + pp.pos) * HD + 8 * (w - QW)) =
+                        make_uint4(out[0], out[1], out[2], out[3]);
+                }
+            } else {
+                const uint32_t c0 = 8 * (w - QW - KW);
+                const uint4 x = *reinterpret_cast<const uint4*>(pp.v + (uint64_t)b * pp.KV * HD + g * HD + c0);
+                *reinterpret_cast<uint4*>(pp.vc + ((uint64_t)bg * C + pp.pos) * HD + c0) = x;
+            }
+        }
+    }
+    if constexpr (!PREP)
+        for (uint32_t e = t; e < G * HD / 2; e += kDaThreads) qs[e] = reinterpret_cast<const uint32_t*>(qg)[e];
     for (uint32_t e = t; e < G * HD; e += kDaThreads) oacc[e] = 0u;
     smx_stage_store(stg, tab, tsrc, 1024);
+    // orders qs and the prep's cache rows (workgroup-scope release / acquire) before their reads
     __syncthreads();
+    if constexpr (PREP) {
+        // the first K loads went out before the prep wrote row pos and left it out: that row now
+#pragma unroll
+        for (uint32_t u = 0; u < KCH; u++)
+            if (u * KR + krow == pp.pos) kv[u] = reinterpret_cast<const int4*>(kg + (uint64_t)pp.pos * HD)[kw];
+    }
     uint32_t qv[G][4];                                      // this lane's 8 d of every query
 #pragma unroll
     for (uint32_t i = 0; i < G; i++)
 #pragma unroll
         for (int w = 0; w < 4; w++) qv[i][w] = qs[i * (HD / 2) + 4 * kw + w];
     for (uint32_t j0 = 0; j0 < C; j0 += KR * KCH) {
-        if (j0) load_k(j0);
+        if (j0) load_k(j0, 0xFFFFFFFFu);
 #pragma unroll
         for (uint32_t u = 0; u < KCH; u++) {
             int acc[G];
@@ -968,19 +1023,19 @@ __global__ __launch_bounds__(kDaThreads) void decode_attn_kernel(const int16_t* 
 }
 
 typedef void (*DecodeAttnFn)(const int16_t*, const int16_t*, const int16_t*, int16_t*, uint32_t, SmxRegs,
-                             const int4*);
+                             const int4*, DaPrep);
 
-template <uint32_t HD>
+template <uint32_t HD, bool PREP = false>
 DecodeAttnFn decode_attn_fn(uint32_t g) {
     switch (g) {
-    case 1: return decode_attn_kernel<HD, 1>;
-    case 2: return decode_attn_kernel<HD, 2>;
-    case 3: return decode_attn_kernel<HD, 3>;
-    case 4: return decode_attn_kernel<HD, 4>;
-    case 5: return decode_attn_kernel<HD, 5>;
-    case 6: return decode_attn_kernel<HD, 6>;
-    case 7: return decode_attn_kernel<HD, 7>;
-    default: return decode_attn_kernel<HD, 8>;
+    case 1: return decode_attn_kernel<HD, 1, PREP>;
+    case 2: return decode_attn_kernel<HD, 2, PREP>;
+    case 3: return decode_attn_kernel<HD, 3, PREP>;
+    case 4: return decode_attn_kernel<HD, 4, PREP>;
+    case 5: return decode_attn_kernel<HD, 5, PREP>;
+    case 6: return decode_attn_kernel<HD, 6, PREP>;
+    case 7: return decode_attn_kernel<HD, 7, PREP>;
+    default: return decode_attn_kernel<HD, 8, PREP>;
     }
 }
 
@@ -1032,6 +1087,10 @@ int prepare_softmax(DeviceState* st) {
     for (const void* f : fns)
         CM_HIP_CHECK(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)st->lds_per_block));
     for (uint32_t g = 1; g <= kDaMaxG; g++) {
+        CM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(decode_attn_fn<32, true>(g)),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)st->lds_per_block));
+        CM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(decode_attn_fn<64, true>(g)),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)st->lds_per_block));
         CM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(decode_attn_fn<32>(g)),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)st->lds_per_block));
         CM_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(decode_attn_fn<64>(g)),
@@ -1113,10 +1172,12 @@ extern "C" int cm_softmax(const int16_t* a, int16_t* c, uint32_t size, uint32_t 
                           as_stream(stream));
 }
 
-extern "C" int cm_decode_attention(const int16_t* q, const int16_t* kc, const int16_t* vc, int16_t* o,
-                                   uint32_t groups, uint32_t g, uint32_t c, uint32_t head_dim, uint32_t smx_cm,
-                                   uint32_t smx_cfg, uint32_t smx_mask, void* stream) {
-    using namespace cm;
+namespace cm {
+namespace {
+
+int decode_attention_run(const int16_t* q, const int16_t* kc, const int16_t* vc, int16_t* o, uint32_t groups,
+                         uint32_t g, uint32_t c, uint32_t head_dim, uint32_t smx_cm, uint32_t smx_cfg,
+                         uint32_t smx_mask, const DaPrep* pp, hipStream_t s) {
     DeviceState* st;
     int rc = state(&st);
     if (rc) return rc;
@@ -1132,8 +1193,42 @@ extern "C" int cm_decode_attention(const int16_t* q, const int16_t* kc, const in
     r.dlim = smx_dlim(r.cm, r.cs);
     const size_t lds = 4 * (4096 + kDaMaxG * 32 + 2 * kDaWaves * kDaMaxG + kDaMaxG * 64) + (size_t)2 * g * c;
     if (lds > st->lds_per_block) return fail(CM_EINVAL, "decode attention: %zu bytes of LDS", lds);
-    const DecodeAttnFn fn = head_dim == 64 ? decode_attn_fn<64>(g) : decode_attn_fn<32>(g);
-    CM_LAUNCH("decode_attn_kernel", fn, dim3(groups), dim3(kDaThreads), lds, as_stream(stream), q, kc, vc, o, c, r,
-              reinterpret_cast<const int4*>(st->smx_tab));
+    const DecodeAttnFn fn = pp != nullptr ? (head_dim == 64 ? decode_attn_fn<64, true>(g) : decode_attn_fn<32, true>(g))
+                                          : (head_dim == 64 ? decode_attn_fn<64>(g) : decode_attn_fn<32>(g));
+    CM_LAUNCH("decode_attn_kernel", fn, dim3(groups), dim3(kDaThreads), lds, s, q, kc, vc, o, c, r,
+              reinterpret_cast<const int4*>(st->smx_tab), pp != nullptr ? *pp : DaPrep{});
     return CM_OK;
+}
+
+}  // namespace
+}  // namespace cm
+
+extern "C" int cm_decode_attention(const int16_t* q, const int16_t* kc, const int16_t* vc, int16_t* o,
+                                   uint32_t groups, uint32_t g, uint32_t c, uint32_t head_dim, uint32_t smx_cm,
+                                   uint32_t smx_cfg, uint32_t smx_mask, void* stream) {
+    return cm::decode_attention_run(q, kc, vc, o, groups, g, c, head_dim, smx_cm, smx_cfg, smx_mask, nullptr,
+                                    cm::as_stream(stream));
+}
+
+extern "C" int cm_decode_attention_prep(const int16_t* q, const int16_t* k, const int16_t* v, int16_t* qr,
+                                        int16_t* kc, int16_t* vc, int16_t* o, uint32_t batch, uint32_t heads,
+                                        uint32_t kv_heads, uint32_t head_dim, uint32_t cache_rows, uint32_t pos,
+                                        const void* rope_row, const void* params_q, uint32_t op_q,
+                                        const void* params_k, uint32_t op_k, uint32_t smx_cm, uint32_t smx_cfg,
+                                        uint32_t smx_mask, void* stream) {
+    using namespace cm;
+    if (batch == 0) return CM_OK;
+    if (kv_heads == 0 || heads % kv_heads) return fail(CM_EINVAL, "decode attention: %u heads over %u KV heads", heads, kv_heads);
+    if (pos >= cache_rows) return fail(CM_EINVAL, "decode attention: position %u of %u cache rows", pos, cache_rows);
+    for (uint32_t op : {op_q, op_k})
+        if ((op & 15) != ro::RO_ROPE || ((op >> 4) & 3) != 0 || ((op >> 8) & 3) != 0 || (op & ro::F_P_KEEP))
+            return fail(CM_EINVAL, "decode attention: 0x%x is not an int16 ROPE job's op word", op);
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(qr) || !aligned16(rope_row) ||
+        (reinterpret_cast<uintptr_t>(params_q) & 15) || (reinterpret_cast<uintptr_t>(params_k) & 15))
+        return fail(CM_EALIGN, "decode attention: the prep's operands are not aligned");
+    const DaPrep pp{q, k, v, qr, kc, vc, static_cast<const int32_t*>(rope_row), static_cast<const uint8_t*>(params_q),
+                    static_cast<const uint8_t*>(params_k), (op_q & ro::F_P_BCAST) ? 1u : 0u,
+                    (op_k & ro::F_P_BCAST) ? 1u : 0u, kv_heads, pos};
+    return decode_attention_run(qr, kc, vc, o, batch * kv_heads, heads / kv_heads, cache_rows, head_dim, smx_cm,
+                                smx_cfg, smx_mask, &pp, as_stream(stream));
 }

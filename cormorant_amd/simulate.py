@@ -164,6 +164,11 @@ class Simulator:
                 continue
             if self._planes_out(sn) is not None and self._planes_node(sn, raw):
                 continue
+            if i < len(nodes) and self._prep_attention_fusable(sn, nodes[i]):
+                # the decode prep and the attention of its outputs: one launch
+                self._prep_attention(sn, nodes[i], raw)
+                i += 1
+                continue
             if isinstance(sn, MatmulNode):
                 raw[sn.output.onnx_name] = self._matmul(sn, raw)
             elif isinstance(sn, LlmEmbedNode):
@@ -999,6 +1004,49 @@ class Simulator:
                                self._get(vt, raw).reshape(-1), o, B * KV, G, C, sn.cm, sn.cfg,
                                sn.mask_reg(C, self._host_int(sn.mask_t, raw)), head_dim=HD)
         return o
+
+    def _prep_attention_fusable(self, sn, nxt) -> bool:
+        """``nxt`` is the decode attention of ``sn``'s outputs: q = the prep's qr, the caches the
+        prep writes, their shapes the ones both calls take."""
+        if not (isinstance(sn, DecodePrepNode) and isinstance(nxt, DecodeAttentionNode)):
+            return False
+        q, k, v, kc, vc = sn.inputs[:5]
+        qt, kt, vt = nxt.inputs[:3]
+        if (qt.onnx_name != sn.output.onnx_name or kt.onnx_name != kc.onnx_name or vt.onnx_name != vc.onnx_name
+                or nxt.kv_heads != sn.kv_heads or nxt.heads != sn.heads or nxt.head_dim != sn.head_dim):
+            return False
+        B, KV, C, HD = (int(x) for x in kc.shape)
+        return HD in (32, 64) and C % 64 == 0 and C <= 8192 and sn.heads % KV == 0 and sn.heads // KV <= 8
+
+    def _prep_attention(self, sn: DecodePrepNode, nxt: DecodeAttentionNode, raw) -> None:
+        """The prep's RoPE / cache writes and the attention over them in one launch (both outputs
+        kept, the caches updated in place); the checks of _decode_prep and _decode_attention."""
+        q, k, v, kc, vc = sn.inputs[:5]
+        B, KV, C, HD = (int(x) for x in kc.shape)
+        pos = sn.position(self._host_int(sn.pos_t, raw))
+        if not 0 <= pos < C:
+            raise SchedulerError(f"decode prep '{sn.output.onnx_name}': position {pos} of {C} cache rows")
+        ot = nxt.output
+        fq, fk, fv, fo = (np.asarray(self._exp_b(t)).reshape(-1) for t in (nxt.inputs[0], nxt.inputs[1], nxt.inputs[2], ot))
+        if any((e != e[0]).any() for e in (fq, fk, fv, fo)):
+            raise SchedulerError(f"decode attention '{ot.onnx_name}': q, the caches and o at one exponent each")
+        if int(fo[0]) != ((nxt.cfg >> 8) & 31) + int(fv[0]) - self._dtype.frac_bits:
+            raise SchedulerError(f"decode attention '{ot.onnx_name}': the output exponent is not f_p + f_v - 8")
+        jq, jk = sn.rope_q.jobs(pos=pos)[0], sn.rope_k.jobs(pos=pos)[0]
+        params = self._params.get(id(sn))
+        if params is None:
+            params = [torch.from_numpy(np.ascontiguousarray(j.params, np.uint8)).to(self.device) for j in (jq, jk)]
+            self._params[id(sn)] = params
+        tab = self._get(sn.rope_q.table, raw).reshape(-1, 2 * HD)
+        qr = self._new(sn.output)
+        o = self._new(ot)
+        units.decode_attention_prep(self._get(q, raw).reshape(-1).contiguous(), self._get(k, raw).reshape(-1).contiguous(),
+                                    self._get(v, raw).reshape(-1).contiguous(), qr, self._get(kc, raw).reshape(-1),
+                                    self._get(vc, raw).reshape(-1), o, B, sn.heads, KV, HD, C, pos, tab[jq.b_row0],
+                                    params[0], jq.op, params[1], jk.op, nxt.cm, nxt.cfg,
+                                    nxt.mask_reg(C, self._host_int(nxt.mask_t, raw)))
+        raw[sn.output.onnx_name] = qr
+        raw[ot.onnx_name] = o
 
     def _decode_prep(self, sn: DecodePrepNode, raw) -> torch.Tensor:
         """RoPE of q (into the output) and k (into the K cache rows) and the V cache rows, one launch."""

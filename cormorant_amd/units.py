@@ -257,6 +257,28 @@ def decode_prep(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, qr: torch.Ten
     _lib.check(rc, "cm_decode_prep")
 
 
+def decode_attention_prep(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, qr: torch.Tensor, kc: torch.Tensor,
+                          vc: torch.Tensor, o: torch.Tensor, batch: int, heads: int, kv_heads: int, head_dim: int,
+                          kc_rows: int, pos: int, rope_row: torch.Tensor, params_q: torch.Tensor, op_q: int,
+                          params_k: torch.Tensor, op_k: int, smx_cm: int, smx_cfg: int, smx_mask: int) -> torch.Tensor:
+    """cm_decode_attention_prep: decode_prep and decode_attention over its outputs in one launch."""
+    _require(q, "q", torch.int16, batch * heads * head_dim)
+    _require(k, "k", torch.int16, batch * kv_heads * head_dim)
+    _require(v, "v", torch.int16, batch * kv_heads * head_dim)
+    _require(qr, "qr", torch.int16, batch * heads * head_dim)
+    _require(o, "o", torch.int16, batch * heads * head_dim)
+    _require(kc, "kc", torch.int16, batch * kv_heads * kc_rows * head_dim)
+    _require(vc, "vc", torch.int16, batch * kv_heads * kc_rows * head_dim)
+    _require(rope_row, "rope_row", torch.int32, 2 * head_dim)
+    rc = _lib.lib().cm_decode_attention_prep(_ptr(q), _ptr(k), _ptr(v), _ptr(qr), _ptr(kc), _ptr(vc), _ptr(o), batch,
+                                             heads, kv_heads, head_dim, kc_rows, pos, _ptr(rope_row), _ptr(params_q),
+                                             op_q & 0xFFFFFFFF, _ptr(params_k), op_k & 0xFFFFFFFF,
+                                             smx_cm & 0xFFFFFFFF, smx_cfg & 0xFFFFFFFF, smx_mask & 0xFFFFFFFF,
+                                             _stream())
+    _lib.check(rc, "cm_decode_attention_prep")
+    return o
+
+
 def matmul_skinny_planes(a: torch.Tensor, n: int, k: int, planes, cs, ms) -> None:
     """cm_matmul_skinny_planes: C_i = sat16(wrap32(A . B_i) >> 8) for up to 4 weights given as
     their split images (matmul_b_planes of the same k and m_i) and the same A [n][k], n <= 16."""

@@ -374,12 +374,24 @@ int cm_decode_attention(const int16_t* q, const int16_t* kc, const int16_t* vc, 
  * into qr and k's straight into the K cache rows kc[b][g][pos][0..hd), and v's rows copied into
  * vc[b][g][pos] (caches [batch][kv_heads][cache_rows][hd]): the cm_rowops ROPE jobs and the two
  * KV row writes of the reference's attention prep (rowops_nodes.py:997-1047, llm_nodes.py:
- * 1012-1030) with the same element rule.  hd a multiple of 16 up to 128, 16-byte aligned rows.
+ * 1012-1030) with the same element rule.  hd a multiple of 16 up to 128, 16-byte aligned rows
+ * and rope_row.
  * The device's row-ops parameter RAM is left as it was. */
 int cm_decode_prep(const int16_t* q, const int16_t* k, const int16_t* v, int16_t* qr, int16_t* kc, int16_t* vc,
                    uint32_t batch, uint32_t heads, uint32_t kv_heads, uint32_t head_dim, uint32_t cache_rows,
                    uint32_t pos, const void* rope_row, const void* params_q, uint32_t op_q, const void* params_k,
                    uint32_t op_k, void* stream);
+
+/* cm_decode_prep followed by cm_decode_attention over its outputs, in one launch: the prep of
+ * each KV group done by that group's attention workgroup before its q.K^T (the group's query
+ * heads into qr, its K / V cache rows at pos), then o as cm_decode_attention(qr, kc, vc, o,
+ * batch kv_heads, heads / kv_heads, cache_rows, head_dim, smx_cm, smx_cfg, smx_mask) computes it.
+ * No counterpart in the reference: its RoPE / KV-write nodes and the attention chain, one launch. */
+int cm_decode_attention_prep(const int16_t* q, const int16_t* k, const int16_t* v, int16_t* qr, int16_t* kc,
+                             int16_t* vc, int16_t* o, uint32_t batch, uint32_t heads, uint32_t kv_heads,
+                             uint32_t head_dim, uint32_t cache_rows, uint32_t pos, const void* rope_row,
+                             const void* params_q, uint32_t op_q, const void* params_k, uint32_t op_k,
+                             uint32_t smx_cm, uint32_t smx_cfg, uint32_t smx_mask, void* stream);
 
 #ifdef __cplusplus
 }
