@@ -65,6 +65,7 @@ SIGNATURES = {
     "cm_matmul_skinny_multi": (_I32, [_P, _U32, _U32, _U32, _P, _P, _P, _U32, _P]),
     "cm_matmul_skinny_planes": (_I32, [_P, _U32, _U32, _U32, _P, _P, _P, _P]),
     "cm_matmul_skinny_planes_addx": (_I32, [_P, _U32, _U32, _P, _P, _U32, _P, _P, _U32, _U32, _P, _P]),
+    "cm_matmul_skinny_planes_mulact": (_I32, [_P, _U32, _U32, _P, _P, _P, _P, _U32, _P, _U32, _P, _P]),
     "cm_timing_enable": (_I32, [_I32]),
     "cm_timing_read": (_I32, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                               ctypes.POINTER(ctypes.c_uint64)]),

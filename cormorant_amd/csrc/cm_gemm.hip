@@ -1383,6 +1383,102 @@ struct SkinnyEpiIn {
     int32_t x = 0;
 };
 
+// The wrapped partial products of one skinny workgroup: NB 16-column blocks whose plane lines
+// start at bh[b] / bl[b] (the block's first column), into red [W][16][16 NB] and A's row sums
+// into rsum [W][16]; ends with the workgroup barrier.
+template <uint32_t NB>
+__device__ __forceinline__ void skinny_products(const int16_t* __restrict__ a, uint32_t n, uint32_t k, uint32_t kp,
+                                                const int8_t* const (&bh)[NB], const int8_t* const (&bl)[NB],
+                                                uint32_t* red, int32_t* rsum) {
+    constexpr uint32_t COLS = 16 * NB, CH = sp_chunk(NB);
+    const uint32_t W = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t r = lane & 15, g = lane >> 4;             // A row and B column of a block; k group
+    const uint32_t nsteps = kp / 64;
+    const bool row_ok = r < n;
+    const int16_t* arow = a + (uint64_t)(row_ok ? r : 0) * k;
+    const int4 pad8 = make_int4(0x00800080, 0x00800080, 0x00800080, 0x00800080);   // eight kPad: A' = 0
+    v4i hh[NB], mid[NB], ll[NB];
+#pragma unroll
+    for (uint32_t b = 0; b < NB; b++) hh[b] = mid[b] = ll[b] = v4i{0, 0, 0, 0};
+    int32_t asum = 0;
+    for (uint32_t s0 = wave; s0 < nsteps; s0 += W * CH) {
+        int4 av[CH][2];
+        v4i bhv[CH][NB], blv[CH][NB];
+#pragma unroll
+        for (uint32_t u = 0; u < CH; u++) {
+            const uint32_t st = s0 + u * W;
+            const bool live = st < nsteps;
+            const uint32_t kk = (live ? st : 0) * 64 + 16 * g;
+            // k % 8 == 0: each half of the lane's 16 k is wholly real or wholly past k; a half past
+            // k loads row 0's first 8 (in bounds) and takes the pad instead
+            const bool h0 = live && row_ok && kk + 8 <= k, h1 = live && row_ok && kk + 16 <= k;
+            const int4 a0 = *reinterpret_cast<const int4*>(arow + (h0 ? kk : 0));
+            const int4 a1 = *reinterpret_cast<const int4*>(arow + (h1 ? kk + 8 : 0));
+            av[u][0] = h0 ? a0 : pad8;
+            av[u][1] = h1 ? a1 : pad8;
+#pragma unroll
+            for (uint32_t b = 0; b < NB; b++) {
+                const uint64_t off = (uint64_t)r * kp + kk;
+                bhv[u][b] = *reinterpret_cast<const v4i*>(bh[b] + off);
+                blv[u][b] = *reinterpret_cast<const v4i*>(bl[b] + off);
+            }
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < CH; u++) {
+            if (s0 + u * W >= nsteps) break;                  // wave-uniform
+            const uint32_t kk = (s0 + u * W) * 64 + 16 * g;
+            if (row_ok && kk + 8 <= k) asum += sum8(av[u][0]);
+            if (row_ok && kk + 16 <= k) asum += sum8(av[u][1]);
+            uint2 h0, l0, h1, l1;
+            split8(av[u][0], h0, l0);
+            split8(av[u][1], h1, l1);
+            const v4i ah{(int)h0.x, (int)h0.y, (int)h1.x, (int)h1.y}, al{(int)l0.x, (int)l0.y, (int)l1.x, (int)l1.y};
+#pragma unroll
+            for (uint32_t b = 0; b < NB; b++) hh[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bhv[u][b], hh[b], 0, 0, 0);
+#pragma unroll
+            for (uint32_t b = 0; b < NB; b++) mid[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, blv[u][b], mid[b], 0, 0, 0);
+#pragma unroll
+            for (uint32_t b = 0; b < NB; b++) ll[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, blv[u][b], ll[b], 0, 0, 0);
+#pragma unroll
+            for (uint32_t b = 0; b < NB; b++) mid[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bhv[u][b], mid[b], 0, 0, 0);
+        }
+    }
+    // this wavefront's wrapped partials: lane l holds column l % 16 of each block, rows 4 g .. + 3
+#pragma unroll
+    for (uint32_t b = 0; b < NB; b++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            red[(wave * 16 + 4 * g + i) * COLS + 16 * b + r] =
+                ((uint32_t)hh[b][i] << 16) + ((uint32_t)mid[b][i] << 8) + (uint32_t)ll[b][i];
+    asum += __shfl_xor(asum, 16, 64);
+    asum += __shfl_xor(asum, 32, 64);
+    if (g == 0) rsum[wave * 16 + r] = asum;
+    __syncthreads();
+}
+
+// C[row][col] of a skinny workgroup from its wavefronts' partials (column cl of the tile), A's
+// row sums and B's column sum cs.
+__device__ __forceinline__ int16_t skinny_value(const uint32_t* red, const int32_t* rsum, uint32_t W, uint32_t cols,
+                                                uint32_t row, uint32_t cl, uint32_t k, uint32_t cs) {
+    uint32_t acc = 0u - 16384u * k, rs = 0;
+    for (uint32_t w = 0; w < W; w++) {
+        acc += red[(w * 16 + row) * cols + cl];
+        rs += (uint32_t)rsum[w * 16 + row];
+    }
+    acc += 128u * rs + 128u * cs;
+    return (int16_t)min(max((int32_t)acc >> 8, -32768), 32767);
+}
+
+// B's column sum of column col from the slabs a prefetch took (the first kSpSlabs) and the rest.
+__device__ __forceinline__ uint32_t skinny_colsum(const uint32_t (&pre)[kSpSlabs], const int32_t* part, uint32_t nslab,
+                                                  uint32_t lp, uint32_t col) {
+    uint32_t cs = 0;
+#pragma unroll
+    for (uint32_t sl = 0; sl < kSpSlabs; sl++) cs += pre[sl];
+    for (uint32_t sl = kSpSlabs; sl < nslab; sl++) cs += (uint32_t)part[(uint64_t)sl * lp + col];
+    return cs;
+}
+
 // XK: the output job's x kind (0: no job, 1: int16, 2: int32).
 template <uint32_t NB, uint32_t XK>
 __global__ __launch_bounds__(64 * sp_max_waves(NB)) void skinny_planes_kernel(const int16_t* __restrict__ a, uint32_t n,
@@ -1390,22 +1486,15 @@ __global__ __launch_bounds__(64 * sp_max_waves(NB)) void skinny_planes_kernel(co
                                                                        SkinnyPlaneSegs segs, SkinnyAddx ax) {
     constexpr uint32_t COLS = 16 * NB;
     extern __shared__ __attribute__((aligned(16))) uint32_t sp_lds[];
-    const uint32_t W = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint32_t W = blockDim.x >> 6;
     uint32_t* red = sp_lds;                                  // [W][16][COLS] wrapped partials
     int32_t* rsum = reinterpret_cast<int32_t*>(sp_lds + W * 16 * COLS);   // [W][16] A row sums
     uint32_t si = 0;
     for (uint32_t i = 1; i < segs.count; i++)
         if (blockIdx.x >= segs.cb0[i]) si = i;
     const uint32_t c0 = (blockIdx.x - segs.cb0[si]) * COLS;
-    const int8_t* __restrict__ bhi = segs.hi[si];
-    const int8_t* __restrict__ blo = segs.lo[si];
     const uint32_t m = segs.m[si], lp = segs.lines_p[si];
     const int32_t* __restrict__ part = segs.part[si];
-    const uint32_t r = lane & 15, g = lane >> 4;             // A row and B column of a block; k group
-    const uint32_t nsteps = kp / 64;
-    const bool row_ok = r < n;
-    const int16_t* arow = a + (uint64_t)(row_ok ? r : 0) * k;
-    const int4 pad8 = make_int4(0x00800080, 0x00800080, 0x00800080, 0x00800080);   // eight kPad: A' = 0
     const uint32_t ck = (ax.op >> 8) & 3;
     const bool pb = (ax.op & ro::F_P_BCAST) != 0;
     // element e of the tile: row e / COLS, column c0 + e % COLS
@@ -1428,78 +1517,19 @@ __global__ __launch_bounds__(64 * sp_max_waves(NB)) void skinny_planes_kernel(co
     SkinnyEpiIn pre[PRE];
 #pragma unroll
     for (uint32_t i = 0; i < PRE; i++) pre[i] = epi_in(threadIdx.x + i * blockDim.x);
-    v4i hh[NB], mid[NB], ll[NB];
+    const int8_t* bh[NB];
+    const int8_t* bl[NB];
 #pragma unroll
-    for (uint32_t b = 0; b < NB; b++) hh[b] = mid[b] = ll[b] = v4i{0, 0, 0, 0};
-    int32_t asum = 0;
-    constexpr uint32_t CH = sp_chunk(NB);
-    for (uint32_t s0 = wave; s0 < nsteps; s0 += W * CH) {
-        int4 av[CH][2];
-        v4i bh[CH][NB], bl[CH][NB];
-#pragma unroll
-        for (uint32_t u = 0; u < CH; u++) {
-            const uint32_t st = s0 + u * W;
-            const bool live = st < nsteps;
-            const uint32_t kk = (live ? st : 0) * 64 + 16 * g;
-            // k % 8 == 0: each half of the lane's 16 k is wholly real or wholly past k; a half past
-            // k loads row 0's first 8 (in bounds) and takes the pad instead
-            const bool h0 = live && row_ok && kk + 8 <= k, h1 = live && row_ok && kk + 16 <= k;
-            const int4 a0 = *reinterpret_cast<const int4*>(arow + (h0 ? kk : 0));
-            const int4 a1 = *reinterpret_cast<const int4*>(arow + (h1 ? kk + 8 : 0));
-            av[u][0] = h0 ? a0 : pad8;
-            av[u][1] = h1 ? a1 : pad8;
-#pragma unroll
-            for (uint32_t b = 0; b < NB; b++) {
-                const uint64_t off = (uint64_t)(c0 + 16 * b + r) * kp + kk;
-                bh[u][b] = *reinterpret_cast<const v4i*>(bhi + off);
-                bl[u][b] = *reinterpret_cast<const v4i*>(blo + off);
-            }
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < CH; u++) {
-            if (s0 + u * W >= nsteps) break;                  // wave-uniform
-            const uint32_t kk = (s0 + u * W) * 64 + 16 * g;
-            if (row_ok && kk + 8 <= k) asum += sum8(av[u][0]);
-            if (row_ok && kk + 16 <= k) asum += sum8(av[u][1]);
-            uint2 h0, l0, h1, l1;
-            split8(av[u][0], h0, l0);
-            split8(av[u][1], h1, l1);
-            const v4i ah{(int)h0.x, (int)h0.y, (int)h1.x, (int)h1.y}, al{(int)l0.x, (int)l0.y, (int)l1.x, (int)l1.y};
-#pragma unroll
-            for (uint32_t b = 0; b < NB; b++) hh[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bh[u][b], hh[b], 0, 0, 0);
-#pragma unroll
-            for (uint32_t b = 0; b < NB; b++) mid[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bl[u][b], mid[b], 0, 0, 0);
-#pragma unroll
-            for (uint32_t b = 0; b < NB; b++) ll[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bl[u][b], ll[b], 0, 0, 0);
-#pragma unroll
-            for (uint32_t b = 0; b < NB; b++) mid[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bh[u][b], mid[b], 0, 0, 0);
-        }
+    for (uint32_t b = 0; b < NB; b++) {
+        bh[b] = segs.hi[si] + (uint64_t)(c0 + 16 * b) * kp;
+        bl[b] = segs.lo[si] + (uint64_t)(c0 + 16 * b) * kp;
     }
-    // this wavefront's wrapped partials: lane l holds column l % 16 of each block, rows 4 g .. + 3
-#pragma unroll
-    for (uint32_t b = 0; b < NB; b++)
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            red[(wave * 16 + 4 * g + i) * COLS + 16 * b + r] =
-                ((uint32_t)hh[b][i] << 16) + ((uint32_t)mid[b][i] << 8) + (uint32_t)ll[b][i];
-    asum += __shfl_xor(asum, 16, 64);
-    asum += __shfl_xor(asum, 32, 64);
-    if (g == 0) rsum[wave * 16 + r] = asum;
-    __syncthreads();
+    skinny_products<NB>(a, n, k, kp, bh, bl, red, rsum);
     int16_t* __restrict__ c = segs.c[si];
     auto store = [&](uint32_t e, const SkinnyEpiIn& in) {
         const uint32_t row = e / COLS, cl = e - row * COLS, col = c0 + cl;
         if (row >= n || col >= m) return;
-        uint32_t acc = 0u - 16384u * k, rs = 0, cs = 0;
-        for (uint32_t w = 0; w < W; w++) {
-            acc += red[(w * 16 + row) * COLS + cl];
-            rs += (uint32_t)rsum[w * 16 + row];
-        }
-#pragma unroll
-        for (uint32_t sl = 0; sl < kSpSlabs; sl++) cs += in.cs[sl];
-        for (uint32_t sl = kSpSlabs; sl < nslab; sl++) cs += (uint32_t)part[(uint64_t)sl * lp + col];
-        acc += 128u * rs + 128u * cs;
-        const int16_t y = (int16_t)min(max((int32_t)acc >> 8, -32768), 32767);
+        const int16_t y = skinny_value(red, rsum, W, COLS, row, cl, k, skinny_colsum(in.cs, part, nslab, lp, col));
         const uint64_t eo = (uint64_t)row * m + col;
         c[eo] = y;
         if constexpr (XK != 0) {
@@ -1512,6 +1542,69 @@ __global__ __launch_bounds__(64 * sp_max_waves(NB)) void skinny_planes_kernel(co
     for (uint32_t i = 0; i < PRE; i++)
         if (threadIdx.x + i * blockDim.x < 16 * COLS) store(threadIdx.x + i * blockDim.x, pre[i]);
     for (uint32_t e = threadIdx.x + PRE * blockDim.x; e < 16 * COLS; e += blockDim.x) store(e, epi_in(e));
+}
+
+// The MULACT job over a gate and an up product of the same A (segments 0 and 1, m columns
+// each): a workgroup's NB blocks are NB / 2 blocks of gate columns and the same columns of up,
+// and its stores write both products and out = MULACT(gate, up) with the job's parameters.
+struct SkinnyMulact {
+    int16_t* out;
+    const uint8_t* params;
+    uint32_t bcast;
+    const uint8_t* tab;       // the row-ops table image (the sigmoid)
+};
+
+struct SkinnyPairIn {
+    uint32_t cg[kSpSlabs] = {0, 0, 0, 0}, cu[kSpSlabs] = {0, 0, 0, 0};
+    uint4 prm{};
+};
+
+template <uint32_t NB>
+__global__ __launch_bounds__(64 * sp_max_waves(NB)) void skinny_mulact_kernel(const int16_t* __restrict__ a, uint32_t n,
+                                                                        uint32_t k, uint32_t kp, uint32_t nslab,
+                                                                        SkinnyPlaneSegs segs, SkinnyMulact mj) {
+    constexpr uint32_t COLS = 16 * NB, H = COLS / 2;
+    extern __shared__ __attribute__((aligned(16))) uint32_t sp_lds[];
+    const uint32_t W = blockDim.x >> 6;
+    uint32_t* red = sp_lds;
+    int32_t* rsum = reinterpret_cast<int32_t*>(sp_lds + W * 16 * COLS);
+    const uint32_t c0 = blockIdx.x * H, m = segs.m[0], lp = segs.lines_p[0];
+    auto epi_in = [&](uint32_t e) {
+        SkinnyPairIn in;
+        const uint32_t row = e / H, col = c0 + e % H;
+        if (row >= n || col >= m) return in;
+#pragma unroll
+        for (uint32_t sl = 0; sl < kSpSlabs; sl++)
+            if (sl < nslab) {
+                in.cg[sl] = (uint32_t)segs.part[0][(uint64_t)sl * lp + col];
+                in.cu[sl] = (uint32_t)segs.part[1][(uint64_t)sl * segs.lines_p[1] + col];
+            }
+        in.prm = *reinterpret_cast<const uint4*>(mj.params + 16u * (mj.bcast ? 0u : col));
+        return in;
+    };
+    const SkinnyPairIn pre = epi_in(threadIdx.x);
+    const int8_t* bh[NB];
+    const int8_t* bl[NB];
+#pragma unroll
+    for (uint32_t b = 0; b < NB; b++) {
+        const uint32_t sg = b < NB / 2 ? 0u : 1u, cb = c0 + 16 * (b % (NB / 2));
+        bh[b] = segs.hi[sg] + (uint64_t)cb * kp;
+        bl[b] = segs.lo[sg] + (uint64_t)cb * kp;
+    }
+    skinny_products<NB>(a, n, k, kp, bh, bl, red, rsum);
+    auto store = [&](uint32_t e, const SkinnyPairIn& in) {
+        const uint32_t row = e / H, cl = e - row * H, col = c0 + cl;
+        if (row >= n || col >= m) return;
+        const int16_t gv = skinny_value(red, rsum, W, COLS, row, cl, k, skinny_colsum(in.cg, segs.part[0], nslab, lp, col));
+        const int16_t uv = skinny_value(red, rsum, W, COLS, row, H + cl, k,
+                                        skinny_colsum(in.cu, segs.part[1], nslab, segs.lines_p[1], col));
+        const uint64_t eo = (uint64_t)row * m + col;
+        segs.c[0][eo] = gv;
+        segs.c[1][eo] = uv;
+        mj.out[eo] = (int16_t)ro::mulact_elem(gv, uv, ro::param_of(in.prm), mj.tab);
+    };
+    if (threadIdx.x < 16 * H) store(threadIdx.x, pre);
+    for (uint32_t e = threadIdx.x + blockDim.x; e < 16 * H; e += blockDim.x) store(e, epi_in(e));
 }
 
 // ---------------------------------------------------------------- drivers
@@ -2206,18 +2299,19 @@ uint32_t skinny_blocks(uint64_t blocks16, uint32_t k) {
     return blocks16 >= 2048 ? 4u : (blocks16 >= 256 ? 2u : 1u);
 }
 
-int skinny_planes(const int16_t* a, uint32_t n, uint32_t k, uint32_t count, const void* const* b_planes,
-                  int16_t* const* c, const uint32_t* m, const SkinnyAddx& ax, hipStream_t s) {
+// The segments of a skinny launch (checked, the planes carved), the slabs of their column sums
+// and the 16-column blocks they hold.
+int skinny_segs(uint32_t n, uint32_t k, uint32_t count, const int16_t* a, const void* const* b_planes,
+                int16_t* const* c, const uint32_t* m, SkinnyPlaneSegs& segs, uint32_t& nslab, uint64_t& blocks16) {
     if (count == 0 || count > kSkinnySegs) return fail(CM_EINVAL, "matmul: %u products (1 .. %u)", count, kSkinnySegs);
-    if (n == 0) return CM_OK;
     if (n > 16 || k == 0 || k > 32768 || (k & 7))
         return fail(CM_EINVAL, "matmul: skinny plane products take n <= 16 and k a multiple of 8 up to 32768");
     if (!aligned16(a)) return fail(CM_EALIGN, "matmul: a not 16-byte aligned");
     const uint32_t kp = (uint32_t)round_up(k, BK);
-    SkinnyPlaneSegs segs{};
+    segs = SkinnyPlaneSegs{};
     segs.count = count;
-    uint64_t blocks16 = 0;
-    uint32_t nslab = 0;
+    blocks16 = 0;
+    nslab = 0;
     for (uint32_t i = 0; i < count; i++) {
         if (m[i] == 0) return fail(CM_EINVAL, "matmul: product %u: m = 0", i);
         if (reinterpret_cast<uintptr_t>(b_planes[i]) & 255)
@@ -2234,6 +2328,26 @@ int skinny_planes(const int16_t* a, uint32_t n, uint32_t k, uint32_t count, cons
         nslab = B.nslab;
         blocks16 += ceil_div(m[i], 16);
     }
+    return CM_OK;
+}
+
+// Wavefronts of an nb-block skinny workgroup over k (one round of loads where they allow) and
+// the LDS of their partials.
+uint32_t skinny_waves(uint32_t k, uint32_t nb) {
+    const uint32_t kp = (uint32_t)round_up(k, BK);
+    return std::min<uint32_t>(sp_max_waves(nb), std::max<uint32_t>(1, ceil_div(kp / 64, sp_chunk(nb))));
+}
+size_t skinny_lds(uint32_t waves, uint32_t nb) { return (size_t)waves * 16 * (16 * nb + 1) * 4; }
+
+int skinny_planes(const int16_t* a, uint32_t n, uint32_t k, uint32_t count, const void* const* b_planes,
+                  int16_t* const* c, const uint32_t* m, const SkinnyAddx& ax, hipStream_t s) {
+    if (n == 0) return CM_OK;
+    SkinnyPlaneSegs segs;
+    uint32_t nslab;
+    uint64_t blocks16;
+    int rc = skinny_segs(n, k, count, a, b_planes, c, m, segs, nslab, blocks16);
+    if (rc) return rc;
+    const uint32_t kp = (uint32_t)round_up(k, BK);
     const uint32_t nb = skinny_blocks(blocks16, k);
     uint64_t cbs = 0;
     for (uint32_t i = 0; i < count; i++) {
@@ -2241,8 +2355,8 @@ int skinny_planes(const int16_t* a, uint32_t n, uint32_t k, uint32_t count, cons
         cbs += ceil_div(m[i], 16 * nb);
     }
     if (cbs > 0x7FFFFFFFull) return fail(CM_EINVAL, "matmul: %llu column blocks", (unsigned long long)cbs);
-    const uint32_t waves = std::min<uint32_t>(sp_max_waves(nb), std::max<uint32_t>(1, ceil_div(kp / 64, sp_chunk(nb))));
-    const size_t lds = (size_t)waves * 16 * (16 * nb + 1) * 4;
+    const uint32_t waves = skinny_waves(k, nb);
+    const size_t lds = skinny_lds(waves, nb);
     const dim3 grid((uint32_t)cbs), block(64 * waves);
     const uint32_t xk = ax.out == nullptr ? 0u : (((ax.op >> 4) & 3) == 0 ? 1u : 2u);
 #define CM_SP_LAUNCH(NB_, XK_)                                                                                  \
@@ -2265,8 +2379,47 @@ int skinny_planes(const int16_t* a, uint32_t n, uint32_t k, uint32_t count, cons
     return CM_OK;
 }
 
+int skinny_mulact(const int16_t* a, uint32_t n, uint32_t k, const void* b_gate, const void* b_up, int16_t* c_gate,
+                  int16_t* c_up, uint32_t m, const SkinnyMulact& mj, hipStream_t s) {
+    if (n == 0) return CM_OK;
+    SkinnyPlaneSegs segs;
+    uint32_t nslab;
+    uint64_t blocks16;
+    const void* bp[2] = {b_gate, b_up};
+    int16_t* cp[2] = {c_gate, c_up};
+    const uint32_t ms[2] = {m, m};
+    int rc = skinny_segs(n, k, 2, a, bp, cp, ms, segs, nslab, blocks16);
+    if (rc) return rc;
+    (void)blocks16;
+    const uint32_t kp = (uint32_t)round_up(k, BK);
+    const uint32_t waves = skinny_waves(k, 2);      // 16 gate and 16 up columns a workgroup
+    CM_LAUNCH("skinny_mulact_kernel", skinny_mulact_kernel<2>, dim3(ceil_div(m, 16)), dim3(64 * waves),
+              skinny_lds(waves, 2), s, a, n, k, kp, nslab, segs, mj);
+    return CM_OK;
+}
+
 }  // namespace
 }  // namespace cm
+
+extern "C" int cm_matmul_skinny_planes_mulact(const int16_t* a, uint32_t n, uint32_t k, const void* b_gate,
+                                              const void* b_up, int16_t* c_gate, int16_t* c_up, uint32_t m,
+                                              const void* params, uint32_t op, int16_t* out, void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    if ((op & 15) != ro::RO_MULACT || !(op & ro::F_B_EN) || (op & ro::F_P_KEEP) || ((op >> 4) & 3) != 0 ||
+        ((op >> 6) & 3) != 0 || ((op >> 8) & 3) != 0)
+        return fail(CM_EINVAL, "matmul: the output job must be an int16 MULACT with B enabled (op 0x%x)", op);
+    if (params == nullptr || out == nullptr || c_gate == nullptr || c_up == nullptr)
+        return fail(CM_EINVAL, "matmul: the MULACT output needs both products, out and a parameter block");
+    if (m > ro::kNMax) return fail(CM_EINVAL, "matmul: the MULACT job's rows of %u above %u", m, ro::kNMax);
+    if ((reinterpret_cast<uintptr_t>(params) & 15) || (reinterpret_cast<uintptr_t>(out) & 1) ||
+        (reinterpret_cast<uintptr_t>(c_gate) & 1) || (reinterpret_cast<uintptr_t>(c_up) & 1))
+        return fail(CM_EALIGN, "matmul: the MULACT operands are not aligned");
+    const SkinnyMulact mj{out, static_cast<const uint8_t*>(params), (op & ro::F_P_BCAST) ? 1u : 0u, st->ro_tables};
+    return skinny_mulact(a, n, k, b_gate, b_up, c_gate, c_up, m, mj, as_stream(stream));
+}
 
 extern "C" int cm_matmul_skinny_planes(const int16_t* a, uint32_t n, uint32_t k, uint32_t count,
                                        const void* const* b_planes, int16_t* const* c, const uint32_t* m,

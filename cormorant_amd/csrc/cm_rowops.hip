@@ -29,25 +29,6 @@ struct Job {
     uint32_t aux, bq_sh, win_lo, win_hi;
 };
 
-// sigma at 2^-24 of g = gv 2^-14 from the table image (rowops_spec.sig_q,
-// rowops_spec.py:346-358): entry i = {D[i] << 25 | T[i]} in the 64-bit half i.
-__device__ __forceinline__ i64 sig_q(i64 gv, const uint8_t* tab) {
-    const i64 a = gv < 0 ? -gv : gv;
-    const bool big = a >= ((i64)16 << 14);
-    const i64 ai = big ? ((i64)16 << 14) - 1 : a;
-    const i64 idx = ai >> 6, fr = ai & 63;
-    const u64 e = *reinterpret_cast<const u64*>(tab + 8 * idx);
-    const i64 T = (i64)(e & 0x1FFFFFF), D = (i64)((e >> 25) & 0xFFFFFF);
-    i64 s = T + ((D * fr) >> 6);
-    if (big) s = (i64)1 << 24;
-    return gv < 0 ? ((i64)1 << 24) - s : s;
-}
-
-// silu(g) at 2^-20 (rowops_spec.silu_q): rne(gv * sigma, 18)
-__device__ __forceinline__ i64 silu_q(i64 gv, const uint8_t* tab) {
-    return (i64)rne_shr((i128)gv * sig_q(gv, tab), 18);
-}
-
 // float32(v * 2^-sh) rounded to nearest even: v is exact in double (|v| < 2^32), one
 // rounding to float.
 __device__ __forceinline__ uint32_t dequant_bits(i64 v, int sh) {
@@ -389,9 +370,6 @@ __global__ __launch_bounds__(256) void ro_addx_fast_kernel(Job j, const uint8_t*
 // |x| < 2^31 and sc <= 63).  ROPE: the unit's rotate-half partner is the unit HD / 2 columns
 // away in the same head (HD a multiple of 16), the table row's cos / sin 8 at a time.  MULACT and
 // GATE come here with B enabled (int16).
-__device__ __forceinline__ i64 silu_fast(i64 gv, const uint8_t* tab) {       // |gv| < 2^39
-    return rne_shr_fast(gv * sig_q(gv, tab), 18);
-}
 
 template <uint32_t CODE>
 __global__ __launch_bounds__(256) void ro_unit_fast_kernel(Job j, const uint8_t* __restrict__ params,
@@ -447,12 +425,7 @@ __global__ __launch_bounds__(256) void ro_unit_fast_kernel(Job j, const uint8_t*
             for (int l = 0; l < 8; l++) {
                 const Param q = param_of(ro_lds[bcast ? 0u : l * units + u]);
                 if constexpr (CODE == RO_MULACT) {
-                    if (q.sa <= 23 && q.sc <= 61) {
-                        const i64 sl = silu_fast((i64)x[l] << q.sa, tab);      // |sl| < 2^37
-                        r[l] = (int)sat16(rne_shr_fast(sl * y[l], (uint32_t)q.sc));
-                    } else {
-                        r[l] = (int)sat16(rne_shr((i128)silu_q((i64)x[l] << q.sa, tab) * y[l], q.sc));
-                    }
+                    r[l] = mulact_elem(x[l], y[l], q, tab);
                 } else {   // GATE
                     if (q.sa <= 23 && q.sb <= 23 && q.sc <= 61) {
                         const i64 th = 2 * sig_q((i64)x[l] << q.sa, tab) - ((i64)1 << 24);
@@ -639,7 +612,7 @@ int run_job(DeviceState* st, const Job& j, const uint8_t* p, hipStream_t s) {
         return CM_OK;
     }
     if (j.n == 0 || j.c1 == 0 || j.c2 == 0) return CM_OK;
-    if (j.n > 4096) return fail(CM_EINVAL, "rowops: n = %u above 4096", j.n);
+    if (j.n > kNMax) return fail(CM_EINVAL, "rowops: n = %u above %u", j.n, kNMax);
     if (code == RO_XPOSE) {
         const uint32_t R = j.aux & 15;
         if (R == 0 || R > 8) return CM_OK;        // outside the contract: the unit writes nothing

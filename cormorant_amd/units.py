@@ -317,6 +317,26 @@ def matmul_skinny_planes_addx(a: torch.Tensor, n: int, k: int, planes: torch.Ten
     _lib.check(rc, "cm_matmul_skinny_planes_addx")
 
 
+def matmul_skinny_planes_mulact(a: torch.Tensor, n: int, k: int, b_gate: torch.Tensor, b_up: torch.Tensor,
+                                c_gate: torch.Tensor, c_up: torch.Tensor, m: int, params: torch.Tensor, op: int,
+                                out: torch.Tensor) -> None:
+    """cm_matmul_skinny_planes_mulact: the gate and up products of A (each as
+    matmul_skinny_planes gives it) and the row-ops MULACT job ``op`` over them into out [n][m],
+    one launch."""
+    _require(a, "a", torch.int16, n * k)
+    need = int(_lib.lib().cm_matmul_b_planes_bytes(k, m, 1))
+    for name, img in (("b_gate", b_gate), ("b_up", b_up)):
+        if img.dtype != torch.uint8 or img.numel() < need or img.data_ptr() % 256:
+            raise ValueError(f"matmul_skinny_planes_mulact: {name} is not the uint8 image of matmul_b_planes for k, m")
+    for name, t in (("c_gate", c_gate), ("c_up", c_up), ("out", out)):
+        _require(t, name, torch.int16, n * m)
+    if params.dtype != torch.uint8 or params.numel() < 16 * (1 if op & F_P_BCAST else m) or not params.is_contiguous():
+        raise ValueError("matmul_skinny_planes_mulact: params must be the contiguous uint8 block of the job's entries")
+    rc = _lib.lib().cm_matmul_skinny_planes_mulact(_ptr(a), n, k, _ptr(b_gate), _ptr(b_up), _ptr(c_gate), _ptr(c_up),
+                                                   m, _ptr(params), op & 0xFFFFFFFF, _ptr(out), _stream())
+    _lib.check(rc, "cm_matmul_skinny_planes_mulact")
+
+
 def matmul_strided(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, n: int, k: int, m: int, batch: int,
                    inner: int, a_view, b_view, c_view, b_trans: bool = False, wrap32: bool = False) -> torch.Tensor:
     """cm_matmul_strided: each view is (offset, ld, bs, bs2) in elements of its tensor; slice bt

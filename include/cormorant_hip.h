@@ -175,6 +175,18 @@ int cm_matmul_skinny_planes_addx(const int16_t* a, uint32_t n, uint32_t k, const
                                  uint32_t m, const void* x, const void* params, uint32_t op, uint32_t bq_sh,
                                  void* out, void* stream);
 
+/* Two products of cm_matmul_skinny_planes over the same A -- a gate and an up weight of m
+ * columns each -- and the row-ops MULACT job over their outputs in one launch (the decode
+ * step's SiLU gate): c_gate and c_up as cm_matmul_skinny_planes writes them, then out[r][j] =
+ * the job of op word `op` (int16 A, B and output, B enabled, F_P_BCAST) over c_gate[r][j] and
+ * c_up[r][j] with the 16-byte parameter block `params` -- the cm_rowops job (c_gate, c_up, out,
+ * params, op, n = m, c1 = n) of ROWOPS_RTL_KERNEL.md section 1 on whole rows (m <= 4096).  The
+ * device's row-ops parameter RAM is left as it was.  No counterpart in the reference's units; the results
+ * equal those calls. */
+int cm_matmul_skinny_planes_mulact(const int16_t* a, uint32_t n, uint32_t k, const void* b_gate, const void* b_up,
+                                   int16_t* c_gate, int16_t* c_up, uint32_t m, const void* params, uint32_t op,
+                                   int16_t* out, void* stream);
+
 /* cm_matmul over strided operands (no counterpart in the reference's units: the per-head
  * operands that VitAttnPrep / LlmAttnMerge would copy out and back, read and written in place):
  * slice bt of `batch` starts at (bt / inner) x_bs + (bt % inner) x_bs2 elements of each

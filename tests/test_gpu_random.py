@@ -332,6 +332,45 @@ def test_matmul_skinny_planes_output_job(U, oracle_lib, n, k, m, kind):
     np.testing.assert_array_equal(host(c2)[:n * m], oracle_lib.matmul(a, b, n, k, m, 1, 0, 0, n * m, 0, 0, True))
 
 
+@pytest.mark.parametrize("n,k,m,kind", [
+    (16, 960, 2560, "silu"),             # SmolLM2's gate / up and its SiLU gate
+    (16, 960, 2560, "wide"),             # shifts past the 64-bit bounds (the 128-bit element rule)
+    (5, 200, 72, "bcast"),               # rows short of 16, columns short of a block, one entry
+    (1, 8, 24, "silu"),                  # one k group
+    (16, 4104, 200, "silu"),             # k past four slabs of column sums
+    (16, 64, 4096, "silu"),              # the unit's longest row
+])
+def test_matmul_skinny_planes_mulact(U, oracle_lib, n, k, m, kind):
+    """cm_matmul_skinny_planes_mulact equals cm_matmul_skinny_planes of gate and up followed by
+    the cm_rowops MULACT job over their outputs (all three outputs, neighbours untouched)."""
+    import torch
+    from cormorant_amd import rowops_nodes as rn
+    rng = np.random.default_rng(7 * n + k + m)
+    a = rint16(rng, n * k)
+    bg, bu = rint16(rng, k * m), rint16(rng, k * m)
+    pg, pu = U.matmul_b_planes(dev16(bg), k, m), U.matmul_b_planes(dev16(bu), k, m)
+    if kind == "silu":
+        blk, bc = rn.pblock(0, 0, rng.integers(0, 15, m), 0, rng.integers(10, 31, m), m)
+    elif kind == "wide":
+        blk, bc = rn.pblock(0, 0, rng.integers(15, 41, m), 0, rng.integers(20, 64, m), m)
+    else:
+        blk, bc = rn.pblock(0, 0, 6, 0, 17, m)
+    op = rn.opword(rn.RO_MULACT, b_en=True, p_bcast=bc)
+    p = torch.from_numpy(np.ascontiguousarray(blk, np.uint8)).cuda()
+    cg, cu, out = poisoned16(n * m + 8), poisoned16(n * m + 8), poisoned16(n * m + 8)
+    U.matmul_skinny_planes_mulact(dev16(a), n, k, pg, pu, cg, cu, m, p, op, out)
+    cg2, cu2, out2 = poisoned16(n * m + 8), poisoned16(n * m + 8), poisoned16(n * m + 8)
+    U.matmul_skinny_planes(dev16(a), n, k, [pg, pu], [cg2, cu2], [m, m])
+    U.rowops(cg2.view(torch.uint8), cu2.view(torch.uint8), out2.view(torch.uint8), p, op, m, n, 1, m * 2, 0, m * 2, 0,
+             m * 2, 0)
+    torch.cuda.synchronize()
+    for got, want in ((cg, cg2), (cu, cu2), (out, out2)):
+        np.testing.assert_array_equal(host(got), host(want))
+    assert (host(out)[n * m:] == POISON16).all()
+    np.testing.assert_array_equal(host(cg2)[:n * m], oracle_lib.matmul(a, bg, n, k, m, 1, 0, 0, n * m, 0, 0, True))
+    np.testing.assert_array_equal(host(cu2)[:n * m], oracle_lib.matmul(a, bu, n, k, m, 1, 0, 0, n * m, 0, 0, True))
+
+
 @pytest.mark.parametrize("groups,G,C,mask,regs,lim", [
     (80, 3, 1024, 1024, 2, 3000),        # SmolLM2's step: 16 sequences x 5 groups, every cache row a key
     (10, 3, 1024, 700, 1, 3000),         # keys past the valid count
