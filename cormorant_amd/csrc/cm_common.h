@@ -116,6 +116,15 @@ __device__ __forceinline__ void store_stream(void* p, int4 v) {
     __builtin_nontemporal_store(__builtin_bit_cast(cm_i32x4, v), reinterpret_cast<cm_i32x4*>(p));
 }
 
+// A workgroup barrier that orders LDS accesses only (its fences are scoped to LDS): global
+// loads in flight stay in flight, where __syncthreads waits for every outstanding memory
+// operation of the wavefront first.  Not for global memory shared through the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ---------------------------------------------------------------- byte planes
 // The byte planes of 8 int16 values (one 16-byte load), x - 128 = 256 h + l: high bytes (1, 3
 // of each dword) and low bytes (0, 2, top bit flipped) as two 8-byte words.

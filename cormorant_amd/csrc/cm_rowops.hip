@@ -321,6 +321,59 @@ __global__ __launch_bounds__(256) void ro_norm_fast_kernel(Job j, const uint8_t*
     }
 }
 
+// NORM over few rows: a workgroup per row (rows in turn over the grid), UPL units of 8 elements
+// per thread (n <= 2048 UPL), the wavefronts' sums added through LDS: a quarter of the serial
+// arithmetic of the wavefront per row for the launches whose rows do not fill the chip.
+template <int AK, int UPL>
+__global__ __launch_bounds__(256) void ro_norm_wg_kernel(Job j, const uint8_t* __restrict__ params, uint8_t* pram_dst,
+                                                         uint32_t p_entries, bool bcast,
+                                                         const uint8_t* __restrict__ tab) {
+    extern __shared__ __attribute__((aligned(16))) uint4 ro_lds[];
+    __shared__ NormSums wsum[2][4];
+    const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const u64 rows = (u64)j.c1 * j.c2;
+    const bool ln = (j.op & F_NORM_LN) != 0;
+    const uint32_t units = j.n / 8;
+    int x[UPL][8];
+    auto load_row = [&](u64 row) {
+        const uint32_t i1 = (uint32_t)(row % j.c1), i2 = (uint32_t)(row / j.c1);
+        const uint8_t* ra = j.a + (u64)i2 * j.a_s2 + (u64)i1 * j.a_s1;
+#pragma unroll
+        for (int k = 0; k < UPL; k++) {
+            const uint32_t u = t + 256 * k;
+            if (u < units) {
+                ld_unit<AK>(ra, u, x[k]);
+            } else {
+#pragma unroll
+                for (int l = 0; l < 8; l++) x[k][l] = 0;
+            }
+        }
+    };
+    u64 row = blockIdx.x;
+    if (row < rows) load_row(row);                       // in flight while the parameters are staged
+    pram_load(params, pram_dst, p_entries);
+    stage_norm_params(ro_lds, params, bcast ? 1u : j.n, units, j.bq_sh);
+    __syncthreads();
+    for (uint32_t it = 0; row < rows; row += gridDim.x, it++) {
+        NormSums ts = norm_sums<UPL>(x);
+        norm_sums_wave(ts);
+        NormSums* ws = wsum[it & 1];                     // alternate: a row's reads end before the next's writes
+        if (lane == 0) ws[wave] = ts;
+        __syncthreads();
+        ts = ws[0];
+#pragma unroll
+        for (int w = 1; w < 4; w++) norm_sums_add(ts, ws[w]);
+        int4 o[UPL];
+        norm_row_finish<UPL>(j.n, j.eps, ts, x, ro_lds, bcast, tab, t, 256, units, ln, o);
+        const uint32_t i1 = (uint32_t)(row % j.c1), i2 = (uint32_t)(row / j.c1);
+        uint8_t* rc = j.c + (u64)i2 * j.c_s2 + (u64)i1 * j.c_s1;
+#pragma unroll
+        for (int k = 0; k < UPL; k++)
+            if (t + 256 * k < units) store_stream(rc + 16u * (t + 256 * k), o[k]);
+        if (row + gridDim.x < rows) load_row(row + gridDim.x);
+    }
+}
+
 // COPY / ADDX: a lane per 8-element unit of a row (units in turn over the grid).
 template <int AK, int BK, int CK, bool BEN>
 __global__ __launch_bounds__(256) void ro_addx_fast_kernel(Job j, const uint8_t* __restrict__ params,
@@ -574,6 +627,22 @@ int run_norm_fast(DeviceState* st, const Job& j, const uint8_t* params, uint8_t*
     const Job jx = ja != nullptr ? *ja : j;
     const APlanes pv = po != nullptr ? *po : APlanes{};
     const uint32_t sel = (ak ? 1u : 0u) | (ja != nullptr ? 2u : 0u) | (po != nullptr ? 4u : 0u);
+    const u64 rows = (u64)j.c1 * j.c2;
+    if (sel <= 1 && rows <= (u64)st->cus && units <= 512) {
+        // rows that do not fill the chip: a workgroup per row
+        const unsigned wblocks = (unsigned)rows;
+        const size_t wlds = (size_t)(bcast ? 1 : j.n) * 16;
+#define CM_NORM_WG(AK, U)                                                                                           \
+    CM_LAUNCH("ro_norm_kernel", (ro_norm_wg_kernel<AK, U>), dim3(wblocks), dim3(256), wlds, s, j, params, dst,      \
+              entries, bcast, st->ro_tables)
+        if (units <= 256) {
+            if (ak) { CM_NORM_WG(1, 1); } else { CM_NORM_WG(0, 1); }
+        } else {
+            if (ak) { CM_NORM_WG(1, 2); } else { CM_NORM_WG(0, 2); }
+        }
+#undef CM_NORM_WG
+        return CM_OK;
+    }
 #define CM_NORM(AK, U, AX, PL)                                                                                     \
     CM_LAUNCH("ro_norm_kernel", (ro_norm_fast_kernel<AK, U, AX, PL>), dim3(blocks), dim3(256), plds, s, j, params, \
               dst, entries, bcast, st->ro_tables, jx, pa, bca, pv)

@@ -227,41 +227,66 @@ __device__ __forceinline__ int4 pack16(const int (&r)[8]) {
     return o;
 }
 
-// The int16 results of one NORM row (n elements, eps, LN or RMS) of the fast path: x[k] = unit
-// lane + 64 k of the row (int32, zero past the row), the parameters staged by
-// stage_norm_params at lds; 64-bit arithmetic where every element's bounds allow, the whole
-// row in 128 bits otherwise (a branch uniform over the wavefront).
+// The sums of a NORM row (or of a lane's part of it): sum x, sum x^2 (128-bit as lo / hi) and
+// max |x|.
+struct NormSums {
+    i64 s1;
+    u64 lo, hi;
+    uint32_t amax;
+};
+
 template <int UPL>
-__device__ __forceinline__ void norm_row_vals(uint32_t n, i64 eps, const int (&x)[UPL][8], const uint4* ro_lds,
-                                              bool bcast, const uint8_t* tab, uint32_t lane, uint32_t units, bool ln,
-                                              int4 (&o)[UPL]) {
-    i64 s1 = 0;
-    u64 lo = 0, hi = 0;
-    uint32_t amax = 0;
+__device__ __forceinline__ NormSums norm_sums(const int (&x)[UPL][8]) {
+    NormSums t{0, 0, 0, 0};
 #pragma unroll
     for (int k = 0; k < UPL; k++) {
 #pragma unroll
         for (int l = 0; l < 8; l++) {
             const i64 v = x[k][l];
-            s1 += v;
+            t.s1 += v;
             const u64 sq = (u64)(v * v);                 // |x| <= 2^31: x^2 <= 2^62
-            lo += sq;
-            hi += lo < sq ? 1 : 0;
+            t.lo += sq;
+            t.hi += t.lo < sq ? 1 : 0;
             const uint32_t av = (uint32_t)(v < 0 ? -v : v);
-            amax = av > amax ? av : amax;
+            t.amax = av > t.amax ? av : t.amax;
         }
     }
+    return t;
+}
+
+__device__ __forceinline__ void norm_sums_add(NormSums& a, const NormSums& b) {
+    a.s1 += b.s1;
+    const u64 nlo = a.lo + b.lo;
+    a.hi = a.hi + b.hi + (nlo < a.lo ? 1 : 0);
+    a.lo = nlo;
+    a.amax = b.amax > a.amax ? b.amax : a.amax;
+}
+
+// The wavefront's total in every lane.
+__device__ __forceinline__ void norm_sums_wave(NormSums& t) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
-        s1 += (i64)shfl64((u64)s1, off);
-        const u64 olo = shfl64(lo, off), ohi = shfl64(hi, off);
-        const u64 nlo = lo + olo;
-        hi = hi + ohi + (nlo < lo ? 1 : 0);
-        lo = nlo;
-        const uint32_t om = (uint32_t)__shfl_xor((int)amax, off, 64);
-        amax = om > amax ? om : amax;
+        NormSums o;
+        o.s1 = (i64)shfl64((u64)t.s1, off);
+        o.lo = shfl64(t.lo, off);
+        o.hi = shfl64(t.hi, off);
+        o.amax = (uint32_t)__shfl_xor((int)t.amax, off, 64);
+        norm_sums_add(t, o);
     }
-    const i128 S1 = s1, S2 = (i128)(((unsigned __int128)hi << 64) | lo);
+}
+
+// The int16 results of a NORM row (n elements, eps, LN or RMS) of the fast path from the row's
+// sums t: x[k] = unit u0 + ustride k of the row (int32, zero past the row), the parameters
+// staged by stage_norm_params at lds; 64-bit arithmetic where every element's bounds allow, the
+// lanes' units in 128 bits otherwise (a branch uniform over the wavefront; both give the exact
+// values).
+template <int UPL>
+__device__ __forceinline__ void norm_row_finish(uint32_t n, i64 eps, const NormSums& t, const int (&x)[UPL][8],
+                                                const uint4* ro_lds, bool bcast, const uint8_t* tab, uint32_t u0,
+                                                uint32_t ustride, uint32_t units, bool ln, int4 (&o)[UPL]) {
+    const i64 s1 = t.s1;
+    const uint32_t amax = t.amax;
+    const i128 S1 = s1, S2 = (i128)(((unsigned __int128)t.hi << 64) | t.lo);
     i128 D = ln ? ((i128)n * S2 - S1 * S1 + (i128)eps) : (S2 + (i128)eps);
     if (D <= 0) D = 1;
     u64 Rm;
@@ -274,9 +299,9 @@ __device__ __forceinline__ void norm_row_vals(uint32_t n, i64 eps, const int (&x
     bool wide = !a32;
 #pragma unroll
     for (int k = 0; k < UPL; k++) {
-        const uint32_t u = lane + 64 * k;
+        const uint32_t u = u0 + ustride * k;
         o[k] = make_int4(0, 0, 0, 0);
-        if (!a32 || u >= units) continue;           // a32 is uniform over the wavefront
+        if (!a32 || u >= units) continue;           // a32 is uniform over the row
         int r[8];
 #pragma unroll
         for (int l = 0; l < 8; l++) {
@@ -293,17 +318,25 @@ __device__ __forceinline__ void norm_row_vals(uint32_t n, i64 eps, const int (&x
         }
         o[k] = pack16(r);
     }
-    // rows with a value outside the 64-bit bounds: the whole row in 128 bits (a branch uniform
-    // over the wavefront)
     if (__any(wide)) {
         for (int k = 0; k < UPL; k++) {
-            const uint32_t u = lane + 64 * k;
+            const uint32_t u = u0 + ustride * k;
             if (u >= units) continue;
             int r[8];
             norm_unit_wide(x[k], u, units, ln, n, s1, Rm, shp, ro_lds, bcast, r);
             o[k] = pack16(r);
         }
     }
+}
+
+// A NORM row held by one wavefront: x[k] = unit lane + 64 k.
+template <int UPL>
+__device__ __forceinline__ void norm_row_vals(uint32_t n, i64 eps, const int (&x)[UPL][8], const uint4* ro_lds,
+                                              bool bcast, const uint8_t* tab, uint32_t lane, uint32_t units, bool ln,
+                                              int4 (&o)[UPL]) {
+    NormSums t = norm_sums<UPL>(x);
+    norm_sums_wave(t);
+    norm_row_finish<UPL>(n, eps, t, x, ro_lds, bcast, tab, lane, 64, units, ln, o);
 }
 
 }  // namespace ro

@@ -830,9 +830,9 @@ __global__ __launch_bounds__(kDaThreads) void decode_attn_kernel(const int16_t* 
             kv[u] = j < C && j != skip ? reinterpret_cast<const int4*>(kg + (uint64_t)j * HD)[kw] : make_int4(0, 0, 0, 0);
         }
     };
-    load_k(0, PREP ? pp.pos : 0xFFFFFFFFu);
     SmxStage stg;
-    smx_stage_load(stg, tsrc, 1024);
+    smx_stage_load(stg, tsrc, 1024);                        // ahead of the K loads: staged first
+    load_k(0, PREP ? pp.pos : 0xFFFFFFFFu);
     if constexpr (PREP) {
         // the prep, under the loads above: a thread per 8-element word: the group's q words, then k's, then v's
         const uint32_t b = bg / pp.KV, g = bg - b * pp.KV, H = pp.KV * G;
@@ -869,8 +869,10 @@ __global__ __launch_bounds__(kDaThreads) void decode_attn_kernel(const int16_t* 
         for (uint32_t e = t; e < G * HD / 2; e += kDaThreads) qs[e] = reinterpret_cast<const uint32_t*>(qg)[e];
     for (uint32_t e = t; e < G * HD; e += kDaThreads) oacc[e] = 0u;
     smx_stage_store(stg, tab, tsrc, 1024);
-    // orders qs and the prep's cache rows (workgroup-scope release / acquire) before their reads
-    __syncthreads();
+    // orders qs and the prep's cache rows (workgroup-scope release / acquire) before their reads;
+    // without the prep only LDS is shared, and the K loads stay in flight
+    if constexpr (PREP) __syncthreads();
+    else lds_barrier();
     if constexpr (PREP) {
         // the first K loads went out before the prep wrote row pos and left it out: that row now
 #pragma unroll
@@ -916,7 +918,7 @@ __global__ __launch_bounds__(kDaThreads) void decode_attn_kernel(const int16_t* 
         }
     };
     load_v(2 * kp0);
-    __syncthreads();
+    lds_barrier();
 
     // ---- phase 2: the softmax of every query row over its valid keys
     uint32_t v[G];
@@ -935,7 +937,7 @@ __global__ __launch_bounds__(kDaThreads) void decode_attn_kernel(const int16_t* 
         m[i] = wave_max(m[i]);
         if (lane == 0) red[wave * kDaMaxG + i] = m[i];
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (uint32_t i = 0; i < G; i++) {
         int x = red[i];
@@ -957,7 +959,7 @@ __global__ __launch_bounds__(kDaThreads) void decode_attn_kernel(const int16_t* 
         S[i] = wave_sum(S[i]);
         if (lane == 0) red2[wave * kDaMaxG + i] = (int32_t)S[i];
     }
-    __syncthreads();
+    lds_barrier();
     double rs[G];
 #pragma unroll
     for (uint32_t i = 0; i < G; i++) {
@@ -976,7 +978,7 @@ __global__ __launch_bounds__(kDaThreads) void decode_attn_kernel(const int16_t* 
             *reinterpret_cast<int*>(&ps[i * C + j]) = smx_p2<true>(e0, e1, rs[i]);
         }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- phase 3: o = P . V, VCH key pairs of a lane in flight at a time
     int acc[G][8];
@@ -1017,7 +1019,7 @@ __global__ __launch_bounds__(kDaThreads) void decode_attn_kernel(const int16_t* 
             const int x = group_sum<KPW>(acc[i][l]);
             if (lane % KPW == 0) atomicAdd(&oacc[i * HD + 8 * dc + l], (uint32_t)x);
         }
-    __syncthreads();
+    lds_barrier();
     for (uint32_t e = t; e < G * HD; e += kDaThreads)
         o[(uint64_t)bg * G * HD + e] = (int16_t)min(max((int32_t)oacc[e] >> 8, -32768), 32767);
 }
