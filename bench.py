@@ -210,8 +210,9 @@ GRAPH_KERNELS = ("gemm_planes_kernel", "split_rows_kernel", "split_cols_kernel",
                  "conv_dw3_kernel", "conv_dw3v_kernel", "pool_kernel", "pool_global_kernel", "pool2x2_kernel",
                  "softmax_long_kernel", "smx_etab_kernel", "copy_elems_kernel", "permute_elems_kernel",
                  "split_fold_kernel", "split_fold_lds_kernel", "skinny_wrap_kernel", "skinny_reduce_kernel",
-                 "skinny_planes_kernel", "decode_attn_kernel", "decode_prep_kernel",
-                 "gemm_reduce_kernel", "attention_kernel", "embed_rows_kernel")
+                 "skinny_planes_kernel", "skinny_mulact_kernel", "decode_attn_kernel", "decode_prep_kernel",
+                 "gemm_reduce_kernel", "attention_kernel", "embed_rows_kernel", "ro_fold_kernel",
+                 "ro_tload_kernel", "ro_xpose_kernel")
 
 
 def run_graph(args, torch, sim, feeds, out_name):
@@ -406,10 +407,14 @@ def smollm2_bench(args, torch, np):
     macs = shape.macs()
     kv_bytes = shape.layers * 2 * shape.batch * shape.kv * shape.ctx * shape.hd * 2
     step_bytes = shape.weight_bytes() + kv_bytes
-    # the linears (7 per layer and the tied head) run as skinny_planes_kernel launches that read
-    # every weight's byte planes once: 2 bytes per weight, the column sums aside
+    # the linears (7 per layer and the tied head) run as skinny_planes_kernel launches and, for
+    # gate / up with the SiLU gate, skinny_mulact_kernel launches; together they read every
+    # weight's byte planes once: 2 bytes per weight, the column sums aside
     sk_bytes = shape.weight_bytes()
-    sk_ms = per_kernel.get("skinny_planes_kernel", {}).get("ms", 0.0) or float("nan")
+    sk_ms = sum(per_kernel.get(k, {}).get("ms", 0.0) for k in ("skinny_planes_kernel", "skinny_mulact_kernel"))
+    sk_ms = sk_ms or float("nan")
+    # the decode attention reads each layer's K and V cache rows once
+    da_ms = per_kernel.get("decode_attn_kernel", {}).get("ms", 0.0) or float("nan")
     result = {
         "metric": "bit-exact fixed-point tokens/s (SmolLM2-360M-shaped decode, batch 16, 1024-row KV cache)",
         "value": round(shape.batch / (ms * 1e-3), 1),
@@ -430,10 +435,16 @@ def smollm2_bench(args, torch, np):
         "roofline": {"bound": "hbm", "achieved": round(sk_bytes / (sk_ms * 1e-3) / 1e9, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(sk_bytes / (sk_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "skinny_planes_kernel", "kernel_ms_per_step": sk_ms,
-                     "bytes_per_step": sk_bytes,
-                     "note": "the linears (7 per layer and the tied head) against their algorithmic bytes: "
-                             "every int16 weight once (its two byte planes)"},
+                     "kernel": "skinny_planes_kernel", "kernels": ["skinny_planes_kernel", "skinny_mulact_kernel"],
+                     "kernel_ms_per_step": sk_ms, "bytes_per_step": sk_bytes,
+                     "note": "the linears (7 per layer and the tied head: skinny_planes_kernel and the gate / up "
+                             "launches of skinny_mulact_kernel) against their algorithmic bytes: every int16 "
+                             "weight once (its two byte planes)"},
+        "attention_roofline": {"bound": "hbm", "kernel": "decode_attn_kernel", "kernel_ms_per_step": da_ms,
+                               "bytes_per_step": kv_bytes,
+                               "achieved": round(kv_bytes / (da_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                               "unit": "GB/s", "frac": round(kv_bytes / (da_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                               "note": "every layer's K and V cache rows once"},
         "kernels_ms_per_step": per_kernel,
         "graph_build_s": round(build_s, 1),
     }
