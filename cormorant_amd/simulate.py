@@ -85,6 +85,10 @@ class Simulator:
         self._plan = None                                  # MatMuls fed byte planes by their A's producer
         for t in graph.input_tensors + graph.output_tensors:
             self._infos[t.onnx_name] = t
+        # the fused launches that apply a row-ops job inside another unit leave the device's
+        # parameter RAM as it was; a graph with a P_KEEP job (which reads that RAM) runs every
+        # row-ops job on the unit itself instead
+        self._ram_free = not any(isinstance(sn, RowOpsNode) and (sn.op & units.F_P_KEEP) for sn in graph.nodes)
         for sn in graph.nodes:
             for t in list(sn.inputs) + [sn.output]:
                 if t is not None:
@@ -622,6 +626,8 @@ class Simulator:
     def _output_job_fusable(self, sn, nxt) -> bool:
         """``nxt`` is a one-job COPY / ADDX adapter over whole rows whose B is the skinny
         MatMul ``sn``'s output (and whose A is another tensor): the pair runs as one launch."""
+        if not self._ram_free:
+            return False
         if not (self._skinny_planes_ok(sn) and isinstance(nxt, RowOpsAdapter) and len(nxt.inputs) == 2
                 and getattr(nxt, "pos_t", None) is None and getattr(nxt, "table", None) is None):
             return False
@@ -711,6 +717,8 @@ class Simulator:
     def _mulact_fusable(self, group, nxt) -> bool:
         """``nxt`` is a one-job MULACT adapter over whole rows of the two skinny plane products
         in ``group`` (gate first, then up, m columns each): the three run as one launch."""
+        if not self._ram_free:
+            return False
         if len(group) != 2 or not isinstance(nxt, RowOpsAdapter) or len(nxt.inputs) != 2:
             return False
         if getattr(nxt, "pos_t", None) is not None or getattr(nxt, "table", None) is not None:
@@ -1056,6 +1064,8 @@ class Simulator:
     def _prep_attention_fusable(self, sn, nxt) -> bool:
         """``nxt`` is the decode attention of ``sn``'s outputs: q = the prep's qr, the caches the
         prep writes, their shapes the ones both calls take."""
+        if not self._ram_free:
+            return False
         if not (isinstance(sn, DecodePrepNode) and isinstance(nxt, DecodeAttentionNode)):
             return False
         q, k, v, kc, vc = sn.inputs[:5]
