@@ -92,6 +92,12 @@ MM_CASES = [  # n, k, m, batch, a_bs_mode, b_bs_mode, layout, kw, full_range, wr
     (64, 4096, 64, 1, 1, 1, "row", 0, True, True),
     (129, 1536, 130, 1, 1, 1, "trans", 0, False, True),
     (96, 1536, 40, 3, 1, 0, "row", 0, True, True),
+    # wrap products of one slice at sizes past the split over k: BERT's output projection,
+    # ragged rows and columns, the packed and transposed images
+    (3072, 768, 768, 1, 1, 1, "row", 0, True, True),
+    (1024, 2048, 640, 1, 1, 1, "packed", 0, True, True),
+    (1000, 1024, 1000, 1, 1, 1, "row", 0, True, True),
+    (640, 4096, 1000, 1, 1, 1, "trans", 0, True, True),
 ]
 
 
