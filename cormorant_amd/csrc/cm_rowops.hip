@@ -321,40 +321,72 @@ __global__ __launch_bounds__(256) void ro_norm_fast_kernel(Job j, const uint8_t*
     }
 }
 
-// NORM over few rows: a workgroup per row (rows in turn over the grid), UPL units of 8 elements
-// per thread (n <= 2048 UPL), the wavefronts' sums added through LDS: a quarter of the serial
-// arithmetic of the wavefront per row for the launches whose rows do not fill the chip.
-template <int AK, int UPL>
-__global__ __launch_bounds__(256) void ro_norm_wg_kernel(Job j, const uint8_t* __restrict__ params, uint8_t* pram_dst,
+// NORM with a workgroup of TPR threads per row (rows in turn over the grid): UPL units of 8
+// elements per thread (n <= 8 TPR UPL), the wavefronts' sums added through LDS.  A wavefront per
+// row leaves each lane a long serial chain of 64-bit arithmetic over several units at a few
+// wavefronts per SIMD; here a lane holds one or two units and a row has TPR / 64 wavefronts.
+// ADDX and PL as in ro_norm_fast_kernel: the residual add's int32 output formed in registers,
+// stored and normalised; the output's byte planes and per-slab row sums for the next GEMM.
+template <int AK, int UPL, bool ADDX, bool PL, int TPR>
+__global__ __launch_bounds__(TPR) void ro_norm_wg_kernel(Job j, const uint8_t* __restrict__ params, uint8_t* pram_dst,
                                                          uint32_t p_entries, bool bcast,
-                                                         const uint8_t* __restrict__ tab) {
+                                                         const uint8_t* __restrict__ tab, Job ja,
+                                                         const uint8_t* __restrict__ pa, bool bca, APlanes po) {
+    constexpr int NWV = TPR / 64;
     extern __shared__ __attribute__((aligned(16))) uint4 ro_lds[];
-    __shared__ NormSums wsum[2][4];
+    __shared__ NormSums wsum[2][NWV];
+    __shared__ int32_t slab_acc[2][4];                   // a row's slab sums (n <= 4096)
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const u64 rows = (u64)j.c1 * j.c2;
     const bool ln = (j.op & F_NORM_LN) != 0;
     const uint32_t units = j.n / 8;
-    int x[UPL][8];
+    const uint32_t nsl = bcast ? 1u : j.n;
+    uint4* a_lds = ro_lds + nsl;                         // the ADDX job's parameters
+    int x[UPL][8], y[UPL][8];
     auto load_row = [&](u64 row) {
-        const uint32_t i1 = (uint32_t)(row % j.c1), i2 = (uint32_t)(row / j.c1);
-        const uint8_t* ra = j.a + (u64)i2 * j.a_s2 + (u64)i1 * j.a_s1;
+        const Job& jl = ADDX ? ja : j;
+        const uint32_t i1 = (uint32_t)(row % jl.c1), i2 = (uint32_t)(row / jl.c1);
+        const uint8_t* ra = jl.a + (u64)i2 * jl.a_s2 + (u64)i1 * jl.a_s1;
 #pragma unroll
         for (int k = 0; k < UPL; k++) {
-            const uint32_t u = t + 256 * k;
+            const uint32_t u = t + TPR * k;
             if (u < units) {
                 ld_unit<AK>(ra, u, x[k]);
+                if constexpr (ADDX) ld_unit<0>(ja.b + (u64)i2 * ja.b_s2 + (u64)i1 * ja.b_s1, u, y[k]);
             } else {
 #pragma unroll
-                for (int l = 0; l < 8; l++) x[k][l] = 0;
+                for (int l = 0; l < 8; l++) x[k][l] = y[k][l] = 0;
             }
         }
     };
     u64 row = blockIdx.x;
     if (row < rows) load_row(row);                       // in flight while the parameters are staged
     pram_load(params, pram_dst, p_entries);
-    stage_norm_params(ro_lds, params, bcast ? 1u : j.n, units, j.bq_sh);
+    if constexpr (ADDX) {
+        for (uint32_t i = t; i < (bca ? 1u : ja.n); i += TPR) a_lds[pslot(i, units)] = reinterpret_cast<const uint4*>(pa)[i];
+    }
+    stage_norm_params(ro_lds, params, nsl, units, j.bq_sh);
+    if (t < 8) slab_acc[t >> 2][t & 3] = 0;
     __syncthreads();
+    const bool scale = (ja.op & F_SCALE) != 0, relu = (ja.op & F_RELU) != 0;
+    const uint32_t nslab = min(po.nsum, (units + 127) / 128);
     for (uint32_t it = 0; row < rows; row += gridDim.x, it++) {
+        const uint32_t i1 = (uint32_t)(row % j.c1), i2 = (uint32_t)(row / j.c1);
+        if constexpr (ADDX) {
+            // the ADDX outputs (int32) replace the row in registers and go to ja.c
+            uint8_t* rc1 = ja.c + (u64)i2 * ja.c_s2 + (u64)i1 * ja.c_s1;
+#pragma unroll
+            for (int k = 0; k < UPL; k++) {
+                const uint32_t u = t + TPR * k;
+                if (u >= units) continue;
+                int r[8];
+                addx_unit<0, 1, true>(x[k], y[k], u, units, ja, a_lds, bca, scale, relu, r);
+                store_stream(rc1 + 32u * u, make_int4(r[0], r[1], r[2], r[3]));
+                store_stream(rc1 + 32u * u + 16, make_int4(r[4], r[5], r[6], r[7]));
+#pragma unroll
+                for (int l = 0; l < 8; l++) x[k][l] = r[l];
+            }
+        }
         NormSums ts = norm_sums<UPL>(x);
         norm_sums_wave(ts);
         NormSums* ws = wsum[it & 1];                     // alternate: a row's reads end before the next's writes
@@ -362,14 +394,40 @@ __global__ __launch_bounds__(256) void ro_norm_wg_kernel(Job j, const uint8_t* _
         __syncthreads();
         ts = ws[0];
 #pragma unroll
-        for (int w = 1; w < 4; w++) norm_sums_add(ts, ws[w]);
+        for (int w = 1; w < NWV; w++) norm_sums_add(ts, ws[w]);
         int4 o[UPL];
-        norm_row_finish<UPL>(j.n, j.eps, ts, x, ro_lds, bcast, tab, t, 256, units, ln, o);
-        const uint32_t i1 = (uint32_t)(row % j.c1), i2 = (uint32_t)(row / j.c1);
+        norm_row_finish<UPL>(j.n, j.eps, ts, x, ro_lds, bcast, tab, t, TPR, units, ln, o);
         uint8_t* rc = j.c + (u64)i2 * j.c_s2 + (u64)i1 * j.c_s1;
 #pragma unroll
-        for (int k = 0; k < UPL; k++)
-            if (t + 256 * k < units) store_stream(rc + 16u * (t + 256 * k), o[k]);
+        for (int k = 0; k < UPL; k++) {
+            const uint32_t u = t + TPR * k;
+            if (u < units) store_stream(rc + 16u * u, o[k]);
+        }
+        if constexpr (PL) {
+            int32_t* sa = slab_acc[it & 1];
+#pragma unroll
+            for (int k = 0; k < UPL; k++) {
+                const uint32_t u = t + TPR * k;
+                int32_t v = 0;
+                if (u < units) {
+                    uint2 h, l;
+                    split8(o[k], h, l);
+                    *reinterpret_cast<uint2*>(po.hi + row * po.k + 8u * u) = h;
+                    *reinterpret_cast<uint2*>(po.lo + row * po.k + 8u * u) = l;
+                    v = sum8(o[k]);
+                }
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+                // a wavefront's 64 units lie in one 128-unit slab (1024 elements)
+                const uint32_t u0 = wave * 64 + TPR * k;
+                if (lane == 0 && u0 < units) atomicAdd(&sa[u0 / 128], v);
+            }
+            __syncthreads();
+            if (t < nslab) {
+                po.part[(u64)t * po.lines + row] = sa[t];
+                sa[t] = 0;                               // for the row after next
+            }
+        }
         if (row + gridDim.x < rows) load_row(row + gridDim.x);
     }
 }
@@ -620,26 +678,37 @@ bool norm_fast_ok(const Job& j) {
 int run_norm_fast(DeviceState* st, const Job& j, const uint8_t* params, uint8_t* dst, uint32_t entries, bool bcast,
                   const Job* ja, const uint8_t* pa, bool bca, const APlanes* po, hipStream_t s) {
     const uint32_t units = j.n / 8;
-    const uint32_t upl = units <= 64 ? 1 : units <= 128 ? 2 : units <= 256 ? 4 : 8;
-    const unsigned blocks = (unsigned)std::min<u64>(((u64)j.c1 * j.c2 + 3) / 4, (u64)st->cus * 8);
+    const uint32_t upl = units <= 64 ? 1 : 2;        // larger rows take the workgroup kernel above
+    // with the ADDX job two parameter blocks are staged per workgroup: fewer workgroups, more
+    // rows each (measured at BERT's 3072 x 768: 17.3 us at two per CU, 19.2 at eight)
+    const unsigned blocks = (unsigned)std::min<u64>(((u64)j.c1 * j.c2 + 3) / 4, (u64)st->cus * (ja != nullptr ? 2 : 8));
     const size_t plds = (size_t)((bcast ? 1 : j.n) + (ja != nullptr ? (bca ? 1 : ja->n) : 0)) * 16;
     const uint32_t ak = ja != nullptr ? (ja->op >> 4) & 3 : (j.op >> 4) & 3;
     const Job jx = ja != nullptr ? *ja : j;
     const APlanes pv = po != nullptr ? *po : APlanes{};
     const uint32_t sel = (ak ? 1u : 0u) | (ja != nullptr ? 2u : 0u) | (po != nullptr ? 4u : 0u);
     const u64 rows = (u64)j.c1 * j.c2;
-    if (sel <= 1 && rows <= (u64)st->cus && units <= 512) {
-        // rows that do not fill the chip: a workgroup per row
-        const unsigned wblocks = (unsigned)rows;
-        const size_t wlds = (size_t)(bcast ? 1 : j.n) * 16;
-#define CM_NORM_WG(AK, U)                                                                                           \
-    CM_LAUNCH("ro_norm_kernel", (ro_norm_wg_kernel<AK, U>), dim3(wblocks), dim3(256), wlds, s, j, params, dst,      \
-              entries, bcast, st->ro_tables)
-        if (units <= 256) {
-            if (ak) { CM_NORM_WG(1, 1); } else { CM_NORM_WG(0, 1); }
-        } else {
-            if (ak) { CM_NORM_WG(1, 2); } else { CM_NORM_WG(0, 2); }
+    if ((rows <= (u64)st->cus || units > 128) && units <= 512) {
+        // rows that do not fill the chip (the decode step's 16), or rows past 1024 elements
+        // (four or more units a lane would spill): a workgroup of 256 per row, rows in turn over
+        // at most four workgroups per CU so that each stages the parameters once for many rows
+        const unsigned wblocks = (unsigned)std::min<u64>(rows, (u64)st->cus * 4);
+#define CM_NORM_WG(AK, U, AX, PL, T)                                                                                \
+    CM_LAUNCH("ro_norm_kernel", (ro_norm_wg_kernel<AK, U, AX, PL, T>), dim3(wblocks), dim3(T), plds, s, j, params,  \
+              dst, entries, bcast, st->ro_tables, jx, pa, bca, pv)
+#define CM_NORM_WG_T(AK, AX, PL)                                                                                    \
+    if (units <= 256) { CM_NORM_WG(AK, 1, AX, PL, 256); } else { CM_NORM_WG(AK, 2, AX, PL, 256); }
+        switch (sel) {
+        case 0: { CM_NORM_WG_T(0, false, false) } break;
+        case 1: { CM_NORM_WG_T(1, false, false) } break;
+        case 4: { CM_NORM_WG_T(0, false, true) } break;
+        case 5: { CM_NORM_WG_T(1, false, true) } break;
+        case 2: { CM_NORM_WG_T(0, true, false) } break;
+        case 3: { CM_NORM_WG_T(1, true, false) } break;
+        case 6: { CM_NORM_WG_T(0, true, true) } break;
+        default: { CM_NORM_WG_T(1, true, true) } break;
         }
+#undef CM_NORM_WG_T
 #undef CM_NORM_WG
         return CM_OK;
     }
@@ -647,8 +716,7 @@ int run_norm_fast(DeviceState* st, const Job& j, const uint8_t* params, uint8_t*
     CM_LAUNCH("ro_norm_kernel", (ro_norm_fast_kernel<AK, U, AX, PL>), dim3(blocks), dim3(256), plds, s, j, params, \
               dst, entries, bcast, st->ro_tables, jx, pa, bca, pv)
 #define CM_NORM_U(AK, AX, PL)                                                                                      \
-    if (upl == 1) { CM_NORM(AK, 1, AX, PL); } else if (upl == 2) { CM_NORM(AK, 2, AX, PL); }                        \
-    else if (upl == 4) { CM_NORM(AK, 4, AX, PL); } else { CM_NORM(AK, 8, AX, PL); }
+    if (upl == 1) { CM_NORM(AK, 1, AX, PL); } else { CM_NORM(AK, 2, AX, PL); }
     switch (sel) {
     case 0: { CM_NORM_U(0, false, false) } break;
     case 1: { CM_NORM_U(1, false, false) } break;

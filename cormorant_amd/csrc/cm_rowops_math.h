@@ -115,13 +115,15 @@ __device__ __forceinline__ Param param_of(uint4 w) {
 // wavefront (consecutive units u) read consecutive 16-byte slots; a broadcast block is slot 0.
 __device__ __forceinline__ uint32_t pslot(uint32_t col, uint32_t units) { return (col & 7) * units + (col >> 3); }
 
-// NORM parameters as the element loop uses them: G, the shift sc and Bq 2^bq_sh (bq_sh <= 40:
-// below 2^61), one 16-byte entry per column.
+// NORM parameters as the element loop uses them: G, the shift sc and Bq 2^bq_sh + 2^(sc - 1)
+// (the bias with the rounding half folded in: bq_sh <= 40 and sc <= 63 keep it below 2^63),
+// one 16-byte entry per column.
+__device__ __forceinline__ i64 norm_half(uint32_t sc) { return sc ? (i64)1 << (sc - 1) : 0; }
 __device__ __forceinline__ void stage_norm_params(uint4* lds, const uint8_t* params, uint32_t entries,
                                                   uint32_t units, uint32_t bq_sh) {
     for (uint32_t i = threadIdx.x; i < entries; i += blockDim.x) {
         const Param q = param_of(reinterpret_cast<const uint4*>(params)[i]);
-        const u64 bs = (u64)(q.bq * ((i64)1 << bq_sh));
+        const u64 bs = (u64)(q.bq * ((i64)1 << bq_sh) + norm_half((uint32_t)q.sc));
         lds[pslot(i, units)] = make_uint4((uint32_t)q.g, (uint32_t)q.sc, (uint32_t)bs, (uint32_t)(bs >> 32));
     }
 }
@@ -213,7 +215,7 @@ __device__ __forceinline__ void norm_unit_wide(const int (&x)[8], uint32_t u, ui
         const uint4 e = lds[bcast ? 0u : l * units + u];
         const i128 A = ln ? (i128)n * x[l] - s1 : (i128)x[l];
         const i128 P1 = (A * (i128)Rm) >> shp;
-        const i64 bs = (i64)(((u64)e.w << 32) | e.z);
+        const i64 bs = (i64)(((u64)e.w << 32) | e.z) - norm_half(e.y);
         r[l] = (int)sat16(rne_shr(P1 * (i128)(int32_t)e.x + (i128)bs, (int)e.y));
     }
 }
@@ -293,10 +295,12 @@ __device__ __forceinline__ void norm_row_finish(uint32_t n, i64 eps, const NormS
     int sh;
     rsqrt_bf(D, Rm, sh, tab);
     const int shp = sh - 24;                             // >= 7: sh >= 31
-    // A = n x - S1 (LN) or x in 32 bits for the whole row: A Rm < 2^63
+    // A = n x - S1 (LN) or x in 32 bits for the whole row: A Rm < 2^63; and |P1| = |A Rm| >> shp
+    // below 2^31 for the whole row (one bound instead of a check per element)
     const u64 abound = ln ? (u64)n * amax + (u64)(s1 < 0 ? -s1 : s1) : (u64)amax;
-    const bool a32 = abound < ((u64)1 << 31);
+    const bool a32 = abound < ((u64)1 << 31) && ((abound * Rm) >> shp) < ((u64)1 << 31) - 2;
     bool wide = !a32;
+    const int32_t rm_lo = (int32_t)(uint32_t)Rm;     // Rm - 2^32: Rm lies in [2^31, 2^32)
 #pragma unroll
     for (int k = 0; k < UPL; k++) {
         const uint32_t u = u0 + ustride * k;
@@ -308,12 +312,17 @@ __device__ __forceinline__ void norm_row_finish(uint32_t n, i64 eps, const NormS
             const uint4 e = ro_lds[bcast ? 0u : l * units + u];
             const int32_t G = (int32_t)e.x;
             const uint32_t sc = e.y;
-            const i64 bs = (i64)(((u64)e.w << 32) | e.z);
+            const i64 bsh = (i64)(((u64)e.w << 32) | e.z);     // the bias + 2^(sc - 1)
             // A in 32 bits (a32): the low 32 bits of n x - S1 are A itself
             const int32_t A = ln ? (int32_t)((uint32_t)n * (uint32_t)x[k][l] - (uint32_t)s1) : x[k][l];
-            const i64 P1 = ((i64)A * (i64)(uint32_t)Rm) >> shp;
-            wide |= !(P1 < ((i64)1 << 31) && P1 > -((i64)1 << 31) && sc <= 61);
-            const i64 v = rne_shr_fast((i64)(int32_t)P1 * G + bs, sc);
+            // A Rm = A (Rm - 2^32) + A 2^32, a signed 32 x 32 product and a high-word add
+            const i64 P1 = ((i64)A * (i64)rm_lo + (i64)((u64)(uint32_t)A << 32)) >> shp;
+            wide |= sc > 61;
+            // round half to even of v / 2^sc, v = P1 G + bias: w = v + 2^(sc - 1), floor(w / 2^sc),
+            // less one where w is an exact multiple of 2^sc (a tie) and the quotient is odd
+            const i64 w = (i64)(int32_t)P1 * G + bsh;
+            i64 v = w >> sc;
+            v &= ~(i64)((u64)w << ((64 - sc) & 63) == 0);
             r[l] = v > 32767 ? 32767 : (v < -32768 ? -32768 : (int)v);
         }
         o[k] = pack16(r);

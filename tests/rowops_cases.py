@@ -32,6 +32,10 @@ RO_CASES = [  # label, op word, n, rows, blocks, kinds (a, b, c bytes), param ra
     ("addx_relu_bcast_u8", 2 | (1 << 12) | (1 << 13) | (1 << 15), 104, 4, 3),
     ("norm_ln_i16_64", 5 | (1 << 16), 64, 9, 1),
     ("norm_rms_i16_2048", 5, 2048, 3, 1),
+    # rows past 1024 elements over more rows than compute units: the workgroup-per-row kernel
+    # taking rows in turn
+    ("norm_ln_i32_4096_rows", 5 | (1 << 4) | (1 << 16), 4096, 150, 3),
+    ("norm_rms_i16_1536_rows", 5, 1536, 400, 2),
     # the 16-byte unit kernel of DEQUANT / MULACT / GATE / ROPE: shifts on both sides of its 64-bit
     # bounds (sa, sb <= 23, sc <= 61), extreme int16 operands, RoPE tables past 2^23
     ("dequant_i16_u8", 3 | (2 << 8), 512, 4, 2),
