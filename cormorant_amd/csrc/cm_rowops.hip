@@ -179,38 +179,60 @@ __device__ __forceinline__ void stage_params(uint4* lds, const uint8_t* params, 
     __syncthreads();
 }
 
-// One COPY / ADDX unit in 128-bit arithmetic (the scale flag, or shifts past the 64-bit bounds).
+// COPY / ADDX parameters as the element loop uses them, one 16-byte entry per column: the
+// three shifts and two fast-path flags in one word (sa | sb << 8 | sc << 16; bit 24: every
+// term within the 64-bit bounds with a 32-bit B, bit 25: with a 16-bit B), G, and
+// Bq 2^bq_sh + 2^(sc - 1) (the bias with the rounding half folded in; 0 when bq_sh > 40, a
+// job the 128-bit path takes whole).
+__device__ __forceinline__ void stage_addx_params(uint4* lds, const uint8_t* params, uint32_t entries, uint32_t units,
+                                                  uint32_t bq_sh) {
+    for (uint32_t i = threadIdx.x; i < entries; i += blockDim.x) {
+        const Param q = param_of(reinterpret_cast<const uint4*>(params)[i]);
+        const bool base = q.sa <= 30 && q.sc <= 61;
+        const uint32_t w = (uint32_t)q.sa | ((uint32_t)q.sb << 8) | ((uint32_t)q.sc << 16) |
+                           ((base && q.sb <= 30) ? 1u << 24 : 0u) | ((base && q.sb <= 46) ? 1u << 25 : 0u);
+        const u64 bs = bq_sh <= 40 ? (u64)(q.bq * ((i64)1 << bq_sh) + norm_half((uint32_t)q.sc)) : 0;
+        lds[pslot(i, units)] = make_uint4(w, (uint32_t)q.g, (uint32_t)bs, (uint32_t)(bs >> 32));
+    }
+}
+
+// One COPY / ADDX unit in 128-bit arithmetic (the scale flag, or shifts past the 64-bit
+// bounds), from the job's own parameter block in global memory.
 __device__ __forceinline__ void addx_unit_wide(const int (&x)[8], const int (&y)[8], bool ben, int ck, uint32_t u,
-                                            uint32_t units, uint32_t bq_sh, bool scale, const uint4* lds, bool bcast, int (&r)[8]) {
+                                            uint32_t bq_sh, bool scale, const uint8_t* praw, bool bcast, int (&r)[8]) {
     for (int l = 0; l < 8; l++) {
-        const Param q = param_of(lds[bcast ? 0u : l * units + u]);
+        const Param q = ld_param(praw, 8 * u + l, bcast);
         const i128 s = ((i128)x[l] << q.sa) + ((i128)(ben ? y[l] : 0) << q.sb) + ((i128)q.bq << bq_sh);
         const i128 v = rne_shr(scale ? s * (i128)q.g : s, q.sc);
         r[l] = (int)(ck == 0 ? sat16(v) : sat32(v));
     }
 }
 
-// One COPY / ADDX unit: 64-bit arithmetic where the shifts keep every term below 2^61, else
-// the 128-bit form (a branch taken by the lanes that need it).
+// One COPY / ADDX unit from the staged entries (stage_addx_params): 64-bit arithmetic where
+// every term stays below 2^61 (x << sa <= 2^61, y << sb, Bq << bq_sh <= 2^61), round half to even
+// as one shift and an exact-tie test; else the 128-bit form (a branch taken by the lanes that
+// need it).
 template <int BK, int CK, bool BEN>
 __device__ __forceinline__ void addx_unit(const int (&x)[8], const int (&y)[8], uint32_t u, uint32_t units,
-                                          const Job& j, const uint4* ro_lds, bool bcast, bool scale, bool relu,
-                                          int (&r)[8]) {
+                                          const Job& j, const uint4* ro_lds, const uint8_t* praw, bool bcast,
+                                          bool scale, bool relu, int (&r)[8]) {
     bool wide = scale || j.bq_sh > 40;
 #pragma unroll
     for (int l = 0; l < 8; l++) {
-        const Param q = param_of(ro_lds[bcast ? 0u : l * units + u]);
+        const uint4 e = ro_lds[bcast ? 0u : l * units + u];
+        const uint32_t sa = e.x & 63, sb = (e.x >> 8) & 63, sc = (e.x >> 16) & 63;
+        wide |= ((e.x >> (BK == 0 ? 25 : 24)) & 1) == 0;
         const i64 yv = BEN ? (i64)y[l] : 0;
-        // each term below 2^61 when: x (32 bits) << sa <= 30, y << sb (16 / 32 bits), Bq (22) << bq_sh <= 40
-        wide |= !(q.sa <= 30 && q.sb <= (BK == 0 ? 46 : 30) && q.sc <= 61);
-        i64 v = rne_shr_fast((i64)x[l] * (i64)((u64)1 << (q.sa & 31)) + yv * (i64)((u64)1 << (q.sb & 63)) +
-                                 q.bq * (i64)((u64)1 << (j.bq_sh & 63)), q.sc & 63);
+        // shifts on the unsigned images (defined for negative operands; exact within the bounds)
+        const i64 w = (i64)(((u64)(i64)x[l] << (sa & 31)) + ((u64)yv << sb) + (((u64)e.w << 32) | e.z));
+        i64 v = w >> sc;
+        v &= ~(i64)((u64)w << ((64 - sc) & 63) == 0);
         v = CK == 0 ? (v > 32767 ? 32767 : (v < -32768 ? -32768 : v))
                     : (v > 2147483647 ? 2147483647 : (v < -2147483647LL - 1 ? -2147483647LL - 1 : v));
         r[l] = (int)v;
     }
     if (__any(wide)) {
-        if (wide) addx_unit_wide(x, y, BEN, CK, u, units, j.bq_sh, scale, ro_lds, bcast, r);
+        if (wide) addx_unit_wide(x, y, BEN, CK, u, j.bq_sh, scale, praw, bcast, r);
     }
     if (relu) {
 #pragma unroll
@@ -292,8 +314,7 @@ __global__ __launch_bounds__(256) void ro_norm_fast_kernel(Job j, const uint8_t*
     if (row < rows) load_row(row);                       // in flight while the parameters are staged
     pram_load(params, pram_dst, p_entries);
     if constexpr (ADDX) {
-        for (uint32_t i = threadIdx.x; i < (bca ? 1u : ja.n); i += blockDim.x)
-            a_lds[pslot(i, units)] = reinterpret_cast<const uint4*>(pa)[i];
+        stage_addx_params(a_lds, pa, bca ? 1u : ja.n, units, ja.bq_sh);
     }
     stage_norm_params(ro_lds, params, nsl, units, j.bq_sh);
     __syncthreads();
@@ -308,7 +329,7 @@ __global__ __launch_bounds__(256) void ro_norm_fast_kernel(Job j, const uint8_t*
                 const uint32_t u = lane + 64 * k;
                 if (u >= units) continue;
                 int r[8];
-                addx_unit<0, 1, true>(x[k], y[k], u, units, ja, a_lds, bca, scale, relu, r);
+                addx_unit<0, 1, true>(x[k], y[k], u, units, ja, a_lds, pa, bca, scale, relu, r);
                 store_stream(rc1 + 32u * u, make_int4(r[0], r[1], r[2], r[3]));
                 store_stream(rc1 + 32u * u + 16, make_int4(r[4], r[5], r[6], r[7]));
 #pragma unroll
@@ -363,7 +384,7 @@ __global__ __launch_bounds__(TPR) void ro_norm_wg_kernel(Job j, const uint8_t* _
     if (row < rows) load_row(row);                       // in flight while the parameters are staged
     pram_load(params, pram_dst, p_entries);
     if constexpr (ADDX) {
-        for (uint32_t i = t; i < (bca ? 1u : ja.n); i += TPR) a_lds[pslot(i, units)] = reinterpret_cast<const uint4*>(pa)[i];
+        stage_addx_params(a_lds, pa, bca ? 1u : ja.n, units, ja.bq_sh);
     }
     stage_norm_params(ro_lds, params, nsl, units, j.bq_sh);
     if (t < 8) slab_acc[t >> 2][t & 3] = 0;
@@ -380,7 +401,7 @@ __global__ __launch_bounds__(TPR) void ro_norm_wg_kernel(Job j, const uint8_t* _
                 const uint32_t u = t + TPR * k;
                 if (u >= units) continue;
                 int r[8];
-                addx_unit<0, 1, true>(x[k], y[k], u, units, ja, a_lds, bca, scale, relu, r);
+                addx_unit<0, 1, true>(x[k], y[k], u, units, ja, a_lds, pa, bca, scale, relu, r);
                 store_stream(rc1 + 32u * u, make_int4(r[0], r[1], r[2], r[3]));
                 store_stream(rc1 + 32u * u + 16, make_int4(r[4], r[5], r[6], r[7]));
 #pragma unroll
@@ -439,7 +460,8 @@ __global__ __launch_bounds__(256) void ro_addx_fast_kernel(Job j, const uint8_t*
     extern __shared__ __attribute__((aligned(16))) uint4 ro_lds[];
     pram_load(params, pram_dst, p_entries);
     const uint32_t units = j.n / 8;
-    stage_params(ro_lds, params, bcast ? 1u : j.n, units);
+    stage_addx_params(ro_lds, params, bcast ? 1u : j.n, units, j.bq_sh);
+    __syncthreads();
     const u64 total = (u64)units * j.c1 * j.c2;
     const bool scale = (j.op & F_SCALE) != 0, relu = (j.op & F_RELU) != 0;
     for (u64 w = (u64)blockIdx.x * blockDim.x + threadIdx.x; w < total; w += (u64)gridDim.x * blockDim.x) {
@@ -456,7 +478,7 @@ __global__ __launch_bounds__(256) void ro_addx_fast_kernel(Job j, const uint8_t*
         }
         if constexpr (BEN) ld_unit<BK>(j.b + (u64)i2 * j.b_s2 + (u64)i1 * j.b_s1, u, y);
         int r[8];
-        addx_unit<BK, CK, BEN>(x, y, u, units, j, ro_lds, bcast, scale, relu, r);
+        addx_unit<BK, CK, BEN>(x, y, u, units, j, ro_lds, params, bcast, scale, relu, r);
         uint8_t* rc = j.c + (u64)i2 * j.c_s2 + (u64)i1 * j.c_s1;
         if constexpr (CK == 0) {
             int4 o;
