@@ -18,8 +18,8 @@
 // Workgroup: 4 wavefronts, wavefront w owns queries q0 + 16 w .. + 15 end to end.  MFMA
 // layouts (16 x 16 blocks): operand lane l holds row / column l % 16 and 16 bytes of k slot
 // group l / 16; result lane l holds column l % 16, rows 4 (l / 16) .. + 3.
-//   phase 1: s for key block kb (16 keys) = K rows (A, from the projection rows, split in
-//            registers) x Q rows (B, loaded once): lane (query l % 16, g = l / 16) ends up
+//   phase 1: s for key block kb (16 keys) = K rows (A: from the projection rows, split into
+//            limbs once per workgroup, 64 keys at a time through LDS) x Q rows (B, loaded once): lane (query l % 16, g = l / 16) ends up
 //            with the scores of keys 16 kb + 4 g + r, r < 4, for all T / 16 blocks;
 //   phase 2: the softmax per query over its lane group (shuffles across g; no LDS):
 //            e = TAB[y & 4095] >> (y >> 12), y = (max - s) Cm >> Cs, R = floor(2^40 / S),
@@ -29,8 +29,9 @@
 //            keys (slot 16 g + 4 q + r of k step ks = key 16 (4 ks + q) + 4 g + r); V^T is
 //            split into byte planes in LDS in that key order, 32 d at a time (the first half
 //            staged before phase 1, the second after the first half's products).
-// LDS: TAB (16 KiB) + V^T hi / lo planes [32][T + 16] + the V column-sum partials, 42.6 KiB at
-// T = 384: three workgroups per compute unit, so that BERT's 576 workgroups are resident at once.
+// LDS: TAB (16 KiB; during phase 1 the K chunks' limbs, two buffers of 64 keys) + V^T hi / lo
+// planes [32][T + 16] + the V column-sum partials, 42.6 KiB at T = 384: three workgroups per
+// compute unit, so that BERT's 576 workgroups are resident at once.
 #include "cm_common.h"
 
 #include <algorithm>
@@ -151,9 +152,27 @@ __global__ __launch_bounds__(256, 3) void attention_kernel(const int16_t* __rest
         }
     };
 
-    // ---- staging: TAB and the first half of V^T
-    for (uint32_t e = t; e < 1024; e += 256)
-        reinterpret_cast<int4*>(stab)[e] = reinterpret_cast<const int4*>(tab)[e];
+    // ---- K's byte limbs through LDS, 64 keys at a time in two buffers (the TAB's 16 KiB until
+    // phase 2): a thread splits 16 d of one key (key 64 c + t / 4, d 16 (t % 4) ..), so the
+    // workgroup reads K from global memory once instead of once per wavefront.  Buffer layout:
+    // [2][hi, lo][64 keys][64 d] bytes.
+    uint8_t* kbuf = lds;
+    const uint32_t kk = t >> 2, kd = 16 * (t & 3);
+    int4 kx0, kx1;
+    auto load_kchunk = [&](uint32_t c) {
+        const int16_t* kp = seq + (uint64_t)(64 * c + kk) * ld + k_off + kHd * h + kd;
+        kx0 = *reinterpret_cast<const int4*>(kp);
+        kx1 = *reinterpret_cast<const int4*>(kp + 8);
+    };
+    auto store_kchunk = [&](uint32_t c) {
+        uint32_t h0, h1, h2, h3, l0, l1, l2, l3;
+        limbs8(kx0, h0, h1, l0, l1);
+        limbs8(kx1, h2, h3, l2, l3);
+        uint8_t* bp = kbuf + (c & 1) * 8192 + kk * 64 + kd;
+        *reinterpret_cast<uint4*>(bp) = make_uint4(h0, h1, h2, h3);
+        *reinterpret_cast<uint4*>(bp + 4096) = make_uint4(l0, l1, l2, l3);
+    };
+    load_kchunk(0);
     stage_v(0);
 
     // ---- the wavefront's Q rows (B of phase 1): query qi, d 16 g .. 16 g + 15
@@ -168,12 +187,26 @@ __global__ __launch_bounds__(256, 3) void attention_kernel(const int16_t* __rest
     const v4i c20 = {1 << 20, 1 << 20, 1 << 20, 1 << 20};
     const v4i qh1 = mfma(ones, qh, zero), ql1 = mfma(ones, ql, zero);
 
-    // ---- phase 1: the scores, key block by key block
+    // ---- phase 1: the scores, key block by key block, 4 blocks a chunk of K in LDS; chunk c
+    // is written before the barrier that precedes its products, chunk c + 1 loaded under them
     int32_t sv[4 * KB];                 // register arrays: every index a constant (loops unrolled)
+    int4 tx[4];                         // the TAB, loaded under the last chunk's products
 #pragma unroll
     for (uint32_t kb = 0; kb < KB; kb++) {
-        v4i kh, kl;
-        limbs16(seq + (uint64_t)(16 * kb + c16) * ld + k_off + kHd * h + 16 * g, kh, kl);
+        if (kb % 4 == 0) {
+            const uint32_t c = kb / 4;
+            store_kchunk(c);
+            __syncthreads();            // chunk c in LDS; every wavefront done with chunk c - 1
+            if (c + 1 < KB / 4) {
+                load_kchunk(c + 1);
+            } else {
+#pragma unroll
+                for (uint32_t q = 0; q < 4; q++) tx[q] = reinterpret_cast<const int4*>(tab)[t + 256 * q];
+            }
+        }
+        const uint8_t* kr = kbuf + ((kb / 4) & 1) * 8192 + (16 * (kb % 4) + c16) * 64 + 16 * g;
+        const v4i kh = *reinterpret_cast<const v4i*>(kr);
+        const v4i kl = *reinterpret_cast<const v4i*>(kr + 4096);
         const v4i hh = mfma(kh, qh, zero);
         v4i mid = mfma(kh, ql, zero);
         mid = mfma(kl, qh, mid);
@@ -186,6 +219,9 @@ __global__ __launch_bounds__(256, 3) void attention_kernel(const int16_t* __rest
             sv[4 * kb + r] = sat16_shr8((int32_t)acc);
         }
     }
+    __syncthreads();                                   // every wavefront done with the K chunks
+#pragma unroll
+    for (uint32_t q = 0; q < 4; q++) reinterpret_cast<int4*>(stab)[t + 256 * q] = tx[q];
     __syncthreads();                                   // TAB, V^T planes and V sums staged
 
     // ---- phase 2: the softmax over the T keys of the lane's query (its lane group g = 0..3)
