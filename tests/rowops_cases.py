@@ -36,6 +36,10 @@ RO_CASES = [  # label, op word, n, rows, blocks, kinds (a, b, c bytes), param ra
     # taking rows in turn
     ("norm_ln_i32_4096_rows", 5 | (1 << 4) | (1 << 16), 4096, 150, 3),
     ("norm_rms_i16_1536_rows", 5, 1536, 400, 2),
+    # two units a lane over at least twelve rows per compute unit (3072 on 256): a workgroup of
+    # twelve wavefronts per compute unit
+    ("norm_ln_i32_768_many_rows", 5 | (1 << 4) | (1 << 16), 768, 1031, 3),
+    ("norm_rms_i16_1000_many_rows", 5, 1000, 3100, 1),
     # the 16-byte unit kernel of DEQUANT / MULACT / GATE / ROPE: shifts on both sides of its 64-bit
     # bounds (sa, sb <= 23, sc <= 61), extreme int16 operands, RoPE tables past 2^23
     ("dequant_i16_u8", 3 | (2 << 8), 512, 4, 2),

@@ -93,7 +93,7 @@ def _params(node):
     return torch.from_numpy(np.ascontiguousarray(node.jobs()[0].params, np.uint8)).cuda()
 
 
-@pytest.mark.parametrize("rows,n", [(300, 768), (64, 1088), (513, 2048)])
+@pytest.mark.parametrize("rows,n", [(300, 768), (64, 1088), (513, 2048), (3100, 768)])
 def test_norm_planes(U, rows, n):
     """A NORM job's planes: the int16 rows as the plain job writes them, their split, and the
     MatMul over them."""
@@ -118,7 +118,7 @@ def test_norm_planes(U, rows, n):
 
 
 @pytest.mark.parametrize("rows,n,a32,planes_on", [(300, 768, True, True), (300, 768, True, False),
-                                                  (77, 1088, False, True)])
+                                                  (77, 1088, False, True), (3100, 768, True, True)])
 def test_addx_norm_one_launch(U, rows, n, a32, planes_on):
     """The residual add and the NORM of its output as one chain call (one launch) write what
     the two jobs write one call at a time, and the NORM's planes."""

@@ -735,6 +735,7 @@ def test_pool_random(U, oracle_lib, case):
 
 @pytest.mark.parametrize("n,rows,ln,bcast,lim,bq_sh", [
     (768, 37, True, False, 1 << 20, 12),       # BERT's residual add + LayerNorm32
+    (768, 3100, True, False, 1 << 20, 12),     # BERT's rows and more: twelve wavefronts per workgroup
     (960, 9, False, False, 1 << 20, 0),        # SmolLM2's residual add + RMSNorm
     (64, 70, True, True, 1 << 30, 40),         # broadcast parameters, values past the 64-bit bounds
     (4096, 3, True, False, 1 << 24, 20),
