@@ -211,7 +211,7 @@ GRAPH_KERNELS = ("gemm_planes_kernel", "split_rows_kernel", "split_cols_kernel",
                  "softmax_long_kernel", "smx_etab_kernel", "copy_elems_kernel", "permute_elems_kernel",
                  "split_fold_kernel", "split_fold_lds_kernel", "skinny_wrap_kernel", "skinny_reduce_kernel",
                  "skinny_planes_kernel", "skinny_mulact_kernel", "decode_attn_kernel", "decode_prep_kernel",
-                 "gemm_reduce_kernel", "attention_kernel", "embed_rows_kernel", "ro_fold_kernel",
+                 "attention_kernel", "embed_rows_kernel", "ro_fold_kernel",
                  "ro_tload_kernel", "ro_xpose_kernel")
 
 

@@ -57,6 +57,8 @@ struct DeviceState {
     std::vector<void*> ws_retired;   // buffers the workspace outgrew (kept: captured graphs may hold them)
     void* scratch = nullptr;         // this device's copy of the no-allocation scratch (cm_gemm.hip)
     size_t scratch_bytes = 0;
+    uint32_t* split_cnt = nullptr;   // this device's per-tile arrival counts of split-k products (cm_gemm.hip)
+    uint32_t split_cnt_n = 0;
     int cus = 0;                     // compute units
     size_t lds_per_cu = 0;           // LDS bytes per compute unit
     size_t lds_per_block = 0;        // LDS bytes one workgroup may hold (dynamic attribute raised to it)
@@ -82,8 +84,8 @@ struct WsRegion {
 };
 int take_workspace(DeviceState* st, const WsRegion* fixed, size_t bytes, void** out, hipStream_t s);
 
-// Looks up this device's address of the no-allocation scratch (cm_gemm.hip); called once
-// per device by the set-up, with that device current.
+// Looks up this device's addresses of the no-allocation scratch and of the split-k arrival
+// counts (cm_gemm.hip); called once per device by the set-up, with that device current.
 int gemm_scratch_setup(DeviceState* st);
 
 // Records a HIP event pair around the launches in its scope while timing is enabled

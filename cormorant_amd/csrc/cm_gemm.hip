@@ -514,9 +514,10 @@ struct EpiConv {                // y pattern (ConvKernel.h:250-258); acc seeded 
 //     int32 and cannot change a saturated result (|2^8 HH| > 2^30 then decides the sign);
 //   kWrap: the sum wrapped to int32 first, i.e. floor(acc / 2^8) mod 2^24, sign-extended;
 //   kSatWide (K > 8192, saturating): the sum in int64.
-//   kPartial (wrap products split over k): the slice's 2^16 HH + 2^8 MID + LL mod 2^32 as an
-//     int32 partial; gemm_reduce_kernel adds the slices, the sum terms and the output rule.
-enum : uint32_t { kSatNarrow = 0, kWrap = 1, kSatWide = 2, kPartial = 3 };
+//   kSplitFix (wrap products split over k): every slice stores its 2^16 HH + 2^8 MID + LL
+//     mod 2^32 as int32 partials, and the slice of a tile that arrives last adds the others'
+//     to its own and stores the tile by the kWrap rule (split_fixup).
+enum : uint32_t { kSatNarrow = 0, kWrap = 1, kSatWide = 2, kSplitFix = 3 };
 
 __device__ __forceinline__ int32_t clamp_i32(int32_t v, int32_t lo, int32_t hi) {   // v_med3_i32
     return min(max(v, lo), hi);
@@ -619,76 +620,73 @@ __device__ __forceinline__ void store_wave_fast(const v16i (&hh)[2][2], const v1
     }
 }
 
-// One wave's 64 x 64 int32 partials (layout as store_wave_tile) into [rows][cols] at `out`.
-__device__ __forceinline__ void store_wave_partial(const v16i (&hh)[2][2], const v16i (&mid)[2][2],
-                                                   const v16i (&ll)[2][2], int32_t* __restrict__ out, uint32_t rows,
-                                                   uint32_t cols, uint32_t row0, uint32_t col0, uint32_t wr,
-                                                   uint32_t wc, uint32_t l32, uint32_t lh) {
+// kSplitFix: this slice's partial of its wave's 64 x 64 outputs, in the accumulators' own
+// layout (a tile's nz slices are consecutive blocks of TM x 128 int32 at `tile_part`; in a
+// block, wave w's accumulator (i, j) rows 4q .. 4q + 3 sit at 1 KiB row (4 (2i + j) + q) of
+// the wave's 16 KiB, 16 bytes a lane), written and read with agent-scope 16-byte buffer
+// accesses (sc1) so that a workgroup on another XCD reads them; then the tile's arrival count.
+// The slice that arrives last (ticket nz - 1) resets the count for the next launch, adds the
+// other slices' partials (all were stored, and their stores had completed, before their slices
+// took their tickets) and returns true with the wrapped total T in limb form -- HH = T >> 16,
+// MID = (T >> 8) & 255, LL = T & 255, 2^16 HH + 2^8 MID + LL = T exactly -- for the kWrap
+// store; the other slices return false.  No workgroup waits for another.  Every wave of the
+// workgroup calls it (two barriers).
+template <int TM>
+__device__ __forceinline__ bool split_fixup(v16i (&hh)[2][2], v16i (&mid)[2][2], v16i (&ll)[2][2],
+                                            int32_t* tile_part, uint32_t nz, uint32_t kz, uint32_t wave,
+                                            uint32_t lane, uint32_t* cnt, uint32_t* ticket) {
+    constexpr uint32_t kBlock = TM * 128 * 4;                  // bytes of one slice's tile
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(tile_part, 0, (int)(nz * kBlock), 0x00020000);
+    const uint32_t wbase = wave * 16384 + lane * 16;
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const uint32_t col = col0 + wc * 64 + j * 32 + l32;
-        if (col >= cols) continue;
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                ll[i][j][r] = (int32_t)(((uint32_t)hh[i][j][r] << 16) + ((uint32_t)mid[i][j][r] << 8) +
+                                        (uint32_t)ll[i][j][r]);
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const v4i v = {ll[i][j][4 * q], ll[i][j][4 * q + 1], ll[i][j][4 * q + 2], ll[i][j][4 * q + 3]};
+                __builtin_amdgcn_raw_buffer_store_b128(v, rs, kz * kBlock + wbase + (4 * (2 * i + j) + q) * 1024, 0, 16);
+            }
+    __builtin_amdgcn_s_waitcnt(0x0070);      // this wave's partial stores complete
+    __syncthreads();
+    if (threadIdx.x == 0) *ticket = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (*ticket != nz - 1) return false;
+    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (uint32_t z = 0; z < nz; z++) {
+        if (z == kz) continue;
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const v4i v = __builtin_amdgcn_raw_buffer_load_b128(rs, z * kBlock + wbase + (4 * (2 * i + j) + q) * 1024, 0, 16);
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        ll[i][j][4 * q + e] = (int32_t)((uint32_t)ll[i][j][4 * q + e] + (uint32_t)v[e]);
+                }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
             for (int r = 0; r < 16; r++) {
-                const uint32_t row = row0 + wr * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (row < rows)
-                    out[(uint64_t)row * cols + col] =
-                        (int32_t)(((uint32_t)hh[i][j][r] << 16) + ((uint32_t)mid[i][j][r] << 8) + (uint32_t)ll[i][j][r]);
+                const int32_t tot = ll[i][j][r];
+                hh[i][j][r] = tot >> 16;
+                mid[i][j][r] = (tot >> 8) & 255;
+                ll[i][j][r] = tot & 255;
             }
-    }
-}
-
-// The wrap products split over k: sum of the slices' partials (mod 2^32) + 128 rowsum + 128
-// colsum - 16384 K, then sat16(>> 8) -- the kWrap rule of the unsplit kernel.  A lane per 8
-// outputs of a row (m % 8 == 0, 16-byte aligned C rows) or per output.
-__global__ __launch_bounds__(256) void gemm_reduce_kernel(const int32_t* __restrict__ part, const int32_t* __restrict__ rpart,
-                                                          uint64_t rp_slice, uint32_t a_lines, uint32_t nsum_a,
-                                                          const int32_t* __restrict__ cpart, uint64_t cp_slice,
-                                                          uint32_t b_lines, uint32_t nslab, int16_t* __restrict__ c,
-                                                          uint64_t c_bs, uint32_t n, uint32_t m, uint32_t nz,
-                                                          uint32_t batch, uint32_t k, uint32_t vec) {
-    const uint64_t per = (uint64_t)n * m;
-    const uint32_t w = vec ? 8u : 1u;
-    const uint64_t total = per / w * batch;
-    for (uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (uint64_t)gridDim.x * blockDim.x) {
-        const uint64_t bt = e / (per / w), i = (e - bt * (per / w)) * w;
-        const uint32_t row = (uint32_t)(i / m), col = (uint32_t)(i - (uint64_t)row * m);
-        int32_t rs = 0;
-        for (uint32_t q = 0; q < nsum_a; q++) rs += rpart[bt * rp_slice + (uint64_t)q * a_lines + row];
-        const uint32_t base = 128u * (uint32_t)rs - 16384u * k;
-        if (vec) {
-            uint32_t acc[8];
-#pragma unroll
-            for (int t = 0; t < 8; t++) acc[t] = base;
-            for (uint32_t z = 0; z < nz; z++) {
-                const int4* pz = reinterpret_cast<const int4*>(part + (bt * nz + z) * per + i);
-                const int4 u = pz[0], v = pz[1];
-                acc[0] += u.x; acc[1] += u.y; acc[2] += u.z; acc[3] += u.w;
-                acc[4] += v.x; acc[5] += v.y; acc[6] += v.z; acc[7] += v.w;
-            }
-            for (uint32_t q = 0; q < nslab; q++) {
-                const int4* cz = reinterpret_cast<const int4*>(cpart + bt * cp_slice + (uint64_t)q * b_lines + col);
-                const int4 u = cz[0], v = cz[1];
-                acc[0] += 128u * u.x; acc[1] += 128u * u.y; acc[2] += 128u * u.z; acc[3] += 128u * u.w;
-                acc[4] += 128u * v.x; acc[5] += 128u * v.y; acc[6] += 128u * v.z; acc[7] += 128u * v.w;
-            }
-            uint32_t o[4];
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const int q0 = min(max((int32_t)acc[2 * t] >> 8, -32768), 32767);
-                const int q1 = min(max((int32_t)acc[2 * t + 1] >> 8, -32768), 32767);
-                o[t] = (uint32_t)(uint16_t)q0 | ((uint32_t)q1 << 16);
-            }
-            *reinterpret_cast<uint4*>(c + bt * c_bs + (uint64_t)row * m + col) = make_uint4(o[0], o[1], o[2], o[3]);
-        } else {
-            uint32_t acc = base;
-            for (uint32_t z = 0; z < nz; z++) acc += (uint32_t)part[(bt * nz + z) * per + i];
-            for (uint32_t q = 0; q < nslab; q++) acc += 128u * (uint32_t)cpart[bt * cp_slice + (uint64_t)q * b_lines + col];
-            c[bt * c_bs + (uint64_t)row * m + col] = (int16_t)min(max((int32_t)acc >> 8, -32768), 32767);
-        }
-    }
+    return true;
 }
 
 // ---------------------------------------------------------------- the plane GEMM
@@ -723,7 +721,7 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
     uint64_t a_slice, uint64_t rp_slice, uint32_t a_lines, const int8_t* __restrict__ Bhi,
     const int8_t* __restrict__ Blo, const int32_t* __restrict__ cpart, uint64_t b_slice, uint64_t cp_slice,
     uint32_t b_lines, uint32_t nslab, uint32_t nsum_a, uint32_t tiles_r, uint32_t tiles_c, uint32_t kp, int32_t k64,
-    uint32_t mode, int32_t* __restrict__ pout, uint32_t ksteps, Epi epi) {
+    uint32_t mode, int32_t* __restrict__ pout, uint32_t ksteps, uint32_t* __restrict__ tcnt, Epi epi) {
     constexpr int TM = 64 * WR;                  // tile rows
     constexpr int NT = 128 * WR;                 // threads
     constexpr int NW = 2 * WR;                   // waves
@@ -739,6 +737,7 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
     __shared__ __attribute__((aligned(1024))) int8_t sm1[STAGE];
     __shared__ __attribute__((aligned(1024))) int8_t sm2[NST == 3 ? STAGE : 16];
     __shared__ int2 rterm[TM], cterm[BN];        // (h, l) halves
+    __shared__ uint32_t ticket;                  // kSplitFix: the tile's arrival ticket
 
     // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so
     // give each XCD a contiguous range of tiles (column-major: tiles sharing a B column
@@ -762,14 +761,14 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
     for (int q = 0; q < TE; q++) {
         const uint32_t e = t + q * NT;
         tsum[q] = 0;
-        if (mode != kPartial && e < TM + BN)
+        if (e < TM + BN)
             tsum[q] = e < TM ? rpart[bt * rp_slice + tr * TM + e] : cpart[bt * cp_slice + tc * BN + (e - TM)];
     }
     auto finish_terms = [&]() {
 #pragma unroll
         for (int q = 0; q < TE; q++) {
             const uint32_t e = t + q * NT;
-            if (mode == kPartial || e >= TM + BN) continue;
+            if (e >= TM + BN) continue;
             const bool is_row = e < TM;
             const uint32_t line = is_row ? tr * TM + e : tc * BN + (e - TM);
             const int32_t* pp = is_row ? rpart + bt * rp_slice + line : cpart + bt * cp_slice + line;
@@ -918,15 +917,20 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
 
     // ---- epilogue: one uniform dispatch to the store routine of this mode
     const uint32_t row0 = tr * TM, col0 = tc * BN;
+    if (mode == kSplitFix) {
+        // the slices' partials meet in the last slice to arrive; the others are done
+        const uint64_t tile_id = (uint64_t)bt * ntiles + g;
+        if (!split_fixup<TM>(hh, mid, ll, pout + tile_id * gridDim.z * (TM * BN), gridDim.z, kz, wave, lane,
+                             tcnt + tile_id, &ticket))
+            return;
+        mode = kWrap;
+    }
 #define CM_STORE(M, P) store_wave_tile<M, P>(hh, mid, ll, rterm, cterm, bt, row0, col0, wr, wc, l32, lh, epi)
-    const TileBase tb = mode != kPartial ? epi.tile_base(bt, row0, col0, TM, BN) : TileBase{nullptr, 0};
+    const TileBase tb = epi.tile_base(bt, row0, col0, TM, BN);
     if (tb.base != nullptr) {           // a whole tile: the lean store
         if (mode == kWrap) store_wave_fast<kWrap>(hh, mid, ll, rterm, cterm, tb.base, tb.ld, wr, wc, l32, lh);
         else if (mode == kSatNarrow) store_wave_fast<kSatNarrow>(hh, mid, ll, rterm, cterm, tb.base, tb.ld, wr, wc, l32, lh);
         else store_wave_fast<kSatWide>(hh, mid, ll, rterm, cterm, tb.base, tb.ld, wr, wc, l32, lh);
-    } else if (mode == kPartial) {
-        store_wave_partial(hh, mid, ll, pout + ((uint64_t)bt * gridDim.z + kz) * epi.rows * epi.cols, epi.rows,
-                           epi.cols, row0, col0, wr, wc, l32, lh);
     } else if (mode == kSatNarrow) {
         if (epi.pairs) CM_STORE(kSatNarrow, true); else CM_STORE(kSatNarrow, false);
     } else if (mode == kWrap) {
@@ -1649,7 +1653,7 @@ uint32_t gemm_tile_rows(uint32_t n, uint32_t m, uint32_t batch, uint32_t cus) {
 
 template <class Epi>
 int run_gemm(const Planes& A, const Planes& B, uint32_t batch, uint32_t k, Epi epi, hipStream_t s,
-             int32_t* pout = nullptr, uint32_t ksteps = 0) {
+             int32_t* pout = nullptr, uint32_t ksteps = 0, uint32_t* tcnt = nullptr) {
     const uint32_t tm = A.tile;
     const uint32_t tiles_r = ceil_div(A.rows, tm), tiles_c = B.lines_p / BN;
     if (tm != 64 && tm != 128 && tm != 256) return fail(CM_EINVAL, "gemm: tile rows %u", tm);
@@ -1658,21 +1662,22 @@ int run_gemm(const Planes& A, const Planes& B, uint32_t batch, uint32_t k, Epi e
     const uint64_t b_slice = B.slices > 1 ? (uint64_t)B.lines_p * B.kp : 0;
     const uint64_t rp_slice = A.slices > 1 ? (uint64_t)A.nslab * A.lines_p : 0;
     const uint64_t cp_slice = B.slices > 1 ? (uint64_t)B.nslab * B.lines_p : 0;
-    const uint32_t mode = ksteps ? kPartial : (epi.wrap ? kWrap : (k <= 8192 ? kSatNarrow : kSatWide));
+    if (ksteps && tcnt == nullptr) return fail(CM_EINVAL, "gemm: a split over k needs the arrival counts");
+    const uint32_t mode = ksteps ? kSplitFix : (epi.wrap ? kWrap : (k <= 8192 ? kSatNarrow : kSatWide));
     const uint32_t nz = ksteps ? ceil_div(A.kp / BK, ksteps) : 1;
     const dim3 grid(tiles_r * tiles_c, batch, nz);
     if (tm == 256) {
         CM_LAUNCH("gemm_planes_kernel", (gemm_planes_kernel<4, 3, Epi>), grid, dim3(512), 0, s, A.hi, A.lo, A.part,
                   a_slice, rp_slice, A.lines_p, B.hi, B.lo, B.part, b_slice, cp_slice, B.lines_p, B.nslab, A.nsum(),
-                  tiles_r, tiles_c, A.kp, (int32_t)(64 * k), mode, pout, ksteps, epi);
+                  tiles_r, tiles_c, A.kp, (int32_t)(64 * k), mode, pout, ksteps, tcnt, epi);
     } else if (tm == 64) {
         CM_LAUNCH("gemm_planes_kernel", (gemm_planes_kernel<1, 2, Epi>), grid, dim3(128), 0, s, A.hi, A.lo, A.part,
                   a_slice, rp_slice, A.lines_p, B.hi, B.lo, B.part, b_slice, cp_slice, B.lines_p, B.nslab, A.nsum(),
-                  tiles_r, tiles_c, A.kp, (int32_t)(64 * k), mode, pout, ksteps, epi);
+                  tiles_r, tiles_c, A.kp, (int32_t)(64 * k), mode, pout, ksteps, tcnt, epi);
     } else {
         CM_LAUNCH("gemm_planes_kernel", (gemm_planes_kernel<2, 2, Epi>), grid, dim3(256), 0, s, A.hi, A.lo, A.part,
                   a_slice, rp_slice, A.lines_p, B.hi, B.lo, B.part, b_slice, cp_slice, B.lines_p, B.nslab, A.nsum(),
-                  tiles_r, tiles_c, A.kp, (int32_t)(64 * k), mode, pout, ksteps, epi);
+                  tiles_r, tiles_c, A.kp, (int32_t)(64 * k), mode, pout, ksteps, tcnt, epi);
     }
     return CM_OK;
 }
@@ -1818,28 +1823,23 @@ uint32_t matmul_ksteps(const Planes& A, const Planes& B, uint32_t n, uint32_t m,
                        const DeviceState* st, size_t* bytes) {
     const uint32_t tiles = ceil_div(n, A.tile) * (B.lines_p / BN) * batch;
     const uint32_t ks = wrap32 ? gemm_ksteps(A.tile, tiles, A.kp, st) : 0;
-    *bytes = ks ? (size_t)batch * ceil_div(A.kp / BK, ks) * n * m * 4 : 0;
+    // the partials of every slice, whole tiles (split_fixup's layout)
+    *bytes = ks ? (size_t)ceil_div(A.kp / BK, ks) * tiles * A.tile * BN * 4 : 0;
     return ks;
 }
 
 int gemm_out(const Planes& A, const Planes& B, int16_t* c, uint32_t n, uint32_t k, uint32_t m, uint32_t batch,
-             int64_t c_bs, uint32_t wrap32, hipStream_t s, int32_t* pout = nullptr, uint32_t ksteps = 0) {
+             int64_t c_bs, uint32_t wrap32, hipStream_t s, const DeviceState* st, int32_t* pout = nullptr,
+             uint32_t ksteps = 0) {
     const bool pairs = (reinterpret_cast<uintptr_t>(c) & 3) == 0 && (m & 1) == 0 && (c_bs & 1) == 0;
     EpiMatmul epi{c, (uint64_t)c_bs, n, m, wrap32 ? 1u : 0u, pairs ? 1u : 0u};
-    int rc = run_gemm(A, B, batch, k, epi, s, pout, ksteps);
-    if (rc || !ksteps) return rc;
-    const uint32_t nz = ceil_div(A.kp / BK, ksteps);
-    const uint64_t rp_slice = A.slices > 1 ? (uint64_t)A.nslab * A.lines_p : 0;
-    const uint64_t cp_slice = B.slices > 1 ? (uint64_t)B.nslab * B.lines_p : 0;
-    // 8 outputs a lane where C's rows and the column sums are whole 16-byte words
-    const bool vec = (m & 7) == 0 && aligned16(c) && (c_bs & 7) == 0 && (B.lines_p & 3) == 0 &&
-                     (cp_slice & 3) == 0 && (reinterpret_cast<uintptr_t>(B.part) & 15) == 0;
-    const uint64_t total = (uint64_t)batch * n * m / (vec ? 8 : 1);
-    const unsigned blocks = (unsigned)std::min<uint64_t>((total + 255) / 256, 65536ull * 8);
-    CM_LAUNCH("gemm_reduce_kernel", gemm_reduce_kernel, dim3(blocks), dim3(256), 0, s, pout, A.part, rp_slice,
-              A.lines_p, A.nsum(), B.part, cp_slice, B.lines_p, B.nslab, c, (uint64_t)c_bs, n, m, nz, batch, k,
-              vec ? 1u : 0u);
-    return CM_OK;
+    // a split product is finished by the last slice of each tile (one launch): an arrival
+    // count per tile (a split has at most one tile per compute unit, gemm_ksteps)
+    const uint64_t tiles = (uint64_t)ceil_div(A.rows, A.tile) * (B.lines_p / BN) * batch;
+    if (ksteps && tiles > st->split_cnt_n)
+        return fail(CM_EINVAL, "gemm: %llu split tiles past the %u arrival counts", (unsigned long long)tiles,
+                    st->split_cnt_n);
+    return run_gemm(A, B, batch, k, epi, s, pout, ksteps, ksteps ? st->split_cnt : nullptr);
 }
 
 }  // namespace
@@ -1876,7 +1876,7 @@ int matmul_run(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint3
     if (rc) return rc;
     rc = split_b(b, b_slice, k, m, b_packed, gemv_kw, B, s);
     if (rc) return rc;
-    return gemm_out(A, B, c, n, k, m, batch, c_bs, wrap32, s, reinterpret_cast<int32_t*>(p), ksteps);
+    return gemm_out(A, B, c, n, k, m, batch, c_bs, wrap32, s, st, reinterpret_cast<int32_t*>(p), ksteps);
 }
 
 // The no-allocation scratch: every call of cm_matmul_noalloc on a device takes its planes, line
@@ -1885,6 +1885,13 @@ int matmul_run(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint3
 // device address per device comes from hipGetSymbolAddress at set-up (DeviceState::scratch).
 constexpr size_t kScratchBytes = CM_NOALLOC_MAX_BYTES;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+// The arrival counts of the split-k products finished in place (kSplitFix), one per output
+// tile and batch slice of a launch: zero from load, and every launch leaves them zero (the
+// last slice of a tile resets its count), so they need no clearing between launches or graph
+// replays.  Launches that overlap on one device (other streams) must not both split.
+constexpr uint32_t kSplitCounts = 16384;
+static __device__ __align__(256) uint32_t split_counts[kSplitCounts];
 
 }  // namespace
 
@@ -1895,6 +1902,11 @@ int gemm_scratch_setup(DeviceState* st) {
         return fail(CM_EHIP, "no-allocation scratch: unusable device address %p", ptr);
     st->scratch = ptr;
     st->scratch_bytes = kScratchBytes;
+    void* cp = nullptr;
+    CM_HIP_CHECK(hipGetSymbolAddress(&cp, HIP_SYMBOL(split_counts)));
+    if (cp == nullptr) return fail(CM_EHIP, "split-k arrival counts: no device address");
+    st->split_cnt = static_cast<uint32_t*>(cp);
+    st->split_cnt_n = kSplitCounts;
     return CM_OK;
 }
 
@@ -1973,7 +1985,7 @@ extern "C" int cm_matmul_planes(const int16_t* a, const void* b_planes, int16_t*
     B.carve(q);
     rc = split_a(a, sa > 1 ? (uint64_t)a_bs : 0, n, k, A, s);
     if (rc) return rc;
-    return gemm_out(A, B, c, n, k, m, batch, c_bs, wrap32, s, reinterpret_cast<int32_t*>(p), ksteps);
+    return gemm_out(A, B, c, n, k, m, batch, c_bs, wrap32, s, st, reinterpret_cast<int32_t*>(p), ksteps);
 }
 
 extern "C" size_t cm_matmul_a_planes_bytes(uint32_t n, uint32_t k, uint32_t nsum) {
@@ -2009,7 +2021,7 @@ extern "C" int cm_matmul_aplanes(const void* a_planes, uint32_t nsum, const void
         rc = workspace(st, pbytes, &ws, s);
         if (rc) return rc;
     }
-    return gemm_out(A, B, c, n, k, m, 1, 0, wrap32, s, static_cast<int32_t*>(ws), ksteps);
+    return gemm_out(A, B, c, n, k, m, 1, 0, wrap32, s, st, static_cast<int32_t*>(ws), ksteps);
 }
 
 namespace cm {

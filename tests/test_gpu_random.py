@@ -85,7 +85,8 @@ MM_CASES = [  # n, k, m, batch, a_bs_mode, b_bs_mode, layout, kw, full_range, wr
     (48, 120, 136, 3, 1, 1, "trans", 0, False, False),
     (33, 256, 64, 2, 1, 0, "row", 0, True, True),
     (130, 192, 72, 1, 1, 1, "trans", 0, True, False),
-    # wrap products of few output tiles split over k (int32 partials + the reduce kernel)
+    # wrap products of few output tiles split over k (int32 partials, the last slice of a tile
+    # to arrive adds the others and stores the tile)
     (512, 1024, 256, 1, 1, 1, "row", 0, True, True),
     (300, 2048, 200, 2, 1, 1, "row", 0, True, True),
     (200, 1280, 96, 1, 1, 1, "packed", 0, True, True),
@@ -152,6 +153,24 @@ def test_matmul_random(U, oracle_lib, case):
     got = host(c)
     np.testing.assert_array_equal(got[:batch * n * m], want)
     assert (got[batch * n * m:] == POISON16).all()
+
+
+def test_matmul_split_calls_in_turn(U, oracle_lib):
+    """Products split over k, finished by the last slice of each tile to arrive (its arrival
+    count reset for the next call): shapes of different tile and slice counts called in turn,
+    each call with new operands, every output against the oracle."""
+    rng = np.random.default_rng(11)
+    shapes = [(300, 2048, 200, 2), (64, 4096, 64, 1), (512, 1024, 256, 1), (300, 2048, 200, 2), (96, 1536, 40, 3)]
+    for rep in range(2):
+        for n, k, m, batch in shapes:
+            a = rint16(rng, batch * n * k, -32768, 32768)
+            b = rint16(rng, batch * k * m, -32768, 32768)
+            want = oracle_lib.matmul(a, b, n, k, m, batch, n * k, k * m, n * m, 0, 0, True)
+            c = poisoned16(batch * n * m + 8)
+            U.matmul(dev16(a), dev16(b), c, n, k, m, batch, n * k, k * m, n * m, 0, 0, True)
+            got = host(c)
+            np.testing.assert_array_equal(got[:batch * n * m], want, err_msg=f"rep {rep} shape {(n, k, m, batch)}")
+            assert (got[batch * n * m:] == POISON16).all()
 
 
 @pytest.mark.parametrize("case", [c for c in MM_CASES if c[0] * c[1] * c[2] <= 2 ** 22], ids=lambda c: "n%d_k%d_m%d_b%d_%s%d_%s" % (
