@@ -293,7 +293,8 @@ __global__ __launch_bounds__(64 * NW) void ro_norm_fast_kernel(Job j, const uint
     const u64 stride = (u64)gridDim.x * (blockDim.x >> 6);
     const uint32_t nsl = bcast ? 1u : j.n;
     uint4* a_lds = ro_lds + nsl;                          // the ADDX job's parameters
-    int x[UPL][8], y[UPL][8];
+    int x[UPL][8];
+    int4 yw[UPL];                                         // the ADDX job's int16 B, unpacked at use
     auto load_row = [&](u64 row) {
         const Job& jl = ADDX ? ja : j;
         const uint32_t i1 = (uint32_t)(row % jl.c1), i2 = (uint32_t)(row / jl.c1);
@@ -303,10 +304,12 @@ __global__ __launch_bounds__(64 * NW) void ro_norm_fast_kernel(Job j, const uint
             const uint32_t u = lane + 64 * k;
             if (u < units) {
                 ld_unit<AK>(ra, u, x[k]);
-                if constexpr (ADDX) ld_unit<0>(ja.b + (u64)i2 * ja.b_s2 + (u64)i1 * ja.b_s1, u, y[k]);
+                if constexpr (ADDX)
+                    yw[k] = *reinterpret_cast<const int4*>(ja.b + (u64)i2 * ja.b_s2 + (u64)i1 * ja.b_s1 + 16u * u);
             } else {
 #pragma unroll
-                for (int l = 0; l < 8; l++) x[k][l] = y[k][l] = 0;
+                for (int l = 0; l < 8; l++) x[k][l] = 0;
+                yw[k] = make_int4(0, 0, 0, 0);
             }
         }
     };
@@ -328,8 +331,11 @@ __global__ __launch_bounds__(64 * NW) void ro_norm_fast_kernel(Job j, const uint
             for (int k = 0; k < UPL; k++) {
                 const uint32_t u = lane + 64 * k;
                 if (u >= units) continue;
-                int r[8];
-                addx_unit<0, 1, true>(x[k], y[k], u, units, ja, a_lds, pa, bca, scale, relu, r);
+                int r[8], y[8];
+                const int16_t* yh = reinterpret_cast<const int16_t*>(&yw[k]);
+#pragma unroll
+                for (int l = 0; l < 8; l++) y[l] = yh[l];
+                addx_unit<0, 1, true>(x[k], y, u, units, ja, a_lds, pa, bca, scale, relu, r);
                 store_stream(rc1 + 32u * u, make_int4(r[0], r[1], r[2], r[3]));
                 store_stream(rc1 + 32u * u + 16, make_int4(r[4], r[5], r[6], r[7]));
 #pragma unroll
