@@ -103,7 +103,7 @@ __global__ __launch_bounds__(256) void vectorop_kernel(const int16_t* __restrict
 
 // vectorop_kernel over `outer` runs of `size` elements (size a multiple of 64) whose outputs
 // are the rows of a matmul's A (row o at c + o size), also writing the output's byte planes and
-// its row sums per 1024 columns (APlanes): a wavefront per (row, 1024-column slab), two
+// its row sums per 1024 columns (APlanes; c null: the planes alone): a wavefront per (row, 1024-column slab), two
 // 8-element units per lane, the slab's sum by a wavefront reduction.  Few workgroups per
 // compute unit (grid-stride) when an activation table is staged.
 template <uint32_t OP>
@@ -142,7 +142,7 @@ __global__ __launch_bounds__(256) void vectorop_planes_kernel(const int16_t* __r
             int16_t* cl = reinterpret_cast<int16_t*>(&cv);
 #pragma unroll
             for (int l = 0; l < 8; l++) cl[l] = (int16_t)act_lane(act, op_lane<OP>(al[l], bl[l]), alpha16, tab, act_len);
-            store_stream(c + o * (a_inc + b_inc) + base, cv);
+            if (c != nullptr) store_stream(c + o * (a_inc + b_inc) + base, cv);
             uint2 h, lw;
             split8(cv, h, lw);
             *reinterpret_cast<uint2*>(po.hi + o * po.k + base) = h;
@@ -1118,6 +1118,9 @@ extern "C" int cm_vectorop_planes(const int16_t* a, const int16_t* b, int16_t* c
     if (size % 64 || size > 32768 || a_inc + b_inc != size)
         return fail(CM_EINVAL, "vectorop planes: runs of %u (a multiple of 64 up to 32768) onto contiguous rows "
                                "(a_inc + b_inc = %u)", size, a_inc + b_inc);
+    if (planes == nullptr) return fail(CM_EINVAL, "vectorop planes: no planes buffer");
+    if (outer != 0 && (a == nullptr || (op < OP_RELU && b == nullptr)))
+        return fail(CM_EINVAL, "vectorop planes: a null operand");
     if (!aligned16(a) || !aligned16(c) || (op < OP_RELU && !aligned16(b)) || (reinterpret_cast<uintptr_t>(planes) & 255))
         return fail(CM_EALIGN, "vectorop planes: a, b, c 16-byte and planes 256-byte aligned");
     if (outer == 0) return CM_OK;
@@ -1146,6 +1149,8 @@ extern "C" int cm_vectorop(const int16_t* a, const int16_t* b, int16_t* c, uint3
     if (size == 0 || outer == 0) return CM_OK;
     if (!aligned16(a) || !aligned16(c) || (op < OP_RELU && !aligned16(b)))
         return fail(CM_EALIGN, "vectorop: a, b and c must be 16-byte aligned");
+    if (outer != 0 && size != 0 && (a == nullptr || c == nullptr || (op < OP_RELU && b == nullptr)))
+        return fail(CM_EINVAL, "vectorop: a null operand or output");
     if (op == OP_SOFTMAX || op == OP_SOFTMAX_T)
         return launch_softmax(a, c, size, op, outer, a_inc, b_inc, smx_cm, smx_cfg, smx_mask, 1, 0, 0, st, s);
     if ((a_inc & 7) || (b_inc & 7))

@@ -83,6 +83,8 @@ class Simulator:
         self._params: Dict[int, list] = {}                # row-ops parameter blocks on the device
         self._staging: Dict[tuple, torch.Tensor] = {}     # row-ops nodes' staging buffers
         self._plan = None                                  # MatMuls fed byte planes by their A's producer
+        self._keep = None                                  # forward_raw's keep (None: every tensor)
+        self._planes_only_names = None                     # tensors only plane-path MatMuls read
         for t in graph.input_tensors + graph.output_tensors:
             self._infos[t.onnx_name] = t
         # the fused launches that apply a row-ops job inside another unit leave the device's
@@ -130,7 +132,7 @@ class Simulator:
             raise KeyError(f"states {missing} have no value")
         feeds = {nm: self._to_device(self._tensor(nm), states[nm]) for nm in st_names if nm not in input_arrays}
         feeds.update({name: self._to_device(self._tensor(name), v) for name, v in input_arrays.items()})
-        raw = self.forward_raw(feeds)
+        raw = self.forward_raw(feeds, keep=None if keep is None else set(keep) | set(st_names))
         for nm in st_names:                      # the states as the pass left them, in place
             if nm in states:
                 states[nm][...] = self._to_values(self._tensor(nm), feeds[nm]).reshape(np.shape(states[nm]))
@@ -138,8 +140,13 @@ class Simulator:
         wanted = {nm for nm in raw if "#" not in nm} if keep is None else set(keep) | set(st_names)
         return {name: self._to_values(self._tensor(name), t) for name, t in raw.items() if name in wanted}
 
-    def forward_raw(self, raw_inputs: Dict[str, torch.Tensor]) -> Dict[str, torch.Tensor]:
-        """The device-resident path: raw input tensors in, raw tensors of every node out."""
+    def forward_raw(self, raw_inputs: Dict[str, torch.Tensor],
+                    keep: Optional[Iterable[str]] = None) -> Dict[str, torch.Tensor]:
+        """The device-resident path: raw input tensors in, raw tensors of every node out.  With
+        ``keep`` (the names the caller reads; the graph's outputs and states are always kept) a
+        tensor that only plane-path MatMuls read, as the byte planes its producer writes, is not
+        written at all and is absent from the result."""
+        self._keep = None if keep is None else set(keep)
         raw: Dict[str, torch.Tensor] = dict(raw_inputs)
         nodes = self._graph.nodes
         i = 0
@@ -483,6 +490,25 @@ class Simulator:
             return None
         return self._plan_planes()[1].get(out.onnx_name)
 
+    def _planes_only(self, name: str) -> bool:
+        """True if forward_raw may leave ``name`` unwritten: the caller does not keep it, it is
+        no graph output or state, and every node reading it is a MatMul on the plane path."""
+        if self._keep is None or name in self._keep:
+            return False
+        if self._planes_only_names is None:
+            plan = self._plan_planes()[0]
+            readers: Dict[str, list] = {}
+            for sn in self._graph.nodes:
+                for t in getattr(sn, "inputs", []) or []:
+                    if t is not None:
+                        readers.setdefault(t.onnx_name, []).append(sn)
+            fixed = {t.onnx_name for t in self._graph.output_tensors} | {t.onnx_name for t in self._graph.state_tensors}
+            self._planes_only_names = {
+                nm for nm, rs in readers.items()
+                if nm not in fixed and all(id(r) in plan and plan[id(r)][0] == nm and r.inputs[0].onnx_name == nm
+                                          and all(t is None or t.onnx_name != nm for t in r.inputs[1:]) for r in rs)}
+        return name in self._planes_only_names
+
     def _planes_node(self, sn, raw) -> bool:
         """Run ``sn`` with the byte planes of its output as well (raw[name + '#planes']); False
         if it runs the plain way after all."""
@@ -504,14 +530,16 @@ class Simulator:
             raw[name] = self._attention_out
         else:
             a = self._get(sn.inputs[0], raw).reshape(-1).contiguous()
-            c = self._new(sn.output, n * k)
+            # the int16 output only where something besides the plane-path MatMuls reads it
+            c = None if self._planes_only(name) else self._new(sn.output, n * k)
             if sn.arity == 1:
                 units.vectorop_planes(a, None, c, k, sn.op_code, n, k, 0, planes, act=sn.act, alpha=sn.alpha)
             else:
                 b = self._get(sn.inputs[1], raw).reshape(-1).contiguous()
                 a_inc, b_inc = (k, 0) if a.numel() == n * k else (0, k)
                 units.vectorop_planes(a, b, c, k, sn.op_code, n, a_inc, b_inc, planes, act=sn.act, alpha=sn.alpha)
-            raw[name] = c
+            if c is not None:
+                raw[name] = c
         raw[name + "#planes"] = planes
         return True
 

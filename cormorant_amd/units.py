@@ -613,15 +613,18 @@ def matmul_aplanes(a_planes: torch.Tensor, nsum: int, b_planes: torch.Tensor, c:
     return c
 
 
-def vectorop_planes(a: torch.Tensor, b: Optional[torch.Tensor], c: torch.Tensor, size: int, op: int, outer: int,
-                    a_inc: int, b_inc: int, planes: torch.Tensor, act: int = 0, alpha: int = 0) -> torch.Tensor:
+def vectorop_planes(a: torch.Tensor, b: Optional[torch.Tensor], c: Optional[torch.Tensor], size: int, op: int,
+                    outer: int, a_inc: int, b_inc: int, planes: torch.Tensor, act: int = 0,
+                    alpha: int = 0) -> Optional[torch.Tensor]:
     """cm_vectorop_planes: the VectorOP over `outer` runs of `size` (contiguous output rows) and
-    the byte planes of c for matmul_aplanes (n = outer, k = size, nsum = ceil(size / 1024))."""
+    the byte planes of its output for matmul_aplanes (n = outer, k = size, nsum = ceil(size /
+    1024)); c None: the planes alone."""
     if outer and size:
         _require(a, "a", torch.int16, (outer - 1) * a_inc + size)
         if op < OP_RELU:
             _require(b, "b", torch.int16, (outer - 1) * b_inc + size)
-        _require(c, "c", torch.int16, outer * size)
+        if c is not None:
+            _require(c, "c", torch.int16, outer * size)
         _require_planes(planes, outer, size, (size + 1023) // 1024)
     rc = _lib.lib().cm_vectorop_planes(_ptr(a), _ptr(b), _ptr(c), size, op, outer, a_inc, b_inc, act, alpha,
                                        _ptr(planes), _stream())

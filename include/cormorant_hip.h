@@ -104,8 +104,9 @@ int cm_vectorop(const int16_t* a, const int16_t* b, int16_t* c, uint32_t size, u
  * outputs are contiguous rows (a_inc + b_inc == size), also writing the output's byte planes
  * for a following cm_matmul_aplanes with A = c (n = outer, k = size): `planes` holds
  * cm_matmul_a_planes_bytes(outer, size, ceil(size / 1024)) bytes, 256-byte aligned.  c is what
- * cm_vectorop writes.  No counterpart in the reference: the operand split of this build's
- * matmul, done by the VectorOP call that produces the operand. */
+ * cm_vectorop writes; c may be NULL when only the matmul reads the output (the planes alone
+ * are written).  No counterpart in the reference: the operand split of this build's matmul,
+ * done by the VectorOP call that produces the operand. */
 int cm_vectorop_planes(const int16_t* a, const int16_t* b, int16_t* c, uint32_t size, uint32_t op, uint32_t outer,
                        uint32_t a_inc, uint32_t b_inc, uint32_t act, uint32_t alpha, void* planes, void* stream);
 

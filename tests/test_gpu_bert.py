@@ -30,3 +30,23 @@ def test_encoder_every_tensor(shape, seed, fused):
     want = oracle_graph.forward(g, inputs)
     for name, v in got.items():
         np.testing.assert_array_equal(v, want[name].reshape(v.shape), err_msg=name)
+
+
+def test_encoder_lean_forward():
+    """forward_raw with keep = the output: the FFN's GELU output, read only by FFN2 as its byte
+    planes, is not written (absent from the result), and the output is the full forward's."""
+    shape = models.BertShape(layers=2, batch=2, seq=64, d=128, heads=2, ff=512, vocab=1000)
+    g, inputs, _ = models.bert_encoder(shape, seed=7)
+    sim = Simulator(g)
+    out = g.output_tensors[0].onnx_name
+    feeds = {nm: sim._to_device(sim._tensor(nm), v) for nm, v in inputs.items()}
+    full = sim.forward_raw(feeds)
+    lean = sim.forward_raw(feeds, keep=[out])
+    skipped = [nm for nm in full if "#" not in nm and nm not in lean]
+    assert skipped, "the lean forward wrote every tensor"
+    assert all(sim._planes_only(nm) for nm in skipped)
+    np.testing.assert_array_equal(lean[out].cpu().numpy(), full[out].cpu().numpy())
+    want = oracle_graph.forward(g, inputs)[out]
+    got = sim._to_values(sim._tensor(out), lean[out])
+    np.testing.assert_array_equal(got, want.reshape(got.shape))
+

@@ -186,6 +186,13 @@ def test_vectorop_planes(U, rows, k, act, arity):
     np.testing.assert_array_equal(lo, rlo)
     np.testing.assert_array_equal(part, rsum)
     check_matmul(U, planes, nsum, c1, rows, k, k)
+    # the planes alone (no int16 output): the same planes and sums
+    p2 = U.a_planes(rows, k, nsum, "cuda")
+    U.vectorop_planes(a, b, None, k, op, rows, k, 0, p2, act=act)
+    hi2, lo2, part2 = read_planes(p2, rows, k, nsum)
+    np.testing.assert_array_equal(hi2, rhi)
+    np.testing.assert_array_equal(lo2, rlo)
+    np.testing.assert_array_equal(part2, rsum)
 
 
 @pytest.mark.parametrize("B,T,H", [(2, 128, 3), (1, 384, 12)])
