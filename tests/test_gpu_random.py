@@ -821,22 +821,26 @@ def test_table_init_round_trip(U, oracle_lib):
         U.vectorop(dev16(xs), dev16(np.zeros(len(xs), np.int16)), c, len(xs), U.OP_ADD, act=4)
         return host(c)[:len(xs)]
     before = silu(x)
-    U.act_table_init(full)
-    U.rowops_tables_init(img)
-    np.testing.assert_array_equal(silu(x), before)
-    changed = full.copy()
-    d1 = -int(changed[0][32768 - 1])                  # SiLU(-1) = -d[1], SiLU(1) = 1 - d[1]
-    d1n = d1 + 1 if d1 < 255 else d1 - 1
-    changed[0][32768 - 1], changed[0][32768 + 1] = -d1n, 1 - d1n
-    U.act_table_init(changed)
-    got = silu(x)
-    want = before.copy()
-    want[2048 - 1], want[2048 + 1] = -d1n, 1 - d1n
-    np.testing.assert_array_equal(got, want)
-    bad = full.copy()
-    bad[1][32768 - 5] = 3                             # GELU(-5) = +3: no byte d[5]
-    with pytest.raises(ValueError):
-        U.act_table_init(bad)
-    np.testing.assert_array_equal(silu(x), got)       # unchanged by the refused call
-    U.act_table_init(full)
+    try:
+        U.act_table_init(full)
+        U.rowops_tables_init(img)
+        np.testing.assert_array_equal(silu(x), before)
+        changed = full.copy()
+        d1 = -int(changed[0][32768 - 1])                  # SiLU(-1) = -d[1], SiLU(1) = 1 - d[1]
+        d1n = d1 + 1 if d1 < 255 else d1 - 1
+        changed[0][32768 - 1], changed[0][32768 + 1] = -d1n, 1 - d1n
+        U.act_table_init(changed)
+        got = silu(x)
+        want = before.copy()
+        want[2048 - 1], want[2048 + 1] = -d1n, 1 - d1n
+        np.testing.assert_array_equal(got, want)
+        bad = full.copy()
+        bad[1][32768 - 5] = 3                             # GELU(-5) = +3: no byte d[5]
+        with pytest.raises(ValueError):
+            U.act_table_init(bad)
+        np.testing.assert_array_equal(silu(x), got)       # unchanged by the refused call
+        U.act_table_init(full)
+    finally:                                         # the library's own tables for every later test
+        U.act_table_init(full)
+        U.rowops_tables_init(img)
     np.testing.assert_array_equal(silu(x), before)
