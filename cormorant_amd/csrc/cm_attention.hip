@@ -260,7 +260,8 @@ __global__ __launch_bounds__(256, 3) void attention_kernel(const int16_t* __rest
     psum += __shfl_xor(psum, 32, 64);                  // sum_j P[qi][j]
 
     // ---- phase 3: o^T[d][qi] over 4 blocks of 16 d, two per staged half of V^T
-    int16_t* orow = o + ((uint64_t)b * T + qi) * o_ld + kHd * h;      // result lane: d = 16 mb + 4 g + r
+    // result lane: d = 16 mb + 4 g + r (o null: the planes alone)
+    int16_t* orow = o != nullptr ? o + ((uint64_t)b * T + qi) * o_ld + kHd * h : nullptr;
     const uint64_t prow = (uint64_t)b * T + qi;
     int32_t osum = 0;                                                   // PL: the lane's 16 outputs' sum
 #pragma unroll
@@ -313,7 +314,7 @@ __global__ __launch_bounds__(256, 3) void attention_kernel(const int16_t* __rest
                 const int o1 = sat16_shr8(wrap_sum(ohh[m][r + 1], omid[m][r + 1], oll[m][r + 1], t1));
                 pk[r / 2] = (uint32_t)(uint16_t)o0 | ((uint32_t)(uint16_t)o1 << 16);
             }
-            *reinterpret_cast<uint2*>(orow + 16 * mb + 4 * g) = make_uint2(pk[0], pk[1]);
+            if (orow != nullptr) *reinterpret_cast<uint2*>(orow + 16 * mb + 4 * g) = make_uint2(pk[0], pk[1]);
             if constexpr (PL) {
                 const uint32_t col = kHd * h + 16 * mb + 4 * g;
                 *reinterpret_cast<uint32_t*>(po.hi + prow * po.k + col) = __builtin_amdgcn_perm(pk[1], pk[0], 0x07050301u);
@@ -344,6 +345,8 @@ int run_attention(const int16_t* qkv, int16_t* o, uint32_t batch, uint32_t seq, 
     int rc = state(&st);
     if (rc) return rc;
     if (batch == 0 || heads == 0) return CM_OK;
+    if (qkv == nullptr || (o == nullptr && planes == nullptr))
+        return fail(CM_EINVAL, "attention: a null qkv, or a null o without planes");
     if (head_dim != kHd) return fail(CM_EINVAL, "attention: head_dim %u (the kernel takes 64)", head_dim);
     if (seq != 64 && seq != 128 && seq != 256 && seq != 384)
         return fail(CM_EINVAL, "attention: %u keys (64, 128, 256 or 384)", seq);

@@ -526,8 +526,10 @@ class Simulator:
             units.rowops_jobs([self._whole_row_job(sn, a2d, None, out, params[0])], planes=planes)
             raw[name] = out.reshape(-1)
         elif isinstance(sn, AttentionNode):
-            self._attention(sn, raw, planes=planes)
-            raw[name] = self._attention_out
+            # o itself only where something besides the output projection's planes reads it
+            self._attention(sn, raw, planes=planes, write_o=not self._planes_only(name))
+            if self._attention_out is not None:
+                raw[name] = self._attention_out
         else:
             a = self._get(sn.inputs[0], raw).reshape(-1).contiguous()
             # the int16 output only where something besides the plane-path MatMuls reads it
@@ -1016,10 +1018,12 @@ class Simulator:
         buf[:, :w] = x2d
         return buf, per * _KB[kind], per
 
-    def _attention(self, sn: AttentionNode, raw, planes: Optional[torch.Tensor] = None) -> torch.Tensor:
+    def _attention(self, sn: AttentionNode, raw, planes: Optional[torch.Tensor] = None,
+                   write_o: bool = True) -> Optional[torch.Tensor]:
         """An encoder layer's attention: one cm_attention call (with ``planes``, cm_attention_planes:
-        o's byte planes as well), or (shapes it does not take) the head split, the two
-        contractions and the softmax unit call by call."""
+        o's byte planes as well, and with ``write_o`` False the planes alone: None returned), or
+        (shapes it does not take) the head split, the two contractions and the softmax unit
+        call by call."""
         xt, ot = sn.inputs[0], sn.output
         B, T, H, hd = sn.batch, sn.seq, sn.heads, sn.head_dim
         ld, cols = int(xt.shape[-1]), sn.heads * sn.head_dim
@@ -1037,7 +1041,7 @@ class Simulator:
         if fo.size != 1 or int(fo[0]) != fp + f["v"] - self._dtype.frac_bits:
             raise SchedulerError(f"attention '{ot.onnx_name}': output exponent is not f_p + f_v - 8")
         x = self._get(xt, raw).reshape(-1)
-        o = self._new(ot)
+        o = self._new(ot) if write_o or planes is None else None
         if (hd == 64 and T in (64, 128, 256, 384) and ld % 8 == 0 and cols % 8 == 0
                 and sn.q_off % 8 == 0 and sn.k_off % 8 == 0 and sn.v_off % 8 == 0):
             if planes is not None:

@@ -632,18 +632,20 @@ def vectorop_planes(a: torch.Tensor, b: Optional[torch.Tensor], c: Optional[torc
     return c
 
 
-def attention_planes(qkv: torch.Tensor, o: torch.Tensor, batch: int, seq: int, heads: int, head_dim: int, ld: int,
-                     q_off: int, k_off: int, v_off: int, smx_cm: int, smx_cfg: int,
-                     planes: torch.Tensor) -> torch.Tensor:
+def attention_planes(qkv: torch.Tensor, o: Optional[torch.Tensor], batch: int, seq: int, heads: int, head_dim: int,
+                     ld: int, q_off: int, k_off: int, v_off: int, smx_cm: int, smx_cfg: int,
+                     planes: torch.Tensor) -> Optional[torch.Tensor]:
     """cm_attention_planes: attention() with o's rows heads x head_dim wide, and o's byte planes
-    for matmul_aplanes (n = batch seq, k = heads head_dim, nsum = heads)."""
+    for matmul_aplanes (n = batch seq, k = heads head_dim, nsum = heads); o None: the planes
+    alone."""
     if batch and heads:
         cols = heads * head_dim
         for off in (q_off, k_off, v_off):
             if off < 0 or off + cols > ld:
                 raise ValueError("attention: head columns past the row")
         _require(qkv, "qkv", torch.int16, (batch * seq - 1) * ld + max(q_off, k_off, v_off) + cols)
-        _require(o, "o", torch.int16, batch * seq * cols)
+        if o is not None:
+            _require(o, "o", torch.int16, batch * seq * cols)
         _require_planes(planes, batch * seq, cols, heads)
     rc = _lib.lib().cm_attention_planes(_ptr(qkv), _ptr(o), batch, seq, heads, head_dim, ld, q_off, k_off, v_off,
                                         smx_cm, smx_cfg, _ptr(planes), _stream())

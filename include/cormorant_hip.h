@@ -360,8 +360,9 @@ int cm_attention(const int16_t* qkv, int16_t* o, uint32_t batch, uint32_t seq, u
 /* cm_attention with o's rows exactly heads x 64 wide (o_ld = heads * 64), also writing o's byte
  * planes for the output projection (cm_matmul_aplanes with A = o: n = batch * seq, k = heads *
  * 64, nsum = heads): `planes` holds cm_matmul_a_planes_bytes(batch * seq, heads * 64, heads)
- * bytes, 256-byte aligned.  No counterpart in the reference: the operand split of this
- * build's matmul, done by the attention that produces the operand. */
+ * bytes, 256-byte aligned; o may be NULL when only the projection reads it (the planes alone
+ * are written).  No counterpart in the reference: the operand split of this build's matmul,
+ * done by the attention that produces the operand. */
 int cm_attention_planes(const int16_t* qkv, int16_t* o, uint32_t batch, uint32_t seq, uint32_t heads,
                         uint32_t head_dim, uint64_t ld, uint32_t q_off, uint32_t k_off, uint32_t v_off,
                         uint32_t smx_cm, uint32_t smx_cfg, void* planes, void* stream);

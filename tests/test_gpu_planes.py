@@ -218,6 +218,13 @@ def test_attention_planes(U, B, T, H):
     np.testing.assert_array_equal(lo, rlo)
     np.testing.assert_array_equal(part, rsum)
     check_matmul(U, planes, H, o1, B * T, D, T)
+    # the planes alone (no o): the same planes and sums
+    p2 = U.a_planes(B * T, D, H, "cuda")
+    U.attention_planes(x, None, B, T, H, hd, ld, 0, D, 2 * D, cm, cfg, p2)
+    hi2, lo2, part2 = read_planes(p2, B * T, D, H)
+    np.testing.assert_array_equal(hi2, rhi)
+    np.testing.assert_array_equal(lo2, rlo)
+    np.testing.assert_array_equal(part2, rsum)
 
 
 def test_graph_with_split_producers(U):
