@@ -240,7 +240,7 @@ __device__ __forceinline__ void addx_unit(const int (&x)[8], const int (&y)[8], 
     }
 }
 
-// One NORM row of the fast path (norm_row_vals), its int16 results to rc and, with PL, their
+// One NORM row of the fast path (norm_row_vals), its int16 results to rc (null: not written) and, with PL, their
 // byte planes and row sums per 1024 columns (unit u in sum u / 128 = k / 2) as row `prow` of
 // `po`.  Wavefront-uniform control.
 template <int UPL, bool PL>
@@ -255,7 +255,7 @@ __device__ __forceinline__ void norm_row(const Job& j, const int (&x)[UPL][8], u
         const uint32_t u = lane + 64 * k;
         ps[k] = 0;
         if (u >= units) continue;
-        store_stream(rc + 16u * u, o[k]);
+        if (rc != nullptr) store_stream(rc + 16u * u, o[k]);
         if constexpr (PL) {
             uint2 h, l;
             split8(o[k], h, l);
@@ -342,7 +342,8 @@ __global__ __launch_bounds__(64 * NW) void ro_norm_fast_kernel(Job j, const uint
                 for (int l = 0; l < 8; l++) x[k][l] = r[l];
             }
         }
-        norm_row<UPL, PL>(j, x, j.c + (u64)i2 * j.c_s2 + (u64)i1 * j.c_s1, ro_lds, bcast, tab, lane, units, ln, po,
+        norm_row<UPL, PL>(j, x, j.c != nullptr ? j.c + (u64)i2 * j.c_s2 + (u64)i1 * j.c_s1 : nullptr, ro_lds, bcast, tab,
+                          lane, units, ln, po,
                           row);
         if (row + stride < rows) load_row(row + stride);
     }
@@ -424,11 +425,11 @@ __global__ __launch_bounds__(TPR) void ro_norm_wg_kernel(Job j, const uint8_t* _
         for (int w = 1; w < NWV; w++) norm_sums_add(ts, ws[w]);
         int4 o[UPL];
         norm_row_finish<UPL>(j.n, j.eps, ts, x, ro_lds, bcast, tab, t, TPR, units, ln, o);
-        uint8_t* rc = j.c + (u64)i2 * j.c_s2 + (u64)i1 * j.c_s1;
+        uint8_t* rc = j.c != nullptr ? j.c + (u64)i2 * j.c_s2 + (u64)i1 * j.c_s1 : nullptr;   // null: planes alone
 #pragma unroll
         for (int k = 0; k < UPL; k++) {
             const uint32_t u = t + TPR * k;
-            if (u < units) store_stream(rc + 16u * u, o[k]);
+            if (u < units && rc != nullptr) store_stream(rc + 16u * u, o[k]);
         }
         if constexpr (PL) {
             int32_t* sa = slab_acc[it & 1];
@@ -944,6 +945,10 @@ int run_chain(const cm_rowops_desc* jobs, uint32_t n_jobs, void* planes, hipStre
             continue;
         }
         const cm_rowops_desc& dn = jobs[fuse ? i + 1 : i];
+        // the NORM's rows may stay unwritten only when this launch writes their planes (the
+        // chain's last job); the residual sum of a fused ADDX is always written
+        if ((dn.c == 0 && !pl) || (fuse && jobs[i].c == 0))
+            return fail(CM_EINVAL, "rowops chain: a null output (only the planes' NORM may leave its rows unwritten)");
         const Job jn = job_of(dn);
         if (jn.c1 == 0 || jn.c2 == 0) {
             i += fuse ? 1 : 0;

@@ -518,13 +518,14 @@ class Simulator:
         if isinstance(sn, RowOpsAdapter):
             at, ot = sn.inputs[0], sn.output
             a2d = self._get(at, raw).reshape(n, k)
-            out = torch.empty((n, k), dtype=_TORCH[ot.kind], device=self.device)
+            out = None if self._planes_only(name) else torch.empty((n, k), dtype=_TORCH[ot.kind], device=self.device)
             params = self._params.get(id(sn))
             if params is None:
                 params = [torch.from_numpy(np.ascontiguousarray(sn.jobs()[0].params, np.uint8)).to(self.device)]
                 self._params[id(sn)] = params
             units.rowops_jobs([self._whole_row_job(sn, a2d, None, out, params[0])], planes=planes)
-            raw[name] = out.reshape(-1)
+            if out is not None:
+                raw[name] = out.reshape(-1)
         elif isinstance(sn, AttentionNode):
             # o itself only where something besides the output projection's planes reads it
             self._attention(sn, raw, planes=planes, write_o=not self._planes_only(name))
@@ -570,6 +571,7 @@ class Simulator:
         when a MatMul takes its output as A)."""
         width = sn.n
         rows = sn.output.numel // width
+        pl = self._planes_out(nxt)
         jobs = []
         for node in (sn, nxt):
             params = self._params.get(id(node))
@@ -578,12 +580,14 @@ class Simulator:
                 self._params[id(node)] = params
             a2d = (self._get(node.inputs[0], raw) if node is sn else out1).reshape(rows, width)
             b_all = self._get(node.inputs[1], raw) if len(node.inputs) > 1 else None
-            out = torch.empty((rows, width), dtype=_TORCH[node.output.kind], device=self.device)
+            # the NORM's rows only where something besides the next MatMul's planes reads them
+            skip = node is nxt and pl is not None and self._planes_only(node.output.onnx_name)
+            out = None if skip else torch.empty((rows, width), dtype=_TORCH[node.output.kind], device=self.device)
             jobs.append(self._whole_row_job(node, a2d, b_all, out, params[0]))
             if node is sn:
                 out1 = out
-            raw[node.output.onnx_name] = out.reshape(-1)
-        pl = self._planes_out(nxt)
+            if out is not None:
+                raw[node.output.onnx_name] = out.reshape(-1)
         planes = units.a_planes(*pl, self.device) if pl is not None else None
         units.rowops_jobs(jobs, planes=planes)
         if planes is not None:

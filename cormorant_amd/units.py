@@ -656,9 +656,10 @@ def attention_planes(qkv: torch.Tensor, o: Optional[torch.Tensor], batch: int, s
 def rowops_jobs(jobs: Sequence[dict], planes: Optional[torch.Tensor] = None) -> None:
     """Row-ops jobs in order through cm_rowops_chain, each job a dict of rowops()'s arguments
     with its own tensors (a / b / c / p: GPU uint8 images or None); with ``planes``
-    (cm_rowops_chain_planes) also the byte planes of the last job's output."""
+    (cm_rowops_chain_planes) also the byte planes of the last job's output, whose c may then be
+    None (the planes alone)."""
     descs = (_lib.CmRowopsDesc * len(jobs))()
-    for d, j in zip(descs, jobs):
+    for idx, (d, j) in enumerate(zip(descs, jobs)):
         ext = rowops_extents(j["op"], j["n"], j["c1"], j["c2"], j["a_s1"], j["a_s2"], j["b_s1"], j["b_s2"],
                              j["c_s1"], j["c_s2"], j.get("aux", 0), j.get("win_lo", 0), j.get("win_hi", 0xFFFFFFFF))
         if ext is not None:
@@ -666,6 +667,10 @@ def rowops_jobs(jobs: Sequence[dict], planes: Optional[torch.Tensor] = None) -> 
             for key, lo, hi in (("a", a_lo, a_hi), ("b", 0, b_end), ("c", 0, c_end), ("p", 0, p_end)):
                 if hi <= lo:
                     continue
+                if key == "c" and j.get("c") is None and planes is not None and idx == len(jobs) - 1:
+                    continue                   # the planes' NORM writing the planes alone
+                if key == "c" and j.get("c") is None:
+                    raise ValueError("rowops: a null output (only the planes' last NORM may omit its rows)")
                 t = j.get(key)
                 if t is None or not t.is_cuda or t.dtype != torch.uint8 or not t.is_contiguous():
                     raise ValueError(f"rowops: {key} must be a contiguous GPU uint8 tensor")

@@ -306,7 +306,9 @@ int cm_rowops_chain(const cm_rowops_desc* jobs, uint32_t n_jobs, void* stream);
 /* cm_rowops_chain that also writes the byte planes of the last job's output for a following
  * cm_matmul_aplanes (A = that output): the last job is a NORM of int16 rows of n elements, n a
  * multiple of 64, with its own parameter block; `planes` holds cm_matmul_a_planes_bytes(c1 c2,
- * n, ceil(n / 1024)) bytes, 256-byte aligned (row r of the job grid = i2 c1 + i1).  In both
+ * n, ceil(n / 1024)) bytes, 256-byte aligned (row r of the job grid = i2 c1 + i1).  That
+ * NORM's c may be 0 when only the matmul reads its rows (the planes alone are written); any
+ * other null output is refused (CM_EINVAL).  In both
  * chain calls a COPY / ADDX job with an int32 output that the next job, a NORM over the same
  * rows, takes as its A runs with that NORM as one launch (each row read once; the parameter
  * RAM ends as the NORM leaves it).  No counterpart in the reference: the chain of

@@ -159,6 +159,18 @@ def test_addx_norm_one_launch(U, rows, n, a32, planes_on):
         np.testing.assert_array_equal(lo, rlo)
         np.testing.assert_array_equal(part, rsum)
         check_matmul(U, outs[1][2], nsum, outs[1][3], rows, n, n)
+        # the NORM's rows left unwritten (c None): the same residual sum and planes
+        h1 = torch.empty(rows * n, dtype=torch.int32, device="cuda")
+        p2 = U.a_planes(rows, n, nsum, "cuda")
+        jn2 = dict(_job(ln, h1, None, outs[1][3], pn), c=None)
+        U.rowops_jobs([_job(add, h, d, h1, pa), jn2], planes=p2)
+        np.testing.assert_array_equal(host(h1), outs[0][0])
+        hi2, lo2, part2 = read_planes(p2, rows, n, nsum)
+        np.testing.assert_array_equal(hi2, rhi)
+        np.testing.assert_array_equal(lo2, rlo)
+        np.testing.assert_array_equal(part2, rsum)
+        with pytest.raises(ValueError):                # a null output without planes is refused
+            U.rowops_jobs([_job(add, h, d, h1, pa), jn2])
 
 
 @pytest.mark.parametrize("rows,k,act,arity", [(300, 3072, 5, 2), (96, 1088, 0, 2), (130, 640, 2, 1)])
