@@ -99,6 +99,7 @@ class TimedLaunch {
 
   private:
     int slot_ = -1;
+    unsigned flags_ = 0;
     hipStream_t s_;
 };
 

@@ -226,12 +226,50 @@ static hipEvent_t take_event() {
     return e;
 }
 
+// On a stream under capture the pair becomes two event-record nodes of the graph, so every
+// replay of the graph re-records them around the launch; otherwise a plain record.  The null
+// stream is never captured; a refused query's error is cleared so that the launch check after
+// it does not report it.
+static unsigned record_flags(hipStream_t s) {
+    if (s == nullptr) return 0;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return cs == hipStreamCaptureStatusActive ? hipEventRecordExternal : 0;
+}
+
+// Under capture the record is an event-record node added to the captured graph by hand, after
+// the stream's current dependencies, which it then replaces (the stream-capture form of an
+// external record, which not every HIP runtime accepts from hipEventRecordWithFlags).
+static hipError_t record_event(hipEvent_t e, hipStream_t s, unsigned flags) {
+    if (!flags) return hipEventRecord(e, s);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    unsigned long long id = 0;
+    hipGraph_t graph = nullptr;
+    const hipGraphNode_t* deps = nullptr;
+    size_t nd = 0;
+    hipError_t r = hipStreamGetCaptureInfo_v2(s, &cs, &id, &graph, &deps, &nd);
+    if (r != hipSuccess) return r;
+    if (cs != hipStreamCaptureStatusActive || graph == nullptr) return hipErrorInvalidValue;
+    hipGraphNode_t node = nullptr;
+    r = hipGraphAddEventRecordNode(&node, graph, deps, nd, e);
+    if (r != hipSuccess) return r;
+    r = hipStreamUpdateCaptureDependencies(s, &node, 1, hipStreamSetCaptureDependencies);
+    return r;
+}
+
 TimedLaunch::TimedLaunch(const char* name, hipStream_t s) : s_(s) {
     std::lock_guard<std::mutex> lk(g_tmu);
     if (!g_timing || (!g_select.empty() && g_select != name)) return;
     TimingRecord r{name, take_event(), take_event()};
     if (!r.start || !r.stop) return;
-    if (hipEventRecord(r.start, s) != hipSuccess) return;
+    flags_ = record_flags(s);
+    if (record_event(r.start, s, flags_) != hipSuccess) {
+        (void)hipGetLastError();
+        return;
+    }
     g_records.push_back(r);
     slot_ = (int)g_records.size() - 1;
 }
@@ -239,7 +277,8 @@ TimedLaunch::TimedLaunch(const char* name, hipStream_t s) : s_(s) {
 TimedLaunch::~TimedLaunch() {
     if (slot_ < 0) return;
     std::lock_guard<std::mutex> lk(g_tmu);
-    if (slot_ < (int)g_records.size()) (void)hipEventRecord(g_records[slot_].stop, s_);
+    if (slot_ < (int)g_records.size() && record_event(g_records[slot_].stop, s_, flags_) != hipSuccess)
+        (void)hipGetLastError();
 }
 
 }  // namespace cm

@@ -245,18 +245,42 @@ static i64 mm_b(const int16_t* b, unsigned kk, unsigned j, unsigned k, unsigned 
 int oracle_matmul(const int16_t* a, const int16_t* b, int16_t* c, unsigned n, unsigned k,
                   unsigned m, unsigned batch, long a_bs, long b_bs, long c_bs, unsigned b_packed,
                   unsigned gemv_kw, int wrap) {
+    /* Rows are independent: one output row per iteration, over every core.  Each row's sums
+     * are formed from B's column j as a contiguous run of k (the transposed image packed == 2
+     * as it is, any other image gathered once per batch slice); the int32-wrap sums are exact
+     * mod 2^32 in uint32 arithmetic, the saturating ones exact in int64. */
     for (unsigned bt = 0; bt < batch; bt++) {
         const int16_t* A = a + (long)bt * a_bs;
         const int16_t* B = b + (long)bt * b_bs;
         int16_t* C = c + (long)bt * c_bs;
-        for (unsigned i = 0; i < n; i++)
+        int16_t* Bt = NULL;
+        if (b_packed != 2 || gemv_kw) {
+            Bt = (int16_t*)malloc((size_t)m * k * sizeof(int16_t));
+            if (!Bt) return -1;
+#pragma omp parallel for schedule(static)
+            for (long j = 0; j < (long)m; j++)
+                for (unsigned kk = 0; kk < k; kk++) Bt[(size_t)j * k + kk] = (int16_t)mm_b(B, kk, (unsigned)j, k, m, b_packed, gemv_kw);
+        }
+        const int16_t* BT = Bt ? Bt : B;
+#pragma omp parallel for schedule(static)
+        for (long i = 0; i < (long)n; i++) {
+            const int16_t* Ar = A + (size_t)i * k;
             for (unsigned j = 0; j < m; j++) {
-                i64 acc = 0;
-                for (unsigned kk = 0; kk < k; kk++)
-                    acc += (i64)A[(size_t)i * k + kk] * mm_b(B, kk, j, k, m, b_packed, gemv_kw);
-                if (wrap) acc = wrap32(acc);
+                const int16_t* Br = BT + (size_t)j * k;
+                i64 acc;
+                if (wrap) {
+                    uint32_t s = 0;
+                    for (unsigned kk = 0; kk < k; kk++) s += (uint32_t)((int32_t)Ar[kk] * (int32_t)Br[kk]);
+                    acc = (i64)(int32_t)s;
+                } else {
+                    i64 s = 0;
+                    for (unsigned kk = 0; kk < k; kk++) s += (i64)((int32_t)Ar[kk] * (int32_t)Br[kk]);
+                    acc = s;
+                }
                 C[(size_t)i * m + j] = (int16_t)sat16(floor_shr(acc, 8));
             }
+        }
+        free(Bt);
     }
     return 0;
 }

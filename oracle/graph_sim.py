@@ -17,6 +17,7 @@ import numpy as np
 from oracle import cm
 from oracle import host_ref
 from oracle import rowops_adapt
+from oracle import sim_ref
 from oracle.attn_prep import attn_prep, clamp_n, transpose
 
 F = 8                                   # the element type's fraction bits (ap_fixed<16,8>)
@@ -237,10 +238,71 @@ def _host_op(sn, ins, vals):
                               T, H, KV, HD)
 
 
-def forward(graph, inputs, states=None):
+def _oracle_matmul(sn, a, b):
+    """A MatMul through the C oracle's integer product on raw lanes: wrap32 for the pow2 path
+    (_simulate.py:814-835), the exact sum for Q8.8 (:620-633)."""
+    at, bt, out = sn.inputs[0], sn.inputs[1], sn.output
+    k, m = int(bt.shape[-2]), int(bt.shape[-1])
+    pow2 = _pow2(at, bt, out)
+    fo = np.broadcast_to(np.asarray(F if out.exp is None or not pow2 else out.exp, np.float64).reshape(-1), (m,))
+    ra = (_raw_of(at, a) if pow2 else _to_raw(a)).reshape(-1, k).astype(np.int16)
+    if pow2:
+        fb = (np.asarray(F if bt.wexp is None else bt.wexp, np.float64) if bt.wexp is not None
+              else np.asarray(F if bt.exp is None else bt.exp, np.float64))
+        rb = np.rint(np.asarray(b, np.float64).reshape(k, m) * np.power(2.0, fb)).astype(np.int16)
+    else:
+        rb = _to_raw(b).reshape(k, m)
+    n = ra.shape[0]
+    c = cm.matmul(np.ascontiguousarray(ra).reshape(-1), np.ascontiguousarray(rb.T).reshape(-1), n, k, m,
+                  b_packed=2, wrap32=pow2)
+    return (c.reshape(n, m).astype(np.float64) / np.power(2.0, fo)).reshape(out.shape)
+
+
+def _oracle_contract(a, b):
+    """sat16(floor(wrap32(a . b) / 2^8)) of raw int16 matrices a [n][k], b [k][m] through the C oracle."""
+    n, k = a.shape
+    m = b.shape[1]
+    c = cm.matmul(np.ascontiguousarray(a, np.int16).reshape(-1), np.ascontiguousarray(b.T, np.int16).reshape(-1),
+                  n, k, m, b_packed=2, wrap32=True)
+    return c.reshape(n, m).astype(np.int64)
+
+
+_UNIT_ACT_OF_OP = {6: 3, 7: 4, 8: 5, 9: 6}      # the activation ops and the act they apply
+
+
+def _ref_norm(sn, x):
+    """A row-ops norm adapter by the reference simulator's per-row integer loop (sim_ref)."""
+    kind, x_t, y = type(sn).__name__, sn.inputs[0], sn.output
+    W = int(x_t.shape[-1])
+    fo = rowops_adapt._chan(y, W, getattr(sn, "F", F))
+    if kind == "RMSNormRoNode":
+        gamma = np.asarray(sn.gamma, np.float64).reshape(-1)
+        n = gamma.size
+        fx = rowops_adapt._chan(x_t, W, getattr(sn, "F", F))
+        raw = rowops_adapt._raw(x_t, x, W).astype(np.int64).reshape(-1, n)
+        r = sim_ref.rms_norm(raw, int(fx[0]), gamma, sn.eps, fo[:n]).reshape(-1, W)
+    else:
+        fx = rowops_adapt._chan(x_t, W, getattr(sn, "F", F))
+        raw = rowops_adapt._raw(x_t, x, W).astype(np.int64)
+        gamma = np.ones(W) if sn.gamma is None else np.asarray(sn.gamma, np.float64).reshape(-1)
+        beta = np.zeros(W) if sn.beta is None else np.asarray(sn.beta, np.float64).reshape(-1)
+        r = sim_ref.layer_norm(raw, int(fx[0]), gamma, beta, sn.eps, fo)
+    return r.astype(np.float64) / np.power(2.0, fo.astype(np.float64))
+
+
+ALGOS = ("port", "ref", "oracle")
+
+
+def forward(graph, inputs, states=None, algo="port"):
     """Every tensor's float64 values.  ``states`` ({name: float64 array}) are the persistent
     states, updated in place (_simulate.py:573-577); default: zeros, or copies of the inputs
-    of those names."""
+    of those names.  ``algo`` picks how the costly units are computed, with the same results:
+    "port" (float64 BLAS contractions, the C oracle for the units), "ref" (as "port" but the
+    row-ops norms and the activation unit by the reference simulator's own algorithms,
+    oracle/sim_ref.py) or "oracle" (every MatMul and attention contraction through the C
+    oracle's integer product on all cores)."""
+    if algo not in ALGOS:
+        raise ValueError(f"algo {algo!r}: one of {ALGOS}")
     vals = {k: np.array(v, np.float64) for k, v in inputs.items()}      # copies: states change in place
     for t in getattr(graph, "state_tensors", []):
         if states is not None and t.onnx_name in states:
@@ -255,7 +317,9 @@ def forward(graph, inputs, states=None):
             # a MatMul lowered onto the conv unit computes exactly MatmulNode's result
             # (_simulate.py:620-633 treats both alike)
             a, b = get(sn.inputs[0]), get(sn.inputs[1])
-            if _pow2(sn.inputs[0], sn.inputs[1], out):
+            if algo == "oracle" and kind == "MatmulNode" and len(sn.inputs[1].shape) == 2:
+                vals[out.onnx_name] = _oracle_matmul(sn, a, b)
+            elif _pow2(sn.inputs[0], sn.inputs[1], out):
                 vals[out.onnx_name] = _matmul_exp(sn, a, b).reshape(out.shape)
             else:
                 vals[out.onnx_name] = _truncate(np.matmul(a, b)).reshape(out.shape)
@@ -267,6 +331,8 @@ def forward(graph, inputs, states=None):
             n = get(sn.inputs[3]) if not sn.static and sn.has_n else sn.T
             vals[out.onnx_name] = _attn_conv(sn, get(sn.inputs[0]), get(sn.inputs[1]), np.asarray(pos).reshape(-1)[0],
                                              np.asarray(n).reshape(-1)[0]).reshape(out.shape)
+        elif algo == "ref" and kind in ("LayerNormRoNode", "LayerNorm32RoNode", "RMSNormRoNode"):
+            vals[out.onnx_name] = _ref_norm(sn, get(sn.inputs[0])).reshape(out.shape)
         elif kind in ADAPTERS:
             host = lambda t: int(np.asarray(get(t)).reshape(-1)[0])        # noqa: E731
             vals[out.onnx_name] = rowops_adapt.adapter(sn, [get(t) for t in sn.inputs], host).reshape(out.shape)
@@ -291,10 +357,16 @@ def forward(graph, inputs, states=None):
                     q = x[b, :, sn.q_off + h * hd:sn.q_off + (h + 1) * hd].astype(np.float64)
                     k = x[b, :, sn.k_off + h * hd:sn.k_off + (h + 1) * hd].astype(np.float64)
                     v = x[b, :, sn.v_off + h * hd:sn.v_off + (h + 1) * hd].astype(np.float64)
-                    s_ = _wrap_floor(k @ q.T).astype(np.int16)                       # [keys][queries]
+                    if algo == "oracle":
+                        s_ = _oracle_contract(k, q.T).astype(np.int16)
+                    else:
+                        s_ = _wrap_floor(k @ q.T).astype(np.int16)                   # [keys][queries]
                     p_ = cm.vectorop(np.ascontiguousarray(s_.reshape(-1)), None, T * k8, T, 11, T, T, k8, 0, 0,
                                      sn.cm, sn.cfg, T).reshape(T, k8)[:, :T]
-                    o[b, :, h * hd:(h + 1) * hd] = _wrap_floor(p_.astype(np.float64) @ v)
+                    if algo == "oracle":
+                        o[b, :, h * hd:(h + 1) * hd] = _oracle_contract(p_, v)
+                    else:
+                        o[b, :, h * hd:(h + 1) * hd] = _wrap_floor(p_.astype(np.float64) @ v)
             fo = float(F if out.exp is None else out.exp)
             vals[out.onnx_name] = (o.astype(np.float64) / 2.0 ** fo).reshape(out.shape)
         elif kind == "LlmEmbedNode":
@@ -416,8 +488,15 @@ def forward(graph, inputs, states=None):
             ar = _to_raw(full(sn.inputs[0])).reshape(-1)
             br = _to_raw(full(sn.inputs[1])).reshape(-1) if binary else None
             n = ar.size
-            c = cm.vectorop(ar, br, (n + 7) & ~7, n, sn.op_code, 1, 0, 0, sn.act, sn.alpha)
-            vals[out.onnx_name] = _from_raw(c[:n]).reshape(out.shape)
+            unit_act = _UNIT_ACT_OF_OP.get(sn.op_code, sn.act if sn.act >= 3 else 0)
+            if algo == "ref" and unit_act:
+                # the op's floored result, then the activation unit per element with libm
+                x = ar if sn.op_code in _UNIT_ACT_OF_OP else cm.vectorop(ar, br, (n + 7) & ~7, n, sn.op_code, 1, 0,
+                                                                         0, 0, 0)[:n]
+                vals[out.onnx_name] = _from_raw(sim_ref.act_unit(unit_act, x, sn.alpha)).reshape(out.shape)
+            else:
+                c = cm.vectorop(ar, br, (n + 7) & ~7, n, sn.op_code, 1, 0, 0, sn.act, sn.alpha)
+                vals[out.onnx_name] = _from_raw(c[:n]).reshape(out.shape)
         else:
             raise NotImplementedError(type(sn).__name__)
     return vals
