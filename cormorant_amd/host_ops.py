@@ -16,7 +16,7 @@ import ctypes
 import math
 import os
 from dataclasses import dataclass, field
-from typing import List, Optional
+from typing import List, Optional, Sequence
 
 import numpy as np
 
@@ -134,6 +134,25 @@ class LayerNormNode(HostNode):
         _check(host_lib().cmh_layernorm(_ptr(x), _ptr(y), x.shape[0], n, _ptr(g), _ptr(b), float(self.eps),
                                         int(self.tf_form)), "host layernorm")
         return (y.astype(np.float64) / 256.0).reshape(self.output.shape)
+
+
+@dataclass
+class TransposeNode(HostNode):
+    """ONNX Transpose on the host (host_nodes.py:1254-1330): a bit move, output[i] =
+    input[i permuted by ``perm``]; values and exponents unchanged."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    perm: Sequence[int] = ()
+
+    def __post_init__(self):
+        x = self.inputs[0]
+        self.perm = [int(p) for p in (self.perm if len(self.perm) else range(len(x.shape) - 1, -1, -1))]
+        if sorted(self.perm) != list(range(len(x.shape))) or list(self.output.shape) != [x.shape[p] for p in self.perm]:
+            raise SchedulerError(f"Transpose '{self.output.onnx_name}': perm {self.perm} of {list(x.shape)}")
+
+    def reference(self, ins, dtype):
+        x = np.asarray(ins[0], np.float64).reshape(self.inputs[0].shape)
+        return np.ascontiguousarray(x.transpose(self.perm)).reshape(self.output.shape)
 
 
 GELU_C1 = 0.044715

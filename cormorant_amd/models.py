@@ -21,8 +21,10 @@ from .host_ops import LlmEmbedNode
 from .rowops_nodes import LayerNorm32RoNode, ResAddBiasRoNode
 
 
-def small_cnn(seed: int = 0):
-    """(graph, inputs): the small CNN and one seeded input image."""
+def small_cnn(seed: int = 0, as_ops: bool = False):
+    """(graph, inputs): the small CNN and one seeded input image.  ``as_ops``: instead of the
+    graph, (ops, tensors, inputs, outputs) -- the network as the reference's ONNX ops for the
+    front end (frontend.build_graph), over the same seeded tensors."""
     rng = np.random.default_rng(seed)
     T = TensorInfo
     x = T("input", [1, 1, 28, 28])
@@ -56,6 +58,20 @@ def small_cnn(seed: int = 0):
     ]
     g = Graph(nodes, input_tensors=[x], output_tensors=[sm])
     inputs = {"input": np.round(rng.uniform(0.0, 1.0, (1, 1, 28, 28)) * 256) / 256}
+    if as_ops:
+        from .frontend import OpDesc as O
+        ops = [O("Conv", ["input", "conv1.w", "conv1.b"], ["conv1"], {"pads": [1, 1, 1, 1]}),
+               O("Relu", ["conv1"], ["relu1"]),
+               O("MaxPool", ["relu1"], ["pool1"], {"kernel_shape": [2, 2], "strides": [2, 2]}),
+               O("Conv", ["pool1", "conv2.w", "conv2.b"], ["conv2"], {"pads": [1, 1, 1, 1]}),
+               O("Relu", ["conv2"], ["relu2"]),
+               O("MaxPool", ["relu2"], ["pool2"], {"kernel_shape": [2, 2], "strides": [2, 2]}),
+               O("Flatten", ["pool2"], ["flat"]),
+               O("MatMul", ["flat", "fc.w"], ["fc"]),
+               O("Add", ["fc", "fc.b"], ["logits"]),
+               O("Softmax", ["logits"], ["probs"], {"axis": -1})]
+        return (ops, {t.onnx_name: t for t in [x, w1, b1, c1, r1, p1, w2, b2, c2, r2, p2, fl, wf, mm, bf, ad, sm]},
+                ["input"], ["probs"]), inputs
     return g, inputs
 
 
@@ -65,7 +81,7 @@ MOBILENET_V2_BLOCKS = ((1, 16, 1, 1), (6, 24, 2, 2), (6, 32, 3, 2), (6, 64, 4, 2
                        (6, 160, 3, 2), (6, 320, 1, 1))
 
 
-def mobilenet_v2(batch: int = 32, res: int = 224, seed: int = 0, classes: int = 1000):
+def mobilenet_v2(batch: int = 32, res: int = 224, seed: int = 0, classes: int = 1000, as_ops: bool = False):
     """(graph, inputs, macs): MobileNetV2 1.0 in Q8.8, NCHW, batch ``batch`` at ``res`` x ``res``.
 
     Stem Conv 3x3 s2 3->32 pad 1 + RELU6; the 17 inverted residual blocks (1x1 expand x t +
@@ -79,15 +95,24 @@ def mobilenet_v2(batch: int = 32, res: int = 224, seed: int = 0, classes: int = 
 
     He-normal weights (std sqrt(2 / fan_in)), the input U[0, 1); every tensor Q8.8.  Weights
     come from their own generator, so a smaller batch of the same seed is the leading images
-    of a larger one.  ``macs`` counts the convolutions' and the classifier's multiply-adds."""
+    of a larger one.  ``macs`` counts the convolutions' and the classifier's multiply-adds.
+    ``as_ops``: (ops, tensors, inputs, outputs) -- the reference's ONNX ops (Conv, Clip(0, 6),
+    Add, GlobalAveragePool, Flatten, MatMul) over the same tensors -- in place of the graph."""
+    from .frontend import OpDesc
     T = TensorInfo
     rng_in = np.random.default_rng([seed, 0])
     x_val = np.round(rng_in.random((batch, 3, res, res)) * 256) / 256
     rng = np.random.default_rng([seed, 1])
-    nodes, macs = [], [0]
+    nodes, macs, ops, reg = [], [0], [], {}
     x_t = T("input", [batch, 3, res, res])
+    reg["input"] = x_t
     cur = x_t
     count = [0]
+
+    def op(kind, ins, out, **attrs):
+        for t in list(ins) + [out]:
+            reg[t.onnx_name] = t
+        ops.append(OpDesc(kind, [t.onnx_name for t in ins], [out.onnx_name], attrs))
 
     def name(tag):
         count[0] += 1
@@ -103,12 +128,14 @@ def mobilenet_v2(batch: int = 32, res: int = 224, seed: int = 0, classes: int = 
         y = T(name("conv"), [batch, cout, oh, ow])
         nodes.append(ConvNode([x, wt], y, stride_h=stride, stride_w=stride, pad_top=pad, pad_left=pad,
                               is_depthwise=depthwise))
+        op("Conv", [x, wt], y, strides=[stride, stride], pads=[pad] * 4, group=cout if depthwise else 1)
         macs[0] += batch * cout * oh * ow * fan_in
         return y
 
     def relu6(x):
         y = T(name("relu6"), list(x.shape))
         nodes.append(ScheduledNode([x], y, units.OP_RELU6))
+        op("Clip", [x], y, min=0.0, max=6.0)
         return y
 
     cur = relu6(conv(cur, 32, 3, 2))
@@ -124,17 +151,23 @@ def mobilenet_v2(batch: int = 32, res: int = 224, seed: int = 0, classes: int = 
             if stride == 1 and inp.shape[1] == c:
                 y = T(name("add"), list(h.shape))
                 nodes.append(ScheduledNode([h, inp], y, units.OP_ADD))
+                op("Add", [h, inp], y)
                 h = y
             cur = h
     cur = relu6(conv(cur, 1280, 1, 1))
     pooled = T("pool", [batch, 1280, 1, 1])
     nodes.append(PoolNode([cur], pooled, units.POOL_AVG, cur.shape[2], cur.shape[3], 1, 1))
+    op("GlobalAveragePool", [cur], pooled)
     flat = T("flat", [batch, 1280])
     nodes.append(ReshapeNode([pooled], flat))
+    op("Flatten", [pooled], flat)
     wf = T("fc.w", [1280, classes], data=rng.standard_normal((1280, classes)) * math.sqrt(2.0 / 1280))
     logits = T("logits", [batch, classes])
     nodes.append(MatmulNode([flat, wf], logits))
+    op("MatMul", [flat, wf], logits)
     macs[0] += batch * 1280 * classes
+    if as_ops:
+        return (ops, reg, ["input"], ["logits"]), {"input": x_val}, macs[0]
     return Graph(nodes, input_tensors=[x_t], output_tensors=[logits]), {"input": x_val}, macs[0]
 
 
@@ -187,7 +220,8 @@ class BertShape:
         return self.layers * self.batch * self.seq * (4 * self.d * self.d + 2 * self.d * self.ff)
 
 
-def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int = 1, fused_attention: bool = True):
+def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int = 1, fused_attention: bool = True,
+                 as_ops: bool = False):
     """(graph, inputs, exps): the BERT-base-shaped encoder in per-tensor power-of-two numerics.
 
     Token ids U{0 .. vocab-1} (the graph's input) and embedding rows N(0, 1), gathered on the
@@ -214,7 +248,11 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
     ``fused_attention`` (default): the head split, q.K^T, the softmax, P.V and the merge as
     one AttentionNode (the same arithmetic in one call, cm_attention on MFMA); False: node by
     node, the contractions on the plane GEMM reading and writing per-head views in place.
+    ``as_ops`` (with the fused attention): (ops, tensors, inputs, outputs) in place of the graph --
+    the encoder as the reference's ops (LlmEmbed, VitLayerNorm, MatMul, the attention chain as
+    VitAttention, VitResAdd, Add + Gelu) for the front end, weights not yet encoded.
     """
+    from .frontend import LLM_DOMAIN, OpDesc
     from .numeric import encode_matmul_weights
     from .dtype import AP_FIXED_16_8
 
@@ -292,20 +330,34 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
     ids_t = T_("ids", [rows], exp=0, kind="i32")
     h_in = T_("h0", [rows, D], exp=RES_BITS, kind="i32")
     nodes = [LlmEmbedNode([ids_t], h_in, table=emb)]
+    ops, reg = [], {"ids": ids_t}
+    if as_ops and not fused_attention:
+        raise ValueError("bert_encoder: the op list describes the fused attention (VitAttention)")
+
+    def op(kind, ins, out, domain="", **attrs):
+        for t in list(ins) + [out]:
+            reg[t.onnx_name] = t
+        ops.append(OpDesc(kind, [t.onnx_name for t in ins], [out.onnx_name], attrs, domain))
+
+    op("LlmEmbed", [ids_t], h_in, LLM_DOMAIN, table=emb)
     hcur = h_in
     for li, (L, e) in enumerate(zip(Ls, exps)):
         p = f"l{li}."
         x1 = T_(p + "x1", [rows, D], exp=e["x1"])
         nodes.append(LayerNorm32RoNode([hcur], x1, gamma=L["g1"], beta=L["be1"], eps=S.eps))
+        op("VitLayerNorm", [hcur], x1, LLM_DOMAIN, gamma=L["g1"], beta=L["be1"], eps=S.eps)
         wqkv = T_(p + "wqkv", [D, 3 * D], data=L["wqkv"])
         qkv = T_(p + "qkv", [rows, 3 * D], exp=np.repeat([e["q"], e["k"], e["v"]], D))
         nodes.append(MatmulNode([x1, wqkv], qkv))
+        op("MatMul", [x1, wqkv], qkv)
         ld = 3 * D
         cmr, cfg = softmax_regs(e["s"], 1.0 / math.sqrt(hd), e["p"])
         om = T_(p + "om", [rows, D], exp=e["o"])
         if fused_attention:
             nodes.append(AttentionNode([qkv], om, batch=S.batch, seq=T, heads=H, head_dim=hd, q_off=0, k_off=D,
                                        v_off=2 * D, cm=cmr, cfg=cfg))
+            op("VitAttention", [qkv], om, LLM_DOMAIN, batch=S.batch, seq=T, heads=H, head_dim=hd, q_off=0, k_off=D,
+               v_off=2 * D, cm=cmr, cfg=cfg)
         else:
             # the per-head q / K / V rows read in place from qkv, o written in place into om
             hv = lambda col: HeadView(col, H, hd, T)                                 # noqa: E731
@@ -318,26 +370,38 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
         wo = T_(p + "wo", [D, D], data=L["wo"])
         ao = T_(p + "ao", [rows, D], exp=e["ao"])
         nodes.append(MatmulNode([om, wo], ao))
+        op("MatMul", [om, wo], ao)
         h1 = T_(p + "h1", [rows, D], exp=RES_BITS, kind="i32")
         nodes.append(ResAddBiasRoNode([hcur, ao], h1, bias=L["bo"]))
+        op("VitResAdd", [hcur, ao], h1, LLM_DOMAIN, bias=L["bo"])
         x2 = T_(p + "x2", [rows, D], exp=e["x2"])
         nodes.append(LayerNorm32RoNode([h1], x2, gamma=L["g2"], beta=L["be2"], eps=S.eps))
+        op("VitLayerNorm", [h1], x2, LLM_DOMAIN, gamma=L["g2"], beta=L["be2"], eps=S.eps)
         w1 = T_(p + "w1", [D, S.ff], data=L["w1"])
         # FFN1's output, the bias and the GELU run in the element type itself (Q8.8: no annotation)
         f = T_(p + "f", [rows, S.ff])
         nodes.append(MatmulNode([x2, w1], f))
+        op("MatMul", [x2, w1], f)
         b1 = T_(p + "b1", [S.ff], data=L["b1"])
         a = T_(p + "a", [rows, S.ff])
         nodes.append(ScheduledNode([f, b1], a, units.OP_ADD, act=units.ACT_GELU))
+        fb = T_(p + "fb", [rows, S.ff])
+        op("Add", [f, b1], fb)
+        op("Gelu", [fb], a)
         w2 = T_(p + "w2", [S.ff, D], data=L["w2"])
         dd = T_(p + "dd", [rows, D], exp=e["dd"])
         nodes.append(MatmulNode([a, w2], dd))
+        op("MatMul", [a, w2], dd)
         hn = T_(p + "h", [rows, D], exp=RES_BITS, kind="i32")
         nodes.append(ResAddBiasRoNode([h1, dd], hn, bias=L["b2"]))
+        op("VitResAdd", [h1, dd], hn, LLM_DOMAIN, bias=L["b2"])
         hcur = hn
+    feeds = {"ids": ids.reshape(-1).astype(np.float64)}
+    if as_ops:
+        return (ops, reg, ["ids"], [hcur.onnx_name]), feeds, exps
     g = Graph(nodes, input_tensors=[ids_t], output_tensors=[hcur])
     encode_matmul_weights(g.nodes, AP_FIXED_16_8)
-    return g, {"ids": ids.reshape(-1).astype(np.float64)}, exps
+    return g, feeds, exps
 
 
 # ---------------------------------------------------------------- SmolLM2-360M-shaped decode step
@@ -421,7 +485,7 @@ def smollm2_weights(shape: LlamaShape = LlamaShape(), seed: int = 0):
 
 
 def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: int = 1, weights=None,
-                   runtime_pos: bool = False, fused_attention: bool = True):
+                   runtime_pos: bool = False, fused_attention: bool = True, as_ops: bool = False):
     """(graph, inputs, exps): one greedy decode step of ``shape.batch`` sequences, each at cache
     position ctx - 1 (the cache full after the step's row: every cache row is a key), pow2
     numerics on the units as the reference's llama.py front end lays out a layer with the
@@ -457,7 +521,12 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
     ``fused_attention``: the RoPE of q / k and the cache row writes as one DecodePrepNode, and
     q.K^T, the softmax and P.V as one DecodeAttentionNode (the same arithmetic; the RoPE'd k rows,
     s and P not materialized) where the kernels take the geometry; otherwise the RoPE and KV-write
-    nodes, the two contractions and the softmax node."""
+    nodes, the two contractions and the softmax node.
+
+    ``as_ops`` (with the fused attention): (ops, tensors, inputs, outputs) in place of the graph --
+    the step as the reference's LLM ops (LlmEmbed, LlmRMSNorm, MatMul, the attention prep and
+    chain as LlmDecodeAttention, LlmResAdd, LlmSiluMul, LlmDequant) for the front end."""
+    from .frontend import LLM_DOMAIN, OpDesc
     from .dtype import AP_FIXED_16_8
     from .numeric import encode_matmul_weights
     from .rowops_nodes import DecodePrepNode, DequantRoNode, RMSNormRoNode, ResAddRoNode, RopeRoNode, SiluMulRoNode
@@ -553,10 +622,20 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
 
     # ---- the integer graph
     T_ = TensorInfo
-    nodes = []
+    nodes, ops, reg = [], [], {}
+    if as_ops and not (fused_attention and DecodeAttentionNode.supports(HD, S.ctx, G) and HD % 16 == 0):
+        raise ValueError("smollm2_decode: the op list describes the fused decode attention")
+
+    def op(kind, ins, outs, domain="", **attrs):
+        outs = outs if isinstance(outs, list) else [outs]
+        for t in list(ins) + outs:
+            reg[t.onnx_name] = t
+        ops.append(OpDesc(kind, [t.onnx_name for t in ins], [t.onnx_name for t in outs], attrs, domain))
+
     ids_t = T_("ids", [B], exp=0, kind="i32")
     h_in = T_("h0", [B, D], exp=RES_BITS, kind="i32")
     nodes.append(LlmEmbedNode([ids_t], h_in, table=emb))
+    op("LlmEmbed", [ids_t], h_in, LLM_DOMAIN, table=emb)
     inputs = {"ids": ids.astype(np.float64)}
     pos_t = T_("pos", [1], kind="host") if runtime_pos else None
     if runtime_pos:
@@ -573,12 +652,16 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
         inputs[vc_t.onnx_name] = np.round(vc.astype(np.float64) * 2.0 ** e["v"]) / 2.0 ** e["v"]
         x = T_(p + "x", [B, D], exp=e["x"])
         nodes.append(RMSNormRoNode([hcur], x, gamma=L["g1"], eps=S.eps))
+        op("LlmRMSNorm", [hcur], x, LLM_DOMAIN, gamma=L["g1"], eps=S.eps)
         q = T_(p + "q", [B, A], exp=e["q"])
         nodes.append(MatmulNode([x, T_(p + "wq", [D, A], data=L["wq"])], q))
+        op("MatMul", nodes[-1].inputs, q)
         k = T_(p + "k", [B, KD], exp=e["k"])
         nodes.append(MatmulNode([x, T_(p + "wk", [D, KD], data=L["wk"])], k))
+        op("MatMul", nodes[-1].inputs, k)
         v = T_(p + "v", [B, KD], exp=e["v"])
         nodes.append(MatmulNode([x, T_(p + "wv", [D, KD], data=L["wv"])], v))
+        op("MatMul", nodes[-1].inputs, v)
         qr = T_(p + "qr", [B, A], exp=e["q"])
         cmr, cfg = softmax_regs(e["s"], 1.0 / math.sqrt(HD), e["p"])
         om = T_(p + "om", [B, A], exp=e["o"])
@@ -588,6 +671,8 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
                                         sin=sin, pos=pos, pos_t=pos_t))
             nodes.append(DecodeAttentionNode([qr, kc_t, vc_t], om, heads=H, kv_heads=KV, head_dim=HD, cm=cmr, cfg=cfg,
                                              mask=pos + 1, mask_t=pos_t, mask_add=1))
+            op("LlmDecodeAttention", [q, k, v, kc_t, vc_t], [qr, om], LLM_DOMAIN, heads=H, kv_heads=KV, head_dim=HD,
+               cos=cos, sin=sin, pos=pos, pos_t=pos_t.onnx_name if pos_t is not None else None, cm=cmr, cfg=cfg)
         else:
             nodes.append(RopeRoNode([q], qr, heads=H, head_dim=HD, cos=cos, sin=sin, pos=pos, same_pos=True,
                                     pos_t=pos_t))
@@ -602,34 +687,52 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
                                       pos_t)
         a = T_(p + "a", [B, D], exp=e["a"])
         nodes.append(MatmulNode([om, T_(p + "wo", [A, D], data=L["wo"])], a))
+        op("MatMul", nodes[-1].inputs, a)
         h1 = T_(p + "h1", [B, D], exp=RES_BITS, kind="i32")
         nodes.append(ResAddRoNode([hcur, a], h1))
+        op("LlmResAdd", [hcur, a], h1, LLM_DOMAIN)
         x2 = T_(p + "x2", [B, D], exp=e["x2"])
         nodes.append(RMSNormRoNode([h1], x2, gamma=L["g2"], eps=S.eps))
+        op("LlmRMSNorm", [h1], x2, LLM_DOMAIN, gamma=L["g2"], eps=S.eps)
         gt = T_(p + "g", [B, S.ff], exp=e["g"])
         nodes.append(MatmulNode([x2, T_(p + "wg", [D, S.ff], data=L["wg"])], gt))
+        op("MatMul", nodes[-1].inputs, gt)
         up = T_(p + "u", [B, S.ff], exp=e["u"])
         nodes.append(MatmulNode([x2, T_(p + "wu", [D, S.ff], data=L["wu"])], up))
+        op("MatMul", nodes[-1].inputs, up)
         mm = T_(p + "m", [B, S.ff], exp=e["m"])
         nodes.append(SiluMulRoNode([gt, up], mm))
+        op("LlmSiluMul", [gt, up], mm, LLM_DOMAIN)
         dd = T_(p + "d", [B, D], exp=e["d"])
         nodes.append(MatmulNode([mm, T_(p + "wd", [S.ff, D], data=L["wd"])], dd))
+        op("MatMul", nodes[-1].inputs, dd)
         hn = T_(p + "h", [B, D], exp=RES_BITS, kind="i32")
         nodes.append(ResAddRoNode([h1, dd], hn))
+        op("LlmResAdd", [h1, dd], hn, LLM_DOMAIN)
         hcur = hn
     xf = T_("xf", [B, D], exp=fin["xf"])
     nodes.append(RMSNormRoNode([hcur], xf, gamma=gf, eps=S.eps))
+    op("LlmRMSNorm", [hcur], xf, LLM_DOMAIN, gamma=gf, eps=S.eps)
     lq = T_("logits_q", [B, S.vocab], exp=fin["logits"])
     nodes.append(MatmulNode([xf, T_("w.lm_head", [D, S.vocab], data=np.ascontiguousarray(emb.T))], lq))
+    op("MatMul", nodes[-1].inputs, lq)
     # the dequant's jobs take rows of at most 4096: the logits as [B * vocab / chunk][chunk]
     chunk = next(c for c in range(4096, 0, -8) if S.vocab % c == 0)
     lr = T_("logits_rows", [B * S.vocab // chunk, chunk], exp=fin["logits"])
     nodes.append(ReshapeNode([lq], lr))
+    op("Reshape", [lq], lr)
     lf = T_("logits_f32", [B * S.vocab // chunk, chunk], kind="f32")
     nodes.append(DequantRoNode([lr], lf))
+    op("LlmDequant", [lr], lf, LLM_DOMAIN)
     lo = T_("logits", [B, S.vocab], kind="f32")
     nodes.append(ReshapeNode([lf], lo))
-    g = Graph(nodes, input_tensors=[ids_t] + ([pos_t] if runtime_pos else []) + cache_ts, output_tensors=[lo])
+    op("Reshape", [lf], lo)
+    graph_inputs = [ids_t] + ([pos_t] if runtime_pos else []) + cache_ts
+    if as_ops:
+        for t in graph_inputs:
+            reg[t.onnx_name] = t
+        return (ops, reg, [t.onnx_name for t in graph_inputs], [lo.onnx_name]), inputs, exps
+    g = Graph(nodes, input_tensors=graph_inputs, output_tensors=[lo])
     encode_matmul_weights(g.nodes, AP_FIXED_16_8)
     return g, inputs, exps
 

@@ -70,7 +70,9 @@ int cm_rowops_tables_init(const void* img64k);
 
 /* Kernel timing (the role of the board runtime's per-call profiler,
  * inference-scheduler/runtime/inference_prof.c): while enabled, every kernel launch of the
- * library records a HIP event pair on its stream.  cm_timing_read waits for the recorded
+ * library records a HIP event pair on its stream; on a stream under graph capture the pair
+ * is two event-record nodes of the graph, re-recorded by each replay (read the records after
+ * a replay).  cm_timing_read waits for the recorded
  * launches of `kernel` (a name such as "gemm_planes_kernel") and returns their summed
  * duration and count; cm_timing_reset drops every record. */
 int cm_timing_enable(int on);

@@ -375,7 +375,7 @@ def forward(graph, inputs, states=None, algo="port"):
                                                  out.kind == "i32").reshape(out.shape)
         elif kind in _HOST_OPS:
             vals[out.onnx_name] = _host_op(sn, [get(t) for t in sn.inputs], vals).reshape(out.shape)
-        elif kind == "TransposeRoNode":
+        elif kind in ("TransposeRoNode", "TransposeNode"):
             xt = sn.inputs[0]
             vals[out.onnx_name] = transpose(get(xt).reshape(xt.shape), sn.perm).reshape(out.shape)
         elif kind == "AttnPrepRoNode":
