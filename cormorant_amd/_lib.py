@@ -42,6 +42,8 @@ SIGNATURES = {
     "cm_conv_w_planes_bytes": (ctypes.c_size_t, [_U32] * 4),
     "cm_conv_split_w": (_I32, [_P, _P, _U32, _U32, _U32, _U32, _P]),
     "cm_conv_planes": (_I32, [_P, _P, _P, _P] + [_U32] * 21 + [_P]),
+    "cm_conv_act": (_I32, [_P, _P, _P, _P] + [_U32] * 22 + [_P]),
+    "cm_conv_planes_act": (_I32, [_P, _P, _P, _P] + [_U32] * 22 + [_P]),
     "cm_pool": (_I32, [_P, _P] + [_U32] * 17 + [_P]),
     "cm_rowops": (_I32, [_P, _P, _P, _P] + [_U32] * 10 + [_I64] + [_U32] * 4 + [_P]),
     "cm_rowops_chain": (_I32, [ctypes.POINTER(CmRowopsDesc), _U32, _P]),

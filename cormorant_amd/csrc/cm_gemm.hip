@@ -463,6 +463,7 @@ struct EpiMatmul {              // C[bt][i][j] = c + off(bt) + i * ldc + j
     uint64_t ldc = 0;           // row stride (0: cols)
     uint64_t c_bs2 = 0;         // with `inner` > 1: slice bt at (bt / inner) c_bs + (bt % inner) c_bs2
     uint32_t inner = 1;
+    int32_t lo = -32768, hi = 32767;    // output bounds (the saturation; a fused RELU / RELU6 narrows them)
     __device__ int32_t row_bias(uint32_t) const { return 0; }
     __device__ int16_t* row_ptr(uint32_t bt, uint32_t i) const {
         if (i >= rows) return nullptr;
@@ -485,6 +486,7 @@ struct EpiConv {                // y pattern (ConvKernel.h:250-258); acc seeded 
     uint64_t img;               // elements per image (out_ch * plane)
     uint32_t rows, cols, cs, cn, gs, wrap, pairs;
     uint32_t fold;              // pixels per image when the images are folded into the columns, else 0
+    int32_t lo = -32768, hi = 32767;    // output bounds (the saturation; a fused RELU / RELU6 narrows them)
     __device__ int32_t row_bias(uint32_t i) const { return bias && i < rows ? (int32_t)bias[i] : 0; }
     __device__ int16_t* row_ptr(uint32_t bt, uint32_t i) const {
         if (i >= rows) return nullptr;
@@ -523,8 +525,11 @@ __device__ __forceinline__ int32_t clamp_i32(int32_t v, int32_t lo, int32_t hi) 
     return min(max(v, lo), hi);
 }
 
+// The result is clamped to [lo, hi] inside the int16 range: the saturation, or with a fused
+// RELU (lo = 0) / RELU6 (lo = 0, hi = 6 * 2^8) the activation of the saturated value as well.
 template <uint32_t MODE>
-__device__ __forceinline__ int32_t recombine(int32_t hh, int32_t mid, int32_t ll, int32_t rhch, int32_t rlcl) {
+__device__ __forceinline__ int32_t recombine(int32_t hh, int32_t mid, int32_t ll, int32_t rhch, int32_t rlcl,
+                                             int32_t lo, int32_t hi) {
     const int32_t y = mid + rhch + ((ll + rlcl) >> 8);
     int32_t q;
     if (MODE == kSatNarrow) {
@@ -536,7 +541,7 @@ __device__ __forceinline__ int32_t recombine(int32_t hh, int32_t mid, int32_t ll
         const long long w = ((long long)hh << 8) + (long long)mid + (long long)rhch + ((ll + rlcl) >> 8);
         q = (int32_t)(w > 32767 ? 32767 : (w < -32768 ? -32768 : w));
     }
-    return clamp_i32(q, -32768, 32767);
+    return clamp_i32(q, lo, hi);
 }
 
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -561,9 +566,10 @@ __device__ __forceinline__ void store_wave_tile(const v16i (&hh)[2][2], const v1
             for (int r = 0; r < 16; r += 2) {
                 const uint32_t rl = wr * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                 const int2 r0 = rterm[rl], r1 = rterm[rl + 1];
-                const int32_t q0 = recombine<MODE>(hh[i][j][r], mid[i][j][r], ll[i][j][r], r0.x + ct.x, r0.y + ct.y);
+                const int32_t q0 = recombine<MODE>(hh[i][j][r], mid[i][j][r], ll[i][j][r], r0.x + ct.x, r0.y + ct.y,
+                                                   epi.lo, epi.hi);
                 const int32_t q1 = recombine<MODE>(hh[i][j][r + 1], mid[i][j][r + 1], ll[i][j][r + 1], r1.x + ct.x,
-                                                   r1.y + ct.y);
+                                                   r1.y + ct.y, epi.lo, epi.hi);
                 if (PAIRS) {
                     const int32_t give = odd ? q0 : q1;
                     const int32_t got = __builtin_amdgcn_mov_dpp(give, 0xB1, 0xF, 0xF, false);
@@ -593,7 +599,7 @@ template <uint32_t MODE>
 __device__ __forceinline__ void store_wave_fast(const v16i (&hh)[2][2], const v16i (&mid)[2][2],
                                                 const v16i (&ll)[2][2], const int2* rterm, const int2* cterm,
                                                 int16_t* __restrict__ base, uint32_t ld, uint32_t wr, uint32_t wc,
-                                                uint32_t l32, uint32_t lh) {
+                                                uint32_t l32, uint32_t lh, int32_t lo, int32_t hi) {
     const uint32_t odd = l32 & 1;
     const uint32_t lane_off = (wr * 64 + 4 * lh + odd) * ld + wc * 64 + l32 - odd;
 #pragma unroll
@@ -605,9 +611,10 @@ __device__ __forceinline__ void store_wave_fast(const v16i (&hh)[2][2], const v1
             for (int r = 0; r < 16; r += 2) {
                 const uint32_t rl = wr * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                 const int2 r0 = rterm[rl], r1 = rterm[rl + 1];
-                const int32_t q0 = recombine<MODE>(hh[i][j][r], mid[i][j][r], ll[i][j][r], r0.x + ct.x, r0.y + ct.y);
+                const int32_t q0 = recombine<MODE>(hh[i][j][r], mid[i][j][r], ll[i][j][r], r0.x + ct.x, r0.y + ct.y,
+                                                   lo, hi);
                 const int32_t q1 = recombine<MODE>(hh[i][j][r + 1], mid[i][j][r + 1], ll[i][j][r + 1], r1.x + ct.x,
-                                                   r1.y + ct.y);
+                                                   r1.y + ct.y, lo, hi);
                 // the pair exchange of store_wave_tile: the even lane stores row r, the odd lane row r + 1
                 const int32_t give = odd ? q0 : q1;
                 const int32_t got = __builtin_amdgcn_mov_dpp(give, 0xB1, 0xF, 0xF, false);
@@ -928,9 +935,10 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
 #define CM_STORE(M, P) store_wave_tile<M, P>(hh, mid, ll, rterm, cterm, bt, row0, col0, wr, wc, l32, lh, epi)
     const TileBase tb = epi.tile_base(bt, row0, col0, TM, BN);
     if (tb.base != nullptr) {           // a whole tile: the lean store
-        if (mode == kWrap) store_wave_fast<kWrap>(hh, mid, ll, rterm, cterm, tb.base, tb.ld, wr, wc, l32, lh);
-        else if (mode == kSatNarrow) store_wave_fast<kSatNarrow>(hh, mid, ll, rterm, cterm, tb.base, tb.ld, wr, wc, l32, lh);
-        else store_wave_fast<kSatWide>(hh, mid, ll, rterm, cterm, tb.base, tb.ld, wr, wc, l32, lh);
+        if (mode == kWrap) store_wave_fast<kWrap>(hh, mid, ll, rterm, cterm, tb.base, tb.ld, wr, wc, l32, lh, epi.lo, epi.hi);
+        else if (mode == kSatNarrow)
+            store_wave_fast<kSatNarrow>(hh, mid, ll, rterm, cterm, tb.base, tb.ld, wr, wc, l32, lh, epi.lo, epi.hi);
+        else store_wave_fast<kSatWide>(hh, mid, ll, rterm, cterm, tb.base, tb.ld, wr, wc, l32, lh, epi.lo, epi.hi);
     } else if (mode == kSatNarrow) {
         if (epi.pairs) CM_STORE(kSatNarrow, true); else CM_STORE(kSatNarrow, false);
     } else if (mode == kWrap) {
@@ -951,7 +959,8 @@ __global__ __launch_bounds__(256) void conv_dw_kernel(const int16_t* __restrict_
                                                       uint32_t kw, uint32_t sh, uint32_t sw,
                                                       uint32_t dh, uint32_t dw, uint32_t pt,
                                                       uint32_t pl, uint32_t dws, uint32_t cs,
-                                                      uint32_t cn, uint32_t gs, uint32_t wrap) {
+                                                      uint32_t cn, uint32_t gs, uint32_t wrap, int32_t lo,
+                                                      int32_t hi) {
     for (uint64_t o = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total;
          o += (uint64_t)gridDim.x * blockDim.x) {
         const uint32_t ow = (uint32_t)(o % out_w);
@@ -976,8 +985,7 @@ __global__ __launch_bounds__(256) void conv_dw_kernel(const int16_t* __restrict_
         long long q = acc >> 8;
         const uint64_t plane = (uint64_t)out_h * out_w;
         uint64_t base = cn ? (uint64_t)(c % cn) * cs + (uint64_t)(c / cn) * gs : (uint64_t)c * cs;
-        y[nb * ch * plane + base + (uint64_t)oh * out_w + ow] =
-            (int16_t)(q > 32767 ? 32767 : (q < -32768 ? -32768 : q));
+        y[nb * ch * plane + base + (uint64_t)oh * out_w + ow] = (int16_t)(q > hi ? hi : (q < lo ? lo : q));
     }
 }
 
@@ -993,7 +1001,7 @@ __global__ __launch_bounds__(256) void conv_dw3_kernel(const int16_t* __restrict
                                                        uint32_t items, uint32_t strips, uint32_t ch, uint32_t in_h,
                                                        uint32_t in_w, uint32_t out_h, uint32_t out_w, uint32_t pt,
                                                        uint32_t pl, uint32_t dws, uint32_t cs, uint32_t cn,
-                                                       uint32_t gs, uint32_t wrap) {
+                                                       uint32_t gs, uint32_t wrap, int32_t lo, int32_t hi) {
     constexpr int NR = (R - 1) * SH + 3;
     const uint32_t per_plane = strips * out_w;
     for (uint32_t it = blockIdx.x * blockDim.x + threadIdx.x; it < items; it += gridDim.x * blockDim.x) {
@@ -1034,8 +1042,7 @@ __global__ __launch_bounds__(256) void conv_dw3_kernel(const int16_t* __restrict
                 for (int a = 0; a < 3; a++)
 #pragma unroll
                     for (int b = 0; b < 3; b++) acc += (uint32_t)(v[i * SH + a][b] * wv[a * 3 + b]);
-                const int q = (int)acc >> 8;
-                out[i] = q > 32767 ? 32767 : (q < -32768 ? -32768 : q);
+                out[i] = clamp_i32((int)acc >> 8, lo, hi);
             }
         } else {
 #pragma unroll
@@ -1046,7 +1053,7 @@ __global__ __launch_bounds__(256) void conv_dw3_kernel(const int16_t* __restrict
 #pragma unroll
                     for (int b = 0; b < 3; b++) acc += (long long)v[i * SH + a][b] * wv[a * 3 + b];
                 const long long q = acc >> 8;
-                out[i] = (int)(q > 32767 ? 32767 : (q < -32768 ? -32768 : q));
+                out[i] = (int)(q > hi ? hi : (q < lo ? lo : q));
             }
         }
         const uint64_t plane = (uint64_t)out_h * out_w;
@@ -1078,7 +1085,7 @@ __global__ __launch_bounds__(256) void conv_dw3v_kernel(const int16_t* __restric
                                                         uint32_t items, uint32_t strips, uint32_t groups, uint32_t ch,
                                                         uint32_t in_h, uint32_t in_w, uint32_t out_h, uint32_t out_w,
                                                         uint32_t pt, uint32_t dws, uint32_t cs, uint32_t cn,
-                                                        uint32_t gs, uint32_t wrap) {
+                                                        uint32_t gs, uint32_t wrap, int32_t lo, int32_t hi) {
     const uint32_t per_plane = strips * groups;
     for (uint32_t it = blockIdx.x * blockDim.x + threadIdx.x; it < items; it += gridDim.x * blockDim.x) {
         const uint32_t p = it / per_plane, rem = it - p * per_plane;
@@ -1116,7 +1123,7 @@ __global__ __launch_bounds__(256) void conv_dw3v_kernel(const int16_t* __restric
                         }
                     }
                     const long long v = a64 >> 8;
-                    yp[(uint64_t)(oh0 + i) * out_w + t] = (int16_t)(v > 32767 ? 32767 : (v < -32768 ? -32768 : v));
+                    yp[(uint64_t)(oh0 + i) * out_w + t] = (int16_t)(v > hi ? hi : (v < lo ? lo : v));
                 }
             }
             continue;
@@ -1173,7 +1180,7 @@ __global__ __launch_bounds__(256) void conv_dw3v_kernel(const int16_t* __restric
             if ((uint32_t)(oh0 + i) >= out_h) break;
             int q[8];
 #pragma unroll
-            for (int t = 0; t < 8; t++) q[t] = acc[i][t] >> 8;
+            for (int t = 0; t < 8; t++) q[t] = clamp_i32(acc[i][t] >> 8, lo, hi);
             int4 o;
             o.x = __builtin_bit_cast(int, __builtin_amdgcn_cvt_pk_i16(q[0], q[1]));
             o.y = __builtin_bit_cast(int, __builtin_amdgcn_cvt_pk_i16(q[2], q[3]));
@@ -2063,7 +2070,7 @@ int conv_split_w(const int16_t* w, Planes& A, uint32_t out_ch, uint32_t in_ch, u
 
 // The input's planes (im2col, or the folded 1x1 form) and the GEMM with the weights' planes A.
 int conv_gemm(const int16_t* x, const Planes& A, Planes& B, const int16_t* bptr, int16_t* y, const ConvGeom& g,
-              const DeviceState* st, hipStream_t s) {
+              const DeviceState* st, hipStream_t s, int32_t lo, int32_t hi) {
     const uint32_t plane = g.plane();
     const uint64_t img = (uint64_t)g.out_ch * plane;
     if (g.fold()) {
@@ -2079,7 +2086,7 @@ int conv_gemm(const int16_t* x, const Planes& A, Planes& B, const int16_t* bptr,
                       x, g.in_ch, plane, (uint64_t)g.in_ch * plane, cols, B.hi, B.lo, B.part, B.lines_p, B.kp);
         }
         const bool pairs = (reinterpret_cast<uintptr_t>(y) & 3) == 0 && (plane & 1) == 0;
-        EpiConv epi{y, bptr, img, g.out_ch, cols, plane, 0, 0, g.wrap, pairs ? 1u : 0u, plane};
+        EpiConv epi{y, bptr, img, g.out_ch, cols, plane, 0, 0, g.wrap, pairs ? 1u : 0u, plane, lo, hi};
         return run_gemm(A, B, 1, g.in_ch * g.kh * g.kw, epi, s);
     }
     SrcIm2col im{x, g.in_ch, g.in_h, g.in_w, g.out_w, g.kh, g.kw, g.sh, g.sw, g.dh, g.dw, g.pt, g.pl, plane};
@@ -2087,22 +2094,40 @@ int conv_gemm(const int16_t* x, const Planes& A, Planes& B, const int16_t* bptr,
     if (rc) return rc;
     const bool pairs = (reinterpret_cast<uintptr_t>(y) & 3) == 0 && (plane & 1) == 0 && (g.cs & 1) == 0 &&
                        (g.gs & 1) == 0 && (img & 1) == 0;
-    EpiConv epi{y, bptr, img, g.out_ch, plane, g.cs, g.cn, g.gs, g.wrap, pairs ? 1u : 0u, 0};
+    EpiConv epi{y, bptr, img, g.out_ch, plane, g.cs, g.cn, g.gs, g.wrap, pairs ? 1u : 0u, 0, lo, hi};
     return run_gemm(A, B, g.batch, g.in_ch * g.kh * g.kw, epi, s);
+}
+
+// The output bounds of a fused activation (the VectorOP act codes RELU = 1, RELU6 = 2, applied
+// to the raw int16 result: VectorOP ops 4 and 5 on the conv's output); CM_EINVAL otherwise.
+int act_bounds(uint32_t act, int32_t& lo, int32_t& hi) {
+    lo = -32768;
+    hi = 32767;
+    if (act == 0) return CM_OK;
+    if (act == 1 || act == 2) {
+        lo = 0;
+        if (act == 2) hi = 6 << 8;
+        return CM_OK;
+    }
+    return fail(CM_EINVAL, "conv: act %u (0 none, 1 RELU, 2 RELU6)", act);
 }
 
 }  // namespace
 }  // namespace cm
 
-extern "C" int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
-                       uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
-                       uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
-                       uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
-                       uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise, uint32_t y_cs,
-                       uint32_t y_cn, uint32_t y_gs, uint32_t wrap32, void* stream) {
-    using namespace cm;
+namespace cm {
+namespace {
+
+int conv_run(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y, uint32_t batch, uint32_t in_ch,
+             uint32_t in_h, uint32_t in_w, uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
+             uint32_t stride_h, uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
+             uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise, uint32_t y_cs, uint32_t y_cn,
+             uint32_t y_gs, uint32_t wrap32, uint32_t act, void* stream) {
     DeviceState* st;
     int rc = state(&st);
+    if (rc) return rc;
+    int32_t lo, hi;
+    rc = act_bounds(act, lo, hi);
     if (rc) return rc;
     if (batch == 0 || out_ch == 0 || out_h == 0 || out_w == 0) return CM_OK;
     if (kh == 0 || kw == 0 || kh > 7 || kw > 7) return fail(CM_EINVAL, "conv: kernel %ux%u outside 1..7", kh, kw);
@@ -2126,7 +2151,7 @@ extern "C" int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, 
 #define CM_DW3V(PL)                                                                                              \
     CM_LAUNCH("conv_dw3v_kernel", (conv_dw3v_kernel<PL, R>), dim3(blocks), dim3(256), 0, s, x, w, bptr, y,       \
               (uint32_t)items, strips, groups, out_ch, in_h, in_w, out_h, out_w, pad_top, 16u, cs, y_cn, y_gs, \
-              wrap32 ? 1u : 0u)
+              wrap32 ? 1u : 0u, lo, hi)
             if (pad_left == 0) { CM_DW3V(0); }
             else if (pad_left == 1) { CM_DW3V(1); }
             else { CM_DW3V(2); }
@@ -2143,11 +2168,11 @@ extern "C" int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, 
             if (stride_h == 1) {
                 CM_LAUNCH("conv_dw3_kernel", (conv_dw3_kernel<1, 1, 8>), dim3(blocks), dim3(256), 0, s, x, w, bptr, y,
                           (uint32_t)items, strips, out_ch, in_h, in_w, out_h, out_w, pad_top, pad_left, 16u, cs, y_cn,
-                          y_gs, wrap32 ? 1u : 0u);
+                          y_gs, wrap32 ? 1u : 0u, lo, hi);
             } else {
                 CM_LAUNCH("conv_dw3_kernel", (conv_dw3_kernel<2, 2, 4>), dim3(blocks), dim3(256), 0, s, x, w, bptr, y,
                           (uint32_t)items, strips, out_ch, in_h, in_w, out_h, out_w, pad_top, pad_left, 16u, cs, y_cn,
-                          y_gs, wrap32 ? 1u : 0u);
+                          y_gs, wrap32 ? 1u : 0u, lo, hi);
             }
             return CM_OK;
         }
@@ -2159,7 +2184,7 @@ extern "C" int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, 
         CM_LAUNCH("conv_dw_kernel", conv_dw_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, w, bptr, y, total,
                            out_ch, in_h, in_w, out_h, out_w, kh, kw, stride_h, stride_w, dilation_h,
                            dilation_w, pad_top, pad_left, (kh * kw + 7) & ~7u, cs, y_cn, y_gs,
-                           wrap32 ? 1u : 0u);
+                           wrap32 ? 1u : 0u, lo, hi);
         return CM_OK;
     }
     if ((uint64_t)in_ch * kh * kw > 32768)
@@ -2177,7 +2202,32 @@ extern "C" int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, 
     B.carve(p);
     rc = conv_split_w(w, A, out_ch, in_ch, kh, kw, s);
     if (rc) return rc;
-    return conv_gemm(x, A, B, bptr, y, g, st, s);
+    return conv_gemm(x, A, B, bptr, y, g, st, s, lo, hi);
+}
+
+}  // namespace
+}  // namespace cm
+
+extern "C" int cm_conv(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
+                       uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
+                       uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
+                       uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
+                       uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise, uint32_t y_cs,
+                       uint32_t y_cn, uint32_t y_gs, uint32_t wrap32, void* stream) {
+    return cm::conv_run(x, w, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w,
+                        dilation_h, dilation_w, pad_top, pad_left, has_bias, is_depthwise, y_cs, y_cn, y_gs, wrap32,
+                        0, stream);
+}
+
+extern "C" int cm_conv_act(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y, uint32_t batch,
+                           uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch, uint32_t out_h,
+                           uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h, uint32_t stride_w,
+                           uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top, uint32_t pad_left,
+                           uint32_t has_bias, uint32_t is_depthwise, uint32_t y_cs, uint32_t y_cn, uint32_t y_gs,
+                           uint32_t wrap32, uint32_t act, void* stream) {
+    return cm::conv_run(x, w, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w,
+                        dilation_h, dilation_w, pad_top, pad_left, has_bias, is_depthwise, y_cs, y_cn, y_gs, wrap32,
+                        act, stream);
 }
 
 extern "C" size_t cm_conv_w_planes_bytes(uint32_t out_ch, uint32_t in_ch, uint32_t kh, uint32_t kw) {
@@ -2203,15 +2253,20 @@ extern "C" int cm_conv_split_w(const int16_t* w, void* planes, uint32_t out_ch, 
     return conv_split_w(w, A, out_ch, in_ch, kh, kw, as_stream(stream));
 }
 
-extern "C" int cm_conv_planes(const int16_t* x, const void* w_planes, const int16_t* bias, int16_t* y,
-                              uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
-                              uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
-                              uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
-                              uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise, uint32_t y_cs,
-                              uint32_t y_cn, uint32_t y_gs, uint32_t wrap32, void* stream) {
-    using namespace cm;
+namespace cm {
+namespace {
+
+int conv_planes_run(const int16_t* x, const void* w_planes, const int16_t* bias, int16_t* y, uint32_t batch,
+                    uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch, uint32_t out_h, uint32_t out_w,
+                    uint32_t kh, uint32_t kw, uint32_t stride_h, uint32_t stride_w, uint32_t dilation_h,
+                    uint32_t dilation_w, uint32_t pad_top, uint32_t pad_left, uint32_t has_bias,
+                    uint32_t is_depthwise, uint32_t y_cs, uint32_t y_cn, uint32_t y_gs, uint32_t wrap32,
+                    uint32_t act, void* stream) {
     DeviceState* st;
     int rc = state(&st);
+    if (rc) return rc;
+    int32_t lo, hi;
+    rc = act_bounds(act, lo, hi);
     if (rc) return rc;
     if (batch == 0 || out_ch == 0 || out_h == 0 || out_w == 0) return CM_OK;
     if (is_depthwise) return fail(CM_EINVAL, "conv: weight planes are for standard convolutions");
@@ -2238,7 +2293,32 @@ extern "C" int cm_conv_planes(const int16_t* x, const void* w_planes, const int1
     if (rc) return rc;
     char* p = static_cast<char*>(ws);
     B.carve(p);
-    return conv_gemm(x, A, B, has_bias ? bias : nullptr, y, g, st, s);
+    return conv_gemm(x, A, B, has_bias ? bias : nullptr, y, g, st, s, lo, hi);
+}
+
+}  // namespace
+}  // namespace cm
+
+extern "C" int cm_conv_planes(const int16_t* x, const void* w_planes, const int16_t* bias, int16_t* y,
+                              uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
+                              uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
+                              uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
+                              uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise, uint32_t y_cs,
+                              uint32_t y_cn, uint32_t y_gs, uint32_t wrap32, void* stream) {
+    return cm::conv_planes_run(x, w_planes, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h,
+                               stride_w, dilation_h, dilation_w, pad_top, pad_left, has_bias, is_depthwise, y_cs,
+                               y_cn, y_gs, wrap32, 0, stream);
+}
+
+extern "C" int cm_conv_planes_act(const int16_t* x, const void* w_planes, const int16_t* bias, int16_t* y,
+                                  uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
+                                  uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
+                                  uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
+                                  uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise, uint32_t y_cs,
+                                  uint32_t y_cn, uint32_t y_gs, uint32_t wrap32, uint32_t act, void* stream) {
+    return cm::conv_planes_run(x, w_planes, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h,
+                               stride_w, dilation_h, dilation_w, pad_top, pad_left, has_bias, is_depthwise, y_cs,
+                               y_cn, y_gs, wrap32, act, stream);
 }
 
 extern "C" int cm_matmul_strided(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k, uint32_t m,

@@ -178,6 +178,12 @@ class Simulator:
                 self._addx_norm(sn, nodes[i], raw)
                 i += 1
                 continue
+            if i < len(nodes) and self._conv_act_fusable(sn, nodes[i]):
+                # a convolution and the RELU / RELU6 of its output: one launch, the activated output alone
+                act = units.ACT_RELU if nodes[i].op_code == units.OP_RELU else units.ACT_RELU6
+                raw[nodes[i].output.onnx_name] = self._conv(sn, raw, act=act, out_t=nodes[i].output)
+                i += 1
+                continue
             if self._planes_out(sn) is not None and self._planes_node(sn, raw):
                 continue
             if i < len(nodes) and self._prep_attention_fusable(sn, nodes[i]):
@@ -803,7 +809,38 @@ class Simulator:
         if not np.array_equal(fa[:, None] + fw, np.broadcast_to(fo[None, :] + F, (k, m))):
             raise ValueError("MatMul: exponents are inconsistent (accumulator not on the 2^-(f_out+F) grid)")
 
-    def _conv(self, sn: ConvNode, raw) -> torch.Tensor:
+    def _reader_counts(self) -> Dict[str, int]:
+        """How many nodes read each tensor."""
+        if getattr(self, "_readers_n", None) is None:
+            n: Dict[str, int] = {}
+            for sn in self._graph.nodes:
+                for t in getattr(sn, "inputs", []) or []:
+                    if t is not None:
+                        n[t.onnx_name] = n.get(t.onnx_name, 0) + 1
+            self._readers_n = n
+        return self._readers_n
+
+    def _conv_act_fusable(self, sn, nxt) -> bool:
+        """``sn`` a Q8.8 convolution whose output only ``nxt``, a unary RELU / RELU6 VectorOP of
+        plain Q8.8 tensors without an act of its own, reads, and which the caller does not keep:
+        the convolution applies the activation as it stores (cm_conv_act) and writes ``nxt``'s
+        output alone -- the two unit calls' result, with the intermediate never written."""
+        if not (isinstance(sn, ConvNode) and isinstance(nxt, ScheduledNode) and nxt.arity == 1
+                and nxt.op_code in (units.OP_RELU, units.OP_RELU6) and nxt.act == units.ACT_NONE):
+            return False
+        ct = sn.output
+        if self._keep is None or ct.onnx_name in self._keep or nxt.inputs[0].onnx_name != ct.onnx_name:
+            return False
+        if nxt.output.numel != ct.numel or self._pow2(*sn.inputs[:2], ct) or self._planes_out(nxt) is not None:
+            return False
+        for t in (ct, nxt.output):
+            if t.exp is not None or t.chexp is not None or t.kind != "i16" or t.state:
+                return False
+        fixed = {t.onnx_name for t in self._graph.output_tensors}
+        return ct.onnx_name not in fixed and self._reader_counts().get(ct.onnx_name, 0) == 1
+
+    def _conv(self, sn: ConvNode, raw, act: int = 0, out_t=None) -> torch.Tensor:
+        """The convolution; with ``act`` (RELU / RELU6) the activated result, stored as ``out_t``."""
         xt, wt, ot = sn.inputs[0], sn.inputs[1], sn.output
         bias_t = sn.inputs[2] if sn.has_bias else None
         x = self._get(xt, raw)
@@ -822,17 +859,17 @@ class Simulator:
             if bias is None:
                 bias = torch.from_numpy(conv_bias_image(self._get(bias_t, raw).cpu().numpy())).to(self.device)
                 self._images[key] = bias
-        y = self._new(ot)
+        y = self._new(ot if out_t is None else out_t)
         if img.dtype == torch.uint8:
             units.conv_planes(x.reshape(-1).contiguous(), img, bias, y, sn.batch, sn.in_ch, sn.in_h, sn.in_w,
                               sn.out_ch, sn.out_h, sn.out_w, sn.kh, sn.kw, sn.stride_h, sn.stride_w, sn.dilation_h,
                               sn.dilation_w, sn.pad_top, sn.pad_left, int(bias is not None),
-                              wrap32=self._pow2(xt, wt, ot))
+                              wrap32=self._pow2(xt, wt, ot), act=act)
             return y
         units.conv(x.reshape(-1).contiguous(), img, bias, y, sn.batch, sn.in_ch, sn.in_h, sn.in_w, sn.out_ch,
                    sn.out_h, sn.out_w, sn.kh, sn.kw, sn.stride_h, sn.stride_w, sn.dilation_h, sn.dilation_w,
                    sn.pad_top, sn.pad_left, int(bias is not None), int(sn.is_depthwise),
-                   wrap32=self._pow2(xt, wt, ot))
+                   wrap32=self._pow2(xt, wt, ot), act=act)
         return y
 
     def _pool(self, sn: PoolNode, raw) -> torch.Tensor:

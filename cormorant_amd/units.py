@@ -413,8 +413,9 @@ def conv(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], y: torc
          kh: int, kw: int, stride_h: int = 1, stride_w: int = 1, dilation_h: int = 1,
          dilation_w: int = 1, pad_top: int = 0, pad_left: int = 0, has_bias: int = 0,
          is_depthwise: int = 0, y_cs: int = 0, y_cn: int = 0, y_gs: int = 0,
-         wrap32: bool = False) -> torch.Tensor:
-    """ConvKernel (ConvKernel.h:229-259) on packed weights."""
+         wrap32: bool = False, act: int = 0) -> torch.Tensor:
+    """ConvKernel (ConvKernel.h:229-259) on packed weights; ``act`` 1 / 2 applies RELU / RELU6 to
+    the result (cm_conv_act: the VectorOP RELU / RELU6 of the output fused)."""
     if batch and out_ch and out_h and out_w:
         _require(x, "x", torch.int16, batch * in_ch * in_h * in_w)
         _require(w, "w", torch.int16, conv_weight_numel(out_ch, in_ch, kh, kw, bool(is_depthwise)))
@@ -425,11 +426,13 @@ def conv(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], y: torc
                                                (out_w, in_w, kw, stride_w, dilation_w, pad_left, "w")):
             if s == 0 or d == 0:
                 raise ValueError(f"conv: zero stride / dilation along {nm}")
-    rc = _lib.lib().cm_conv(_ptr(x), _ptr(w), _ptr(bias) if has_bias else None, _ptr(y), batch,
-                            in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w,
-                            dilation_h, dilation_w, pad_top, pad_left, int(has_bias),
-                            int(is_depthwise), y_cs, y_cn, y_gs, int(bool(wrap32)), _stream())
-    _lib.check(rc, "cm_conv")
+    args = (_ptr(x), _ptr(w), _ptr(bias) if has_bias else None, _ptr(y), batch, in_ch, in_h, in_w, out_ch, out_h,
+            out_w, kh, kw, stride_h, stride_w, dilation_h, dilation_w, pad_top, pad_left, int(has_bias),
+            int(is_depthwise), y_cs, y_cn, y_gs, int(bool(wrap32)))
+    if act:
+        _lib.check(_lib.lib().cm_conv_act(*args, int(act), _stream()), "cm_conv_act")
+    else:
+        _lib.check(_lib.lib().cm_conv(*args, _stream()), "cm_conv")
     return y
 
 
@@ -451,8 +454,9 @@ def conv_planes(x: torch.Tensor, w_planes: torch.Tensor, bias: Optional[torch.Te
                 batch: int, in_ch: int, in_h: int, in_w: int, out_ch: int, out_h: int, out_w: int,
                 kh: int, kw: int, stride_h: int = 1, stride_w: int = 1, dilation_h: int = 1,
                 dilation_w: int = 1, pad_top: int = 0, pad_left: int = 0, has_bias: int = 0,
-                y_cs: int = 0, y_cn: int = 0, y_gs: int = 0, wrap32: bool = False) -> torch.Tensor:
-    """cm_conv of a standard convolution with the weights' split image from conv_w_planes."""
+                y_cs: int = 0, y_cn: int = 0, y_gs: int = 0, wrap32: bool = False, act: int = 0) -> torch.Tensor:
+    """cm_conv of a standard convolution with the weights' split image from conv_w_planes;
+    ``act`` as conv's (cm_conv_planes_act)."""
     if batch and out_ch and out_h and out_w:
         _require(x, "x", torch.int16, batch * in_ch * in_h * in_w)
         if has_bias:
@@ -463,11 +467,13 @@ def conv_planes(x: torch.Tensor, w_planes: torch.Tensor, bias: Optional[torch.Te
             raise ValueError("w_planes: the uint8 image of conv_w_planes for these out_ch, in_ch, kh, kw")
         if stride_h == 0 or stride_w == 0 or dilation_h == 0 or dilation_w == 0:
             raise ValueError("conv: zero stride / dilation")
-    rc = _lib.lib().cm_conv_planes(_ptr(x), _ptr(w_planes), _ptr(bias) if has_bias else None, _ptr(y), batch,
-                                   in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w,
-                                   dilation_h, dilation_w, pad_top, pad_left, int(has_bias), 0, y_cs, y_cn, y_gs,
-                                   int(bool(wrap32)), _stream())
-    _lib.check(rc, "cm_conv_planes")
+    args = (_ptr(x), _ptr(w_planes), _ptr(bias) if has_bias else None, _ptr(y), batch, in_ch, in_h, in_w, out_ch,
+            out_h, out_w, kh, kw, stride_h, stride_w, dilation_h, dilation_w, pad_top, pad_left, int(has_bias), 0,
+            y_cs, y_cn, y_gs, int(bool(wrap32)))
+    if act:
+        _lib.check(_lib.lib().cm_conv_planes_act(*args, int(act), _stream()), "cm_conv_planes_act")
+    else:
+        _lib.check(_lib.lib().cm_conv_planes(*args, _stream()), "cm_conv_planes")
     return y
 
 

@@ -259,6 +259,25 @@ int cm_conv_planes(const int16_t* x, const void* w_planes, const int16_t* bias, 
                    uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise, uint32_t y_cs,
                    uint32_t y_cn, uint32_t y_gs, uint32_t wrap32, void* stream);
 
+/* cm_conv / cm_conv_planes with the VectorOP activation that follows the conv in the graph
+ * applied to the result before it is stored: act 1 = RELU (VectorOP op 4), 2 = RELU6 (op 5,
+ * clamp of the raw int16 to [0, 6 * 2^8]), 0 = none; CM_EINVAL for any other act.  No
+ * counterpart in the reference's units (the reference runs the activation as its own VectorOP
+ * call, nodes.py:395-441): a fusion of two unit calls into one, with the second call's exact
+ * result. */
+int cm_conv_act(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
+                uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
+                uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
+                uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
+                uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise, uint32_t y_cs,
+                uint32_t y_cn, uint32_t y_gs, uint32_t wrap32, uint32_t act, void* stream);
+int cm_conv_planes_act(const int16_t* x, const void* w_planes, const int16_t* bias, int16_t* y,
+                       uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
+                       uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
+                       uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
+                       uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise, uint32_t y_cs,
+                       uint32_t y_cn, uint32_t y_gs, uint32_t wrap32, uint32_t act, void* stream);
+
 /* ---------------------------------------------------------------- Pooling
  * Replaces PoolingKernel (kernels/pool_rtl/model/include/PoolingKernel.h:120-140) and the
  * simulator's pool reference (_simulate.py:230-358, 701-719): pool_type 0 MAX, 1 AVG
