@@ -780,6 +780,7 @@ int run_job(DeviceState* st, const Job& j, const uint8_t* p, hipStream_t s) {
     if (code == RO_FOLD) {
         const uint32_t m = (j.aux >> 4) & 127;
         if (j.n == 0 || j.c1 == 0 || j.c2 == 0 || m == 0) return CM_OK;
+        if (j.c == nullptr) return fail(CM_EINVAL, "rowops FOLD: a null output");
         if (reinterpret_cast<uintptr_t>(j.c) & 15) return fail(CM_EALIGN, "rowops FOLD: c not 16-byte aligned");
         const u64 total = ((u64)j.c2 * j.c1 * j.n + 7) & ~7ull;
         CM_LAUNCH("ro_fold_kernel", ro_fold_kernel, dim3(grid_for(total)), dim3(256), 0, s, j);
@@ -790,6 +791,7 @@ int run_job(DeviceState* st, const Job& j, const uint8_t* p, hipStream_t s) {
     if (code == RO_XPOSE) {
         const uint32_t R = j.aux & 15;
         if (R == 0 || R > 8) return CM_OK;        // outside the contract: the unit writes nothing
+        if (j.c == nullptr) return fail(CM_EINVAL, "rowops TRANSPOSE: a null output");
         CM_LAUNCH("ro_xpose_kernel", ro_xpose_kernel, dim3(grid_for((u64)j.n * R * j.c1 * j.c2)), dim3(256), 0, s, j);
         return CM_OK;
     }
@@ -798,6 +800,9 @@ int run_job(DeviceState* st, const Job& j, const uint8_t* p, hipStream_t s) {
         const uint32_t HD = j.aux & 0xFFF;
         if (HD == 0 || (HD & 15) || HD > 128 || j.n % HD) return CM_OK;   // the unit writes nothing
     }
+    // every job here writes c: a null output is refused (only cm_rowops_chain_planes' last NORM,
+    // whose rows its planes replace, may have none, and that job does not come through here)
+    if (j.c == nullptr) return fail(CM_EINVAL, "rowops: a null output");
     if ((reinterpret_cast<uintptr_t>(j.c) & 15) || (j.c_s1 & 15) || (j.c_s2 & 15))
         return fail(CM_EALIGN, "rowops: c and its strides must be 16-byte aligned");
     // parameter RAM: a load (unless P_KEEP finds a valid RAM) or the RAM as the last load left it

@@ -173,6 +173,37 @@ def test_addx_norm_one_launch(U, rows, n, a32, planes_on):
             U.rowops_jobs([_job(add, h, d, h1, pa), jn2])
 
 
+def test_null_outputs_refused_at_the_c_abi(U):
+    """cm_rowops and cm_rowops_chain called directly (no Python checks in between): a job with
+    work and a null c is CM_EINVAL for NORM, COPY, ADDX and TRANSPOSE, alone and in a chain
+    without planes; nothing is launched for it."""
+    import ctypes
+    from cormorant_amd import _lib
+    lib = _lib.lib()
+    n, rows = 64, 4
+    a = torch.zeros(rows * n, dtype=torch.int32, device="cuda")
+    b = torch.zeros(rows * n, dtype=torch.int16, device="cuda")
+    p = torch.zeros(16, dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    for code, bk in ((U.RO_NORM, None), (U.RO_COPY, None), (U.RO_ADDX, U.K_I16)):
+        op = code | (U.K_I32 << 4) | ((bk or 0) << 6) | U.F_P_BCAST | (U.F_B_EN if bk is not None else 0)
+        if code == U.RO_ADDX:
+            op |= U.K_I32 << 8
+        rc = lib.cm_rowops(a.data_ptr(), b.data_ptr() if bk is not None else None, None, p.data_ptr(), op, n, rows,
+                           1, 4 * n, 0, 2 * n, 0, 4 * n, 0, 1 << 20, 0, 0, 0, 0xFFFFFFFF, stream)
+        assert rc < 0, (code, rc)
+        assert "null output" in lib.cm_last_error().decode()
+        desc = _lib.CmRowopsDesc(a=a.data_ptr(), b=b.data_ptr() if bk is not None else 0, c=0, p=p.data_ptr(), op=op,
+                            n=n, c1=rows, c2=1, a_s1=4 * n, b_s1=2 * n, c_s1=4 * n, eps=1 << 20, win_hi=0xFFFFFFFF)
+        rc = lib.cm_rowops_chain(ctypes.byref(desc), 1, stream)
+        assert rc < 0, (code, rc)
+    xop = U.RO_XPOSE
+    rc = lib.cm_rowops(b.data_ptr(), None, None, None, xop, 16, 1, 1, 2 * 64, 0, 0, 0, 2 * 16, 0, 0, 8, 0, 0,
+                       0xFFFFFFFF, stream)
+    assert rc < 0
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("rows,k,act,arity", [(300, 3072, 5, 2), (96, 1088, 0, 2), (130, 640, 2, 1)])
 def test_vectorop_planes(U, rows, k, act, arity):
     """A VectorOP over rows of k (ADD of a broadcast bias row with GELU / no act; RELU6 alone):

@@ -844,3 +844,54 @@ def test_table_init_round_trip(U, oracle_lib):
         U.act_table_init(full)
         U.rowops_tables_init(img)
     np.testing.assert_array_equal(silu(x), before)
+
+
+def test_rowops_table_entry_reaches_norm(U, monkeypatch):
+    """A changed rsqrt entry installed by cm_rowops_tables_init shows in a NORM's output: RMSNorm
+    rows whose D falls on the changed entry take it (exactly the reference algorithm with that
+    table: oracle/sim_ref.rms_norm over the patched table), the other rows do not change, and the
+    library's own image restores the results."""
+    from oracle import rowops_adapt as ra
+    from oracle import sim_ref
+    rng = np.random.default_rng(44)
+    n, rows, f_h, f_out = 64, 12, 15, 11
+    h = rng.integers(-2 ** 20, 2 ** 20, (rows, n)).astype(np.int64)
+    gamma = 1.0 + 0.05 * rng.standard_normal(n)
+    G, g, _b, E = ra.norm_params(gamma, n, 1e-5, f_h, rms=True)
+
+    def index(D):
+        d = D.bit_length() - 32
+        d += d & 1
+        return (D >> d if d >= 0 else D << -d) >> 19
+
+    idx = [index(int((h[r] * h[r]).sum()) + E) for r in range(rows)]
+    target = idx[0]
+    img = U.host_rowops_table_image()
+    changed = img.copy()
+    words = changed[32768:].view(np.uint32)
+    words[target] = words[target] - (1 << 26)      # a 1.5 % error in the Newton step's start
+    table = sim_ref._rsqrt_table()
+    patched = list(table)
+    patched[target] = int(words[target])
+    op = U.RO_NORM | (U.K_I32 << 4) | (U.K_I16 << 8)
+    p = dev8(ra._params(n, G, 0, 0, 0, ra.P1_BITS + g - f_out))
+
+    def norm_rows():
+        c = dev8(np.full(rows * n * 2, 0xDE, np.uint8))
+        U.rowops(dev8(h.astype(np.int32).view(np.uint8).reshape(-1)), None, c, p, op, n, rows, 1, 4 * n, 0, 0, 0,
+                 2 * n, 0, E, 0, 0)
+        return host(c).view(np.int16).reshape(rows, n).astype(np.int64)
+
+    want_default = sim_ref.rms_norm(h, f_h, gamma, 1e-5, f_out)
+    monkeypatch.setattr(sim_ref, "_rsqrt_table", lambda: patched)
+    want_changed = sim_ref.rms_norm(h, f_h, gamma, 1e-5, f_out)
+    monkeypatch.undo()
+    hit = np.array([i == target for i in idx])
+    assert (want_changed[hit] != want_default[hit]).any() and (want_changed[~hit] == want_default[~hit]).all()
+    np.testing.assert_array_equal(norm_rows(), want_default)
+    try:
+        U.rowops_tables_init(changed)
+        np.testing.assert_array_equal(norm_rows(), want_changed)
+    finally:
+        U.rowops_tables_init(img)
+    np.testing.assert_array_equal(norm_rows(), want_default)
