@@ -14,7 +14,7 @@ from typing import Dict, Iterable, Optional
 import numpy as np
 import torch
 
-from . import units
+from . import residuals, units
 from .dtype import AP_FIXED_16_8, ApFixed16
 from .graph import (AttentionNode, AttnContractNode, ConvNode, DecodeAttentionNode, Graph, KvWriteNode, LlmAttnConvNode,
                     MatmulConvNode,
@@ -85,6 +85,7 @@ class Simulator:
         self._plan = None                                  # MatMuls fed byte planes by their A's producer
         self._keep = None                                  # forward_raw's keep (None: every tensor)
         self._planes_only_names = None                     # tensors only plane-path MatMuls read
+        self._errors = None                                # residual statistics being collected
         for t in graph.input_tensors + graph.output_tensors:
             self._infos[t.onnx_name] = t
         # the fused launches that apply a row-ops job inside another unit leave the device's
@@ -120,10 +121,9 @@ class Simulator:
         nodes update them in place on the device and the caller's arrays receive the new values,
         so a caller can run several passes over the same states (_simulate.py:573-577,
         609-611).  Inputs may also carry a state's value (it then replaces the array's).
-        ``errors_out`` (the residual statistics of _simulate.py:77-118) is not computed on the
-        GPU: passing one raises NotImplementedError."""
-        if errors_out is not None:
-            raise NotImplementedError("residual statistics (errors_out) are not computed by the GPU simulator")
+        ``errors_out`` (a dict) receives {output name: ResidualStats} of every MatMul, Conv
+        without exponents, Pool and VectorOP node (_simulate.py:594-602): each node then runs
+        in its own launch, so that its output exists to compare."""
         st_names = [t.onnx_name for t in self._graph.state_tensors]
         if states is None:
             states = self.initial_states()
@@ -132,7 +132,11 @@ class Simulator:
             raise KeyError(f"states {missing} have no value")
         feeds = {nm: self._to_device(self._tensor(nm), states[nm]) for nm in st_names if nm not in input_arrays}
         feeds.update({name: self._to_device(self._tensor(name), v) for name, v in input_arrays.items()})
-        raw = self.forward_raw(feeds, keep=None if keep is None else set(keep) | set(st_names))
+        self._errors = errors_out
+        try:
+            raw = self.forward_raw(feeds, keep=None if keep is None else set(keep) | set(st_names))
+        finally:
+            self._errors = None
         for nm in st_names:                      # the states as the pass left them, in place
             if nm in states:
                 states[nm][...] = self._to_values(self._tensor(nm), feeds[nm]).reshape(np.shape(states[nm]))
@@ -149,10 +153,15 @@ class Simulator:
         self._keep = None if keep is None else set(keep)
         raw: Dict[str, torch.Tensor] = dict(raw_inputs)
         nodes = self._graph.nodes
+        fuse = self._errors is None                 # residual statistics read every node's own output
         i = 0
         while i < len(nodes):
             sn = nodes[i]
             i += 1
+            if not fuse:
+                self._dispatch(sn, raw)
+                self._record_residuals(sn, raw)
+                continue
             if self._skinny_single(sn):
                 # the skinny MatMuls that follow on the same A: one launch for up to 4
                 group = [sn]
@@ -191,47 +200,51 @@ class Simulator:
                 self._prep_attention(sn, nodes[i], raw)
                 i += 1
                 continue
-            if isinstance(sn, MatmulNode):
-                raw[sn.output.onnx_name] = self._matmul(sn, raw)
-            elif isinstance(sn, LlmEmbedNode):
-                raw[sn.output.onnx_name] = self._embed(sn, raw)
-            elif isinstance(sn, HostNode):
-                raw[sn.output.onnx_name] = self._host_node(sn, raw)
-            elif isinstance(sn, MatmulConvNode):
-                raw[sn.output.onnx_name] = self._matmul_conv(sn, raw)
-            elif isinstance(sn, ConvNode):
-                raw[sn.output.onnx_name] = self._conv(sn, raw)
-            elif isinstance(sn, ReshapeNode):
-                raw[sn.output.onnx_name] = self._get(sn.inputs[0], raw)
-            elif isinstance(sn, PoolNode):
-                raw[sn.output.onnx_name] = self._pool(sn, raw)
-            elif isinstance(sn, SoftmaxVopNode):
-                raw[sn.output.onnx_name] = self._softmax(sn, raw)
-            elif isinstance(sn, RowOpsNode):
-                raw[sn.output.onnx_name] = self._rowops(sn, raw)
-            elif isinstance(sn, RowOpsAdapter):
-                raw[sn.output.onnx_name] = self._adapter(sn, raw)
-            elif isinstance(sn, RoCallNode):
-                raw[sn.output.onnx_name] = self._ro_calls(sn, raw)
-            elif isinstance(sn, LlmAttnConvNode):
-                raw[sn.output.onnx_name] = self._attn_conv(sn, raw)
-            elif isinstance(sn, PermuteNode):
-                raw[sn.output.onnx_name] = self._permute(sn, raw)
-            elif isinstance(sn, AttnContractNode):
-                raw[sn.output.onnx_name] = self._attn_contract(sn, raw)
-            elif isinstance(sn, KvWriteNode):
-                raw[sn.output.onnx_name] = self._kv_write(sn, raw)
-            elif isinstance(sn, DecodeAttentionNode):
-                raw[sn.output.onnx_name] = self._decode_attention(sn, raw)
-            elif isinstance(sn, DecodePrepNode):
-                raw[sn.output.onnx_name] = self._decode_prep(sn, raw)
-            elif isinstance(sn, AttentionNode):
-                raw[sn.output.onnx_name] = self._attention(sn, raw)
-            elif isinstance(sn, ScheduledNode):
-                raw[sn.output.onnx_name] = self._vectorop(sn, raw)
-            else:
-                raise SchedulerError(f"_forward_pass: unsupported node {type(sn).__name__}")
+            self._dispatch(sn, raw)
         return raw
+
+    def _dispatch(self, sn, raw: Dict[str, torch.Tensor]) -> None:
+        """Run one node on its unit, its output into ``raw``."""
+        if isinstance(sn, MatmulNode):
+            raw[sn.output.onnx_name] = self._matmul(sn, raw)
+        elif isinstance(sn, LlmEmbedNode):
+            raw[sn.output.onnx_name] = self._embed(sn, raw)
+        elif isinstance(sn, HostNode):
+            raw[sn.output.onnx_name] = self._host_node(sn, raw)
+        elif isinstance(sn, MatmulConvNode):
+            raw[sn.output.onnx_name] = self._matmul_conv(sn, raw)
+        elif isinstance(sn, ConvNode):
+            raw[sn.output.onnx_name] = self._conv(sn, raw)
+        elif isinstance(sn, ReshapeNode):
+            raw[sn.output.onnx_name] = self._get(sn.inputs[0], raw)
+        elif isinstance(sn, PoolNode):
+            raw[sn.output.onnx_name] = self._pool(sn, raw)
+        elif isinstance(sn, SoftmaxVopNode):
+            raw[sn.output.onnx_name] = self._softmax(sn, raw)
+        elif isinstance(sn, RowOpsNode):
+            raw[sn.output.onnx_name] = self._rowops(sn, raw)
+        elif isinstance(sn, RowOpsAdapter):
+            raw[sn.output.onnx_name] = self._adapter(sn, raw)
+        elif isinstance(sn, RoCallNode):
+            raw[sn.output.onnx_name] = self._ro_calls(sn, raw)
+        elif isinstance(sn, LlmAttnConvNode):
+            raw[sn.output.onnx_name] = self._attn_conv(sn, raw)
+        elif isinstance(sn, PermuteNode):
+            raw[sn.output.onnx_name] = self._permute(sn, raw)
+        elif isinstance(sn, AttnContractNode):
+            raw[sn.output.onnx_name] = self._attn_contract(sn, raw)
+        elif isinstance(sn, KvWriteNode):
+            raw[sn.output.onnx_name] = self._kv_write(sn, raw)
+        elif isinstance(sn, DecodeAttentionNode):
+            raw[sn.output.onnx_name] = self._decode_attention(sn, raw)
+        elif isinstance(sn, DecodePrepNode):
+            raw[sn.output.onnx_name] = self._decode_prep(sn, raw)
+        elif isinstance(sn, AttentionNode):
+            raw[sn.output.onnx_name] = self._attention(sn, raw)
+        elif isinstance(sn, ScheduledNode):
+            raw[sn.output.onnx_name] = self._vectorop(sn, raw)
+        else:
+            raise SchedulerError(f"_forward_pass: unsupported node {type(sn).__name__}")
 
     # ------------------------------------------------------------------ expected outputs on disk
     def _build_ramp_inputs(self) -> Dict[str, np.ndarray]:
@@ -263,6 +276,60 @@ class Simulator:
     def _simulate(self) -> Dict[str, np.ndarray]:
         """The forward pass with the ramp inputs (_simulate.py:506-525)."""
         return self._forward_pass(self._build_ramp_inputs())
+
+    def compute_quant_errors(self) -> Dict[str, "residuals.ResidualStats"]:
+        """{output name: ResidualStats(abs_max, nrmse, sqnr_db)} of every MatMul, Conv without
+        exponents, Pool and VectorOP node over the ramp inputs (_simulate.py:409-422)."""
+        errors: Dict[str, residuals.ResidualStats] = {}
+        self._forward_pass(self._build_ramp_inputs(), errors_out=errors)
+        return errors
+
+    # ------------------------------------------------------------------ residual statistics
+    def _dev_values(self, t: TensorInfo, r: torch.Tensor) -> torch.Tensor:
+        """float64 values of a raw device tensor, on the device, in the tensor's logical shape: a
+        weight with a rank-1 exponent at raw * 2^-wexp (the value the reference's forward pass
+        holds for it, _simulate.py:531-539), others at their own exponent(s)."""
+        v = r.to(torch.float64)
+        if t.kind == "f32":
+            return v.reshape(t.shape)
+        if t.group_layout is not None:
+            KV, HD = t.group_layout
+            v = v.reshape(KV, -1, HD).transpose(0, 1)
+        v = v.reshape(t.shape)
+        e = np.asarray(t.wexp, np.float64) if t.wexp is not None else np.asarray(self._exp_b(t), np.float64)
+        return v * torch.as_tensor(np.power(2.0, -e), dtype=torch.float64, device=self.device)
+
+    def _record_residuals(self, sn, raw: Dict[str, torch.Tensor]) -> None:
+        """The node's ResidualStats into the collected statistics (_simulate.py:594-602, 620-765,
+        814-835): its full-precision result in float64 on the device against the value its unit
+        wrote.  Conv with exponents, reshapes, host and row-ops nodes record none, as in the
+        reference."""
+        ot = sn.output
+        if isinstance(sn, (MatmulNode, MatmulConvNode)):
+            at, bt = sn.inputs[0], sn.inputs[1]
+            full = torch.matmul(self._dev_values(at, self._get(at, raw)), self._dev_values(bt, self._get(bt, raw)))
+        elif isinstance(sn, ConvNode):
+            if any(t is not None and (t.exp is not None or t.wexp is not None or t.chexp is not None)
+                   for t in (sn.inputs[0], sn.inputs[1], ot)):
+                return
+            x = self._dev_values(sn.inputs[0], self._get(sn.inputs[0], raw))
+            w = self._dev_values(sn.inputs[1], self._get(sn.inputs[1], raw))
+            bias = self._dev_values(sn.inputs[2], self._get(sn.inputs[2], raw)) if sn.has_bias else None
+            full = residuals.conv_full(x, w, bias, sn.stride_h, sn.stride_w, sn.pad_top, sn.pad_left, sn.dilation_h,
+                                       sn.dilation_w, sn.out_h, sn.out_w, sn.is_depthwise)
+        elif isinstance(sn, PoolNode):
+            x = self._dev_values(sn.inputs[0], self._get(sn.inputs[0], raw))
+            full = residuals.pool_full(x, sn.pool_h, sn.pool_w, sn.stride_h, sn.stride_w, sn.pad_top, sn.pad_left,
+                                       sn.dil_h, sn.dil_w, int(ot.shape[2]), int(ot.shape[3]), sn.pool_type,
+                                       sn.lp_order, sn.count_include_pad)
+        elif type(sn) is ScheduledNode:
+            a = self._dev_values(sn.inputs[0], self._get(sn.inputs[0], raw))
+            b = self._dev_values(sn.inputs[1], self._get(sn.inputs[1], raw)) if sn.arity == 2 else None
+            full, _ = residuals.vectorop_full(sn.op_code, sn.act, sn.alpha, a, b)
+        else:
+            return
+        quant = self._dev_values(ot, raw[ot.onnx_name][:ot.numel])
+        self._errors[ot.onnx_name] = residuals.residual_stats(full.reshape(ot.shape), quant)
 
     def _expected_storage(self, name: str, logical: np.ndarray) -> np.ndarray:
         """A tensor's values as the buffer lanes the board writes (_simulate.py:841-891): float32

@@ -103,22 +103,26 @@ _LIBM = {name: np.vectorize(getattr(math, name), otypes=[np.float64]) for name i
 ACT_LEAKY, ACT_SILU, ACT_GELU, ACT_GELU_TANH = 3, 4, 5, 6
 
 
+def act_values(act: int, x, alpha: int = 0):
+    """The activation unit's unrounded double result of the values x, libm per element
+    (vectorop_act.py:60-73)."""
+    x = np.asarray(x, np.float64)
+    if act == ACT_LEAKY:
+        return np.where(x >= 0.0, x, x * ((alpha & 0xFFFF) / 65536.0))
+    if act == ACT_SILU:
+        return x / (1.0 + _LIBM["exp"](-x))
+    if act == ACT_GELU:
+        return x * (0.5 * (1.0 + _LIBM["erf"](x / math.sqrt(2.0))))
+    if act == ACT_GELU_TANH:
+        return x * (0.5 * (1.0 + _LIBM["tanh"](math.sqrt(2.0 / math.pi) * (x + 0.044715 * (x * x * x)))))
+    raise ValueError(f"act {act} is not one of the activation unit's")
+
+
 def act_unit(act: int, x_raw, alpha: int = 0):
     """The activation unit on Q8.8 raws: the double activation of x = raw / 2^8 with libm per
     element, then rounded half to even at 2^-8 and saturated (NaN to 0)."""
-    x = np.asarray(x_raw, np.float64) / 256.0
-    if act == ACT_LEAKY:
-        v = np.where(x >= 0.0, x, x * ((alpha & 0xFFFF) / 65536.0))
-    elif act == ACT_SILU:
-        v = x / (1.0 + _LIBM["exp"](-x))
-    elif act == ACT_GELU:
-        v = x * (0.5 * (1.0 + _LIBM["erf"](x / math.sqrt(2.0))))
-    elif act == ACT_GELU_TANH:
-        v = x * (0.5 * (1.0 + _LIBM["tanh"](math.sqrt(2.0 / math.pi) * (x + 0.044715 * (x * x * x)))))
-    else:
-        raise ValueError(f"act {act} is not one of the activation unit's")
-    v = np.nan_to_num(v, nan=0.0)
+    v = np.nan_to_num(act_values(act, np.asarray(x_raw, np.float64) / 256.0, alpha), nan=0.0)
     return np.round(np.clip(v, -128.0, 127.99609375) * 256.0).astype(np.int64)
 
 
-__all__ = ["layer_norm", "rms_norm", "act_unit", "beta_bits"]
+__all__ = ["layer_norm", "rms_norm", "act_values", "act_unit", "beta_bits"]
