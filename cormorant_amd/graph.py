@@ -407,6 +407,103 @@ class LlmAttnConvNode(KernelNode):
         return self.H // self.KV
 
 
+SMX_MAX_KEYS = 1024        # the softmax unit's column mode: keys per query column (vectorop_smx.py:34)
+
+
+@dataclass
+class AttnSoftmaxNode(KernelNode):
+    """The prefill attention's softmax of KV group ``group`` on the softmax unit (LlmAttnSoftmax
+    under the vsmx policy, smx_nodes.py:284-338): scores s_g [C][G T] (raw, keys-major, rows j <
+    keys valid) -> P_g [G T][C] (raw at cfg's f_p), keys = roundup(pos + n, Q) (attn_keys).
+    Column h' T + t (head h' of the group, query row t) is the unit's column-mode softmax over
+    the keys j < min(keys, pos + 1 + t) (``causal``: the mask register valid0 = pos + 1 with
+    period T) or j < max(min(keys, pos + n), 1) (not causal: an encoder's valid frames); P is 0
+    at j >= keys.  ``cm`` / ``cfg``: the registers of softmax_regs, one pair for the group or one
+    per head.  inputs [s_g, pos (host), n (host, optional: n = T)]."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    T: int = 16
+    G: int = 1
+    C: int = 16
+    Q: int = KEY_QUANTUM
+    group: int = 0
+    cm: object = 12102203
+    cfg: object = 0x0813
+    causal: bool = True
+
+    def __post_init__(self):
+        what = f"attention softmax '{self.output.onnx_name}'"
+        if len(self.inputs) not in (2, 3):
+            raise SchedulerError(f"{what}: inputs scores, pos, [n]")
+        s, pos = self.inputs[0], self.inputs[1]
+        GT = self.G * self.T
+        if list(s.shape) != [self.C, GT] or list(self.output.shape) != [GT, self.C]:
+            raise SchedulerError(f"{what}: scores [{self.C}][{GT}] -> P [{GT}][{self.C}]")
+        if self.T % 16 or self.C % self.Q or self.Q % KEY_QUANTUM or not 0 < self.C <= SMX_MAX_KEYS:
+            raise SchedulerError(f"{what}: query rows a multiple of 16, cache rows a multiple of the key "
+                                 f"quantum and at most {SMX_MAX_KEYS}")
+        if pos.kind != "host" or (self.has_n and self.inputs[2].kind != "host"):
+            raise SchedulerError(f"{what}: pos / n are host tensors")
+        if any(np.asarray(r).size not in (1, self.G) for r in (self.cm, self.cfg)):
+            raise SchedulerError(f"{what}: cm / cfg one pair, or one per head of the group")
+
+    @property
+    def has_n(self) -> bool:
+        return len(self.inputs) == 3
+
+    def regs(self) -> List[Tuple[int, int]]:
+        """(cm, cfg) of each head of the group."""
+        cm = np.broadcast_to(np.asarray(self.cm, np.int64).reshape(-1), (self.G,))
+        cfg = np.broadcast_to(np.asarray(self.cfg, np.int64).reshape(-1), (self.G,))
+        return [(int(a), int(b)) for a, b in zip(cm, cfg)]
+
+    def mask_reg(self, pos: int, n: int, keys: int) -> int:
+        """The softmax unit's mask register for this call: valid0 | period << 16."""
+        if self.causal:
+            return (int(pos) + 1) | (self.T << 16)
+        return max(min(keys, int(pos) + int(n)), 1)
+
+
+@dataclass
+class AttnMergeNode(KernelNode):
+    """LlmAttnMerge (llm_nodes.py:1560-1600, reference() :1660-1675): the P.V outputs o_g
+    [G T][HD] of the KV groups, in group order, into pv [T][H HD] in head order,
+    pv[t][(g G + h') HD + d] = o_g[h' T + t][d]; raw values move unchanged (pv's exponent is
+    f_p + f_v - 8)."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    T: int = 1
+    H: int = 1
+    KV: int = 1
+    HD: int = 16
+
+    def __post_init__(self):
+        G = self.H // self.KV
+        if len(self.inputs) != self.KV or any(t.numel != G * self.T * self.HD for t in self.inputs) \
+                or self.output.numel != self.T * self.H * self.HD:
+            raise SchedulerError(f"attention merge '{self.output.onnx_name}': {self.KV} inputs "
+                                 f"[{G * self.T}][{self.HD}] -> [{self.T}][{self.H * self.HD}]")
+
+
+@dataclass
+class SelectRowNode(KernelNode):
+    """LlmSelectRow (llm_nodes.py:1681-1718): y = h[n - 1] with n clamped to [1, rows], the last
+    valid row of a padded prefill, written into its output (a state the head entry reads).
+    inputs [h [rows][width], n (host)]; the output one row of h's kind and exponent."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+
+    def __post_init__(self):
+        h = self.inputs[0]
+        if len(self.inputs) != 2 or self.inputs[1].kind != "host" or self.output.kind != h.kind \
+                or self.output.numel != int(h.shape[-1]):
+            raise SchedulerError(f"select row '{self.output.onnx_name}': inputs h, n (host); one row of h out")
+
+    @property
+    def rows(self) -> int:
+        return self.inputs[0].numel // int(self.inputs[0].shape[-1])
+
+
 @dataclass(frozen=True)
 class HeadView:
     """Per-head blocks of a token-major tensor [batch seq][ld] as the slices [batch heads][seq]
@@ -545,7 +642,7 @@ def conv_out(size: int, k: int, stride: int, pad_lo: int, pad_hi: int, dil: int 
 
 __all__ = ["SchedulerError", "KernelNode", "TensorInfo", "HeadView", "ScheduledNode", "MatmulNode", "MatmulConvNode", "ConvNode", "PoolNode",
            "ReshapeNode", "SoftmaxVopNode", "DecodeAttentionNode", "RowOpsNode", "LlmAttnConvNode", "KvWriteNode", "AttentionNode", "attn_keys",
-           "KEY_QUANTUM",
+           "AttnSoftmaxNode", "AttnMergeNode", "SelectRowNode", "KEY_QUANTUM", "SMX_MAX_KEYS",
            "Graph", "conv_out", "OP_ADD", "OP_SUB",
            "OP_MUL", "OP_DIV", "OP_RELU", "OP_RELU6", "OP_SOFTMAX", "OP_SOFTMAX_T", "POOL_MAX",
            "POOL_AVG", "POOL_LP"]

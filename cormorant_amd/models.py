@@ -736,6 +736,124 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
     encode_matmul_weights(g.nodes, AP_FIXED_16_8)
     return g, inputs, exps
 
+def smollm2_prefill(shape: LlamaShape, T: int, exps, weights, with_head: bool = False):
+    """The prefill_T entry of one sequence (llama.py:28-33; the layers :404-450 with the FPGA
+    prefill attention :329-402; the entry :465-497): ids [T] (int32), pos and n (host) -> every
+    layer's KV cache rows pos .. pos + n - 1 written in place, and the state ``h_last`` = the
+    residual's row n - 1 after the last layer (LlmSelectRow).  Rows t >= n are computed but
+    write nothing the caches or h_last keep.  ``with_head``: also that row's float32 logits
+    (the prefill_T_logits entry).
+
+    The numerics and weights are the decode step's (``exps`` and ``weights`` as smollm2_decode
+    returns and takes them), and the caches are the decode graph's, one sequence of them: the
+    states ``l<i>.kc`` / ``l<i>.vc`` hold logical [C][KV HD] stored group-major [KV][C][HD],
+    byte for byte sequence b's slice of the decode graph's [B][KV][C][HD] caches (prefill_cache
+    / decode_cache convert the float64 values).  A layer: RMSNorm; the q / k / v MatMuls; the
+    attention prep on the row-ops unit (AttnPrepRoNode: RoPE of q / k at positions pos + t, the
+    q.K^T image, the cache rows); per KV group q.K^T (LlmAttnConvNode) over keys = roundup(pos
+    + n, 16), the causal column-mode softmax (AttnSoftmaxNode) and P.V; the merge; the o MatMul,
+    ResAdd, RMSNorm, gate / up, SiluMul, down, ResAdd.  T a multiple of 16, ctx at most 1024
+    (the softmax unit's column mode)."""
+    from .dtype import AP_FIXED_16_8
+    from .graph import AttnMergeNode, AttnSoftmaxNode, LlmAttnConvNode, SelectRowNode, SMX_MAX_KEYS
+    from .numeric import encode_matmul_weights
+    from .rowops_nodes import AttnPrepRoNode, DequantRoNode, RMSNormRoNode, ResAddRoNode, SiluMulRoNode
+
+    S = shape
+    if T % 16 or S.ctx % 16 or S.ctx > SMX_MAX_KEYS or S.heads % S.kv or S.hd % 16:
+        raise ValueError(f"prefill: T a multiple of 16, ctx a multiple of 16 up to {SMX_MAX_KEYS}, heads a multiple "
+                         "of the KV heads, head_dim a multiple of 16")
+    D, H, KV, HD, G, C = S.d, S.heads, S.kv, S.hd, S.group, S.ctx
+    A, KD = H * HD, KV * HD
+    emb, Ls, gf = weights
+    cos, sin = rope_half_tables(S.theta, HD, C)
+    T_ = TensorInfo
+    ids_t = T_("ids", [T], exp=0, kind="i32")
+    pos_t = T_("pos", [1], kind="host")
+    n_t = T_("n", [1], kind="host")
+    h0 = T_("h0", [T, D], exp=RES_BITS, kind="i32")
+    nodes = [LlmEmbedNode([ids_t], h0, table=emb)]
+    hcur = h0
+    for li, (L, e) in enumerate(zip(Ls, exps)):
+        p = f"l{li}."
+        kc_t = T_(p + "kc", [C, KD], exp=e["k"], group_layout=(KV, HD), state=True)
+        vc_t = T_(p + "vc", [C, KD], exp=e["v"], group_layout=(KV, HD), state=True)
+        x = T_(p + "x", [T, D], exp=e["x"])
+        nodes.append(RMSNormRoNode([hcur], x, gamma=L["g1"], eps=S.eps))
+        q0 = T_(p + "q", [T, A], exp=e["q"])
+        nodes.append(MatmulNode([x, T_(p + "wq", [D, A], data=L["wq"])], q0))
+        k0 = T_(p + "k", [T, KD], exp=e["k"])
+        nodes.append(MatmulNode([x, T_(p + "wk", [D, KD], data=L["wk"])], k0))
+        v = T_(p + "v", [T, KD], exp=e["v"])
+        nodes.append(MatmulNode([x, T_(p + "wv", [D, KD], data=L["wv"])], v))
+        qx = T_(p + "qx", [KV, HD, G * T], exp=0)
+        nodes.append(AttnPrepRoNode([q0, k0, v, pos_t, n_t, kc_t, vc_t], qx, heads=H, kv_heads=KV, head_dim=HD,
+                                    fq=np.full(H, e["q"]), cos=cos, sin=sin))
+        cmr, cfg = softmax_regs(e["s"], 1.0 / math.sqrt(HD), e["p"])
+        geo = dict(T=T, H=H, KV=KV, HD=HD, C=C)
+        outs = []
+        for grp in range(KV):
+            s = T_(p + f"s{grp}", [C, G * T], exp=0)
+            nodes.append(LlmAttnConvNode([kc_t, qx, pos_t, n_t], s, kind="qk", group=grp, **geo))
+            pg = T_(p + f"p{grp}", [G * T, C], exp=0)
+            nodes.append(AttnSoftmaxNode([s, pos_t, n_t], pg, T=T, G=G, C=C, group=grp, cm=cmr, cfg=cfg))
+            og = T_(p + f"o{grp}", [G * T, HD], exp=0)
+            nodes.append(LlmAttnConvNode([pg, vc_t, pos_t, n_t], og, kind="pv", group=grp, **geo))
+            outs.append(og)
+        om = T_(p + "om", [T, A], exp=e["o"])
+        nodes.append(AttnMergeNode(outs, om, T=T, H=H, KV=KV, HD=HD))
+        a = T_(p + "a", [T, D], exp=e["a"])
+        nodes.append(MatmulNode([om, T_(p + "wo", [A, D], data=L["wo"])], a))
+        h1 = T_(p + "h1", [T, D], exp=RES_BITS, kind="i32")
+        nodes.append(ResAddRoNode([hcur, a], h1))
+        x2 = T_(p + "x2", [T, D], exp=e["x2"])
+        nodes.append(RMSNormRoNode([h1], x2, gamma=L["g2"], eps=S.eps))
+        gt = T_(p + "g", [T, S.ff], exp=e["g"])
+        nodes.append(MatmulNode([x2, T_(p + "wg", [D, S.ff], data=L["wg"])], gt))
+        up = T_(p + "u", [T, S.ff], exp=e["u"])
+        nodes.append(MatmulNode([x2, T_(p + "wu", [D, S.ff], data=L["wu"])], up))
+        mm = T_(p + "m", [T, S.ff], exp=e["m"])
+        nodes.append(SiluMulRoNode([gt, up], mm))
+        dd = T_(p + "d", [T, D], exp=e["d"])
+        nodes.append(MatmulNode([mm, T_(p + "wd", [S.ff, D], data=L["wd"])], dd))
+        hn = T_(p + "h", [T, D], exp=RES_BITS, kind="i32")
+        nodes.append(ResAddRoNode([h1, dd], hn))
+        hcur = hn
+    h_last = T_("h_last", [1, D], exp=RES_BITS, kind="i32", state=True)
+    nodes.append(SelectRowNode([hcur, n_t], h_last))
+    outputs = [h_last]
+    if with_head:
+        fin = exps[-1]
+        xf = T_("xf", [1, D], exp=fin["xf"])
+        nodes.append(RMSNormRoNode([h_last], xf, gamma=gf, eps=S.eps))
+        lq = T_("logits_q", [1, S.vocab], exp=fin["logits"])
+        nodes.append(MatmulNode([xf, T_("w.lm_head", [D, S.vocab], data=np.ascontiguousarray(emb.T))], lq))
+        chunk = next(c for c in range(4096, 0, -8) if S.vocab % c == 0)
+        lr = T_("logits_rows", [S.vocab // chunk, chunk], exp=fin["logits"])
+        nodes.append(ReshapeNode([lq], lr))
+        lf = T_("logits_f32", [S.vocab // chunk, chunk], kind="f32")
+        nodes.append(DequantRoNode([lr], lf))
+        lo = T_("logits", [1, S.vocab], kind="f32")
+        nodes.append(ReshapeNode([lf], lo))
+        outputs.append(lo)
+    g = Graph(nodes, input_tensors=[ids_t, pos_t, n_t], output_tensors=outputs)
+    encode_matmul_weights(g.nodes, AP_FIXED_16_8)
+    return g
+
+
+def prefill_cache(decode_cache: np.ndarray, b: int) -> np.ndarray:
+    """Sequence b's rows of a decode graph's cache values [B][KV][C][HD] as the prefill entry's
+    logical [C][KV HD] (a copy)."""
+    _, KV, C, HD = decode_cache.shape
+    return np.ascontiguousarray(decode_cache[b].transpose(1, 0, 2)).reshape(C, KV * HD)
+
+
+def decode_cache(prefill_cache_values: np.ndarray, out: np.ndarray, b: int) -> None:
+    """The prefill entry's cache values [C][KV HD] into sequence b of a decode graph's [B][KV][C][HD]."""
+    _, KV, C, HD = out.shape
+    out[b] = np.asarray(prefill_cache_values).reshape(C, KV, HD).transpose(1, 0, 2)
+
+
 def _decode_attention_unfused(nodes, T_, p, e, qr, kc2, vc2, om, B, KV, G, HD, keys, ctx, cmr, cfg, pos, pos_t):
     """A decode layer's attention as the reference's nodes: per (sequence, group) the group's G
     query rows against the cache's K rows, the scores query-major s[b g][h'][j] (the unit's

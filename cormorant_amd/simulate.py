@@ -16,8 +16,8 @@ import torch
 
 from . import residuals, units
 from .dtype import AP_FIXED_16_8, ApFixed16
-from .graph import (AttentionNode, AttnContractNode, ConvNode, DecodeAttentionNode, Graph, KvWriteNode, LlmAttnConvNode,
-                    MatmulConvNode,
+from .graph import (AttentionNode, AttnContractNode, AttnMergeNode, AttnSoftmaxNode, ConvNode, DecodeAttentionNode, Graph,
+                    KvWriteNode, LlmAttnConvNode, MatmulConvNode, SelectRowNode,
                     MatmulNode, PermuteNode, PoolNode, ReshapeNode, RowOpsNode, ScheduledNode, SchedulerError, SoftmaxVopNode,
                     TensorInfo, attn_keys)
 from .packing import conv_bias_image, conv_lowered_b_image, conv_weight_image, pack_matmul_b
@@ -73,12 +73,16 @@ def _pad8(n: int) -> int:
 class Simulator:
     """Forward-simulates ``graph`` with the HIP units on ``device``."""
 
-    def __init__(self, graph: Graph, dtype: ApFixed16 = AP_FIXED_16_8, device: str = "cuda"):
+    def __init__(self, graph: Graph, dtype: ApFixed16 = AP_FIXED_16_8, device: str = "cuda",
+                 share: Optional["Simulator"] = None):
+        """``share``: another entry of the same model (a prefill and a decode graph over one set of
+        weights): its device copies of the weights and their packed images are used, not uploaded
+        again -- the entries of a reference project read the same initializers by name."""
         self._graph = graph
         self._dtype = dtype
         self.device = torch.device(device)
-        self._weights: Dict[str, torch.Tensor] = {}      # raw device copies of the weights
-        self._images: Dict[str, torch.Tensor] = {}       # packed weight images
+        self._weights: Dict[str, torch.Tensor] = {} if share is None else share._weights    # raw device weights
+        self._images: Dict[str, torch.Tensor] = {} if share is None else share._images      # packed weight images
         self._infos: Dict[str, TensorInfo] = {}
         self._params: Dict[int, list] = {}                # row-ops parameter blocks on the device
         self._staging: Dict[tuple, torch.Tensor] = {}     # row-ops nodes' staging buffers
@@ -229,6 +233,12 @@ class Simulator:
             raw[sn.output.onnx_name] = self._ro_calls(sn, raw)
         elif isinstance(sn, LlmAttnConvNode):
             raw[sn.output.onnx_name] = self._attn_conv(sn, raw)
+        elif isinstance(sn, AttnSoftmaxNode):
+            raw[sn.output.onnx_name] = self._attn_softmax(sn, raw)
+        elif isinstance(sn, AttnMergeNode):
+            raw[sn.output.onnx_name] = self._attn_merge(sn, raw)
+        elif isinstance(sn, SelectRowNode):
+            raw[sn.output.onnx_name] = self._select_row(sn, raw)
         elif isinstance(sn, PermuteNode):
             raw[sn.output.onnx_name] = self._permute(sn, raw)
         elif isinstance(sn, AttnContractNode):
@@ -1061,6 +1071,50 @@ class Simulator:
         vc = self._get(x, raw).reshape(sn.KV, C, HD)[g, :keys]
         out = torch.empty(GT * HD, dtype=torch.int16, device=self.device)
         units.matmul(p.reshape(-1), vc.reshape(-1), out, GT, keys, HD, wrap32=True)
+        return out
+
+    def _attn_softmax(self, sn: AttnSoftmaxNode, raw) -> torch.Tensor:
+        """The prefill softmax of one KV group over keys = roundup(pos + n, Q): one column-mode
+        call over the group's G T query columns (the mask's period T restarts the causal valid
+        length at each head), or one call per head where their registers differ; P is zero past
+        the keys."""
+        T, C = sn.T, sn.C
+        GT = sn.G * T
+        pos = self._host_int(sn.inputs[1], raw)
+        n, keys = attn_keys(pos, self._host_int(sn.inputs[2], raw) if sn.has_n else T, T, C, sn.Q)
+        s = self._get(sn.inputs[0], raw).reshape(-1)
+        out = torch.zeros(GT * C, dtype=torch.int16, device=self.device)
+        mask = sn.mask_reg(pos, n, keys)
+        regs = sn.regs()
+        if len(set(regs)) == 1:
+            units.softmax(s, out, keys, units.OP_SOFTMAX_T, GT, GT, C, regs[0][0], regs[0][1], mask)
+        else:
+            for h, (cm_h, cfg_h) in enumerate(regs):
+                units.softmax(s[h * T:], out[h * T * C:], keys, units.OP_SOFTMAX_T, T, GT, C, cm_h, cfg_h, mask)
+        return out
+
+    def _attn_merge(self, sn: AttnMergeNode, raw) -> torch.Tensor:
+        """Each group's P.V rows [G T][HD] copied into their heads' columns of pv [T][H HD]."""
+        T, H, HD = sn.T, sn.H, sn.HD
+        G = H // sn.KV
+        out = self._new(sn.output)
+        for g, t in enumerate(sn.inputs):
+            units.copy16(self._get(t, raw).reshape(-1), out[g * G * HD:], (1, G, T, HD), (0, T * HD, HD, 1),
+                         (0, HD, H * HD, 1))
+        return out
+
+    def _select_row(self, sn: SelectRowNode, raw) -> torch.Tensor:
+        """Row n - 1 of h (n clamped to 1 .. rows) into the output, in place where it is a state."""
+        h, ot = sn.inputs[0], sn.output
+        w = int(h.shape[-1])
+        r = min(max(self._host_int(sn.inputs[1], raw), 1), sn.rows) - 1
+        x = self._get(h, raw).reshape(-1)
+        out = raw.get(ot.onnx_name)
+        if out is None:
+            out = self._new(ot)
+        lanes = x.element_size() // 2                   # int16 lanes per element
+        units.copy16(x.view(torch.int16)[r * w * lanes:], out.reshape(-1).view(torch.int16), (1, 1, 1, w * lanes),
+                     (0, 0, 0, 1), (0, 0, 0, 1))
         return out
 
     def _attn_contract(self, sn: AttnContractNode, raw) -> torch.Tensor:

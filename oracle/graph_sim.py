@@ -381,6 +381,52 @@ def forward(graph, inputs, states=None, algo="port", errors_out=None):
                         o[b, :, h * hd:(h + 1) * hd] = _wrap_floor(p_.astype(np.float64) @ v)
             fo = float(F if out.exp is None else out.exp)
             vals[out.onnx_name] = (o.astype(np.float64) / 2.0 ** fo).reshape(out.shape)
+        elif kind == "AttnSoftmaxNode":
+            # LlmAttnSoftmaxVopNode.reference (smx_nodes.py:326-338): per head h', the column-mode
+            # softmax of s_g[:keys][h' T + t] with the valid lengths causal_valid(T, pos + 1, T,
+            # keys) (vectorop_smx.py:75-79); column mode is the row mode of the transpose
+            # (softmax_cols, :69-72): one row-mode call of the C oracle per column, its valid
+            # length as a period-0 mask
+            st = sn.inputs[0]
+            T, G, C = sn.T, sn.G, sn.C
+            pos = int(np.asarray(get(sn.inputs[1])).reshape(-1)[0])
+            n_in = int(np.asarray(get(sn.inputs[2])).reshape(-1)[0]) if len(sn.inputs) == 3 else T
+            n, keys = clamp_n(pos, n_in, T, C, sn.Q)
+            valid = (np.minimum(keys, pos + 1 + np.arange(T)) if sn.causal
+                     else np.full(T, max(min(keys, pos + n), 1)))
+            s_ = _raw_of(st, get(st)).reshape(C, G * T).astype(np.int16)
+            cms = np.broadcast_to(np.asarray(sn.cm).reshape(-1), (G,))
+            cfgs = np.broadcast_to(np.asarray(sn.cfg).reshape(-1), (G,))
+            k8 = (keys + 7) & ~7
+            P = np.zeros((G * T, C))
+            for h in range(G):
+                for t in range(T):
+                    col = np.ascontiguousarray(s_[:keys, h * T + t])
+                    P[h * T + t, :keys] = cm.vectorop(col, None, k8, keys, 10, 1, k8, k8, 0, 0, int(cms[h]),
+                                                      int(cfgs[h]), int(valid[t]))[:keys]
+            vals[out.onnx_name] = P.reshape(out.shape)
+        elif kind == "AttnMergeNode":
+            # LlmAttnMergeNode.reference (llm_nodes.py:1660-1675): pv[t][(g G + h') HD + d] = o_g[h' T + t][d]
+            T, H, KV, HD = sn.T, sn.H, sn.KV, sn.HD
+            G = H // KV
+            r = np.zeros((T, H, HD))
+            for g, t_ in enumerate(sn.inputs):
+                o_ = _raw_of(t_, get(t_)).reshape(G, T, HD)
+                for hh in range(G):
+                    r[:, g * G + hh, :] = o_[hh]
+            fo = np.asarray(F if out.exp is None else out.exp, np.float64)
+            vals[out.onnx_name] = (r.reshape(T, H * HD) / np.power(2.0, fo)).reshape(out.shape)
+        elif kind == "SelectRowNode":
+            # LlmSelectRowNode.reference (llm_nodes.py:1714-1718): row n - 1, n clamped to [1, rows]
+            ht = sn.inputs[0]
+            w = int(ht.shape[-1])
+            rows = ht.numel // w
+            r = min(max(int(np.asarray(get(sn.inputs[1])).reshape(-1)[0]), 1), rows) - 1
+            y = np.asarray(get(ht), np.float64).reshape(rows, w)[r].reshape(out.shape)
+            if out.onnx_name in vals and getattr(out, "state", False):
+                vals[out.onnx_name][...] = y.reshape(vals[out.onnx_name].shape)       # the state, in place
+            else:
+                vals[out.onnx_name] = y.copy()
         elif kind == "LlmEmbedNode":
             fo = F if out.exp is None else np.asarray(out.exp).reshape(-1)[0]
             vals[out.onnx_name] = host_ref.embed(get(sn.inputs[0]), sn.table, sn.scale, fo,
