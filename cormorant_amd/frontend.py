@@ -26,7 +26,9 @@ producing their inputs (``graph.fuse_activations``, graph.py:1005-1069).
 
 The custom-domain ops this build takes are the ones its node kinds cover: LlmEmbed,
 LlmRMSNorm, LlmResAdd, LlmSiluMul, LlmDequant, LlmToHost, LlmAttention (the host attention),
-VitLayerNorm, VitResAdd, VitGelu; and two ops of this build's own that stand for the
+VitLayerNorm, VitResAdd, VitGelu; the prefill attention chain on the units (LlmAttnPrep on the
+row-ops unit, LlmAttnScores / LlmAttnPV, LlmAttnSoftmax under the vsmx policy, LlmAttnMerge;
+llama.py:329-402) and LlmSelectRow; and two ops of this build's own that stand for the
 reference's attention chains, which it runs as one fused node each: ``VitAttention`` (VitAttnPrep,
 LlmAttnScores, VitAttnSoftmax on the unit, LlmAttnPV, LlmAttnMerge: vit.py:19-32 -> AttentionNode)
 and ``LlmDecodeAttention`` (LlmAttnPrep's RoPE and cache-row writes, the scores, LlmAttnSoftmax,
@@ -41,12 +43,12 @@ from typing import Any, Callable, Dict, List, Optional, Sequence
 import numpy as np
 
 from . import units
-from .graph import (AttentionNode, ConvNode, DecodeAttentionNode, Graph, MatmulNode, PoolNode, ReshapeNode,
-                    ScheduledNode, SchedulerError, SoftmaxVopNode, TensorInfo, conv_out, fuse_activations,
-                    softmax_regs)
+from .graph import (KEY_QUANTUM, AttentionNode, AttnMergeNode, AttnSoftmaxNode, ConvNode, DecodeAttentionNode, Graph,
+                    LlmAttnConvNode, MatmulNode, PoolNode, ReshapeNode, ScheduledNode, SchedulerError, SelectRowNode,
+                    SoftmaxVopNode, TensorInfo, conv_out, fuse_activations, softmax_regs)
 from .host_ops import (GeluNode, LayerNormNode, LlmAttentionNode, LlmDequantNode, LlmEmbedNode, LlmResAddNode,
                        LlmRMSNormNode, LlmSiluMulNode, LlmToHostNode, SoftmaxNode, TransposeNode)
-from .rowops_nodes import (N_MAX, P1_BITS, DecodePrepNode, DequantRoNode, LayerNorm32RoNode, LayerNormRoNode,
+from .rowops_nodes import (N_MAX, P1_BITS, AttnPrepRoNode, DecodePrepNode, DequantRoNode, LayerNorm32RoNode, LayerNormRoNode,
                            ResAddBiasRoNode, ResAddRoNode, RMSNormRoNode, SiluMulRoNode, TransposeRoNode, beta_bits,
                            collapse, gamma_scale, transpose_job)
 
@@ -470,11 +472,76 @@ def _llm_decode_attention(op, ctx):
     return [prep, att]
 
 
+def _heads(op):
+    a = op.attrs
+    H, KV, HD = int(a["num_heads"]), int(a["num_kv_heads"]), int(a["head_dim"])
+    return H, KV, HD, H // KV
+
+
+def _llm_attn_prep(op, ctx):
+    """LlmAttnPrep [q0, k0, v, pos, n, K cache, V cache] -> qx on the row-ops unit (the rowops
+    policy, rowops_nodes.py:1134-1219); the host prep is not built."""
+    _need_rowops(op, ctx, "the attention prep (the host LlmAttnPrep is not built)")
+    a = op.attrs
+    H, KV, HD, _ = _heads(op)
+    ins = [ctx.t(n, op) for n in op.inputs if n]
+    return AttnPrepRoNode(ins, ctx.out(op), heads=H, kv_heads=KV, head_dim=HD, fq=np.asarray(a["q_exp"], np.int64),
+                          cos=a["cos"], sin=a["sin"], key_quantum=int(a.get("key_quantum", KEY_QUANTUM)))
+
+
+def _llm_attn_conv(op, ctx):
+    """LlmAttnScores [K cache, qx, pos, n] -> s_g, LlmAttnPV [P_g, V cache, pos, n] -> o_g
+    (llm_nodes.py:1183-1425): one KV group's contraction on the conv unit over the runtime keys."""
+    H, KV, HD, G = _heads(op)
+    ins = [ctx.t(n, op) for n in op.inputs if n]
+    qk = op.op_type == "LlmAttnScores"
+    cache = ins[0] if qk else ins[1]
+    T = (ins[1].shape[-1] if qk else ins[0].shape[0]) // G
+    return LlmAttnConvNode(ins, ctx.out(op), kind="qk" if qk else "pv", group=int(op.attrs["group"]), T=int(T), H=H,
+                           KV=KV, HD=HD, C=int(cache.shape[0]), Q=int(op.attrs.get("key_quantum", KEY_QUANTUM)),
+                           has_n=len(ins) == 4)
+
+
+def _llm_attn_softmax(op, ctx):
+    """LlmAttnSoftmax [s_g, pos, n] -> P_g with vsmx = 1 on the softmax unit (smx_nodes.py:284-324);
+    the host p12 softmax is not built."""
+    a = op.attrs
+    if not (ctx.platform.softmax and int(a.get("vsmx", 0))):
+        raise SchedulerError(f"LlmAttnSoftmax node '{op.label}': runs on VectorOPKernel's softmax unit (vsmx = 1); "
+                             f"the host p12 softmax is not built")
+    if int(a.get("window", 0)):
+        raise SchedulerError(f"LlmAttnSoftmax node '{op.label}': a sliding window is the host softmax's (not built)")
+    H, KV, HD, G = _heads(op)
+    ins = [ctx.t(n, op) for n in op.inputs if n]
+    C, GT = (int(d) for d in ins[0].shape)
+    scale = float(a.get("logit_scale", 1.0 / np.sqrt(HD)))
+    fs = np.broadcast_to(np.asarray(a["s_exp"], np.int64).reshape(-1), (G,))
+    fp = np.broadcast_to(np.asarray(a["p_exp"], np.int64).reshape(-1), (G,))
+    regs = [softmax_regs(int(fs[h]), scale, int(fp[h])) for h in range(G)]
+    cm, cfg = (regs[0] if len(set(regs)) == 1 else ([r[0] for r in regs], [r[1] for r in regs]))
+    if int(a.get("causal", 1)) == 2:
+        raise SchedulerError(f"LlmAttnSoftmax node '{op.label}': the prefix-LM mask (causal 2) is not built")
+    return AttnSoftmaxNode(ins, ctx.out(op), T=GT // G, G=G, C=C, Q=int(a.get("key_quantum", KEY_QUANTUM)),
+                           group=int(a["group"]), cm=cm, cfg=cfg, causal=int(a.get("causal", 1)) == 1)
+
+
+def _llm_attn_merge(op, ctx):
+    H, KV, HD, G = _heads(op)
+    ins = ctx.ins(op)
+    return AttnMergeNode(ins, ctx.out(op), T=ins[0].numel // (G * HD), H=H, KV=KV, HD=HD)
+
+
+def _llm_select_row(op, ctx):
+    return SelectRowNode(ctx.ins(op)[:2], ctx.out(op))
+
+
 LLM_FACTORIES: Dict[str, Callable] = {
     "LlmEmbed": _llm_embed, "LlmRMSNorm": _llm_rmsnorm, "LlmResAdd": _llm_resadd, "LlmSiluMul": _llm_silu_mul,
     "LlmDequant": _llm_dequant, "LlmToHost": _llm_dequant, "LlmAttention": _llm_attention,
     "VitLayerNorm": _vit_layernorm, "VitResAdd": _llm_resadd, "VitGelu": _vit_gelu, "VitAttention": _vit_attention,
-    "LlmDecodeAttention": _llm_decode_attention,
+    "LlmDecodeAttention": _llm_decode_attention, "LlmAttnPrep": _llm_attn_prep, "LlmAttnScores": _llm_attn_conv,
+    "LlmAttnPV": _llm_attn_conv, "LlmAttnSoftmax": _llm_attn_softmax, "LlmAttnMerge": _llm_attn_merge,
+    "LlmSelectRow": _llm_select_row,
 }
 SUPPORTED = sorted(set(_VECTOROP) | set(ACT_OPS) | {"Softmax", "LayerNormalization", "Transpose", "MatMul", "Conv"}
                    | set(_POOLS) | RESHAPE_OPS)

@@ -736,7 +736,7 @@ def smollm2_decode(shape: LlamaShape = LlamaShape(), seed: int = 0, calib_seqs: 
     encode_matmul_weights(g.nodes, AP_FIXED_16_8)
     return g, inputs, exps
 
-def smollm2_prefill(shape: LlamaShape, T: int, exps, weights, with_head: bool = False):
+def smollm2_prefill(shape: LlamaShape, T: int, exps, weights, with_head: bool = False, as_ops: bool = False):
     """The prefill_T entry of one sequence (llama.py:28-33; the layers :404-450 with the FPGA
     prefill attention :329-402; the entry :465-497): ids [T] (int32), pos and n (host) -> every
     layer's KV cache rows pos .. pos + n - 1 written in place, and the state ``h_last`` = the
@@ -753,8 +753,13 @@ def smollm2_prefill(shape: LlamaShape, T: int, exps, weights, with_head: bool = 
     q.K^T image, the cache rows); per KV group q.K^T (LlmAttnConvNode) over keys = roundup(pos
     + n, 16), the causal column-mode softmax (AttnSoftmaxNode) and P.V; the merge; the o MatMul,
     ResAdd, RMSNorm, gate / up, SiluMul, down, ResAdd.  T a multiple of 16, ctx at most 1024
-    (the softmax unit's column mode)."""
+    (the softmax unit's column mode).
+
+    ``as_ops``: (ops, tensors, inputs, outputs) in place of the graph -- the entry as the
+    reference's LLM ops (LlmEmbed, LlmRMSNorm, MatMul, LlmAttnPrep, LlmAttnScores, LlmAttnSoftmax
+    with vsmx, LlmAttnPV, LlmAttnMerge, LlmResAdd, LlmSiluMul, LlmSelectRow) for the front end."""
     from .dtype import AP_FIXED_16_8
+    from .frontend import LLM_DOMAIN, OpDesc
     from .graph import AttnMergeNode, AttnSoftmaxNode, LlmAttnConvNode, SelectRowNode, SMX_MAX_KEYS
     from .numeric import encode_matmul_weights
     from .rowops_nodes import AttnPrepRoNode, DequantRoNode, RMSNormRoNode, ResAddRoNode, SiluMulRoNode
@@ -768,75 +773,94 @@ def smollm2_prefill(shape: LlamaShape, T: int, exps, weights, with_head: bool = 
     emb, Ls, gf = weights
     cos, sin = rope_half_tables(S.theta, HD, C)
     T_ = TensorInfo
+    nodes, ops, reg = [], [], {}
+
+    def add(node, kind, domain=LLM_DOMAIN, outs=None, **attrs):
+        nodes.append(node)
+        ins = [t for t in node.inputs if t is not None]
+        outs = [node.output] if outs is None else outs
+        for t in ins + outs:
+            reg[t.onnx_name] = t
+        ops.append(OpDesc(kind, [t.onnx_name for t in ins], [t.onnx_name for t in outs], attrs, domain))
+
     ids_t = T_("ids", [T], exp=0, kind="i32")
     pos_t = T_("pos", [1], kind="host")
     n_t = T_("n", [1], kind="host")
     h0 = T_("h0", [T, D], exp=RES_BITS, kind="i32")
-    nodes = [LlmEmbedNode([ids_t], h0, table=emb)]
+    add(LlmEmbedNode([ids_t], h0, table=emb), "LlmEmbed", table=emb)
     hcur = h0
+    heads = dict(num_heads=H, num_kv_heads=KV, head_dim=HD)
     for li, (L, e) in enumerate(zip(Ls, exps)):
         p = f"l{li}."
         kc_t = T_(p + "kc", [C, KD], exp=e["k"], group_layout=(KV, HD), state=True)
         vc_t = T_(p + "vc", [C, KD], exp=e["v"], group_layout=(KV, HD), state=True)
         x = T_(p + "x", [T, D], exp=e["x"])
-        nodes.append(RMSNormRoNode([hcur], x, gamma=L["g1"], eps=S.eps))
+        add(RMSNormRoNode([hcur], x, gamma=L["g1"], eps=S.eps), "LlmRMSNorm", gamma=L["g1"], eps=S.eps)
         q0 = T_(p + "q", [T, A], exp=e["q"])
-        nodes.append(MatmulNode([x, T_(p + "wq", [D, A], data=L["wq"])], q0))
+        add(MatmulNode([x, T_(p + "wq", [D, A], data=L["wq"])], q0), "MatMul", domain="")
         k0 = T_(p + "k", [T, KD], exp=e["k"])
-        nodes.append(MatmulNode([x, T_(p + "wk", [D, KD], data=L["wk"])], k0))
+        add(MatmulNode([x, T_(p + "wk", [D, KD], data=L["wk"])], k0), "MatMul", domain="")
         v = T_(p + "v", [T, KD], exp=e["v"])
-        nodes.append(MatmulNode([x, T_(p + "wv", [D, KD], data=L["wv"])], v))
+        add(MatmulNode([x, T_(p + "wv", [D, KD], data=L["wv"])], v), "MatMul", domain="")
         qx = T_(p + "qx", [KV, HD, G * T], exp=0)
-        nodes.append(AttnPrepRoNode([q0, k0, v, pos_t, n_t, kc_t, vc_t], qx, heads=H, kv_heads=KV, head_dim=HD,
-                                    fq=np.full(H, e["q"]), cos=cos, sin=sin))
+        fq = np.full(H, e["q"])
+        add(AttnPrepRoNode([q0, k0, v, pos_t, n_t, kc_t, vc_t], qx, heads=H, kv_heads=KV, head_dim=HD, fq=fq,
+                           cos=cos, sin=sin), "LlmAttnPrep", q_exp=fq, cos=cos, sin=sin, rowops=1, **heads)
         cmr, cfg = softmax_regs(e["s"], 1.0 / math.sqrt(HD), e["p"])
         geo = dict(T=T, H=H, KV=KV, HD=HD, C=C)
         outs = []
         for grp in range(KV):
             s = T_(p + f"s{grp}", [C, G * T], exp=0)
-            nodes.append(LlmAttnConvNode([kc_t, qx, pos_t, n_t], s, kind="qk", group=grp, **geo))
+            add(LlmAttnConvNode([kc_t, qx, pos_t, n_t], s, kind="qk", group=grp, **geo), "LlmAttnScores", group=grp,
+                **heads)
             pg = T_(p + f"p{grp}", [G * T, C], exp=0)
-            nodes.append(AttnSoftmaxNode([s, pos_t, n_t], pg, T=T, G=G, C=C, group=grp, cm=cmr, cfg=cfg))
+            add(AttnSoftmaxNode([s, pos_t, n_t], pg, T=T, G=G, C=C, group=grp, cm=cmr, cfg=cfg), "LlmAttnSoftmax",
+                group=grp, s_exp=[e["s"]] * G, p_exp=[e["p"]] * G, vsmx=1, **heads)
             og = T_(p + f"o{grp}", [G * T, HD], exp=0)
-            nodes.append(LlmAttnConvNode([pg, vc_t, pos_t, n_t], og, kind="pv", group=grp, **geo))
+            add(LlmAttnConvNode([pg, vc_t, pos_t, n_t], og, kind="pv", group=grp, **geo), "LlmAttnPV", group=grp,
+                **heads)
             outs.append(og)
         om = T_(p + "om", [T, A], exp=e["o"])
-        nodes.append(AttnMergeNode(outs, om, T=T, H=H, KV=KV, HD=HD))
+        add(AttnMergeNode(outs, om, T=T, H=H, KV=KV, HD=HD), "LlmAttnMerge", **heads)
         a = T_(p + "a", [T, D], exp=e["a"])
-        nodes.append(MatmulNode([om, T_(p + "wo", [A, D], data=L["wo"])], a))
+        add(MatmulNode([om, T_(p + "wo", [A, D], data=L["wo"])], a), "MatMul", domain="")
         h1 = T_(p + "h1", [T, D], exp=RES_BITS, kind="i32")
-        nodes.append(ResAddRoNode([hcur, a], h1))
+        add(ResAddRoNode([hcur, a], h1), "LlmResAdd")
         x2 = T_(p + "x2", [T, D], exp=e["x2"])
-        nodes.append(RMSNormRoNode([h1], x2, gamma=L["g2"], eps=S.eps))
+        add(RMSNormRoNode([h1], x2, gamma=L["g2"], eps=S.eps), "LlmRMSNorm", gamma=L["g2"], eps=S.eps)
         gt = T_(p + "g", [T, S.ff], exp=e["g"])
-        nodes.append(MatmulNode([x2, T_(p + "wg", [D, S.ff], data=L["wg"])], gt))
+        add(MatmulNode([x2, T_(p + "wg", [D, S.ff], data=L["wg"])], gt), "MatMul", domain="")
         up = T_(p + "u", [T, S.ff], exp=e["u"])
-        nodes.append(MatmulNode([x2, T_(p + "wu", [D, S.ff], data=L["wu"])], up))
+        add(MatmulNode([x2, T_(p + "wu", [D, S.ff], data=L["wu"])], up), "MatMul", domain="")
         mm = T_(p + "m", [T, S.ff], exp=e["m"])
-        nodes.append(SiluMulRoNode([gt, up], mm))
+        add(SiluMulRoNode([gt, up], mm), "LlmSiluMul")
         dd = T_(p + "d", [T, D], exp=e["d"])
-        nodes.append(MatmulNode([mm, T_(p + "wd", [S.ff, D], data=L["wd"])], dd))
+        add(MatmulNode([mm, T_(p + "wd", [S.ff, D], data=L["wd"])], dd), "MatMul", domain="")
         hn = T_(p + "h", [T, D], exp=RES_BITS, kind="i32")
-        nodes.append(ResAddRoNode([h1, dd], hn))
+        add(ResAddRoNode([h1, dd], hn), "LlmResAdd")
         hcur = hn
     h_last = T_("h_last", [1, D], exp=RES_BITS, kind="i32", state=True)
-    nodes.append(SelectRowNode([hcur, n_t], h_last))
+    add(SelectRowNode([hcur, n_t], h_last), "LlmSelectRow")
     outputs = [h_last]
     if with_head:
         fin = exps[-1]
         xf = T_("xf", [1, D], exp=fin["xf"])
-        nodes.append(RMSNormRoNode([h_last], xf, gamma=gf, eps=S.eps))
+        add(RMSNormRoNode([h_last], xf, gamma=gf, eps=S.eps), "LlmRMSNorm", gamma=gf, eps=S.eps)
         lq = T_("logits_q", [1, S.vocab], exp=fin["logits"])
-        nodes.append(MatmulNode([xf, T_("w.lm_head", [D, S.vocab], data=np.ascontiguousarray(emb.T))], lq))
+        add(MatmulNode([xf, T_("w.lm_head", [D, S.vocab], data=np.ascontiguousarray(emb.T))], lq), "MatMul",
+            domain="")
         chunk = next(c for c in range(4096, 0, -8) if S.vocab % c == 0)
         lr = T_("logits_rows", [S.vocab // chunk, chunk], exp=fin["logits"])
-        nodes.append(ReshapeNode([lq], lr))
+        add(ReshapeNode([lq], lr), "Reshape", domain="")
         lf = T_("logits_f32", [S.vocab // chunk, chunk], kind="f32")
-        nodes.append(DequantRoNode([lr], lf))
+        add(DequantRoNode([lr], lf), "LlmDequant")
         lo = T_("logits", [1, S.vocab], kind="f32")
-        nodes.append(ReshapeNode([lf], lo))
+        add(ReshapeNode([lf], lo), "Reshape", domain="")
         outputs.append(lo)
-    g = Graph(nodes, input_tensors=[ids_t, pos_t, n_t], output_tensors=outputs)
+    graph_inputs = [ids_t, pos_t, n_t]
+    if as_ops:
+        return ops, reg, [t.onnx_name for t in graph_inputs], [t.onnx_name for t in outputs]
+    g = Graph(nodes, input_tensors=graph_inputs, output_tensors=outputs)
     encode_matmul_weights(g.nodes, AP_FIXED_16_8)
     return g
 

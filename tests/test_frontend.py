@@ -68,6 +68,41 @@ def test_smollm2_decode_from_ops(runtime_pos):
     assert_same_graph(build_graph(ops, tensors, ins, outs), g)
 
 
+@pytest.mark.parametrize("with_head", [False, True])
+def test_smollm2_prefill_from_ops(with_head):
+    """The prefill entry's op list (LlmAttnPrep, LlmAttnScores, LlmAttnSoftmax vsmx, LlmAttnPV,
+    LlmAttnMerge, LlmSelectRow among the usual ops) builds the hand-built graph."""
+    shape = models.LlamaShape(layers=2, batch=1, d=128, heads=4, kv=2, hd=32, ff=256, vocab=512, ctx=128)
+    w = models.smollm2_weights(shape, 3)
+    _, _, exps = models.smollm2_decode(shape, seed=3, weights=w, runtime_pos=True)
+    g = models.smollm2_prefill(shape, 32, exps, w, with_head=with_head)
+    ops, tensors, ins, outs = models.smollm2_prefill(shape, 32, exps, w, with_head=with_head, as_ops=True)
+    assert_same_graph(build_graph(ops, tensors, ins, outs), g)
+
+
+def test_prefill_attention_ops_refused_off_the_units():
+    """The host forms of the prefill chain are not built: LlmAttnPrep without the row-ops unit,
+    LlmAttnSoftmax without vsmx or the softmax unit, the prefix-LM mask."""
+    shape = models.LlamaShape(layers=1, batch=1, d=128, heads=4, kv=2, hd=32, ff=256, vocab=512, ctx=128)
+    w = models.smollm2_weights(shape, 3)
+    _, _, exps = models.smollm2_decode(shape, seed=3, weights=w, runtime_pos=True)
+    ops, tensors, ins, outs = models.smollm2_prefill(shape, 16, exps, w, as_ops=True)
+    prep = next(o for o in ops if o.op_type == "LlmAttnPrep")
+    smx = next(o for o in ops if o.op_type == "LlmAttnSoftmax")
+    with pytest.raises(SchedulerError, match="row-ops"):
+        _one(prep, tensors, Platform(rowops=False))
+    with pytest.raises(SchedulerError, match="vsmx"):
+        _one(smx, tensors, Platform(softmax=False))
+    host = frontend.OpDesc(smx.op_type, smx.inputs, smx.outputs, {**smx.attrs, "vsmx": 0}, smx.domain)
+    with pytest.raises(SchedulerError, match="p12"):
+        _one(host, tensors)
+    prefix = frontend.OpDesc(smx.op_type, smx.inputs, smx.outputs, {**smx.attrs, "causal": 2}, smx.domain)
+    with pytest.raises(SchedulerError, match="prefix"):
+        _one(prefix, tensors)
+    enc = frontend.OpDesc(smx.op_type, smx.inputs, smx.outputs, {**smx.attrs, "causal": 0}, smx.domain)
+    assert _one(enc, tensors).causal is False
+
+
 # ---------------------------------------------------------------- the unit-or-host rules
 def _t(name, shape, **kw):
     return TensorInfo(name, list(shape), **kw)
