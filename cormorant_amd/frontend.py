@@ -28,7 +28,8 @@ The custom-domain ops this build takes are the ones its node kinds cover: LlmEmb
 LlmRMSNorm, LlmResAdd, LlmSiluMul, LlmDequant, LlmToHost, LlmAttention (the host attention),
 VitLayerNorm, VitResAdd, VitGelu; the prefill attention chain on the units (LlmAttnPrep on the
 row-ops unit, LlmAttnScores / LlmAttnPV, LlmAttnSoftmax under the vsmx policy, LlmAttnMerge;
-llama.py:329-402) and LlmSelectRow; and two ops of this build's own that stand for the
+llama.py:329-402), LlmSelectRow, and the encoder template's VitAttnPrep (rowops) and
+VitAttnSoftmax (vsmx; vit.py:564-630); and two ops of this build's own that stand for the
 reference's attention chains, which it runs as one fused node each: ``VitAttention`` (VitAttnPrep,
 LlmAttnScores, VitAttnSoftmax on the unit, LlmAttnPV, LlmAttnMerge: vit.py:19-32 -> AttentionNode)
 and ``LlmDecodeAttention`` (LlmAttnPrep's RoPE and cache-row writes, the scores, LlmAttnSoftmax,
@@ -48,7 +49,7 @@ from .graph import (KEY_QUANTUM, AttentionNode, AttnMergeNode, AttnSoftmaxNode, 
                     SoftmaxVopNode, TensorInfo, conv_out, fuse_activations, softmax_regs)
 from .host_ops import (GeluNode, LayerNormNode, LlmAttentionNode, LlmDequantNode, LlmEmbedNode, LlmResAddNode,
                        LlmRMSNormNode, LlmSiluMulNode, LlmToHostNode, SoftmaxNode, TransposeNode)
-from .rowops_nodes import (N_MAX, P1_BITS, AttnPrepRoNode, DecodePrepNode, DequantRoNode, LayerNorm32RoNode, LayerNormRoNode,
+from .rowops_nodes import (N_MAX, P1_BITS, AttnPrepRoNode, DecodePrepNode, DequantRoNode, VitAttnPrepRoNode, LayerNorm32RoNode, LayerNormRoNode,
                            ResAddBiasRoNode, ResAddRoNode, RMSNormRoNode, SiluMulRoNode, TransposeRoNode, beta_bits,
                            collapse, gamma_scale, transpose_job)
 
@@ -499,7 +500,40 @@ def _llm_attn_conv(op, ctx):
     T = (ins[1].shape[-1] if qk else ins[0].shape[0]) // G
     return LlmAttnConvNode(ins, ctx.out(op), kind="qk" if qk else "pv", group=int(op.attrs["group"]), T=int(T), H=H,
                            KV=KV, HD=HD, C=int(cache.shape[0]), Q=int(op.attrs.get("key_quantum", KEY_QUANTUM)),
-                           has_n=len(ins) == 4)
+                           static=len(ins) == 2, has_n=len(ins) != 3)
+
+
+def _vit_attn_prep(op, ctx):
+    """VitAttnPrep [q0, k0, v, K cache, V cache] -> qx with rowops = 1 (rowops_nodes.py:1596-1712):
+    VitAttnPrepRoNode; the biases bq / bk / bv and the columns ``cols`` are attributes here.  The
+    host VitAttnPrep, RoPE and the key rows are not built."""
+    a = op.attrs
+    if not (ctx.platform.rowops and int(a.get("rowops", 0))):
+        raise SchedulerError(f"VitAttnPrep node '{op.label}': runs on the row-ops unit (rowops = 1); the host "
+                             f"prep is not built")
+    if int(a.get("rope", 0)):
+        raise SchedulerError(f"VitAttnPrep node '{op.label}': the 3-D RoPE variant is not built")
+    ins = [ctx.t(n, op) for n in op.inputs]
+    return VitAttnPrepRoNode(ins, ctx.out(op), heads=int(a["num_heads"]), head_dim=int(a["head_dim"]),
+                             fq=np.asarray(a["q_exp"]), fk=np.asarray(a["k_exp"]), fv=np.asarray(a["v_exp"]),
+                             bq=a.get("bq"), bk=a.get("bk"), bv=a.get("bv"), cols=tuple(a.get("cols", (0, 0, 0))),
+                             query_major=bool(int(a.get("query_major", 0))))
+
+
+def _vit_attn_softmax(op, ctx):
+    """VitAttnSoftmax [s] -> P with vsmx = 1: the static column-mode call on the softmax unit
+    (smx_nodes.py:206-248); the host softmax and the row splits (``cols``) are not built."""
+    a = op.attrs
+    if not (ctx.platform.softmax and int(a.get("vsmx", 0))):
+        raise SchedulerError(f"VitAttnSoftmax node '{op.label}': runs on VectorOPKernel's softmax unit (vsmx = 1); "
+                             f"the host softmax is not built")
+    if "cols" in a or int(a.get("query_major", 0)):
+        raise SchedulerError(f"VitAttnSoftmax node '{op.label}': row splits / query-major scores are not built")
+    s = ctx.t(op.inputs[0], op)
+    C, T = (int(d) for d in s.shape)
+    scale = float(a.get("logit_scale", 1.0 / np.sqrt(int(a["head_dim"]))))
+    cm, cfg = softmax_regs(int(np.asarray(a["s_exp"]).reshape(-1)[0]), scale, int(np.asarray(a["p_exp"]).reshape(-1)[0]))
+    return AttnSoftmaxNode([s], ctx.out(op), T=T, G=1, C=C, cm=cm, cfg=cfg, causal=False)
 
 
 def _llm_attn_softmax(op, ctx):
@@ -541,7 +575,7 @@ LLM_FACTORIES: Dict[str, Callable] = {
     "VitLayerNorm": _vit_layernorm, "VitResAdd": _llm_resadd, "VitGelu": _vit_gelu, "VitAttention": _vit_attention,
     "LlmDecodeAttention": _llm_decode_attention, "LlmAttnPrep": _llm_attn_prep, "LlmAttnScores": _llm_attn_conv,
     "LlmAttnPV": _llm_attn_conv, "LlmAttnSoftmax": _llm_attn_softmax, "LlmAttnMerge": _llm_attn_merge,
-    "LlmSelectRow": _llm_select_row,
+    "LlmSelectRow": _llm_select_row, "VitAttnPrep": _vit_attn_prep, "VitAttnSoftmax": _vit_attn_softmax,
 }
 SUPPORTED = sorted(set(_VECTOROP) | set(ACT_OPS) | {"Softmax", "LayerNormalization", "Transpose", "MatMul", "Conv"}
                    | set(_POOLS) | RESHAPE_OPS)

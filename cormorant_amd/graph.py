@@ -419,7 +419,8 @@ class AttnSoftmaxNode(KernelNode):
     the keys j < min(keys, pos + 1 + t) (``causal``: the mask register valid0 = pos + 1 with
     period T) or j < max(min(keys, pos + n), 1) (not causal: an encoder's valid frames); P is 0
     at j >= keys.  ``cm`` / ``cfg``: the registers of softmax_regs, one pair for the group or one
-    per head.  inputs [s_g, pos (host), n (host, optional: n = T)]."""
+    per head.  inputs [s_g, pos (host), n (host, optional: n = T)], or [s_g] alone (``static``: an
+    encoder's VitAttnSoftmax, smx_nodes.py:206-248 -- pos 0, n = T, keys = C)."""
     inputs: List[TensorInfo]
     output: TensorInfo
     T: int = 16
@@ -433,23 +434,36 @@ class AttnSoftmaxNode(KernelNode):
 
     def __post_init__(self):
         what = f"attention softmax '{self.output.onnx_name}'"
-        if len(self.inputs) not in (2, 3):
-            raise SchedulerError(f"{what}: inputs scores, pos, [n]")
-        s, pos = self.inputs[0], self.inputs[1]
+        if len(self.inputs) not in (1, 2, 3):
+            raise SchedulerError(f"{what}: inputs scores, [pos, [n]]")
+        s = self.inputs[0]
         GT = self.G * self.T
         if list(s.shape) != [self.C, GT] or list(self.output.shape) != [GT, self.C]:
             raise SchedulerError(f"{what}: scores [{self.C}][{GT}] -> P [{GT}][{self.C}]")
         if self.T % 16 or self.C % self.Q or self.Q % KEY_QUANTUM or not 0 < self.C <= SMX_MAX_KEYS:
             raise SchedulerError(f"{what}: query rows a multiple of 16, cache rows a multiple of the key "
                                  f"quantum and at most {SMX_MAX_KEYS}")
-        if pos.kind != "host" or (self.has_n and self.inputs[2].kind != "host"):
+        if any(t.kind != "host" for t in self.inputs[1:]):
             raise SchedulerError(f"{what}: pos / n are host tensors")
+        if self.static and self.C != -(-self.T // self.Q) * self.Q:
+            raise SchedulerError(f"{what}: a static call has every key valid: C = roundup(T, {self.Q})")
         if any(np.asarray(r).size not in (1, self.G) for r in (self.cm, self.cfg)):
             raise SchedulerError(f"{what}: cm / cfg one pair, or one per head of the group")
 
     @property
     def has_n(self) -> bool:
         return len(self.inputs) == 3
+
+    @property
+    def static(self) -> bool:
+        return len(self.inputs) == 1
+
+    def pos_n(self, host) -> Tuple[int, int]:
+        """(pos, n) of a call: the host values of the pos / n inputs (``host``: tensor -> int),
+        n = T without its input, (0, T) for a static call."""
+        if self.static:
+            return 0, self.T
+        return int(host(self.inputs[1])), int(host(self.inputs[2])) if self.has_n else self.T
 
     def regs(self) -> List[Tuple[int, int]]:
         """(cm, cfg) of each head of the group."""

@@ -221,7 +221,7 @@ class BertShape:
 
 
 def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int = 1, fused_attention: bool = True,
-                 as_ops: bool = False):
+                 as_ops: bool = False, prep_attention: bool = False):
     """(graph, inputs, exps): the BERT-base-shaped encoder in per-tensor power-of-two numerics.
 
     Token ids U{0 .. vocab-1} (the graph's input) and embedding rows N(0, 1), gathered on the
@@ -248,9 +248,15 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
     ``fused_attention`` (default): the head split, q.K^T, the softmax, P.V and the merge as
     one AttentionNode (the same arithmetic in one call, cm_attention on MFMA); False: node by
     node, the contractions on the plane GEMM reading and writing per-head views in place.
-    ``as_ops`` (with the fused attention): (ops, tensors, inputs, outputs) in place of the graph --
-    the encoder as the reference's ops (LlmEmbed, VitLayerNorm, MatMul, the attention chain as
-    VitAttention, VitResAdd, Add + Gelu) for the front end, weights not yet encoded.
+    ``prep_attention`` (one sequence): the reference's own chain of the encoder template instead
+    (vit.py:564-630) -- VitAttnPrep on the row-ops unit (VitAttnPrepRoNode: q into the q.K^T
+    image, k / v into the K / V caches, raw states [T][D] group-major shared by the layers), per
+    head q.K^T (LlmAttnConvNode, static keys), the column-mode softmax (AttnSoftmaxNode, static)
+    and P.V, and LlmAttnMerge -- the same integers as the fused node.
+    ``as_ops`` (the fused or the prep attention): (ops, tensors, inputs, outputs) in place of the
+    graph -- the encoder as the reference's ops (LlmEmbed, VitLayerNorm, MatMul, the attention
+    chain as VitAttention or as VitAttnPrep / LlmAttnScores / VitAttnSoftmax / LlmAttnPV /
+    LlmAttnMerge, VitResAdd, Add + Gelu) for the front end, weights not yet encoded.
     """
     from .frontend import LLM_DOMAIN, OpDesc
     from .numeric import encode_matmul_weights
@@ -331,8 +337,16 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
     h_in = T_("h0", [rows, D], exp=RES_BITS, kind="i32")
     nodes = [LlmEmbedNode([ids_t], h_in, table=emb)]
     ops, reg = [], {"ids": ids_t}
-    if as_ops and not fused_attention:
-        raise ValueError("bert_encoder: the op list describes the fused attention (VitAttention)")
+    if as_ops and not (fused_attention or prep_attention):
+        raise ValueError("bert_encoder: the op list describes the fused (VitAttention) or the prep attention")
+    if prep_attention:
+        from .graph import AttnMergeNode, AttnSoftmaxNode, LlmAttnConvNode
+        from .rowops_nodes import VitAttnPrepRoNode
+        if S.batch != 1 or T % 16:
+            raise ValueError("bert_encoder: the prep attention takes one sequence of a multiple of 16 tokens")
+        # the K / V caches: raw states [T][D] stored group-major [H][T][hd], shared by the layers
+        kc_t = T_("vit.kc", [T, D], exp=0, group_layout=(H, hd), state=True)
+        vc_t = T_("vit.vc", [T, D], exp=0, group_layout=(H, hd), state=True)
 
     def op(kind, ins, out, domain="", **attrs):
         for t in list(ins) + [out]:
@@ -353,7 +367,30 @@ def bert_encoder(shape: BertShape = BertShape(), seed: int = 0, calib_seqs: int 
         ld = 3 * D
         cmr, cfg = softmax_regs(e["s"], 1.0 / math.sqrt(hd), e["p"])
         om = T_(p + "om", [rows, D], exp=e["o"])
-        if fused_attention:
+        if prep_attention:
+            qx = T_(p + "qx", [H, hd, T], exp=0)
+            nodes.append(VitAttnPrepRoNode([qkv, qkv, qkv, kc_t, vc_t], qx, heads=H, head_dim=hd, fq=e["q"], fk=e["k"],
+                                           fv=e["v"], cols=(0, D, 2 * D)))
+            op("VitAttnPrep", [qkv, qkv, qkv, kc_t, vc_t], qx, LLM_DOMAIN, num_heads=H, head_dim=hd, q_exp=[e["q"]] * H,
+               k_exp=[e["k"]] * H, v_exp=[e["v"]] * D, cols=(0, D, 2 * D), rowops=1)
+            geo = dict(T=T, H=H, KV=H, HD=hd, C=T, static=True)
+            heads_attrs = dict(num_heads=H, num_kv_heads=H, head_dim=hd)
+            outs = []
+            for hh in range(H):
+                st = T_(p + f"s{hh}", [T, T], exp=0)
+                nodes.append(LlmAttnConvNode([kc_t, qx], st, kind="qk", group=hh, **geo))
+                op("LlmAttnScores", [kc_t, qx], st, LLM_DOMAIN, group=hh, **heads_attrs)
+                pt = T_(p + f"p{hh}", [T, T], exp=0)
+                nodes.append(AttnSoftmaxNode([st], pt, T=T, G=1, C=T, cm=cmr, cfg=cfg, causal=False))
+                op("VitAttnSoftmax", [st], pt, LLM_DOMAIN, head_dim=hd, s_exp=[e["s"]], p_exp=[e["p"]], vsmx=1)
+                ot = T_(p + f"o{hh}", [T, hd], exp=0)
+                nodes.append(LlmAttnConvNode([pt, vc_t], ot, kind="pv", group=hh, **geo))
+                op("LlmAttnPV", [pt, vc_t], ot, LLM_DOMAIN, group=hh, **heads_attrs)
+                outs.append(ot)
+            nodes.append(AttnMergeNode(outs, om, T=T, H=H, KV=H, HD=hd))
+            ops.append(OpDesc("LlmAttnMerge", [t.onnx_name for t in outs], [om.onnx_name], heads_attrs, LLM_DOMAIN))
+            reg[om.onnx_name] = om
+        elif fused_attention:
             nodes.append(AttentionNode([qkv], om, batch=S.batch, seq=T, heads=H, head_dim=hd, q_off=0, k_off=D,
                                        v_off=2 * D, cm=cmr, cfg=cfg))
             op("VitAttention", [qkv], om, LLM_DOMAIN, batch=S.batch, seq=T, heads=H, head_dim=hd, q_off=0, k_off=D,

@@ -863,10 +863,124 @@ class AttnPrepRoNode(RoCallNode):
         return jobs
 
 
+@dataclass
+class VitAttnPrepRoNode(RoCallNode):
+    """VitAttnPrep on the unit (rowops_nodes.py:1415-1593, from_vit_attn_prep :1596-1712): an
+    encoder's attention prep with every key valid (T = C rows, position 0, static jobs) --
+
+      * q0 + bq rounded at the per-head exponents ``fq`` into the staging rows, then one
+        TRANSPOSE (8-row tiles, the heads as blocks) into the q.K^T image qx [H][HD][T];
+      * per head, k0 + bk at that head's exponent ``fk`` straight into the K cache rows;
+      * v + bv at the V cache's exponents ``fv`` (per column) into staging, then one COPY into
+        the V cache rows (the heads as blocks).
+
+    Each add is a COPY with a bias (rowops_spec.bias_round: sat16(rne_shr((x << (fp - f_x)) +
+    round(b 2^fp), fp - f_out)), the bias rounded once at 2^-fp); no bias rounds x alone.  The
+    caches are raw states (exponent 0) stored group-major [H][C][HD]; qx holds raw integers.
+    ``query_major``: q and k swap roles (k takes the image path, q the cache rows), so the
+    scores come out query-major.
+
+    inputs [q0, k0, v, cache_k, cache_v]: q0 / k0 / v rows of T, each read from column ``cols[i]``
+    of its tensor's rows (one fused projection [T][3 D] may serve all three).  The V cache
+    without interleave (the reference's group_kw 1); head_dim a multiple of 16, T a multiple
+    of 8."""
+    inputs: List[TensorInfo]
+    output: TensorInfo
+    heads: int = 1
+    head_dim: int = 16
+    fq: Optional[np.ndarray] = None
+    fk: Optional[np.ndarray] = None
+    fv: Optional[np.ndarray] = None
+    bq: Optional[np.ndarray] = None
+    bk: Optional[np.ndarray] = None
+    bv: Optional[np.ndarray] = None
+    cols: tuple = (0, 0, 0)
+    query_major: bool = False
+    F: int = 8
+
+    def __post_init__(self):
+        H, HD = self.heads, self.head_dim
+        D = H * HD
+        what = f"VitAttnPrep '{self.output.onnx_name}'"
+        _require(len(self.inputs) == 5, what, "inputs q0, k0, v, cache_k, cache_v")
+        ck, cv = self.inputs[3], self.inputs[4]
+        _require(HD % 16 == 0 and 16 <= HD <= 1024 and D <= N_MAX, what, f"head_dim {HD}: a multiple of 16")
+        C = int(ck.shape[0])
+        self.T = T = C
+        _require(T % QIMAGE_R == 0, what, f"rows {T} % {QIMAGE_R} (the q image's tiles)")
+        for i, (t, nm) in enumerate(zip(self.inputs[:3], ("q0", "k0", "v"))):
+            w = int(t.shape[-1])
+            _require(t.kind == "i16" and t.numel == T * w and 0 <= self.cols[i] and self.cols[i] + D <= w
+                     and self.cols[i] % 8 == 0 and w % 8 == 0, what,
+                     f"{nm}: int16 rows of {T} holding {D} columns from column {self.cols[i]} (16-byte aligned)")
+        for t, nm in ((ck, "cache_k"), (cv, "cache_v")):
+            _require(t.kind == "i16" and t.state and t.group_layout == (H, HD) and list(t.shape) == [T, D]
+                     and (np.asarray(0 if t.exp is None else t.exp) == 0).all(), what,
+                     f"{nm}: a raw state (exponent 0), logical [{T}][{D}] stored group-major [{H}][{T}][{HD}]")
+        _require(list(self.output.shape) == [H, HD, T] and self.output.kind == "i16"
+                 and (np.asarray(0 if self.output.exp is None else self.output.exp) == 0).all(), what,
+                 f"qx: raw integers [{H}][{HD}][{T}]")
+        fq = np.broadcast_to(np.asarray(self.fq, np.int64).reshape(-1), (H,))
+        fk = np.broadcast_to(np.asarray(self.fk, np.int64).reshape(-1), (H,))
+        self.fq, self.fk = fq.copy(), fk.copy()
+        self.fv = np.broadcast_to(np.asarray(self.fv, np.int64).reshape(-1), (D,)).copy()
+        zero = np.zeros(D)
+        bq, bk, bv = (zero if b is None else np.asarray(b, np.float64).reshape(-1) for b in (self.bq, self.bk, self.bv))
+        _require(bq.size == D and bk.size == D and bv.size == D, what, f"biases of {D} columns")
+        q0, k0 = self.inputs[0], self.inputs[1]
+        cq, ckc = self.cols[0], self.cols[1]
+        if self.query_major:             # k the image path, q the cache rows
+            q0, k0, bq, bk, fq, fk, cq, ckc = k0, q0, bk, bq, fk, fq, ckc, cq
+        self._img, self._rows = (q0, cq), (k0, ckc)
+
+        def params(x, col, bias, f_out):
+            fx = _exps(x, self.F, int(x.shape[-1]))[col:col + D]
+            try:
+                b, sa, sc = bias_params(bias, fx, f_out)
+            except SchedulerError as e:
+                raise SchedulerError(f"{what}: {e}") from None
+            _require((sa >= 0).all() and (sa <= 63).all() and (sc >= 0).all() and (sc <= 63).all(), what,
+                     "exponents beyond the shifts")
+            return b, sa, sc
+
+        b, sa, sc = params(q0, cq, bq, np.repeat(fq, HD))
+        self._pq, self._pq_bc = pblock(0, b, sa, 0, sc, D)
+        b, sa, sc = params(k0, ckc, bk, np.repeat(fk, HD))
+        self._pk = [param_block(np.zeros(HD, np.int64), b[h * HD:(h + 1) * HD], sa[h * HD:(h + 1) * HD], 0,
+                                sc[h * HD:(h + 1) * HD]) for h in range(H)]
+        b, sa, sc = params(self.inputs[2], self.cols[2], bv, self.fv)
+        self._pv, self._pv_bc = pblock(0, b, sa, 0, sc, D)
+
+    def staging(self):
+        D2 = self.heads * self.head_dim * 2
+        return {"qs": self.T * D2, "vs": self.T * D2}
+
+    def calls(self, host):
+        T, H, HD = self.T, self.heads, self.head_dim
+        D = H * HD
+        SQ = D * 2
+        (img, ci), (rows_t, cr), v = self._img, self._rows, self.inputs[2]
+        stride = lambda t: int(t.shape[-1]) * 2                                   # noqa: E731
+        ck, cv, qx = self.inputs[3].onnx_name, self.inputs[4].onnx_name, self.output.onnx_name
+        jobs = [RoCall(img.onnx_name, ci * 2, None, 0, "node:qs", 0, self._pq, opword(RO_COPY, p_bcast=self._pq_bc),
+                       D, T, 1, stride(img), 0, 0, 0, SQ, 0),
+                RoCall("node:qs", 0, None, 0, qx, 0, None, opword(RO_XPOSE), HD, T // QIMAGE_R, H, QIMAGE_R * SQ,
+                       HD * 2, SQ, 2 * T, 2 * QIMAGE_R, HD * T * 2, aux=QIMAGE_R)]
+        for h in range(H):
+            jobs.append(RoCall(rows_t.onnx_name, (cr + h * HD) * 2, None, 0, ck, h * T * HD * 2, self._pk[h],
+                               opword(RO_COPY), HD, T, 1, stride(rows_t), 0, 0, 0, HD * 2, 0))
+        jobs.append(RoCall(v.onnx_name, self.cols[2] * 2, None, 0, "node:vs", 0, self._pv,
+                           opword(RO_COPY, p_bcast=self._pv_bc), D, T, 1, stride(v), 0, 0, 0, SQ, 0))
+        jobs.append(RoCall("node:vs", 0, None, 0, cv, 0, ZERO_PARAMS, opword(RO_COPY, p_bcast=True), HD, T, H, SQ,
+                           HD * 2, 0, 0, HD * 2, T * HD * 2))
+        return jobs
+
+
 ADAPTERS = (LayerNormRoNode, LayerNorm32RoNode, RMSNormRoNode, ResAddRoNode, ResAddBiasRoNode, WidenRoNode,
             SiluMulRoNode, DequantRoNode, BiasCopyRoNode, RopeRoNode)
 
-__all__ = ["RoJob", "RowOpsAdapter", "RoCall", "RoCallNode", "TransposeRoNode", "AttnPrepRoNode", "collapse",
+__all__ = ["RoJob", "RowOpsAdapter", "RoCall", "RoCallNode", "TransposeRoNode", "AttnPrepRoNode", "VitAttnPrepRoNode",
+           "collapse",
            "transpose_job", "opword", "gamma_scale", "beta_bits", "bias_bits", "quant_bias", "bias_exp",
            "bias_params", "norm_params", "param_block", "pblock", "rope_tables_raw", "rope_table"] + \
           [c.__name__ for c in ADAPTERS]

@@ -1080,8 +1080,8 @@ class Simulator:
         the keys."""
         T, C = sn.T, sn.C
         GT = sn.G * T
-        pos = self._host_int(sn.inputs[1], raw)
-        n, keys = attn_keys(pos, self._host_int(sn.inputs[2], raw) if sn.has_n else T, T, C, sn.Q)
+        pos, n_in = sn.pos_n(lambda t: self._host_int(t, raw))
+        n, keys = attn_keys(pos, n_in, T, C, sn.Q)
         s = self._get(sn.inputs[0], raw).reshape(-1)
         out = torch.zeros(GT * C, dtype=torch.int16, device=self.device)
         mask = sn.mask_reg(pos, n, keys)

@@ -1,6 +1,7 @@
-"""CPU restatements of two row-ops nodes' ``reference()`` for the graph-level checker: the
-Transpose on the unit (a numpy transpose) and LlmAttnPrep on the unit (RoPE of q / k, the
-V re-round, the q.K^T x image, the cache rows).  TEST INFRASTRUCTURE ONLY (the checker,
+"""CPU restatements of three row-ops nodes' ``reference()`` for the graph-level checker: the
+Transpose on the unit (a numpy transpose), LlmAttnPrep on the unit (RoPE of q / k, the V
+re-round, the q.K^T x image, the cache rows) and VitAttnPrep on the unit (the bias adds into
+the q image and the caches).  TEST INFRASTRUCTURE ONLY (the checker,
 never the thing measured or shipped).  Nothing here imports the product: the spec functions
 are restated from inference-scheduler/src/rowops_spec.py.
 """
@@ -96,3 +97,27 @@ def attn_prep(q0, k0, v, pos, n, ck, cv, f_q0, f_k0, f_v, f_kc, f_vc, fq, cos, s
 def transpose(x, perm):
     """TransposeRoNode.reference (rowops_nodes.py:293-295): numpy's transpose, a bit copy."""
     return np.ascontiguousarray(np.transpose(np.asarray(x), perm))
+
+
+def bias_round(x_raw, f_x, bias, f_out):
+    """A COPY with a bias (rowops_spec.py:195-203): per column sat16(rne_shr((x << (fp - f_x)) +
+    round(bias 2^fp), fp - f_out)) with fp = bias_exp (the bias rounded once at 2^-fp)."""
+    from oracle.rowops_adapt import bias_params
+    x_raw = np.asarray(x_raw, np.int64)
+    bq, sa, sc = bias_params(bias, f_x, f_out)
+    return sat16(rne_shr_vec((x_raw << sa[None, :]) + bq[None, :], sc[None, :]))
+
+
+def vit_attn_prep(q_raw, k_raw, v_raw, f_q0, f_k0, f_v0, bq, bk, bv, fq, fk, fv, H, HD, query_major=False):
+    """VitAttnPrepRoNode.reference (rowops_nodes.py:1570-1593) without RoPE or key rows, on raw
+    int16 rows [T][H HD] at their column exponents: (qx [H][HD][T], K cache rows [T][H HD],
+    V cache rows [T][H HD]) -- k0 + bk at f_k per head into the K cache, v + bv at f_v per
+    column into the V cache, q0 + bq at f_q per head transposed per head into qx; with
+    ``query_major`` k takes the image path and q the K cache rows."""
+    T = np.asarray(q_raw).shape[0]
+    if query_major:
+        q_raw, k_raw, f_q0, f_k0, bq, bk, fq, fk = k_raw, q_raw, f_k0, f_q0, bk, bq, fk, fq
+    ck = bias_round(k_raw, f_k0, bk, np.repeat(np.asarray(fk, np.int64), HD))
+    cv = bias_round(v_raw, f_v0, bv, fv)
+    yq = bias_round(q_raw, f_q0, bq, np.repeat(np.asarray(fq, np.int64), HD))
+    return yq.reshape(T, H, HD).transpose(1, 2, 0).copy(), ck, cv

@@ -19,7 +19,7 @@ from oracle import host_ref
 from oracle import residual_ref
 from oracle import rowops_adapt
 from oracle import sim_ref
-from oracle.attn_prep import attn_prep, clamp_n, transpose
+from oracle.attn_prep import attn_prep, clamp_n, transpose, vit_attn_prep
 
 F = 8                                   # the element type's fraction bits (ap_fixed<16,8>)
 Q_MIN, Q_MAX = -128.0, 127.99609375
@@ -389,8 +389,11 @@ def forward(graph, inputs, states=None, algo="port", errors_out=None):
             # length as a period-0 mask
             st = sn.inputs[0]
             T, G, C = sn.T, sn.G, sn.C
-            pos = int(np.asarray(get(sn.inputs[1])).reshape(-1)[0])
-            n_in = int(np.asarray(get(sn.inputs[2])).reshape(-1)[0]) if len(sn.inputs) == 3 else T
+            if len(sn.inputs) == 1:                 # static (VitAttnSoftmax): pos 0, n = T
+                pos, n_in = 0, T
+            else:
+                pos = int(np.asarray(get(sn.inputs[1])).reshape(-1)[0])
+                n_in = int(np.asarray(get(sn.inputs[2])).reshape(-1)[0]) if len(sn.inputs) == 3 else T
             n, keys = clamp_n(pos, n_in, T, C, sn.Q)
             valid = (np.minimum(keys, pos + 1 + np.arange(T)) if sn.causal
                      else np.full(T, max(min(keys, pos + n), 1)))
@@ -449,6 +452,21 @@ def forward(graph, inputs, states=None, algo="port", errors_out=None):
                                             _chan(k0t, KV * HD), _chan(vt, KV * HD), _chan(ckt, KV * HD),
                                             _chan(cvt, KV * HD), sn.fq, sn.cos, sn.sin, H, KV, HD,
                                             sn.key_quantum).reshape(out.shape)
+        elif kind == "VitAttnPrepRoNode":
+            H, HD = sn.heads, sn.head_dim
+            D = H * HD
+            rows = []
+            for t_, col in zip(sn.inputs[:3], sn.cols):
+                w = int(t_.shape[-1])
+                r = _raw_of(t_, get(t_)).reshape(-1, w)[:, col:col + D]
+                rows.append((r, _chan(t_, w)[col:col + D]))
+            zero = np.zeros(D)
+            b = [zero if x is None else np.asarray(x, np.float64).reshape(-1) for x in (sn.bq, sn.bk, sn.bv)]
+            qx, ck, cv = vit_attn_prep(rows[0][0], rows[1][0], rows[2][0], rows[0][1], rows[1][1], rows[2][1], *b,
+                                       sn.fq, sn.fk, sn.fv, H, HD, sn.query_major)
+            vals[sn.inputs[3].onnx_name].reshape(-1, D)[...] = ck            # the states, in place (raw)
+            vals[sn.inputs[4].onnx_name].reshape(-1, D)[...] = cv
+            vals[out.onnx_name] = qx.astype(np.float64).reshape(out.shape)
         elif kind == "KvWriteNode":
             xt, ct = sn.inputs[0], sn.inputs[1]
             B, KV, C, HD = (int(v) for v in ct.shape)
