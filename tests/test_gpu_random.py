@@ -402,6 +402,8 @@ def test_matmul_skinny_planes_mulact(U, oracle_lib, n, k, m, kind):
     (4, 8, 2048, (100 | (3 << 16)), 3, 32768),   # a periodic mask (per-row valid counts), full range
     (7, 1, 64, 0, 0, 32768),             # no valid key: P = 0, o = 0
     (3, 5, 128, 128, 1, 32768),
+    (300, 2, 192, 150, 2, 3000),         # more groups than CUs
+    (2, 4, 8192, 8000, 1, 3000),         # the longest cache
 ])
 def test_decode_attention(U, oracle_lib, groups, G, C, mask, regs, lim):
     """cm_decode_attention against the oracle's chain per group: s = q K^T (int32 wrap), the
