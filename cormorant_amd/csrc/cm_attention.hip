@@ -190,19 +190,13 @@ __global__ __launch_bounds__(256, 3) void attention_kernel(const int16_t* __rest
     // ---- phase 1: the scores, key block by key block, 4 blocks a chunk of K in LDS; chunk c
     // is written before the barrier that precedes its products, chunk c + 1 loaded under them
     int32_t sv[4 * KB];                 // register arrays: every index a constant (loops unrolled)
-    int4 tx[4];                         // the TAB, loaded under the last chunk's products
 #pragma unroll
     for (uint32_t kb = 0; kb < KB; kb++) {
         if (kb % 4 == 0) {
             const uint32_t c = kb / 4;
             store_kchunk(c);
             __syncthreads();            // chunk c in LDS; every wavefront done with chunk c - 1
-            if (c + 1 < KB / 4) {
-                load_kchunk(c + 1);
-            } else {
-#pragma unroll
-                for (uint32_t q = 0; q < 4; q++) tx[q] = reinterpret_cast<const int4*>(tab)[t + 256 * q];
-            }
+            if (c + 1 < KB / 4) load_kchunk(c + 1);
         }
         const uint8_t* kr = kbuf + ((kb / 4) & 1) * 8192 + (16 * (kb % 4) + c16) * 64 + 16 * g;
         const v4i kh = *reinterpret_cast<const v4i*>(kr);
@@ -220,8 +214,13 @@ __global__ __launch_bounds__(256, 3) void attention_kernel(const int16_t* __rest
         }
     }
     __syncthreads();                                   // every wavefront done with the K chunks
+    // the TAB straight into LDS (global_load_lds: no registers, four 16-byte copies a lane in
+    // flight at once), then this wave's copies waited for
 #pragma unroll
-    for (uint32_t q = 0; q < 4; q++) reinterpret_cast<int4*>(stab)[t + 256 * q] = tx[q];
+    for (uint32_t q = 0; q < 4; q++)
+        __builtin_amdgcn_global_load_lds(tab + 4 * (t + 256 * q),
+                                         (__attribute__((address_space(3))) void*)(stab + 4 * (64 * w + 256 * q)), 16, 0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0070);
     __syncthreads();                                   // TAB, V^T planes and V sums staged
 
     // ---- phase 2: the softmax over the T keys of the lane's query (its lane group g = 0..3)
