@@ -23,6 +23,8 @@ pytestmark = pytest.mark.gpu
     # the configuration's own batch: 3072 rows through every linear (FFN2's split over k and its
     # reduce), 96 (sequence, head) pairs of the fused attention; every sequence compared
     (models.BertShape(layers=1, batch=8), 5, True),
+    # the whole 12-layer stack at full width, one sequence
+    (models.BertShape(layers=12, batch=1), 6, True),
 ])
 def test_encoder_every_tensor(shape, seed, fused):
     g, inputs, _ = models.bert_encoder(shape, seed=seed, fused_attention=fused)

@@ -19,6 +19,8 @@ pytestmark = pytest.mark.gpu
     # the configuration's own step: 16 sequences (the 16-row skinny products and the grouped
     # q / k / v and gate / up launches), 1024-row caches, the 49152-column tied head
     (models.LlamaShape(layers=1, batch=16), 5),
+    # the whole 32-layer stack at full width (two sequences, a 4096-row head, 256-row caches)
+    (models.LlamaShape(layers=32, batch=2, vocab=4096, ctx=256), 7),
 ])
 def test_decode_step_every_tensor(shape, seed):
     g, inputs, _ = models.smollm2_decode(shape, seed=seed)
