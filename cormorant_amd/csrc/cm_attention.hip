@@ -211,7 +211,10 @@ __global__ __launch_bounds__(256, 3) void attention_kernel(const int16_t* __rest
             const uint32_t acc = ((uint32_t)hh[r] << 16) + ((uint32_t)mid[r] << 8) + (uint32_t)ll[r] +
                                  ((uint32_t)ha[r] << 15) + ((uint32_t)la[r] << 7);
             sv[4 * kb + r] = sat16_shr8((int32_t)acc);
+            __asm__ volatile("" : "+v"(sv[4 * kb + r]));   // the score itself held, not its terms
         }
+        // one key block at a time: left free, the scheduler gathers the blocks' MFMAs and spills
+        __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();                                   // every wavefront done with the K chunks
     // the TAB straight into LDS (global_load_lds: no registers, four 16-byte copies a lane in
