@@ -949,6 +949,130 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
 #undef CM_STORE
 }
 
+// ---------------------------------------------------------------- standard conv, few taps
+// A standard convolution whose taps per output (in_ch kh kw) are few -- a network's stem over
+// its 1 .. 4 input channels -- straight on the VALU instead of im2col + GEMM (which would pad
+// each kernel position to 16 channels): a lane per output pixel over OG output channels, its
+// taps gathered once (zero outside the input) and packed in pairs, each channel's sum by
+// v_dot2_i32_i16 against the channel's pairs staged in LDS (read by every lane at one
+// address).  The sum is int32 where that is exact -- the wrap path (the int32 wrap is its
+// rule), or a channel whose bound sum |w| 2^15 + |bias| 2^8 stays below 2^31 -- and int64
+// otherwise; then floor(acc / 2^8) clamped to [lo, hi] (saturation and a fused RELU / RELU6),
+// as the GEMM path stores it.  w in the packed layout of cm_conv (ConvKernel.h:136-159).
+constexpr uint32_t kCsMaxTaps = 80;          // taps a lane holds (40 pairs)
+constexpr uint32_t kCsOg = 16;               // output channels of a workgroup
+
+struct ConvSmall {
+    const int16_t* x;
+    const int16_t* w;
+    const int16_t* bias;
+    int16_t* y;
+    uint32_t in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, sh, sw, dh, dw, pt, pl;
+    uint32_t per_m, lanes;                   // the packed weights: entries per output channel, lanes a position
+    uint32_t cs, cn, gs, wrap;
+    int32_t lo, hi;
+};
+
+template <uint32_t NP>                        // tap pairs, a multiple of 4 (16-byte LDS reads)
+__global__ __launch_bounds__(256) void conv_small_kernel(ConvSmall c) {
+    __shared__ __attribute__((aligned(16))) uint32_t wl[kCsOg][NP];
+    __shared__ int32_t bl[kCsOg];
+    __shared__ uint32_t exact[kCsOg];
+    __shared__ int4 tapt[2 * NP];             // per tap: element offset, row and column offset, valid
+    const uint32_t t = threadIdx.x, plane = c.out_h * c.out_w, taps = c.in_ch * c.kh * c.kw;
+    const uint32_t oc0 = blockIdx.y * kCsOg, nb = blockIdx.z;
+    const uint32_t og = min(kCsOg, c.out_ch - oc0);
+    // the group's weights as int16 pairs in tap order (ci, a, b), zero past the taps
+    for (uint32_t i = t; i < kCsOg * NP; i += 256) {
+        const uint32_t o = i / NP, pr = i - o * NP;
+        uint32_t v = 0;
+#pragma unroll
+        for (uint32_t h = 0; h < 2; h++) {
+            const uint32_t tp = 2 * pr + h;
+            if (o < og && tp < taps) {
+                const uint32_t ci = tp / (c.kh * c.kw), pos = tp - ci * c.kh * c.kw;
+                v |= (uint32_t)(uint16_t)c.w[(uint64_t)(oc0 + o) * c.per_m + pos * c.lanes + ci] << (16 * h);
+            }
+        }
+        wl[o][pr] = v;
+    }
+    if (t < kCsOg) {
+        int32_t b = 0;
+        uint64_t bound = 0;
+        if (t < og) {
+            b = c.bias ? (int32_t)c.bias[oc0 + t] : 0;
+            for (uint32_t tp = 0; tp < taps; tp++) {
+                const uint32_t ci = tp / (c.kh * c.kw), pos = tp - ci * c.kh * c.kw;
+                const int32_t wv = c.w[(uint64_t)(oc0 + t) * c.per_m + pos * c.lanes + ci];
+                bound += (uint64_t)(wv < 0 ? -wv : wv) << 15;
+            }
+            bound += (uint64_t)(b < 0 ? -b : b) << 8;
+        }
+        bl[t] = b;
+        exact[t] = c.wrap || bound < ((uint64_t)1 << 31);
+    }
+    for (uint32_t tp = t; tp < 2 * NP; tp += 256) {
+        int4 e = make_int4(0, 0, 0, 0);
+        if (tp < taps) {
+            const uint32_t ci = tp / (c.kh * c.kw), pos = tp - ci * c.kh * c.kw, a = pos / c.kw, b = pos - a * c.kw;
+            const int dy = (int)(a * c.dh), dx = (int)(b * c.dw);
+            e = make_int4((int)(ci * c.in_h * c.in_w) + dy * (int)c.in_w + dx, dy, dx, 1);
+        }
+        tapt[tp] = e;
+    }
+    __syncthreads();
+    const uint32_t p = blockIdx.x * 256 + t;
+    if (p >= plane) return;
+    const uint32_t oh = p / c.out_w, ow = p - oh * c.out_w;
+    const int16_t* xb = c.x + (uint64_t)nb * c.in_ch * c.in_h * c.in_w;
+    // the taps from the table (every index a constant: xv stays in registers)
+    const int ih0 = (int)(oh * c.sh) - (int)c.pt, iw0 = (int)(ow * c.sw) - (int)c.pl;
+    const int64_t o0 = (int64_t)ih0 * c.in_w + iw0;
+    uint32_t xv[NP];
+#pragma unroll
+    for (uint32_t pr = 0; pr < NP; pr++) {
+        uint32_t v2 = 0;
+#pragma unroll
+        for (uint32_t h = 0; h < 2; h++) {
+            const int4 e = tapt[2 * pr + h];
+            const int ih = ih0 + e.y, iw = iw0 + e.z;
+            const bool in = e.w && ih >= 0 && ih < (int)c.in_h && iw >= 0 && iw < (int)c.in_w;
+            const uint32_t v = in ? (uint32_t)(uint16_t)xb[o0 + e.x] : 0u;
+            v2 |= v << (16 * h);
+        }
+        xv[pr] = v2;
+    }
+    typedef short v2s __attribute__((ext_vector_type(2)));
+    int16_t* yb = c.y + (uint64_t)nb * c.out_ch * plane + p;
+    for (uint32_t o = 0; o < og; o++) {
+        const uint32_t oc = oc0 + o;
+        int64_t q;
+        if (exact[o]) {
+            int32_t acc = (int32_t)((uint32_t)bl[o] << 8);
+#pragma unroll
+            for (uint32_t pr = 0; pr < NP; pr += 4) {
+                const uint4 wq = *reinterpret_cast<const uint4*>(&wl[o][pr]);
+                acc = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr]), __builtin_bit_cast(v2s, wq.x), acc, false);
+                if (pr + 1 < NP) acc = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr + 1]), __builtin_bit_cast(v2s, wq.y), acc, false);
+                if (pr + 2 < NP) acc = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr + 2]), __builtin_bit_cast(v2s, wq.z), acc, false);
+                if (pr + 3 < NP) acc = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr + 3]), __builtin_bit_cast(v2s, wq.w), acc, false);
+            }
+            q = acc >> 8;
+        } else {
+            long long acc = (long long)bl[o] * 256;
+#pragma unroll
+            for (uint32_t pr = 0; pr < NP; pr++) {
+                const uint32_t wv = wl[o][pr];
+                acc += (long long)(int16_t)(xv[pr] & 0xFFFF) * (int16_t)(wv & 0xFFFF) +
+                       (long long)(int16_t)(xv[pr] >> 16) * (int16_t)(wv >> 16);
+            }
+            q = acc >> 8;
+        }
+        const uint64_t base = c.cn ? (uint64_t)(oc % c.cn) * c.cs + (uint64_t)(oc / c.cn) * c.gs : (uint64_t)oc * c.cs;
+        yb[base] = (int16_t)(q > c.hi ? c.hi : (q < c.lo ? c.lo : q));
+    }
+}
+
 // ---------------------------------------------------------------- depthwise conv
 __global__ __launch_bounds__(256) void conv_dw_kernel(const int16_t* __restrict__ x,
                                                       const int16_t* __restrict__ w,
@@ -2186,6 +2310,22 @@ int conv_run(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y
                            dilation_w, pad_top, pad_left, (kh * kw + 7) & ~7u, cs, y_cn, y_gs,
                            wrap32 ? 1u : 0u, lo, hi);
         return CM_OK;
+    }
+    if (in_ch <= 16 && in_ch * kh * kw <= kCsMaxTaps && batch <= 65535 && (uint64_t)in_ch * in_h * in_w < (1ull << 31)) {
+        // few taps (one 16-channel tile of the packed weights): straight on the VALU
+        const uint32_t taps = in_ch * kh * kw, lanes = in_ch <= 8 ? 8u : 16u;
+        const uint32_t np = (uint32_t)round_up(ceil_div(taps, 2), 4);
+        const ConvSmall cv{x, w, bptr, y, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w,
+                           dilation_h, dilation_w, pad_top, pad_left, kh * kw * lanes, lanes, cs, y_cn, y_gs,
+                           wrap32 ? 1u : 0u, lo, hi};
+        const dim3 grid(ceil_div(plane, 256), ceil_div(out_ch, kCsOg), batch);
+#define CM_CS(NP_) \
+    case NP_: CM_LAUNCH("conv_small_kernel", conv_small_kernel<NP_>, grid, dim3(256), 0, s, cv); return CM_OK;
+        switch (np) {
+            CM_CS(4) CM_CS(8) CM_CS(12) CM_CS(16) CM_CS(20) CM_CS(24) CM_CS(28) CM_CS(32) CM_CS(36) CM_CS(40)
+        default: break;
+        }
+#undef CM_CS
     }
     if ((uint64_t)in_ch * kh * kw > 32768)
         return fail(CM_EINVAL, "conv: in_ch * kh * kw = %u above 32768", in_ch * kh * kw);

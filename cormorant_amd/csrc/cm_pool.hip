@@ -120,20 +120,17 @@ __global__ __launch_bounds__(64) void pool_global_small_kernel(const int16_t* __
     const uint32_t np = (uint32_t)(planes - p0 < 64 ? planes - p0 : 64);
     const int16_t* xs = x + p0 * hw;
     if (np == 64 && aligned16(x)) {
-        // 64 whole planes: 8 hw 16-byte words (128 hw bytes from a 16-byte aligned start), all
-        // loads in flight before the LDS writes
+        // 64 whole planes: 8 hw 16-byte words (128 hw bytes from a 16-byte aligned start), copied
+        // straight into LDS (global_load_lds: every copy in flight at once, no registers)
         const uint32_t n4 = 8 * hw;
-        int4 v[kSmallPlane / 8];
 #pragma unroll
         for (uint32_t u = 0; u < kSmallPlane / 8; u++) {
             const uint32_t i = threadIdx.x + 64 * u;
-            if (i < n4) v[u] = reinterpret_cast<const int4*>(xs)[i];
+            if (i < n4)
+                __builtin_amdgcn_global_load_lds(xs + 8 * i, (__attribute__((address_space(3))) void*)(buf + 8 * 64 * u),
+                                                 16, 0, 0);
         }
-#pragma unroll
-        for (uint32_t u = 0; u < kSmallPlane / 8; u++) {
-            const uint32_t i = threadIdx.x + 64 * u;
-            if (i < n4) reinterpret_cast<int4*>(buf)[i] = v[u];
-        }
+        __builtin_amdgcn_s_waitcnt(0x0070);
     } else {
         for (uint32_t i = threadIdx.x; i < np * hw; i += 64) buf[i] = xs[i];
     }

@@ -408,6 +408,12 @@ def conv_y_extent(batch, out_ch, out_h, out_w, y_cs=0, y_cn=0, y_gs=0) -> int:
     return (batch - 1) * out_ch * plane + (out_ch - 1) * cs + plane
 
 
+def conv_small(in_ch: int, kh: int, kw: int, batch: int = 1) -> bool:
+    """A standard convolution cm_conv runs straight on the VALU (its packed weights as they are,
+    no GEMM operand): at most 16 input channels and 80 taps per output, batch up to 65535."""
+    return in_ch <= 16 and in_ch * kh * kw <= 80 and batch <= 65535
+
+
 def conv(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], y: torch.Tensor,
          batch: int, in_ch: int, in_h: int, in_w: int, out_ch: int, out_h: int, out_w: int,
          kh: int, kw: int, stride_h: int = 1, stride_w: int = 1, dilation_h: int = 1,

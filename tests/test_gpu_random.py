@@ -530,6 +530,16 @@ CONV_CASES = [  # batch, C, H, W, M, kh, kw, sh, sw, dh, dw, pt, pl, pb, pr, bia
     # folded 1x1 with 2^16 lines and more (the LDS-tiled split): an even and an odd plane
     (4, 24, 128, 128, 40, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 1, 0, False, False),
     (3, 20, 151, 149, 24, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 0, 0, True, False),
+    # few taps (at most 16 channels, 80 taps): straight on the VALU -- MobileNetV2's stem, the
+    # small CNN's first layer, 7x7 over one channel with asymmetric pads (int64 sums), dilation
+    # and wrap with 33 output channels, a wide plane, exactly 80 taps, 64 taps full range wrapped
+    (4, 3, 224, 224, 32, 3, 3, 2, 2, 1, 1, 1, 1, 1, 1, 1, 0, False, False),
+    (2, 1, 28, 28, 8, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1, 1, 0, False, False),
+    (1, 1, 20, 23, 20, 7, 7, 1, 2, 1, 1, 3, 2, 3, 4, 1, 0, True, False),
+    (3, 8, 15, 14, 33, 3, 3, 2, 1, 2, 1, 2, 1, 0, 2, 1, 0, False, True),
+    (1, 4, 9, 300, 5, 1, 3, 1, 3, 1, 2, 0, 2, 0, 2, 1, 0, True, False),
+    (2, 5, 11, 11, 16, 4, 4, 3, 3, 1, 1, 0, 0, 1, 1, 0, 0, False, False),
+    (2, 16, 12, 12, 7, 2, 2, 2, 2, 1, 1, 0, 0, 0, 0, 1, 0, True, True),
 ]
 
 
