@@ -960,7 +960,8 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
 // otherwise; then floor(acc / 2^8) clamped to [lo, hi] (saturation and a fused RELU / RELU6),
 // as the GEMM path stores it.  w in the packed layout of cm_conv (ConvKernel.h:136-159).
 constexpr uint32_t kCsMaxTaps = 80;          // taps a lane holds (40 pairs)
-constexpr uint32_t kCsOg = 16;               // output channels of a workgroup
+constexpr uint32_t kCsOg = 16;               // output channels of a workgroup (4 at a time)
+constexpr uint32_t kCsPix = 1;               // output pixels of a lane (256 apart)
 
 struct ConvSmall {
     const int16_t* x;
@@ -977,12 +978,14 @@ template <uint32_t NP>                        // tap pairs, a multiple of 4 (16-
 __global__ __launch_bounds__(256) void conv_small_kernel(ConvSmall c) {
     __shared__ __attribute__((aligned(16))) uint32_t wl[kCsOg][NP];
     __shared__ int32_t bl[kCsOg];
-    __shared__ uint32_t exact[kCsOg];
+    __shared__ uint32_t exact[kCsOg], exact4[kCsOg / 4];
+    __shared__ uint64_t ybase[kCsOg];         // a channel's offset in the output (the y pattern)
     __shared__ int4 tapt[2 * NP];             // per tap: element offset, row and column offset, valid
-    const uint32_t t = threadIdx.x, plane = c.out_h * c.out_w, taps = c.in_ch * c.kh * c.kw;
+    const uint32_t t = threadIdx.x, plane = c.out_h * c.out_w, taps = c.in_ch * c.kh * c.kw, khw = c.kh * c.kw;
     const uint32_t oc0 = blockIdx.y * kCsOg, nb = blockIdx.z;
     const uint32_t og = min(kCsOg, c.out_ch - oc0);
-    // the group's weights as int16 pairs in tap order (ci, a, b), zero past the taps
+    // the group's weights as int16 pairs in tap order (ci, a, b), zero past the taps; the taps'
+    // offsets from a pixel's window origin
     for (uint32_t i = t; i < kCsOg * NP; i += 256) {
         const uint32_t o = i / NP, pr = i - o * NP;
         uint32_t v = 0;
@@ -990,86 +993,105 @@ __global__ __launch_bounds__(256) void conv_small_kernel(ConvSmall c) {
         for (uint32_t h = 0; h < 2; h++) {
             const uint32_t tp = 2 * pr + h;
             if (o < og && tp < taps) {
-                const uint32_t ci = tp / (c.kh * c.kw), pos = tp - ci * c.kh * c.kw;
+                const uint32_t ci = tp / khw, pos = tp - ci * khw;
                 v |= (uint32_t)(uint16_t)c.w[(uint64_t)(oc0 + o) * c.per_m + pos * c.lanes + ci] << (16 * h);
             }
         }
         wl[o][pr] = v;
     }
-    if (t < kCsOg) {
-        int32_t b = 0;
-        uint64_t bound = 0;
-        if (t < og) {
-            b = c.bias ? (int32_t)c.bias[oc0 + t] : 0;
-            for (uint32_t tp = 0; tp < taps; tp++) {
-                const uint32_t ci = tp / (c.kh * c.kw), pos = tp - ci * c.kh * c.kw;
-                const int32_t wv = c.w[(uint64_t)(oc0 + t) * c.per_m + pos * c.lanes + ci];
-                bound += (uint64_t)(wv < 0 ? -wv : wv) << 15;
-            }
-            bound += (uint64_t)(b < 0 ? -b : b) << 8;
-        }
-        bl[t] = b;
-        exact[t] = c.wrap || bound < ((uint64_t)1 << 31);
-    }
     for (uint32_t tp = t; tp < 2 * NP; tp += 256) {
         int4 e = make_int4(0, 0, 0, 0);
         if (tp < taps) {
-            const uint32_t ci = tp / (c.kh * c.kw), pos = tp - ci * c.kh * c.kw, a = pos / c.kw, b = pos - a * c.kw;
+            const uint32_t ci = tp / khw, pos = tp - ci * khw, a = pos / c.kw, b = pos - a * c.kw;
             const int dy = (int)(a * c.dh), dx = (int)(b * c.dw);
             e = make_int4((int)(ci * c.in_h * c.in_w) + dy * (int)c.in_w + dx, dy, dx, 1);
         }
         tapt[tp] = e;
     }
+    if (t < kCsOg) bl[t] = t < og && c.bias ? (int32_t)c.bias[oc0 + t] : 0;
     __syncthreads();
-    const uint32_t p = blockIdx.x * 256 + t;
-    if (p >= plane) return;
-    const uint32_t oh = p / c.out_w, ow = p - oh * c.out_w;
-    const int16_t* xb = c.x + (uint64_t)nb * c.in_ch * c.in_h * c.in_w;
-    // the taps from the table (every index a constant: xv stays in registers)
-    const int ih0 = (int)(oh * c.sh) - (int)c.pt, iw0 = (int)(ow * c.sw) - (int)c.pl;
-    const int64_t o0 = (int64_t)ih0 * c.in_w + iw0;
-    uint32_t xv[NP];
-#pragma unroll
-    for (uint32_t pr = 0; pr < NP; pr++) {
-        uint32_t v2 = 0;
-#pragma unroll
-        for (uint32_t h = 0; h < 2; h++) {
-            const int4 e = tapt[2 * pr + h];
-            const int ih = ih0 + e.y, iw = iw0 + e.z;
-            const bool in = e.w && ih >= 0 && ih < (int)c.in_h && iw >= 0 && iw < (int)c.in_w;
-            const uint32_t v = in ? (uint32_t)(uint16_t)xb[o0 + e.x] : 0u;
-            v2 |= v << (16 * h);
+    if (t < kCsOg) {
+        // int32 is exact when sum |w| 2^15 + |bias| 2^8 < 2^31 (and always for the wrap rule)
+        uint64_t bound = (uint64_t)(bl[t] < 0 ? -bl[t] : bl[t]) << 8;
+        for (uint32_t pr = 0; pr < NP; pr++) {
+            const int32_t w0 = (int16_t)(wl[t][pr] & 0xFFFF), w1 = (int16_t)(wl[t][pr] >> 16);
+            bound += (uint64_t)((w0 < 0 ? -w0 : w0) + (w1 < 0 ? -w1 : w1)) << 15;
         }
-        xv[pr] = v2;
+        exact[t] = c.wrap || bound < ((uint64_t)1 << 31);
+        const uint32_t oc = oc0 + t;
+        ybase[t] = c.cn ? (uint64_t)(oc % c.cn) * c.cs + (uint64_t)(oc / c.cn) * c.gs : (uint64_t)oc * c.cs;
     }
+    __syncthreads();
+    if (t < kCsOg / 4) exact4[t] = exact[4 * t] & exact[4 * t + 1] & exact[4 * t + 2] & exact[4 * t + 3];
+    __syncthreads();
     typedef short v2s __attribute__((ext_vector_type(2)));
-    int16_t* yb = c.y + (uint64_t)nb * c.out_ch * plane + p;
-    for (uint32_t o = 0; o < og; o++) {
-        const uint32_t oc = oc0 + o;
-        int64_t q;
-        if (exact[o]) {
-            int32_t acc = (int32_t)((uint32_t)bl[o] << 8);
+    const int16_t* xb = c.x + (uint64_t)nb * c.in_ch * c.in_h * c.in_w;
+#pragma unroll 1
+    for (uint32_t i = 0; i < kCsPix; i++) {                // one pixel's taps in registers at a time
+        const uint32_t p = blockIdx.x * 256 * kCsPix + 256 * i + t;
+        if (p >= plane) break;
+        const uint32_t oh = p / c.out_w, ow = p - oh * c.out_w;
+        // the taps from the table (every index into xv a constant: it stays in registers); the
+        // table is read per pixel (an opaque zero in its index), not held in registers across
+        // the pixels
+        const int ih0 = (int)(oh * c.sh) - (int)c.pt, iw0 = (int)(ow * c.sw) - (int)c.pl;
+        const int64_t o0 = (int64_t)ih0 * c.in_w + iw0;
+        uint32_t z = i;
+        __asm__ volatile("" : "+v"(z));
+        z &= 0u;
+        uint32_t xv[NP];
 #pragma unroll
-            for (uint32_t pr = 0; pr < NP; pr += 4) {
-                const uint4 wq = *reinterpret_cast<const uint4*>(&wl[o][pr]);
-                acc = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr]), __builtin_bit_cast(v2s, wq.x), acc, false);
-                if (pr + 1 < NP) acc = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr + 1]), __builtin_bit_cast(v2s, wq.y), acc, false);
-                if (pr + 2 < NP) acc = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr + 2]), __builtin_bit_cast(v2s, wq.z), acc, false);
-                if (pr + 3 < NP) acc = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr + 3]), __builtin_bit_cast(v2s, wq.w), acc, false);
-            }
-            q = acc >> 8;
-        } else {
-            long long acc = (long long)bl[o] * 256;
+        for (uint32_t pr = 0; pr < NP; pr++) {
+            uint32_t v2 = 0;
 #pragma unroll
-            for (uint32_t pr = 0; pr < NP; pr++) {
-                const uint32_t wv = wl[o][pr];
-                acc += (long long)(int16_t)(xv[pr] & 0xFFFF) * (int16_t)(wv & 0xFFFF) +
-                       (long long)(int16_t)(xv[pr] >> 16) * (int16_t)(wv >> 16);
+            for (uint32_t h = 0; h < 2; h++) {
+                const int4 e = tapt[2 * pr + h + z];
+                const int ih = ih0 + e.y, iw = iw0 + e.z;
+                const bool in = e.w && ih >= 0 && ih < (int)c.in_h && iw >= 0 && iw < (int)c.in_w;
+                const uint32_t v = in ? (uint32_t)(uint16_t)xb[o0 + e.x] : 0u;
+                v2 |= v << (16 * h);
             }
-            q = acc >> 8;
+            xv[pr] = v2;
         }
-        const uint64_t base = c.cn ? (uint64_t)(oc % c.cn) * c.cs + (uint64_t)(oc / c.cn) * c.gs : (uint64_t)oc * c.cs;
-        yb[base] = (int16_t)(q > c.hi ? c.hi : (q < c.lo ? c.lo : q));
+        int16_t* yb = c.y + (uint64_t)nb * c.out_ch * plane + p;
+        // four channels at a time: four independent sums (channels past og have zero weights,
+        // their stores are skipped)
+        for (uint32_t o = 0; o < og; o += 4) {
+            int64_t q[4];
+            if (exact4[o / 4]) {
+                int32_t acc[4];
+#pragma unroll
+                for (uint32_t j = 0; j < 4; j++) acc[j] = (int32_t)((uint32_t)bl[o + j] << 8);
+#pragma unroll
+                for (uint32_t pr = 0; pr < NP; pr += 4) {
+#pragma unroll
+                    for (uint32_t j = 0; j < 4; j++) {
+                        const uint4 wq = *reinterpret_cast<const uint4*>(&wl[o + j][pr]);
+                        acc[j] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr]), __builtin_bit_cast(v2s, wq.x), acc[j], false);
+                        acc[j] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr + 1]), __builtin_bit_cast(v2s, wq.y), acc[j], false);
+                        acc[j] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr + 2]), __builtin_bit_cast(v2s, wq.z), acc[j], false);
+                        acc[j] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr + 3]), __builtin_bit_cast(v2s, wq.w), acc[j], false);
+                    }
+                }
+#pragma unroll
+                for (uint32_t j = 0; j < 4; j++) q[j] = acc[j] >> 8;
+            } else {
+#pragma unroll
+                for (uint32_t j = 0; j < 4; j++) {
+                    long long acc = (long long)bl[o + j] * 256;
+#pragma unroll
+                    for (uint32_t pr = 0; pr < NP; pr++) {
+                        const uint32_t wv = wl[o + j][pr];
+                        acc += (long long)(int16_t)(xv[pr] & 0xFFFF) * (int16_t)(wv & 0xFFFF) +
+                               (long long)(int16_t)(xv[pr] >> 16) * (int16_t)(wv >> 16);
+                    }
+                    q[j] = acc >> 8;
+                }
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < 4; j++)
+                if (o + j < og) yb[ybase[o + j]] = (int16_t)(q[j] > c.hi ? c.hi : (q[j] < c.lo ? c.lo : q[j]));
+        }
     }
 }
 
@@ -2318,7 +2340,7 @@ int conv_run(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y
         const ConvSmall cv{x, w, bptr, y, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w,
                            dilation_h, dilation_w, pad_top, pad_left, kh * kw * lanes, lanes, cs, y_cn, y_gs,
                            wrap32 ? 1u : 0u, lo, hi};
-        const dim3 grid(ceil_div(plane, 256), ceil_div(out_ch, kCsOg), batch);
+        const dim3 grid(ceil_div(plane, 256 * kCsPix), ceil_div(out_ch, kCsOg), batch);
 #define CM_CS(NP_) \
     case NP_: CM_LAUNCH("conv_small_kernel", conv_small_kernel<NP_>, grid, dim3(256), 0, s, cv); return CM_OK;
         switch (np) {
