@@ -950,9 +950,11 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
 }
 
 // ---------------------------------------------------------------- standard conv, few taps
-// A standard convolution whose taps per output (in_ch kh kw) are few -- a network's stem over
-// its 1 .. 4 input channels -- straight on the VALU instead of im2col + GEMM (which would pad
-// each kernel position to 16 channels): a lane per output pixel over OG output channels, its
+// A standard convolution whose taps per output (in_ch kh kw <= 80) are few -- a network's stem
+// over its 1 .. 4 input channels, the 1x1 convolutions of up to 80 channels -- straight on the
+// VALU instead of im2col + GEMM (which would pad each kernel position to 16 channels, and
+// whose folded 1x1 operand costs a transposing split; such products are bound by their output
+// bytes, not by the multiplies): a lane per output pixel over OG output channels, its
 // taps gathered once (zero outside the input) and packed in pairs, each channel's sum by
 // v_dot2_i32_i16 against the channel's pairs staged in LDS (read by every lane at one
 // address).  The sum is int32 where that is exact -- the wrap path (the int32 wrap is its
@@ -960,6 +962,9 @@ __global__ __launch_bounds__(128 * WR, WR == 1 ? 1 : 8 / (2 * WR)) void gemm_pla
 // otherwise; then floor(acc / 2^8) clamped to [lo, hi] (saturation and a fused RELU / RELU6),
 // as the GEMM path stores it.  w in the packed layout of cm_conv (ConvKernel.h:136-159).
 constexpr uint32_t kCsMaxTaps = 80;          // taps a lane holds (40 pairs)
+// taps x output channels up to which the VALU path beats the GEMM's (measured on MobileNetV2's
+// 1x1 shapes: 32 x 192 at 28^2 pixels 18 vs 21 us, 64 x 384 at 14^2 21 vs 17 us)
+constexpr uint64_t kCsMaxWork = 12288;
 constexpr uint32_t kCsOg = 16;               // output channels of a workgroup (4 at a time)
 constexpr uint32_t kCsPix = 1;               // output pixels of a lane (256 apart)
 
@@ -969,7 +974,8 @@ struct ConvSmall {
     const int16_t* bias;
     int16_t* y;
     uint32_t in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, sh, sw, dh, dw, pt, pl;
-    uint32_t per_m, lanes;                   // the packed weights: entries per output channel, lanes a position
+    uint32_t per_m, tiles, last;             // the packed weights: entries per output channel, 16-channel
+                                             // tiles, lanes of a position in the last tile
     uint32_t cs, cn, gs, wrap;
     int32_t lo, hi;
 };
@@ -993,8 +999,10 @@ __global__ __launch_bounds__(256) void conv_small_kernel(ConvSmall c) {
         for (uint32_t h = 0; h < 2; h++) {
             const uint32_t tp = 2 * pr + h;
             if (o < og && tp < taps) {
-                const uint32_t ci = tp / khw, pos = tp - ci * khw;
-                v |= (uint32_t)(uint16_t)c.w[(uint64_t)(oc0 + o) * c.per_m + pos * c.lanes + ci] << (16 * h);
+                const uint32_t ci = tp / khw, pos = tp - ci * khw, ict = ci >> 4;
+                const uint32_t lanes = ict + 1 == c.tiles ? c.last : 16u;
+                v |= (uint32_t)(uint16_t)c.w[(uint64_t)(oc0 + o) * c.per_m + ict * khw * 16 + pos * lanes + (ci & 15)]
+                     << (16 * h);
             }
         }
         wl[o][pr] = v;
@@ -2333,13 +2341,15 @@ int conv_run(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y
                            wrap32 ? 1u : 0u, lo, hi);
         return CM_OK;
     }
-    if (in_ch <= 16 && in_ch * kh * kw <= kCsMaxTaps && batch <= 65535 && (uint64_t)in_ch * in_h * in_w < (1ull << 31)) {
-        // few taps (one 16-channel tile of the packed weights): straight on the VALU
-        const uint32_t taps = in_ch * kh * kw, lanes = in_ch <= 8 ? 8u : 16u;
+    if (in_ch * kh * kw <= kCsMaxTaps && (uint64_t)in_ch * kh * kw * out_ch <= kCsMaxWork && batch <= 65535 &&
+        (uint64_t)in_ch * in_h * in_w < (1ull << 31)) {
+        // few taps: straight on the VALU
+        const uint32_t taps = in_ch * kh * kw, tiles = (in_ch + 15) / 16;
+        const uint32_t rem = in_ch - (tiles - 1) * 16, last = rem <= 8 ? 8u : 16u;
         const uint32_t np = (uint32_t)round_up(ceil_div(taps, 2), 4);
         const ConvSmall cv{x, w, bptr, y, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w,
-                           dilation_h, dilation_w, pad_top, pad_left, kh * kw * lanes, lanes, cs, y_cn, y_gs,
-                           wrap32 ? 1u : 0u, lo, hi};
+                           dilation_h, dilation_w, pad_top, pad_left, kh * kw * ((tiles - 1) * 16 + last), tiles, last,
+                           cs, y_cn, y_gs, wrap32 ? 1u : 0u, lo, hi};
         const dim3 grid(ceil_div(plane, 256 * kCsPix), ceil_div(out_ch, kCsOg), batch);
 #define CM_CS(NP_) \
     case NP_: CM_LAUNCH("conv_small_kernel", conv_small_kernel<NP_>, grid, dim3(256), 0, s, cv); return CM_OK;

@@ -925,7 +925,7 @@ class Simulator:
         if img is None:
             w = self._get(wt, raw).cpu().numpy().reshape(wt.shape)
             img = torch.from_numpy(conv_weight_image(w, sn.is_depthwise)).to(self.device)
-            if not sn.is_depthwise and wt.data is not None and not units.conv_small(sn.in_ch, sn.kh, sn.kw, sn.batch):
+            if not sn.is_depthwise and wt.data is not None and not units.conv_small(sn.in_ch, sn.kh, sn.kw, sn.out_ch, sn.batch):
                 # a constant weight of a standard convolution on the GEMM: its operand split once
                 img = units.conv_w_planes(img, sn.out_ch, sn.in_ch, sn.kh, sn.kw)
             self._images[wt.onnx_name] = img

@@ -408,10 +408,11 @@ def conv_y_extent(batch, out_ch, out_h, out_w, y_cs=0, y_cn=0, y_gs=0) -> int:
     return (batch - 1) * out_ch * plane + (out_ch - 1) * cs + plane
 
 
-def conv_small(in_ch: int, kh: int, kw: int, batch: int = 1) -> bool:
+def conv_small(in_ch: int, kh: int, kw: int, out_ch: int, batch: int = 1) -> bool:
     """A standard convolution cm_conv runs straight on the VALU (its packed weights as they are,
-    no GEMM operand): at most 16 input channels and 80 taps per output, batch up to 65535."""
-    return in_ch <= 16 and in_ch * kh * kw <= 80 and batch <= 65535
+    no GEMM operand): at most 80 taps (in_ch kh kw) per output and 12288 taps x output
+    channels, batch up to 65535."""
+    return in_ch * kh * kw <= 80 and in_ch * kh * kw * out_ch <= 12288 and batch <= 65535
 
 
 def conv(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], y: torch.Tensor,

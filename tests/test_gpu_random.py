@@ -540,6 +540,11 @@ CONV_CASES = [  # batch, C, H, W, M, kh, kw, sh, sw, dh, dw, pt, pl, pb, pr, bia
     (1, 4, 9, 300, 5, 1, 3, 1, 3, 1, 2, 0, 2, 0, 2, 1, 0, True, False),
     (2, 5, 11, 11, 16, 4, 4, 3, 3, 1, 1, 0, 0, 1, 1, 0, 0, False, False),
     (2, 16, 12, 12, 7, 2, 2, 2, 2, 1, 1, 0, 0, 0, 0, 1, 0, True, True),
+    # 1x1 over several 16-channel tiles of the packed weights (a last tile of 8 and of 16 lanes)
+    (2, 32, 20, 20, 16, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 1, 0, False, False),
+    (3, 40, 9, 10, 50, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 1, 0, True, False),
+    (1, 80, 7, 7, 130, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 0, 0, True, True),
+    (2, 20, 9, 9, 24, 2, 2, 1, 1, 1, 1, 1, 0, 0, 1, 1, 0, False, False),
 ]
 
 
