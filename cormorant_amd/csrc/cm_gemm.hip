@@ -980,7 +980,9 @@ struct ConvSmall {
     int32_t lo, hi;
 };
 
-template <uint32_t NP>                        // tap pairs, a multiple of 4 (16-byte LDS reads)
+// PW: a pointwise convolution (1x1, stride 1, no padding, the output plane the input's): the
+// lane's taps are its pixel in each input channel, loaded before the weights are staged.
+template <uint32_t NP, bool PW>                // tap pairs, a multiple of 4 (16-byte LDS reads)
 __global__ __launch_bounds__(256) void conv_small_kernel(ConvSmall c) {
     __shared__ __attribute__((aligned(16))) uint32_t wl[kCsOg][NP];
     __shared__ int32_t bl[kCsOg];
@@ -990,6 +992,18 @@ __global__ __launch_bounds__(256) void conv_small_kernel(ConvSmall c) {
     const uint32_t t = threadIdx.x, plane = c.out_h * c.out_w, taps = c.in_ch * c.kh * c.kw, khw = c.kh * c.kw;
     const uint32_t oc0 = blockIdx.y * kCsOg, nb = blockIdx.z;
     const uint32_t og = min(kCsOg, c.out_ch - oc0);
+    const int16_t* xb = c.x + (uint64_t)nb * c.in_ch * c.in_h * c.in_w;
+    uint32_t xw[PW ? NP : 1];
+    static_assert(!PW || kCsPix == 1, "the pointwise taps are the lane's one pixel");
+    if constexpr (PW) {
+        const uint32_t p = blockIdx.x * 256 + t;
+#pragma unroll
+        for (uint32_t pr = 0; pr < NP; pr++) {
+            const uint32_t lo = p < plane && 2 * pr < taps ? (uint32_t)(uint16_t)xb[(uint64_t)(2 * pr) * plane + p] : 0u;
+            const uint32_t hi = p < plane && 2 * pr + 1 < taps ? (uint32_t)(uint16_t)xb[(uint64_t)(2 * pr + 1) * plane + p] : 0u;
+            xw[pr] = lo | (hi << 16);
+        }
+    }
     // the group's weights as int16 pairs in tap order (ci, a, b), zero past the taps; the taps'
     // offsets from a pixel's window origin
     for (uint32_t i = t; i < kCsOg * NP; i += 256) {
@@ -1033,7 +1047,6 @@ __global__ __launch_bounds__(256) void conv_small_kernel(ConvSmall c) {
     if (t < kCsOg / 4) exact4[t] = exact[4 * t] & exact[4 * t + 1] & exact[4 * t + 2] & exact[4 * t + 3];
     __syncthreads();
     typedef short v2s __attribute__((ext_vector_type(2)));
-    const int16_t* xb = c.x + (uint64_t)nb * c.in_ch * c.in_h * c.in_w;
 #pragma unroll 1
     for (uint32_t i = 0; i < kCsPix; i++) {                // one pixel's taps in registers at a time
         const uint32_t p = blockIdx.x * 256 * kCsPix + 256 * i + t;
@@ -1050,6 +1063,10 @@ __global__ __launch_bounds__(256) void conv_small_kernel(ConvSmall c) {
         uint32_t xv[NP];
 #pragma unroll
         for (uint32_t pr = 0; pr < NP; pr++) {
+            if constexpr (PW) {
+                xv[pr] = xw[pr];
+                continue;
+            }
             uint32_t v2 = 0;
 #pragma unroll
             for (uint32_t h = 0; h < 2; h++) {
@@ -2351,8 +2368,13 @@ int conv_run(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y
                            dilation_h, dilation_w, pad_top, pad_left, kh * kw * ((tiles - 1) * 16 + last), tiles, last,
                            cs, y_cn, y_gs, wrap32 ? 1u : 0u, lo, hi};
         const dim3 grid(ceil_div(plane, 256 * kCsPix), ceil_div(out_ch, kCsOg), batch);
-#define CM_CS(NP_) \
-    case NP_: CM_LAUNCH("conv_small_kernel", conv_small_kernel<NP_>, grid, dim3(256), 0, s, cv); return CM_OK;
+        const bool pw = kh == 1 && kw == 1 && stride_h == 1 && stride_w == 1 && pad_top == 0 && pad_left == 0 &&
+                        in_h == out_h && in_w == out_w;
+#define CM_CS(NP_)                                                                                              \
+    case NP_:                                                                                                   \
+        if (pw) { CM_LAUNCH("conv_small_kernel", (conv_small_kernel<NP_, true>), grid, dim3(256), 0, s, cv); }   \
+        else { CM_LAUNCH("conv_small_kernel", (conv_small_kernel<NP_, false>), grid, dim3(256), 0, s, cv); }     \
+        return CM_OK;
         switch (np) {
             CM_CS(4) CM_CS(8) CM_CS(12) CM_CS(16) CM_CS(20) CM_CS(24) CM_CS(28) CM_CS(32) CM_CS(36) CM_CS(40)
         default: break;
