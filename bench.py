@@ -212,20 +212,21 @@ GRAPH_KERNELS = ("gemm_planes_kernel", "split_rows_kernel", "split_cols_kernel",
                  "split_fold_kernel", "split_fold_lds_kernel", "skinny_wrap_kernel", "skinny_reduce_kernel",
                  "skinny_planes_kernel", "skinny_mulact_kernel", "decode_attn_kernel", "decode_prep_kernel",
                  "attention_kernel", "embed_rows_kernel", "ro_fold_kernel",
-                 "ro_tload_kernel", "ro_xpose_kernel")
+                 "ro_tload_kernel", "ro_xpose_kernel", "conv_small_kernel")
 
 
 TIMED_REPLAYS = 10      # replays of the instrumented graph whose per-launch events are read
 
 
-def run_graph(args, torch, sim, feeds, out_name):
+def run_graph(args, torch, sim, feeds, out_name, each=()):
     """Warm the simulator up, capture the forward as a HIP graph and time ``args.steps``
     replays after ``args.warmup`` (the step time).  Then capture the same forward a second time
     with a HIP event pair around every kernel launch -- on a stream under capture the pairs are
     event-record nodes of the graph, re-recorded by each replay -- and read them after each of
     TIMED_REPLAYS replays, each run right after three replays of the plain graph so that the GPU
     is in the same loaded state as in the timed region.  Returns (ms per step, {kernel: {ms per
-    step (mean over the instrumented replays), launches per step}}, the output tensor)."""
+    step (mean over the instrumented replays), launches per step}}, the output tensor); with
+    ``each``, per_kernel[name]["each"] for those kernels: every launch's mean ms, in launch order."""
     from cormorant_amd import _lib
     keep = [out_name]                         # the step's result; intermediates only the GEMMs read stay unwritten
     for _ in range(2):                        # weights, packed images, tables, workspace
@@ -269,7 +270,7 @@ def run_graph(args, torch, sim, feeds, out_name):
             sim.forward_raw(feeds, keep=keep)
     finally:
         _lib.timing_enable(False)
-    acc = {}
+    acc, acc_each = {}, {}
     for _ in range(TIMED_REPLAYS):
         for _ in range(3):
             hg.replay()
@@ -280,9 +281,16 @@ def run_graph(args, torch, sim, feeds, out_name):
             if n_k:
                 a = acc.setdefault(k, [0.0, n_k])
                 a[0] += ms_k
+        for k in each:
+            e = _lib.timing_read_each(k)
+            a = acc_each.setdefault(k, [0.0] * len(e))
+            for i, v in enumerate(e):
+                a[i] += v
     _lib.timing_reset()
     del hg_t
     per_kernel = {k: {"ms": round(v[0] / TIMED_REPLAYS, 4), "launches": v[1]} for k, v in acc.items()}
+    for k, v in acc_each.items():
+        per_kernel.setdefault(k, {"ms": 0.0, "launches": 0})["each"] = [x / TIMED_REPLAYS for x in v]
     return ms, per_kernel, out
 
 
@@ -396,6 +404,88 @@ def bert_bench(args, torch, np):
 
 
 # ---------------------------------------------------------------- config 3: MobileNetV2, batch 32
+def conv_macs(sn) -> int:
+    return sn.batch * sn.out_ch * sn.out_h * sn.out_w * sn.kh * sn.kw * (1 if sn.is_depthwise else sn.in_ch)
+
+
+def conv_pointwise(sn) -> bool:
+    return (sn.kh == sn.kw == sn.stride_h == sn.stride_w == 1 and sn.pad_top == sn.pad_left == 0
+            and (sn.in_h, sn.in_w) == (sn.out_h, sn.out_w))
+
+
+def conv_on_gemm(sn) -> bool:
+    """A convolution the library runs on the plane GEMM (not depthwise, not a few-tap one)."""
+    from cormorant_amd import units
+    return not sn.is_depthwise and not units.conv_small(sn.in_ch, sn.kh, sn.kw, sn.out_ch, sn.batch)
+
+
+def write_conv_roofline(path, g, per_kernel, batch, ms):
+    """A markdown table of every convolution and product launch of one forward against its own
+    roofline: the GEMM launches (and the fold split before each folded 1x1) against
+    max(i8-MFMA time, HBM time) of their algorithmic work and bytes, the few-tap convolutions
+    (VALU) against their HBM time.  Algorithmic bytes: each operand once at int16, the output
+    once.  The i-th GEMM / fold / few-tap launch is the i-th node of the graph that makes one."""
+    gemm = per_kernel.get("gemm_planes_kernel", {}).get("each", [])
+    fold = per_kernel.get("split_fold_kernel", {}).get("each", [])
+    small = per_kernel.get("conv_small_kernel", {}).get("each", [])
+    gi = fi = si = 0
+    rows = []
+    for sn in g.nodes:
+        kind = type(sn).__name__
+        if kind == "ConvNode" and not sn.is_depthwise:
+            n = sn.batch * sn.out_h * sn.out_w
+            k = sn.in_ch * sn.kh * sn.kw
+            byt = 2 * (sn.out_ch * k + sn.batch * sn.in_ch * sn.in_h * sn.in_w + sn.out_ch * n)
+            shape = f"{sn.in_ch}x{sn.in_h}x{sn.in_w} -> {sn.out_ch}, {sn.kh}x{sn.kw} s{sn.stride_h}"
+            if conv_on_gemm(sn):
+                split_us = None
+                if conv_pointwise(sn):
+                    split_us = fold[fi] * 1e3 if fi < len(fold) else float("nan")
+                    fi += 1
+                us = gemm[gi] * 1e3 if gi < len(gemm) else float("nan")
+                gi += 1
+                rows.append((sn.output.onnx_name, shape, "gemm_planes_kernel", us, conv_macs(sn), byt, split_us))
+            else:
+                us = small[si] * 1e3 if si < len(small) else float("nan")
+                si += 1
+                rows.append((sn.output.onnx_name, shape, "conv_small_kernel", us, conv_macs(sn), byt, None))
+        elif kind == "MatmulNode":
+            a, b = sn.inputs
+            n, kk, m = int(a.shape[-2]), int(a.shape[-1]), int(b.shape[-1])
+            us = gemm[gi] * 1e3 if gi < len(gemm) else float("nan")
+            gi += 1
+            rows.append((sn.output.onnx_name, f"{n}x{kk} . {kk}x{m}", "gemm_planes_kernel", us, n * kk * m,
+                         2 * (n * kk + kk * m + n * m), None))
+    tot_us = tot_bound = 0.0
+    lines = [f"| output | shape (batch {batch}) | kernel | us | G MAC | MB | MFMA-bound us | HBM-bound us | "
+             "of roofline | fold split us (HBM-bound us) |", "|---|---|---|---|---|---|---|---|---|---|"]
+    for name, shape, kern, us, macs, byt, split_us in rows:
+        t_mfma = 8.0 * macs / (I8_PEAK_TOPS * 1e12) * 1e6 if kern == "gemm_planes_kernel" else 0.0
+        t_hbm = byt / (HBM_PEAK_GBS * 1e9) * 1e6
+        bound = max(t_mfma, t_hbm)
+        split = ""
+        if split_us is not None:
+            # the split reads the int16 input and writes its two byte planes (as many bytes)
+            s_hbm = 2.0 * sn_bytes_in(g, name) / (HBM_PEAK_GBS * 1e9) * 1e6
+            split = f"{split_us:.1f} ({s_hbm:.2f})"
+            tot_us += split_us
+            tot_bound += s_hbm
+        tot_us += us
+        tot_bound += bound
+        lines.append(f"| {name} | {shape} | {kern} | {us:.1f} | {macs / 1e9:.3f} | {byt / 1e6:.1f} | "
+                     f"{t_mfma:.2f} | {t_hbm:.2f} | {bound / us:.2f} | {split} |")
+    lines.append(f"\nThese launches, with the fold splits: {tot_us:.1f} us of the {ms * 1e3:.1f} us step; their "
+                 f"rooflines sum to {tot_bound:.1f} us ({tot_bound / tot_us:.2f} of their time).")
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+
+def sn_bytes_in(g, out_name) -> int:
+    """Bytes of the int16 input of the convolution writing ``out_name``."""
+    sn = next(n for n in g.nodes if n.output.onnx_name == out_name)
+    return 2 * sn.batch * sn.in_ch * sn.in_h * sn.in_w
+
+
 def mobilenet_bench(args, torch, np):
     """One step = one forward of MobileNetV2 1.0 over 32 images of 3 x 224 x 224 (Q8.8), the
     input resident on the GPU, replayed as a captured HIP graph."""
@@ -407,7 +497,12 @@ def mobilenet_bench(args, torch, np):
     sim = Simulator(g)
     out_name = g.output_tensors[0].onnx_name
     x = sim._to_device(sim._tensor("input"), inputs["input"])
-    ms, per_kernel, out = run_graph(args, torch, sim, {"input": x}, out_name)
+    each = ("gemm_planes_kernel", "split_fold_kernel", "conv_small_kernel") if args.per_launch else ()
+    ms, per_kernel, out = run_graph(args, torch, sim, {"input": x}, out_name, each=each)
+    if args.per_launch:
+        write_conv_roofline(args.per_launch, g, per_kernel, batch, ms)
+        for k in each:
+            per_kernel.get(k, {}).pop("each", None)
     result = {
         "metric": "bit-exact fixed-point images/s (MobileNetV2 batch 32, 224x224, Q8.8)",
         "value": round(batch / (ms * 1e-3), 1),
@@ -420,11 +515,10 @@ def mobilenet_bench(args, torch, np):
                    "batch": batch, "res": 224, "macs_per_step": macs},
         "kernels_ms_per_step": per_kernel,
     }
-    # the GEMM's share of the MACs: standard / pointwise convolutions and the classifier
-    dw_macs = sum(sn.batch * sn.out_ch * sn.out_h * sn.out_w * sn.kh * sn.kw for sn in g.nodes
-                  if type(sn).__name__ == "ConvNode" and sn.is_depthwise)
-    result["roofline"] = gemm_roofline(per_kernel, macs - dw_macs)
-    result["roofline"]["macs_on_mfma"] = macs - dw_macs
+    # the GEMM's share of the MACs: the standard / pointwise convolutions it runs and the classifier
+    off_mfma = sum(conv_macs(sn) for sn in g.nodes if type(sn).__name__ == "ConvNode" and not conv_on_gemm(sn))
+    result["roofline"] = gemm_roofline(per_kernel, macs - off_mfma)
+    result["roofline"]["macs_on_mfma"] = macs - off_mfma
     ok = None
     if not args.no_cpu_baseline:
         from oracle import graph_sim
@@ -572,10 +666,11 @@ def cnn_bench(args, torch, np):
         "data": f"synthetic (seed {args.seed}): input U[0,1), weights U(+-0.25), biases U(+-0.1), Q8.8",
         "config": {"workload": "small CNN forward, batch 1: Conv3x3 1->8 + RELU + MaxPool, Conv3x3 8->16 + RELU "
                                "+ MaxPool, MatMul 784x10 + bias, Softmax", "batch": 1, "macs_per_step": macs},
-        "roofline": gemm_roofline(per_kernel, macs),
+        "roofline": gemm_roofline(per_kernel, 784 * 10),
         "kernels_ms_per_step": per_kernel,
     }
-    result["roofline"]["note"] = "latency-bound: the fraction is not meaningful at 290 k MAC"
+    result["roofline"]["note"] = ("latency-bound: the fraction is not meaningful at 7840 MAC (the MatMul; the two "
+                                  "convolutions run on the VALU)")
     ok = None
     if not args.no_cpu_baseline:
         from oracle import graph_sim
@@ -603,6 +698,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--per-launch", default="",
+                    help="(--config mobilenet) write a markdown table of every convolution / product launch "
+                         "against its roofline to this path")
     ap.add_argument("--hbm", action="store_true",
                     help="measure the HBM-bound units (VectorOP, softmax, pooling, depthwise conv, "
                          "row-ops) against the 8 TB/s roofline instead of the matmul step")

@@ -72,6 +72,8 @@ SIGNATURES = {
     "cm_timing_read": (_I32, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                               ctypes.POINTER(ctypes.c_uint64)]),
     "cm_timing_reset": (_I32, []),
+    "cm_timing_read_each": (_I32, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.c_uint64,
+                                   ctypes.POINTER(ctypes.c_uint64)]),
     "cm_timing_select": (_I32, [ctypes.c_char_p]),
 }
 
@@ -95,6 +97,14 @@ def timing_read(kernel: str):
     n = ctypes.c_uint64(0)
     check(lib().cm_timing_read(kernel.encode(), ctypes.byref(ms), ctypes.byref(n)), "cm_timing_read")
     return ms.value, n.value
+
+def timing_read_each(kernel: str):
+    """The recorded launches of ``kernel`` one by one, in launch order (milliseconds)."""
+    n = ctypes.c_uint64(0)
+    check(lib().cm_timing_read_each(kernel.encode(), None, 0, ctypes.byref(n)), "cm_timing_read_each")
+    buf = (ctypes.c_double * max(n.value, 1))()
+    check(lib().cm_timing_read_each(kernel.encode(), buf, n.value, ctypes.byref(n)), "cm_timing_read_each")
+    return list(buf[:n.value])
 
 _lib = None
 

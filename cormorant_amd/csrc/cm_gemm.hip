@@ -401,6 +401,58 @@ __global__ __launch_bounds__(1024) void split_fold_kernel(const int16_t* __restr
     }
 }
 
+// The same operand for few lines (small planes): 16 lines a workgroup so that the grid has
+// four times the workgroups.  Wave w takes the slab's 64 k from 64 w; lane (line l % 16, chunk
+// l / 16) loads its line's 16 k of the chunk (the 16 lanes of one chunk read 32 consecutive bytes
+// of a channel row where the lines stay in one image), so the four chunk lanes of a line write
+// 64 contiguous bytes of each plane.  Grid (lines_p / 16, nslab).
+__global__ __launch_bounds__(1024) void split_fold16_kernel(const int16_t* __restrict__ x, uint32_t in_ch,
+                                                            uint32_t plane, uint64_t img_elems, uint32_t cols,
+                                                            int8_t* __restrict__ hi, int8_t* __restrict__ lo,
+                                                            int32_t* __restrict__ part, uint32_t lines_p,
+                                                            uint32_t kp) {
+    __shared__ int32_t wsum[16][16];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    const uint32_t ln = lane & 15, ch = lane >> 4;
+    const uint32_t j = blockIdx.x * 16 + ln, slab = blockIdx.y;
+    const bool real = j < cols;
+    const uint32_t img = real ? j / plane : 0, p = real ? j - img * plane : 0;
+    const int16_t* src = x + img * img_elems + p;
+    int32_t sum = 0;
+    const uint32_t k0 = slab * SLAB + 64 * wave + 16 * ch;
+    if (k0 < kp) {
+        int16_t e[16];
+        if (real && k0 + 16 <= in_ch) {
+#pragma unroll
+            for (int q = 0; q < 16; q++) e[q] = src[(uint64_t)(k0 + q) * plane];
+#pragma unroll
+            for (int q = 0; q < 16; q++) sum += e[q];
+        } else {
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const bool r = real && k0 + q < in_ch;
+                e[q] = r ? src[(uint64_t)(k0 + q) * plane] : kPad;
+                sum += r ? e[q] : 0;
+            }
+        }
+        uint2 h0, l0, h1, l1;
+        split8(*reinterpret_cast<const int4*>(e), h0, l0);
+        split8(*reinterpret_cast<const int4*>(e + 8), h1, l1);
+        const uint64_t off = (uint64_t)j * kp + k0;
+        *reinterpret_cast<uint4*>(hi + off) = make_uint4(h0.x, h0.y, h1.x, h1.y);
+        *reinterpret_cast<uint4*>(lo + off) = make_uint4(l0.x, l0.y, l1.x, l1.y);
+    }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    if (ch == 0) wsum[wave][ln] = sum;
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        int32_t t = 0;
+        for (uint32_t w = 0; w < waves; w++) t += wsum[w][threadIdx.x];
+        part[(uint64_t)slab * lines_p + blockIdx.x * 16 + threadIdx.x] = t;
+    }
+}
+
 // The same operand for planes with many lines: a workgroup takes 64 lines and one SLAB of
 // k in 64 x 64 tiles through LDS.  Thread t loads line t % 64 at 16 k (2-byte loads, the 64
 // lanes of one load on consecutive lines), then packs 16 consecutive k of line t / 4 into
@@ -2250,11 +2302,16 @@ int conv_gemm(const int16_t* x, const Planes& A, Planes& B, const int16_t* bptr,
             // lines enough for the workgroups of whole slabs to fill the chip
             CM_LAUNCH("split_fold_kernel", split_fold_lds_kernel, dim3(B.lines_p / 64, B.nslab), dim3(256), 0, s, x,
                       g.in_ch, plane, (uint64_t)g.in_ch * plane, cols, B.hi, B.lo, B.part, B.lines_p, B.kp);
-        } else {
+        } else if (B.lines_p / 64 >= (uint32_t)st->cus) {
             // one wave per 64 k of the slab
             const uint32_t waves = std::min<uint32_t>(16, ceil_div(std::min<uint32_t>(B.kp, SLAB), 64));
             CM_LAUNCH("split_fold_kernel", split_fold_kernel, dim3(B.lines_p / 64, B.nslab), dim3(64 * waves), 0, s,
                       x, g.in_ch, plane, (uint64_t)g.in_ch * plane, cols, B.hi, B.lo, B.part, B.lines_p, B.kp);
+        } else {
+            // few lines: 16 a workgroup
+            const uint32_t waves = std::min<uint32_t>(16, ceil_div(std::min<uint32_t>(B.kp, SLAB), 64));
+            CM_LAUNCH("split_fold_kernel", split_fold16_kernel, dim3(B.lines_p / 16, B.nslab), dim3(64 * waves), 0,
+                      s, x, g.in_ch, plane, (uint64_t)g.in_ch * plane, cols, B.hi, B.lo, B.part, B.lines_p, B.kp);
         }
         const bool pairs = (reinterpret_cast<uintptr_t>(y) & 3) == 0 && (plane & 1) == 0;
         EpiConv epi{y, bptr, img, g.out_ch, cols, plane, 0, 0, g.wrap, pairs ? 1u : 0u, plane, lo, hi};

@@ -325,6 +325,22 @@ int cm_timing_read(const char* kernel, double* total_ms, uint64_t* launches) {
     return CM_OK;
 }
 
+int cm_timing_read_each(const char* kernel, double* ms, uint64_t cap, uint64_t* launches) {
+    std::lock_guard<std::mutex> lk(cm::g_tmu);
+    uint64_t n = 0;
+    for (auto& r : cm::g_records) {
+        if (std::strcmp(r.name, kernel) != 0) continue;
+        if (n < cap && ms != nullptr) {
+            CM_HIP_CHECK(hipEventSynchronize(r.stop));
+            float e = 0.f;
+            CM_HIP_CHECK(hipEventElapsedTime(&e, r.start, r.stop));
+            ms[n] = e;
+        }
+        n++;
+    }
+    if (launches) *launches = n;
+    return CM_OK;
+}
 
 int cm_abi_version(void) { return 100; }
 

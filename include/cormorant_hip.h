@@ -82,6 +82,9 @@ int cm_timing_reset(void);
  * kernel inside a loop adds two events per launch of it and none elsewhere.  The events
  * skip the system-scope fence, so they neither flush caches nor slow the launches after. */
 int cm_timing_select(const char* kernel);
+/* The recorded launches of `kernel` one by one, in launch order: their durations (ms) into
+ * ms[0 .. min(cap, count)), the count into *launches.  Waits for them as cm_timing_read. */
+int cm_timing_read_each(const char* kernel, double* ms, uint64_t cap, uint64_t* launches);
 
 /* ---------------------------------------------------------------- VectorOP
  * Replaces VectorOPKernel (kernels/vectorop_rtl/model/include/VectorOP.h:319-333) and the

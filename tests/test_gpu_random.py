@@ -527,9 +527,12 @@ CONV_CASES = [  # batch, C, H, W, M, kh, kw, sh, sw, dh, dw, pt, pl, pb, pr, bia
     (3, 16, 33, 35, 24, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 0, 0, False, False),
     (2, 16, 9, 9, 24, 1, 1, 2, 2, 1, 1, 0, 0, 0, 0, 1, 0, False, False),
     (2, 16, 9, 9, 24, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 0, False, False),
-    # folded 1x1 with 2^16 lines and more (the LDS-tiled split): an even and an odd plane
+    # folded 1x1 with 2^16 lines and more (the LDS-tiled split): an even and an odd plane (the
+    # first two run on the VALU as few-tap convolutions, the other two on the GEMM)
     (4, 24, 128, 128, 40, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 1, 0, False, False),
     (3, 20, 151, 149, 24, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 0, 0, True, False),
+    (4, 96, 128, 128, 160, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 1, 0, False, False),
+    (3, 100, 151, 149, 130, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 0, 0, True, False),
     # few taps (at most 16 channels, 80 taps): straight on the VALU -- MobileNetV2's stem, the
     # small CNN's first layer, 7x7 over one channel with asymmetric pads (int64 sums), dilation
     # and wrap with 33 output channels, a wide plane, exactly 80 taps, 64 taps full range wrapped
