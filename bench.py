@@ -307,6 +307,23 @@ def gemm_roofline(per_kernel, macs):
             "kernel_ms_per_step": gemm_ms, "ops_per_step": 8 * macs}
 
 
+def cnn_roofline(g, per_kernel):
+    """The small CNN's dominant kernel, the two few-tap convolutions (conv_small_kernel, on the
+    VALU), against HBM: their algorithmic bytes (input, weights, output once at int16) over
+    their summed launch time.  At batch 1 every launch is latency-bound."""
+    byt = 0
+    for sn in g.nodes:
+        if type(sn).__name__ == "ConvNode":
+            byt += 2 * (sn.batch * sn.in_ch * sn.in_h * sn.in_w + sn.out_ch * sn.in_ch * sn.kh * sn.kw
+                        + sn.batch * sn.out_ch * sn.out_h * sn.out_w)
+    t_ms = per_kernel.get("conv_small_kernel", {}).get("ms", float("nan"))
+    gbs = byt / (t_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 6), "traffic": None, "kernel": "conv_small_kernel",
+            "kernel_ms_per_step": t_ms, "bytes_per_step": byt,
+            "note": "latency-bound: two launches over 26 KB of tensors; the fraction is not meaningful"}
+
+
 def cores():
     return len(os.sched_getaffinity(0))
 
@@ -320,7 +337,7 @@ def finish(result, ok=None):
         sys.exit(1)
 
 
-# ---------------------------------------------------------------- config 4: BERT-base L384
+# ---------------------------------------------------------------- BERT-base L384 encoder forward
 def bert_bench(args, torch, np):
     """One step = one forward of the 12-layer encoder over the batch of 8 x 384 tokens, the
     int32 residual input resident on the GPU, replayed as a captured HIP graph."""
@@ -403,7 +420,7 @@ def bert_bench(args, torch, np):
     finish(result, ok)
 
 
-# ---------------------------------------------------------------- config 3: MobileNetV2, batch 32
+# ---------------------------------------------------------------- MobileNetV2, batch 32
 def conv_macs(sn) -> int:
     return sn.batch * sn.out_ch * sn.out_h * sn.out_w * sn.kh * sn.kw * (1 if sn.is_depthwise else sn.in_ch)
 
@@ -419,6 +436,14 @@ def conv_on_gemm(sn) -> bool:
     return not sn.is_depthwise and not units.conv_small(sn.in_ch, sn.kh, sn.kw, sn.out_ch, sn.batch)
 
 
+def matmul_on_skinny(sn) -> bool:
+    """A saturating MatMul of a constant weight and at most 32 rows, which the simulator runs as
+    saturating skinny products (skinny_planes_kernel, 16 rows a launch)."""
+    a, b = sn.inputs
+    return (b.data is not None and len(a.shape) == 2 and len(b.shape) == 2 and int(a.shape[-2]) <= 32
+            and int(a.shape[-1]) % 8 == 0 and a.exp is None and b.exp is None and b.wexp is None)
+
+
 def write_conv_roofline(path, g, per_kernel, batch, ms):
     """A markdown table of every convolution and product launch of one forward against its own
     roofline: the GEMM launches (and the fold split before each folded 1x1) against
@@ -428,7 +453,8 @@ def write_conv_roofline(path, g, per_kernel, batch, ms):
     gemm = per_kernel.get("gemm_planes_kernel", {}).get("each", [])
     fold = per_kernel.get("split_fold_kernel", {}).get("each", [])
     small = per_kernel.get("conv_small_kernel", {}).get("each", [])
-    gi = fi = si = 0
+    skinny = per_kernel.get("skinny_planes_kernel", {}).get("each", [])
+    gi = fi = si = ki = 0
     rows = []
     for sn in g.nodes:
         kind = type(sn).__name__
@@ -452,15 +478,22 @@ def write_conv_roofline(path, g, per_kernel, batch, ms):
         elif kind == "MatmulNode":
             a, b = sn.inputs
             n, kk, m = int(a.shape[-2]), int(a.shape[-1]), int(b.shape[-1])
-            us = gemm[gi] * 1e3 if gi < len(gemm) else float("nan")
-            gi += 1
-            rows.append((sn.output.onnx_name, f"{n}x{kk} . {kk}x{m}", "gemm_planes_kernel", us, n * kk * m,
+            if matmul_on_skinny(sn):
+                launches = (n + 15) // 16
+                us = sum(skinny[ki:ki + launches]) * 1e3 if ki + launches <= len(skinny) else float("nan")
+                ki += launches
+                kern = "skinny_planes_kernel" if launches == 1 else f"skinny_planes_kernel x {launches}"
+            else:
+                us = gemm[gi] * 1e3 if gi < len(gemm) else float("nan")
+                gi += 1
+                kern = "gemm_planes_kernel"
+            rows.append((sn.output.onnx_name, f"{n}x{kk} . {kk}x{m}", kern, us, n * kk * m,
                          2 * (n * kk + kk * m + n * m), None))
     tot_us = tot_bound = 0.0
     lines = [f"| output | shape (batch {batch}) | kernel | us | G MAC | MB | MFMA-bound us | HBM-bound us | "
              "of roofline | fold split us (HBM-bound us) |", "|---|---|---|---|---|---|---|---|---|---|"]
     for name, shape, kern, us, macs, byt, split_us in rows:
-        t_mfma = 8.0 * macs / (I8_PEAK_TOPS * 1e12) * 1e6 if kern == "gemm_planes_kernel" else 0.0
+        t_mfma = 8.0 * macs / (I8_PEAK_TOPS * 1e12) * 1e6 if kern.startswith(("gemm", "skinny")) else 0.0
         t_hbm = byt / (HBM_PEAK_GBS * 1e9) * 1e6
         bound = max(t_mfma, t_hbm)
         split = ""
@@ -497,7 +530,8 @@ def mobilenet_bench(args, torch, np):
     sim = Simulator(g)
     out_name = g.output_tensors[0].onnx_name
     x = sim._to_device(sim._tensor("input"), inputs["input"])
-    each = ("gemm_planes_kernel", "split_fold_kernel", "conv_small_kernel") if args.per_launch else ()
+    each = (("gemm_planes_kernel", "split_fold_kernel", "conv_small_kernel", "skinny_planes_kernel")
+            if args.per_launch else ())
     ms, per_kernel, out = run_graph(args, torch, sim, {"input": x}, out_name, each=each)
     if args.per_launch:
         write_conv_roofline(args.per_launch, g, per_kernel, batch, ms)
@@ -515,8 +549,11 @@ def mobilenet_bench(args, torch, np):
                    "batch": batch, "res": 224, "macs_per_step": macs},
         "kernels_ms_per_step": per_kernel,
     }
-    # the GEMM's share of the MACs: the standard / pointwise convolutions it runs and the classifier
+    # the GEMM's share of the MACs: the standard / pointwise convolutions it runs (the few-tap
+    # convolutions run on the VALU, the classifier on the skinny products)
     off_mfma = sum(conv_macs(sn) for sn in g.nodes if type(sn).__name__ == "ConvNode" and not conv_on_gemm(sn))
+    off_mfma += sum(int(sn.inputs[0].shape[-2]) * int(sn.inputs[0].shape[-1]) * int(sn.inputs[1].shape[-1])
+                    for sn in g.nodes if type(sn).__name__ == "MatmulNode" and matmul_on_skinny(sn))
     result["roofline"] = gemm_roofline(per_kernel, macs - off_mfma)
     result["roofline"]["macs_on_mfma"] = macs - off_mfma
     ok = None
@@ -537,7 +574,7 @@ def mobilenet_bench(args, torch, np):
     finish(result, ok)
 
 
-# ---------------------------------------------------------------- config 5: SmolLM2-360M decode, batch 16
+# ---------------------------------------------------------------- SmolLM2-360M decode, batch 16
 def smollm2_bench(args, torch, np):
     """One step = one greedy decode step of 16 sequences at cache position 1023 (every one of
     the 1024 cache rows a key): 32 layers and the tied head, the residual and the 64 KV caches
@@ -644,7 +681,7 @@ def smollm2_bench(args, torch, np):
     finish(result, ok)
 
 
-# ---------------------------------------------------------------- config 1: small CNN, batch 1
+# ---------------------------------------------------------------- small CNN, batch 1
 def cnn_bench(args, torch, np):
     """One step = one forward of the small CNN (batch 1, 28 x 28, Q8.8): latency-bound, so
     the figure is inferences/s of the replayed graph."""
@@ -666,11 +703,9 @@ def cnn_bench(args, torch, np):
         "data": f"synthetic (seed {args.seed}): input U[0,1), weights U(+-0.25), biases U(+-0.1), Q8.8",
         "config": {"workload": "small CNN forward, batch 1: Conv3x3 1->8 + RELU + MaxPool, Conv3x3 8->16 + RELU "
                                "+ MaxPool, MatMul 784x10 + bias, Softmax", "batch": 1, "macs_per_step": macs},
-        "roofline": gemm_roofline(per_kernel, 784 * 10),
+        "roofline": cnn_roofline(g, per_kernel),
         "kernels_ms_per_step": per_kernel,
     }
-    result["roofline"]["note"] = ("latency-bound: the fraction is not meaningful at 7840 MAC (the MatMul; the two "
-                                  "convolutions run on the VALU)")
     ok = None
     if not args.no_cpu_baseline:
         from oracle import graph_sim
@@ -705,10 +740,10 @@ def main():
                     help="measure the HBM-bound units (VectorOP, softmax, pooling, depthwise conv, "
                          "row-ops) against the 8 TB/s roofline instead of the matmul step")
     ap.add_argument("--config", default="bert", choices=["bert", "matmul", "mobilenet", "cnn", "smollm2"],
-                    help="bert: config 4, the BERT-base L384 encoder forward (the headline metric); "
-                         "matmul: config 2, the batched Q8.8 MatMul; mobilenet: config 3, MobileNetV2 "
-                         "batch 32; cnn: config 1, the small CNN at batch 1; smollm2: config 5, a "
-                         "SmolLM2-360M-shaped decode step of 16 sequences")
+                    help="bert: the BERT-base L384 encoder forward of 8 sequences (the headline metric); "
+                         "matmul: the batched Q8.8 MatMul 4 x 512 x 4096 x 4096; mobilenet: MobileNetV2 "
+                         "at batch 32; cnn: the small CNN at batch 1; smollm2: a SmolLM2-360M-shaped "
+                         "decode step of 16 sequences")
     ap.add_argument("--calibrate", action="store_true",
                     help="run only the copy used to scale HBM counters: a RELU over 256 MiB of "
                          "non-negative int16 (reads and writes exactly 256 MiB each)")

@@ -66,6 +66,7 @@ SIGNATURES = {
     "cm_matmul_strided": (_I32, [_P, _P, _P] + [_U32] * 5 + [ctypes.c_uint64] * 6 + [_U32] + [ctypes.c_uint64] * 3 + [_U32, _P]),
     "cm_matmul_skinny_multi": (_I32, [_P, _U32, _U32, _U32, _P, _P, _P, _U32, _P]),
     "cm_matmul_skinny_planes": (_I32, [_P, _U32, _U32, _U32, _P, _P, _P, _P]),
+    "cm_matmul_skinny_planes_sat": (_I32, [_P, _U32, _U32, _U32, _P, _P, _P, _P]),
     "cm_matmul_skinny_planes_addx": (_I32, [_P, _U32, _U32, _P, _P, _U32, _P, _P, _U32, _U32, _P, _P]),
     "cm_matmul_skinny_planes_mulact": (_I32, [_P, _U32, _U32, _P, _P, _P, _P, _U32, _P, _U32, _P, _P]),
     "cm_timing_enable": (_I32, [_I32]),

@@ -1619,8 +1619,9 @@ struct SkinnyEpiIn {
 
 // The wrapped partial products of one skinny workgroup: NB 16-column blocks whose plane lines
 // start at bh[b] / bl[b] (the block's first column), into red [W][16][16 NB] and A's row sums
-// into rsum [W][16]; ends with the workgroup barrier.
-template <uint32_t NB>
+// into rsum [W][16]; ends with the workgroup barrier.  SAT: each wavefront's three limb sums
+// (exact in int32) into red [3][W][16][16 NB] -- HH, MID, LL -- for the exact recombination.
+template <uint32_t NB, bool SAT = false>
 __device__ __forceinline__ void skinny_products(const int16_t* __restrict__ a, uint32_t n, uint32_t k, uint32_t kp,
                                                 const int8_t* const (&bh)[NB], const int8_t* const (&bl)[NB],
                                                 uint32_t* red, int32_t* rsum) {
@@ -1681,9 +1682,17 @@ __device__ __forceinline__ void skinny_products(const int16_t* __restrict__ a, u
 #pragma unroll
     for (uint32_t b = 0; b < NB; b++)
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            red[(wave * 16 + 4 * g + i) * COLS + 16 * b + r] =
-                ((uint32_t)hh[b][i] << 16) + ((uint32_t)mid[b][i] << 8) + (uint32_t)ll[b][i];
+        for (int i = 0; i < 4; i++) {
+            const uint32_t e = (wave * 16 + 4 * g + i) * COLS + 16 * b + r;
+            if constexpr (SAT) {
+                const uint32_t plane = W * 16 * COLS;
+                red[e] = (uint32_t)hh[b][i];
+                red[plane + e] = (uint32_t)mid[b][i];
+                red[2 * plane + e] = (uint32_t)ll[b][i];
+            } else {
+                red[e] = ((uint32_t)hh[b][i] << 16) + ((uint32_t)mid[b][i] << 8) + (uint32_t)ll[b][i];
+            }
+        }
     asum += __shfl_xor(asum, 16, 64);
     asum += __shfl_xor(asum, 32, 64);
     if (g == 0) rsum[wave * 16 + r] = asum;
@@ -1703,6 +1712,25 @@ __device__ __forceinline__ int16_t skinny_value(const uint32_t* red, const int32
     return (int16_t)min(max((int32_t)acc >> 8, -32768), 32767);
 }
 
+// The same by the saturating rule: the wavefronts' limb sums (red [3][W][16][cols]) and the
+// row / column sums recombined exactly in int64 (each term is exact in int32: |A|, |B| <=
+// 2^15 and k <= 32768), then floor(acc / 2^8) saturated to int16.
+__device__ __forceinline__ int16_t skinny_value_sat(const uint32_t* red, const int32_t* rsum, uint32_t W,
+                                                    uint32_t cols, uint32_t row, uint32_t cl, uint32_t k,
+                                                    uint32_t cs) {
+    const uint32_t plane = W * 16 * cols;
+    long long acc = -16384ll * k, rs = 0;
+    for (uint32_t w = 0; w < W; w++) {
+        const uint32_t e = (w * 16 + row) * cols + cl;
+        acc += ((long long)(int32_t)red[e] << 16) + ((long long)(int32_t)red[plane + e] << 8) +
+               (long long)(int32_t)red[2 * plane + e];
+        rs += rsum[w * 16 + row];
+    }
+    acc += 128ll * rs + 128ll * (int32_t)cs;
+    const long long q = acc >> 8;
+    return (int16_t)(q > 32767 ? 32767 : (q < -32768 ? -32768 : q));
+}
+
 // B's column sum of column col from the slabs a prefetch took (the first kSpSlabs) and the rest.
 __device__ __forceinline__ uint32_t skinny_colsum(const uint32_t (&pre)[kSpSlabs], const int32_t* part, uint32_t nslab,
                                                   uint32_t lp, uint32_t col) {
@@ -1713,16 +1741,17 @@ __device__ __forceinline__ uint32_t skinny_colsum(const uint32_t (&pre)[kSpSlabs
     return cs;
 }
 
-// XK: the output job's x kind (0: no job, 1: int16, 2: int32).
-template <uint32_t NB, uint32_t XK>
+// XK: the output job's x kind (0: no job, 1: int16, 2: int32); SAT: the saturating rule (no job).
+template <uint32_t NB, uint32_t XK, bool SAT = false>
 __global__ __launch_bounds__(64 * sp_max_waves(NB)) void skinny_planes_kernel(const int16_t* __restrict__ a, uint32_t n,
                                                                        uint32_t k, uint32_t kp, uint32_t nslab,
                                                                        SkinnyPlaneSegs segs, SkinnyAddx ax) {
     constexpr uint32_t COLS = 16 * NB;
     extern __shared__ __attribute__((aligned(16))) uint32_t sp_lds[];
     const uint32_t W = blockDim.x >> 6;
-    uint32_t* red = sp_lds;                                  // [W][16][COLS] wrapped partials
-    int32_t* rsum = reinterpret_cast<int32_t*>(sp_lds + W * 16 * COLS);   // [W][16] A row sums
+    static_assert(!SAT || XK == 0, "no output job on the saturating products");
+    uint32_t* red = sp_lds;                                  // [W][16][COLS] wrapped partials ([3][..] SAT)
+    int32_t* rsum = reinterpret_cast<int32_t*>(sp_lds + (SAT ? 3 : 1) * W * 16 * COLS);   // [W][16] A row sums
     uint32_t si = 0;
     for (uint32_t i = 1; i < segs.count; i++)
         if (blockIdx.x >= segs.cb0[i]) si = i;
@@ -1758,12 +1787,14 @@ __global__ __launch_bounds__(64 * sp_max_waves(NB)) void skinny_planes_kernel(co
         bh[b] = segs.hi[si] + (uint64_t)(c0 + 16 * b) * kp;
         bl[b] = segs.lo[si] + (uint64_t)(c0 + 16 * b) * kp;
     }
-    skinny_products<NB>(a, n, k, kp, bh, bl, red, rsum);
+    skinny_products<NB, SAT>(a, n, k, kp, bh, bl, red, rsum);
     int16_t* __restrict__ c = segs.c[si];
     auto store = [&](uint32_t e, const SkinnyEpiIn& in) {
         const uint32_t row = e / COLS, cl = e - row * COLS, col = c0 + cl;
         if (row >= n || col >= m) return;
-        const int16_t y = skinny_value(red, rsum, W, COLS, row, cl, k, skinny_colsum(in.cs, part, nslab, lp, col));
+        const uint32_t cs = skinny_colsum(in.cs, part, nslab, lp, col);
+        const int16_t y = SAT ? skinny_value_sat(red, rsum, W, COLS, row, cl, k, cs)
+                              : skinny_value(red, rsum, W, COLS, row, cl, k, cs);
         const uint64_t eo = (uint64_t)row * m + col;
         c[eo] = y;
         if constexpr (XK != 0) {
@@ -2680,10 +2711,12 @@ uint32_t skinny_waves(uint32_t k, uint32_t nb) {
     const uint32_t kp = (uint32_t)round_up(k, BK);
     return std::min<uint32_t>(sp_max_waves(nb), std::max<uint32_t>(1, ceil_div(kp / 64, sp_chunk(nb))));
 }
-size_t skinny_lds(uint32_t waves, uint32_t nb) { return (size_t)waves * 16 * (16 * nb + 1) * 4; }
+size_t skinny_lds(uint32_t waves, uint32_t nb, bool sat = false) {
+    return (size_t)waves * 16 * (16 * nb * (sat ? 3 : 1) + 1) * 4;
+}
 
 int skinny_planes(const int16_t* a, uint32_t n, uint32_t k, uint32_t count, const void* const* b_planes,
-                  int16_t* const* c, const uint32_t* m, const SkinnyAddx& ax, hipStream_t s) {
+                  int16_t* const* c, const uint32_t* m, const SkinnyAddx& ax, hipStream_t s, bool sat = false) {
     if (n == 0) return CM_OK;
     SkinnyPlaneSegs segs;
     uint32_t nslab;
@@ -2691,7 +2724,8 @@ int skinny_planes(const int16_t* a, uint32_t n, uint32_t k, uint32_t count, cons
     int rc = skinny_segs(n, k, count, a, b_planes, c, m, segs, nslab, blocks16);
     if (rc) return rc;
     const uint32_t kp = (uint32_t)round_up(k, BK);
-    const uint32_t nb = skinny_blocks(blocks16, k);
+    // the saturating partials take three times the LDS: at most two blocks a workgroup (50 KiB)
+    const uint32_t nb = sat ? std::min<uint32_t>(2, skinny_blocks(blocks16, k)) : skinny_blocks(blocks16, k);
     uint64_t cbs = 0;
     for (uint32_t i = 0; i < count; i++) {
         segs.cb0[i] = (uint32_t)cbs;
@@ -2699,13 +2733,20 @@ int skinny_planes(const int16_t* a, uint32_t n, uint32_t k, uint32_t count, cons
     }
     if (cbs > 0x7FFFFFFFull) return fail(CM_EINVAL, "matmul: %llu column blocks", (unsigned long long)cbs);
     const uint32_t waves = skinny_waves(k, nb);
-    const size_t lds = skinny_lds(waves, nb);
+    const size_t lds = skinny_lds(waves, nb, sat);
     const dim3 grid((uint32_t)cbs), block(64 * waves);
     const uint32_t xk = ax.out == nullptr ? 0u : (((ax.op >> 4) & 3) == 0 ? 1u : 2u);
+    if (sat && xk) return fail(CM_EINVAL, "matmul: no output job on saturating skinny products");
 #define CM_SP_LAUNCH(NB_, XK_)                                                                                  \
     CM_LAUNCH("skinny_planes_kernel", (skinny_planes_kernel<NB_, XK_>), grid, block, lds, s, a, n, k, kp, nslab, \
               segs, ax)
-    if (xk == 0) {
+#define CM_SP_LAUNCH_SAT(NB_)                                                                                   \
+    CM_LAUNCH("skinny_planes_kernel", (skinny_planes_kernel<NB_, 0, true>), grid, block, lds, s, a, n, k, kp,    \
+              nslab, segs, ax)
+    if (sat) {
+        if (nb == 1) { CM_SP_LAUNCH_SAT(1); }
+        else { CM_SP_LAUNCH_SAT(2); }
+    } else if (xk == 0) {
         if (nb == 1) { CM_SP_LAUNCH(1, 0); }
         else if (nb == 2) { CM_SP_LAUNCH(2, 0); }
         else { CM_SP_LAUNCH(4, 0); }
@@ -2719,6 +2760,7 @@ int skinny_planes(const int16_t* a, uint32_t n, uint32_t k, uint32_t count, cons
         else { CM_SP_LAUNCH(4, 2); }
     }
 #undef CM_SP_LAUNCH
+#undef CM_SP_LAUNCH_SAT
     return CM_OK;
 }
 
@@ -2772,6 +2814,16 @@ extern "C" int cm_matmul_skinny_planes(const int16_t* a, uint32_t n, uint32_t k,
     int rc = state(&st);
     if (rc) return rc;
     return skinny_planes(a, n, k, count, b_planes, c, m, SkinnyAddx{}, as_stream(stream));
+}
+
+extern "C" int cm_matmul_skinny_planes_sat(const int16_t* a, uint32_t n, uint32_t k, uint32_t count,
+                                           const void* const* b_planes, int16_t* const* c, const uint32_t* m,
+                                           void* stream) {
+    using namespace cm;
+    DeviceState* st;
+    int rc = state(&st);
+    if (rc) return rc;
+    return skinny_planes(a, n, k, count, b_planes, c, m, SkinnyAddx{}, as_stream(stream), true);
 }
 
 extern "C" int cm_matmul_skinny_planes_addx(const int16_t* a, uint32_t n, uint32_t k, const void* b_planes,

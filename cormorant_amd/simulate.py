@@ -429,7 +429,7 @@ class Simulator:
             raise KeyError(f"tensor '{t.onnx_name}' has no value (not an input, weight or node output)")
         w = self._weights.get(t.onnx_name)
         if w is None and t.raw:
-            w = torch.from_numpy(np.ascontiguousarray(np.asarray(t.data).astype(_NP[t.kind]))).to(self.device)
+            w = self._upload(np.asarray(t.data).astype(_NP[t.kind]))
             self._weights[t.onnx_name] = w
         if w is None:
             # a weight as the kernels read it (_simulate.py:531-539): quantized to the element
@@ -437,17 +437,36 @@ class Simulator:
             # are the Q8.8 raw; otherwise the raw at the tensor's own exponent
             q = self._dtype.quantize(np.asarray(t.data, np.float64).reshape(t.shape))
             r = self._dtype.to_raw(q) if t.wexp is not None else self._dtype.to_raw(q, self._exp(t))
-            w = torch.from_numpy(r).to(self.device)
+            w = self._upload(r)
             self._weights[t.onnx_name] = w
         return w
 
+    def _upload(self, arr: np.ndarray) -> torch.Tensor:
+        """A weight on the device in a buffer whose last 8-lane word is whole (zero lanes past
+        the data), so that the VectorOP unit reads it in place (_padded)."""
+        src = torch.from_numpy(np.ascontiguousarray(arr))
+        buf = torch.zeros(_pad8(src.numel()), dtype=src.dtype, device=self.device)
+        buf[:src.numel()].copy_(src.reshape(-1))
+        return buf[:src.numel()].view(src.shape)
+
     def _new(self, t: TensorInfo, numel: Optional[int] = None) -> torch.Tensor:
-        return torch.empty(t.numel if numel is None else numel, dtype=_TORCH[t.kind], device=self.device)
+        """An output buffer of `numel` lanes (the tensor's by default) with room for its last
+        8-lane word, which the VectorOP unit reads whole (_padded)."""
+        n = t.numel if numel is None else numel
+        return torch.empty(_pad8(n), dtype=_TORCH[t.kind], device=self.device)[:n]
 
     @staticmethod
     def _padded(x: torch.Tensor, rows: int, n: int, n_pad: int) -> torch.Tensor:
+        """Rows of n lanes at a stride of n_pad (the VectorOP unit's 8-lane words).  One row
+        whose buffer holds the lanes past n (every _new / _upload buffer) is read in place: the
+        unit's results in lanes below n do not depend on the lanes past it (element-wise ops;
+        the softmax counts at most n valid scores), and its own lanes past n are not read back."""
         if n == n_pad:
             return x.reshape(-1).contiguous()
+        if rows == 1 and x.is_contiguous() and x.dim() >= 1:
+            lanes = x.untyped_storage().nbytes() // x.element_size()
+            if x.storage_offset() + n_pad <= lanes:
+                return torch.as_strided(x, (n_pad,), (1,), x.storage_offset())
         out = torch.zeros((rows, n_pad), dtype=x.dtype, device=x.device)
         out[:, :n] = x.reshape(rows, n)
         return out.reshape(-1)
@@ -484,6 +503,13 @@ class Simulator:
         if bt.data is not None and b_batch == 1 and batch == 1 and wrap and n <= 16 and k % 8 == 0:
             # a decode-sized product: MFMA over the weight's split image, one launch
             units.matmul_skinny_planes(a.reshape(-1).contiguous(), n, k, [self._row_planes(bt, b, k, m)], [c], [m])
+            return c
+        if bt.data is not None and b_batch == 1 and batch == 1 and not wrap and n <= 32 and k % 8 == 0:
+            # a classifier at a small batch: the saturating skinny products, 16 rows a launch
+            af, planes = a.reshape(-1).contiguous(), self._row_planes(bt, b, k, m)
+            for r0 in range(0, n, 16):
+                rows = min(16, n - r0)
+                units.matmul_skinny_planes(af[r0 * k:], rows, k, [planes], [c[r0 * m:]], [m], wrap32=False)
             return c
         if bt.data is not None and b_batch == 1 and wrap and n <= 32 and m % 2 == 0 and k % 8 == 0:
             # a decode-sized product: the library's skinny path reads the weight itself, kept

@@ -279,9 +279,10 @@ def decode_attention_prep(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, qr:
     return o
 
 
-def matmul_skinny_planes(a: torch.Tensor, n: int, k: int, planes, cs, ms) -> None:
+def matmul_skinny_planes(a: torch.Tensor, n: int, k: int, planes, cs, ms, wrap32: bool = True) -> None:
     """cm_matmul_skinny_planes: C_i = sat16(wrap32(A . B_i) >> 8) for up to 4 weights given as
-    their split images (matmul_b_planes of the same k and m_i) and the same A [n][k], n <= 16."""
+    their split images (matmul_b_planes of the same k and m_i) and the same A [n][k], n <= 16;
+    with wrap32 False, cm_matmul_skinny_planes_sat: C_i = sat16(floor(A . B_i / 2^8)), exact."""
     count = len(planes)
     if not (len(cs) == len(ms) == count):
         raise ValueError("matmul_skinny_planes: one c and one m per weight")
@@ -292,10 +293,10 @@ def matmul_skinny_planes(a: torch.Tensor, n: int, k: int, planes, cs, ms) -> Non
             raise ValueError("matmul_skinny_planes: the uint8 image of matmul_b_planes for these k, m")
         _require(c, "c", torch.int16, n * m)
     P = ctypes.c_void_p * max(count, 1)
-    rc = _lib.lib().cm_matmul_skinny_planes(_ptr(a), n, k, count, P(*[_ptr(x) for x in planes]),
-                                            P(*[_ptr(c) for c in cs]), (ctypes.c_uint32 * max(count, 1))(*ms),
-                                            _stream())
-    _lib.check(rc, "cm_matmul_skinny_planes")
+    name = "cm_matmul_skinny_planes" if wrap32 else "cm_matmul_skinny_planes_sat"
+    rc = getattr(_lib.lib(), name)(_ptr(a), n, k, count, P(*[_ptr(x) for x in planes]),
+                                   P(*[_ptr(c) for c in cs]), (ctypes.c_uint32 * max(count, 1))(*ms), _stream())
+    _lib.check(rc, name)
 
 
 def matmul_skinny_planes_addx(a: torch.Tensor, n: int, k: int, planes: torch.Tensor, c: torch.Tensor, m: int,

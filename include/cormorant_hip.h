@@ -173,6 +173,14 @@ int cm_matmul_skinny_multi(const int16_t* a, uint32_t n, uint32_t k, uint32_t co
 int cm_matmul_skinny_planes(const int16_t* a, uint32_t n, uint32_t k, uint32_t count, const void* const* b_planes,
                             int16_t* const* c, const uint32_t* m, void* stream);
 
+/* cm_matmul_skinny_planes by the saturating Q8.8 rule (MatmulKernel's wrap32 = 0): C_i =
+ * sat16(floor(A . B_i / 2^8)) with the sum exact, as cm_matmul with wrap32 = 0 writes it (the
+ * same operands, n <= 16, k a multiple of 8).  No counterpart in the reference's units (each
+ * product is the MatmulKernel call of cm_matmul, MatmulKernel.h:228-242): one launch, no
+ * workspace, for few-row products of a constant weight (a classifier at a small batch). */
+int cm_matmul_skinny_planes_sat(const int16_t* a, uint32_t n, uint32_t k, uint32_t count,
+                                const void* const* b_planes, int16_t* const* c, const uint32_t* m, void* stream);
+
 /* One product of cm_matmul_skinny_planes followed, in the same launch, by a row-ops COPY /
  * ADDX job on its output (the decode step's residual add): C = sat16(wrap32(A . B) >> 8) as
  * there, then out[r][j] = the job of op word `op` (A kind int16 / int32, B the int16 C, output

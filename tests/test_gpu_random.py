@@ -93,6 +93,12 @@ MM_CASES = [  # n, k, m, batch, a_bs_mode, b_bs_mode, layout, kw, full_range, wr
     (64, 4096, 64, 1, 1, 1, "row", 0, True, True),
     (129, 1536, 130, 1, 1, 1, "trans", 0, False, True),
     (96, 1536, 40, 3, 1, 0, "row", 0, True, True),
+    # saturating products of few output tiles (one workgroup per tile over all of k):
+    # MobileNetV2's classifier at batch 32, ragged tiles, K past 8192 (the int64 recombination)
+    (32, 1280, 1000, 1, 1, 1, "packed", 0, True, False),
+    (160, 960, 300, 2, 1, 1, "row", 0, True, False),
+    (100, 12288, 130, 1, 1, 1, "trans", 0, True, False),
+    (70, 600, 33, 3, 1, 0, "row", 0, False, False),
     # wrap products of one slice at sizes past the split over k: BERT's output projection,
     # ragged rows and columns, the packed and transposed images
     (3072, 768, 768, 1, 1, 1, "row", 0, True, True),
@@ -155,19 +161,23 @@ def test_matmul_random(U, oracle_lib, case):
     assert (got[batch * n * m:] == POISON16).all()
 
 
-def test_matmul_split_calls_in_turn(U, oracle_lib):
+@pytest.mark.parametrize("wrap", [True, False])
+def test_matmul_split_calls_in_turn(U, oracle_lib, wrap):
     """Products split over k, finished by the last slice of each tile to arrive (its arrival
     count reset for the next call): shapes of different tile and slice counts called in turn,
-    each call with new operands, every output against the oracle."""
+    each call with new operands, every output against the oracle.  The saturating products of
+    the same shapes (and of MobileNetV2's few-tile shapes) run unsplit in turn between them."""
     rng = np.random.default_rng(11)
     shapes = [(300, 2048, 200, 2), (64, 4096, 64, 1), (512, 1024, 256, 1), (300, 2048, 200, 2), (96, 1536, 40, 3)]
+    if not wrap:
+        shapes += [(32, 1280, 1000, 1), (160, 960, 160, 1), (64, 4096, 64, 1)]
     for rep in range(2):
         for n, k, m, batch in shapes:
             a = rint16(rng, batch * n * k, -32768, 32768)
             b = rint16(rng, batch * k * m, -32768, 32768)
-            want = oracle_lib.matmul(a, b, n, k, m, batch, n * k, k * m, n * m, 0, 0, True)
+            want = oracle_lib.matmul(a, b, n, k, m, batch, n * k, k * m, n * m, 0, 0, wrap)
             c = poisoned16(batch * n * m + 8)
-            U.matmul(dev16(a), dev16(b), c, n, k, m, batch, n * k, k * m, n * m, 0, 0, True)
+            U.matmul(dev16(a), dev16(b), c, n, k, m, batch, n * k, k * m, n * m, 0, 0, wrap)
             got = host(c)
             np.testing.assert_array_equal(got[:batch * n * m], want, err_msg=f"rep {rep} shape {(n, k, m, batch)}")
             assert (got[batch * n * m:] == POISON16).all()
@@ -306,6 +316,51 @@ def test_matmul_skinny_planes(U, oracle_lib, n, k, ms):
         g = host(got)
         np.testing.assert_array_equal(g[:n * m], want)
         assert (g[n * m:] == POISON16).all()
+
+
+@pytest.mark.parametrize("n,k,ms,full", [
+    (16, 1280, (1000,), False),          # MobileNetV2's classifier, half its batch
+    (1, 784, (10,), True),               # a small CNN's classifier
+    (16, 960, (2560, 2560), True),       # two products, two blocks a workgroup
+    (5, 200, (31, 100), True),           # k past a step, rows short of 16
+    (3, 32768, (17,), True),             # the longest k: every limb sum at its bound
+    (16, 4104, (40, 600), False),        # several chunks per wavefront, k past a slab
+])
+def test_matmul_skinny_planes_sat(U, oracle_lib, n, k, ms, full):
+    """cm_matmul_skinny_planes_sat against the oracle's saturating products (the outputs'
+    neighbours untouched): sums far past int32, B from its split image."""
+    rng = np.random.default_rng(n + 5 * k + len(ms))
+    lim = 32768 if full else 2048
+    a = rint16(rng, n * k, -lim, lim)
+    bl = [rint16(rng, k * m, -lim, lim) for m in ms]
+    planes = [U.matmul_b_planes(dev16(x), k, m) for x, m in zip(bl, ms)]
+    wants = [oracle_lib.matmul(a, x, n, k, m, 1, 0, 0, n * m, 0, 0, False) for x, m in zip(bl, ms)]
+    outs = [poisoned16(n * m + 8) for m in ms]
+    U.matmul_skinny_planes(dev16(a), n, k, planes, outs, list(ms), wrap32=False)
+    for got, want, m in zip(outs, wants, ms):
+        g = host(got)
+        np.testing.assert_array_equal(g[:n * m], want)
+        assert (g[n * m:] == POISON16).all()
+
+
+def test_matmul_skinny_planes_sat_extremes(U, oracle_lib):
+    """Rows and columns of the int16 extremes through the saturating skinny products: the
+    largest |sum| (2^30 k) each side of the saturation."""
+    n, k = 4, 32768
+    a = np.empty((n, k), np.int16)
+    a[0], a[1], a[2], a[3] = -32768, 32767, -32768, 32767
+    a[3, ::2] = -32768
+    b = np.empty((k, 6), np.int16)
+    b[:, 0], b[:, 1], b[:, 2], b[:, 3], b[:, 4], b[:, 5] = -32768, 32767, -32768, 32767, 1, -1
+    b[1::2, 2] = 32767
+    b[::3, 5] = 0
+    a, b = a.reshape(-1), b.reshape(-1)
+    want = oracle_lib.matmul(a, b, n, k, 6, 1, 0, 0, n * 6, 0, 0, False)
+    c = poisoned16(n * 6 + 8)
+    U.matmul_skinny_planes(dev16(a), n, k, [U.matmul_b_planes(dev16(b), k, 6)], [c], [6], wrap32=False)
+    got = host(c)
+    np.testing.assert_array_equal(got[:n * 6], want)
+    assert (got[n * 6:] == POISON16).all()
 
 
 @pytest.mark.parametrize("n,k,m,kind", [
@@ -548,6 +603,11 @@ CONV_CASES = [  # batch, C, H, W, M, kh, kw, sh, sw, dh, dw, pt, pl, pb, pr, bia
     (3, 40, 9, 10, 50, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 1, 0, True, False),
     (1, 80, 7, 7, 130, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 0, 0, True, True),
     (2, 20, 9, 9, 24, 2, 2, 1, 1, 1, 1, 1, 0, 0, 1, 1, 0, False, False),
+    # GEMM convolutions of few output tiles and long k: MobileNetV2's 7 x 7 960 -> 160 (folded),
+    # 3 x 3 over 128 channels (im2col) at full range, 1100 channels wrapped
+    (4, 960, 7, 7, 160, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 1, 0, False, False),
+    (2, 128, 8, 8, 64, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1, 1, 0, True, False),
+    (2, 1100, 7, 7, 320, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 0, 0, True, True),
 ]
 
 
