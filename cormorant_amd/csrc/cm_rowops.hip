@@ -184,16 +184,17 @@ __device__ __forceinline__ void stage_params(uint4* lds, const uint8_t* params, 
 // term within the 64-bit bounds with a 32-bit B, bit 25: with a 16-bit B), G, and
 // Bq 2^bq_sh + 2^(sc - 1) (the bias with the rounding half folded in; 0 when bq_sh > 40, a
 // job the 128-bit path takes whole).
+template <uint32_t BATCH = 1>
 __device__ __forceinline__ void stage_addx_params(uint4* lds, const uint8_t* params, uint32_t entries, uint32_t units,
                                                   uint32_t bq_sh) {
-    for (uint32_t i = threadIdx.x; i < entries; i += blockDim.x) {
-        const Param q = param_of(reinterpret_cast<const uint4*>(params)[i]);
+    stage_entries<BATCH>(params, entries, [&](uint32_t i, const uint4& raw) {
+        const Param q = param_of(raw);
         const bool base = q.sa <= 30 && q.sc <= 61;
         const uint32_t w = (uint32_t)q.sa | ((uint32_t)q.sb << 8) | ((uint32_t)q.sc << 16) |
                            ((base && q.sb <= 30) ? 1u << 24 : 0u) | ((base && q.sb <= 46) ? 1u << 25 : 0u);
         const u64 bs = bq_sh <= 40 ? (u64)(q.bq * ((i64)1 << bq_sh) + norm_half((uint32_t)q.sc)) : 0;
         lds[pslot(i, units)] = make_uint4(w, (uint32_t)q.g, (uint32_t)bs, (uint32_t)(bs >> 32));
-    }
+    });
 }
 
 // One COPY / ADDX unit in 128-bit arithmetic (the scale flag, or shifts past the 64-bit
@@ -390,10 +391,12 @@ __global__ __launch_bounds__(TPR) void ro_norm_wg_kernel(Job j, const uint8_t* _
     u64 row = blockIdx.x;
     if (row < rows) load_row(row);                       // in flight while the parameters are staged
     pram_load(params, pram_dst, p_entries);
+    // few rows a workgroup: the staging's memory latency is on the critical path, so each
+    // thread's entries are loaded four at a time
     if constexpr (ADDX) {
-        stage_addx_params(a_lds, pa, bca ? 1u : ja.n, units, ja.bq_sh);
+        stage_addx_params<4>(a_lds, pa, bca ? 1u : ja.n, units, ja.bq_sh);
     }
-    stage_norm_params(ro_lds, params, nsl, units, j.bq_sh);
+    stage_norm_params<4>(ro_lds, params, nsl, units, j.bq_sh);
     if (t < 8) slab_acc[t >> 2][t & 3] = 0;
     __syncthreads();
     const bool scale = (ja.op & F_SCALE) != 0, relu = (ja.op & F_RELU) != 0;

@@ -119,13 +119,37 @@ __device__ __forceinline__ uint32_t pslot(uint32_t col, uint32_t units) { return
 // (the bias with the rounding half folded in: bq_sh <= 40 and sc <= 63 keep it below 2^63),
 // one 16-byte entry per column.
 __device__ __forceinline__ i64 norm_half(uint32_t sc) { return sc ? (i64)1 << (sc - 1) : 0; }
+// A workgroup's pass over a parameter block of `entries` 16-byte entries: thread t takes
+// entries t + blockDim.x (4 r + q), the loads of four of them issued before any is decoded
+// (one memory latency for up to four entries a thread, not one each); put(i, raw) stages one.
+// BATCH 1: one entry at a time (a thread with a single entry, the row kernels whose registers
+// hold a whole row while they stage).
+template <uint32_t BATCH, class F>
+__device__ __forceinline__ void stage_entries(const uint8_t* params, uint32_t entries, F&& put) {
+    const uint4* src = reinterpret_cast<const uint4*>(params);
+    for (uint32_t i0 = threadIdx.x; i0 < entries; i0 += BATCH * blockDim.x) {
+        uint4 raw[BATCH];
+#pragma unroll
+        for (uint32_t q = 0; q < BATCH; q++) {
+            const uint32_t i = i0 + q * blockDim.x;
+            raw[q] = i < entries ? src[i] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < BATCH; q++) {
+            const uint32_t i = i0 + q * blockDim.x;
+            if (i < entries) put(i, raw[q]);
+        }
+    }
+}
+
+template <uint32_t BATCH = 1>
 __device__ __forceinline__ void stage_norm_params(uint4* lds, const uint8_t* params, uint32_t entries,
                                                   uint32_t units, uint32_t bq_sh) {
-    for (uint32_t i = threadIdx.x; i < entries; i += blockDim.x) {
-        const Param q = param_of(reinterpret_cast<const uint4*>(params)[i]);
+    stage_entries<BATCH>(params, entries, [&](uint32_t i, const uint4& raw) {
+        const Param q = param_of(raw);
         const u64 bs = (u64)(q.bq * ((i64)1 << bq_sh) + norm_half((uint32_t)q.sc));
         lds[pslot(i, units)] = make_uint4((uint32_t)q.g, (uint32_t)q.sc, (uint32_t)bs, (uint32_t)(bs >> 32));
-    }
+    });
 }
 
 // Round half to even of v / 2^k for 0 <= k <= 61 and |v| < 1.5 2^62:
