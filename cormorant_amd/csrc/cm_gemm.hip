@@ -1017,8 +1017,7 @@ constexpr uint32_t kCsMaxTaps = 80;          // taps a lane holds (40 pairs)
 // taps x output channels up to which the VALU path beats the GEMM's (measured on MobileNetV2's
 // 1x1 shapes: 32 x 192 at 28^2 pixels 18 vs 21 us, 64 x 384 at 14^2 21 vs 17 us)
 constexpr uint64_t kCsMaxWork = 12288;
-constexpr uint32_t kCsOg = 16;               // output channels of a workgroup (4 at a time)
-constexpr uint32_t kCsPix = 1;               // output pixels of a lane (256 apart)
+constexpr uint32_t kCsOg = 32;               // output channels a workgroup holds at most (4 at a time)
 
 struct ConvSmall {
     const int16_t* x;
@@ -1030,6 +1029,7 @@ struct ConvSmall {
                                              // tiles, lanes of a position in the last tile
     uint32_t cs, cn, gs, wrap;
     int32_t lo, hi;
+    uint32_t og;                             // output channels of a workgroup (a multiple of 4, <= kCsOg)
 };
 
 // PW: a pointwise convolution (1x1, stride 1, no padding, the output plane the input's): the
@@ -1040,25 +1040,54 @@ __global__ __launch_bounds__(256) void conv_small_kernel(ConvSmall c) {
     __shared__ int32_t bl[kCsOg];
     __shared__ uint32_t exact[kCsOg], exact4[kCsOg / 4];
     __shared__ uint64_t ybase[kCsOg];         // a channel's offset in the output (the y pattern)
-    __shared__ int4 tapt[2 * NP];             // per tap: element offset, row and column offset, valid
     const uint32_t t = threadIdx.x, plane = c.out_h * c.out_w, taps = c.in_ch * c.kh * c.kw, khw = c.kh * c.kw;
-    const uint32_t oc0 = blockIdx.y * kCsOg, nb = blockIdx.z;
-    const uint32_t og = min(kCsOg, c.out_ch - oc0);
+    const uint32_t oc0 = blockIdx.y * c.og, nb = blockIdx.z;
+    const uint32_t og = min(c.og, c.out_ch - oc0);
     const int16_t* xb = c.x + (uint64_t)nb * c.in_ch * c.in_h * c.in_w;
-    uint32_t xw[PW ? NP : 1];
-    static_assert(!PW || kCsPix == 1, "the pointwise taps are the lane's one pixel");
+    // the lane's output pixel and its taps, loaded before the weights are staged (their
+    // latency under the staging's): PW from the input planes at the pixel; otherwise the taps
+    // in order (ci, a, b) from running counters, the same for every lane (scalar registers),
+    // so that all the loads go out at once
+    const uint32_t p = blockIdx.x * 256 + t;
+    const bool live = p < plane;
+    uint32_t xv[NP];
     if constexpr (PW) {
-        const uint32_t p = blockIdx.x * 256 + t;
 #pragma unroll
         for (uint32_t pr = 0; pr < NP; pr++) {
-            const uint32_t lo = p < plane && 2 * pr < taps ? (uint32_t)(uint16_t)xb[(uint64_t)(2 * pr) * plane + p] : 0u;
-            const uint32_t hi = p < plane && 2 * pr + 1 < taps ? (uint32_t)(uint16_t)xb[(uint64_t)(2 * pr + 1) * plane + p] : 0u;
-            xw[pr] = lo | (hi << 16);
+            const uint32_t lo = live && 2 * pr < taps ? (uint32_t)(uint16_t)xb[(uint64_t)(2 * pr) * plane + p] : 0u;
+            const uint32_t hi = live && 2 * pr + 1 < taps ? (uint32_t)(uint16_t)xb[(uint64_t)(2 * pr + 1) * plane + p] : 0u;
+            xv[pr] = lo | (hi << 16);
+        }
+    } else {
+        const uint32_t pc = live ? p : 0u;
+        const uint32_t oh = pc / c.out_w, ow = pc - oh * c.out_w;
+        const int ih0 = (int)(oh * c.sh) - (int)c.pt, iw0 = (int)(ow * c.sw) - (int)c.pl;
+        const int64_t o0 = (int64_t)ih0 * c.in_w + iw0;
+        uint32_t ci = 0, ta = 0, tb = 0;
+#pragma unroll
+        for (uint32_t pr = 0; pr < NP; pr++) {
+            uint32_t v2 = 0;
+#pragma unroll
+            for (uint32_t h = 0; h < 2; h++) {
+                const uint32_t tp = 2 * pr + h;
+                const int dy = (int)(ta * c.dh), dx = (int)(tb * c.dw);
+                const int ih = ih0 + dy, iw = iw0 + dx;
+                const bool in = live && tp < taps && ih >= 0 && ih < (int)c.in_h && iw >= 0 && iw < (int)c.in_w;
+                const int64_t off = o0 + (int64_t)ci * c.in_h * c.in_w + (int64_t)dy * c.in_w + dx;
+                v2 |= (in ? (uint32_t)(uint16_t)xb[off] : 0u) << (16 * h);
+                if (++tb == c.kw) {
+                    tb = 0;
+                    if (++ta == c.kh) {
+                        ta = 0;
+                        ci++;
+                    }
+                }
+            }
+            xv[pr] = v2;
         }
     }
-    // the group's weights as int16 pairs in tap order (ci, a, b), zero past the taps; the taps'
-    // offsets from a pixel's window origin
-    for (uint32_t i = t; i < kCsOg * NP; i += 256) {
+    // the group's weights as int16 pairs in tap order (ci, a, b), zero past the taps
+    for (uint32_t i = t; i < c.og * NP; i += 256) {
         const uint32_t o = i / NP, pr = i - o * NP;
         uint32_t v = 0;
 #pragma unroll
@@ -1072,15 +1101,6 @@ __global__ __launch_bounds__(256) void conv_small_kernel(ConvSmall c) {
             }
         }
         wl[o][pr] = v;
-    }
-    for (uint32_t tp = t; tp < 2 * NP; tp += 256) {
-        int4 e = make_int4(0, 0, 0, 0);
-        if (tp < taps) {
-            const uint32_t ci = tp / khw, pos = tp - ci * khw, a = pos / c.kw, b = pos - a * c.kw;
-            const int dy = (int)(a * c.dh), dx = (int)(b * c.dw);
-            e = make_int4((int)(ci * c.in_h * c.in_w) + dy * (int)c.in_w + dx, dy, dx, 1);
-        }
-        tapt[tp] = e;
     }
     if (t < kCsOg) bl[t] = t < og && c.bias ? (int32_t)c.bias[oc0 + t] : 0;
     __syncthreads();
@@ -1099,76 +1119,45 @@ __global__ __launch_bounds__(256) void conv_small_kernel(ConvSmall c) {
     if (t < kCsOg / 4) exact4[t] = exact[4 * t] & exact[4 * t + 1] & exact[4 * t + 2] & exact[4 * t + 3];
     __syncthreads();
     typedef short v2s __attribute__((ext_vector_type(2)));
-#pragma unroll 1
-    for (uint32_t i = 0; i < kCsPix; i++) {                // one pixel's taps in registers at a time
-        const uint32_t p = blockIdx.x * 256 * kCsPix + 256 * i + t;
-        if (p >= plane) break;
-        const uint32_t oh = p / c.out_w, ow = p - oh * c.out_w;
-        // the taps from the table (every index into xv a constant: it stays in registers); the
-        // table is read per pixel (an opaque zero in its index), not held in registers across
-        // the pixels
-        const int ih0 = (int)(oh * c.sh) - (int)c.pt, iw0 = (int)(ow * c.sw) - (int)c.pl;
-        const int64_t o0 = (int64_t)ih0 * c.in_w + iw0;
-        uint32_t z = i;
-        __asm__ volatile("" : "+v"(z));
-        z &= 0u;
-        uint32_t xv[NP];
+    if (!live) return;                                    // no barrier follows
+    int16_t* yb = c.y + (uint64_t)nb * c.out_ch * plane + p;
+    // four channels at a time: four independent sums (channels past og have zero weights,
+    // their stores are skipped)
+    for (uint32_t o = 0; o < og; o += 4) {
+        int64_t q[4];
+        if (exact4[o / 4]) {
+            int32_t acc[4];
 #pragma unroll
-        for (uint32_t pr = 0; pr < NP; pr++) {
-            if constexpr (PW) {
-                xv[pr] = xw[pr];
-                continue;
-            }
-            uint32_t v2 = 0;
+            for (uint32_t j = 0; j < 4; j++) acc[j] = (int32_t)((uint32_t)bl[o + j] << 8);
 #pragma unroll
-            for (uint32_t h = 0; h < 2; h++) {
-                const int4 e = tapt[2 * pr + h + z];
-                const int ih = ih0 + e.y, iw = iw0 + e.z;
-                const bool in = e.w && ih >= 0 && ih < (int)c.in_h && iw >= 0 && iw < (int)c.in_w;
-                const uint32_t v = in ? (uint32_t)(uint16_t)xb[o0 + e.x] : 0u;
-                v2 |= v << (16 * h);
-            }
-            xv[pr] = v2;
-        }
-        int16_t* yb = c.y + (uint64_t)nb * c.out_ch * plane + p;
-        // four channels at a time: four independent sums (channels past og have zero weights,
-        // their stores are skipped)
-        for (uint32_t o = 0; o < og; o += 4) {
-            int64_t q[4];
-            if (exact4[o / 4]) {
-                int32_t acc[4];
-#pragma unroll
-                for (uint32_t j = 0; j < 4; j++) acc[j] = (int32_t)((uint32_t)bl[o + j] << 8);
-#pragma unroll
-                for (uint32_t pr = 0; pr < NP; pr += 4) {
-#pragma unroll
-                    for (uint32_t j = 0; j < 4; j++) {
-                        const uint4 wq = *reinterpret_cast<const uint4*>(&wl[o + j][pr]);
-                        acc[j] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr]), __builtin_bit_cast(v2s, wq.x), acc[j], false);
-                        acc[j] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr + 1]), __builtin_bit_cast(v2s, wq.y), acc[j], false);
-                        acc[j] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr + 2]), __builtin_bit_cast(v2s, wq.z), acc[j], false);
-                        acc[j] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr + 3]), __builtin_bit_cast(v2s, wq.w), acc[j], false);
-                    }
-                }
-#pragma unroll
-                for (uint32_t j = 0; j < 4; j++) q[j] = acc[j] >> 8;
-            } else {
+            for (uint32_t pr = 0; pr < NP; pr += 4) {
 #pragma unroll
                 for (uint32_t j = 0; j < 4; j++) {
-                    long long acc = (long long)bl[o + j] * 256;
-#pragma unroll
-                    for (uint32_t pr = 0; pr < NP; pr++) {
-                        const uint32_t wv = wl[o + j][pr];
-                        acc += (long long)(int16_t)(xv[pr] & 0xFFFF) * (int16_t)(wv & 0xFFFF) +
-                               (long long)(int16_t)(xv[pr] >> 16) * (int16_t)(wv >> 16);
-                    }
-                    q[j] = acc >> 8;
+                    const uint4 wq = *reinterpret_cast<const uint4*>(&wl[o + j][pr]);
+                    acc[j] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr]), __builtin_bit_cast(v2s, wq.x), acc[j], false);
+                    acc[j] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr + 1]), __builtin_bit_cast(v2s, wq.y), acc[j], false);
+                    acc[j] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr + 2]), __builtin_bit_cast(v2s, wq.z), acc[j], false);
+                    acc[j] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, xv[pr + 3]), __builtin_bit_cast(v2s, wq.w), acc[j], false);
                 }
             }
 #pragma unroll
-            for (uint32_t j = 0; j < 4; j++)
-                if (o + j < og) yb[ybase[o + j]] = (int16_t)(q[j] > c.hi ? c.hi : (q[j] < c.lo ? c.lo : q[j]));
+            for (uint32_t j = 0; j < 4; j++) q[j] = acc[j] >> 8;
+        } else {
+#pragma unroll
+            for (uint32_t j = 0; j < 4; j++) {
+                long long acc = (long long)bl[o + j] * 256;
+#pragma unroll
+                for (uint32_t pr = 0; pr < NP; pr++) {
+                    const uint32_t wv = wl[o + j][pr];
+                    acc += (long long)(int16_t)(xv[pr] & 0xFFFF) * (int16_t)(wv & 0xFFFF) +
+                           (long long)(int16_t)(xv[pr] >> 16) * (int16_t)(wv >> 16);
+                }
+                q[j] = acc >> 8;
+            }
         }
+#pragma unroll
+        for (uint32_t j = 0; j < 4; j++)
+            if (o + j < og) yb[ybase[o + j]] = (int16_t)(q[j] > c.hi ? c.hi : (q[j] < c.lo ? c.lo : q[j]));
     }
 }
 
@@ -2452,10 +2441,15 @@ int conv_run(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y
         const uint32_t taps = in_ch * kh * kw, tiles = (in_ch + 15) / 16;
         const uint32_t rem = in_ch - (tiles - 1) * 16, last = rem <= 8 ? 8u : 16u;
         const uint32_t np = (uint32_t)round_up(ceil_div(taps, 2), 4);
+        // output channels a workgroup: 32 over planes of at least 56 x 56 (the pixels' taps
+        // loaded once for more channels), 16 below, 4 where 16 would leave most compute units
+        // idle (a small CNN's 14 x 14 planes at batch 1)
+        const uint64_t pblocks = (uint64_t)ceil_div(plane, 256) * batch;
+        const uint32_t og = pblocks * ceil_div(out_ch, 16) < (uint64_t)st->cus ? 4u : (plane >= 3136 ? 32u : 16u);
         const ConvSmall cv{x, w, bptr, y, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w,
                            dilation_h, dilation_w, pad_top, pad_left, kh * kw * ((tiles - 1) * 16 + last), tiles, last,
-                           cs, y_cn, y_gs, wrap32 ? 1u : 0u, lo, hi};
-        const dim3 grid(ceil_div(plane, 256 * kCsPix), ceil_div(out_ch, kCsOg), batch);
+                           cs, y_cn, y_gs, wrap32 ? 1u : 0u, lo, hi, og};
+        const dim3 grid(ceil_div(plane, 256), ceil_div(out_ch, og), batch);
         const bool pw = kh == 1 && kw == 1 && stride_h == 1 && stride_w == 1 && pad_top == 0 && pad_left == 0 &&
                         in_h == out_h && in_w == out_w;
 #define CM_CS(NP_)                                                                                              \
