@@ -473,13 +473,21 @@ __global__ __launch_bounds__(256) void split_fold_lds_kernel(const int16_t* __re
     const uint32_t my_line = t >> 2, part_k = (t & 3) * 16;
     int32_t sum = 0;
     const uint32_t k_end = min(kp, (slab + 1) * SLAB);
-    for (uint32_t k0 = slab * SLAB; k0 < k_end; k0 += 64) {
+    // a 64-k chunk's loads in registers, the next chunk's issued while this one is split
+    int16_t v[16];
+    auto load_chunk = [&](uint32_t k0) {
 #pragma unroll
         for (uint32_t r = 0; r < 16; r++) {
             const uint32_t kk = k0 + 4 * r + kr;
-            tile[la][4 * r + kr] = (real_a && kk < in_ch) ? src[(uint64_t)kk * plane] : kPad;
+            v[r] = (real_a && kk < in_ch) ? src[(uint64_t)kk * plane] : kPad;
         }
+    };
+    load_chunk(slab * SLAB);
+    for (uint32_t k0 = slab * SLAB; k0 < k_end; k0 += 64) {
+#pragma unroll
+        for (uint32_t r = 0; r < 16; r++) tile[la][4 * r + kr] = v[r];
         __syncthreads();
+        if (k0 + 64 < k_end) load_chunk(k0 + 64);
         int16_t e[16];
 #pragma unroll
         for (int q = 0; q < 16; q++) {
