@@ -369,7 +369,8 @@ __global__ __launch_bounds__(1024) void split_fold_kernel(const int16_t* __restr
     const int16_t* src = x + img * img_elems + p;
     int32_t sum = 0;
     const uint32_t kb = slab * SLAB + 64 * wave, ke = min(kb + 64, kp);
-#pragma unroll 2
+    // the wave's four 16-k chunks unrolled: every load in flight before the first is used
+#pragma unroll 4
     for (uint32_t k0 = kb; k0 < ke; k0 += 16) {
         int16_t e[16];
         if (real && k0 + 16 <= in_ch) {
