@@ -391,14 +391,30 @@ __global__ __launch_bounds__(TPR) void ro_norm_wg_kernel(Job j, const uint8_t* _
     u64 row = blockIdx.x;
     if (row < rows) load_row(row);                       // in flight while the parameters are staged
     pram_load(params, pram_dst, p_entries);
-    // few rows a workgroup: the staging's memory latency is on the critical path, so each
-    // thread's entries are loaded four at a time
-    if constexpr (ADDX) {
-        stage_addx_params<4>(a_lds, pa, bca ? 1u : ja.n, units, ja.bq_sh);
+    // A plain NORM: each lane stages the entries of its own units (the only slots it reads,
+    // norm_row_finish / norm_unit_wide), so no barrier waits for the staging; their loads go
+    // out here beside the row's and are decoded after the row's sums.
+    constexpr bool SELF = !ADDX && !PL;
+    uint4 praw[SELF ? UPL : 1][SELF ? 8 : 1];
+    if constexpr (SELF) {
+        const uint4* src = reinterpret_cast<const uint4*>(params);
+#pragma unroll
+        for (int k = 0; k < UPL; k++) {
+            const uint32_t u = t + TPR * k;
+#pragma unroll
+            for (int l = 0; l < 8; l++)
+                praw[k][l] = u < units ? src[bcast ? 0u : 8u * u + l] : make_uint4(0, 0, 0, 0);
+        }
+    } else {
+        // few rows a workgroup: the staging's memory latency is on the critical path, so each
+        // thread's entries are loaded four at a time
+        if constexpr (ADDX) {
+            stage_addx_params<4>(a_lds, pa, bca ? 1u : ja.n, units, ja.bq_sh);
+        }
+        stage_norm_params<4>(ro_lds, params, nsl, units, j.bq_sh);
+        if (t < 8) slab_acc[t >> 2][t & 3] = 0;
+        __syncthreads();
     }
-    stage_norm_params<4>(ro_lds, params, nsl, units, j.bq_sh);
-    if (t < 8) slab_acc[t >> 2][t & 3] = 0;
-    __syncthreads();
     const bool scale = (ja.op & F_SCALE) != 0, relu = (ja.op & F_RELU) != 0;
     const uint32_t nslab = min(po.nsum, (units + 127) / 128);
     for (uint32_t it = 0; row < rows; row += gridDim.x, it++) {
@@ -420,6 +436,21 @@ __global__ __launch_bounds__(TPR) void ro_norm_wg_kernel(Job j, const uint8_t* _
         }
         NormSums ts = norm_sums<UPL>(x);
         norm_sums_wave(ts);
+        if constexpr (SELF) {
+            if (it == 0) {
+#pragma unroll
+                for (int k = 0; k < UPL; k++) {
+                    const uint32_t u = t + TPR * k;
+                    if (u >= units) continue;
+#pragma unroll
+                    for (int l = 0; l < 8; l++) {
+                        const uint32_t i = bcast ? 0u : 8u * u + l;
+                        if (bcast && l > 0) break;
+                        norm_entry(ro_lds, i, praw[k][l], units, j.bq_sh);
+                    }
+                }
+            }
+        }
         NormSums* ws = wsum[it & 1];                     // alternate: a row's reads end before the next's writes
         if (lane == 0) ws[wave] = ts;
         __syncthreads();

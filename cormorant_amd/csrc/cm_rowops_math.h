@@ -142,14 +142,17 @@ __device__ __forceinline__ void stage_entries(const uint8_t* params, uint32_t en
     }
 }
 
+// One entry of the staged form at its slot.
+__device__ __forceinline__ void norm_entry(uint4* lds, uint32_t i, const uint4& raw, uint32_t units, uint32_t bq_sh) {
+    const Param q = param_of(raw);
+    const u64 bs = (u64)(q.bq * ((i64)1 << bq_sh) + norm_half((uint32_t)q.sc));
+    lds[pslot(i, units)] = make_uint4((uint32_t)q.g, (uint32_t)q.sc, (uint32_t)bs, (uint32_t)(bs >> 32));
+}
+
 template <uint32_t BATCH = 1>
 __device__ __forceinline__ void stage_norm_params(uint4* lds, const uint8_t* params, uint32_t entries,
                                                   uint32_t units, uint32_t bq_sh) {
-    stage_entries<BATCH>(params, entries, [&](uint32_t i, const uint4& raw) {
-        const Param q = param_of(raw);
-        const u64 bs = (u64)(q.bq * ((i64)1 << bq_sh) + norm_half((uint32_t)q.sc));
-        lds[pslot(i, units)] = make_uint4((uint32_t)q.g, (uint32_t)q.sc, (uint32_t)bs, (uint32_t)(bs >> 32));
-    });
+    stage_entries<BATCH>(params, entries, [&](uint32_t i, const uint4& raw) { norm_entry(lds, i, raw, units, bq_sh); });
 }
 
 // Round half to even of v / 2^k for 0 <= k <= 61 and |v| < 1.5 2^62:
