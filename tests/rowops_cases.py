@@ -36,6 +36,11 @@ RO_CASES = [  # label, op word, n, rows, blocks, kinds (a, b, c bytes), param ra
     # taking rows in turn
     ("norm_ln_i32_4096_rows", 5 | (1 << 4) | (1 << 16), 4096, 150, 3),
     ("norm_rms_i16_1536_rows", 5, 1536, 400, 2),
+    # broadcast parameters on the workgroup-per-row kernel, one and two units a lane: each lane
+    # decodes the one entry it reads
+    ("norm_ln_i32_4096_bcast", 5 | (1 << 4) | (1 << 13) | (1 << 16), 4096, 3, 2),
+    ("norm_rms_i16_2560_bcast", 5 | (1 << 13), 2560, 5, 1),
+    ("norm_rms_i32_1280_bcast", 5 | (1 << 4) | (1 << 13), 1280, 7, 1),
     # two units a lane over at least twelve rows per compute unit (3072 on 256): a workgroup of
     # twelve wavefronts per compute unit
     ("norm_ln_i32_768_many_rows", 5 | (1 << 4) | (1 << 16), 768, 1031, 3),
