@@ -1071,25 +1071,46 @@ __global__ __launch_bounds__(256) void conv_small_kernel(ConvSmall c) {
         const uint32_t pc = live ? p : 0u;
         const uint32_t oh = pc / c.out_w, ow = pc - oh * c.out_w;
         const int ih0 = (int)(oh * c.sh) - (int)c.pt, iw0 = (int)(ow * c.sw) - (int)c.pl;
-        const int64_t o0 = (int64_t)ih0 * c.in_w + iw0;
-        uint32_t ci = 0, ta = 0, tb = 0;
+        // the kernel rows and columns whose input row / column lies inside the plane, as bit
+        // masks (kh, kw <= 32), so that a tap's test is two shifts and an AND
+        uint32_t rm = 0, cmk = 0;
+        for (uint32_t a = 0; a < c.kh; a++) {
+            const int ih = ih0 + (int)(a * c.dh);
+            rm |= (ih >= 0 && ih < (int)c.in_h ? 1u : 0u) << a;
+        }
+        for (uint32_t b = 0; b < c.kw; b++) {
+            const int iw = iw0 + (int)(b * c.dw);
+            cmk |= (iw >= 0 && iw < (int)c.in_w ? 1u : 0u) << b;
+        }
+        if (!live) rm = 0;
+        // the lane's offset from the window origin at row -pt, column -pl (never negative), and
+        // the tap's offset from that origin, the same for every lane (scalar
+        // registers, stepped as the counters run), so that a tap's load address is one add
+        const uint32_t vo = oh * c.sh * c.in_w + ow * c.sw;
+        int64_t uo = -((int64_t)c.pt * c.in_w + c.pl);
+        const int64_t step_a = (int64_t)c.dh * c.in_w - (int64_t)c.kw * c.dw;
+        const int64_t step_c = (int64_t)c.in_h * c.in_w - (int64_t)c.kh * c.dh * c.in_w;
+        // the valid columns of the current kernel row, zero past the last input channel (the
+        // taps past in_ch kh kw), updated only where a kernel row ends
+        uint32_t ta = 0, tb = 0, ci = 0;
+        uint32_t crow = (rm & 1u) ? cmk : 0u;
 #pragma unroll
         for (uint32_t pr = 0; pr < NP; pr++) {
             uint32_t v2 = 0;
 #pragma unroll
             for (uint32_t h = 0; h < 2; h++) {
-                const uint32_t tp = 2 * pr + h;
-                const int dy = (int)(ta * c.dh), dx = (int)(tb * c.dw);
-                const int ih = ih0 + dy, iw = iw0 + dx;
-                const bool in = live && tp < taps && ih >= 0 && ih < (int)c.in_h && iw >= 0 && iw < (int)c.in_w;
-                const int64_t off = o0 + (int64_t)ci * c.in_h * c.in_w + (int64_t)dy * c.in_w + dx;
-                v2 |= (in ? (uint32_t)(uint16_t)xb[off] : 0u) << (16 * h);
+                const bool in = (crow & (1u << tb)) != 0u;
+                v2 |= (in ? (uint32_t)(uint16_t)xb[uo + (int64_t)vo] : 0u) << (16 * h);
+                uo += c.dw;
                 if (++tb == c.kw) {
                     tb = 0;
+                    uo += step_a;
                     if (++ta == c.kh) {
                         ta = 0;
+                        uo += step_c;
                         ci++;
                     }
+                    crow = ci < c.in_ch && ((rm >> ta) & 1u) ? cmk : 0u;
                 }
             }
             xv[pr] = v2;
@@ -2445,7 +2466,8 @@ int conv_run(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y
         return CM_OK;
     }
     if (in_ch * kh * kw <= kCsMaxTaps && (uint64_t)in_ch * kh * kw * out_ch <= kCsMaxWork && batch <= 65535 &&
-        (uint64_t)in_ch * in_h * in_w < (1ull << 31)) {
+        (uint64_t)in_ch * in_h * in_w < (1ull << 31) && kh <= 32 && kw <= 32 &&
+        (uint64_t)out_h * stride_h * in_w + (uint64_t)out_w * stride_w < (1ull << 31)) {
         // few taps: straight on the VALU
         const uint32_t taps = in_ch * kh * kw, tiles = (in_ch + 15) / 16;
         const uint32_t rem = in_ch - (tiles - 1) * 16, last = rem <= 8 ? 8u : 16u;
